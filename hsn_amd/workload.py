@@ -1,0 +1,170 @@
+"""Synthetic window workloads: the five configurations of the benchmark contract.
+
+Every tensor is drawn on the CPU from ``torch.Generator().manual_seed(seed)`` in a fixed order,
+so a checker on the CPU and the GPU path see identical bits after a copy. The draws follow the
+workload definitions (units ``M = 1``, uniform cost table ``1/(N*M)``, zero overhead and shared
+cost, budget 1.0 so all ``K`` slots are valid, candidate ``tanh(y)``, write gate
+``b = sigmoid(gate_pre)``):
+
+==========  ==========================  ==========================================  =========
+config      B, T, N, d, K               distributions                               storage
+==========  ==========================  ==========================================  =========
+tiny        2, 8, 16, 16, 2             y, logits ~ N(0,1); gate_pre ~ N(2,0.5);     fp32
+                                        h0 = q0 = 0; one reset at row 1, pos 4
+ref         32, 256, 256, 64, 8         h0 ~ N(0, 0.1^2), q0 = mean_n h0;            fp32
+                                        reset ~ Bernoulli(1/256)
+bf16        64, 512, 1024, 64, 16       logits += bias_n ~ N(0, 0.5^2);              bf16 I/O
+                                        reset ~ Bernoulli(1/128)
+tbptt       128, 128 (x16), 512, 128, 8 gate_pre ~ N(3, 0.5); reset ~ Bernoulli(1/256)  fp32
+skewed      256, 1024, 4096, 64, 32     logits += -1.1 ln(1 + rank_n) (Zipf bias);   bf16 I/O
+                                        reset ~ Bernoulli(1/512)
+==========  ==========================  ==========================================  =========
+
+Builder decisions (fixed here, used on both sides): the "decay gate" is the write gate's
+pre-activation; ``N(0, 0.1)`` means sigma = 0.1; the cotangents ``d_q_pre, d_q_post [B,T,d]``,
+``d_h_sel [B,T,K,d]`` and the end-state cotangents ``d_h_T [B,N,d]``, ``d_q_T [B,d]`` are N(0,1).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import Optional
+
+import torch
+
+__all__ = ["Config", "CONFIGS", "make_window", "make_cotangents", "byte_model"]
+
+
+@dataclasses.dataclass(frozen=True)
+class Config:
+    name: str
+    B: int
+    T: int
+    N: int
+    d: int
+    K: int
+    M: int = 1
+    io: str = "f32"  # storage dtype of inputs/outputs: "f32" or "bf16"
+    gate_mu: float = 2.0
+    h0_sigma: float = 0.1  # 0 => zero initial state
+    reset_p: float = 0.0
+    reset_at: Optional[tuple] = None  # explicit (row, pos) resets
+    logit_bias: str = "none"  # "none" | "normal" | "zipf"
+    windows: int = 1
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return torch.bfloat16 if self.io == "bf16" else torch.float32
+
+    def scaled(self, **kw) -> "Config":
+        return dataclasses.replace(self, **kw)
+
+
+CONFIGS = {
+    "tiny": Config("tiny", 2, 8, 16, 16, 2, h0_sigma=0.0, reset_at=((1, 4),)),
+    "ref": Config("ref", 32, 256, 256, 64, 8, reset_p=1 / 256),
+    "bf16": Config("bf16", 64, 512, 1024, 64, 16, io="bf16", reset_p=1 / 128,
+                   logit_bias="normal"),
+    "tbptt": Config("tbptt", 128, 128, 512, 128, 8, gate_mu=3.0, reset_p=1 / 256, windows=16),
+    "skewed": Config("skewed", 256, 1024, 4096, 64, 32, io="bf16", reset_p=1 / 512,
+                     logit_bias="zipf"),
+}
+
+
+def make_window(cfg: Config, seed: int, *, window: int = 0) -> dict:
+    """The inputs of one window of ``cfg`` as CPU tensors (``window`` > 0: the later windows of
+    a TBPTT segment draw fresh inputs from the same generator stream but keep the config's
+    start state only for window 0)."""
+    g = torch.Generator().manual_seed(seed)
+    B, T, N, d, K, M = cfg.B, cfg.T, cfg.N, cfg.d, cfg.K, cfg.M
+    bias = torch.zeros(N)
+    if cfg.logit_bias == "normal":
+        bias = torch.randn(N, generator=g) * 0.5
+    elif cfg.logit_bias == "zipf":
+        rank = torch.randperm(N, generator=g).to(torch.float32)
+        bias = -1.1 * torch.log1p(rank)
+    for _ in range(window):  # advance the stream deterministically per window
+        torch.randn(1, generator=g)
+    logits = torch.randn(B, T, N, M, generator=g) + bias[None, None, :, None]
+    y = torch.randn(B, T, K, d, generator=g)
+    gate_pre = torch.randn(B, T, K, d, generator=g) * 0.5 + cfg.gate_mu
+    if cfg.h0_sigma > 0:
+        h0 = torch.randn(B, N, d, generator=g) * cfg.h0_sigma
+    else:
+        h0 = torch.zeros(B, N, d)
+    q0 = h0.mean(dim=1)
+    reset = torch.zeros(B, T, dtype=torch.bool)
+    if cfg.reset_p > 0:
+        reset = torch.rand(B, T, generator=g) < cfg.reset_p
+    if cfg.reset_at:
+        for r, t in cfg.reset_at:
+            reset[r, t] = True
+    dt = cfg.dtype
+    return {
+        "logits": logits.to(dt),
+        "y": y.to(dt),
+        "gate_pre": gate_pre.to(dt),
+        "reset": reset,
+        "h0": h0,
+        "q0": q0,
+        "age0": torch.zeros(B, N, dtype=torch.int64),
+        "pos0": torch.zeros(B, dtype=torch.int64),
+        "cost": torch.full((M,), 1.0 / (N * M), dtype=torch.float32),
+    }
+
+
+def make_cotangents(cfg: Config, seed: int, *, carried: bool = True) -> dict:
+    """The backward inputs: cotangents of ``q`` before / after each position, of the selected
+    updated states, and (``carried``) of the window's end state."""
+    g = torch.Generator().manual_seed(seed + 7919)
+    B, T, N, d, K = cfg.B, cfg.T, cfg.N, cfg.d, cfg.K
+    dt = cfg.dtype
+    out = {
+        "d_q_pre": torch.randn(B, T, d, generator=g).to(dt),
+        "d_q_post": torch.randn(B, T, d, generator=g).to(dt),
+        "d_h_sel": torch.randn(B, T, K, d, generator=g).to(dt),
+        "d_h_T": None,
+        "d_q_T": None,
+    }
+    if carried:
+        out["d_h_T"] = torch.randn(B, N, d, generator=g)
+        out["d_q_T"] = torch.randn(B, d, generator=g)
+    return out
+
+
+def byte_model(cfg: Config) -> dict:
+    """Algorithmic HBM bytes per (row, position) of the window's fwd + bwd.
+
+    F = storage bytes (4 fp32, 2 bf16), S = 4 (fp32 state), indices int32, valid/reset u8.
+
+    forward reads  N*M*F (logits) + 2*K*d*F (y, gate_pre) + 1 (reset)
+    forward writes 4K + K + 4 (cells, valid, theta) + 2*d*F (q_pre, q_post)
+                   + 2*K*d*F (h_sel, h_old)
+    forward state  (2*N*d*S + 2*d*S + 2*N*8) / T (h0 in, h_T out, q0/q_T, age0/age_T)
+    backward reads 2*K*d*F (y, gate_pre) + K*d*F (h_old) + 5K + 1 (cells, valid, reset)
+                   + 2*d*F (d_q_pre, d_q_post) + K*d*F (d_h_sel)
+    backward writes 2*K*d*F (dy, dgate)
+    backward state (2*N*d*S + 2*d*S) / T (d_h_T, d_q_T in; d_h0, d_q0 out)
+    """
+    F = 2 if cfg.io == "bf16" else 4
+    S = 4
+    B, T, N, d, K, M = cfg.B, cfg.T, cfg.N, cfg.d, cfg.K, cfg.M
+    route = N * M * F + 1 + 4 * K + K + 4
+    fwd_only = 2 * K * d * F + 2 * d * F + 2 * K * d * F + (2 * N * d * S + 2 * d * S + 2 * N * 8) / T
+    fwd = route + fwd_only
+    bwd = 2 * K * d * F + K * d * F + 5 * K + 1 + 2 * d * F + K * d * F + 2 * K * d * F \
+        + (2 * N * d * S + 2 * d * S) / T
+    return {"route": route, "forward": fwd, "forward_update": fwd_only, "backward": bwd,
+            "total": fwd + bwd, "window_bytes": (fwd + bwd) * B * T}
+
+
+def describe(cfg: Config) -> str:
+    return f"B{cfg.B} T{cfg.T} N{cfg.N} d{cfg.d} K{cfg.K} M{cfg.M} {cfg.io}"
+
+
+def _check_byte_model() -> None:  # pragma: no cover - used interactively
+    for name, cfg in CONFIGS.items():
+        bm = byte_model(cfg)
+        print(name, round(bm["forward"]), round(bm["backward"]), round(bm["total"]),
+              bm["window_bytes"] / 1e6, math.floor(8e12 / bm["total"] / 1e6))

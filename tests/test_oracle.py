@@ -1,0 +1,445 @@
+"""The CPU oracle pinned against the reference's golden vectors, autograd closed forms, the
+router's known answers and brute force. CPU only."""
+
+from __future__ import annotations
+
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import load_golden
+from oracle import hsn_oracle as O
+
+F64 = torch.float64
+
+
+def _close(got, want, atol=1e-5, rtol=1e-5):
+    torch.testing.assert_close(got, want, atol=atol, rtol=rtol)
+
+
+# --------------------------------------------------------------------------------------------
+# the golden vectors of the reference's four-op ABI (gated update, gather)
+# --------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("size", ["tiny", "ref", "odd"])
+def test_gated_update_matches_golden_vectors(size):
+    v = load_golden(f"{size}_gated_delta_update.safetensors")
+    h_out, q_out, age_out, h_old = O.gated_delta_update_abi(
+        v["h"], v["q"], v["age"], v["cell_idx"], v["valid"], v["c"], v["b"])
+    _close(h_out, v["h_out"])
+    _close(q_out, v["q_out"])
+    assert torch.equal(age_out, v["age_out"])
+    _close(h_old, v["h_old_saved"])
+    gh, gq, gc, gb = O.gated_delta_update_bwd(v["cell_idx"], v["valid"], v["c"], v["b"],
+                                              v["h_old_saved"], v["grad_h_out"], v["grad_q_out"])
+    _close(gh, v["grad_h"])
+    _close(gq, v["grad_q"])
+    _close(gc, v["grad_c"])
+    _close(gb, v["grad_b"])
+
+
+@pytest.mark.parametrize("size", ["tiny", "ref", "odd"])
+def test_gather_concat_matches_golden_vectors(size):
+    v = load_golden(f"{size}_gather_concat.safetensors")
+    out = O.gather_concat(v["u"], v["eps"], v["h"], v["m"], v["cell_idx"])
+    _close(out, v["v"])
+    N = v["h"].shape[1]
+    gu, ge, gh, gm = O.gather_concat_bwd(v["grad_v"], v["cell_idx"], N)
+    _close(gu, v["grad_u"])
+    _close(ge, v["grad_eps"])
+    _close(gh, v["grad_h"])
+    _close(gm, v["grad_m"])
+
+
+def test_golden_tiny_vector_has_padded_repeat():
+    """The tiny vector holds the case the dummy row exists for: a padded slot repeating a valid
+    slot's cell (``cell_idx=[[0,1],[2,2]]``, ``valid=[[1,1],[1,0]]``)."""
+    v = load_golden("tiny_gated_delta_update.safetensors")
+    assert v["cell_idx"].tolist() == [[0, 1], [2, 2]]
+    assert v["valid"].tolist() == [[1, 1], [1, 0]]
+
+
+def test_gated_update_bwd_equals_autograd():
+    g = torch.Generator().manual_seed(3)
+    B, N, d, K = 3, 7, 5, 4
+    h = torch.randn(B, N, d, generator=g, dtype=F64, requires_grad=True)
+    q = torch.randn(B, d, generator=g, dtype=F64, requires_grad=True)
+    c = torch.randn(B, K, d, generator=g, dtype=F64, requires_grad=True)
+    b = torch.rand(B, K, d, generator=g, dtype=F64, requires_grad=True)
+    cells = torch.stack([torch.randperm(N, generator=g)[:K] for _ in range(B)])
+    valid = torch.rand(B, K, generator=g) > 0.3
+    cells = torch.where(valid, cells, torch.zeros_like(cells))
+    age = torch.zeros(B, N, dtype=torch.int64)
+    h2, q2, _, h_old = O.gated_delta_update(h, q, age, cells, c, b, valid)
+    G = torch.randn(B, N, d, generator=g, dtype=F64)
+    gq = torch.randn(B, d, generator=g, dtype=F64)
+    want = torch.autograd.grad((h2 * G).sum() + (q2 * gq).sum(), [h, q, c, b])
+    got = O.gated_delta_update_bwd(cells.to(torch.int32), valid.to(torch.int32), c.detach(),
+                                   b.detach(), h_old.detach(), G, gq)
+    for x, y in zip(got, want):
+        _close(x, y, atol=1e-12, rtol=1e-12)
+
+
+# --------------------------------------------------------------------------------------------
+# the backward recurrence and the carried-state gradient against float64 autograd
+# --------------------------------------------------------------------------------------------
+
+
+def _recurrence_case(seed=7, B=3, T=9, N=5, K=3, d=4):
+    g = torch.Generator().manual_seed(seed)
+    c = torch.rand(B, T, K, d, generator=g, dtype=F64, requires_grad=True)
+    b = torch.rand(B, T, K, d, generator=g, dtype=F64, requires_grad=True)
+    cells = torch.stack([torch.stack([torch.randperm(N, generator=g)[:K] for _ in range(T)])
+                         for _ in range(B)])
+    valid = torch.rand(B, T, K, generator=g) > 0.3
+    cells = torch.where(valid, cells, torch.zeros_like(cells))
+    reset = torch.zeros(B, T, dtype=torch.bool)
+    reset[0, 0] = reset[1, 4] = reset[2, 7] = reset[2, 8] = True
+    w_pre = torch.randn(B, T, d, generator=g, dtype=F64)
+    w_post = torch.randn(B, T, d, generator=g, dtype=F64)
+    w_sel = torch.randn(B, T, K, d, generator=g, dtype=F64)
+    w_hT = torch.randn(B, N, d, generator=g, dtype=F64)
+    w_qT = torch.randn(B, d, generator=g, dtype=F64)
+    h0 = torch.rand(B, N, d, generator=g, dtype=F64, requires_grad=True)
+    q0 = torch.randn(B, d, generator=g, dtype=F64, requires_grad=True)
+    return locals()
+
+
+@pytest.mark.parametrize("carry_end", [False, True])
+def test_recurrence_equals_autograd_of_the_update_chain(carry_end):
+    """``split.recurrence_backward`` is the VJP of ``gated_delta_update`` and ``reset`` over the
+    window (the reference's own check, ``tests/test_p2_10_split_window.py:31-84``), extended with
+    the start-state outputs ``d_h0, d_q0`` and an end-state cotangent."""
+    s = _recurrence_case()
+    B, T, N, K, d = s["B"], s["T"], s["N"], s["K"], s["d"]
+    h, q = s["h0"], s["q0"]
+    age = torch.zeros(B, N, dtype=torch.int64)
+    pos = torch.zeros(B, dtype=torch.int64)
+    total = torch.zeros((), dtype=F64)
+    h_old = []
+    for t in range(T):
+        h, q, age, pos = O.reset_state(h, q, age, pos, s["reset"][:, t])
+        total = total + (q * s["w_pre"][:, t]).sum()
+        index = s["cells"][:, t, :, None].expand(B, K, d)
+        h_old.append(h.gather(1, index).detach())
+        h, q, age, _ = O.gated_delta_update(h, q, age, s["cells"][:, t], s["c"][:, t],
+                                            s["b"][:, t], s["valid"][:, t])
+        total = total + (q * s["w_post"][:, t]).sum()
+        chosen = h.gather(1, index)
+        total = total + (torch.where(s["valid"][:, t, :, None], chosen, 0.0) * s["w_sel"][:, t]).sum()
+    if carry_end:
+        total = total + (h * s["w_hT"]).sum() + (q * s["w_qT"]).sum()
+    want_c, want_b, want_h0, want_q0 = torch.autograd.grad(total, [s["c"], s["b"], s["h0"], s["q0"]])
+    got_c, got_b, got_h0, got_q0 = O.recurrence_backward(
+        s["c"].detach(), s["b"].detach(), torch.stack(h_old, dim=1), s["cells"], s["valid"],
+        s["reset"], N, s["w_pre"], s["w_post"], torch.where(s["valid"][..., None], s["w_sel"], 0.0),
+        s["w_hT"] if carry_end else None, s["w_qT"] if carry_end else None, carried=True)
+    for got, want in ((got_c, want_c), (got_b, want_b), (got_h0, want_h0), (got_q0, want_q0)):
+        _close(got, want, atol=1e-13, rtol=1e-12)
+    assert bool((got_c[~s["valid"]] == 0).all()) and bool((got_b[~s["valid"]] == 0).all())
+
+
+def test_carried_gradient_is_zero_through_a_reset_at_zero():
+    s = _recurrence_case()
+    reset = torch.ones(s["B"], s["T"], dtype=torch.bool)
+    _, _, d_h0, d_q0 = O.recurrence_backward(
+        s["c"].detach(), s["b"].detach(), s["c"].detach(), s["cells"], s["valid"], reset, s["N"],
+        s["w_pre"], s["w_post"], None, s["w_hT"], s["w_qT"], carried=True)
+    assert bool((d_h0 == 0).all()) and bool((d_q0 == 0).all())
+
+
+def test_recurrence_keeps_a_padded_nan_out():
+    """``tests/test_p2_10_split_window.py:87-100``."""
+    B, T, N, K, d = 1, 2, 3, 2, 2
+    c = torch.full((B, T, K, d), 0.5, dtype=F64)
+    c[0, 0, 1] = float("nan")
+    b = torch.full((B, T, K, d), 0.25, dtype=F64)
+    cells = torch.tensor([[[1, 0], [2, 0]]])
+    valid = torch.tensor([[[True, False], [True, False]]])
+    reset = torch.zeros(B, T, dtype=torch.bool)
+    ones = torch.ones(B, T, d, dtype=F64)
+    dc, db = O.recurrence_backward(c, b, torch.zeros_like(c), cells, valid, reset, N, None, ones,
+                                   None)
+    assert bool(torch.isfinite(dc).all()) and bool(torch.isfinite(db).all())
+
+
+def test_dense_recurrence_equals_autograd():
+    g = torch.Generator().manual_seed(5)
+    Bd, T, N, d = 2, 6, 4, 3
+    c = torch.rand(Bd, T, N, d, generator=g, dtype=F64, requires_grad=True)
+    b = torch.rand(Bd, T, N, d, generator=g, dtype=F64, requires_grad=True)
+    reset = torch.zeros(Bd, T, dtype=torch.bool)
+    reset[1, 3] = True
+    w_pre = torch.randn(Bd, T, d, generator=g, dtype=F64)
+    w_post = torch.randn(Bd, T, d, generator=g, dtype=F64)
+    h = torch.rand(Bd, N, d, generator=g, dtype=F64)
+    q = h.mean(dim=1)
+    total = torch.zeros((), dtype=F64)
+    h_old = []
+    for t in range(T):
+        row = reset[:, t]
+        h = h.masked_fill(row[:, None, None], 0)
+        q = q.masked_fill(row[:, None], 0)
+        total = total + (q * w_pre[:, t]).sum()
+        h_old.append(h.detach())
+        h = (1 - b[:, t]) * h + b[:, t] * c[:, t]
+        q = h.mean(dim=1)
+        total = total + (q * w_post[:, t]).sum()
+    want = torch.autograd.grad(total, [c, b])
+    got = O.dense_recurrence_backward(c.detach(), b.detach(), torch.stack(h_old, dim=1), reset, N,
+                                      w_pre, w_post)
+    for x, y in zip(got, want):
+        _close(x, y, atol=1e-13, rtol=1e-12)
+
+
+# --------------------------------------------------------------------------------------------
+# the router: known answers, brute force, threshold and probes
+# --------------------------------------------------------------------------------------------
+
+
+def test_router_known_answers():
+    """``tests/test_p2_1_router.py:443-453``: all-equal logits select cells ``0..K-1`` with unit 0;
+    a two-way tie between cells 9 and 2 puts the lower index first; a unit tie picks unit 0."""
+    N, M = 16, 4
+    cost = torch.full((M,), 1.0 / (N * M))
+    cells, units, valid, theta, _ = O.router_select(torch.zeros(2, N, M), None, cost, k=5)
+    assert cells.tolist() == [[0, 1, 2, 3, 4]] * 2 and units.tolist() == [[0] * 5] * 2
+    assert bool(valid.all())
+    tied = torch.zeros(1, N, M)
+    tied[0, 9, 3] = 1.0
+    tied[0, 2, 0] = 1.0
+    tied[0, 2, 1] = 1.0
+    cells, units, *_ = O.router_select(tied, None, cost, k=3)
+    assert cells[0].tolist() == [2, 9, 0] and units[0].tolist() == [0, 3, 0]
+
+
+def _f32(x):
+    return float(np.float32(x))
+
+
+def _brute_select(scores_cell, unit_arg, cost, K, limit, shared, overhead, age=None, age_max=0,
+                  probes=False, reserved=0, fixed_units=False, M=1):
+    """A direct restatement on Python lists: stable order by (-score, index) with NaN first,
+    budget by a double running sum rounded to fp32, the threshold from its definition, the
+    probes by repeated stalest-first picks."""
+    N = len(scores_cell)
+
+    # reserved first (+inf), then NaN (torch sorts NaN above +inf: handled by explicit rank)
+    nan_cells = [n for n in range(reserved, N) if math.isnan(scores_cell[n])]
+    rest = [n for n in range(reserved, N) if not math.isnan(scores_cell[n])]
+    rest.sort(key=lambda n: (-scores_cell[n], n))
+    order = nan_cells + list(range(reserved)) + rest if nan_cells else list(range(reserved)) + rest
+    top = order[:K]
+    units = [(k % M) if (fixed_units and k < reserved) else unit_arg[c] for k, c in enumerate(top)]
+    acc = 0.0
+    valid = []
+    for u in units:
+        acc += _f32(_f32(overhead) + cost[u])
+        valid.append(_f32(_f32(shared) + _f32(acc)) <= _f32(limit))
+    cells = [c if v else 0 for c, v in zip(top, valid)]
+    units = [u if v else 0 for u, v in zip(units, valid)]
+    sel = {c for c, v in zip(cells, valid) if v}
+    lo = [scores_cell[n] for n in sel if n >= reserved]
+    hi = [scores_cell[n] for n in range(N) if n not in sel]
+
+    def amin(xs):
+        return math.nan if any(math.isnan(x) for x in xs) else (min(xs) if xs else math.inf)
+
+    def amax(xs):
+        return math.nan if any(math.isnan(x) for x in xs) else (max(xs) if xs else -math.inf)
+
+    theta = _f32(0.5 * _f32(amin(lo) + amax(hi)))
+    refreshed = [False] * K
+    if probes:
+        n_valid = sum(valid)
+        stale = [n for n in range(N) if age[n] > age_max and n not in sel]
+        n_force = min(len(stale), max(n_valid - reserved, 0))
+        stale.sort(key=lambda n: (-_f32(age[n]), n))
+        new_cells, new_units = list(cells), list(units)
+        for j in range(n_force):
+            kk = n_valid - 1 - j
+            new_cells[kk] = stale[j]
+            new_units[kk] = unit_arg[stale[j]]
+            refreshed[kk] = True
+        spent = 0.0
+        for u, v in zip(new_units, valid):
+            spent = _f32(spent + (_f32(_f32(overhead) + cost[u]) if v else 0.0))
+        if _f32(_f32(shared) + spent) > _f32(limit):
+            refreshed = [False] * K
+        else:
+            cells, units = new_cells, new_units
+    return cells, units, valid, theta, refreshed
+
+
+@pytest.mark.parametrize("trial", range(24))
+def test_router_matches_brute_force(trial):
+    g = torch.Generator().manual_seed(100 + trial)
+    B, N, M = 3, 9, 1 + trial % 3
+    K = 1 + trial % 6
+    logits = torch.randn(B, N, M, generator=g)
+    if trial % 2:
+        logits = (logits * 2).round() / 2  # exact ties between cells and between units
+    if trial % 5 == 0:
+        logits[0, 3, 0] = float("nan")
+    cost = torch.tensor([0.125, 0.0625, 0.25][:M])  # dyadic: sums are order-independent
+    overhead = 0.0625 if trial % 4 == 1 else 0.0
+    shared = 0.125 if trial % 3 == 2 else 0.0
+    limit = [10.0, 0.3, 0.5][trial % 3]
+    reserved = 2 if (trial % 7 == 3 and K > 2) else 0
+    fixed_units = reserved > 0 and trial % 2 == 1
+    age = torch.randint(0, 6, (B, N), generator=g)
+    probes = trial % 3 != 0
+    cells, units, valid, theta, refreshed = O.router_select(
+        logits, age, cost, k=K, age_max=2, probes=probes, cell_overhead=overhead,
+        shared_cost=shared, limit=limit, reserved=reserved, reserved_units=fixed_units)
+    for r in range(B):
+        sc = logits[r].float().amax(dim=-1).tolist()
+        ua = logits[r].float().argmax(dim=-1).tolist()
+        want = _brute_select(sc, ua, cost.tolist(), K, limit, shared, overhead, age=age[r].tolist(),
+                             age_max=2, probes=probes, reserved=reserved, fixed_units=fixed_units,
+                             M=M)
+        assert cells[r].tolist() == want[0]
+        assert units[r].tolist() == want[1]
+        assert valid[r].tolist() == want[2]
+        th = float(theta[r])
+        assert (math.isnan(th) and math.isnan(want[3])) or th == want[3]
+        assert refreshed[r].tolist() == want[4]
+
+
+def test_router_enumerates_stable_order_exhaustively():
+    """Every assignment of scores from {0, 0.5, 1} to 4 cells: the selected cells are the first
+    K of the permutation sorted by (descending score, ascending index)."""
+    N, K = 4, 2
+    cost = torch.tensor([1.0 / N])
+    for values in itertools.product([0.0, 0.5, 1.0], repeat=N):
+        logits = torch.tensor(values).reshape(1, N, 1)
+        cells, *_ = O.router_select(logits, None, cost, k=K)
+        want = sorted(range(N), key=lambda n: (-values[n], n))[:K]
+        assert cells[0].tolist() == want
+
+
+def test_router_theta_conventions():
+    N = 4
+    cost = torch.tensor([1.0 / N])
+    logits = torch.tensor([[[1.0], [2.0], [3.0], [4.0]]])
+    *_, theta, _ = O.router_select(logits, None, cost, k=2)
+    assert float(theta[0]) == 2.5  # midpoint of 3 (lowest in) and 2 (highest out)
+    *_, theta, _ = O.router_select(logits, None, cost, k=4)
+    assert float(theta[0]) == -math.inf  # everything selected
+    *_, theta, _ = O.router_select(logits, None, cost, k=2, limit=0.0)
+    assert float(theta[0]) == math.inf  # nothing selected
+
+
+# --------------------------------------------------------------------------------------------
+# the window: composition and invariants, and its backward against float64 autograd
+# --------------------------------------------------------------------------------------------
+
+
+def _tiny_window(seed=1, B=2, T=8, N=16, d=16, K=2, M=1, rms=False):
+    from hsn_amd.workload import CONFIGS, make_window
+
+    cfg = CONFIGS["tiny"].scaled(B=B, T=T, N=N, d=d, K=K, M=M, h0_sigma=0.3)
+    w = make_window(cfg, seed)
+    return cfg, w
+
+
+def test_window_forward_invariants():
+    cfg, w = _tiny_window()
+    out = O.window_forward(w["logits"], w["y"], w["gate_pre"], w["reset"], w["h0"], w["q0"],
+                           w["age0"], w["pos0"], w["cost"], k=cfg.K)
+    B, T, N, d = cfg.B, cfg.T, cfg.N, cfg.d
+    # q stays the mean of h (q0 = mean h0 and every update moves q by the mean delta)
+    _close(out["q"], out["h"].mean(dim=1), atol=1e-6, rtol=1e-5)
+    # ages and positions from a direct count
+    for r in range(B):
+        resets = [t for t in range(T) if w["reset"][r, t]]
+        lr = resets[-1] if resets else -1
+        assert int(out["pos"][r]) == (T - lr if lr >= 0 else T)
+        for n in range(N):
+            sel = [t for t in range(T) if bool(((out["cells"][r, t] == n) & out["valid"][r, t]).any())]
+            ls = sel[-1] if sel else -1
+            want = T - 1 - ls if (ls >= 0 and ls >= lr) else (T - lr if lr >= 0 else T)
+            assert int(out["age"][r, n]) == want
+    # h_sel of a valid slot is the updated state; h_old the pre-round one
+    assert out["h_sel"].shape == (B, T, cfg.K, d) and out["h_old"].shape == (B, T, cfg.K, d)
+
+
+@pytest.mark.parametrize("rms", [False, True])
+def test_window_backward_equals_autograd_of_the_forward(rms):
+    """``window_backward`` (recurrence + activation VJPs + carried state) is the float64 autograd
+    gradient of a window objective built from the restated forward chain."""
+    cfg, w = _tiny_window(B=2, T=7, N=6, d=5, K=3)
+    g = torch.Generator().manual_seed(11)
+    B, T, N, d, K = cfg.B, cfg.T, cfg.N, cfg.d, cfg.K
+    y = w["y"].to(F64).requires_grad_(True)
+    gp = w["gate_pre"].to(F64).requires_grad_(True)
+    h0 = w["h0"].to(F64).requires_grad_(True)
+    q0 = w["q0"].to(F64).detach().requires_grad_(True)
+    cw = (torch.rand(d, generator=g, dtype=F64) + 0.5).requires_grad_(True) if rms else None
+    w_pre = torch.randn(B, T, d, generator=g, dtype=F64)
+    w_post = torch.randn(B, T, d, generator=g, dtype=F64)
+    w_sel = torch.randn(B, T, K, d, generator=g, dtype=F64)
+    w_hT = torch.randn(B, N, d, generator=g, dtype=F64)
+    w_qT = torch.randn(B, d, generator=g, dtype=F64)
+    reset = w["reset"].clone()
+    reset[1, 3] = True
+    total = O.window_objective_f64(w["logits"], y, gp, reset, h0, q0, w["cost"], K, w_pre, w_post,
+                                   w_sel, w_hT, w_qT, cand_norm=rms, cand_w=cw)
+    wanted = [y, gp, h0, q0] + ([cw] if rms else [])
+    want = torch.autograd.grad(total, wanted)
+    fwd = O.window_forward(w["logits"], y.detach(), gp.detach(), reset, h0.detach(), q0.detach(),
+                           w["age0"], w["pos0"], w["cost"], k=K, cand_norm=rms,
+                           cand_w=None if cw is None else cw.detach())
+    # window_backward computes in fp32 on widened inputs; rebuild it in float64 for the pin
+    yf = y.detach().requires_grad_(True)
+    gf = gp.detach().requires_grad_(True)
+    wf = None if cw is None else cw.detach().requires_grad_(True)
+    c = O.candidate(yf, rms, wf)
+    b = O.gate(gf)
+    dc, db, d_h0, d_q0 = O.recurrence_backward(
+        c.detach(), b.detach(), fwd["h_old"].to(F64), fwd["cells"], fwd["valid"], reset, N, w_pre,
+        w_post, torch.where(fwd["valid"][..., None], w_sel, 0.0), w_hT, w_qT, carried=True)
+    inputs = [yf, gf] + ([wf] if rms else [])
+    got = list(torch.autograd.grad([c, b], inputs, [dc, db]))
+    got = got[:2] + [d_h0, d_q0] + got[2:]
+    for x, ref in zip(got, want):
+        _close(x, ref, atol=1e-12, rtol=1e-10)
+    # and the fp32 entry point agrees with the float64 pin to fp32 rounding
+    dy, dg, dh0, dq0, dw = O.window_backward(
+        w["y"], w["gate_pre"], fwd["h_old"].float(), fwd["cells"], fwd["valid"], reset, N,
+        w_pre.float(), w_post.float(), w_sel.float(), w_hT.float(), w_qT.float(), cand_norm=rms,
+        cand_w=None if cw is None else cw.detach().float())
+    for x, ref in zip([dy, dg, dh0, dq0] + ([dw] if rms else []), want):
+        _close(x.double(), ref, atol=2e-5, rtol=2e-4)
+
+
+def test_planted_mistake_fails_the_pin():
+    """A dropped summary term (``share``) in the sweep is caught by the autograd comparison."""
+    s = _recurrence_case()
+    N = s["N"]
+
+    def broken(c, b, h_old, cells, valid, reset, n, dpre, dpost, dsel):
+        # the sweep without R / N in g: a plausible dropped term
+        return O.recurrence_backward(c, b, h_old, cells, valid, reset, n, None, None, dsel)
+
+    B, T, K, d = s["B"], s["T"], s["K"], s["d"]
+    h, q = s["h0"], s["q0"]
+    age = torch.zeros(B, N, dtype=torch.int64)
+    pos = torch.zeros(B, dtype=torch.int64)
+    total = torch.zeros((), dtype=F64)
+    h_old = []
+    for t in range(T):
+        h, q, age, pos = O.reset_state(h, q, age, pos, s["reset"][:, t])
+        total = total + (q * s["w_pre"][:, t]).sum()
+        h_old.append(h.gather(1, s["cells"][:, t, :, None].expand(B, K, d)).detach())
+        h, q, age, _ = O.gated_delta_update(h, q, age, s["cells"][:, t], s["c"][:, t],
+                                            s["b"][:, t], s["valid"][:, t])
+        total = total + (q * s["w_post"][:, t]).sum()
+    want_c, _ = torch.autograd.grad(total, [s["c"], s["b"]])
+    got_c, _ = broken(s["c"].detach(), s["b"].detach(), torch.stack(h_old, 1), s["cells"],
+                      s["valid"], s["reset"], N, s["w_pre"], s["w_post"], None)
+    assert not torch.allclose(got_c, want_c)
