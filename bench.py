@@ -1,0 +1,201 @@
+"""Benchmark of the window hot path on one MI355X: window positions/s, fwd+bwd, at the ref shape.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config ref] [--no-cpu]
+
+A step is one window of the configuration, inputs resident in HBM: the router
+(``hsn_win_route``), the forward sweep (``hsn_win_forward``) and the backward with the
+carried-state gradient (``hsn_win_backward``). ``value`` is positions/s over the K timed steps
+(B*T positions per step, bracketed by synchronisations). Each kernel's average duration is
+measured with HIP events recorded on the stream the kernels run on (torch's current stream);
+``roofline`` reports the dominant kernel's algorithmic bytes per launch (the byte model of
+``hsn_amd.workload.byte_model``) over its average duration against the 8 TB/s HBM peak.
+``cpu_baseline`` times the repository's CPU oracle (the reference's profile:cpu algorithm) on a
+bounded sample of the same workload on the host cores. One GPU only: ``--gpus`` above 1 exits.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def _args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--config", default="ref")
+    p.add_argument("--seed", type=int, default=1)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-h-max", action="store_true", help="do not produce the row maxima")
+    return p.parse_args()
+
+
+def _traffic(workload: str):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter summary
+    (profiles/traffic_<workload>.json), or None."""
+    path = ROOT / "profiles" / f"traffic_{workload}.json"
+    if not path.is_file():
+        return None
+    try:
+        return json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+
+
+def _cpu_baseline(cfg, seed):
+    """The CPU oracle on one full window of the configuration (or a prefix of its positions for
+    the large configurations), on all host cores."""
+    import torch
+
+    from hsn_amd.workload import make_cotangents, make_window
+    from oracle import hsn_oracle as O
+
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    T = cfg.T if cfg.B * cfg.T <= 8192 else max(8, 8192 // cfg.B)
+    sample = cfg.scaled(T=T)
+    w = make_window(sample, seed)
+    c = make_cotangents(sample, seed)
+    kw = dict(k=sample.K)
+    # warm-up on two positions
+    short = {k: (v[:, :2] if k in ("logits", "y", "gate_pre", "reset") else v) for k, v in w.items()}
+    O.window_forward(short["logits"], short["y"], short["gate_pre"], short["reset"], w["h0"], w["q0"],
+                     w["age0"], w["pos0"], w["cost"], **kw)
+    t0 = time.perf_counter()
+    f = O.window_forward(w["logits"], w["y"], w["gate_pre"], w["reset"], w["h0"], w["q0"],
+                         w["age0"], w["pos0"], w["cost"], **kw)
+    O.window_backward(w["y"], w["gate_pre"], f["h_old"], f["cells"], f["valid"], w["reset"],
+                      sample.N, c["d_q_pre"], c["d_q_post"],
+                      torch.where(f["valid"][..., None], c["d_h_sel"].float(), 0.0).to(c["d_h_sel"].dtype),
+                      c["d_h_T"], c["d_q_T"])
+    secs = time.perf_counter() - t0
+    positions = sample.B * sample.T
+    return {
+        "value": positions / secs,
+        "unit": "positions/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{sample.B} rows x {sample.T} positions of the {cfg.name} window, fwd+bwd, "
+                  f"the repository's PyTorch-CPU oracle ({secs:.2f} s)",
+    }
+
+
+def main() -> int:
+    args = _args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the window path "
+              "shards over rows with no exchange, see DESIGN.md", file=sys.stderr)
+        return 2
+    import torch
+
+    from hsn_amd import window
+    from hsn_amd.workload import CONFIGS, byte_model, describe, make_cotangents, make_window
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    w = {k: v.to(dev) for k, v in make_window(cfg, args.seed).items()}
+    cot = make_cotangents(cfg, args.seed, carried=True)
+    cot = {k: (None if v is None else v.to(dev)) for k, v in cot.items()}
+    rcfg = window.RouteConfig(k=cfg.K)
+    B, T, N, d, K = cfg.B, cfg.T, cfg.N, cfg.d, cfg.K
+
+    def step(ev=None):
+        h_max = None if args.no_h_max else torch.empty(B, T, device=dev)
+        if ev:
+            ev[0].record()
+        cells, units, valid, theta, refreshed = window.route(w["logits"], w["cost"], rcfg,
+                                                             h_max_zero=h_max)
+        if ev:
+            ev[1].record()
+        out = window.forward(w["y"], w["gate_pre"], w["reset"], cells, valid, w["h0"], w["q0"],
+                             w["age0"], w["pos0"], N, h_max=h_max)
+        if ev:
+            ev[2].record()
+        grads = window.backward(w["y"], w["gate_pre"], out["h_old"], cells, valid, w["reset"], N,
+                                cot["d_q_pre"], cot["d_q_post"], cot["d_h_sel"], cot["d_h_T"],
+                                cot["d_q_T"])
+        if ev:
+            ev[3].record()
+        return out, grads
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    secs = time.perf_counter() - t0
+    per_kernel = {"route": 0.0, "forward": 0.0, "backward": 0.0}
+    for ev in events:
+        per_kernel["route"] += ev[0].elapsed_time(ev[1])
+        per_kernel["forward"] += ev[1].elapsed_time(ev[2])
+        per_kernel["backward"] += ev[2].elapsed_time(ev[3])
+    per_kernel = {k: v / args.steps for k, v in per_kernel.items()}  # ms per launch
+
+    bm = byte_model(cfg)
+    positions = B * T
+    algo = {  # algorithmic bytes per launch
+        "route": bm["route"] * positions,
+        "forward": bm["forward_update"] * positions,
+        "backward": bm["backward"] * positions,
+    }
+    dominant = max(per_kernel, key=per_kernel.get)
+    achieved = algo[dominant] / (per_kernel[dominant] * 1e-3) / 1e9
+    ms_per_step = secs / args.steps * 1e3
+    window_gbs = bm["window_bytes"] / (ms_per_step * 1e-3) / 1e9
+    traffic = _traffic(cfg.name)
+    result = {
+        "metric": "window positions/sec fwd+bwd at ref shape (1 GPU); achieved HBM GB/s vs peak",
+        "value": positions / (ms_per_step * 1e-3),
+        "unit": "positions/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.io == "bf16" else "f32",
+        "data": "synthetic (seeded workload generator, hsn_amd/workload.py)",
+        "config": {"workload": cfg.name, "shape": describe(cfg), "B": B, "T": T, "N": N, "d": d,
+                   "K": K, "M": cfg.M, "storage": cfg.io, "h_max": not args.no_h_max,
+                   "parallelism": "single GPU"},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dominant,
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None if traffic is None else traffic.get(dominant),
+        },
+        "kernels_ms": per_kernel,
+        "kernels_gbs": {k: algo[k] / (per_kernel[k] * 1e-3) / 1e9 for k in per_kernel},
+        "window_gbs": window_gbs,
+        "window_frac": window_gbs / HBM_PEAK_GBS,
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = _cpu_baseline(cfg, args.seed)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

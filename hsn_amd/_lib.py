@@ -1,0 +1,95 @@
+"""The C ABI of ``libhsn_amd.so`` (``include/hsn_window.h``, ``include/hsn_ops.h``) via ctypes.
+
+The library is the product: every operator in :mod:`hsn_amd` reaches the GPU through these
+entry points, and nothing here falls back to another implementation. :func:`library` raises a
+``RuntimeError`` when the library is missing or was built from other sources, and
+:func:`call` turns a non-zero status into a ``RuntimeError`` carrying the library's message.
+Loading the library initialises no GPU context; the first kernel launch does.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_char_p, c_float, c_int, c_int64, c_void_p
+from functools import lru_cache
+
+from . import build as _build
+
+HSN_OK = 0
+STATUS = {
+    1: "HSN_ERR_INVALID_ARGUMENT",
+    2: "HSN_ERR_UNSUPPORTED_DTYPE",
+    3: "HSN_ERR_INDEX_OUT_OF_RANGE",
+    4: "HSN_ERR_DUPLICATE_INDEX",
+    5: "HSN_ERR_SIZE_OVERFLOW",
+    6: "HSN_ERR_BAD_GRAPH",
+    7: "HSN_ERR_BACKEND",
+}
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+
+P, I, F, L = c_void_p, c_int, c_float, c_int64
+
+#: argument types of every exported entry point, in declaration order of the headers
+SIGNATURES: dict[str, list] = {
+    "hsn_win_abi_version": [],
+    "hsn_win_last_error": [],
+    "hsn_win_route": [P, I, L, P, P, P, P, P, I, P, P, P, P, I, I, I, I, I, I, I, F, F, F, F, I, I,
+                      P],
+    "hsn_win_select": [P, I, L, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, F, F, F, F, I, I, P],
+    "hsn_win_forward": [P, P, I, P, I, F, P, P, P, P, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I,
+                        I, I, I, P],
+    "hsn_win_backward": [P, P, P, I, P, I, F, P, P, P, I, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I,
+                         I, P],
+    "hsn_win_recurrence": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P],
+    "hsn_win_recurrence_dense": [P, P, P, P, P, P, P, P, I, I, I, I, P],
+    "hsn_win_cell_update": [P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I,
+                            I, I, I, I, I, P],
+    "hsn_gather_concat": [P, P, P, P, P, P, I, I, I, I, I, P],
+    "hsn_gather_concat_bwd": [P, P, P, P, P, P, I, I, I, I, I, I, P],
+    "hsn_gated_delta_update": [P, P, P, P, P, P, P, P, I, I, I, I, I, P],
+    "hsn_gated_delta_update_bwd": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P],
+}
+
+_lock = threading.Lock()
+
+
+@lru_cache(maxsize=1)
+def library() -> ctypes.CDLL:
+    """The loaded library (built in-tree and matching its sources), else ``RuntimeError``."""
+    with _lock:
+        why = _build.stale()
+        if why is not None:
+            raise RuntimeError(f"hsn_amd HIP library unusable: {why}")
+        lib = ctypes.CDLL(str(_build.LIBRARY))
+        for name, args in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = c_char_p if name == "hsn_win_last_error" else c_int
+        return lib
+
+
+def available() -> bool:
+    """Whether the library is built and current (no load, no GPU work)."""
+    return _build.stale() is None
+
+
+def call(name: str, *args) -> None:
+    """Call entry point ``name``; a non-zero status raises ``RuntimeError``."""
+    lib = library()
+    status = getattr(lib, name)(*args)
+    if status != HSN_OK:
+        message = lib.hsn_win_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name}: {STATUS.get(status, status)}: {message}")
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (``None`` for an absent optional tensor)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device) -> int:
+    """The current torch stream of ``device`` as a hipStream_t handle."""
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

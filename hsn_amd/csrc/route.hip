@@ -1,0 +1,484 @@
+// The router's hard top-k decision on gfx950: one 64-lane wavefront per position.
+//
+// Restates Router.select(mode="topk") (reference python/hsn/model/router.py:1263-1417: scores
+// :1246-1252, _topk :1640-1648, _truncate :1650-1657, _ste_threshold :1771-1786, the refresh
+// probes of _post_process :1788-1850) so that the integer outputs are bit-identical to the CPU
+// path on the same inputs.
+//
+// Layout: lane l holds cells n = l + 64 i (i < NPL), so a position's logits are read with
+// coalesced loads. The K winners are found by K rounds of a wavefront argmax over a total-order
+// key (descending score, ties by ascending index, NaN above +inf, -0 equal to +0, reserved cells
+// at +inf); each lane keeps its own best so a round costs one cross-lane reduction plus one
+// lane's rescan. Without probes the positions are independent (the logits are inputs), so the
+// whole window is one launch with a wavefront per (row, position); with probes the ages evolve
+// with the decisions and one wavefront walks a row's positions in order, its ages in VGPRs.
+#include "common.cuh"
+
+namespace hsn {
+namespace {
+
+struct RouteArgs {
+    const void* logits;
+    int64_t l_row, l_pos, width;  // element offset of (b, p, n, j) = b*l_row + p*l_pos + n*width + j
+    const float* cost;
+    const int64_t* age;  // per-position form: [B, n_age, N], record `age_rec` of row b
+    int64_t age_row, age_rec;
+    const int64_t* age0;  // window form with probes: [B, N]
+    const uint8_t* reset;  // window form with probes: [B, P]
+    void* cells;
+    void* units;
+    uint8_t* valid;
+    uint8_t* refreshed;
+    int64_t o_row, o_pos;  // output slot offset of (b, p, k) = b*o_row + p*o_pos + k
+    float* theta;
+    int64_t th_row, th_pos;
+    float* h_max_zero;  // [B, P] (optional)
+    int B, P, N, M, K, age_max, probes, reserved, fixed_units;
+    float lambda, overhead, shared, limit;
+};
+
+// (key, n) ordering: a before b in the stable descending order.
+__device__ __forceinline__ bool before(uint32_t ka, int na, uint32_t kb, int nb) {
+    return ka > kb || (ka == kb && na < nb);
+}
+
+// Wavefront argmax of (key, n) pairs: the largest key, the smallest n among equal keys.
+__device__ __forceinline__ void wave_argmax(uint32_t k, int n, uint32_t& wk, int& wn) {
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) {
+        const uint32_t ko = wave_shfl_xor(k, m);
+        const int no = wave_shfl_xor(n, m);
+        if (before(ko, no, k, n)) {
+            k = ko;
+            n = no;
+        }
+    }
+    wk = k;
+    wn = n;
+}
+
+__device__ __forceinline__ float wave_nan_min(float v) {
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) v = nan_min(v, wave_shfl_xor(v, m));
+    return v;
+}
+__device__ __forceinline__ float wave_nan_max(float v) {
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) v = nan_max(v, wave_shfl_xor(v, m));
+    return v;
+}
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) v += wave_shfl_xor(v, m);
+    return v;
+}
+
+template <typename IDX>
+__device__ __forceinline__ void store_index(void* p, int64_t i, int v) {
+    static_cast<IDX*>(p)[i] = static_cast<IDX>(v);
+}
+
+// The decision of one position. `ages` (probes only) are this lane's cells' ages on entry and
+// are ticked in place on exit when `tick` is set (the window form walks a row).
+template <int NPL, typename IO, typename IDX>
+__device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], bool tick) {
+    const int lane = lane_id();
+    const int N = a.N, M = a.M, K = a.K, R = a.reserved;
+    const IO* logits = static_cast<const IO*>(a.logits) + b * a.l_row + p * a.l_pos;
+    const bool scale_cost = a.lambda > 0.0f;
+
+    // scores, units and sort keys of this lane's cells
+    float sc[NPL];
+    int unit[NPL];
+    uint32_t key[NPL];
+    int slot_of[NPL];  // 1 + the scored slot that took the cell, 0 if none
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const int n = lane + kWave * i;
+        sc[i] = -INFINITY;
+        unit[i] = 0;
+        key[i] = 0u;  // below every real key: never chosen
+        slot_of[i] = 0;
+        if (n < N) {
+            const IO* row = logits + static_cast<int64_t>(n) * a.width;
+            float best = to_f32(row[0]);
+            if (scale_cost) best = __fsub_rn(best, __fmul_rn(a.lambda, a.cost[0]));
+            int arg = 0;
+            for (int j = 1; j < M; ++j) {
+                float s = to_f32(row[j]);
+                if (scale_cost) s = __fsub_rn(s, __fmul_rn(a.lambda, a.cost[j]));
+                // amax / argmax: the first maximiser, a NaN counts as the maximum (first NaN)
+                if (best == best && (s > best || s != s)) {
+                    best = s;
+                    arg = j;
+                }
+            }
+            sc[i] = best;
+            unit[i] = arg;
+            key[i] = n < R ? kKeyPosInf : score_key(best);
+        }
+    }
+
+    // this lane's best remaining (key, n)
+    uint32_t bk = 0u;
+    int bn = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        if (key[i] > bk) {  // strict: the first (smallest n) of equal keys stays
+            bk = key[i];
+            bn = lane + kWave * i;
+        }
+    }
+
+    // K rounds of a wavefront argmax; lane k keeps slot k's cell, score and unit
+    int my_cell = 0, my_unit = 0;
+    float my_score = 0.0f;
+    for (int r = 0; r < K; ++r) {
+        uint32_t wk;
+        int wn;
+        wave_argmax(bk, bn, wk, wn);
+        const int wl = wn & (kWave - 1), wi = wn >> 6;
+        float ws = 0.0f;
+        int wu = 0;
+        if (lane == wl) {
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                if (i == wi) {
+                    ws = sc[i];
+                    wu = unit[i];
+                    key[i] = 0u;
+                    slot_of[i] = r + 1;
+                }
+            }
+            bk = 0u;
+            bn = 0x7fffffff;
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                if (key[i] > bk) {
+                    bk = key[i];
+                    bn = lane + kWave * i;
+                }
+            }
+        }
+        ws = readlane(ws, wl);
+        wu = readlane(wu, wl);
+        if (lane == r) {
+            my_cell = wn;
+            my_score = ws;
+            my_unit = (a.fixed_units && r < R) ? r % M : wu;
+        }
+    }
+
+    // the budget: per-slot cost, prefix sums accumulated in double in slot order and rounded to
+    // fp32 per slot (torch's CPU cumsum of fp32), then the shared cost and the limit in fp32
+    const bool is_slot = lane < K;
+    const float per_slot = is_slot ? __fadd_rn(a.overhead, a.cost[my_unit]) : 0.0f;
+    double acc = 0.0;
+    for (int j = 0; j < K; ++j) {
+        const float v = readlane(per_slot, j);
+        if (j <= lane) acc += static_cast<double>(v);
+    }
+    const float cumulative = __fadd_rn(a.shared, static_cast<float>(acc));
+    const bool ok = is_slot && cumulative <= a.limit;
+    const uint64_t vmask = ballot(ok);
+    const int n_valid = __popcll(vmask);
+
+    // the threshold of the scored decision: lowest selected (scored slots only) and highest
+    // unselected score, NaN-propagating
+    float low = (ok && my_cell >= R) ? my_score : INFINITY;
+    low = wave_nan_min(low);
+    float high = -INFINITY;
+    int n_stale = 0;
+    bool stale[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const int n = lane + kWave * i;
+        const bool sel = slot_of[i] > 0 && ((vmask >> (slot_of[i] - 1)) & 1ull);
+        if (n < N && !sel) high = nan_max(high, sc[i]);
+        stale[i] = a.probes && n < N && !sel && ages[i] > static_cast<int64_t>(a.age_max);
+        n_stale += stale[i] ? 1 : 0;
+    }
+    high = wave_nan_max(high);
+    const float th = 0.5f * (low + high);
+
+    int out_cell = ok ? my_cell : 0;
+    int out_unit = ok ? my_unit : 0;
+    bool out_refreshed = false;
+    int probe_of[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) probe_of[i] = 0;
+    bool over = true;  // no probes taken yet: the scored selection stands
+
+    if (a.probes) {
+        n_stale = wave_sum(n_stale);
+        const int scored_slots = n_valid > R ? n_valid - R : 0;
+        const int n_force = n_stale < scored_slots ? n_stale : scored_slots;
+        if (n_force > 0) {
+            // the stalest first (age as fp32, descending), equal ages in index order
+            uint32_t pk[NPL];
+            uint32_t qk = 0u;
+            int qn = 0x7fffffff;
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                pk[i] = stale[i] ? __float_as_uint(static_cast<float>(ages[i])) + 1u : 0u;
+                if (pk[i] > qk) {
+                    qk = pk[i];
+                    qn = lane + kWave * i;
+                }
+            }
+            int new_cell = out_cell, new_unit = out_unit;
+            bool replaced = false;
+            for (int j = 0; j < n_force; ++j) {
+                uint32_t wk;
+                int wn;
+                wave_argmax(qk, qn, wk, wn);
+                const int wl = wn & (kWave - 1), wi = wn >> 6;
+                int wu = 0;
+                if (lane == wl) {
+#pragma unroll
+                    for (int i = 0; i < NPL; ++i) {
+                        if (i == wi) {
+                            wu = unit[i];
+                            pk[i] = 0u;
+                            probe_of[i] = j + 1;
+                        }
+                    }
+                    qk = 0u;
+                    qn = 0x7fffffff;
+#pragma unroll
+                    for (int i = 0; i < NPL; ++i) {
+                        if (pk[i] > qk) {
+                            qk = pk[i];
+                            qn = lane + kWave * i;
+                        }
+                    }
+                }
+                wu = readlane(wu, wl);
+                if (lane == n_valid - 1 - j) {
+                    new_cell = wn;
+                    new_unit = wu;
+                    replaced = true;
+                }
+            }
+            // the budget guarantee: over the limit after the probes, keep the scored selection
+            const float cost_k = ok ? __fadd_rn(a.overhead, a.cost[new_unit]) : 0.0f;
+            float spent = 0.0f;
+            for (int j = 0; j < K; ++j) spent = __fadd_rn(spent, readlane(cost_k, j));
+            over = __fadd_rn(a.shared, spent) > a.limit;
+            if (!over) {
+                out_cell = new_cell;
+                out_unit = new_unit;
+                out_refreshed = replaced;
+            }
+        }
+    }
+
+    if (is_slot) {
+        const int64_t o = b * a.o_row + p * a.o_pos + lane;
+        store_index<IDX>(a.cells, o, out_cell);
+        store_index<IDX>(a.units, o, out_unit);
+        a.valid[o] = ok ? 1 : 0;
+        a.refreshed[o] = out_refreshed ? 1 : 0;
+    }
+    if (lane == 0) {
+        a.theta[b * a.th_row + p * a.th_pos] = th;
+        if (a.h_max_zero) a.h_max_zero[static_cast<int64_t>(b) * a.P + p] = 0.0f;
+    }
+
+    if (tick) {
+        // CellGraphState.tick: the final selection's cells restart at 0, every other cell ages
+        const uint64_t refreshed_slots = ballot(is_slot && out_refreshed);
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            bool sel = slot_of[i] > 0 && ((vmask >> (slot_of[i] - 1)) & 1ull);
+            if (!over) {
+                if (sel && ((refreshed_slots >> (slot_of[i] - 1)) & 1ull)) sel = false;
+                if (probe_of[i] > 0) sel = true;
+            }
+            ages[i] = sel ? 0 : ages[i] + 1;
+        }
+    }
+}
+
+// Whole window without probes: a wavefront per (row, position), four per workgroup.
+template <int NPL, typename IO, typename IDX>
+__global__ __launch_bounds__(256) void route_parallel(RouteArgs a) {
+    const int wave = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (wave >= a.B * a.P) return;
+    const int b = wave / a.P, p = wave - b * a.P;
+    int64_t ages[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) ages[i] = 0;
+    decide<NPL, IO, IDX>(a, b, p, ages, false);
+}
+
+// With probes (or the per-position form): one wavefront walks a row's positions in order.
+// Window form (a.age0): ages start at age0, a reset at p zeroes them before p reads them, and
+// each decision ticks them. Per-position form (a.age): the ages of record a.age_rec, P = 1.
+template <int NPL, typename IO, typename IDX>
+__global__ __launch_bounds__(64) void route_sequential(RouteArgs a) {
+    const int b = blockIdx.x;
+    const int lane = lane_id();
+    int64_t ages[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const int n = lane + kWave * i;
+        int64_t v = 0;
+        if (n < a.N) {
+            if (a.age0) v = a.age0[static_cast<int64_t>(b) * a.N + n];
+            else if (a.age) v = a.age[b * a.age_row + a.age_rec * a.N + n];
+        }
+        ages[i] = v;
+    }
+    for (int p = 0; p < a.P; ++p) {
+        if (a.reset && a.reset[static_cast<int64_t>(b) * a.P + p]) {
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) ages[i] = 0;
+        }
+        decide<NPL, IO, IDX>(a, b, p, ages, a.P > 1);
+    }
+}
+
+template <typename IO, typename IDX>
+hipError_t launch_route(const RouteArgs& a, bool sequential, hipStream_t stream) {
+    const int npl = (a.N + kWave - 1) / kWave;
+#define HSN_ROUTE_CASE(V)                                                                      \
+    if (npl <= V) {                                                                            \
+        if (sequential) {                                                                      \
+            hipLaunchKernelGGL((route_sequential<V, IO, IDX>), dim3(a.B), dim3(kWave), 0,      \
+                               stream, a);                                                     \
+        } else {                                                                               \
+            const int waves = a.B * a.P;                                                       \
+            hipLaunchKernelGGL((route_parallel<V, IO, IDX>), dim3((waves + 3) / 4), dim3(256),  \
+                               0, stream, a);                                                  \
+        }                                                                                      \
+        return hipGetLastError();                                                              \
+    }
+    HSN_ROUTE_CASE(1)
+    HSN_ROUTE_CASE(2)
+    HSN_ROUTE_CASE(4)
+    HSN_ROUTE_CASE(8)
+    HSN_ROUTE_CASE(16)
+    HSN_ROUTE_CASE(32)
+    HSN_ROUTE_CASE(64)
+#undef HSN_ROUTE_CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t dispatch_route(const RouteArgs& a, int io_dtype, int index_bits, bool sequential,
+                          hipStream_t stream) {
+    if (io_dtype == HSN_DTYPE_F32) {
+        return index_bits == 64 ? launch_route<float, int64_t>(a, sequential, stream)
+                                : launch_route<float, int32_t>(a, sequential, stream);
+    }
+    return index_bits == 64 ? launch_route<bf16_t, int64_t>(a, sequential, stream)
+                            : launch_route<bf16_t, int32_t>(a, sequential, stream);
+}
+
+}  // namespace
+}  // namespace hsn
+
+#include "abi_util.h"
+
+using namespace hsn;
+
+extern "C" int hsn_win_route(const void* logits, int io_dtype, int64_t width, const float* cost,
+                             const int64_t* age0, const uint8_t* reset, void* cells, void* units,
+                             int index_bits, uint8_t* valid, float* theta, uint8_t* refreshed,
+                             float* h_max_zero, int B, int T, int N, int M, int K, int age_max,
+                             int probes, float lambda_cost, float cell_overhead,
+                             float shared_cost, float limit, int reserved, int reserved_units,
+                             void* stream) {
+    HSN_ABI_BEGIN
+    HSN_REQUIRE(logits && cost && cells && units && valid && theta && refreshed,
+                HSN_ERR_INVALID_ARGUMENT, "hsn_win_route: a required pointer is NULL");
+    HSN_REQUIRE(B >= 1 && T >= 1 && N >= 1 && M >= 1 && K >= 1, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_route: dimensions must be >= 1");
+    HSN_REQUIRE(K <= N && K <= kWave, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_route: need K <= N and K <= 64");
+    HSN_REQUIRE(N <= 64 * kWave, HSN_ERR_INVALID_ARGUMENT, "hsn_win_route: N above 4096");
+    HSN_REQUIRE(width >= M, HSN_ERR_INVALID_ARGUMENT, "hsn_win_route: width < M");
+    HSN_REQUIRE(reserved >= 0 && reserved <= K, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_route: reserved must lie in [0, K]");
+    HSN_REQUIRE(index_bits == 32 || index_bits == 64, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_route: index_bits must be 32 or 64");
+    HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
+                HSN_ERR_UNSUPPORTED_DTYPE, "hsn_win_route: logits must be f32 or bf16");
+    HSN_REQUIRE(!probes || (age0 && reset), HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_route: probes need age0 and reset");
+    HSN_REQUIRE(check_elems({int64_t(B) * T * N * width, int64_t(B) * T * K, int64_t(B) * N}),
+                HSN_ERR_SIZE_OVERFLOW, "hsn_win_route: a tensor is too large");
+    RouteArgs a{};
+    a.logits = logits;
+    a.width = width;
+    a.l_pos = int64_t(N) * width;
+    a.l_row = int64_t(T) * a.l_pos;
+    a.cost = cost;
+    a.age0 = probes ? age0 : nullptr;
+    a.reset = probes ? reset : nullptr;
+    a.cells = cells;
+    a.units = units;
+    a.valid = valid;
+    a.refreshed = refreshed;
+    a.o_pos = K;
+    a.o_row = int64_t(T) * K;
+    a.theta = theta;
+    a.th_pos = 1;
+    a.th_row = T;
+    a.h_max_zero = h_max_zero;
+    a.B = B, a.P = T, a.N = N, a.M = M, a.K = K, a.age_max = age_max, a.probes = probes ? 1 : 0;
+    a.reserved = reserved, a.fixed_units = reserved_units ? 1 : 0;
+    a.lambda = lambda_cost, a.overhead = cell_overhead, a.shared = shared_cost, a.limit = limit;
+    HSN_HIP(dispatch_route(a, io_dtype, index_bits, probes != 0, as_stream(stream)));
+    HSN_ABI_END
+}
+
+extern "C" int hsn_win_select(const void* logits, int io_dtype, int64_t width, const int64_t* age,
+                              const float* cost, int64_t* cells, int64_t* units, uint8_t* valid,
+                              float* theta, uint8_t* refreshed, int B, int N, int M, int K, int t,
+                              int n_out, int n_age, int age_max, int probes, float lambda_cost,
+                              float cell_overhead, float shared_cost, float limit, int reserved,
+                              int reserved_units, void* stream) {
+    HSN_ABI_BEGIN
+    HSN_REQUIRE(logits && cost && cells && units && valid && theta && refreshed,
+                HSN_ERR_INVALID_ARGUMENT, "hsn_win_select: a required pointer is NULL");
+    HSN_REQUIRE(B >= 1 && N >= 1 && M >= 1 && K >= 1, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_select: dimensions must be >= 1");
+    HSN_REQUIRE(K <= N && K <= kWave && N <= 64 * kWave, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_select: need K <= N, K <= 64, N <= 4096");
+    HSN_REQUIRE(width >= M, HSN_ERR_INVALID_ARGUMENT, "hsn_win_select: width < M");
+    HSN_REQUIRE(t >= 0 && t < n_out && (!probes || (age && t < n_age)), HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_select: record t outside the tapes (or probes without ages)");
+    HSN_REQUIRE(reserved >= 0 && reserved <= K, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_select: reserved must lie in [0, K]");
+    HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
+                HSN_ERR_UNSUPPORTED_DTYPE, "hsn_win_select: logits must be f32 or bf16");
+    RouteArgs a{};
+    a.logits = logits;
+    a.width = width;
+    a.l_pos = 0;
+    a.l_row = int64_t(N) * width;
+    a.cost = cost;
+    a.age = probes ? age : nullptr;
+    a.age_row = int64_t(n_age) * N;
+    a.age_rec = t;
+    a.cells = cells;
+    a.units = units;
+    a.valid = valid;
+    a.refreshed = refreshed;
+    a.o_row = int64_t(n_out) * K;
+    a.o_pos = 0;
+    // the record offset rides on the base pointers
+    a.cells = cells + int64_t(t) * K;
+    a.units = units + int64_t(t) * K;
+    a.valid = valid + int64_t(t) * K;
+    a.refreshed = refreshed + int64_t(t) * K;
+    a.theta = theta + t;
+    a.th_row = n_out;
+    a.th_pos = 0;
+    a.B = B, a.P = 1, a.N = N, a.M = M, a.K = K, a.age_max = age_max, a.probes = probes ? 1 : 0;
+    a.reserved = reserved, a.fixed_units = reserved_units ? 1 : 0;
+    a.lambda = lambda_cost, a.overhead = cell_overhead, a.shared = shared_cost, a.limit = limit;
+    HSN_HIP(dispatch_route(a, io_dtype, 64, probes != 0, as_stream(stream)));
+    HSN_ABI_END
+}

@@ -1,0 +1,368 @@
+"""The reference's window-kernel module on MI355X: the same names, signatures, custom ops and
+decline convention as ``hsn.kernels.window`` (python/hsn/kernels/window.py:56-1143), backed by
+``libhsn_amd.so`` (``include/hsn_window.h``) instead of a CUDA fatbin.
+
+Convention, as there: a wrapper returns ``None`` for inputs it does not take (dtype, device,
+shape) so the caller keeps its own path; misuse raises; a missing or stale library raises on
+:func:`prepare`. Beyond the reference: no 48 KiB shared-memory ceiling (the recurrence and the
+update take any ``N`` whose state slice fits the 160 KiB LDS), the carried-state outputs
+(:func:`recurrence_backward_carried`), bf16 storage, and N up to 4096 in the router.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from .. import _lib
+from .._lib import DTYPE_BF16, DTYPE_F32, call, ptr, stream_of
+from ..state import CellGraphState
+
+_prepared: set[int] = set()
+
+#: LDS per workgroup on gfx950
+_MAX_LDS_BYTES = 160 * 1024
+#: the router's limits: one 64-lane wavefront per position, cells 64 per lane at most
+_MAX_SELECT_CELLS = 4096
+_MAX_SELECT_K = 64
+
+
+def available() -> bool:
+    """Library presence and freshness only: never initialises the GPU."""
+    return _lib.available()
+
+
+def prepare(device: int = 0) -> None:
+    """Load the library for ``device`` (idempotent); raises when it is missing or stale."""
+    _lib.library()
+    _prepared.add(int(device))
+
+
+def prepared(device: torch.device) -> bool:
+    return device.type == "cuda" and (device.index or 0) in _prepared
+
+
+def _slice_fits(n_cells: int, extra_per_cell: int = 0) -> bool:
+    return n_cells * (4 + extra_per_cell) <= _MAX_LDS_BYTES
+
+
+# --------------------------------------------------------------------------------------------
+# the backward recurrence (reference window.py:108-192)
+# --------------------------------------------------------------------------------------------
+
+
+def _recurrence(c, b, h_old, cells, valid, reset, n_cells, d_q_pre, d_q_post, d_h_sel, d_h_T,
+                d_q_T, carried):
+    if not prepared(c.device) or c.dtype != torch.float32 or cells.dtype != torch.int64:
+        return None
+    for cot in (d_q_pre, d_q_post, d_h_sel, d_h_T, d_q_T):
+        if cot is not None and cot.dtype != torch.float32:
+            return None
+    B, T, K, d = (int(n) for n in c.shape)
+    N = int(n_cells)
+    if not _slice_fits(N):
+        return None
+    dc = torch.empty(B, T, K, d, dtype=torch.float32, device=c.device)
+    db = torch.empty_like(dc)
+    d_h0 = torch.empty(B, N, d, dtype=torch.float32, device=c.device) if carried else None
+    d_q0 = torch.empty(B, d, dtype=torch.float32, device=c.device) if carried else None
+    cont = lambda t: None if t is None else t.contiguous()  # noqa: E731
+    args = [cont(t) for t in (c, b, h_old, cells, valid, reset, d_q_pre, d_q_post, d_h_sel,
+                              d_h_T, d_q_T)]
+    call("hsn_win_recurrence", *(ptr(t) for t in args), ptr(dc), ptr(db), ptr(d_h0), ptr(d_q0),
+         B, T, K, d, N, stream_of(c.device))
+    return (dc, db, d_h0, d_q0) if carried else (dc, db)
+
+
+def recurrence_backward(c: Tensor, b: Tensor, h_old: Tensor, cells: Tensor, valid: Tensor,
+                        reset: Tensor, n_cells: int, d_q_pre: Optional[Tensor],
+                        d_q_post: Optional[Tensor], d_h_sel: Optional[Tensor]):
+    """``hsn.train.split.recurrence_backward`` (python/hsn/train/split.py:128-174) as one
+    launch: ``(dc, db)`` or ``None`` when the inputs are not fp32 / int64 on a prepared device.
+    The reference's kernel declines above 48 KiB of shared memory; this one takes any N whose
+    ``[N, S]`` cotangent slice fits the LDS."""
+    return _recurrence(c, b, h_old, cells, valid, reset, n_cells, d_q_pre, d_q_post, d_h_sel,
+                       None, None, False)
+
+
+def recurrence_backward_carried(c, b, h_old, cells, valid, reset, n_cells, d_q_pre, d_q_post,
+                                d_h_sel, d_h_T=None, d_q_T=None):
+    """:func:`recurrence_backward` with the carried state: ``d_h_T [B,N,d]`` / ``d_q_T [B,d]``
+    seed the cotangents (the next window's start-state gradient) and the result adds
+    ``d_h0, d_q0``, the gradient into this window's start state: ``(dc, db, d_h0, d_q0)``."""
+    return _recurrence(c, b, h_old, cells, valid, reset, n_cells, d_q_pre, d_q_post, d_h_sel,
+                       d_h_T, d_q_T, True)
+
+
+def dense_recurrence_backward(c: Tensor, b: Tensor, h_old: Tensor, reset: Tensor, n_cells: int,
+                              d_q_pre: Optional[Tensor], d_q_post: Optional[Tensor]):
+    """``hsn.train.split.dense_recurrence_backward`` (split.py:177-209) as one launch, or
+    ``None`` for non-fp32 inputs or an unprepared device."""
+    if not prepared(c.device) or c.dtype != torch.float32:
+        return None
+    Bd, T, N, d = (int(n) for n in c.shape)
+    if N != int(n_cells):
+        return None
+    for cot in (d_q_pre, d_q_post):
+        if cot is not None and cot.dtype != torch.float32:
+            return None
+    dc = torch.empty(Bd, T, N, d, dtype=torch.float32, device=c.device)
+    db = torch.empty_like(dc)
+    cont = lambda t: None if t is None else t.contiguous()  # noqa: E731
+    call("hsn_win_recurrence_dense", ptr(cont(c)), ptr(cont(b)), ptr(cont(h_old)),
+         ptr(cont(reset)), ptr(cont(d_q_pre)), ptr(cont(d_q_post)), ptr(dc), ptr(db), Bd, T, N, d,
+         stream_of(c.device))
+    return dc, db
+
+
+# --------------------------------------------------------------------------------------------
+# the per-position decision (reference window.py:356-602)
+# --------------------------------------------------------------------------------------------
+
+
+def _io(t: Tensor) -> int:
+    return DTYPE_BF16 if t.dtype == torch.bfloat16 else DTYPE_F32
+
+
+def _launch_select(logits, width, n_units, age, cost, cells, units, valid, theta, refreshed, t,
+                   n_out, n_age, B, N, k, age_max, probes, lambda_cost, cell_overhead,
+                   shared_cost, limit, reserved, reserved_units):
+    call("hsn_win_select", ptr(logits), _io(logits), int(width), ptr(age) if probes else None,
+         ptr(cost), ptr(cells), ptr(units), ptr(valid), ptr(theta), ptr(refreshed), B, N,
+         int(n_units), int(k), int(t), int(n_out), int(n_age), int(age_max), int(bool(probes)),
+         float(lambda_cost), float(cell_overhead), float(shared_cost), float(limit),
+         int(reserved), int(bool(reserved_units)), stream_of(logits.device))
+
+
+@torch.library.custom_op("hsn::window_select", mutates_args=(), device_types="cuda")
+def select_op(logits: Tensor, age: Tensor, cost: Tensor, k: int, age_max: int, probes: bool,
+              lambda_cost: float, cell_overhead: float, shared_cost: float, limit: float,
+              reserved: int = 0, reserved_units: bool = False
+              ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """One position's decision ``(cells, units, valid, theta, refreshed)`` from ``logits
+    [B,N,M]`` (fp32 or bf16), ``age [B,N]`` int64, ``cost [M]`` fp32 (reference
+    window.py:233-283)."""
+    B, N, M = (int(n) for n in logits.shape)
+    dev = logits.device
+    cells = torch.empty((B, k), dtype=torch.int64, device=dev)
+    units = torch.empty((B, k), dtype=torch.int64, device=dev)
+    valid = torch.empty((B, k), dtype=torch.bool, device=dev)
+    theta = torch.empty((B,), dtype=torch.float32, device=dev)
+    refreshed = torch.empty((B, k), dtype=torch.bool, device=dev)
+    _launch_select(logits, M, M, age, cost, cells, units, valid, theta, refreshed, 0, 1, 1, B, N,
+                   k, age_max, probes, lambda_cost, cell_overhead, shared_cost, limit, reserved,
+                   reserved_units)
+    return cells, units, valid, theta, refreshed
+
+
+@select_op.register_fake
+def _select_fake(logits, age, cost, k, age_max, probes, lambda_cost, cell_overhead, shared_cost,
+                 limit, reserved=0, reserved_units=False):
+    B = logits.shape[0]
+    return (logits.new_empty((B, k), dtype=torch.int64), logits.new_empty((B, k), dtype=torch.int64),
+            logits.new_empty((B, k), dtype=torch.bool), logits.new_empty((B,), dtype=torch.float32),
+            logits.new_empty((B, k), dtype=torch.bool))
+
+
+@torch.library.custom_op("hsn::window_select_tape",
+                         mutates_args=("cells", "units", "valid", "theta", "refreshed"),
+                         device_types="cuda")
+def select_tape_op(logits: Tensor, age: Tensor, cost: Tensor, cells: Tensor, units: Tensor,
+                   valid: Tensor, theta: Tensor, refreshed: Tensor, t: int, age_max: int,
+                   probes: bool, lambda_cost: float, cell_overhead: float, shared_cost: float,
+                   limit: float, reserved: int = 0, reserved_units: bool = False) -> None:
+    """:func:`select_op` into record ``t`` of the decision tape (``[B, n, K]``, ``theta
+    [B, n]``) from the ages ``age[:, t]`` (``[B, n + 1, N]``) (reference window.py:356-420)."""
+    B, N, M = (int(n) for n in logits.shape)
+    n, k = int(cells.shape[1]), int(cells.shape[2])
+    _launch_select(logits, M, M, age, cost, cells, units, valid, theta, refreshed, t, n,
+                   int(age.shape[1]), B, N, k, age_max, probes, lambda_cost, cell_overhead,
+                   shared_cost, limit, reserved, reserved_units)
+
+
+@select_tape_op.register_fake
+def _select_tape_fake(logits, age, cost, cells, units, valid, theta, refreshed, t, age_max, probes,
+                      lambda_cost, cell_overhead, shared_cost, limit, reserved=0,
+                      reserved_units=False):
+    return None
+
+
+@torch.library.custom_op("hsn::window_select_fold",
+                         mutates_args=("cells", "units", "valid", "theta", "refreshed"),
+                         device_types="cuda")
+def select_fold_op(scored: Tensor, age: Tensor, cost: Tensor, cells: Tensor, units: Tensor,
+                   valid: Tensor, theta: Tensor, refreshed: Tensor, t: int, n_units: int,
+                   age_max: int, probes: bool, lambda_cost: float, cell_overhead: float,
+                   shared_cost: float, limit: float, reserved: int = 0,
+                   reserved_units: bool = False) -> None:
+    """:func:`select_tape_op` on the scorer's product as it is: ``scored [B*N, W]`` (fp32 or
+    bf16) holds the logits in its first ``n_units`` columns, read in place (reference
+    window.py:421-486)."""
+    rows, width = int(scored.shape[0]), int(scored.shape[1])
+    B = int(cells.shape[0])
+    N = rows // B
+    n, k = int(cells.shape[1]), int(cells.shape[2])
+    _launch_select(scored, width, n_units, age, cost, cells, units, valid, theta, refreshed, t, n,
+                   int(age.shape[1]), B, N, k, age_max, probes, lambda_cost, cell_overhead,
+                   shared_cost, limit, reserved, reserved_units)
+
+
+@select_fold_op.register_fake
+def _select_fold_fake(scored, age, cost, cells, units, valid, theta, refreshed, t, n_units,
+                      age_max, probes, lambda_cost, cell_overhead, shared_cost, limit, reserved=0,
+                      reserved_units=False):
+    return None
+
+
+def select_unsupported(n_cells: int, k: int, n_units: int = 1) -> Optional[str]:
+    """Why :func:`select` cannot take a model of this shape (``None``: it can)."""
+    if n_cells > _MAX_SELECT_CELLS:
+        return f"model.n_cells={n_cells}: at most {_MAX_SELECT_CELLS} cells (64 per lane)"
+    if k > n_cells:
+        return f"k_select={k} exceeds model.n_cells={n_cells}"
+    if k > _MAX_SELECT_K:
+        return f"k_select={k}: one lane per slot of a 64-lane wavefront"
+    return None
+
+
+def select(logits: Tensor, age: Tensor, cost_table: Tensor, *, k: int, age_max: int, probes: bool,
+           lambda_cost: float, cell_overhead: float, shared_cost: float, limit: float,
+           reserved: int = 0, reserved_units: bool = False):
+    """``Router.select`` for the forward sweep (mode ``topk``, the hard decision, the refresh
+    probes when ``probes``): ``(cells, units, valid, theta, refreshed)`` with the router's
+    values and tie rules (reference window.py:568-602). ``limit = budget * (1 + slack)``."""
+    logits = logits if logits.dtype in (torch.float32, torch.bfloat16) else logits.float()
+    return select_op(logits.contiguous(), age.contiguous(), cost_table.to(torch.float32).contiguous(),
+                     k, age_max, probes, lambda_cost, cell_overhead, shared_cost, limit, reserved,
+                     reserved_units)
+
+
+def select_tape(logits, tape_age, cost_table, cells, units, valid, theta, refreshed, *, t, age_max,
+                probes, lambda_cost, cell_overhead, shared_cost, limit, reserved=0,
+                reserved_units=False) -> None:
+    """:func:`select` for position ``t``, written into record ``t`` of the decision tape."""
+    logits = logits if logits.dtype in (torch.float32, torch.bfloat16) else logits.float()
+    select_tape_op(logits.contiguous(), tape_age, cost_table.to(torch.float32).contiguous(), cells,
+                   units, valid, theta, refreshed, t, age_max, probes, lambda_cost, cell_overhead,
+                   shared_cost, limit, reserved, reserved_units)
+
+
+def select_fold(scored, tape_age, cost_table, cells, units, valid, theta, refreshed, *, t, n_units,
+                age_max, probes, lambda_cost, cell_overhead, shared_cost, limit, reserved=0,
+                reserved_units=False) -> None:
+    """:func:`select_tape` reading the logits in place from a wider product."""
+    select_fold_op(scored, tape_age, cost_table.to(torch.float32).contiguous(), cells, units,
+                   valid, theta, refreshed, t, n_units, age_max, probes, lambda_cost,
+                   cell_overhead, shared_cost, limit, reserved, reserved_units)
+
+
+# --------------------------------------------------------------------------------------------
+# the per-position end of round (reference window.py:605-1004)
+# --------------------------------------------------------------------------------------------
+
+
+def _launch_update(y, gate, cand_w, cand_norm, cand_eps, h, q, age, pos, cells, valid, h_next,
+                   q_next, age_next, pos_next, h_sel, h_max, reset, q_post, B, N, d, K, t, n_state,
+                   n_slot, t_out):
+    scratch = torch.empty(B, K, dtype=torch.float32, device=y.device) if cand_norm else None
+    call("hsn_win_cell_update", ptr(y), ptr(gate), _io(y), ptr(cand_w) if cand_norm else None,
+         int(bool(cand_norm)), float(cand_eps), ptr(scratch), ptr(h), ptr(q), ptr(age), ptr(pos),
+         ptr(cells), ptr(valid), ptr(h_next), ptr(q_next), ptr(age_next), ptr(pos_next),
+         ptr(h_sel), ptr(h_max), ptr(reset), ptr(q_post), B, N, d, K, t, n_state, n_slot, t_out,
+         stream_of(y.device))
+
+
+@torch.library.custom_op("hsn::window_cell_update", mutates_args=(), device_types="cuda")
+def cell_update_op(y: Tensor, gate: Tensor, h: Tensor, q: Tensor, age: Tensor, pos: Tensor,
+                   cells: Tensor, valid: Tensor, cand_w: Tensor, cand_norm: bool, cand_eps: float
+                   ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The end of one position's round: ``(h, q, age, pos, h_sel, h_max)`` (reference
+    window.py:605-659). ``y, gate [B,K,d]`` fp32 (or bf16); state fp32 / int64; cells int64."""
+    B, N, d = (int(n) for n in h.shape)
+    K = int(cells.shape[1])
+    h_next = torch.empty_like(h)
+    q_next = torch.empty_like(q)
+    age_next = torch.empty_like(age)
+    pos_next = torch.empty_like(pos)
+    h_sel = h.new_empty((B, K, d))
+    h_max = h.new_empty((B,))
+    _launch_update(y, gate, cand_w, cand_norm, cand_eps, h, q, age, pos, cells, valid, h_next,
+                   q_next, age_next, pos_next, h_sel, h_max, None, None, B, N, d, K, 0, 1, 1, 0)
+    return h_next, q_next, age_next, pos_next, h_sel, h_max
+
+
+@cell_update_op.register_fake
+def _cell_update_fake(y, gate, h, q, age, pos, cells, valid, cand_w, cand_norm, cand_eps):
+    return (torch.empty_like(h), torch.empty_like(q), torch.empty_like(age), torch.empty_like(pos),
+            h.new_empty((*cells.shape, h.shape[2])), h.new_empty((h.shape[0],)))
+
+
+@torch.library.custom_op("hsn::window_update_tape",
+                         mutates_args=("tape_h", "tape_q", "tape_age", "tape_hsel", "h_max", "qs"),
+                         device_types="cuda")
+def update_tape_op(y: Tensor, gate: Tensor, tape_h: Tensor, tape_q: Tensor, tape_age: Tensor,
+                   cells: Tensor, valid: Tensor, cand_w: Tensor, reset: Tensor, tape_hsel: Tensor,
+                   h_max: Tensor, qs: Tensor, t: int, cand_norm: bool, cand_eps: float) -> None:
+    """:func:`cell_update_op` on a tape (reference window.py:682-741): reads record ``t`` of
+    ``tape_h [B,n+1,N,d]``, ``tape_q [B,n+1,d]``, ``tape_age [B,n+1,N]`` and of the decision
+    ``[B,n,K]``; writes record ``t+1`` of the state tape (zeroed on rows whose ``reset[:, t+1]``
+    is set, never for the last record) and record ``t`` of ``tape_hsel [B,n,K,d]``,
+    ``h_max [B,n]`` and ``qs [B,n,d]`` (the summary after the position, before that reset)."""
+    B, n_state, N, d = (int(n) for n in tape_h.shape)
+    n, K = int(cells.shape[1]), int(cells.shape[2])
+    _launch_update(y, gate, cand_w, cand_norm, cand_eps, tape_h, tape_q, tape_age, None, cells,
+                   valid, tape_h, tape_q, tape_age, None, tape_hsel, h_max, reset, qs, B, N, d, K, t,
+                   n_state, n, t + 1)
+
+
+@update_tape_op.register_fake
+def _update_tape_fake(y, gate, tape_h, tape_q, tape_age, cells, valid, cand_w, reset, tape_hsel,
+                      h_max, qs, t, cand_norm, cand_eps):
+    return None
+
+
+def cell_update_unsupported(n_cells: int, d: int, k: int) -> Optional[str]:
+    """Why :func:`cell_update` cannot take a model of this shape (``None``: it can)."""
+    if k > n_cells:
+        return f"k_select={k} exceeds model.n_cells={n_cells}"
+    if k > 8 * 64:
+        return f"k_select={k}: at most 8 slots per lane"
+    if not _slice_fits(n_cells, 8):
+        return f"model.n_cells={n_cells}: the state slice does not fit the LDS"
+    return None
+
+
+def _cand(cell):
+    cand_norm = getattr(cell, "cand_norm_kind", "none") != "none"
+    if cand_norm:
+        w = cell.cand_norm.weight
+        eps = float(getattr(cell.cand_norm, "eps", None) or 0.0)
+    else:
+        w = cell.norm.weight
+        eps = 0.0
+    return cand_norm, w.detach().to(torch.float32).contiguous(), eps
+
+
+def cell_update(cell, y: Tensor, gate: Tensor, state: CellGraphState, cells: Tensor,
+                valid: Tensor):
+    """The round of one position from its products: candidate (norm, tanh), the gate's
+    sigmoid, the gated delta update and the tick as one launch. Returns the state after the
+    position, the slots' cells after the update ``[B,K,d]`` (cell 0 on padded slots) and each
+    row's ``max |h|`` ``[B]`` (reference window.py:900-931)."""
+    cand_norm, w, eps = _cand(cell)
+    h, q, age, pos, h_sel, h_max = cell_update_op(
+        y.contiguous(), gate.contiguous(), state.h.contiguous(), state.q.contiguous(),
+        state.age.contiguous(), state.pos.contiguous(), cells.contiguous(), valid.contiguous(), w,
+        cand_norm, eps)
+    return CellGraphState._make(h=h, q=q, age=age, pos=pos), h_sel, h_max
+
+
+def update_tape(cell, y, gate, tape_h, tape_q, tape_age, cells, valid, reset, tape_hsel, h_max, qs,
+                *, t: int) -> None:
+    """:func:`cell_update` for position ``t`` on its tapes, in place (reference
+    window.py:967-1004)."""
+    cand_norm, w, eps = _cand(cell)
+    update_tape_op(y.contiguous(), gate.contiguous(), tape_h, tape_q, tape_age, cells, valid, w,
+                   reset, tape_hsel, h_max, qs, t, cand_norm, eps)

@@ -1,0 +1,79 @@
+/*
+ * hsn_ops.h -- the four-op numerical C ABI of HSN's sparse round, the two ops on the window
+ * hot path (the gated delta update and the gather of the selected cells), for MI355X.
+ *
+ * Same function names, argument order, dtype codes and status codes as the reference's ABI
+ * (kernels/include/hsn_ops.h:64-77,85-99,155-187), so a host that binds that header binds this
+ * library unchanged. Conventions as there: dense row-major tensors, int32_t indices, one float
+ * dtype per call (f32 or bf16 here; f16 is HSN_ERR_UNSUPPORTED_DTYPE), fp32 accumulation with
+ * one rounding per output, outputs written in full, `stream` a hipStream_t, functions return
+ * once the work is enqueued. Tolerances against the reference's golden vectors: f32 1e-5,
+ * bf16 1e-2 (atol = rtol).
+ */
+#ifndef HSN_OPS_H
+#define HSN_OPS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HSN_OPS_SPEC_VERSION 1
+
+#define HSN_DTYPE_F32 0
+#define HSN_DTYPE_F16 1
+#define HSN_DTYPE_BF16 2
+
+#define HSN_OK 0
+#define HSN_ERR_INVALID_ARGUMENT 1
+#define HSN_ERR_UNSUPPORTED_DTYPE 2
+#define HSN_ERR_INDEX_OUT_OF_RANGE 3
+#define HSN_ERR_DUPLICATE_INDEX 4
+#define HSN_ERR_SIZE_OVERFLOW 5
+#define HSN_ERR_BAD_GRAPH 6
+#define HSN_ERR_BACKEND 7
+
+/*
+ * v[r,k,:] = [u[r,:]; eps[r,:]; h[r, cell_idx[r,k], :]; m[r,k,:]]     (reference hsn_ops.h:79-87)
+ * u, eps [B,d]; h [B,N,d]; m [B,K,d]; cell_idx [B,K]; v [B,K,4d].
+ */
+int hsn_gather_concat(const void* u, const void* eps, const void* h, const void* m,
+                      const int32_t* cell_idx, void* v, int B, int N, int d, int K, int dtype,
+                      void* stream);
+
+/*
+ * Backward of the gather (reference hsn_ops.h:88-99): grad_u, grad_eps [B,d] sum the slots'
+ * first two blocks; grad_h [B,N,d] is the scatter-add of the third block over cell_idx (0 for
+ * cells no slot names); grad_m [B,K,d] is the fourth block. `deterministic` is accepted for
+ * the ABI's sake: every reduction here has a fixed order, so results are always reproducible.
+ */
+int hsn_gather_concat_bwd(const void* grad_v, const int32_t* cell_idx, void* grad_u,
+                          void* grad_eps, void* grad_h, void* grad_m, int B, int N, int d, int K,
+                          int dtype, int deterministic, void* stream);
+
+/*
+ * The gated delta update, in place on h, q, age (reference hsn_ops.h:155-171): for every valid
+ * slot, n = cell_idx[r,k]: h_old_saved = h[r,n,:]; h[r,n,:] = (1-b) h + b c; q[r,:] += sum of
+ * the deltas / N; age[r,n] = 0. Padded slots (valid 0) are never read and get h_old_saved = 0.
+ */
+int hsn_gated_delta_update(void* h, void* q, int32_t* age, const int32_t* cell_idx,
+                           const int32_t* valid, const void* c, const void* b, void* h_old_saved,
+                           int B, int N, int d, int K, int dtype, void* stream);
+
+/*
+ * Its backward (reference hsn_ops.h:173-187), from G = grad_h_out [B,N,d], g = grad_q_out [B,d]:
+ * for a valid slot grad_h[n] = (1-b) G[n] - b g/N, grad_c = b (G[n] + g/N),
+ * grad_b = (c - h_old) (G[n] + g/N); grad_h = G on cells no valid slot names; grad_q = g;
+ * zeros on padded slots.
+ */
+int hsn_gated_delta_update_bwd(const int32_t* cell_idx, const int32_t* valid, const void* c,
+                               const void* b, const void* h_old_saved, const void* grad_h_out,
+                               const void* grad_q_out, void* grad_h, void* grad_q, void* grad_c,
+                               void* grad_b, int B, int N, int d, int K, int dtype, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* HSN_OPS_H */

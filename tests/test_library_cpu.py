@@ -1,0 +1,92 @@
+"""The C-ABI library on the CPU: it is built from the current sources, it loads without a GPU,
+and it exports every entry point the headers declare with the status codes of the reference's
+ABI. No kernel runs here."""
+
+from __future__ import annotations
+
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared() -> set[str]:
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(hsn_\w+)\s*\(", text))
+    return names
+
+
+def test_headers_declare_the_hot_path_entry_points():
+    names = _declared()
+    for expected in ("hsn_win_route", "hsn_win_select", "hsn_win_forward", "hsn_win_backward",
+                     "hsn_win_recurrence", "hsn_win_recurrence_dense", "hsn_win_cell_update",
+                     "hsn_gated_delta_update", "hsn_gated_delta_update_bwd", "hsn_gather_concat",
+                     "hsn_gather_concat_bwd", "hsn_win_abi_version", "hsn_win_last_error"):
+        assert expected in names
+
+
+def test_library_is_current_and_exports_every_declared_symbol():
+    from hsn_amd import _lib, build
+
+    why = build.stale()
+    if why is not None:
+        pytest.skip(f"library not built here: {why}")
+    out = subprocess.run(["nm", "-D", "--defined-only", str(build.LIBRARY)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r" T (hsn_\w+)$", out, flags=re.M))
+    assert _declared() <= exported, _declared() - exported
+    assert set(_lib.SIGNATURES) == _declared()
+    lib = _lib.library()  # loads without a GPU
+    assert lib.hsn_win_abi_version() == 1
+
+
+def test_status_codes_match_the_reference_abi():
+    """HSN_OK and HSN_ERR_* 1..7 as kernels/include/hsn_ops.h:69-77 numbers them."""
+    text = (ROOT / "include" / "hsn_ops.h").read_text()
+    codes = dict(re.findall(r"#define (HSN_(?:OK|ERR_\w+)) (\d+)", text))
+    assert codes == {"HSN_OK": "0", "HSN_ERR_INVALID_ARGUMENT": "1",
+                     "HSN_ERR_UNSUPPORTED_DTYPE": "2", "HSN_ERR_INDEX_OUT_OF_RANGE": "3",
+                     "HSN_ERR_DUPLICATE_INDEX": "4", "HSN_ERR_SIZE_OVERFLOW": "5",
+                     "HSN_ERR_BAD_GRAPH": "6", "HSN_ERR_BACKEND": "7"}
+
+
+def test_argument_errors_return_status_without_a_gpu():
+    """Preconditions that need no device are checked before any launch: the call returns the
+    status code and a message, and never touches the GPU."""
+    from hsn_amd import _lib, build
+
+    if build.stale() is not None:
+        pytest.skip("library not built here")
+    lib = _lib.library()
+    # K > N is rejected up front
+    status = lib.hsn_win_route(1, 0, 1, 1, None, None, 1, 1, 32, 1, 1, 1, None, 1, 1, 4, 1, 8, 0,
+                               0, 0.0, 0.0, 0.0, 1.0, 0, 0, None)
+    assert status == 1
+    assert b"K <= N" in lib.hsn_win_last_error()
+    # f16 is not a window storage type
+    status = lib.hsn_win_forward(1, 1, 1, None, 0, 0.0, None, 1, 1, 1, 32, 1, 1, None, None, None,
+                                 None, None, None, None, None, None, None, None, 1, 1, 4, 4, 2,
+                                 None)
+    assert status == 2
+    # a NULL required pointer
+    status = lib.hsn_gated_delta_update(None, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, None)
+    assert status == 1
+
+
+def test_product_path_fails_loudly_without_the_library(monkeypatch):
+    """No CPU fallback: a missing library raises on first use."""
+    from hsn_amd import _lib, build
+
+    monkeypatch.setattr(build, "stale", lambda: "the HIP library is not built (test)")
+    _lib.library.cache_clear()
+    try:
+        with pytest.raises(RuntimeError, match="not built"):
+            _lib.library()
+    finally:
+        monkeypatch.undo()
+        _lib.library.cache_clear()
