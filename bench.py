@@ -117,15 +117,15 @@ def main() -> int:
         h_max = None if args.no_h_max else torch.empty(B, T, device=dev)
         if ev:
             ev[0].record()
-        cells, units, valid, theta, refreshed = window.route(w["logits"], w["cost"], rcfg,
-                                                             h_max_zero=h_max)
+        cells, units, valid, theta, refreshed, slots = window.route(
+            w["logits"], w["cost"], rcfg, h_max_zero=h_max, with_slots=True)
         if ev:
             ev[1].record()
-        out = window.forward(w["y"], w["gate_pre"], w["reset"], cells, valid, w["h0"], w["q0"],
+        out = window.forward(w["y"], w["gate_pre"], w["reset"], slots, w["h0"], w["q0"],
                              w["age0"], w["pos0"], N, h_max=h_max)
         if ev:
             ev[2].record()
-        grads = window.backward(w["y"], w["gate_pre"], out["h_old"], cells, valid, w["reset"], N,
+        grads = window.backward(w["y"], w["gate_pre"], out["h_old"], slots, w["reset"], N,
                                 cot["d_q_pre"], cot["d_q_post"], cot["d_h_sel"], cot["d_h_T"],
                                 cot["d_q_T"])
         if ev:

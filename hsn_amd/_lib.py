@@ -34,13 +34,13 @@ P, I, F, L = c_void_p, c_int, c_float, c_int64
 SIGNATURES: dict[str, list] = {
     "hsn_win_abi_version": [],
     "hsn_win_last_error": [],
-    "hsn_win_route": [P, I, L, P, P, P, P, P, I, P, P, P, P, I, I, I, I, I, I, I, F, F, F, F, I, I,
-                      P],
+    "hsn_win_route": [P, I, L, P, P, P, P, P, I, P, P, P, P, P, I, I, I, I, I, I, I, F, F, F, F, I,
+                      I, P],
     "hsn_win_select": [P, I, L, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, F, F, F, F, I, I, P],
-    "hsn_win_forward": [P, P, I, P, I, F, P, P, P, P, I, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I,
-                        I, I, I, P],
-    "hsn_win_backward": [P, P, P, I, P, I, F, P, P, P, I, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I,
-                         I, P],
+    "hsn_win_forward": [P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I,
+                        I, P],
+    "hsn_win_backward": [P, P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I,
+                         P],
     "hsn_win_recurrence": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P],
     "hsn_win_recurrence_dense": [P, P, P, P, P, P, P, P, I, I, I, I, P],
     "hsn_win_cell_update": [P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I,

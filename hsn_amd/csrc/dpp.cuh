@@ -1,0 +1,85 @@
+// Reductions over aligned groups of L consecutive lanes of a 64-lane wavefront, with DPP.
+//
+// Within a 16-lane row, gfx9 DPP reaches lane i^1 and i^2 (quad_perm), the mirror within an
+// 8-lane half row (row_half_mirror) and the rotation by 8 (row_ror:8), so groups of up to 16
+// lanes reduce with one v_*_dpp instruction per step and no LDS traffic; each step combines a
+// lane with its partner symmetrically, so every lane of the group ends with the bit-identical
+// result. Wider groups (32, 64 lanes) take the LDS-permute shuffle for the remaining steps.
+#pragma once
+
+#include "common.cuh"
+
+namespace hsn {
+
+namespace dpp {
+constexpr int kXor1 = 0xB1;        // quad_perm:[1,0,3,2]
+constexpr int kXor2 = 0x4E;        // quad_perm:[2,3,0,1]
+constexpr int kHalfMirror = 0x141;  // lane i <- lane 7-i within each 8 lanes
+constexpr int kRor8 = 0x128;       // lane i <- lane (i+8) mod 16 within each row
+}  // namespace dpp
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over each aligned group of L lanes; every lane of a group gets the group's sum.
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(L == 1 || L == 2 || L == 4 || L == 8 || L == 16 || L == 32 || L == 64, "L");
+    if constexpr (L >= 2) v += dpp_f32<dpp::kXor1>(v);
+    if constexpr (L >= 4) v += dpp_f32<dpp::kXor2>(v);
+    if constexpr (L >= 8) v += dpp_f32<dpp::kHalfMirror>(v);
+    if constexpr (L >= 16) v += dpp_f32<dpp::kRor8>(v);
+    if constexpr (L >= 32) v += __shfl_xor(v, 16, kWave);
+    if constexpr (L >= 64) v += __shfl_xor(v, 32, kWave);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// Unsigned max over each aligned group of L lanes.
+template <int L>
+__device__ __forceinline__ uint32_t group_max(uint32_t v) {
+    if constexpr (L >= 2) v = umax(v, dpp_u32<dpp::kXor1>(v));
+    if constexpr (L >= 4) v = umax(v, dpp_u32<dpp::kXor2>(v));
+    if constexpr (L >= 8) v = umax(v, dpp_u32<dpp::kHalfMirror>(v));
+    if constexpr (L >= 16) v = umax(v, dpp_u32<dpp::kRor8>(v));
+    if constexpr (L >= 32) v = umax(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 16, kWave)));
+    if constexpr (L >= 64) v = umax(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 32, kWave)));
+    return v;
+}
+
+// ------------------------------------------------------------------------------------------
+// Activations, branch-free, from exp2 and reciprocal (v_exp_f32 / v_rcp_f32, about 1 ulp each):
+//   sigmoid(x) = 1 / (1 + 2^(-x log2 e))
+//   tanh(x)    = sign(x) (1 - t) / (1 + t),  t = 2^(-2|x| log2 e)
+// with the odd Taylor polynomial x - x^3/3 + 2x^5/15 - 17x^7/315 for |x| < 1/16, where the
+// quotient form loses relative accuracy (the polynomial's truncation error is below 2^-33 there).
+// Absolute error stays a few ulps of 1, well inside the 1e-5 parity bar.
+// ------------------------------------------------------------------------------------------
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float fast_sigmoid(float x) {
+    const float e = __builtin_amdgcn_exp2f(-x * kLog2e);
+    return __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+__device__ __forceinline__ float fast_tanh(float x) {
+    const float ax = fabsf(x);
+    const float t = __builtin_amdgcn_exp2f(-2.0f * kLog2e * ax);
+    const float q = (1.0f - t) * __builtin_amdgcn_rcpf(1.0f + t);
+    const float x2 = x * x;
+    const float poly =
+        ax * (1.0f + x2 * (-1.0f / 3.0f + x2 * (2.0f / 15.0f + x2 * (-17.0f / 315.0f))));
+    const float m = ax < 0.0625f ? poly : q;
+    return copysignf(m, x);
+}
+
+}  // namespace hsn

@@ -29,6 +29,7 @@ struct RouteArgs {
     void* units;
     uint8_t* valid;
     uint8_t* refreshed;
+    int32_t* slots;  // optional: the cell where valid, -1 where padded (the sweeps' input)
     int64_t o_row, o_pos;  // output slot offset of (b, p, k) = b*o_row + p*o_pos + k
     float* theta;
     int64_t th_row, th_pos;
@@ -279,6 +280,7 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
         store_index<IDX>(a.units, o, out_unit);
         a.valid[o] = ok ? 1 : 0;
         a.refreshed[o] = out_refreshed ? 1 : 0;
+        if (a.slots) a.slots[o] = ok ? out_cell : -1;
     }
     if (lane == 0) {
         a.theta[b * a.th_row + p * a.th_pos] = th;
@@ -385,7 +387,8 @@ using namespace hsn;
 extern "C" int hsn_win_route(const void* logits, int io_dtype, int64_t width, const float* cost,
                              const int64_t* age0, const uint8_t* reset, void* cells, void* units,
                              int index_bits, uint8_t* valid, float* theta, uint8_t* refreshed,
-                             float* h_max_zero, int B, int T, int N, int M, int K, int age_max,
+                             int32_t* slots, float* h_max_zero, int B, int T, int N, int M, int K,
+                             int age_max,
                              int probes, float lambda_cost, float cell_overhead,
                              float shared_cost, float limit, int reserved, int reserved_units,
                              void* stream) {
@@ -420,6 +423,7 @@ extern "C" int hsn_win_route(const void* logits, int io_dtype, int64_t width, co
     a.units = units;
     a.valid = valid;
     a.refreshed = refreshed;
+    a.slots = slots;
     a.o_pos = K;
     a.o_row = int64_t(T) * K;
     a.theta = theta;

@@ -1,0 +1,144 @@
+// Entry points of the forward sweep: the whole window (hsn_win_forward) and the reference's
+// per-position end of round (hsn_win_cell_update), over the kernels of sweep.cuh.
+#include "sweep.cuh"
+#include "abi_util.h"
+
+using namespace hsn;
+
+namespace {
+
+// The RMS candidate's prologue: writes the normalised candidate input into the workspace
+// (layout: [slots, d] of the storage type, then [slots] fp32 of 1/rms) and returns it.
+const void* rms_normalise(const void* y, int io_dtype, const float* cand_w, float cand_eps,
+                          void* scratch, int64_t slots, int d, hipStream_t st) {
+    const int blocks = static_cast<int>((slots + 3) / 4);
+    const size_t elem = io_dtype == HSN_DTYPE_F32 ? 4 : 2;
+    float* inv = reinterpret_cast<float*>(static_cast<char*>(scratch) + slots * d * elem);
+    if (io_dtype == HSN_DTYPE_F32)
+        hipLaunchKernelGGL((rms_prologue<float>), dim3(blocks), dim3(256), 0, st,
+                           static_cast<const float*>(y), cand_w, static_cast<float*>(scratch), inv,
+                           slots, d, cand_eps);
+    else
+        hipLaunchKernelGGL((rms_prologue<bf16_t>), dim3(blocks), dim3(256), 0, st,
+                           static_cast<const bf16_t*>(y), cand_w, static_cast<bf16_t*>(scratch),
+                           inv, slots, d, cand_eps);
+    return scratch;
+}
+
+}  // namespace
+
+extern "C" int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype,
+                               const float* cand_w, int cand_norm, float cand_eps,
+                               void* rms_scratch, const uint8_t* reset, const int32_t* slots,
+                               const float* h0, const float* q0, const int64_t* age0,
+                               const int64_t* pos0, void* q_pre, void* q_post, void* h_sel,
+                               void* h_old, float* h_max, float* h_T, float* q_T, int64_t* age_T,
+                               int64_t* pos_T, int B, int T, int N, int d, int K, void* stream) {
+    HSN_ABI_BEGIN
+    HSN_REQUIRE(y && gate_pre && reset && slots && h0 && q0, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_forward: a required pointer is NULL");
+    HSN_REQUIRE(B >= 1 && T >= 1 && N >= 1 && d >= 1 && K >= 1 && K <= N,
+                HSN_ERR_INVALID_ARGUMENT, "hsn_win_forward: bad dimensions");
+    HSN_REQUIRE(!age_T || age0, HSN_ERR_INVALID_ARGUMENT, "hsn_win_forward: age_T needs age0");
+    HSN_REQUIRE(!pos_T || (pos0 && age_T), HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_forward: pos_T needs pos0 and age_T");
+    HSN_REQUIRE(!cand_norm || (cand_w && rms_scratch), HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_forward: the RMS candidate needs cand_w and rms_scratch");
+    HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
+                HSN_ERR_UNSUPPORTED_DTYPE, "hsn_win_forward: io_dtype must be f32 or bf16");
+    HSN_REQUIRE(check_elems({int64_t(B) * T * K * d, int64_t(B) * N * d}) &&
+                    int64_t(T) * K * d <= INT32_MAX,
+                HSN_ERR_SIZE_OVERFLOW,
+                "hsn_win_forward: a tensor is too large");
+    SliceShape sh;
+    const int64_t fixed = int64_t(N) * 4;  // the ages' last-selection table
+    HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, fixed, sh), HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_forward: the state slice does not fit the LDS (N too large)");
+    const size_t lds = size_t(N) * 4 * sh.S + size_t(fixed);
+    hipStream_t st = as_stream(stream);
+    if (cand_norm) {
+        y = rms_normalise(y, io_dtype, cand_w, cand_eps, rms_scratch, int64_t(B) * T * K, d, st);
+        HSN_HIP(hipGetLastError());
+    }
+    FwdArgs a{};
+    a.y = y, a.g = gate_pre, a.y_row = int64_t(T) * K * d;
+    a.reset = reset, a.r_row = T, a.clear = nullptr, a.c_row = 0;
+    a.cells = slots, a.valid = nullptr, a.s_row = int64_t(T) * K;
+    a.h0 = h0, a.h0_row = int64_t(N) * d, a.q0 = q0, a.q0_row = d;
+    a.age0 = age0, a.a0_row = N, a.pos0 = pos0;
+    a.q_pre = q_pre, a.q_post = q_post, a.qo_row = int64_t(T) * d;
+    a.h_sel = h_sel, a.h_old = h_old, a.o_row = int64_t(T) * K * d;
+    a.h_max = h_max, a.hm_row = T;
+    a.h_T = h_T, a.hT_row = int64_t(N) * d, a.q_T = q_T, a.qT_row = d;
+    a.age_T = age_T, a.aT_row = N, a.pos_T = pos_T;
+    a.B = B, a.T = T, a.N = N, a.d = d, a.K = K, a.xcd_rows = xcd_rows_of(B);
+    fill_n_consts(N, a.n_pow2, a.inv_n, a.n_f);
+    if (io_dtype == HSN_DTYPE_F32)
+        HSN_HIP((launch_fwd<float, float, Packed32>(a, sh, lds, st)));
+    else
+        HSN_HIP((launch_fwd<bf16_t, bf16_t, Packed32>(a, sh, lds, st)));
+    HSN_ABI_END
+}
+
+extern "C" int hsn_win_cell_update(const void* y, const void* gate, int io_dtype,
+                                   const float* cand_w, int cand_norm, float cand_eps,
+                                   void* rms_scratch, const float* h, const float* q,
+                                   const int64_t* age, const int64_t* pos, const int64_t* cells,
+                                   const uint8_t* valid, float* h_next, float* q_next,
+                                   int64_t* age_next, int64_t* pos_next, float* h_sel,
+                                   float* h_max, const uint8_t* reset, float* q_post, int B,
+                                   int N, int d, int K, int t, int n_state, int n_slot, int t_out,
+                                   void* stream) {
+    HSN_ABI_BEGIN
+    HSN_REQUIRE(y && gate && h && q && age && cells && valid && h_next && q_next && age_next &&
+                    h_sel && h_max,
+                HSN_ERR_INVALID_ARGUMENT, "hsn_win_cell_update: a required pointer is NULL");
+    HSN_REQUIRE(B >= 1 && N >= 1 && d >= 1 && K >= 1 && K <= N, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_cell_update: bad dimensions");
+    HSN_REQUIRE(t >= 0 && t < n_state && t_out >= 0 && t_out < n_state && t < n_slot,
+                HSN_ERR_INVALID_ARGUMENT, "hsn_win_cell_update: record outside the tapes");
+    HSN_REQUIRE(!pos_next || pos, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_cell_update: pos_next needs pos");
+    HSN_REQUIRE(!cand_norm || (cand_w && rms_scratch), HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_cell_update: the RMS candidate needs cand_w and rms_scratch");
+    HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
+                HSN_ERR_UNSUPPORTED_DTYPE, "hsn_win_cell_update: io_dtype must be f32 or bf16");
+    SliceShape sh;
+    const int64_t fixed = int64_t(N) * 4;
+    HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, fixed, sh), HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_cell_update: the state slice does not fit the LDS (N too large)");
+    const size_t lds = size_t(N) * 4 * sh.S + size_t(fixed);
+    hipStream_t st = as_stream(stream);
+    if (cand_norm) {
+        y = rms_normalise(y, io_dtype, cand_w, cand_eps, rms_scratch, int64_t(B) * K, d, st);
+        HSN_HIP(hipGetLastError());
+    }
+    FwdArgs a{};
+    a.y = y, a.g = gate, a.y_row = int64_t(K) * d;
+    a.reset = nullptr, a.r_row = 0;
+    const bool clear = reset && t + 1 < n_slot;
+    a.clear = clear ? reset + t + 1 : nullptr, a.c_row = n_slot;
+    a.cells = cells + int64_t(t) * K, a.valid = valid + int64_t(t) * K, a.s_row = int64_t(n_slot) * K;
+    a.h0 = h + int64_t(t) * N * d, a.h0_row = int64_t(n_state) * N * d;
+    a.q0 = q + int64_t(t) * d, a.q0_row = int64_t(n_state) * d;
+    a.age0 = age + int64_t(t) * N, a.a0_row = int64_t(n_state) * N, a.pos0 = pos;
+    a.q_pre = nullptr, a.q_post = q_post ? q_post + int64_t(t) * d : nullptr;
+    a.qo_row = int64_t(n_slot) * d;
+    a.h_sel = h_sel + int64_t(t) * K * d, a.h_old = nullptr, a.o_row = int64_t(n_slot) * K * d;
+    a.h_max = h_max + t, a.hm_row = n_slot;
+    a.h_T = h_next + int64_t(t_out) * N * d, a.hT_row = int64_t(n_state) * N * d;
+    a.q_T = q_next + int64_t(t_out) * d, a.qT_row = int64_t(n_state) * d;
+    a.age_T = age_next + int64_t(t_out) * N, a.aT_row = int64_t(n_state) * N, a.pos_T = pos_next;
+    a.B = B, a.T = 1, a.N = N, a.d = d, a.K = K, a.xcd_rows = xcd_rows_of(B);
+    fill_n_consts(N, a.n_pow2, a.inv_n, a.n_f);
+    // h_max is max-reduced across the row's slices: zero it first (a kernel, not a memset, so
+    // the call stays capturable)
+    hipLaunchKernelGGL(zero_strided_kernel, dim3((B + 255) / 256), dim3(256), 0, st, a.h_max,
+                       int64_t(B), int64_t(n_slot));
+    HSN_HIP(hipGetLastError());
+    if (io_dtype == HSN_DTYPE_F32)
+        HSN_HIP((launch_fwd<float, float, Cells64>(a, sh, lds, st)));
+    else
+        HSN_HIP((launch_fwd<bf16_t, float, Cells64>(a, sh, lds, st)));
+    HSN_ABI_END
+}

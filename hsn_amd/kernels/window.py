@@ -266,7 +266,10 @@ def select_fold(scored, tape_age, cost_table, cells, units, valid, theta, refres
 def _launch_update(y, gate, cand_w, cand_norm, cand_eps, h, q, age, pos, cells, valid, h_next,
                    q_next, age_next, pos_next, h_sel, h_max, reset, q_post, B, N, d, K, t, n_state,
                    n_slot, t_out):
-    scratch = torch.empty(B, K, dtype=torch.float32, device=y.device) if cand_norm else None
+    scratch = None
+    if cand_norm:
+        elem = 4 if y.dtype == torch.float32 else 2
+        scratch = torch.empty(B * K * (d * elem + 4), dtype=torch.uint8, device=y.device)
     call("hsn_win_cell_update", ptr(y), ptr(gate), _io(y), ptr(cand_w) if cand_norm else None,
          int(bool(cand_norm)), float(cand_eps), ptr(scratch), ptr(h), ptr(q), ptr(age), ptr(pos),
          ptr(cells), ptr(valid), ptr(h_next), ptr(q_next), ptr(age_next), ptr(pos_next),
@@ -356,7 +359,7 @@ def cell_update(cell, y: Tensor, gate: Tensor, state: CellGraphState, cells: Ten
         y.contiguous(), gate.contiguous(), state.h.contiguous(), state.q.contiguous(),
         state.age.contiguous(), state.pos.contiguous(), cells.contiguous(), valid.contiguous(), w,
         cand_norm, eps)
-    return CellGraphState._make(h=h, q=q, age=age, pos=pos), h_sel, h_max
+    return CellGraphState.make(h=h, q=q, age=age, pos=pos), h_sel, h_max
 
 
 def update_tape(cell, y, gate, tape_h, tape_q, tape_age, cells, valid, reset, tape_hsel, h_max, qs,

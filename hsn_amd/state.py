@@ -24,9 +24,8 @@ class CellGraphState(NamedTuple):
     pos: Tensor
 
     @classmethod
-    def _make(cls, iterable=None, *, h=None, q=None, age=None, pos=None):  # noqa: D401
-        if iterable is not None:
-            return cls(*iterable)
+    def make(cls, *, h: Tensor, q: Tensor, age: Tensor, pos: Tensor) -> "CellGraphState":
+        """The reference's ``CellGraphState._make(h=, q=, age=, pos=)``."""
         return cls(h=h, q=q, age=age, pos=pos)
 
     @classmethod

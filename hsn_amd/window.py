@@ -36,6 +36,7 @@ __all__ = [
     "window_forward",
     "window_backward",
     "WindowRecurrence",
+    "pack_slots",
 ]
 
 
@@ -77,9 +78,12 @@ def _check(t: Tensor, name: str, shape: tuple, dtype=None, device=None) -> None:
 
 
 def route(logits: Tensor, cost: Tensor, cfg: RouteConfig, *, reset: Optional[Tensor] = None,
-          age0: Optional[Tensor] = None, h_max_zero: Optional[Tensor] = None):
+          age0: Optional[Tensor] = None, h_max_zero: Optional[Tensor] = None,
+          with_slots: bool = False):
     """Every position's decision: ``(cells, units, valid, theta, refreshed)`` with shapes
-    ``[B,T,K]`` (int32, int32, bool), ``[B,T]`` fp32 and ``[B,T,K]`` bool.
+    ``[B,T,K]`` (int32, int32, bool), ``[B,T]`` fp32 and ``[B,T,K]`` bool; with ``with_slots``
+    a sixth ``slots [B,T,K]`` int32, the packed decision the sweeps read (the cell where the slot
+    is valid, -1 where it is padded).
 
     ``logits [B,T,N,M]`` fp32/bf16, ``cost [M]`` fp32. With ``cfg.probes`` the ages evolve
     with the decisions from ``age0 [B,N]`` (int64) and the resets ``reset [B,T]``.
@@ -99,22 +103,38 @@ def route(logits: Tensor, cost: Tensor, cfg: RouteConfig, *, reset: Optional[Ten
     valid = torch.empty(B, T, K, dtype=torch.bool, device=dev)
     refreshed = torch.empty_like(valid)
     theta = torch.empty(B, T, dtype=torch.float32, device=dev)
+    slots = torch.empty(B, T, K, dtype=torch.int32, device=dev) if with_slots else None
     if h_max_zero is not None:
         _check(h_max_zero, "h_max_zero", (B, T), torch.float32, dev)
     call("hsn_win_route", ptr(logits), _io_code(logits.dtype), M, ptr(cost),
          ptr(age0) if cfg.probes else None, ptr(reset) if cfg.probes else None, ptr(cells),
-         ptr(units), 32, ptr(valid), ptr(theta), ptr(refreshed), ptr(h_max_zero), B, T, N, M, K,
+         ptr(units), 32, ptr(valid), ptr(theta), ptr(refreshed), ptr(slots), ptr(h_max_zero), B, T,
+         N, M, K,
          int(cfg.age_max), int(bool(cfg.probes)), float(cfg.lambda_cost),
          float(cfg.cell_overhead), float(cfg.shared_cost), float(cfg.limit), int(cfg.reserved),
          int(bool(cfg.reserved_units)), stream_of(dev))
+    if with_slots:
+        return cells, units, valid, theta, refreshed, slots
     return cells, units, valid, theta, refreshed
 
 
-def forward(y: Tensor, gate_pre: Tensor, reset: Tensor, cells: Tensor, valid: Tensor, h0: Tensor,
-            q0: Tensor, age0: Tensor, pos0: Tensor, n_cells: int, *, cand_norm: bool = False,
+def pack_slots(cells: Tensor, valid: Tensor) -> Tensor:
+    """The packed decision ``where(valid, cells, -1)`` as int32 (what :func:`route` emits as
+    ``slots``), for decisions that come from elsewhere."""
+    return torch.where(valid, cells.to(torch.int32), torch.full_like(cells, -1, dtype=torch.int32))
+
+
+def _rms_scratch(slots: int, d: int, io: torch.dtype, dev) -> Tensor:
+    elem = 4 if io == torch.float32 else 2
+    return torch.empty(slots * (d * elem + 4), dtype=torch.uint8, device=dev)
+
+
+def forward(y: Tensor, gate_pre: Tensor, reset: Tensor, slots: Tensor, h0: Tensor, q0: Tensor,
+            age0: Tensor, pos0: Tensor, n_cells: int, *, cand_norm: bool = False,
             cand_w: Optional[Tensor] = None, cand_eps: float = 1e-6,
             h_max: Optional[Tensor] = None) -> dict:
-    """The forward sweep from given decisions. Returns ``q_pre, q_post [B,T,d]``,
+    """The forward sweep from given decisions (``slots [B,T,K]`` int32, see :func:`route`).
+    Returns ``q_pre, q_post [B,T,d]``,
     ``h_sel, h_old [B,T,K,d]`` (storage dtype), the end state ``h [B,N,d], q [B,d]`` (fp32),
     ``age [B,N], pos [B]`` (int64) and ``h_max [B,T]`` when a zeroed buffer is passed."""
     B, T, K, d = (int(s) for s in y.shape)
@@ -123,8 +143,7 @@ def forward(y: Tensor, gate_pre: Tensor, reset: Tensor, cells: Tensor, valid: Te
     _check(y, "y", (B, T, K, d))
     _check(gate_pre, "gate_pre", (B, T, K, d), io, dev)
     _check(reset, "reset", (B, T), torch.bool, dev)
-    _check(cells, "cells", (B, T, K), torch.int32, dev)
-    _check(valid, "valid", (B, T, K), torch.bool, dev)
+    _check(slots, "slots", (B, T, K), torch.int32, dev)
     _check(h0, "h0", (B, N, d), torch.float32, dev)
     _check(q0, "q0", (B, d), torch.float32, dev)
     _check(age0, "age0", (B, N), torch.int64, dev)
@@ -134,7 +153,7 @@ def forward(y: Tensor, gate_pre: Tensor, reset: Tensor, cells: Tensor, valid: Te
         if cand_w is None:
             raise ValueError("cand_norm needs cand_w")
         _check(cand_w, "cand_w", (d,), torch.float32, dev)
-        scratch = torch.empty(B, T, K, dtype=torch.float32, device=dev)
+        scratch = _rms_scratch(B * T * K, d, io, dev)
     out = {
         "q_pre": torch.empty(B, T, d, dtype=io, device=dev),
         "q_post": torch.empty(B, T, d, dtype=io, device=dev),
@@ -149,14 +168,14 @@ def forward(y: Tensor, gate_pre: Tensor, reset: Tensor, cells: Tensor, valid: Te
         _check(h_max, "h_max", (B, T), torch.float32, dev)
         out["h_max"] = h_max
     call("hsn_win_forward", ptr(y), ptr(gate_pre), _io_code(io), ptr(cand_w) if cand_norm else None,
-         int(bool(cand_norm)), float(cand_eps), ptr(scratch), ptr(reset), ptr(cells), ptr(valid),
-         32, ptr(h0), ptr(q0), ptr(age0), ptr(pos0), ptr(out["q_pre"]), ptr(out["q_post"]),
+         int(bool(cand_norm)), float(cand_eps), ptr(scratch), ptr(reset), ptr(slots),
+         ptr(h0), ptr(q0), ptr(age0), ptr(pos0), ptr(out["q_pre"]), ptr(out["q_post"]),
          ptr(out["h_sel"]), ptr(out["h_old"]), ptr(h_max), ptr(out["h"]), ptr(out["q"]),
          ptr(out["age"]), ptr(out["pos"]), B, T, N, d, K, stream_of(dev))
     return out
 
 
-def backward(y: Tensor, gate_pre: Tensor, h_old: Tensor, cells: Tensor, valid: Tensor,
+def backward(y: Tensor, gate_pre: Tensor, h_old: Tensor, slots: Tensor,
              reset: Tensor, n_cells: int, d_q_pre: Optional[Tensor], d_q_post: Optional[Tensor],
              d_h_sel: Optional[Tensor], d_h_T: Optional[Tensor] = None,
              d_q_T: Optional[Tensor] = None, *, cand_norm: bool = False,
@@ -173,8 +192,7 @@ def backward(y: Tensor, gate_pre: Tensor, h_old: Tensor, cells: Tensor, valid: T
     _check(y, "y", (B, T, K, d))
     for name, t in (("gate_pre", gate_pre), ("h_old", h_old)):
         _check(t, name, (B, T, K, d), io, dev)
-    _check(cells, "cells", (B, T, K), torch.int32, dev)
-    _check(valid, "valid", (B, T, K), torch.bool, dev)
+    _check(slots, "slots", (B, T, K), torch.int32, dev)
     _check(reset, "reset", (B, T), torch.bool, dev)
     for name, t in (("d_q_pre", d_q_pre), ("d_q_post", d_q_post)):
         if t is not None:
@@ -190,7 +208,7 @@ def backward(y: Tensor, gate_pre: Tensor, h_old: Tensor, cells: Tensor, valid: T
         if cand_w is None:
             raise ValueError("cand_norm needs cand_w")
         _check(cand_w, "cand_w", (d,), torch.float32, dev)
-        scratch = torch.empty(B, T, K, dtype=torch.float32, device=dev)
+        scratch = _rms_scratch(B * T * K, d, io, dev)
         d_w = torch.empty(d, dtype=torch.float32, device=dev)
     dy = torch.empty_like(y)
     dgate = torch.empty_like(y)
@@ -198,7 +216,7 @@ def backward(y: Tensor, gate_pre: Tensor, h_old: Tensor, cells: Tensor, valid: T
     d_q0 = torch.empty(B, d, dtype=torch.float32, device=dev)
     call("hsn_win_backward", ptr(y), ptr(gate_pre), ptr(h_old), _io_code(io),
          ptr(cand_w) if cand_norm else None, int(bool(cand_norm)), float(cand_eps), ptr(scratch),
-         ptr(cells), ptr(valid), 32, ptr(reset), ptr(d_q_pre), ptr(d_q_post), ptr(d_h_sel),
+         ptr(slots), ptr(reset), ptr(d_q_pre), ptr(d_q_post), ptr(d_h_sel),
          ptr(d_h_T), ptr(d_q_T), ptr(dy), ptr(dgate), ptr(d_h0), ptr(d_q0), ptr(d_w), B, T, N, d, K,
          stream_of(dev))
     return dy, dgate, d_h0, d_q0, d_w
@@ -212,19 +230,22 @@ def window_forward(logits: Tensor, y: Tensor, gate_pre: Tensor, reset: Tensor, h
     refreshed``), the sweep's outputs (:func:`forward`) and ``h_max [B,T]``."""
     B, T, N, M = (int(s) for s in logits.shape)
     h_max = torch.empty(B, T, dtype=torch.float32, device=y.device) if with_h_max else None
-    cells, units, valid, theta, refreshed = route(logits, cost, cfg, reset=reset, age0=age0,
-                                                  h_max_zero=h_max)
-    out = forward(y, gate_pre, reset, cells, valid, h0, q0, age0, pos0, N, cand_norm=cand_norm,
+    cells, units, valid, theta, refreshed, slots = route(logits, cost, cfg, reset=reset,
+                                                         age0=age0, h_max_zero=h_max,
+                                                         with_slots=True)
+    out = forward(y, gate_pre, reset, slots, h0, q0, age0, pos0, N, cand_norm=cand_norm,
                   cand_w=cand_w, cand_eps=cand_eps, h_max=h_max)
-    out.update(cells=cells, units=units, valid=valid, theta=theta, refreshed=refreshed)
+    out.update(cells=cells, units=units, valid=valid, theta=theta, refreshed=refreshed,
+               slots=slots)
     return out
 
 
 def window_backward(y, gate_pre, h_old, cells, valid, reset, n_cells, d_q_pre, d_q_post, d_h_sel,
                     d_h_T=None, d_q_T=None, *, cand_norm=False, cand_w=None, cand_eps=1e-6):
-    """Alias of :func:`backward` with the oracle's argument order."""
-    return backward(y, gate_pre, h_old, cells, valid, reset, n_cells, d_q_pre, d_q_post, d_h_sel,
-                    d_h_T, d_q_T, cand_norm=cand_norm, cand_w=cand_w, cand_eps=cand_eps)
+    """:func:`backward` with the oracle's argument order (separate cells and valid)."""
+    return backward(y, gate_pre, h_old, pack_slots(cells, valid), reset, n_cells, d_q_pre,
+                    d_q_post, d_h_sel, d_h_T, d_q_T, cand_norm=cand_norm, cand_w=cand_w,
+                    cand_eps=cand_eps)
 
 
 class WindowRecurrence(torch.autograd.Function):
@@ -245,7 +266,7 @@ class WindowRecurrence(torch.autograd.Function):
         out = window_forward(logits, y, gate_pre, reset, h0.detach().float().contiguous(),
                              q0.detach().float().contiguous(), age0, pos0, cost, cfg,
                              cand_norm=cand_norm, cand_w=cand_w, cand_eps=cand_eps)
-        ctx.save_for_backward(y, gate_pre, out["h_old"], out["cells"], out["valid"], reset,
+        ctx.save_for_backward(y, gate_pre, out["h_old"], out["slots"], reset,
                               cand_w if cand_norm else None)
         ctx.n_cells = int(logits.shape[2])
         ctx.cand_norm = cand_norm
@@ -255,14 +276,14 @@ class WindowRecurrence(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, d_q_pre, d_q_post, d_h_sel, d_h_T, d_q_T):
-        y, gate_pre, h_old, cells, valid, reset, cand_w = ctx.saved_tensors
+        y, gate_pre, h_old, slots, reset, cand_w = ctx.saved_tensors
         io = y.dtype
 
         def cot(t, dtype):
             return None if t is None else t.to(dtype).contiguous()
 
         dy, dgate, d_h0, d_q0, d_w = backward(
-            y, gate_pre, h_old, cells, valid, reset, ctx.n_cells, cot(d_q_pre, io),
+            y, gate_pre, h_old, slots, reset, ctx.n_cells, cot(d_q_pre, io),
             cot(d_q_post, io), cot(d_h_sel, io), cot(d_h_T, torch.float32),
             cot(d_q_T, torch.float32), cand_norm=ctx.cand_norm, cand_w=cand_w,
             cand_eps=ctx.cand_eps)

@@ -61,6 +61,8 @@ const char* hsn_win_last_error(void);
  *   age0 [B,N] int64, reset [B,T] u8: read only with probes (the ages evolve with the
  *          decisions, so a window with probes is walked position by position per row)
  *   cells, units [B,T,K] (index_bits), valid, refreshed [B,T,K] u8, theta [B,T] f32
+ *   slots [B,T,K] int32, optional: the slot's cell where valid, -1 where padded (the packed
+ *          decision the sweeps read)
  *   h_max_zero [B,T] f32, optional: set to 0 (the forward sweep max-reduces into it)
  * For every position: score_i = max_j (logit_ij - lambda cost_j) (fp32, no contraction), unit
  * the first maximiser; cells sorted by descending score, ties by index (NaN first, -0 = +0,
@@ -73,7 +75,8 @@ const char* hsn_win_last_error(void);
 int hsn_win_route(const void* logits, int io_dtype, int64_t width, const float* cost,
                   const int64_t* age0, const uint8_t* reset, void* cells, void* units,
                   int index_bits, uint8_t* valid, float* theta, uint8_t* refreshed,
-                  float* h_max_zero, int B, int T, int N, int M, int K, int age_max, int probes,
+                  int32_t* slots, float* h_max_zero, int B, int T, int N, int M, int K,
+                  int age_max, int probes,
                   float lambda_cost, float cell_overhead, float shared_cost, float limit,
                   int reserved, int reserved_units, void* stream);
 
@@ -100,8 +103,8 @@ int hsn_win_select(const void* logits, int io_dtype, int64_t width, const int64_
  * python/hsn/kernels/native.py:244-303; python/hsn/model/state.py:267-324).
  *   y, gate_pre [B,T,K,d] io_dtype: candidate input and write-gate pre-activation
  *   c = tanh(y) (cand_norm 0) or tanh(y * rsqrt(mean_d(y^2) + cand_eps) * cand_w) (cand_norm 1,
- *   cand_w [d] f32, rms_scratch [B,T,K] f32 workspace); b = sigmoid(gate_pre)
- *   reset [B,T] u8; cells [B,T,K] (index_bits), valid [B,T,K] u8 (the router's decision)
+ *   cand_w [d] f32, rms_scratch a workspace of B*T*K*(d*sizeof(io) + 4) bytes); b = sigmoid
+ *   reset [B,T] u8; slots [B,T,K] int32 (hsn_win_route's packed decision: cell or -1)
  *   h0 [B,N,d], q0 [B,d] f32; age0 [B,N], pos0 [B] int64
  * Outputs (each optional): q_pre, q_post [B,T,d] io_dtype (summary before / after each
  * position), h_sel [B,T,K,d] io_dtype (the slots' cells after the update; cell 0 on padded
@@ -110,12 +113,11 @@ int hsn_win_select(const void* logits, int io_dtype, int64_t width, const int64_
  * hsn_win_route zeroes it), h_T [B,N,d], q_T [B,d] f32, age_T [B,N], pos_T [B] int64.
  */
 int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype, const float* cand_w,
-                    int cand_norm, float cand_eps, float* rms_scratch, const uint8_t* reset,
-                    const void* cells, const uint8_t* valid, int index_bits, const float* h0,
-                    const float* q0, const int64_t* age0, const int64_t* pos0, void* q_pre,
-                    void* q_post, void* h_sel, void* h_old, float* h_max, float* h_T, float* q_T,
-                    int64_t* age_T, int64_t* pos_T, int B, int T, int N, int d, int K,
-                    void* stream);
+                    int cand_norm, float cand_eps, void* rms_scratch, const uint8_t* reset,
+                    const int32_t* slots, const float* h0, const float* q0, const int64_t* age0,
+                    const int64_t* pos0, void* q_pre, void* q_post, void* h_sel, void* h_old,
+                    float* h_max, float* h_T, float* q_T, int64_t* age_T, int64_t* pos_T, int B,
+                    int T, int N, int d, int K, void* stream);
 
 /*
  * Backward of the window with the activations fused and the carried-state gradient: the
@@ -123,20 +125,18 @@ int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype, const flo
  * seeded with the end-state cotangent (python/hsn/train/state_gradient.py:402-416), the VJPs
  * of tanh / RMSNorm and sigmoid (the replay's autograd, python/hsn/train/split.py:588-716),
  * and the start-state cotangent that split.py:173-174 drops.
- *   y, gate_pre, h_old [B,T,K,d] io_dtype; cells, valid [B,T,K]; reset [B,T] u8
+ *   y, gate_pre, h_old [B,T,K,d] io_dtype; slots [B,T,K] int32; reset [B,T] u8
  *   d_q_pre, d_q_post [B,T,d], d_h_sel [B,T,K,d] io_dtype (optional: absent = zero)
  *   d_h_T [B,N,d], d_q_T [B,d] f32 (optional: absent = zero)
  * Outputs: dy, dgate [B,T,K,d] io_dtype (exact zeros on padded slots); d_h0 [B,N,d], d_q0 [B,d]
- * f32 (optional); d_cand_w [d] f32 (cand_norm 1 only; rms_scratch [B,T,K] holds the forward's
- * 1/rms and is overwritten).
+ * f32 (optional); d_cand_w [d] f32 (cand_norm 1; rms_scratch as hsn_win_forward's).
  */
 int hsn_win_backward(const void* y, const void* gate_pre, const void* h_old, int io_dtype,
-                     const float* cand_w, int cand_norm, float cand_eps, float* rms_scratch,
-                     const void* cells, const uint8_t* valid, int index_bits,
-                     const uint8_t* reset, const void* d_q_pre, const void* d_q_post,
-                     const void* d_h_sel, const float* d_h_T, const float* d_q_T, void* dy,
-                     void* dgate, float* d_h0, float* d_q0, float* d_cand_w, int B, int T,
-                     int N, int d, int K, void* stream);
+                     const float* cand_w, int cand_norm, float cand_eps, void* rms_scratch,
+                     const int32_t* slots, const uint8_t* reset, const void* d_q_pre,
+                     const void* d_q_post, const void* d_h_sel, const float* d_h_T,
+                     const float* d_q_T, void* dy, void* dgate, float* d_h0, float* d_q0,
+                     float* d_cand_w, int B, int T, int N, int d, int K, void* stream);
 
 /*
  * The reference's backward recurrence from the candidate and gate themselves (no activation):
@@ -170,7 +170,7 @@ int hsn_win_recurrence_dense(const float* c, const float* b, const float* h_old,
  * kernels/cuda/hsn_window.cu:751-954 `hsn_win_cell_update`, wrappers cell_update_op /
  * update_tape_op (python/hsn/kernels/window.py:605-760).
  *   y [B,K,d], gate [B,K,d] io_dtype (the round's products); cand_w [d] f32 (cand_norm 1;
- *   rms_scratch [B,K] f32 workspace)
+ *   rms_scratch a workspace of B*K*(d*sizeof(io) + 4) bytes)
  *   h [B,n_state,N,d], q [B,n_state,d] f32, age [B,n_state,N] int64: record t read
  *   pos [B] int64 (optional), cells [B,n_slot,K] int64, valid [B,n_slot,K] u8: record t
  *   h_next, q_next, age_next: record t_out written (may be the buffers above, t_out != t);
@@ -179,7 +179,7 @@ int hsn_win_recurrence_dense(const float* c, const float* b, const float* h_old,
  *   record); q_post [B,n_slot,d] f32 (optional, the summary after the round).
  */
 int hsn_win_cell_update(const void* y, const void* gate, int io_dtype, const float* cand_w,
-                        int cand_norm, float cand_eps, float* rms_scratch, const float* h,
+                        int cand_norm, float cand_eps, void* rms_scratch, const float* h,
                         const float* q, const int64_t* age, const int64_t* pos,
                         const int64_t* cells, const uint8_t* valid, float* h_next,
                         float* q_next, int64_t* age_next, int64_t* pos_next, float* h_sel,

@@ -64,14 +64,13 @@ def test_argument_errors_return_status_without_a_gpu():
         pytest.skip("library not built here")
     lib = _lib.library()
     # K > N is rejected up front
-    status = lib.hsn_win_route(1, 0, 1, 1, None, None, 1, 1, 32, 1, 1, 1, None, 1, 1, 4, 1, 8, 0,
-                               0, 0.0, 0.0, 0.0, 1.0, 0, 0, None)
+    status = lib.hsn_win_route(1, 0, 1, 1, None, None, 1, 1, 32, 1, 1, 1, None, None, 1, 1, 4, 1,
+                               8, 0, 0, 0.0, 0.0, 0.0, 1.0, 0, 0, None)
     assert status == 1
     assert b"K <= N" in lib.hsn_win_last_error()
     # f16 is not a window storage type
-    status = lib.hsn_win_forward(1, 1, 1, None, 0, 0.0, None, 1, 1, 1, 32, 1, 1, None, None, None,
-                                 None, None, None, None, None, None, None, None, 1, 1, 4, 4, 2,
-                                 None)
+    status = lib.hsn_win_forward(1, 1, 1, None, 0, 0.0, None, 1, 1, 1, 1, None, None, None, None,
+                                 None, None, None, None, None, None, None, 1, 1, 4, 4, 2, None)
     assert status == 2
     # a NULL required pointer
     status = lib.hsn_gated_delta_update(None, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, None)

@@ -211,8 +211,8 @@ def test_window_forward_and_backward_match_oracle(dev, case):
     wb = O.window_backward(w["y"], w["gate_pre"], want["h_old"], want["cells"], want["valid"],
                            w["reset"], cfg_w.N, cot["d_q_pre"], cot["d_q_post"], d_h_sel,
                            cot["d_h_T"], cot["d_q_T"], cand_norm=rms, cand_w=cand_w)
-    gb = window.backward(D["y"], D["gate_pre"], want["h_old"].to(dev), got["cells"],
-                         got["valid"], D["reset"], cfg_w.N, cot["d_q_pre"].to(dev),
+    gb = window.backward(D["y"], D["gate_pre"], want["h_old"].to(dev), got["slots"],
+                         D["reset"], cfg_w.N, cot["d_q_pre"].to(dev),
                          cot["d_q_post"].to(dev), d_h_sel.to(dev), cot["d_h_T"].to(dev),
                          cot["d_q_T"].to(dev), cand_norm=rms,
                          cand_w=None if cand_w is None else cand_w.to(dev))
@@ -236,7 +236,7 @@ def test_backward_without_optional_cotangents(dev):
         pre, post, sel = (cot[k] if p else None for k, p in zip(("d_q_pre", "d_q_post", "d_h_sel"), present))
         sel = None if sel is None else _valid_mask(sel, fw["valid"])
         wb = O.window_backward(*args_cpu, pre, post, sel)
-        gb = window.backward(w["y"].to(dev), w["gate_pre"].to(dev), fw["h_old"].to(dev),
+        gb = window.window_backward(w["y"].to(dev), w["gate_pre"].to(dev), fw["h_old"].to(dev),
                              fw["cells"].int().to(dev), fw["valid"].to(dev), w["reset"].to(dev),
                              cfg_w.N, None if pre is None else pre.to(dev),
                              None if post is None else post.to(dev),
@@ -439,7 +439,7 @@ def test_ref_shape_window_rows_match_oracle(dev):
     _close(got["h"][rows], want["h"], F32_TOL, "h_T")
     assert torch.equal(got["age"][rows].cpu(), want["age"])
     d_sel = cot["d_h_sel"]
-    args = (D["y"], D["gate_pre"], got["h_old"], got["cells"], got["valid"], D["reset"], cfg_w.N)
+    args = (D["y"], D["gate_pre"], got["h_old"], got["slots"], D["reset"], cfg_w.N)
     g1 = window.backward(*args, cot["d_q_pre"].to(dev), cot["d_q_post"].to(dev), d_sel.to(dev),
                          cot["d_h_T"].to(dev), cot["d_q_T"].to(dev))
     g2 = window.backward(*args, 2 * cot["d_q_pre"].to(dev), 2 * cot["d_q_post"].to(dev),
