@@ -55,31 +55,46 @@ __device__ __forceinline__ uint32_t group_max(uint32_t v) {
     return v;
 }
 
+// Unsigned max over the whole wavefront of a value already uniform within aligned groups of L
+// lanes: finish the row with DPP, join the four 16-lane rows with row_bcast:15 / row_bcast:31
+// (gfx9 DPP), and read the result from lane 63.
+template <int L>
+__device__ __forceinline__ uint32_t wave_max_from_groups(uint32_t v) {
+    if constexpr (L < 2) v = umax(v, dpp_u32<dpp::kXor1>(v));
+    if constexpr (L < 4) v = umax(v, dpp_u32<dpp::kXor2>(v));
+    if constexpr (L < 8) v = umax(v, dpp_u32<dpp::kHalfMirror>(v));
+    if constexpr (L < 16) v = umax(v, dpp_u32<dpp::kRor8>(v));
+    if constexpr (L < 32) {
+        const uint32_t a = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+            static_cast<int>(v), static_cast<int>(v), 0x142, 0xa, 0xf, false));  // row_bcast:15
+        v = umax(v, a);
+    }
+    if constexpr (L < 64) {
+        const uint32_t a = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+            static_cast<int>(v), static_cast<int>(v), 0x143, 0xc, 0xf, false));  // row_bcast:31
+        v = umax(v, a);
+    }
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
 // ------------------------------------------------------------------------------------------
 // Activations, branch-free, from exp2 and reciprocal (v_exp_f32 / v_rcp_f32, about 1 ulp each):
 //   sigmoid(x) = 1 / (1 + 2^(-x log2 e))
-//   tanh(x)    = sign(x) (1 - t) / (1 + t),  t = 2^(-2|x| log2 e)
-// with the odd Taylor polynomial x - x^3/3 + 2x^5/15 - 17x^7/315 for |x| < 1/16, where the
-// quotient form loses relative accuracy (the polynomial's truncation error is below 2^-33 there).
-// Absolute error stays a few ulps of 1, well inside the 1e-5 parity bar.
+//   tanh(x)    = 2 sigmoid(2x) - 1
+// The tanh form has an absolute error of a few ulps of 1 everywhere (its relative error grows
+// as |x| -> 0, where tanh(x) ~ x), well inside the 1e-5 parity bar |err| <= 1e-5 max(|want|, 1).
+// Both saturate correctly: exp2 overflows to +inf (reciprocal 0) or underflows to 0.
 // ------------------------------------------------------------------------------------------
 
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float fast_sigmoid(float x) {
-    const float e = __builtin_amdgcn_exp2f(-x * kLog2e);
-    return __builtin_amdgcn_rcpf(1.0f + e);
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-kLog2e * x));
 }
 
 __device__ __forceinline__ float fast_tanh(float x) {
-    const float ax = fabsf(x);
-    const float t = __builtin_amdgcn_exp2f(-2.0f * kLog2e * ax);
-    const float q = (1.0f - t) * __builtin_amdgcn_rcpf(1.0f + t);
-    const float x2 = x * x;
-    const float poly =
-        ax * (1.0f + x2 * (-1.0f / 3.0f + x2 * (2.0f / 15.0f + x2 * (-17.0f / 315.0f))));
-    const float m = ax < 0.0625f ? poly : q;
-    return copysignf(m, x);
+    const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.0f * kLog2e * x));
+    return 2.0f * s - 1.0f;
 }
 
 }  // namespace hsn

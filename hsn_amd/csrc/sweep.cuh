@@ -22,6 +22,7 @@
 #pragma once
 
 #include "common.cuh"
+#include "bufio.cuh"
 #include "dpp.cuh"
 
 namespace hsn {
@@ -43,26 +44,32 @@ __device__ __forceinline__ int slot_cell(typename SLOT::Raw c, uint8_t v) {
     else return v ? static_cast<int>(c) : -1;
 }
 
-// (row, slice) of a workgroup. With B a multiple of 8 the slices of one row go to one XCD
-// (workgroups are dealt to the 8 XCDs round-robin by id), so the row's shared cache lines (the
-// slots' rows of y/gate, the decisions) are fetched into one L2 instead of several.
-__device__ __forceinline__ void block_coords(int bid, int nslices, int xcd_rows, int& b,
-                                             int& slice) {
-    if (xcd_rows > 0) {
-        const int x8 = bid & 7, q = bid >> 3;
-        const int rl = q / nslices;
-        slice = q - rl * nslices;
-        b = x8 * xcd_rows + rl;
-    } else {
-        b = bid / nslices;
-        slice = bid - b * nslices;
-    }
+// (row, slice) of a workgroup, from a grid (G, nslices, B/G), G = 8 when B is a multiple of 8
+// (else 1). Workgroups are dealt to the 8 XCDs round-robin by linear id, so blockIdx.x is the
+// XCD and all slices of a row land on one XCD: the row's shared cache lines (the slots' rows of
+// y/gate, the decisions) are fetched into one L2 instead of several. No division: the resources
+// built from (row, slice) stay in SGPRs.
+__device__ __forceinline__ void block_coords(int& b, int& slice) {
+    b = blockIdx.x * gridDim.z + blockIdx.z;
+    slice = blockIdx.y;
+}
+
+inline dim3 sweep_grid(int B, int nslices) {
+    const int g = B % 8 == 0 ? 8 : 1;
+    return dim3(g, nslices, B / g);
 }
 
 constexpr int fwd_depth(int kpl) { return kpl >= 8 ? 2 : 8 / kpl; }
 constexpr int bwd_depth(int kpl) { return kpl >= 4 ? 2 : (kpl == 2 ? 3 : 6); }
 
-__device__ __forceinline__ int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+// Select element `i` (a lane-dependent index) of a register array without indexing memory.
+template <int P, typename T>
+__device__ __forceinline__ T pick(const T (&v)[P], int i) {
+    T r = v[0];
+#pragma unroll
+    for (int p = 1; p < P; ++p) r = i == p ? v[p] : r;
+    return r;
+}
 
 // ------------------------------------------------------------------------------------------
 // Forward
@@ -71,7 +78,7 @@ __device__ __forceinline__ int clampi(int v, int lo, int hi) { return v < lo ? l
 struct FwdArgs {
     const void* y;  // the candidate's pre-activation (the RMS prologue's output with the norm)
     const void* g;
-    int64_t y_row;  // row stride of y and g; position stride K*d
+    int64_t y_row;  // row stride of y and g (elements); position stride K*d
     const uint8_t* reset;  // reset[b*r_row + t] zeroes the state before position t (NULL: none)
     int64_t r_row;
     const uint8_t* clear;  // clear[b*c_row] zeroes the written end state (NULL: none)
@@ -116,68 +123,80 @@ struct FwdStage {
 
 template <typename IN, typename OUT, typename SLOT, int S, int KPL>
 __global__ __launch_bounds__(64) void fwd_sweep(FwdArgs a) {
+    using Raw = typename SLOT::Raw;
     extern __shared__ float lds[];
     constexpr int L = kWave / S;
     constexpr int P = fwd_depth(KPL);
     const int lane = lane_id();
     const int x = lane / L, kl = lane % L;
-    const int nslices = a.d / S;
     int b, slice;
-    block_coords(blockIdx.x, nslices, a.xcd_rows, b, slice);
+    block_coords(b, slice);
     const int col = slice * S + x;
     const int N = a.N, d = a.d, K = a.K, T = a.T;
-    float* lds_h = lds;
-    int* lds_last = reinterpret_cast<int*>(lds + N * S);
+    float* lds_h = lds;                                  // [N*S], then one dummy word
+    int* lds_last = reinterpret_cast<int*>(lds + N * S + 1);  // [N], then one dummy word
+    const int dummy_h = N * S;
     const bool track_age = slice == 0 && a.age_T != nullptr;
     const bool want_max = a.h_max != nullptr;
+    const bool has_reset = a.reset != nullptr;
 
-    // uniform row bases; per position a uniform offset, per lane a 32-bit offset (the loads
-    // take the saddr + voffset form, no per-lane 64-bit address arithmetic)
-    const typename SLOT::Raw* cells_row = static_cast<const typename SLOT::Raw*>(a.cells) + b * a.s_row;
-    const uint8_t* valid_row = a.valid ? a.valid + b * a.s_row : nullptr;
-    const IN* y = static_cast<const IN*>(a.y) + b * a.y_row;
-    const IN* g = static_cast<const IN*>(a.g) + b * a.y_row;
-    uint32_t ko[KPL];  // this lane's slot offsets within a position (slots clamped into [0, K))
-    uint32_t kq[KPL];
+    // the row's tensors as buffer resources: per position a uniform soffset, per lane a voffset
+    const uint32_t kd = uint32_t(K) * d;
+    const rsrc_t ry = make_rsrc(static_cast<const IN*>(a.y) + b * a.y_row, T * kd * sizeof(IN));
+    const rsrc_t rg = make_rsrc(static_cast<const IN*>(a.g) + b * a.y_row, T * kd * sizeof(IN));
+    const rsrc_t rc = make_rsrc(static_cast<const Raw*>(a.cells) + b * a.s_row, T * K * sizeof(Raw));
+    const rsrc_t rv = make_rsrc(a.valid ? a.valid + b * a.s_row : nullptr, a.valid ? T * K : 0);
+    const rsrc_t rr = make_rsrc(has_reset ? a.reset + b * a.r_row : nullptr, has_reset ? T : 0);
+    // outputs: uniform row pointers, a per-position uniform offset, per-lane element offsets
+    OUT* const ho_row = a.h_old ? static_cast<OUT*>(a.h_old) + b * a.o_row : nullptr;
+    OUT* const hs_row = a.h_sel ? static_cast<OUT*>(a.h_sel) + b * a.o_row : nullptr;
+    OUT* const qa_row = a.q_pre ? static_cast<OUT*>(a.q_pre) + b * a.qo_row : nullptr;
+    OUT* const qb_row = a.q_post ? static_cast<OUT*>(a.q_post) + b * a.qo_row : nullptr;
+    bool active[KPL];
+    uint32_t vy[KPL], vc[KPL], vv[KPL], eo[KPL];
 #pragma unroll
     for (int j = 0; j < KPL; ++j) {
-        const int k = kl + j * L < K ? kl + j * L : K - 1;
-        ko[j] = static_cast<uint32_t>(k * d + col);
-        kq[j] = static_cast<uint32_t>(k);
+        const int k = kl + j * L;
+        active[j] = k < K;
+        vy[j] = active[j] ? uint32_t(k * d + col) * sizeof(IN) : kOob;
+        eo[j] = uint32_t((active[j] ? k : 0) * d + col);
+        vc[j] = active[j] ? uint32_t(k) * sizeof(Raw) : kOob;
+        vv[j] = active[j] ? uint32_t(k) : kOob;
     }
 
     // the start state of this slice and the column maxima of |h|
+    // (every loop below runs a uniform trip count with a per-lane guard: a divergent loop exit
+    // would make the values defined in it divergent, row pointers included)
     uint32_t colmax = 0u;
-    for (int n = kl; n < N; n += L) {
-        const float v = a.h0[b * a.h0_row + int64_t(n) * d + col];
-        lds_h[n * S + x] = v;
-        colmax = umax(colmax, abs_bits(v));
+    const float* h0_row = a.h0 + b * a.h0_row;
+    for (int n0 = 0; n0 < N; n0 += L) {
+        const int n = n0 + kl;
+        if (n < N) {
+            const float v = h0_row[int64_t(n) * d + col];
+            lds_h[n * S + x] = v;
+            colmax = umax(colmax, abs_bits(v));
+        }
     }
     colmax = group_max<L>(colmax);
     if (track_age)
-        for (int n = lane; n < N; n += kWave) lds_last[n] = -1;
+        for (int n0 = 0; n0 < N; n0 += kWave)
+            if (n0 + lane < N) lds_last[n0 + lane] = -1;
     float q = a.q0[b * a.q0_row + col];
     int last_reset = -1;
 
-    // without resets the flag load reads a valid dummy (the first byte of the decisions) and
-    // has_reset masks it, so the load stays unconditional
-    const bool has_reset = a.reset != nullptr;
-    const uint8_t* reset_row = has_reset ? a.reset + b * a.r_row : static_cast<const uint8_t*>(a.cells);
-    const uint32_t kd32 = static_cast<uint32_t>(K * d);  // a row's T*K*d fits int32 (host check)
     auto load = [&](FwdStage<IN, SLOT, KPL>& st, int t) {
         t = uniform(t < T ? t : T - 1);
-        const IN* yt = y + uint32_t(t) * kd32;
-        const IN* gt = g + uint32_t(t) * kd32;
-        const typename SLOT::Raw* ct = cells_row + uint32_t(t) * uint32_t(K);
+        const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
+        const uint32_t sc = uint32_t(t) * K;
 #pragma unroll
         for (int j = 0; j < KPL; ++j) {
-            st.y[j] = yt[ko[j]];
-            st.g[j] = gt[ko[j]];
-            st.c[j] = ct[kq[j]];
-            if constexpr (sizeof(typename SLOT::Raw) == 8) st.v[j] = (valid_row + uint32_t(t) * uint32_t(K))[kq[j]];
+            st.y[j] = bload<IN>(ry, vy[j], sy);
+            st.g[j] = bload<IN>(rg, vy[j], sy);
+            st.c[j] = bload<Raw>(rc, vc[j], sc * sizeof(Raw));
+            if constexpr (sizeof(Raw) == 8) st.v[j] = bload<uint8_t>(rv, vv[j], sc);
             else st.v[j] = 1;
         }
-        st.r = reset_row[has_reset ? t : 0];
+        st.r = bload<uint8_t>(rr, 0u, uint32_t(t));
     };
 
     // the prologue keeps its loads in stage order (the scheduler would otherwise reorder
@@ -190,132 +209,110 @@ __global__ __launch_bounds__(64) void fwd_sweep(FwdArgs a) {
     }
 
     for (int t0 = 0; t0 < T; t0 += P) {
-        float qpre_b[P], qpost_b[P];
-        uint32_t hmax_b[P];
+        uint32_t hm_b[P];  // the row max |h| of each position of the block (uniform)
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const int t = t0 + p;
-            qpre_b[p] = 0.0f;
-            qpost_b[p] = 0.0f;
-            hmax_b[p] = 0u;
+            hm_b[p] = 0u;
             if (t < T) {
                 if (has_reset && uniform(stage[p].r)) {
                     // a document boundary: h, q (and the ages) restart at zero before t reads them
-                    for (int e = lane; e < N * S; e += kWave) lds_h[e] = 0.0f;
+                    for (int e0 = 0; e0 < N * S; e0 += kWave)
+                        if (e0 + lane < N * S) lds_h[e0 + lane] = 0.0f;
                     colmax = 0u;
                     q = 0.0f;
                     last_reset = t;
                 }
-                qpre_b[p] = q;
+                const uint32_t tq = uint32_t(uniform(t)) * d;
+                if (qa_row && kl == 0) store_f32(qa_row + tq, col, q);
                 int cell[KPL];
                 float hold[KPL];
 #pragma unroll
                 for (int j = 0; j < KPL; ++j) {
-                    cell[j] = kl + j * L < K ? slot_cell<SLOT>(stage[p].c[j], stage[p].v[j]) : -2;
+                    cell[j] = active[j] ? slot_cell<SLOT>(stage[p].c[j], stage[p].v[j]) : -2;
                     hold[j] = lds_h[(cell[j] > 0 ? cell[j] : 0) * S + x];
                 }
+                float delta = 0.0f;
+                bool padded = false, drop = false;
+                uint32_t up = 0u;
                 float hnew[KPL];
 #pragma unroll
                 for (int j = 0; j < KPL; ++j) {
                     const float c = fast_tanh(to_f32(stage[p].y[j]));
                     const float bg = fast_sigmoid(to_f32(stage[p].g[j]));
                     hnew[j] = (1.0f - bg) * hold[j] + bg * c;
-                }
-                float delta = 0.0f;
-                bool padded = false, drop = false;
-                uint32_t up = 0u;
-#pragma unroll
-                for (int j = 0; j < KPL; ++j) {
-                    if (cell[j] >= 0) {
-                        lds_h[cell[j] * S + x] = hnew[j];
-                        delta += hnew[j] - hold[j];
-                        const uint32_t ob = abs_bits(hold[j]), nb = abs_bits(hnew[j]);
-                        drop |= ob == colmax && nb < ob;
-                        up = umax(up, nb);
-                    }
+                    const bool ok = cell[j] >= 0;
+                    lds_h[ok ? cell[j] * S + x : dummy_h] = hnew[j];
+                    delta += ok ? hnew[j] - hold[j] : 0.0f;
+                    const uint32_t ob = abs_bits(hold[j]), nb = abs_bits(hnew[j]);
+                    drop |= ok && ob == colmax && nb < ob;
+                    up = umax(up, ok ? nb : 0u);
                     padded |= cell[j] == -1;
                 }
                 float cell0 = 0.0f;
                 if (ballot(padded)) cell0 = lds_h[x];  // a padded slot shows cell 0 after the update
+                const uint32_t to = uint32_t(uniform(t)) * kd;
 #pragma unroll
                 for (int j = 0; j < KPL; ++j) {
-                    if (cell[j] != -2) {
-                        const int64_t ot = b * a.o_row + uint32_t(uniform(t)) * kd32;
-                        if (a.h_old) store_f32(static_cast<OUT*>(a.h_old) + ot, ko[j], hold[j]);
-                        if (a.h_sel)
-                            store_f32(static_cast<OUT*>(a.h_sel) + ot, ko[j], cell[j] >= 0 ? hnew[j] : cell0);
+                    if (active[j]) {
+                        if (ho_row) store_f32(ho_row + to, eo[j], hold[j]);
+                        if (hs_row) store_f32(hs_row + to, eo[j], cell[j] >= 0 ? hnew[j] : cell0);
                     }
                 }
                 // q' = q + sum_k (h' - h)[k] / N over the column's slot lanes
                 delta = group_sum<L>(delta);
                 q = q + (a.n_pow2 ? delta * a.inv_n : delta / a.n_f);
-                qpost_b[p] = q;
+                if (qb_row && kl == 0) store_f32(qb_row + tq, col, q);
                 if (want_max) {
                     // the column's max |h|: raised by the new values, rescanned only when a cell
-                    // that held it shrank
+                    // that held it shrank; the row's is the max over the slice's columns
                     colmax = umax(colmax, group_max<L>(up));
                     if (ballot(drop)) {
                         uint32_t m = 0u;
-                        for (int n = kl; n < N; n += L) m = umax(m, abs_bits(lds_h[n * S + x]));
+                        for (int n0 = 0; n0 < N; n0 += L)
+                            if (n0 + kl < N) m = umax(m, abs_bits(lds_h[(n0 + kl) * S + x]));
                         colmax = group_max<L>(m);
                     }
-                    uint32_t row = 0u;
-#pragma unroll
-                    for (int xx = 0; xx < S; ++xx)
-                        row = umax(row, static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(colmax), xx * L)));
-                    hmax_b[p] = row;
+                    hm_b[p] = wave_max_from_groups<L>(colmax);
                 }
-                if (track_age && x == 0) {
+                if (track_age) {
 #pragma unroll
                     for (int j = 0; j < KPL; ++j)
-                        if (cell[j] >= 0) lds_last[cell[j]] = t;
+                        lds_last[(cell[j] >= 0 && x == 0) ? cell[j] : N] = t;
                 }
             }
             load(stage[p], t + P);
         }
-        // the block's per-position outputs, one store per lane: lane (x, kl) takes position
-        // t0 + kl (+ L, ...) of column x
+        if (want_max) {  // lane p sends position t0 + p's row max
+            uint32_t m = 0u;
 #pragma unroll
-        for (int jj = 0; jj * L < P; ++jj) {
-            const int p = kl + jj * L;
-            float vpre = 0.0f, vpost = 0.0f;
-            uint32_t vmax = 0u;
-#pragma unroll
-            for (int pp = 0; pp < P; ++pp) {
-                if (p == pp) {
-                    vpre = qpre_b[pp];
-                    vpost = qpost_b[pp];
-                    vmax = hmax_b[pp];
-                }
-            }
-            if (p < P && t0 + p < T) {
-                const uint32_t qo = static_cast<uint32_t>((t0 + p) * d + col);
-                const int64_t qb = b * a.qo_row;
-                if (a.q_pre) store_f32(static_cast<OUT*>(a.q_pre) + qb, qo, vpre);
-                if (a.q_post) store_f32(static_cast<OUT*>(a.q_post) + qb, qo, vpost);
-                if (want_max && x == 0)
-                    atomicMax(reinterpret_cast<unsigned int*>(a.h_max + b * a.hm_row) + (t0 + p), vmax);
-            }
+            for (int p = 0; p < P; ++p) m = lane == p ? hm_b[p] : m;
+            if (lane < P && t0 + lane < T)
+                atomicMax(reinterpret_cast<unsigned int*>(a.h_max + b * a.hm_row) + (t0 + lane), m);
         }
     }
 
     // the end state (zeroed when the caller's next record resets this row)
     const bool clear = a.clear ? a.clear[b * a.c_row] != 0 : false;
     if (a.h_T) {
-        for (int e = lane; e < N * S; e += kWave) {
-            const int n = e / S, xx = e % S;
-            a.h_T[b * a.hT_row + int64_t(n) * d + slice * S + xx] = clear ? 0.0f : lds_h[e];
-        }
+        float* hT_row = a.h_T + b * a.hT_row;
+        for (int n0 = 0; n0 < N; n0 += L)
+            if (n0 + kl < N) hT_row[int64_t(n0 + kl) * d + col] = clear ? 0.0f : lds_h[(n0 + kl) * S + x];
     }
     if (a.q_T && kl == 0) a.q_T[b * a.qT_row + col] = clear ? 0.0f : q;
     if (track_age) {
-        for (int n = lane; n < N; n += kWave) {
-            const int ls = lds_last[n];
-            int64_t age;
-            if (ls >= 0 && ls >= last_reset) age = (T - 1) - ls;
-            else if (last_reset >= 0) age = T - last_reset;
-            else age = a.age0[b * a.a0_row + n] + T;
-            a.age_T[b * a.aT_row + n] = clear ? 0 : age;
+        const int64_t* age0_row = a.age0 + b * a.a0_row;
+        int64_t* ageT_row = a.age_T + b * a.aT_row;
+        for (int n0 = 0; n0 < N; n0 += kWave) {
+            const int n = n0 + lane;
+            if (n < N) {
+                const int ls = lds_last[n];
+                int64_t age;
+                if (ls >= 0 && ls >= last_reset) age = (T - 1) - ls;
+                else if (last_reset >= 0) age = T - last_reset;
+                else age = age0_row[n] + T;
+                ageT_row[n] = clear ? 0 : age;
+            }
         }
         if (a.pos_T && lane == 0)
             a.pos_T[b] = last_reset >= 0 ? int64_t(T - last_reset) : a.pos0[b] + T;
@@ -327,18 +324,18 @@ __global__ __launch_bounds__(64) void fwd_sweep(FwdArgs a) {
 // ------------------------------------------------------------------------------------------
 
 struct BwdArgs {
-    const void* y;  // the candidate's pre-activation (act 0: the candidate c itself)
-    const void* g;  // the gate's pre-activation (act 0: the gate b itself)
+    const void* y;  // the candidate's pre-activation (ACT false: the candidate c itself)
+    const void* g;  // the gate's pre-activation (ACT false: the gate b itself)
     const void* h_old;
-    const void* dsel;  // never NULL: a dummy of the same shape when absent (has_dsel 0)
+    const void* dsel;  // optional (NULL: zero)
     int64_t y_row;  // row stride of y, g, h_old, dsel, dy, dg ([., T, K, d])
     const void* cells;
     const uint8_t* valid;
     int64_t s_row;
     const uint8_t* reset;
     int64_t r_row;
-    const void* dq_pre;  // never NULL (dummy when absent)
-    const void* dq_post;
+    const void* dq_pre;  // optional
+    const void* dq_post;  // optional
     int64_t q_row;  // [., T, d]
     const float* dh_T;
     const float* dq_T;
@@ -346,7 +343,7 @@ struct BwdArgs {
     void* dg;
     float* dh0;
     float* dq0;
-    int B, T, N, d, K, S, act, xcd_rows, n_pow2, has_dsel, has_pre, has_post;
+    int B, T, N, d, K, S, xcd_rows, n_pow2;
     float inv_n, n_f;
 };
 
@@ -363,63 +360,76 @@ struct BwdStage {
     uint8_t r;
 };
 
-template <typename IN, typename SLOT, int KPL>
+template <typename IN, typename SLOT, bool ACT, int KPL>
 __global__ __launch_bounds__(64) void bwd_sweep(BwdArgs a) {
+    using Raw = typename SLOT::Raw;
     extern __shared__ float lds[];
     constexpr int P = bwd_depth(KPL);
     const int lane = lane_id();
     const int S = a.S, L = kWave / S;
     const int x = lane / L, kl = lane % L;
-    const int nslices = a.d / S;
     int b, slice;
-    block_coords(blockIdx.x, nslices, a.xcd_rows, b, slice);
+    block_coords(b, slice);
     const int col = slice * S + x;
     const int N = a.N, d = a.d, K = a.K, T = a.T;
-    float* lds_A = lds;
-    for (int n = kl; n < N; n += L)
-        lds_A[n * S + x] = a.dh_T ? a.dh_T[int64_t(b) * N * d + int64_t(n) * d + col] : 0.0f;
+    float* lds_A = lds;  // [N*S], then one dummy word
+    const int dummy = N * S;
+    // (uniform trip counts with per-lane guards: a divergent loop exit would make the values
+    // defined in it divergent, row pointers included)
+    const float* dhT_row = a.dh_T ? a.dh_T + int64_t(b) * N * d : nullptr;
+    for (int n0 = 0; n0 < N; n0 += L)
+        if (n0 + kl < N) lds_A[(n0 + kl) * S + x] = dhT_row ? dhT_row[int64_t(n0 + kl) * d + col] : 0.0f;
     float R = a.dq_T ? a.dq_T[int64_t(b) * d + col] : 0.0f;
 
-    const typename SLOT::Raw* cells_row = static_cast<const typename SLOT::Raw*>(a.cells) + b * a.s_row;
-    const uint8_t* valid_row = a.valid ? a.valid + b * a.s_row : nullptr;
+    const uint32_t kd = uint32_t(K) * d;
+    const uint32_t row_bytes = T * kd * sizeof(IN);
     const int64_t base = b * a.y_row;
-    const IN* y = static_cast<const IN*>(a.y) + base;
-    const IN* g = static_cast<const IN*>(a.g) + base;
-    const IN* ho = static_cast<const IN*>(a.h_old) + base;
-    const IN* ds = static_cast<const IN*>(a.dsel) + base;
-    const IN* dqa = static_cast<const IN*>(a.dq_pre) + b * a.q_row;
-    const IN* dqb = static_cast<const IN*>(a.dq_post) + b * a.q_row;
-    IN* dyo = static_cast<IN*>(a.dy) + base;
-    IN* dgo = static_cast<IN*>(a.dg) + base;
-    const uint8_t* reset_row = a.reset + b * a.r_row;
-    uint32_t ko[KPL], kq[KPL];
+    const rsrc_t ry = make_rsrc(static_cast<const IN*>(a.y) + base, row_bytes);
+    const rsrc_t rg = make_rsrc(static_cast<const IN*>(a.g) + base, row_bytes);
+    const rsrc_t rho = make_rsrc(static_cast<const IN*>(a.h_old) + base, row_bytes);
+    const rsrc_t rds = make_rsrc(a.dsel ? static_cast<const IN*>(a.dsel) + base : nullptr,
+                                 a.dsel ? row_bytes : 0);
+    IN* const dy_row = static_cast<IN*>(a.dy) + base;
+    IN* const dg_row = static_cast<IN*>(a.dg) + base;
+    const rsrc_t rc = make_rsrc(static_cast<const Raw*>(a.cells) + b * a.s_row, T * K * sizeof(Raw));
+    const rsrc_t rv = make_rsrc(a.valid ? a.valid + b * a.s_row : nullptr, a.valid ? T * K : 0);
+    const rsrc_t rr = make_rsrc(a.reset + b * a.r_row, T);
+    const uint32_t qbytes = T * uint32_t(d) * sizeof(IN);
+    const rsrc_t rqa = make_rsrc(a.dq_pre ? static_cast<const IN*>(a.dq_pre) + b * a.q_row : nullptr,
+                                 a.dq_pre ? qbytes : 0);
+    const rsrc_t rqb = make_rsrc(a.dq_post ? static_cast<const IN*>(a.dq_post) + b * a.q_row : nullptr,
+                                 a.dq_post ? qbytes : 0);
+    bool active[KPL];
+    uint32_t vy[KPL], vc[KPL], vv[KPL], eo[KPL];
 #pragma unroll
     for (int j = 0; j < KPL; ++j) {
-        const int k = kl + j * L < K ? kl + j * L : K - 1;
-        ko[j] = static_cast<uint32_t>(k * d + col);
-        kq[j] = static_cast<uint32_t>(k);
+        const int k = kl + j * L;
+        active[j] = k < K;
+        vy[j] = active[j] ? uint32_t(k * d + col) * sizeof(IN) : kOob;
+        eo[j] = uint32_t((active[j] ? k : 0) * d + col);
+        vc[j] = active[j] ? uint32_t(k) * sizeof(Raw) : kOob;
+        vv[j] = active[j] ? uint32_t(k) : kOob;
     }
-    const uint32_t colu = static_cast<uint32_t>(col);
-    const bool act = a.act != 0;
+    const uint32_t vq = uint32_t(col) * sizeof(IN);
 
-    const uint32_t kd32 = static_cast<uint32_t>(K * d);  // a row's T*K*d fits int32 (host check)
     auto load = [&](BwdStage<IN, SLOT, KPL>& st, int t) {
         t = uniform(t >= 0 ? t : 0);
-        const uint32_t tk = uint32_t(t) * kd32;
-        const typename SLOT::Raw* ct = cells_row + uint32_t(t) * uint32_t(K);
+        const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
+        const uint32_t sc = uint32_t(t) * K;
 #pragma unroll
         for (int j = 0; j < KPL; ++j) {
-            st.y[j] = (y + tk)[ko[j]];
-            st.g[j] = (g + tk)[ko[j]];
-            st.ho[j] = (ho + tk)[ko[j]];
-            st.ds[j] = (ds + tk)[ko[j]];
-            st.c[j] = ct[kq[j]];
-            if constexpr (sizeof(typename SLOT::Raw) == 8) st.v[j] = (valid_row + uint32_t(t) * uint32_t(K))[kq[j]];
+            st.y[j] = bload<IN>(ry, vy[j], sy);
+            st.g[j] = bload<IN>(rg, vy[j], sy);
+            st.ho[j] = bload<IN>(rho, vy[j], sy);
+            st.ds[j] = bload<IN>(rds, vy[j], sy);
+            st.c[j] = bload<Raw>(rc, vc[j], sc * sizeof(Raw));
+            if constexpr (sizeof(Raw) == 8) st.v[j] = bload<uint8_t>(rv, vv[j], sc);
             else st.v[j] = 1;
         }
-        st.qpre = (dqa + uint32_t(t) * uint32_t(d))[colu];
-        st.qpost = (dqb + uint32_t(t) * uint32_t(d))[colu];
-        st.r = reset_row[t];
+        const uint32_t sq = uint32_t(t) * d * sizeof(IN);
+        st.qpre = bload<IN>(rqa, vq, sq);
+        st.qpost = bload<IN>(rqb, vq, sq);
+        st.r = bload<uint8_t>(rr, 0u, uint32_t(t));
     };
 
     BwdStage<IN, SLOT, KPL> stage[P];
@@ -434,57 +444,57 @@ __global__ __launch_bounds__(64) void bwd_sweep(BwdArgs a) {
         for (int p = 0; p < P; ++p) {
             const int t = t0 - p;
             if (t >= 0) {
-                if (a.has_post) R += to_f32(stage[p].qpost);
+                R += to_f32(stage[p].qpost);  // absent cotangents read as zero
                 const float share = a.n_pow2 ? R * a.inv_n : R / a.n_f;
                 int cell[KPL];
                 float aold[KPL];
 #pragma unroll
                 for (int j = 0; j < KPL; ++j) {
-                    cell[j] = kl + j * L < K ? slot_cell<SLOT>(stage[p].c[j], stage[p].v[j]) : -2;
+                    cell[j] = active[j] ? slot_cell<SLOT>(stage[p].c[j], stage[p].v[j]) : -2;
                     aold[j] = lds_A[(cell[j] > 0 ? cell[j] : 0) * S + x];
                 }
+                const uint32_t to = uint32_t(uniform(t)) * kd;
 #pragma unroll
                 for (int j = 0; j < KPL; ++j) {
                     float c, bg;
-                    if (act) {
+                    if constexpr (ACT) {
                         c = fast_tanh(to_f32(stage[p].y[j]));
                         bg = fast_sigmoid(to_f32(stage[p].g[j]));
                     } else {
                         c = to_f32(stage[p].y[j]);
                         bg = to_f32(stage[p].g[j]);
                     }
-                    const float carried = aold[j] + (a.has_dsel ? to_f32(stage[p].ds[j]) : 0.0f);
+                    const bool ok = cell[j] >= 0;
+                    const float carried = aold[j] + to_f32(stage[p].ds[j]);
                     const float gg = carried + share;
-                    float dc = bg * gg;
-                    float db = (c - to_f32(stage[p].ho[j])) * gg;
-                    if (cell[j] >= 0) {
-                        lds_A[cell[j] * S + x] = (1.0f - bg) * carried - bg * share;
-                    } else {
-                        dc = 0.0f;
-                        db = 0.0f;
-                    }
-                    if (act) {
-                        dc = dc * (1.0f - c * c);  // tanh'
+                    float dc = ok ? bg * gg : 0.0f;
+                    float db = ok ? (c - to_f32(stage[p].ho[j])) * gg : 0.0f;
+                    lds_A[ok ? cell[j] * S + x : dummy] = (1.0f - bg) * carried - bg * share;
+                    if constexpr (ACT) {
+                        dc = dc * (1.0f - c * c);    // tanh'
                         db = db * (1.0f - bg) * bg;  // sigmoid'
                     }
-                    if (cell[j] != -2) {
-                        const uint32_t tk = uint32_t(uniform(t)) * kd32;
-                        store_f32(dyo + tk, ko[j], dc);
-                        store_f32(dgo + tk, ko[j], db);
+                    if (active[j]) {
+                        store_f32(dy_row + to, eo[j], dc);
+                        store_f32(dg_row + to, eo[j], db);
                     }
                 }
-                if (a.has_pre) R += to_f32(stage[p].qpre);
+                R += to_f32(stage[p].qpre);
                 if (uniform(stage[p].r)) {
                     // the boundary: nothing before it reaches past the reset
-                    for (int e = lane; e < N * S; e += kWave) lds_A[e] = 0.0f;
+                    for (int e0 = 0; e0 < N * S; e0 += kWave)
+                        if (e0 + lane < N * S) lds_A[e0 + lane] = 0.0f;
                     R = 0.0f;
                 }
             }
             load(stage[p], t - P);
         }
     }
-    if (a.dh0)
-        for (int n = kl; n < N; n += L) a.dh0[int64_t(b) * N * d + int64_t(n) * d + col] = lds_A[n * S + x];
+    if (a.dh0) {
+        float* dh0_row = a.dh0 + int64_t(b) * N * d;
+        for (int n0 = 0; n0 < N; n0 += L)
+            if (n0 + kl < N) dh0_row[int64_t(n0 + kl) * d + col] = lds_A[(n0 + kl) * S + x];
+    }
     if (a.dq0 && kl == 0) a.dq0[int64_t(b) * d + col] = R;
 }
 
@@ -614,13 +624,13 @@ hipError_t allow_lds(K kernel, size_t lds) {
 
 template <typename IN, typename OUT, typename SLOT, int S>
 hipError_t launch_fwd_s(const FwdArgs& a, int kpl, size_t lds, hipStream_t st) {
-    const int blocks = a.B * (a.d / S);
+    const dim3 blocks = sweep_grid(a.B, a.d / S);
 #define HSN_FWD_CASE(KP)                                                                          \
     case KP: {                                                                                    \
         auto k = fwd_sweep<IN, OUT, SLOT, S, KP>;                                                 \
         hipError_t e = allow_lds(k, lds);                                                         \
         if (e != hipSuccess) return e;                                                            \
-        hipLaunchKernelGGL(k, dim3(blocks), dim3(kWave), lds, st, a);                             \
+        hipLaunchKernelGGL(k, blocks, dim3(kWave), lds, st, a);                             \
         return hipGetLastError();                                                                 \
     }
     switch (kpl) {
@@ -644,15 +654,15 @@ hipError_t launch_fwd(const FwdArgs& a, SliceShape sh, size_t lds, hipStream_t s
     return hipErrorInvalidValue;
 }
 
-template <typename IN, typename SLOT>
+template <typename IN, typename SLOT, bool ACT>
 hipError_t launch_bwd(const BwdArgs& a, int kpl, size_t lds, hipStream_t st) {
-    const int blocks = a.B * (a.d / a.S);
+    const dim3 blocks = sweep_grid(a.B, a.d / a.S);
 #define HSN_BWD_CASE(KP)                                                                          \
     case KP: {                                                                                    \
-        auto k = bwd_sweep<IN, SLOT, KP>;                                                         \
+        auto k = bwd_sweep<IN, SLOT, ACT, KP>;                                                         \
         hipError_t e = allow_lds(k, lds);                                                         \
         if (e != hipSuccess) return e;                                                            \
-        hipLaunchKernelGGL(k, dim3(blocks), dim3(kWave), lds, st, a);                             \
+        hipLaunchKernelGGL(k, blocks, dim3(kWave), lds, st, a);                             \
         return hipGetLastError();                                                                 \
     }
     switch (kpl) {

@@ -45,10 +45,7 @@ void fill_common(BwdArgs& a, const void* y, const void* g, const void* h_old, co
                  const float* d_h_T, const float* d_q_T, void* dy, void* dg, float* d_h0,
                  float* d_q0, int B, int T, int N, int d, int K, int S) {
     a.y = y, a.g = g, a.h_old = h_old, a.y_row = int64_t(T) * K * d;
-    // absent cotangents read a valid dummy (y, at least as large) and are masked at use
-    a.dsel = d_h_sel ? d_h_sel : y, a.has_dsel = d_h_sel ? 1 : 0;
-    a.dq_pre = d_q_pre ? d_q_pre : y, a.has_pre = d_q_pre ? 1 : 0;
-    a.dq_post = d_q_post ? d_q_post : y, a.has_post = d_q_post ? 1 : 0;
+    a.dsel = d_h_sel, a.dq_pre = d_q_pre, a.dq_post = d_q_post;  // absent: read as zero
     a.q_row = int64_t(T) * d;
     a.reset = reset, a.r_row = T, a.s_row = int64_t(T) * K;
     a.dh_T = d_h_T, a.dq_T = d_q_T, a.dy = dy, a.dg = dg, a.dh0 = d_h0, a.dq0 = d_q0;
@@ -79,9 +76,9 @@ extern "C" int hsn_win_backward(const void* y, const void* gate_pre, const void*
                 HSN_ERR_SIZE_OVERFLOW,
                 "hsn_win_backward: a tensor is too large");
     SliceShape sh;
-    HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, 0, sh), HSN_ERR_INVALID_ARGUMENT,
+    HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, 4, sh), HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_backward: the cotangent slice does not fit the LDS (N too large)");
-    const size_t lds = size_t(N) * 4 * sh.S;
+    const size_t lds = size_t(N) * 4 * sh.S + 4;  // one dummy word
     hipStream_t st = as_stream(stream);
     const int64_t nslots = int64_t(B) * T * K;
     const size_t elem = io_dtype == HSN_DTYPE_F32 ? 4 : 2;
@@ -104,11 +101,11 @@ extern "C" int hsn_win_backward(const void* y, const void* gate_pre, const void*
     BwdArgs a{};
     fill_common(a, pre, gate_pre, h_old, d_h_sel, d_q_pre, d_q_post, reset, d_h_T, d_q_T, dy,
                 dgate, d_h0, d_q0, B, T, N, d, K, sh.S);
-    a.cells = slots, a.valid = nullptr, a.act = 1;
+    a.cells = slots, a.valid = nullptr;
     if (io_dtype == HSN_DTYPE_F32)
-        HSN_HIP((launch_bwd<float, Packed32>(a, sh.kpl, lds, st)));
+        HSN_HIP((launch_bwd<float, Packed32, true>(a, sh.kpl, lds, st)));
     else
-        HSN_HIP((launch_bwd<bf16_t, Packed32>(a, sh.kpl, lds, st)));
+        HSN_HIP((launch_bwd<bf16_t, Packed32, true>(a, sh.kpl, lds, st)));
     if (cand_norm) {  // the norm's VJP: dy holds dL/dpre
         const int blocks = static_cast<int>((nslots + 3) / 4);
         if (io_dtype == HSN_DTYPE_F32) {
@@ -149,14 +146,14 @@ extern "C" int hsn_win_recurrence(const float* c, const float* b, const float* h
                 HSN_ERR_SIZE_OVERFLOW,
                 "hsn_win_recurrence: a tensor is too large");
     SliceShape sh;
-    HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, 0, sh), HSN_ERR_INVALID_ARGUMENT,
+    HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, 4, sh), HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_recurrence: the cotangent slice does not fit the LDS (N too large)");
-    const size_t lds = size_t(N) * 4 * sh.S;
+    const size_t lds = size_t(N) * 4 * sh.S + 4;  // one dummy word
     BwdArgs a{};
     fill_common(a, c, b, h_old, d_h_sel, d_q_pre, d_q_post, reset, d_h_T, d_q_T, dc, db, d_h0,
                 d_q0, B, T, N, d, K, sh.S);
-    a.cells = cells, a.valid = valid, a.act = 0;
-    HSN_HIP((launch_bwd<float, Cells64>(a, sh.kpl, lds, as_stream(stream))));
+    a.cells = cells, a.valid = valid;
+    HSN_HIP((launch_bwd<float, Cells64, false>(a, sh.kpl, lds, as_stream(stream))));
     HSN_ABI_END
 }
 

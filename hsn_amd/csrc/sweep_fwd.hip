@@ -51,7 +51,7 @@ extern "C" int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype
                 HSN_ERR_SIZE_OVERFLOW,
                 "hsn_win_forward: a tensor is too large");
     SliceShape sh;
-    const int64_t fixed = int64_t(N) * 4;  // the ages' last-selection table
+    const int64_t fixed = int64_t(N) * 4 + 8;  // the ages' last-selection table, two dummies
     HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, fixed, sh), HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_forward: the state slice does not fit the LDS (N too large)");
     const size_t lds = size_t(N) * 4 * sh.S + size_t(fixed);
@@ -104,7 +104,7 @@ extern "C" int hsn_win_cell_update(const void* y, const void* gate, int io_dtype
     HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
                 HSN_ERR_UNSUPPORTED_DTYPE, "hsn_win_cell_update: io_dtype must be f32 or bf16");
     SliceShape sh;
-    const int64_t fixed = int64_t(N) * 4;
+    const int64_t fixed = int64_t(N) * 4 + 8;
     HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, fixed, sh), HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_cell_update: the state slice does not fit the LDS (N too large)");
     const size_t lds = size_t(N) * 4 * sh.S + size_t(fixed);
