@@ -1,24 +1,38 @@
-// The window's forward sweep and backward recurrence on gfx950, with the state resident in LDS.
+// The window's forward sweep and backward recurrence on gfx950, time-chunked, with the state
+// resident in LDS.
 //
-// Both directions are separable over the state's d columns: the gated update
+// Columns. Both directions are separable over the state's d columns: the gated update
 // h'[n,x] = (1-b) h[n,x] + b c touches column x only, the summary q[x] sums column x over the
-// slots, and the reverse recurrence (A[n,x], R[x]) likewise (reference
-// python/hsn/kernels/native.py:292-302, python/hsn/train/split.py:154-173). So one 64-lane
-// wavefront owns (row b, a slice of S columns) for the whole window and keeps that slice of the
-// state -- h[N][S] forward, the cotangent A[N][S] backward -- in LDS from the first position to
-// the last: HBM is read for the inputs, the decisions and the start state once, and written for
-// the per-slot outputs and the end state once.
+// cells, and the reverse recurrence (A[n,x], R[x]) likewise (reference
+// python/hsn/kernels/native.py:292-302, python/hsn/train/split.py:154-173). A workgroup owns
+// (row b, a slice of S columns) and keeps that slice of the state in LDS.
 //
-// Lanes are (column, slot lane) with the slot fastest: lane = x*L + kl, L = 64/S, slot
-// k = kl + j*L (j < KPL). A column's L slot lanes are consecutive, so the per-column sums and
-// maxima reduce with DPP inside a row. Valid slots of one position name distinct cells, so no
-// two lanes write one LDS word, and every LDS read of a position is issued before its writes (a
+// Time. One wavefront walking all T positions of a row leaves most of the chip idle at small
+// batch (B*d/S wavefronts), so the workgroup splits the window into W chunks of Tc positions,
+// one wavefront each. For a fixed chunk, each cell's state maps affinely from the chunk's start
+// to its end: forward h_end = alpha h_start + beta, backward A_before = mu A_after + nu (the
+// product of the (1-b) factors of the cell's updates, and the run from zero; a reset zeroes
+// both). The kernel runs
+//   phase A  every wavefront composes its chunk's per-cell maps in LDS (independent of the
+//            start state, so all chunks run at once),
+//   phase B  the workgroup walks the W maps per (cell, column) to every chunk's exact start
+//            state (W steps per element, all elements in parallel),
+//   phase C  every wavefront replays its chunk from its start state with the real outputs.
+// The summary q needs no map: q - sum_n h[n]/N is constant between resets (q starts at q0,
+// every update adds its delta / N, a reset zeroes both), so a chunk's start q follows from the
+// column sums of its start state. The backward's R depends on the cotangents only, so a
+// chunk-sum pre-pass gives every chunk its start R. W = 1 is the plain sequential sweep.
+//
+// Lanes. Lane = k*S + x: slot k of the position, column x of the slice (columns fastest), one
+// slot per lane (S*K <= 64). A slot's S columns are an aligned group of lanes, so the max over
+// a cell's columns reduces with DPP. Valid slots of one position name distinct cells, so no two
+// lanes write one LDS word, and every LDS read of a position is issued before its writes (a
 // padded slot reads cell 0 before the update, as the reference's gather does).
 //
-// Latency: the only sequential chain is LDS read -> FMA -> LDS write per position. The inputs of
-// the next P positions stay in flight in a rolling register buffer: every load is unconditional
-// (indices clamped into the window, optional inputs aimed at a valid dummy and masked at use), so
-// the compiler's wait counts stay exact and a position waits only for its own loads.
+// Registers. A sub-block of TB positions of a chunk is loaded at once (every load unconditional,
+// clamped into the chunk, so the compiler's wait counts are exact and the loads of all TB
+// positions are in flight together) and its activations are kept in registers for the phases;
+// a chunk longer than TB reloads its sub-blocks in phase C.
 #pragma once
 
 #include "common.cuh"
@@ -29,20 +43,14 @@ namespace hsn {
 
 // The decisions of a slot as the sweeps read them: `Packed32` is one int32 per slot, the cell
 // where the slot is valid and -1 where it is padded (hsn_win_route's `slots`); `Cells64` is the
-// reference's pair of arrays, int64 cells and uint8 valid flags.
+// reference's pair of arrays, int64 cells and uint8 valid flags (the low word of a cell in
+// [0, N) is the cell).
 struct Packed32 {
     using Raw = int32_t;
 };
 struct Cells64 {
     using Raw = int64_t;
 };
-
-// Decode a slot: the cell where valid, -1 where padded.
-template <typename SLOT>
-__device__ __forceinline__ int slot_cell(typename SLOT::Raw c, uint8_t v) {
-    if constexpr (sizeof(typename SLOT::Raw) == 4) return static_cast<int>(c);
-    else return v ? static_cast<int>(c) : -1;
-}
 
 // (row, slice) of a workgroup, from a grid (G, nslices, B/G), G = 8 when B is a multiple of 8
 // (else 1). Workgroups are dealt to the 8 XCDs round-robin by linear id, so blockIdx.x is the
@@ -59,16 +67,33 @@ inline dim3 sweep_grid(int B, int nslices) {
     return dim3(g, nslices, B / g);
 }
 
-constexpr int fwd_depth(int kpl) { return kpl >= 8 ? 2 : 8 / kpl; }
-constexpr int bwd_depth(int kpl) { return kpl >= 4 ? 2 : (kpl == 2 ? 3 : 6); }
+constexpr int kMaxChunks = 8;  // wavefronts (chunks) per workgroup
 
-// Select element `i` (a lane-dependent index) of a register array without indexing memory.
-template <int P, typename T>
-__device__ __forceinline__ T pick(const T (&v)[P], int i) {
-    T r = v[0];
+// v / N as the reference divides (an exact reciprocal product when N is a power of two)
+struct DivN {
+    int pow2;
+    float inv, n;
+    __device__ __forceinline__ float operator()(float v) const { return pow2 ? v * inv : v / n; }
+    __device__ __forceinline__ double operator()(double v) const {
+        return pow2 ? v * double(inv) : v / double(n);
+    }
+};
+
+// Sum over the lanes with equal lane % S (a column's slot lanes).
+template <int S>
+__device__ __forceinline__ float col_sum(float v) {
 #pragma unroll
-    for (int p = 1; p < P; ++p) r = i == p ? v[p] : r;
-    return r;
+    for (int m = S; m < kWave; m <<= 1) {
+        if (m == 8) v += dpp_f32<dpp::kRor8>(v);  // xor 8 inside a 16-lane row
+        else v += __shfl_xor(v, m, kWave);
+    }
+    return v;
+}
+
+// Zero `count` words of LDS from `p` with the wavefront (a uniform trip count).
+__device__ __forceinline__ void lds_zero(float* p, int count, int lane) {
+    for (int e0 = 0; e0 < count; e0 += kWave)
+        if (e0 + lane < count) p[e0 + lane] = 0.0f;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -108,205 +133,303 @@ struct FwdArgs {
     int64_t* age_T;
     int64_t aT_row;
     int64_t* pos_T;
-    int B, T, N, d, K, xcd_rows, n_pow2;
-    float inv_n, n_f;
+    int B, T, N, d, K;
+    int W, Tc;   // chunks per row and positions per chunk
+    int region;  // LDS words per wavefront
+    DivN divn;
 };
 
-template <typename IN, typename SLOT, int KPL>
-struct FwdStage {
-    IN y[KPL];
-    IN g[KPL];
-    typename SLOT::Raw c[KPL];
-    uint8_t v[KPL];
-    uint8_t r;  // the position's reset flag (the same in every lane)
-};
+// LDS words of the forward: per wavefront the state slice h [N*S] (alpha in phase A) and a
+// second array (beta in phase A, the cells' max |h| in phase C), each with a dummy word; then
+// the ages' last-selection table [N+1], the column-sum partials [W][W][S] and two flags per chunk.
+inline int fwd_region(int N, int S, int W) {
+    const int ns = N * S + 1;
+    return W > 1 ? 2 * ns : ns + N + 1;
+}
+inline size_t fwd_lds_bytes(int N, int S, int W) {
+    return 4 * (size_t(W) * fwd_region(N, S, W) + (N + 1) + size_t(W) * W * S + 2 * W);
+}
 
-template <typename IN, typename OUT, typename SLOT, int S, int KPL>
-__global__ __launch_bounds__(64) void fwd_sweep(FwdArgs a) {
+template <typename IN, typename OUT, typename SLOT, int S, int TB>
+__global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     using Raw = typename SLOT::Raw;
+    constexpr bool kWide = sizeof(Raw) == 8;
     extern __shared__ float lds[];
-    constexpr int L = kWave / S;
-    constexpr int P = fwd_depth(KPL);
     const int lane = lane_id();
-    const int x = lane / L, kl = lane % L;
+    const int gl = threadIdx.x;
+    const int w = uniform(gl / kWave);
+    const int W = a.W;
+    const int kslot = lane / S, x = lane % S;
     int b, slice;
     block_coords(b, slice);
     const int col = slice * S + x;
     const int N = a.N, d = a.d, K = a.K, T = a.T;
-    float* lds_h = lds;                                  // [N*S], then one dummy word
-    int* lds_last = reinterpret_cast<int*>(lds + N * S + 1);  // [N], then one dummy word
-    const int dummy_h = N * S;
+    const int NS = N * S;
+    const bool active = kslot < K;
+    float* st = lds + w * a.region;  // alpha, then h: [NS] + a dummy word
+    float* st2 = st + NS + 1;        // beta, then the cells' max |h| over the slice (as bits)
+    uint32_t* cm = reinterpret_cast<uint32_t*>(st2);
+    float* shared = lds + W * a.region;
+    int* last = reinterpret_cast<int*>(shared);  // [N] + a dummy
+    float* part = shared + N + 1;                // [W waves][W chunks][S]
+    int* rflag = reinterpret_cast<int*>(part + W * W * S);
+    int* rlast = rflag + W;
+    const int t_begin = w * a.Tc;
+    const int t_end = min(T, t_begin + a.Tc);
+    const int nsb = (t_end - t_begin + TB - 1) / TB;
     const bool track_age = slice == 0 && a.age_T != nullptr;
     const bool want_max = a.h_max != nullptr;
-    const bool has_reset = a.reset != nullptr;
+    const DivN divn = a.divn;
 
-    // the row's tensors as buffer resources: per position a uniform soffset, per lane a voffset
     const uint32_t kd = uint32_t(K) * d;
-    const rsrc_t ry = make_rsrc(static_cast<const IN*>(a.y) + b * a.y_row, T * kd * sizeof(IN));
-    const rsrc_t rg = make_rsrc(static_cast<const IN*>(a.g) + b * a.y_row, T * kd * sizeof(IN));
+    const uint32_t row_elems = uint32_t(T) * kd;
+    const rsrc_t ry = make_rsrc(static_cast<const IN*>(a.y) + b * a.y_row, row_elems * sizeof(IN));
+    const rsrc_t rg = make_rsrc(static_cast<const IN*>(a.g) + b * a.y_row, row_elems * sizeof(IN));
     const rsrc_t rc = make_rsrc(static_cast<const Raw*>(a.cells) + b * a.s_row, T * K * sizeof(Raw));
     const rsrc_t rv = make_rsrc(a.valid ? a.valid + b * a.s_row : nullptr, a.valid ? T * K : 0);
-    const rsrc_t rr = make_rsrc(has_reset ? a.reset + b * a.r_row : nullptr, has_reset ? T : 0);
-    // outputs: uniform row pointers, a per-position uniform offset, per-lane element offsets
-    OUT* const ho_row = a.h_old ? static_cast<OUT*>(a.h_old) + b * a.o_row : nullptr;
-    OUT* const hs_row = a.h_sel ? static_cast<OUT*>(a.h_sel) + b * a.o_row : nullptr;
-    OUT* const qa_row = a.q_pre ? static_cast<OUT*>(a.q_pre) + b * a.qo_row : nullptr;
-    OUT* const qb_row = a.q_post ? static_cast<OUT*>(a.q_post) + b * a.qo_row : nullptr;
-    bool active[KPL];
-    uint32_t vy[KPL], vc[KPL], vv[KPL], eo[KPL];
-#pragma unroll
-    for (int j = 0; j < KPL; ++j) {
-        const int k = kl + j * L;
-        active[j] = k < K;
-        vy[j] = active[j] ? uint32_t(k * d + col) * sizeof(IN) : kOob;
-        eo[j] = uint32_t((active[j] ? k : 0) * d + col);
-        vc[j] = active[j] ? uint32_t(k) * sizeof(Raw) : kOob;
-        vv[j] = active[j] ? uint32_t(k) : kOob;
-    }
+    const rsrc_t rr = make_rsrc(a.reset ? a.reset + b * a.r_row : nullptr, a.reset ? T : 0);
+    // outputs: an absent one is a resource of size 0 (its stores are dropped)
+    const rsrc_t rho = make_rsrc(a.h_old ? static_cast<OUT*>(a.h_old) + b * a.o_row : nullptr,
+                                 a.h_old ? row_elems * sizeof(OUT) : 0);
+    const rsrc_t rhs = make_rsrc(a.h_sel ? static_cast<OUT*>(a.h_sel) + b * a.o_row : nullptr,
+                                 a.h_sel ? row_elems * sizeof(OUT) : 0);
+    const uint32_t qbytes = uint32_t(T) * d * sizeof(OUT);
+    const rsrc_t rqa = make_rsrc(a.q_pre ? static_cast<OUT*>(a.q_pre) + b * a.qo_row : nullptr,
+                                 a.q_pre ? qbytes : 0);
+    const rsrc_t rqb = make_rsrc(a.q_post ? static_cast<OUT*>(a.q_post) + b * a.qo_row : nullptr,
+                                 a.q_post ? qbytes : 0);
+    const uint32_t vy = active ? uint32_t(kslot * d + col) * sizeof(IN) : kOob;
+    const uint32_t vo = active ? uint32_t(kslot * d + col) * sizeof(OUT) : kOob;
+    const uint32_t vc = active ? uint32_t(kslot) * sizeof(Raw) : kOob;
+    const uint32_t vv = active ? uint32_t(kslot) : kOob;
+    const uint32_t vq = kslot == 0 ? uint32_t(col) * sizeof(OUT) : kOob;  // one lane per column
 
-    // the start state of this slice and the column maxima of |h|
-    // (every loop below runs a uniform trip count with a per-lane guard: a divergent loop exit
-    // would make the values defined in it divergent, row pointers included)
-    uint32_t colmax = 0u;
-    const float* h0_row = a.h0 + b * a.h0_row;
-    for (int n0 = 0; n0 < N; n0 += L) {
-        const int n = n0 + kl;
-        if (n < N) {
-            const float v = h0_row[int64_t(n) * d + col];
-            lds_h[n * S + x] = v;
-            colmax = umax(colmax, abs_bits(v));
-        }
-    }
-    colmax = group_max<L>(colmax);
     if (track_age)
-        for (int n0 = 0; n0 < N; n0 += kWave)
-            if (n0 + lane < N) lds_last[n0 + lane] = -1;
-    float q = a.q0[b * a.q0_row + col];
-    int last_reset = -1;
+        for (int n0 = 0; n0 <= N; n0 += kWave * W)
+            if (n0 + gl <= N) last[n0 + gl] = -1;
 
-    auto load = [&](FwdStage<IN, SLOT, KPL>& st, int t) {
-        t = uniform(t < T ? t : T - 1);
-        const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
-        const uint32_t sc = uint32_t(t) * K;
+    // the sub-block in registers: (1 - b), b*c and the decoded cell of every position
+    float omb[TB], bcv[TB];
+    int cl[TB];
+    uint32_t rmask = 0u;
+    auto fetch = [&](int tb0) {
+        const int tl = t_end - 1;
+        IN yv[TB], gv[TB];
+        int32_t cv[TB];
+        uint8_t vb[TB];
 #pragma unroll
-        for (int j = 0; j < KPL; ++j) {
-            st.y[j] = bload<IN>(ry, vy[j], sy);
-            st.g[j] = bload<IN>(rg, vy[j], sy);
-            st.c[j] = bload<Raw>(rc, vc[j], sc * sizeof(Raw));
-            if constexpr (sizeof(Raw) == 8) st.v[j] = bload<uint8_t>(rv, vv[j], sc);
-            else st.v[j] = 1;
+        for (int i = 0; i < TB; ++i) {
+            const int t = uniform(min(tb0 + i, tl));
+            const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
+            yv[i] = bload<IN>(ry, vy, sy);
+            gv[i] = bload<IN>(rg, vy, sy);
+            cv[i] = bload<int32_t>(rc, vc, uint32_t(t) * K * sizeof(Raw));
+            if constexpr (kWide) vb[i] = bload<uint8_t>(rv, vv, uint32_t(t) * K);
         }
-        st.r = bload<uint8_t>(rr, 0u, uint32_t(t));
+        const bool rin = lane < TB && tb0 + lane < t_end;
+        const uint8_t r = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
+        rmask = static_cast<uint32_t>(ballot(r != 0));
+#pragma unroll
+        for (int i = 0; i < TB; ++i) {
+            const float bg = fast_sigmoid(to_f32(gv[i]));
+            omb[i] = 1.0f - bg;
+            bcv[i] = bg * fast_tanh(to_f32(yv[i]));
+            int c = cv[i];
+            if constexpr (kWide) c = vb[i] ? c : -1;
+            cl[i] = active ? c : -2;
+        }
     };
 
-    // the prologue keeps its loads in stage order (the scheduler would otherwise reorder
-    // them, and the loop's first waits would then have to drain the whole pipeline)
-    FwdStage<IN, SLOT, KPL> stage[P];
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        load(stage[p], p);
-        __builtin_amdgcn_sched_barrier(0);
-    }
+    float q_run = a.q0[b * a.q0_row + col];
+    const float* h0_row = a.h0 + b * a.h0_row;
 
-    for (int t0 = 0; t0 < T; t0 += P) {
-        uint32_t hm_b[P];  // the row max |h| of each position of the block (uniform)
+    if (W > 1) {
+        // phase A: the chunk's per-cell maps, alpha (st) and beta (st2), from the identity
+        for (int e0 = 0; e0 < NS; e0 += kWave) {
+            const int e = e0 + lane;
+            if (e < NS) {
+                st[e] = 1.0f;
+                st2[e] = 0.0f;
+            }
+        }
+        bool any_reset = false;
+        for (int sb = 0; sb < nsb; ++sb) {
+            const int tb0 = t_begin + sb * TB;
+            const int n = min(TB, t_end - tb0);
+            fetch(tb0);
 #pragma unroll
-        for (int p = 0; p < P; ++p) {
-            const int t = t0 + p;
-            hm_b[p] = 0u;
-            if (t < T) {
-                if (has_reset && uniform(stage[p].r)) {
-                    // a document boundary: h, q (and the ages) restart at zero before t reads them
-                    for (int e0 = 0; e0 < N * S; e0 += kWave)
-                        if (e0 + lane < N * S) lds_h[e0 + lane] = 0.0f;
-                    colmax = 0u;
-                    q = 0.0f;
-                    last_reset = t;
-                }
-                const uint32_t tq = uint32_t(uniform(t)) * d;
-                if (qa_row && kl == 0) store_f32(qa_row + tq, col, q);
-                int cell[KPL];
-                float hold[KPL];
-#pragma unroll
-                for (int j = 0; j < KPL; ++j) {
-                    cell[j] = active[j] ? slot_cell<SLOT>(stage[p].c[j], stage[p].v[j]) : -2;
-                    hold[j] = lds_h[(cell[j] > 0 ? cell[j] : 0) * S + x];
-                }
-                float delta = 0.0f;
-                bool padded = false, drop = false;
-                uint32_t up = 0u;
-                float hnew[KPL];
-#pragma unroll
-                for (int j = 0; j < KPL; ++j) {
-                    const float c = fast_tanh(to_f32(stage[p].y[j]));
-                    const float bg = fast_sigmoid(to_f32(stage[p].g[j]));
-                    hnew[j] = (1.0f - bg) * hold[j] + bg * c;
-                    const bool ok = cell[j] >= 0;
-                    lds_h[ok ? cell[j] * S + x : dummy_h] = hnew[j];
-                    delta += ok ? hnew[j] - hold[j] : 0.0f;
-                    const uint32_t ob = abs_bits(hold[j]), nb = abs_bits(hnew[j]);
-                    drop |= ok && ob == colmax && nb < ob;
-                    up = umax(up, ok ? nb : 0u);
-                    padded |= cell[j] == -1;
-                }
-                float cell0 = 0.0f;
-                if (ballot(padded)) cell0 = lds_h[x];  // a padded slot shows cell 0 after the update
-                const uint32_t to = uint32_t(uniform(t)) * kd;
-#pragma unroll
-                for (int j = 0; j < KPL; ++j) {
-                    if (active[j]) {
-                        if (ho_row) store_f32(ho_row + to, eo[j], hold[j]);
-                        if (hs_row) store_f32(hs_row + to, eo[j], cell[j] >= 0 ? hnew[j] : cell0);
+            for (int i = 0; i < TB; ++i) {
+                if (i < n) {
+                    if ((rmask >> i) & 1u) {  // the state restarts from zero before t
+                        lds_zero(st, NS, lane);
+                        lds_zero(st2, NS, lane);
+                        any_reset = true;
                     }
-                }
-                // q' = q + sum_k (h' - h)[k] / N over the column's slot lanes
-                delta = group_sum<L>(delta);
-                q = q + (a.n_pow2 ? delta * a.inv_n : delta / a.n_f);
-                if (qb_row && kl == 0) store_f32(qb_row + tq, col, q);
-                if (want_max) {
-                    // the column's max |h|: raised by the new values, rescanned only when a cell
-                    // that held it shrank; the row's is the max over the slice's columns
-                    colmax = umax(colmax, group_max<L>(up));
-                    if (ballot(drop)) {
-                        uint32_t m = 0u;
-                        for (int n0 = 0; n0 < N; n0 += L)
-                            if (n0 + kl < N) m = umax(m, abs_bits(lds_h[(n0 + kl) * S + x]));
-                        colmax = group_max<L>(m);
-                    }
-                    hm_b[p] = wave_max_from_groups<L>(colmax);
-                }
-                if (track_age) {
-#pragma unroll
-                    for (int j = 0; j < KPL; ++j)
-                        lds_last[(cell[j] >= 0 && x == 0) ? cell[j] : N] = t;
+                    const int ci = cl[i];
+                    const int ri = (ci > 0 ? ci : 0) * S + x;
+                    const float al = st[ri], be = st2[ri];
+                    const int wi = ci >= 0 ? ci * S + x : NS;
+                    st[wi] = omb[i] * al;
+                    st2[wi] = omb[i] * be + bcv[i];
                 }
             }
-            load(stage[p], t + P);
         }
-        if (want_max) {  // lane p sends position t0 + p's row max
-            uint32_t m = 0u;
+        if (lane == 0) rflag[w] = any_reset ? 1 : 0;
+        __syncthreads();
+
+        // phase B: every chunk's start state (into its alpha's place), and its column sums
+        float ps[kMaxChunks];
 #pragma unroll
-            for (int p = 0; p < P; ++p) m = lane == p ? hm_b[p] : m;
-            if (lane < P && t0 + lane < T)
-                atomicMax(reinterpret_cast<unsigned int*>(a.h_max + b * a.hm_row) + (t0 + lane), m);
+        for (int j = 0; j < kMaxChunks; ++j) ps[j] = 0.0f;
+        for (int e0 = 0; e0 < NS; e0 += kWave * W) {
+            const int e = e0 + gl;
+            if (e < NS) {
+                float h = h0_row[int64_t(e / S) * d + slice * S + e % S];
+#pragma unroll
+                for (int j = 0; j < kMaxChunks; ++j) {
+                    if (j < W) {
+                        float* sj = lds + j * a.region;
+                        const float al = sj[e], be = sj[NS + 1 + e];
+                        sj[e] = h;
+                        ps[j] += h;
+                        h = al * h + be;
+                    }
+                }
+            }
         }
+#pragma unroll
+        for (int j = 0; j < kMaxChunks; ++j) {
+            if (j < W) {
+                const float v = col_sum<S>(ps[j]);  // lanes with equal lane % S hold column x
+                if (lane < S) part[(w * W + j) * S + lane] = v;
+            }
+        }
+        __syncthreads();
+        if (w > 0) {
+            float cs_w = 0.0f, cs_0 = 0.0f;
+            for (int wp = 0; wp < W; ++wp) {
+                cs_w += part[(wp * W + w) * S + x];
+                cs_0 += part[(wp * W) * S + x];
+            }
+            bool reset_before = false;
+            for (int j = 0; j < w; ++j) reset_before |= rflag[j] != 0;
+            // q - sum_n h[n] / N is constant between resets, zero after one
+            q_run = (reset_before ? 0.0f : q_run - divn(cs_0)) + divn(cs_w);
+        }
+    } else {
+        for (int e0 = 0; e0 < NS; e0 += kWave) {
+            const int e = e0 + lane;
+            if (e < NS) st[e] = h0_row[int64_t(e / S) * d + slice * S + e % S];
+        }
+    }
+
+    // phase C: the replay with the outputs
+    uint32_t M = 0u;  // the slice's max |h| (bits), the max over cm
+    if (want_max) {
+        for (int n0 = 0; n0 < N; n0 += kWave) {
+            const int n = n0 + lane;
+            if (n < N) {
+                uint32_t m = 0u;
+#pragma unroll
+                for (int xx = 0; xx < S; ++xx) m = umax(m, abs_bits(st[n * S + xx]));
+                cm[n] = m;
+                M = umax(M, m);
+            }
+        }
+        M = wave_max_from_groups<1>(M);
+    }
+    int lr = -1;  // the chunk's last reset
+    for (int sb = 0; sb < nsb; ++sb) {
+        const int tb0 = t_begin + sb * TB;
+        const int n = min(TB, t_end - tb0);
+        if (W == 1 || nsb > 1) fetch(tb0);
+        float delta[TB];
+        uint32_t hmv = 0u;
+#pragma unroll
+        for (int i = 0; i < TB; ++i) {
+            delta[i] = 0.0f;
+            if (i < n) {
+                const int t = tb0 + i;
+                if ((rmask >> i) & 1u) {  // a document boundary: h, q (and the ages) restart at zero
+                    lds_zero(st, NS, lane);
+                    if (want_max) {
+                        lds_zero(st2, N, lane);
+                        M = 0u;
+                    }
+                    lr = t;
+                }
+                const int ci = cl[i];
+                const bool ok = ci >= 0;
+                const float hold = st[(ci > 0 ? ci : 0) * S + x];
+                const uint32_t mo = (want_max && ok) ? cm[ci] : 0u;
+                const float hnew = omb[i] * hold + bcv[i];
+                st[ok ? ci * S + x : NS] = hnew;
+                const uint32_t so = uint32_t(t) * kd * sizeof(OUT);
+                bstore_f32<OUT>(hold, rho, vo, so);
+                float hs = hnew;
+                if (ballot(ci == -1)) {  // a padded slot shows cell 0 after the update
+                    const float c0 = st[x];
+                    hs = ci == -1 ? c0 : hnew;
+                }
+                bstore_f32<OUT>(hs, rhs, vo, so);
+                delta[i] = ok ? hnew - hold : 0.0f;
+                if (want_max) {
+                    // the cell's max over the slice's columns replaces its old one; the slice max
+                    // rises with it, and is rescanned only when the cell that held it shrank
+                    const uint32_t mn = group_max<S>(abs_bits(hnew));
+                    if (ok && x == 0) cm[ci] = mn;
+                    const bool drop = ok && mo == M && mn < M;
+                    M = umax(M, wave_max_from_groups<S>(ok ? mn : 0u));
+                    if (ballot(drop)) {
+                        uint32_t m = 0u;
+                        for (int n0 = 0; n0 < N; n0 += kWave)
+                            if (n0 + lane < N) m = umax(m, cm[n0 + lane]);
+                        M = wave_max_from_groups<1>(m);
+                    }
+                    hmv = lane == i ? M : hmv;
+                }
+                if (track_age && ok && x == 0) atomicMax(&last[ci], t);
+            }
+        }
+        // the summary before and after each position: q' = q + sum_k (h' - h)[k] / N
+#pragma unroll
+        for (int i = 0; i < TB; ++i) {
+            const float s = col_sum<S>(delta[i]);
+            if (i < n) {
+                if ((rmask >> i) & 1u) q_run = 0.0f;
+                const uint32_t sq = uint32_t(tb0 + i) * d * sizeof(OUT);
+                bstore_f32<OUT>(q_run, rqa, vq, sq);
+                q_run = q_run + divn(s);
+                bstore_f32<OUT>(q_run, rqb, vq, sq);
+            }
+        }
+        if (want_max && lane < n)  // lane i sends position tb0 + i's slice max
+            atomicMax(reinterpret_cast<unsigned int*>(a.h_max + b * a.hm_row) + (tb0 + lane), hmv);
     }
 
     // the end state (zeroed when the caller's next record resets this row)
     const bool clear = a.clear ? a.clear[b * a.c_row] != 0 : false;
-    if (a.h_T) {
-        float* hT_row = a.h_T + b * a.hT_row;
-        for (int n0 = 0; n0 < N; n0 += L)
-            if (n0 + kl < N) hT_row[int64_t(n0 + kl) * d + col] = clear ? 0.0f : lds_h[(n0 + kl) * S + x];
+    if (w == W - 1) {
+        if (a.h_T) {
+            float* hT_row = a.h_T + b * a.hT_row;
+            for (int e0 = 0; e0 < NS; e0 += kWave) {
+                const int e = e0 + lane;
+                if (e < NS) hT_row[int64_t(e / S) * d + slice * S + e % S] = clear ? 0.0f : st[e];
+            }
+        }
+        if (a.q_T && kslot == 0) a.q_T[b * a.qT_row + col] = clear ? 0.0f : q_run;
     }
-    if (a.q_T && kl == 0) a.q_T[b * a.qT_row + col] = clear ? 0.0f : q;
     if (track_age) {
+        if (lane == 0) rlast[w] = lr;
+        __syncthreads();
+        int last_reset = -1;
+        for (int j = 0; j < W; ++j) last_reset = max(last_reset, rlast[j]);
         const int64_t* age0_row = a.age0 + b * a.a0_row;
         int64_t* ageT_row = a.age_T + b * a.aT_row;
-        for (int n0 = 0; n0 < N; n0 += kWave) {
-            const int n = n0 + lane;
+        for (int n0 = 0; n0 < N; n0 += kWave * W) {
+            const int n = n0 + gl;
             if (n < N) {
-                const int ls = lds_last[n];
+                const int ls = last[n];
                 int64_t age;
                 if (ls >= 0 && ls >= last_reset) age = (T - 1) - ls;
                 else if (last_reset >= 0) age = T - last_reset;
@@ -314,7 +437,7 @@ __global__ __launch_bounds__(64) void fwd_sweep(FwdArgs a) {
                 ageT_row[n] = clear ? 0 : age;
             }
         }
-        if (a.pos_T && lane == 0)
+        if (a.pos_T && gl == 0)
             a.pos_T[b] = last_reset >= 0 ? int64_t(T - last_reset) : a.pos0[b] + T;
     }
 }
@@ -343,159 +466,276 @@ struct BwdArgs {
     void* dg;
     float* dh0;
     float* dq0;
-    int B, T, N, d, K, S, xcd_rows, n_pow2;
-    float inv_n, n_f;
+    int B, T, N, d, K;
+    int W, Tc, region;
+    DivN divn;
 };
 
-template <typename IN, typename SLOT, int KPL>
-struct BwdStage {
-    IN y[KPL];
-    IN g[KPL];
-    IN ho[KPL];
-    IN ds[KPL];
-    typename SLOT::Raw c[KPL];
-    uint8_t v[KPL];
-    IN qpre;
-    IN qpost;
-    uint8_t r;
-};
+// LDS words of the backward: per wavefront the cotangent slice A [N*S] (mu in phase A) and, when
+// chunked, nu [N*S], each with a dummy word; then the chunks' summary-cotangent sums [W][S]
+// (fp64) and reset flags [W].
+inline int bwd_region(int N, int S, int W) {
+    const int ns = N * S + 1;
+    return W > 1 ? 2 * ns : ns;
+}
+inline size_t bwd_lds_bytes(int N, int S, int W) {
+    return 4 * (size_t(W) * bwd_region(N, S, W) + 2 * size_t(W) * S + W);
+}
 
-template <typename IN, typename SLOT, bool ACT, int KPL>
-__global__ __launch_bounds__(64) void bwd_sweep(BwdArgs a) {
+template <typename IN, typename SLOT, bool ACT, int S, int TB>
+__global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     using Raw = typename SLOT::Raw;
+    constexpr bool kWide = sizeof(Raw) == 8;
     extern __shared__ float lds[];
-    constexpr int P = bwd_depth(KPL);
     const int lane = lane_id();
-    const int S = a.S, L = kWave / S;
-    const int x = lane / L, kl = lane % L;
+    const int gl = threadIdx.x;
+    const int w = uniform(gl / kWave);
+    const int W = a.W;
+    const int kslot = lane / S, x = lane % S;
     int b, slice;
     block_coords(b, slice);
     const int col = slice * S + x;
     const int N = a.N, d = a.d, K = a.K, T = a.T;
-    float* lds_A = lds;  // [N*S], then one dummy word
-    const int dummy = N * S;
-    // (uniform trip counts with per-lane guards: a divergent loop exit would make the values
-    // defined in it divergent, row pointers included)
-    const float* dhT_row = a.dh_T ? a.dh_T + int64_t(b) * N * d : nullptr;
-    for (int n0 = 0; n0 < N; n0 += L)
-        if (n0 + kl < N) lds_A[(n0 + kl) * S + x] = dhT_row ? dhT_row[int64_t(n0 + kl) * d + col] : 0.0f;
-    float R = a.dq_T ? a.dq_T[int64_t(b) * d + col] : 0.0f;
+    const int NS = N * S;
+    const bool active = kslot < K;
+    float* st = lds + w * a.region;  // mu, then A: [NS] + a dummy word
+    float* st2 = st + NS + 1;        // nu (chunked only)
+    // [W][S]: the chunks' summary-cotangent sums (the region is an even number of words, so
+    // this is 8-byte aligned); [W]: whether the chunk resets R
+    double* rl = reinterpret_cast<double*>(lds + W * a.region);
+    int* rf = reinterpret_cast<int*>(rl + W * S);
+    const int t_begin = w * a.Tc;
+    const int t_end = min(T, t_begin + a.Tc);
+    const int nsb = (t_end - t_begin + TB - 1) / TB;
+    const DivN divn = a.divn;
 
     const uint32_t kd = uint32_t(K) * d;
-    const uint32_t row_bytes = T * kd * sizeof(IN);
+    const uint32_t row_bytes = uint32_t(T) * kd * sizeof(IN);
     const int64_t base = b * a.y_row;
     const rsrc_t ry = make_rsrc(static_cast<const IN*>(a.y) + base, row_bytes);
     const rsrc_t rg = make_rsrc(static_cast<const IN*>(a.g) + base, row_bytes);
     const rsrc_t rho = make_rsrc(static_cast<const IN*>(a.h_old) + base, row_bytes);
     const rsrc_t rds = make_rsrc(a.dsel ? static_cast<const IN*>(a.dsel) + base : nullptr,
                                  a.dsel ? row_bytes : 0);
-    IN* const dy_row = static_cast<IN*>(a.dy) + base;
-    IN* const dg_row = static_cast<IN*>(a.dg) + base;
+    const rsrc_t rdy = make_rsrc(static_cast<IN*>(a.dy) + base, row_bytes);
+    const rsrc_t rdg = make_rsrc(static_cast<IN*>(a.dg) + base, row_bytes);
     const rsrc_t rc = make_rsrc(static_cast<const Raw*>(a.cells) + b * a.s_row, T * K * sizeof(Raw));
     const rsrc_t rv = make_rsrc(a.valid ? a.valid + b * a.s_row : nullptr, a.valid ? T * K : 0);
     const rsrc_t rr = make_rsrc(a.reset + b * a.r_row, T);
-    const uint32_t qbytes = T * uint32_t(d) * sizeof(IN);
+    const uint32_t qbytes = uint32_t(T) * d * sizeof(IN);
     const rsrc_t rqa = make_rsrc(a.dq_pre ? static_cast<const IN*>(a.dq_pre) + b * a.q_row : nullptr,
                                  a.dq_pre ? qbytes : 0);
     const rsrc_t rqb = make_rsrc(a.dq_post ? static_cast<const IN*>(a.dq_post) + b * a.q_row : nullptr,
                                  a.dq_post ? qbytes : 0);
-    bool active[KPL];
-    uint32_t vy[KPL], vc[KPL], vv[KPL], eo[KPL];
-#pragma unroll
-    for (int j = 0; j < KPL; ++j) {
-        const int k = kl + j * L;
-        active[j] = k < K;
-        vy[j] = active[j] ? uint32_t(k * d + col) * sizeof(IN) : kOob;
-        eo[j] = uint32_t((active[j] ? k : 0) * d + col);
-        vc[j] = active[j] ? uint32_t(k) * sizeof(Raw) : kOob;
-        vv[j] = active[j] ? uint32_t(k) : kOob;
-    }
-    const uint32_t vq = uint32_t(col) * sizeof(IN);
+    const uint32_t vy = active ? uint32_t(kslot * d + col) * sizeof(IN) : kOob;
+    const uint32_t vc = active ? uint32_t(kslot) * sizeof(Raw) : kOob;
+    const uint32_t vv = active ? uint32_t(kslot) : kOob;
+    const uint32_t vq = uint32_t(col) * sizeof(IN);  // every lane reads its column's cotangent
 
-    auto load = [&](BwdStage<IN, SLOT, KPL>& st, int t) {
-        t = uniform(t >= 0 ? t : 0);
-        const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
-        const uint32_t sc = uint32_t(t) * K;
+    // the summary cotangents of a sub-block and its reset mask
+    float qa[TB], qb[TB];
+    uint32_t rmask = 0u;
+    auto fetch_q = [&](int tb0) {
+        const int tl = t_end - 1;
 #pragma unroll
-        for (int j = 0; j < KPL; ++j) {
-            st.y[j] = bload<IN>(ry, vy[j], sy);
-            st.g[j] = bload<IN>(rg, vy[j], sy);
-            st.ho[j] = bload<IN>(rho, vy[j], sy);
-            st.ds[j] = bload<IN>(rds, vy[j], sy);
-            st.c[j] = bload<Raw>(rc, vc[j], sc * sizeof(Raw));
-            if constexpr (sizeof(Raw) == 8) st.v[j] = bload<uint8_t>(rv, vv[j], sc);
-            else st.v[j] = 1;
+        for (int i = 0; i < TB; ++i) {
+            const uint32_t sq = uint32_t(uniform(min(tb0 + i, tl))) * d * sizeof(IN);
+            qa[i] = to_f32(bload<IN>(rqa, vq, sq));
+            qb[i] = to_f32(bload<IN>(rqb, vq, sq));
         }
-        const uint32_t sq = uint32_t(t) * d * sizeof(IN);
-        st.qpre = bload<IN>(rqa, vq, sq);
-        st.qpost = bload<IN>(rqb, vq, sq);
-        st.r = bload<uint8_t>(rr, 0u, uint32_t(t));
+        const bool rin = lane < TB && tb0 + lane < t_end;
+        const uint8_t r = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
+        rmask = static_cast<uint32_t>(ballot(r != 0));
     };
 
-    BwdStage<IN, SLOT, KPL> stage[P];
+    // The summary cotangent R is a running sum of 2T cotangents; it is accumulated in fp64 (its
+    // chunked sums would otherwise round differently from a sequential fp32 sum by about
+    // sqrt(2T) ulps of its largest partial), and every position's share R/N is rounded to fp32.
+    // R at the chunk's end (its later side): the end-state cotangent, then the later chunks'
+    double R_in = a.dq_T ? double(a.dq_T[int64_t(b) * d + col]) : 0.0;
+    double R_out = 0.0;  // R after the chunk (its position t_begin)
+    if (W > 1) {
+        // pre-pass: each chunk's own sum (restarted at its resets, processed latest first)
+        double Rl = 0.0;
+        bool hasr = false;
+        for (int sb = nsb - 1; sb >= 0; --sb) {
+            const int tb0 = t_begin + sb * TB;
+            const int n = min(TB, t_end - tb0);
+            fetch_q(tb0);
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-        load(stage[p], T - 1 - p);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-
-    for (int t0 = T - 1; t0 >= 0; t0 -= P) {
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-            const int t = t0 - p;
-            if (t >= 0) {
-                R += to_f32(stage[p].qpost);  // absent cotangents read as zero
-                const float share = a.n_pow2 ? R * a.inv_n : R / a.n_f;
-                int cell[KPL];
-                float aold[KPL];
-#pragma unroll
-                for (int j = 0; j < KPL; ++j) {
-                    cell[j] = active[j] ? slot_cell<SLOT>(stage[p].c[j], stage[p].v[j]) : -2;
-                    aold[j] = lds_A[(cell[j] > 0 ? cell[j] : 0) * S + x];
-                }
-                const uint32_t to = uint32_t(uniform(t)) * kd;
-#pragma unroll
-                for (int j = 0; j < KPL; ++j) {
-                    float c, bg;
-                    if constexpr (ACT) {
-                        c = fast_tanh(to_f32(stage[p].y[j]));
-                        bg = fast_sigmoid(to_f32(stage[p].g[j]));
-                    } else {
-                        c = to_f32(stage[p].y[j]);
-                        bg = to_f32(stage[p].g[j]);
+            for (int i = TB - 1; i >= 0; --i) {
+                if (i < n) {
+                    Rl += double(qb[i]);
+                    Rl += double(qa[i]);
+                    if ((rmask >> i) & 1u) {
+                        Rl = 0.0;
+                        hasr = true;
                     }
-                    const bool ok = cell[j] >= 0;
-                    const float carried = aold[j] + to_f32(stage[p].ds[j]);
-                    const float gg = carried + share;
-                    float dc = ok ? bg * gg : 0.0f;
-                    float db = ok ? (c - to_f32(stage[p].ho[j])) * gg : 0.0f;
-                    lds_A[ok ? cell[j] * S + x : dummy] = (1.0f - bg) * carried - bg * share;
-                    if constexpr (ACT) {
-                        dc = dc * (1.0f - c * c);    // tanh'
-                        db = db * (1.0f - bg) * bg;  // sigmoid'
-                    }
-                    if (active[j]) {
-                        store_f32(dy_row + to, eo[j], dc);
-                        store_f32(dg_row + to, eo[j], db);
-                    }
-                }
-                R += to_f32(stage[p].qpre);
-                if (uniform(stage[p].r)) {
-                    // the boundary: nothing before it reaches past the reset
-                    for (int e0 = 0; e0 < N * S; e0 += kWave)
-                        if (e0 + lane < N * S) lds_A[e0 + lane] = 0.0f;
-                    R = 0.0f;
                 }
             }
-            load(stage[p], t - P);
+        }
+        if (kslot == 0) rl[w * S + x] = Rl;
+        if (lane == 0) rf[w] = hasr ? 1 : 0;
+        __syncthreads();
+        for (int j = W - 1; j > w; --j) R_in = (rf[j] ? 0.0 : R_in) + rl[j * S + x];
+        R_out = (hasr ? 0.0 : R_in) + Rl;
+    }
+
+    // the sub-block in registers: (1 - b), the A update's constant term, dsel + share, and the
+    // output factors dc = p1 g, db = p2 g (activation derivatives folded in)
+    float omb[TB], e2[TB], e3[TB], p1[TB], p2[TB];
+    int cl[TB];
+    // positions' shares and A-update terms from the running R (latest position first)
+    auto fetch_a = [&](int tb0, int n, double& R) {
+        const int tl = t_end - 1;
+        IN gv[TB], dv[TB];
+        int32_t cv[TB];
+        uint8_t vb[TB];
+#pragma unroll
+        for (int i = 0; i < TB; ++i) {
+            const int t = uniform(min(tb0 + i, tl));
+            const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
+            gv[i] = bload<IN>(rg, vy, sy);
+            dv[i] = bload<IN>(rds, vy, sy);
+            cv[i] = bload<int32_t>(rc, vc, uint32_t(t) * K * sizeof(Raw));
+            if constexpr (kWide) vb[i] = bload<uint8_t>(rv, vv, uint32_t(t) * K);
+        }
+        fetch_q(tb0);
+#pragma unroll
+        for (int i = TB - 1; i >= 0; --i) {
+            float share = 0.0f;
+            if (i < n) {
+                R += double(qb[i]);
+                share = static_cast<float>(divn(R));
+                R += double(qa[i]);
+                if ((rmask >> i) & 1u) R = 0.0;
+            }
+            const float bg = ACT ? fast_sigmoid(to_f32(gv[i])) : to_f32(gv[i]);
+            const float ds = to_f32(dv[i]);
+            omb[i] = 1.0f - bg;
+            e2[i] = omb[i] * ds - bg * share;
+            e3[i] = ds + share;
+            p1[i] = bg;  // the gate, until fetch_c folds the candidate in
+            int c = cv[i];
+            if constexpr (kWide) c = vb[i] ? c : -1;
+            cl[i] = active ? c : -2;
+        }
+    };
+    auto fetch_c = [&](int tb0) {
+        const int tl = t_end - 1;
+        IN yv[TB], hv[TB];
+#pragma unroll
+        for (int i = 0; i < TB; ++i) {
+            const uint32_t sy = uint32_t(uniform(min(tb0 + i, tl))) * kd * sizeof(IN);
+            yv[i] = bload<IN>(ry, vy, sy);
+            hv[i] = bload<IN>(rho, vy, sy);
+        }
+#pragma unroll
+        for (int i = 0; i < TB; ++i) {
+            const float bg = p1[i];
+            const float c = ACT ? fast_tanh(to_f32(yv[i])) : to_f32(yv[i]);
+            const float diff = c - to_f32(hv[i]);
+            if constexpr (ACT) {
+                p1[i] = bg * (1.0f - c * c);         // tanh'
+                p2[i] = diff * (omb[i] * bg);        // sigmoid'
+            } else {
+                p2[i] = diff;
+            }
+        }
+    };
+
+    double R = R_in;
+    if (W > 1) {
+        // phase A: the chunk's per-cell maps A_before = mu A_after + nu, latest position first
+        for (int e0 = 0; e0 < NS; e0 += kWave) {
+            const int e = e0 + lane;
+            if (e < NS) {
+                st[e] = 1.0f;
+                st2[e] = 0.0f;
+            }
+        }
+        for (int sb = nsb - 1; sb >= 0; --sb) {
+            const int tb0 = t_begin + sb * TB;
+            const int n = min(TB, t_end - tb0);
+            fetch_a(tb0, n, R);
+#pragma unroll
+            for (int i = TB - 1; i >= 0; --i) {
+                if (i < n) {
+                    const int ci = cl[i];
+                    const int ri = (ci > 0 ? ci : 0) * S + x;
+                    const float mu = st[ri], nu = st2[ri];
+                    const int wi = ci >= 0 ? ci * S + x : NS;
+                    st[wi] = omb[i] * mu;
+                    st2[wi] = omb[i] * nu + e2[i];
+                    if ((rmask >> i) & 1u) {  // nothing before the boundary reaches past it
+                        lds_zero(st, NS, lane);
+                        lds_zero(st2, NS, lane);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        // phase B: every chunk's end cotangent (into its mu's place), latest chunk first
+        const float* dhT_row = a.dh_T ? a.dh_T + int64_t(b) * N * d : nullptr;
+        for (int e0 = 0; e0 < NS; e0 += kWave * W) {
+            const int e = e0 + gl;
+            if (e < NS) {
+                float A = dhT_row ? dhT_row[int64_t(e / S) * d + slice * S + e % S] : 0.0f;
+#pragma unroll
+                for (int j = kMaxChunks - 1; j >= 0; --j) {
+                    if (j < W) {
+                        float* sj = lds + j * a.region;
+                        const float mu = sj[e], nu = sj[NS + 1 + e];
+                        sj[e] = A;
+                        A = mu * A + nu;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        R = R_in;
+    } else {
+        const float* dhT_row = a.dh_T ? a.dh_T + int64_t(b) * N * d : nullptr;
+        for (int e0 = 0; e0 < NS; e0 += kWave) {
+            const int e = e0 + lane;
+            if (e < NS) st[e] = dhT_row ? dhT_row[int64_t(e / S) * d + slice * S + e % S] : 0.0f;
         }
     }
-    if (a.dh0) {
-        float* dh0_row = a.dh0 + int64_t(b) * N * d;
-        for (int n0 = 0; n0 < N; n0 += L)
-            if (n0 + kl < N) dh0_row[int64_t(n0 + kl) * d + col] = lds_A[(n0 + kl) * S + x];
+
+    // phase C: the replay with the outputs, latest position first
+    for (int sb = nsb - 1; sb >= 0; --sb) {
+        const int tb0 = t_begin + sb * TB;
+        const int n = min(TB, t_end - tb0);
+        if (W == 1 || nsb > 1) fetch_a(tb0, n, R);
+        fetch_c(tb0);
+#pragma unroll
+        for (int i = TB - 1; i >= 0; --i) {
+            if (i < n) {
+                const int ci = cl[i];
+                const bool ok = ci >= 0;
+                const float aold = st[(ci > 0 ? ci : 0) * S + x];
+                const float gg = aold + e3[i];
+                st[ok ? ci * S + x : NS] = omb[i] * aold + e2[i];
+                const uint32_t so = uint32_t(tb0 + i) * kd * sizeof(IN);
+                bstore_f32<IN>(ok ? p1[i] * gg : 0.0f, rdy, vy, so);
+                bstore_f32<IN>(ok ? p2[i] * gg : 0.0f, rdg, vy, so);
+                if ((rmask >> i) & 1u) lds_zero(st, NS, lane);
+            }
+        }
     }
-    if (a.dq0 && kl == 0) a.dq0[int64_t(b) * d + col] = R;
+    if (W == 1) R_out = R;
+
+    // the carried-state gradient: A and R after position 0
+    if (w == 0) {
+        if (a.dh0) {
+            float* dh0_row = a.dh0 + int64_t(b) * N * d;
+            for (int e0 = 0; e0 < NS; e0 += kWave) {
+                const int e = e0 + lane;
+                if (e < NS) dh0_row[int64_t(e / S) * d + slice * S + e % S] = st[e];
+            }
+        }
+        if (a.dq0 && kslot == 0) a.dq0[int64_t(b) * d + col] = static_cast<float>(R_out);
+    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -565,54 +805,48 @@ __global__ __launch_bounds__(256) void zero_strided_kernel(float* p, int64_t cou
 }  // namespace
 
 // ------------------------------------------------------------------------------------------
-// Host-side shape choice
+// Host-side geometry
 // ------------------------------------------------------------------------------------------
 
-struct SliceShape {
-    int S;    // columns per wavefront (1, 4, 8 or 16)
-    int kpl;  // slots per lane (1, 2, 4 or 8)
+struct Geometry {
+    int S;   // columns per wavefront (1, 2, 4, 8 or 16), S * K <= 64
+    int W;   // chunks (wavefronts) per workgroup
+    int Tc;  // positions per chunk
 };
 
-// S: one slot per lane (S <= 64 / K) keeps the most wavefronts in flight for small batches;
-// wider slices (up to 16 columns, 64-byte fp32 segments) are taken while the grid still holds
-// >= 2048 wavefronts. Narrowed while the slice's LDS does not fit.
-inline bool choose_shape(int B, int d, int K, int64_t lds_per_col, int64_t lds_fixed,
-                         SliceShape& out) {
-    constexpr int64_t kLdsMax = 160 * 1024;
-    const int cand[4] = {16, 8, 4, 1};
-    int best = -1;
-    for (int i = 0; i < 4; ++i) {  // the widest S dividing d with one slot per lane
+constexpr int64_t kLdsMax = 160 * 1024;
+constexpr int64_t kTargetWaves = 2048;  // two wavefronts per SIMD of the 256-CU chip
+
+// The widest S dividing d with one slot per lane; then as many chunks as bring the grid to
+// about two wavefronts per SIMD, within the LDS. `lds_of(N, S, W)` is the kernel's LDS bytes.
+template <typename F>
+inline bool choose_geometry(int B, int T, int N, int d, int K, F lds_of, Geometry& g) {
+    const int cand[5] = {16, 8, 4, 2, 1};
+    for (int i = 0; i < 5; ++i) {
         const int S = cand[i];
-        if (d % S == 0 && S * K <= kWave) {
-            best = i;
-            break;
-        }
-    }
-    if (best < 0) best = 3;
-    // widen while many wavefronts remain
-    while (best > 0 && d % cand[best - 1] == 0 && int64_t(B) * (d / cand[best - 1]) >= 2048) --best;
-    for (int i = best; i < 4; ++i) {
-        const int S = cand[i];
-        if (d % S) continue;
-        const int L = kWave / S;
-        const int kpl_need = (K + L - 1) / L;
-        if (kpl_need > 8) continue;
-        if (lds_per_col * S + lds_fixed > kLdsMax) continue;
-        int kpl = 1;
-        while (kpl < kpl_need) kpl <<= 1;
-        out.S = S;
-        out.kpl = kpl;
+        if (d % S || S * K > kWave) continue;
+        if (int64_t(lds_of(N, S, 1)) > kLdsMax) continue;
+        const int64_t waves = int64_t(B) * (d / S);
+        int W = 1;
+        while (W < kMaxChunks && W < T && waves * W < kTargetWaves &&
+               int64_t(lds_of(N, S, 2 * W)) <= kLdsMax)
+            W *= 2;
+        if (W > T) W = T;
+        const int Tc = (T + W - 1) / W;
+        g.S = S;
+        g.W = (T + Tc - 1) / Tc;  // no empty chunk
+        g.Tc = Tc;
         return true;
     }
     return false;
 }
 
-inline int xcd_rows_of(int B) { return (B % 8 == 0) ? B / 8 : 0; }
-
-inline void fill_n_consts(int N, int& pow2, float& inv_n, float& n_f) {
-    pow2 = (N & (N - 1)) == 0 ? 1 : 0;
-    inv_n = 1.0f / static_cast<float>(N);
-    n_f = static_cast<float>(N);
+inline DivN make_divn(int N) {
+    DivN v;
+    v.pow2 = (N & (N - 1)) == 0 ? 1 : 0;
+    v.inv = 1.0f / static_cast<float>(N);
+    v.n = static_cast<float>(N);
+    return v;
 }
 
 template <typename K>
@@ -623,55 +857,46 @@ hipError_t allow_lds(K kernel, size_t lds) {
 }
 
 template <typename IN, typename OUT, typename SLOT, int S>
-hipError_t launch_fwd_s(const FwdArgs& a, int kpl, size_t lds, hipStream_t st) {
-    const dim3 blocks = sweep_grid(a.B, a.d / S);
-#define HSN_FWD_CASE(KP)                                                                          \
-    case KP: {                                                                                    \
-        auto k = fwd_sweep<IN, OUT, SLOT, S, KP>;                                                 \
-        hipError_t e = allow_lds(k, lds);                                                         \
-        if (e != hipSuccess) return e;                                                            \
-        hipLaunchKernelGGL(k, blocks, dim3(kWave), lds, st, a);                             \
-        return hipGetLastError();                                                                 \
-    }
-    switch (kpl) {
-        HSN_FWD_CASE(1)
-        HSN_FWD_CASE(2)
-        HSN_FWD_CASE(4)
-        HSN_FWD_CASE(8)
-    }
-#undef HSN_FWD_CASE
-    return hipErrorInvalidValue;
+hipError_t launch_fwd_s(const FwdArgs& a, size_t lds, hipStream_t st) {
+    constexpr int TB = sizeof(typename SLOT::Raw) == 8 ? 16 : 32;
+    auto k = fwd_chunk<IN, OUT, SLOT, S, TB>;
+    hipError_t e = allow_lds(k, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k, sweep_grid(a.B, a.d / S), dim3(kWave * a.W), lds, st, a);
+    return hipGetLastError();
 }
 
 template <typename IN, typename OUT, typename SLOT>
-hipError_t launch_fwd(const FwdArgs& a, SliceShape sh, size_t lds, hipStream_t st) {
-    switch (sh.S) {
-        case 1: return launch_fwd_s<IN, OUT, SLOT, 1>(a, sh.kpl, lds, st);
-        case 4: return launch_fwd_s<IN, OUT, SLOT, 4>(a, sh.kpl, lds, st);
-        case 8: return launch_fwd_s<IN, OUT, SLOT, 8>(a, sh.kpl, lds, st);
-        case 16: return launch_fwd_s<IN, OUT, SLOT, 16>(a, sh.kpl, lds, st);
+hipError_t launch_fwd(const FwdArgs& a, int S, size_t lds, hipStream_t st) {
+    switch (S) {
+        case 1: return launch_fwd_s<IN, OUT, SLOT, 1>(a, lds, st);
+        case 2: return launch_fwd_s<IN, OUT, SLOT, 2>(a, lds, st);
+        case 4: return launch_fwd_s<IN, OUT, SLOT, 4>(a, lds, st);
+        case 8: return launch_fwd_s<IN, OUT, SLOT, 8>(a, lds, st);
+        case 16: return launch_fwd_s<IN, OUT, SLOT, 16>(a, lds, st);
     }
     return hipErrorInvalidValue;
 }
 
+template <typename IN, typename SLOT, bool ACT, int S>
+hipError_t launch_bwd_s(const BwdArgs& a, size_t lds, hipStream_t st) {
+    constexpr int TB = 16;
+    auto k = bwd_chunk<IN, SLOT, ACT, S, TB>;
+    hipError_t e = allow_lds(k, lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k, sweep_grid(a.B, a.d / S), dim3(kWave * a.W), lds, st, a);
+    return hipGetLastError();
+}
+
 template <typename IN, typename SLOT, bool ACT>
-hipError_t launch_bwd(const BwdArgs& a, int kpl, size_t lds, hipStream_t st) {
-    const dim3 blocks = sweep_grid(a.B, a.d / a.S);
-#define HSN_BWD_CASE(KP)                                                                          \
-    case KP: {                                                                                    \
-        auto k = bwd_sweep<IN, SLOT, ACT, KP>;                                                         \
-        hipError_t e = allow_lds(k, lds);                                                         \
-        if (e != hipSuccess) return e;                                                            \
-        hipLaunchKernelGGL(k, blocks, dim3(kWave), lds, st, a);                             \
-        return hipGetLastError();                                                                 \
+hipError_t launch_bwd(const BwdArgs& a, int S, size_t lds, hipStream_t st) {
+    switch (S) {
+        case 1: return launch_bwd_s<IN, SLOT, ACT, 1>(a, lds, st);
+        case 2: return launch_bwd_s<IN, SLOT, ACT, 2>(a, lds, st);
+        case 4: return launch_bwd_s<IN, SLOT, ACT, 4>(a, lds, st);
+        case 8: return launch_bwd_s<IN, SLOT, ACT, 8>(a, lds, st);
+        case 16: return launch_bwd_s<IN, SLOT, ACT, 16>(a, lds, st);
     }
-    switch (kpl) {
-        HSN_BWD_CASE(1)
-        HSN_BWD_CASE(2)
-        HSN_BWD_CASE(4)
-        HSN_BWD_CASE(8)
-    }
-#undef HSN_BWD_CASE
     return hipErrorInvalidValue;
 }
 

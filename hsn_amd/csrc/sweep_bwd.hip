@@ -43,14 +43,14 @@ __global__ __launch_bounds__(256) void dense_recurrence(const float* c, const fl
 void fill_common(BwdArgs& a, const void* y, const void* g, const void* h_old, const void* d_h_sel,
                  const void* d_q_pre, const void* d_q_post, const uint8_t* reset,
                  const float* d_h_T, const float* d_q_T, void* dy, void* dg, float* d_h0,
-                 float* d_q0, int B, int T, int N, int d, int K, int S) {
+                 float* d_q0, int B, int T, int N, int d, int K, const Geometry& geo) {
     a.y = y, a.g = g, a.h_old = h_old, a.y_row = int64_t(T) * K * d;
     a.dsel = d_h_sel, a.dq_pre = d_q_pre, a.dq_post = d_q_post;  // absent: read as zero
     a.q_row = int64_t(T) * d;
     a.reset = reset, a.r_row = T, a.s_row = int64_t(T) * K;
     a.dh_T = d_h_T, a.dq_T = d_q_T, a.dy = dy, a.dg = dg, a.dh0 = d_h0, a.dq0 = d_q0;
-    a.B = B, a.T = T, a.N = N, a.d = d, a.K = K, a.S = S, a.xcd_rows = xcd_rows_of(B);
-    fill_n_consts(N, a.n_pow2, a.inv_n, a.n_f);
+    a.B = B, a.T = T, a.N = N, a.d = d, a.K = K;
+    a.W = geo.W, a.Tc = geo.Tc, a.region = bwd_region(N, geo.S, geo.W), a.divn = make_divn(N);
 }
 
 }  // namespace
@@ -75,10 +75,10 @@ extern "C" int hsn_win_backward(const void* y, const void* gate_pre, const void*
                     int64_t(T) * K * d <= INT32_MAX,
                 HSN_ERR_SIZE_OVERFLOW,
                 "hsn_win_backward: a tensor is too large");
-    SliceShape sh;
-    HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, 4, sh), HSN_ERR_INVALID_ARGUMENT,
+    Geometry g;
+    HSN_REQUIRE(choose_geometry(B, T, N, d, K, bwd_lds_bytes, g), HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_backward: the cotangent slice does not fit the LDS (N too large)");
-    const size_t lds = size_t(N) * 4 * sh.S + 4;  // one dummy word
+    const size_t lds = bwd_lds_bytes(N, g.S, g.W);
     hipStream_t st = as_stream(stream);
     const int64_t nslots = int64_t(B) * T * K;
     const size_t elem = io_dtype == HSN_DTYPE_F32 ? 4 : 2;
@@ -100,12 +100,12 @@ extern "C" int hsn_win_backward(const void* y, const void* gate_pre, const void*
     }
     BwdArgs a{};
     fill_common(a, pre, gate_pre, h_old, d_h_sel, d_q_pre, d_q_post, reset, d_h_T, d_q_T, dy,
-                dgate, d_h0, d_q0, B, T, N, d, K, sh.S);
+                dgate, d_h0, d_q0, B, T, N, d, K, g);
     a.cells = slots, a.valid = nullptr;
     if (io_dtype == HSN_DTYPE_F32)
-        HSN_HIP((launch_bwd<float, Packed32, true>(a, sh.kpl, lds, st)));
+        HSN_HIP((launch_bwd<float, Packed32, true>(a, g.S, lds, st)));
     else
-        HSN_HIP((launch_bwd<bf16_t, Packed32, true>(a, sh.kpl, lds, st)));
+        HSN_HIP((launch_bwd<bf16_t, Packed32, true>(a, g.S, lds, st)));
     if (cand_norm) {  // the norm's VJP: dy holds dL/dpre
         const int blocks = static_cast<int>((nslots + 3) / 4);
         if (io_dtype == HSN_DTYPE_F32) {
@@ -145,15 +145,15 @@ extern "C" int hsn_win_recurrence(const float* c, const float* b, const float* h
                     int64_t(T) * K * d <= INT32_MAX,
                 HSN_ERR_SIZE_OVERFLOW,
                 "hsn_win_recurrence: a tensor is too large");
-    SliceShape sh;
-    HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, 4, sh), HSN_ERR_INVALID_ARGUMENT,
+    Geometry g;
+    HSN_REQUIRE(choose_geometry(B, T, N, d, K, bwd_lds_bytes, g), HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_recurrence: the cotangent slice does not fit the LDS (N too large)");
-    const size_t lds = size_t(N) * 4 * sh.S + 4;  // one dummy word
+    const size_t lds = bwd_lds_bytes(N, g.S, g.W);
     BwdArgs a{};
     fill_common(a, c, b, h_old, d_h_sel, d_q_pre, d_q_post, reset, d_h_T, d_q_T, dc, db, d_h0,
-                d_q0, B, T, N, d, K, sh.S);
+                d_q0, B, T, N, d, K, g);
     a.cells = cells, a.valid = valid;
-    HSN_HIP((launch_bwd<float, Cells64, false>(a, sh.kpl, lds, as_stream(stream))));
+    HSN_HIP((launch_bwd<float, Cells64, false>(a, g.S, lds, as_stream(stream))));
     HSN_ABI_END
 }
 

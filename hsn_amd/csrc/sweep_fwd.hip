@@ -50,11 +50,10 @@ extern "C" int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype
                     int64_t(T) * K * d <= INT32_MAX,
                 HSN_ERR_SIZE_OVERFLOW,
                 "hsn_win_forward: a tensor is too large");
-    SliceShape sh;
-    const int64_t fixed = int64_t(N) * 4 + 8;  // the ages' last-selection table, two dummies
-    HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, fixed, sh), HSN_ERR_INVALID_ARGUMENT,
+    Geometry g;
+    HSN_REQUIRE(choose_geometry(B, T, N, d, K, fwd_lds_bytes, g), HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_forward: the state slice does not fit the LDS (N too large)");
-    const size_t lds = size_t(N) * 4 * sh.S + size_t(fixed);
+    const size_t lds = fwd_lds_bytes(N, g.S, g.W);
     hipStream_t st = as_stream(stream);
     if (cand_norm) {
         y = rms_normalise(y, io_dtype, cand_w, cand_eps, rms_scratch, int64_t(B) * T * K, d, st);
@@ -71,12 +70,12 @@ extern "C" int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype
     a.h_max = h_max, a.hm_row = T;
     a.h_T = h_T, a.hT_row = int64_t(N) * d, a.q_T = q_T, a.qT_row = d;
     a.age_T = age_T, a.aT_row = N, a.pos_T = pos_T;
-    a.B = B, a.T = T, a.N = N, a.d = d, a.K = K, a.xcd_rows = xcd_rows_of(B);
-    fill_n_consts(N, a.n_pow2, a.inv_n, a.n_f);
+    a.B = B, a.T = T, a.N = N, a.d = d, a.K = K;
+    a.W = g.W, a.Tc = g.Tc, a.region = fwd_region(N, g.S, g.W), a.divn = make_divn(N);
     if (io_dtype == HSN_DTYPE_F32)
-        HSN_HIP((launch_fwd<float, float, Packed32>(a, sh, lds, st)));
+        HSN_HIP((launch_fwd<float, float, Packed32>(a, g.S, lds, st)));
     else
-        HSN_HIP((launch_fwd<bf16_t, bf16_t, Packed32>(a, sh, lds, st)));
+        HSN_HIP((launch_fwd<bf16_t, bf16_t, Packed32>(a, g.S, lds, st)));
     HSN_ABI_END
 }
 
@@ -103,11 +102,10 @@ extern "C" int hsn_win_cell_update(const void* y, const void* gate, int io_dtype
                 "hsn_win_cell_update: the RMS candidate needs cand_w and rms_scratch");
     HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
                 HSN_ERR_UNSUPPORTED_DTYPE, "hsn_win_cell_update: io_dtype must be f32 or bf16");
-    SliceShape sh;
-    const int64_t fixed = int64_t(N) * 4 + 8;
-    HSN_REQUIRE(choose_shape(B, d, K, int64_t(N) * 4, fixed, sh), HSN_ERR_INVALID_ARGUMENT,
+    Geometry g;
+    HSN_REQUIRE(choose_geometry(B, 1, N, d, K, fwd_lds_bytes, g), HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_cell_update: the state slice does not fit the LDS (N too large)");
-    const size_t lds = size_t(N) * 4 * sh.S + size_t(fixed);
+    const size_t lds = fwd_lds_bytes(N, g.S, g.W);
     hipStream_t st = as_stream(stream);
     if (cand_norm) {
         y = rms_normalise(y, io_dtype, cand_w, cand_eps, rms_scratch, int64_t(B) * K, d, st);
@@ -129,16 +127,16 @@ extern "C" int hsn_win_cell_update(const void* y, const void* gate, int io_dtype
     a.h_T = h_next + int64_t(t_out) * N * d, a.hT_row = int64_t(n_state) * N * d;
     a.q_T = q_next + int64_t(t_out) * d, a.qT_row = int64_t(n_state) * d;
     a.age_T = age_next + int64_t(t_out) * N, a.aT_row = int64_t(n_state) * N, a.pos_T = pos_next;
-    a.B = B, a.T = 1, a.N = N, a.d = d, a.K = K, a.xcd_rows = xcd_rows_of(B);
-    fill_n_consts(N, a.n_pow2, a.inv_n, a.n_f);
+    a.B = B, a.T = 1, a.N = N, a.d = d, a.K = K;
+    a.W = g.W, a.Tc = g.Tc, a.region = fwd_region(N, g.S, g.W), a.divn = make_divn(N);
     // h_max is max-reduced across the row's slices: zero it first (a kernel, not a memset, so
     // the call stays capturable)
     hipLaunchKernelGGL(zero_strided_kernel, dim3((B + 255) / 256), dim3(256), 0, st, a.h_max,
                        int64_t(B), int64_t(n_slot));
     HSN_HIP(hipGetLastError());
     if (io_dtype == HSN_DTYPE_F32)
-        HSN_HIP((launch_fwd<float, float, Cells64>(a, sh, lds, st)));
+        HSN_HIP((launch_fwd<float, float, Cells64>(a, g.S, lds, st)));
     else
-        HSN_HIP((launch_fwd<bf16_t, float, Cells64>(a, sh, lds, st)));
+        HSN_HIP((launch_fwd<bf16_t, float, Cells64>(a, g.S, lds, st)));
     HSN_ABI_END
 }

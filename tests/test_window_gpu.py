@@ -44,6 +44,22 @@ def _close(got, want, tol, what=""):
                              f"(max err {float(err.max()):.3g})")
 
 
+def _d_q0_exact(reset, d_q_pre, d_q_post, d_q_T, n_cells):
+    """The summary cotangent after position 0 (``d_q0``) from the oracle's recurrence in float64.
+
+    ``R`` is a running sum of the window's ``2T`` summary cotangents. Summed in fp32 in the
+    reference's sequential order it carries about sqrt(2T)/2 ulps of its largest partial (2e-5
+    at the ref shape, above the 1e-5 bar), and the HIP sweep sums it chunk by chunk in fp64, so
+    ``d_q0`` is checked against the exact sum. ``R`` reads no other input."""
+    B, T, d = (d_q_post if d_q_post is not None else d_q_pre).shape
+    z = torch.zeros(B, T, 1, d, dtype=torch.float64)
+    cells = torch.zeros(B, T, 1, dtype=torch.int64)
+    valid = torch.zeros(B, T, 1, dtype=torch.bool)
+    f = lambda t: None if t is None else t.detach().cpu().double()  # noqa: E731
+    return O.recurrence_backward(z, z, z, cells, valid, reset.cpu(), n_cells, f(d_q_pre),
+                                 f(d_q_post), None, None, f(d_q_T), carried=True)[3]
+
+
 def _route_cfg(**kw):
     from hsn_amd.window import RouteConfig
 
@@ -157,6 +173,9 @@ WINDOW_CASES = [
     dict(B=2, T=17, N=48, d=32, K=32, io="f32", rms=True),  # many slots per lane
     dict(B=4, T=32, N=128, d=64, K=16, io="bf16"),
     dict(B=2, T=16, N=64, d=16, K=8, io="bf16", rms=True, limit=0.1),
+    dict(B=8, T=300, N=64, d=64, K=8, io="f32"),  # chunks longer than a register sub-block
+    dict(B=256, T=70, N=32, d=64, K=8, io="f32"),  # one chunk per row, several sub-blocks
+    dict(B=3, T=5, N=16, d=4, K=4, io="f32"),  # fewer positions than chunks per row
 ]
 
 
@@ -216,8 +235,10 @@ def test_window_forward_and_backward_match_oracle(dev, case):
                          cot["d_q_post"].to(dev), d_h_sel.to(dev), cot["d_h_T"].to(dev),
                          cot["d_q_T"].to(dev), cand_norm=rms,
                          cand_w=None if cand_w is None else cand_w.to(dev))
-    for name, g_, w_ in zip(("dy", "dgate", "d_h0", "d_q0"), gb[:4], wb[:4]):
+    for name, g_, w_ in zip(("dy", "dgate", "d_h0"), gb[:3], wb[:3]):
         _close(g_, w_, tol, name)
+    _close(gb[3], _d_q0_exact(w["reset"], cot["d_q_pre"], cot["d_q_post"], cot["d_q_T"], cfg_w.N),
+           tol, "d_q0")
     if rms:
         _close(gb[4], wb[4], tol * 10, "d_cand_w")  # a sum over every slot of the window
     zero_pad = ~want["valid"]
@@ -241,8 +262,13 @@ def test_backward_without_optional_cotangents(dev):
                              cfg_w.N, None if pre is None else pre.to(dev),
                              None if post is None else post.to(dev),
                              None if sel is None else sel.to(dev))
-        for name, g_, w_ in zip(("dy", "dgate", "d_h0", "d_q0"), gb[:4], wb[:4]):
+        for name, g_, w_ in zip(("dy", "dgate", "d_h0"), gb[:3], wb[:3]):
             _close(g_, w_, F32_TOL, f"{name} {present}")
+        if pre is not None or post is not None:
+            _close(gb[3], _d_q0_exact(w["reset"], pre, post, None, cfg_w.N), F32_TOL,
+                   f"d_q0 {present}")
+        else:
+            assert bool((gb[3] == 0).all())
 
 
 @pytest.mark.parametrize("shape", [(3, 7, 5, 3, 4), (1, 1, 2, 1, 1), (4, 50, 300, 8, 64),
@@ -271,8 +297,9 @@ def test_recurrence_backward_matches_oracle(dev, shape):
     got = W.recurrence_backward_carried(put(c), put(b), put(h_old), put(cells), put(valid),
                                         put(reset), N, put(pre), put(post), put(sel), put(dhT),
                                         put(dqT))
-    for name, g_, w_ in zip(("dc", "db", "d_h0", "d_q0"), got, want):
+    for name, g_, w_ in zip(("dc", "db", "d_h0"), got, want):
         _close(g_, w_, F32_TOL, name)
+    _close(got[3], _d_q0_exact(reset, pre, post, dqT, N), F32_TOL, "d_q0")
     dc, db = W.recurrence_backward(put(c), put(b), put(h_old), put(cells), put(valid), put(reset),
                                    N, put(pre), put(post), put(sel))
     want2 = O.recurrence_backward(c, b, h_old, cells, valid, reset, N, pre, post, sel)
@@ -450,6 +477,8 @@ def test_ref_shape_window_rows_match_oracle(dev):
     wb = O.window_backward(sub["y"], sub["gate_pre"], want["h_old"], want["cells"], want["valid"],
                            sub["reset"], cfg_w.N, csub["d_q_pre"], csub["d_q_post"],
                            csub["d_h_sel"], csub["d_h_T"], csub["d_q_T"])
-    for name, g_, w_ in zip(("dy", "dgate", "d_h0", "d_q0"), g1[:4], wb[:4]):
+    for name, g_, w_ in zip(("dy", "dgate", "d_h0"), g1[:3], wb[:3]):
         _close(g_[rows], w_, F32_TOL, name)
+    _close(g1[3][rows], _d_q0_exact(sub["reset"], csub["d_q_pre"], csub["d_q_post"],
+                                    csub["d_q_T"], cfg_w.N), F32_TOL, "d_q0")
     assert math.isfinite(float(got["h_max"].max()))
