@@ -5,14 +5,15 @@
 // probes of _post_process :1788-1850) so that the integer outputs are bit-identical to the CPU
 // path on the same inputs.
 //
-// Layout: lane l holds cells n = l + 64 i (i < NPL), so a position's logits are read with
-// coalesced loads. The K winners are found by K rounds of a wavefront argmax over a total-order
-// key (descending score, ties by ascending index, NaN above +inf, -0 equal to +0, reserved cells
-// at +inf); each lane keeps its own best so a round costs one cross-lane reduction plus one
-// lane's rescan. Without probes the positions are independent (the logits are inputs), so the
+// Layout: lane l holds the block of cells n = l*NPL + i (i < NPL), so a position's logits are one
+// contiguous read per wavefront and, among equal keys, the lowest lane holds the smallest cell.
+// The K winners are found by K rounds of a wavefront argmax over a total-order key (descending
+// score, ties by ascending index, NaN above +inf, -0 equal to +0, reserved cells at +inf): a DPP
+// max of the lanes' bests, the first lane holding it by ballot, and that lane's rescan. Without probes the positions are independent (the logits are inputs), so the
 // whole window is one launch with a wavefront per (row, position); with probes the ages evolve
 // with the decisions and one wavefront walks a row's positions in order, its ages in VGPRs.
 #include "common.cuh"
+#include "dpp.cuh"
 
 namespace hsn {
 namespace {
@@ -38,40 +39,48 @@ struct RouteArgs {
     float lambda, overhead, shared, limit;
 };
 
-// (key, n) ordering: a before b in the stable descending order.
-__device__ __forceinline__ bool before(uint32_t ka, int na, uint32_t kb, int nb) {
-    return ka > kb || (ka == kb && na < nb);
+// Wavefront reductions with DPP (no LDS traffic): the four steps inside each 16-lane row are
+// symmetric (every lane ends with the row's result), row_bcast:15 / row_bcast:31 then fold the
+// rows into lane 63, which is read as a uniform value.
+template <typename F>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v, F op, uint32_t identity) {
+    v = op(v, dpp_u32<dpp::kXor1>(v));
+    v = op(v, dpp_u32<dpp::kXor2>(v));
+    v = op(v, dpp_u32<dpp::kHalfMirror>(v));
+    v = op(v, dpp_u32<dpp::kRor8>(v));
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+                  static_cast<int>(identity), static_cast<int>(v), 0x142, 0xa, 0xf, false)));
+    v = op(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+                  static_cast<int>(identity), static_cast<int>(v), 0x143, 0xc, 0xf, false)));
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+template <typename F>
+__device__ __forceinline__ float wave_reduce_f32(float v, F op, float identity) {
+    auto u = [](float f) { return static_cast<uint32_t>(__float_as_int(f)); };
+    auto f = [](uint32_t x) { return __int_as_float(static_cast<int>(x)); };
+    const uint32_t r = wave_reduce_u32(
+        u(v), [&](uint32_t a, uint32_t b) { return u(op(f(a), f(b))); }, u(identity));
+    return f(r);
 }
 
-// Wavefront argmax of (key, n) pairs: the largest key, the smallest n among equal keys.
+// Wavefront argmax of this lane's best (key, n): the largest key, the smallest n among equal
+// keys. Cells are laid out in blocks (lane l holds n = l*NPL + i), so among equal keys the
+// lowest lane holds the smallest n, and a lane's best is its first maximum.
 __device__ __forceinline__ void wave_argmax(uint32_t k, int n, uint32_t& wk, int& wn) {
-#pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) {
-        const uint32_t ko = wave_shfl_xor(k, m);
-        const int no = wave_shfl_xor(n, m);
-        if (before(ko, no, k, n)) {
-            k = ko;
-            n = no;
-        }
-    }
-    wk = k;
-    wn = n;
+    wk = wave_reduce_u32(k, [](uint32_t a, uint32_t b) { return a > b ? a : b; }, 0u);
+    const int src = __builtin_ctzll(ballot(k == wk));
+    wn = __builtin_amdgcn_readlane(n, src);
 }
 
 __device__ __forceinline__ float wave_nan_min(float v) {
-#pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v = nan_min(v, wave_shfl_xor(v, m));
-    return v;
+    return wave_reduce_f32(v, [](float a, float b) { return nan_min(a, b); }, INFINITY);
 }
 __device__ __forceinline__ float wave_nan_max(float v) {
-#pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v = nan_max(v, wave_shfl_xor(v, m));
-    return v;
+    return wave_reduce_f32(v, [](float a, float b) { return nan_max(a, b); }, -INFINITY);
 }
 __device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) v += wave_shfl_xor(v, m);
-    return v;
+    return static_cast<int>(wave_reduce_u32(
+        static_cast<uint32_t>(v), [](uint32_t a, uint32_t b) { return a + b; }, 0u));
 }
 
 template <typename IDX>
@@ -95,7 +104,7 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
     int slot_of[NPL];  // 1 + the scored slot that took the cell, 0 if none
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
-        const int n = lane + kWave * i;
+        const int n = lane * NPL + i;
         sc[i] = -INFINITY;
         unit[i] = 0;
         key[i] = 0u;  // below every real key: never chosen
@@ -127,7 +136,7 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
     for (int i = 0; i < NPL; ++i) {
         if (key[i] > bk) {  // strict: the first (smallest n) of equal keys stays
             bk = key[i];
-            bn = lane + kWave * i;
+            bn = lane * NPL + i;
         }
     }
 
@@ -138,7 +147,7 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
         uint32_t wk;
         int wn;
         wave_argmax(bk, bn, wk, wn);
-        const int wl = wn & (kWave - 1), wi = wn >> 6;
+        const int wl = wn / NPL, wi = wn % NPL;
         float ws = 0.0f;
         int wu = 0;
         if (lane == wl) {
@@ -157,7 +166,7 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
             for (int i = 0; i < NPL; ++i) {
                 if (key[i] > bk) {
                     bk = key[i];
-                    bn = lane + kWave * i;
+                    bn = lane * NPL + i;
                 }
             }
         }
@@ -193,7 +202,7 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
     bool stale[NPL];
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
-        const int n = lane + kWave * i;
+        const int n = lane * NPL + i;
         const bool sel = slot_of[i] > 0 && ((vmask >> (slot_of[i] - 1)) & 1ull);
         if (n < N && !sel) high = nan_max(high, sc[i]);
         stale[i] = a.probes && n < N && !sel && ages[i] > static_cast<int64_t>(a.age_max);
@@ -224,7 +233,7 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
                 pk[i] = stale[i] ? __float_as_uint(static_cast<float>(ages[i])) + 1u : 0u;
                 if (pk[i] > qk) {
                     qk = pk[i];
-                    qn = lane + kWave * i;
+                    qn = lane * NPL + i;
                 }
             }
             int new_cell = out_cell, new_unit = out_unit;
@@ -233,7 +242,7 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
                 uint32_t wk;
                 int wn;
                 wave_argmax(qk, qn, wk, wn);
-                const int wl = wn & (kWave - 1), wi = wn >> 6;
+                const int wl = wn / NPL, wi = wn % NPL;
                 int wu = 0;
                 if (lane == wl) {
 #pragma unroll
@@ -250,7 +259,7 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
                     for (int i = 0; i < NPL; ++i) {
                         if (pk[i] > qk) {
                             qk = pk[i];
-                            qn = lane + kWave * i;
+                            qn = lane * NPL + i;
                         }
                     }
                 }
@@ -324,7 +333,7 @@ __global__ __launch_bounds__(64) void route_sequential(RouteArgs a) {
     int64_t ages[NPL];
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
-        const int n = lane + kWave * i;
+        const int n = lane * NPL + i;
         int64_t v = 0;
         if (n < a.N) {
             if (a.age0) v = a.age0[static_cast<int64_t>(b) * a.N + n];

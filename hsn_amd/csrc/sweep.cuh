@@ -35,6 +35,9 @@
 // a chunk longer than TB reloads its sub-blocks in phase C.
 #pragma once
 
+#include <stddef.h>
+#include <type_traits>
+
 #include "common.cuh"
 #include "bufio.cuh"
 #include "dpp.cuh"
@@ -68,6 +71,8 @@ inline dim3 sweep_grid(int B, int nslices) {
 }
 
 constexpr int kMaxChunks = 8;  // wavefronts (chunks) per workgroup
+constexpr int kResTB = 32;     // positions per chunk held in registers (resident kernels)
+constexpr int kStreamTB = 16;  // positions per streamed sub-block
 
 // v / N as the reference divides (an exact reciprocal product when N is a power of two)
 struct DivN {
@@ -79,15 +84,19 @@ struct DivN {
     }
 };
 
-// Sum over the lanes with equal lane % S (a column's slot lanes).
-template <int S>
-__device__ __forceinline__ float col_sum(float v) {
+
+// Sums over the lanes with equal lane % S (a column's slot lanes) of every element of an array,
+// step by step across the array so the cross-lane moves of all elements are in flight together.
+template <int S, int M>
+__device__ __forceinline__ void col_sums(float (&v)[M]) {
 #pragma unroll
     for (int m = S; m < kWave; m <<= 1) {
-        if (m == 8) v += dpp_f32<dpp::kRor8>(v);  // xor 8 inside a 16-lane row
-        else v += __shfl_xor(v, m, kWave);
+#pragma unroll
+        for (int i = 0; i < M; ++i) {
+            if (m == 8) v[i] += dpp_f32<dpp::kRor8>(v[i]);  // xor 8 inside a 16-lane row
+            else v[i] += __shfl_xor(v[i], m, kWave);
+        }
     }
-    return v;
 }
 
 // Zero `count` words of LDS from `p` with the wavefront (a uniform trip count).
@@ -139,18 +148,29 @@ struct FwdArgs {
     DivN divn;
 };
 
-// LDS words of the forward: per wavefront the state slice h [N*S] (alpha in phase A) and a
-// second array (beta in phase A, the cells' max |h| in phase C), each with a dummy word; then
-// the ages' last-selection table [N+1], the column-sum partials [W][W][S] and two flags per chunk.
-inline int fwd_region(int N, int S, int W) {
+// LDS words of the forward: per wavefront the state slice h [N*S] (alpha in phase A) with a
+// dummy word, and when chunked beta [N*S] with a dummy; then the ages' last-selection table
+// [N+1], the column-sum partials [W][W][S], two flags per chunk and, when chunked, the start
+// state [N*S] staged for phase B.
+inline int fwd_region(int N, int S, int W) {  // a multiple of 4 words: 16-byte aligned slices
     const int ns = N * S + 1;
-    return W > 1 ? 2 * ns : ns + N + 1;
+    return ((W > 1 ? 2 * ns : ns) + 3) & ~3;
 }
 inline size_t fwd_lds_bytes(int N, int S, int W) {
-    return 4 * (size_t(W) * fwd_region(N, S, W) + (N + 1) + size_t(W) * W * S + 2 * W);
+    const size_t h0_stage = W > 1 ? size_t(N) * S : 0;  // the start state, for phase B
+    return 4 * (size_t(W) * fwd_region(N, S, W) + (N + 1) + size_t(W) * W * S + 2 * W + h0_stage);
 }
 
-template <typename IN, typename OUT, typename SLOT, int S, int TB>
+// An LDS word by byte address.
+__device__ __forceinline__ float& lds_at(float* lds, uint32_t byte) {
+    return *reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + byte);
+}
+
+constexpr uint32_t kNoCell = 0xffffffffu;  // no tracked cell
+
+// RES: the whole chunk is one register sub-block (W > 1, Tc <= TB): phase C replays what phase A
+// loaded. Otherwise every phase streams its sub-blocks from memory.
+template <typename IN, typename OUT, typename SLOT, int S, int TB, bool RES>
 __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     using Raw = typename SLOT::Raw;
     constexpr bool kWide = sizeof(Raw) == 8;
@@ -167,18 +187,23 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     const int NS = N * S;
     const bool active = kslot < K;
     float* st = lds + w * a.region;  // alpha, then h: [NS] + a dummy word
-    float* st2 = st + NS + 1;        // beta, then the cells' max |h| over the slice (as bits)
-    uint32_t* cm = reinterpret_cast<uint32_t*>(st2);
+    float* st2 = st + NS + 1;        // beta (chunked only)
+    const uint32_t rb = uint32_t(w * a.region) * 4u;  // byte address of st
+    const uint32_t boff = uint32_t(NS + 1) * 4u;      // st2 - st, bytes
+    const uint32_t dummy = rb + uint32_t(NS) * 4u;    // where padded and idle lanes write
+    const uint32_t x0 = rb + uint32_t(x) * 4u;        // cell 0, this lane's column
     float* shared = lds + W * a.region;
     int* last = reinterpret_cast<int*>(shared);  // [N] + a dummy
     float* part = shared + N + 1;                // [W waves][W chunks][S]
     int* rflag = reinterpret_cast<int*>(part + W * W * S);
     int* rlast = rflag + W;
+    float* h0s = reinterpret_cast<float*>(rlast + W);  // [NS] when chunked
     const int t_begin = w * a.Tc;
     const int t_end = min(T, t_begin + a.Tc);
-    const int nsb = (t_end - t_begin + TB - 1) / TB;
+    const int nsb = RES ? 1 : (t_end - t_begin + TB - 1) / TB;
     const bool track_age = slice == 0 && a.age_T != nullptr;
     const bool want_max = a.h_max != nullptr;
+    const uint32_t qbytes = uint32_t(T) * d * sizeof(OUT);
     const DivN divn = a.divn;
 
     const uint32_t kd = uint32_t(K) * d;
@@ -188,35 +213,32 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     const rsrc_t rc = make_rsrc(static_cast<const Raw*>(a.cells) + b * a.s_row, T * K * sizeof(Raw));
     const rsrc_t rv = make_rsrc(a.valid ? a.valid + b * a.s_row : nullptr, a.valid ? T * K : 0);
     const rsrc_t rr = make_rsrc(a.reset ? a.reset + b * a.r_row : nullptr, a.reset ? T : 0);
-    // outputs: an absent one is a resource of size 0 (its stores are dropped)
-    const rsrc_t rho = make_rsrc(a.h_old ? static_cast<OUT*>(a.h_old) + b * a.o_row : nullptr,
-                                 a.h_old ? row_elems * sizeof(OUT) : 0);
-    const rsrc_t rhs = make_rsrc(a.h_sel ? static_cast<OUT*>(a.h_sel) + b * a.o_row : nullptr,
-                                 a.h_sel ? row_elems * sizeof(OUT) : 0);
-    const uint32_t qbytes = uint32_t(T) * d * sizeof(OUT);
-    const rsrc_t rqa = make_rsrc(a.q_pre ? static_cast<OUT*>(a.q_pre) + b * a.qo_row : nullptr,
-                                 a.q_pre ? qbytes : 0);
-    const rsrc_t rqb = make_rsrc(a.q_post ? static_cast<OUT*>(a.q_post) + b * a.qo_row : nullptr,
-                                 a.q_post ? qbytes : 0);
+    // the outputs as resources, made where phase C starts (an absent output is a resource of
+    // size 0: its stores are dropped)
+    auto out_rsrc = [&](void* p, int64_t row, uint32_t bytes) __attribute__((always_inline)) {
+        OUT* const q = static_cast<OUT*>(p);
+        return make_rsrc(q ? q + b * row : nullptr, q ? bytes : 0u);
+    };
     const uint32_t vy = active ? uint32_t(kslot * d + col) * sizeof(IN) : kOob;
     const uint32_t vo = active ? uint32_t(kslot * d + col) * sizeof(OUT) : kOob;
     const uint32_t vc = active ? uint32_t(kslot) * sizeof(Raw) : kOob;
     const uint32_t vv = active ? uint32_t(kslot) : kOob;
-    const uint32_t vq = kslot == 0 ? uint32_t(col) * sizeof(OUT) : kOob;  // one lane per column
 
     if (track_age)
         for (int n0 = 0; n0 <= N; n0 += kWave * W)
             if (n0 + gl <= N) last[n0 + gl] = -1;
 
-    // the sub-block in registers: (1 - b), b*c and the decoded cell of every position
-    float omb[TB], bcv[TB];
-    int cl[TB];
+    // A sub-block: the raw loads, then per position (1 - b), b*c and the LDS byte address of
+    // the slot's (cell, column) word. Padded and idle lanes get the identity update (1, 0) on
+    // the dummy word, so no step of the loops below tests them.
+    IN yv[TB], gv[TB];
+    int32_t cv[TB];
+    uint8_t vb[TB];
     uint32_t rmask = 0u;
-    auto fetch = [&](int tb0) {
+    float omb[TB], bcv[TB];
+    uint32_t ca[TB];
+    auto fetch = [&](int tb0) __attribute__((always_inline)) {
         const int tl = t_end - 1;
-        IN yv[TB], gv[TB];
-        int32_t cv[TB];
-        uint8_t vb[TB];
 #pragma unroll
         for (int i = 0; i < TB; ++i) {
             const int t = uniform(min(tb0 + i, tl));
@@ -229,21 +251,31 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
         const bool rin = lane < TB && tb0 + lane < t_end;
         const uint8_t r = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
         rmask = static_cast<uint32_t>(ballot(r != 0));
-#pragma unroll
-        for (int i = 0; i < TB; ++i) {
-            const float bg = fast_sigmoid(to_f32(gv[i]));
-            omb[i] = 1.0f - bg;
-            bcv[i] = bg * fast_tanh(to_f32(yv[i]));
-            int c = cv[i];
-            if constexpr (kWide) c = vb[i] ? c : -1;
-            cl[i] = active ? c : -2;
-        }
+    };
+    // returns whether the lane's slot is padded
+    auto prep = [&](int i, bool in_block) __attribute__((always_inline)) -> bool {
+        int c = cv[i];
+        if constexpr (kWide) c = vb[i] ? c : -1;
+        const bool ok = in_block && active && c >= 0;
+        const float bg = fast_sigmoid(to_f32(gv[i]));
+        omb[i] = ok ? 1.0f - bg : 1.0f;
+        bcv[i] = ok ? bg * fast_tanh(to_f32(yv[i])) : 0.0f;
+        ca[i] = ok ? rb + uint32_t(c * S + x) * 4u : dummy;
+        return in_block && active && c < 0;
     };
 
     float q_run = a.q0[b * a.q0_row + col];
     const float* h0_row = a.h0 + b * a.h0_row;
-
-    if (W > 1) {
+    bool pad_lane = false;
+    // The start state for phase B is staged in LDS during phase A: the first kPre elements of
+    // each lane are fetched before the sub-block's loads and written after them (so waiting for
+    // them waits for nothing else), the rest after phase A's first sub-block.
+    constexpr int kPre = 4;
+    float h0v[kPre];
+    auto h0_elem = [&](int e) __attribute__((always_inline)) -> float {
+        return h0_row[int64_t(e / S) * d + slice * S + e % S];
+    };
+    if (RES || W > 1) {
         // phase A: the chunk's per-cell maps, alpha (st) and beta (st2), from the identity
         for (int e0 = 0; e0 < NS; e0 += kWave) {
             const int e = e0 + lane;
@@ -256,54 +288,78 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
         for (int sb = 0; sb < nsb; ++sb) {
             const int tb0 = t_begin + sb * TB;
             const int n = min(TB, t_end - tb0);
+            if (sb == 0) {
+#pragma unroll
+                for (int q = 0; q < kPre; ++q) {
+                    const int e = q * kWave * W + gl;
+                    h0v[q] = h0_elem(min(e, NS - 1));
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
             fetch(tb0);
+            if (sb == 0) {
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int q = 0; q < kPre; ++q) {
+                    const int e = q * kWave * W + gl;
+                    if (e < NS) h0s[e] = h0v[q];
+                }
+                for (int e = kPre * kWave * W + gl; e < NS; e += kWave * W) h0s[e] = h0_elem(e);
+            }
+            any_reset |= rmask != 0u;
+            pad_lane = false;
 #pragma unroll
             for (int i = 0; i < TB; ++i) {
-                if (i < n) {
-                    if ((rmask >> i) & 1u) {  // the state restarts from zero before t
-                        lds_zero(st, NS, lane);
-                        lds_zero(st2, NS, lane);
-                        any_reset = true;
-                    }
-                    const int ci = cl[i];
-                    const int ri = (ci > 0 ? ci : 0) * S + x;
-                    const float al = st[ri], be = st2[ri];
-                    const int wi = ci >= 0 ? ci * S + x : NS;
-                    st[wi] = omb[i] * al;
-                    st2[wi] = omb[i] * be + bcv[i];
+                pad_lane |= prep(i, i < n);  // the loads of position i arrive in order
+                if (rmask != 0u && ((rmask >> i) & 1u)) {  // the state restarts from zero at t
+                    lds_zero(st, NS, lane);
+                    lds_zero(st2, NS, lane);
                 }
+                float& al = lds_at(lds, ca[i]);
+                float& be = lds_at(lds, ca[i] + boff);
+                const float va = al, vbe = be;
+                al = omb[i] * va;
+                be = omb[i] * vbe + bcv[i];
             }
         }
         if (lane == 0) rflag[w] = any_reset ? 1 : 0;
         __syncthreads();
 
-        // phase B: every chunk's start state (into its alpha's place), and its column sums
+        // phase B: every chunk's start state (into its alpha's place), and its column sums.
+        // Chunk by chunk over all of the lane's elements, so each chunk's reads are in flight
+        // together (a chunk's store may alias the next chunk's reads as far as the compiler knows).
         float ps[kMaxChunks];
 #pragma unroll
         for (int j = 0; j < kMaxChunks; ++j) ps[j] = 0.0f;
-        for (int e0 = 0; e0 < NS; e0 += kWave * W) {
-            const int e = e0 + gl;
-            if (e < NS) {
-                float h = h0_row[int64_t(e / S) * d + slice * S + e % S];
+        for (int g0 = 0; g0 < NS; g0 += kWave * W * kPre) {  // groups of kPre elements per lane
+            float h[kPre];
 #pragma unroll
-                for (int j = 0; j < kMaxChunks; ++j) {
-                    if (j < W) {
-                        float* sj = lds + j * a.region;
-                        const float al = sj[e], be = sj[NS + 1 + e];
-                        sj[e] = h;
-                        ps[j] += h;
-                        h = al * h + be;
+            for (int q = 0; q < kPre; ++q) h[q] = h0s[min(g0 + q * kWave * W + gl, NS - 1)];
+#pragma unroll
+            for (int j = 0; j < kMaxChunks; ++j) {
+                if (j < W) {
+                    float* sj = lds + j * a.region;
+                    float al[kPre], be[kPre];
+#pragma unroll
+                    for (int q = 0; q < kPre; ++q) {
+                        const int e = min(g0 + q * kWave * W + gl, NS);  // NS: the dummy
+                        al[q] = sj[e];
+                        be[q] = sj[NS + 1 + e];
+                    }
+#pragma unroll
+                    for (int q = 0; q < kPre; ++q) {  // past the end: the dummy word
+                        const int e = g0 + q * kWave * W + gl;
+                        sj[min(e, NS)] = h[q];
+                        ps[j] += e < NS ? h[q] : 0.0f;
+                        h[q] = al[q] * h[q] + be[q];
                     }
                 }
             }
         }
+        col_sums<S>(ps);  // lanes with equal lane % S hold column x
 #pragma unroll
-        for (int j = 0; j < kMaxChunks; ++j) {
-            if (j < W) {
-                const float v = col_sum<S>(ps[j]);  // lanes with equal lane % S hold column x
-                if (lane < S) part[(w * W + j) * S + lane] = v;
-            }
-        }
+        for (int j = 0; j < kMaxChunks; ++j)
+            if (j < W && lane < S) part[(w * W + j) * S + lane] = ps[j];
         __syncthreads();
         if (w > 0) {
             float cs_w = 0.0f, cs_0 = 0.0f;
@@ -322,102 +378,181 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
             if (e < NS) st[e] = h0_row[int64_t(e / S) * d + slice * S + e % S];
         }
     }
+    if (lane == 0) st[NS] = 0.0f;  // the dummy: idle lanes read it as a zero state
 
-    // phase C: the replay with the outputs
-    uint32_t M = 0u;  // the slice's max |h| (bits), the max over cm
-    if (want_max) {
-        for (int n0 = 0; n0 < N; n0 += kWave) {
-            const int n = n0 + lane;
-            if (n < N) {
-                uint32_t m = 0u;
+    // phase C: the replay with the outputs.
+    // The slice's max |h| (bits, NaN above +inf) is M, held by the tracked cell (cw: its word in
+    // this lane's column, kNoCell when none). A position changes it only when a new value
+    // exceeds it or the tracked cell is written; otherwise M stands.
+    uint32_t M = 0u, cw = kNoCell;
+    auto rescan = [&]() __attribute__((always_inline)) {  // the max and a cell holding it, over the whole slice
+        constexpr int U = 8;  // reads in flight per lane (the dummy word NS reads as zero)
+        uint32_t best = 0u;
+        int bi = 0;
+        if (NS % (kWave * 4) == 0) {  // four words per lane and read
+            for (int e0 = 0; e0 < NS; e0 += kWave * 4 * U) {
+                float4 v[U];
 #pragma unroll
-                for (int xx = 0; xx < S; ++xx) m = umax(m, abs_bits(st[n * S + xx]));
-                cm[n] = m;
-                M = umax(M, m);
+                for (int u = 0; u < U; ++u)
+                    v[u] = *reinterpret_cast<const float4*>(st + min(e0 + (u * kWave + lane) * 4, NS - 4));
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int e = e0 + (u * kWave + lane) * 4;
+                    const float c4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const uint32_t a = e < NS ? abs_bits(c4[c]) : 0u;
+                        if (a > best) {
+                            best = a;
+                            bi = e + c;
+                        }
+                    }
+                }
+            }
+        } else {
+            for (int e0 = 0; e0 < NS; e0 += kWave * U) {
+                uint32_t v[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) v[u] = abs_bits(st[min(e0 + u * kWave + lane, NS)]);
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    if (v[u] > best) {
+                        best = v[u];
+                        bi = e0 + u * kWave + lane;
+                    }
+                }
             }
         }
-        M = wave_max_from_groups<1>(M);
-    }
+        M = wave_max_from_groups<1>(best);
+        const uint64_t who = ballot(best == M);
+        const int src = __builtin_ctzll(who);
+        const int e_max = __builtin_amdgcn_readlane(bi, src);
+        cw = M == 0u ? kNoCell : rb + uint32_t((e_max / S) * S + x) * 4u;
+    };
+    auto raise = [&](uint32_t av, uint32_t cai) __attribute__((always_inline)) {  // new values above M, none on the tracked cell
+        const uint32_t m = wave_max_from_groups<1>(av > M ? av : 0u);
+        const uint64_t who = ballot(av == m);
+        const int src = __builtin_ctzll(who);
+        const uint32_t cell_x = static_cast<uint32_t>(__builtin_amdgcn_readlane(
+                                    static_cast<int>(cai), src)) - uint32_t(src % S) * 4u;
+        M = m;
+        cw = cell_x + uint32_t(x) * 4u;
+    };
+    if (want_max) rescan();
+
     int lr = -1;  // the chunk's last reset
-    for (int sb = 0; sb < nsb; ++sb) {
-        const int tb0 = t_begin + sb * TB;
-        const int n = min(TB, t_end - tb0);
-        if (W == 1 || nsb > 1) fetch(tb0);
+    const rsrc_t rho = out_rsrc(a.h_old, a.o_row, row_elems * sizeof(OUT));
+    const rsrc_t rhs = out_rsrc(a.h_sel, a.o_row, row_elems * sizeof(OUT));
+    const rsrc_t rqa = out_rsrc(a.q_pre, a.qo_row, qbytes);
+    const rsrc_t rqb = out_rsrc(a.q_post, a.qo_row, qbytes);
+    // One sub-block of phase C: the steps, specialised for a full block without resets or
+    // padded slots (the common case) and general otherwise; then the summaries, the slice maxima
+    // and the cells' last selections.
+    auto block = [&](int tb0, int n) __attribute__((always_inline)) {
+        const bool pad = ballot(pad_lane) != 0u;
         float delta[TB];
         uint32_t hmv = 0u;
+        auto steps = [&](auto full_c, auto reset_c, auto pad_c) __attribute__((always_inline)) {
+            constexpr bool kFull = decltype(full_c)::value;
+            constexpr bool kReset = decltype(reset_c)::value;
+            constexpr bool kPad = decltype(pad_c)::value;
 #pragma unroll
-        for (int i = 0; i < TB; ++i) {
-            delta[i] = 0.0f;
-            if (i < n) {
-                const int t = tb0 + i;
-                if ((rmask >> i) & 1u) {  // a document boundary: h, q (and the ages) restart at zero
-                    lds_zero(st, NS, lane);
-                    if (want_max) {
-                        lds_zero(st2, N, lane);
+            for (int i = 0; i < TB; ++i) {
+                delta[i] = 0.0f;
+                if (kFull || i < n) {
+                    const int t = tb0 + i;
+                    if (kReset && ((rmask >> i) & 1u)) {  // a boundary: h, q and ages restart
+                        lds_zero(st, NS, lane);
                         M = 0u;
+                        cw = kNoCell;
+                        lr = t;
                     }
-                    lr = t;
-                }
-                const int ci = cl[i];
-                const bool ok = ci >= 0;
-                const float hold = st[(ci > 0 ? ci : 0) * S + x];
-                const uint32_t mo = (want_max && ok) ? cm[ci] : 0u;
-                const float hnew = omb[i] * hold + bcv[i];
-                st[ok ? ci * S + x : NS] = hnew;
-                const uint32_t so = uint32_t(t) * kd * sizeof(OUT);
-                bstore_f32<OUT>(hold, rho, vo, so);
-                float hs = hnew;
-                if (ballot(ci == -1)) {  // a padded slot shows cell 0 after the update
-                    const float c0 = st[x];
-                    hs = ci == -1 ? c0 : hnew;
-                }
-                bstore_f32<OUT>(hs, rhs, vo, so);
-                delta[i] = ok ? hnew - hold : 0.0f;
-                if (want_max) {
-                    // the cell's max over the slice's columns replaces its old one; the slice max
-                    // rises with it, and is rescanned only when the cell that held it shrank
-                    const uint32_t mn = group_max<S>(abs_bits(hnew));
-                    if (ok && x == 0) cm[ci] = mn;
-                    const bool drop = ok && mo == M && mn < M;
-                    M = umax(M, wave_max_from_groups<S>(ok ? mn : 0u));
-                    if (ballot(drop)) {
-                        uint32_t m = 0u;
-                        for (int n0 = 0; n0 < N; n0 += kWave)
-                            if (n0 + lane < N) m = umax(m, cm[n0 + lane]);
-                        M = wave_max_from_groups<1>(m);
+                    const bool ok = !kPad || ca[i] != dummy;
+                    const float hold = lds_at(lds, kPad && !ok ? x0 : ca[i]);
+                    const float hnew = omb[i] * hold + bcv[i];
+                    lds_at(lds, ca[i]) = kPad && !ok ? 0.0f : hnew;
+                    const uint32_t so = uint32_t(t) * kd * sizeof(OUT);
+                    bstore_f32<OUT>(hold, rho, vo, so);
+                    float hs = hnew;
+                    if (kPad && ballot(active && !ok)) {  // a padded slot shows cell 0 after
+                        const float c0 = lds_at(lds, x0);
+                        hs = ok ? hnew : c0;
                     }
-                    hmv = lane == i ? M : hmv;
+                    bstore_f32<OUT>(hs, rhs, vo, so);
+                    delta[i] = kPad && !ok ? 0.0f : hnew - hold;
+                    if (want_max) {
+                        const uint32_t av = kPad && !ok ? 0u : abs_bits(hnew);
+                        if (ballot(av > M || ca[i] == cw)) {
+                            if (ballot(ca[i] == cw)) rescan();  // the tracked cell changed
+                            else raise(av, ca[i]);
+                        }
+                        hmv = lane == i ? M : hmv;
+                    }
                 }
-                if (track_age && ok && x == 0) atomicMax(&last[ci], t);
             }
-        }
-        // the summary before and after each position: q' = q + sum_k (h' - h)[k] / N
+        };
+        if (n == TB && rmask == 0u && !pad) steps(std::true_type{}, std::false_type{}, std::false_type{});
+        else steps(std::false_type{}, std::true_type{}, std::true_type{});
+
+        // the summary before and after each position: q' = q + sum_k (h' - h)[k] / N, written by
+        // one lane per column
+        col_sums<S>(delta);
+        auto summaries = [&](auto pow2_c, auto reset_c) __attribute__((always_inline)) {
+            constexpr bool kPow2 = decltype(pow2_c)::value;
+            constexpr bool kReset = decltype(reset_c)::value;
+            const uint32_t qstep = uint32_t(d) * sizeof(OUT);
+            uint32_t vqt = uint32_t(col) * sizeof(OUT) + uint32_t(tb0) * qstep;
 #pragma unroll
-        for (int i = 0; i < TB; ++i) {
-            const float s = col_sum<S>(delta[i]);
-            if (i < n) {
-                if ((rmask >> i) & 1u) q_run = 0.0f;
-                const uint32_t sq = uint32_t(tb0 + i) * d * sizeof(OUT);
-                bstore_f32<OUT>(q_run, rqa, vq, sq);
-                q_run = q_run + divn(s);
-                bstore_f32<OUT>(q_run, rqb, vq, sq);
+            for (int i = 0; i < TB; ++i, vqt += qstep) {
+                if (i < n) {
+                    if (kReset && ((rmask >> i) & 1u)) q_run = 0.0f;
+                    bstore_f32<OUT>(q_run, rqa, vqt, 0u);
+                    q_run = q_run + (kPow2 ? delta[i] * divn.inv : delta[i] / divn.n);
+                    bstore_f32<OUT>(q_run, rqb, vqt, 0u);
+                }
             }
+        };
+        if (kslot == 0) {
+            if (divn.pow2 && rmask == 0u) summaries(std::true_type{}, std::false_type{});
+            else if (divn.pow2) summaries(std::true_type{}, std::true_type{});
+            else summaries(std::false_type{}, std::true_type{});
         }
         if (want_max && lane < n)  // lane i sends position tb0 + i's slice max
-            atomicMax(reinterpret_cast<unsigned int*>(a.h_max + b * a.hm_row) + (tb0 + lane), hmv);
+            atomicMax(reinterpret_cast<unsigned int*>(a.h_max + b * a.hm_row) + (tb0 + lane),
+                      hmv);
+        if (track_age && x == 0) {  // the cells' last selection (idle and padded: the dummy N)
+#pragma unroll
+            for (int i = 0; i < TB; ++i)
+                if (i < n) atomicMax(&last[(ca[i] - rb) / (4u * S)], tb0 + i);
+        }
+    };
+    if constexpr (RES) {
+        block(t_begin, t_end - t_begin);  // the chunk is in registers since phase A
+    } else {
+        for (int sb = 0; sb < nsb; ++sb) {
+            const int tb0 = t_begin + sb * TB;
+            const int n = min(TB, t_end - tb0);
+            fetch(tb0);
+            pad_lane = false;
+#pragma unroll
+            for (int i = 0; i < TB; ++i) pad_lane |= prep(i, i < n);
+            block(tb0, n);
+        }
     }
 
     // the end state (zeroed when the caller's next record resets this row)
-    const bool clear = a.clear ? a.clear[b * a.c_row] != 0 : false;
+    const uint8_t* const clear_p = a.clear;
+    const bool clear = clear_p ? clear_p[b * a.c_row] != 0 : false;
     if (w == W - 1) {
-        if (a.h_T) {
-            float* hT_row = a.h_T + b * a.hT_row;
+        if (float* const hT = a.h_T) {
+            float* hT_row = hT + b * a.hT_row;
             for (int e0 = 0; e0 < NS; e0 += kWave) {
                 const int e = e0 + lane;
                 if (e < NS) hT_row[int64_t(e / S) * d + slice * S + e % S] = clear ? 0.0f : st[e];
             }
         }
-        if (a.q_T && kslot == 0) a.q_T[b * a.qT_row + col] = clear ? 0.0f : q_run;
+        float* const qT = a.q_T;
+        if (qT && kslot == 0) qT[b * a.qT_row + col] = clear ? 0.0f : q_run;
     }
     if (track_age) {
         if (lane == 0) rlast[w] = lr;
@@ -437,8 +572,8 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
                 ageT_row[n] = clear ? 0 : age;
             }
         }
-        if (a.pos_T && gl == 0)
-            a.pos_T[b] = last_reset >= 0 ? int64_t(T - last_reset) : a.pos0[b] + T;
+        int64_t* const posT = a.pos_T;
+        if (posT && gl == 0) posT[b] = last_reset >= 0 ? int64_t(T - last_reset) : a.pos0[b] + T;
     }
 }
 
@@ -471,18 +606,22 @@ struct BwdArgs {
     DivN divn;
 };
 
-// LDS words of the backward: per wavefront the cotangent slice A [N*S] (mu in phase A) and, when
-// chunked, nu [N*S], each with a dummy word; then the chunks' summary-cotangent sums [W][S]
-// (fp64) and reset flags [W].
-inline int bwd_region(int N, int S, int W) {
+// LDS words of the backward: per wavefront the cotangent slice A [N*S] (mu in phase A) with a
+// dummy word, and when chunked nu [N*S] with a dummy; then the chunks' summary-cotangent sums
+// [W][S] (fp64), reset flags [W], per wavefront the shares of a sub-block [S][TB] and, when
+// chunked, the end cotangent [N*S] staged for phase B.
+inline int bwd_region(int N, int S, int W) {  // a multiple of 4 words
     const int ns = N * S + 1;
-    return W > 1 ? 2 * ns : ns;
+    return ((W > 1 ? 2 * ns : ns) + 3) & ~3;
 }
 inline size_t bwd_lds_bytes(int N, int S, int W) {
-    return 4 * (size_t(W) * bwd_region(N, S, W) + 2 * size_t(W) * S + W);
+    const size_t dh_stage = W > 1 ? size_t(N) * S : 0;  // the end cotangent, for phase B
+    return 4 * (size_t(W) * bwd_region(N, S, W) + 2 * size_t(W) * S + W + size_t(W) * S * kResTB +
+                dh_stage) + 8;
 }
 
-template <typename IN, typename SLOT, bool ACT, int S, int TB>
+// RES: as the forward's (the whole chunk is one register sub-block, W > 1).
+template <typename IN, typename SLOT, bool ACT, int S, int TB, bool RES>
 __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     using Raw = typename SLOT::Raw;
     constexpr bool kWide = sizeof(Raw) == 8;
@@ -500,13 +639,18 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     const bool active = kslot < K;
     float* st = lds + w * a.region;  // mu, then A: [NS] + a dummy word
     float* st2 = st + NS + 1;        // nu (chunked only)
-    // [W][S]: the chunks' summary-cotangent sums (the region is an even number of words, so
-    // this is 8-byte aligned); [W]: whether the chunk resets R
-    double* rl = reinterpret_cast<double*>(lds + W * a.region);
+    const uint32_t rb = uint32_t(w * a.region) * 4u;
+    const uint32_t boff = uint32_t(NS + 1) * 4u;
+    const uint32_t dummy = rb + uint32_t(NS) * 4u;
+    // [W][S]: the chunks' summary-cotangent sums, 8-byte aligned; [W]: whether a chunk resets R
+    const uint32_t rl_word = (uint32_t(W * a.region) + 1u) & ~1u;
+    double* rl = reinterpret_cast<double*>(lds + rl_word);
     int* rf = reinterpret_cast<int*>(rl + W * S);
+    float* shl = reinterpret_cast<float*>(rf + W) + w * S * TB + x * TB;  // this column's shares
+    float* dhs = reinterpret_cast<float*>(rf + W) + W * S * kResTB;       // [NS] when chunked
     const int t_begin = w * a.Tc;
     const int t_end = min(T, t_begin + a.Tc);
-    const int nsb = (t_end - t_begin + TB - 1) / TB;
+    const int nsb = RES ? 1 : (t_end - t_begin + TB - 1) / TB;
     const DivN divn = a.divn;
 
     const uint32_t kd = uint32_t(K) * d;
@@ -517,8 +661,6 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     const rsrc_t rho = make_rsrc(static_cast<const IN*>(a.h_old) + base, row_bytes);
     const rsrc_t rds = make_rsrc(a.dsel ? static_cast<const IN*>(a.dsel) + base : nullptr,
                                  a.dsel ? row_bytes : 0);
-    const rsrc_t rdy = make_rsrc(static_cast<IN*>(a.dy) + base, row_bytes);
-    const rsrc_t rdg = make_rsrc(static_cast<IN*>(a.dg) + base, row_bytes);
     const rsrc_t rc = make_rsrc(static_cast<const Raw*>(a.cells) + b * a.s_row, T * K * sizeof(Raw));
     const rsrc_t rv = make_rsrc(a.valid ? a.valid + b * a.s_row : nullptr, a.valid ? T * K : 0);
     const rsrc_t rr = make_rsrc(a.reset + b * a.r_row, T);
@@ -532,10 +674,13 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     const uint32_t vv = active ? uint32_t(kslot) : kOob;
     const uint32_t vq = uint32_t(col) * sizeof(IN);  // every lane reads its column's cotangent
 
-    // the summary cotangents of a sub-block and its reset mask
+    // raw loads of a sub-block
     float qa[TB], qb[TB];
+    IN gv[TB], dv[TB], yv[TB], hv[TB];
+    int32_t cv[TB];
+    uint8_t vb[TB];
     uint32_t rmask = 0u;
-    auto fetch_q = [&](int tb0) {
+    auto fetch_q = [&](int tb0) __attribute__((always_inline)) {  // the summary cotangents and the reset mask
         const int tl = t_end - 1;
 #pragma unroll
         for (int i = 0; i < TB; ++i) {
@@ -547,17 +692,94 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
         const uint8_t r = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
         rmask = static_cast<uint32_t>(ballot(r != 0));
     };
+    auto fetch_a = [&](int tb0) __attribute__((always_inline)) {  // the gate, the selection cotangent and the decisions
+        const int tl = t_end - 1;
+#pragma unroll
+        for (int i = 0; i < TB; ++i) {
+            const int t = uniform(min(tb0 + i, tl));
+            const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
+            gv[i] = bload<IN>(rg, vy, sy);
+            dv[i] = bload<IN>(rds, vy, sy);
+            cv[i] = bload<int32_t>(rc, vc, uint32_t(t) * K * sizeof(Raw));
+            if constexpr (kWide) vb[i] = bload<uint8_t>(rv, vv, uint32_t(t) * K);
+        }
+    };
+    auto fetch_c = [&](int tb0) __attribute__((always_inline)) {  // the candidate and the gathered old state
+        const int tl = t_end - 1;
+#pragma unroll
+        for (int i = 0; i < TB; ++i) {
+            const uint32_t sy = uint32_t(uniform(min(tb0 + i, tl))) * kd * sizeof(IN);
+            yv[i] = bload<IN>(ry, vy, sy);
+            hv[i] = bload<IN>(rho, vy, sy);
+        }
+    };
 
     // The summary cotangent R is a running sum of 2T cotangents; it is accumulated in fp64 (its
     // chunked sums would otherwise round differently from a sequential fp32 sum by about
     // sqrt(2T) ulps of its largest partial), and every position's share R/N is rounded to fp32.
+    float sh[TB];
+    auto shares = [&](int n, double& R) __attribute__((always_inline)) {  // latest position first, through the resets
+        const double inv = double(divn.inv), nf = double(divn.n);
+        auto run = [&](auto pow2_c) __attribute__((always_inline)) {
+            constexpr bool kPow2 = decltype(pow2_c)::value;
+#pragma unroll
+            for (int i = TB - 1; i >= 0; --i) {
+                sh[i] = 0.0f;
+                if (i < n) {
+                    R += double(qb[i]);
+                    sh[i] = static_cast<float>(kPow2 ? R * inv : R / nf);
+                    R += double(qa[i]);
+                    if ((rmask >> i) & 1u) R = 0.0;
+                }
+            }
+        };
+        if (divn.pow2) run(std::true_type{});
+        else run(std::false_type{});
+    };
+    // per position: (1 - b), the selection cotangent and the LDS byte address of the slot's word.
+    // Padded and idle lanes get the identity update (1, no cotangent) on the dummy word.
+    float omb[TB], dsv[TB];
+    uint32_t ca[TB];
+    auto prep = [&](int i, bool in_block) __attribute__((always_inline)) -> bool {
+        int c = cv[i];
+        if constexpr (kWide) c = vb[i] ? c : -1;
+        const bool ok = in_block && active && c >= 0;
+        const float bg = ACT ? fast_sigmoid(to_f32(gv[i])) : to_f32(gv[i]);
+        omb[i] = ok ? 1.0f - bg : 1.0f;
+        dsv[i] = ok ? to_f32(dv[i]) : 0.0f;
+        ca[i] = ok ? rb + uint32_t(c * S + x) * 4u : dummy;
+        return in_block && active && c < 0;
+    };
+    auto keep_shares = [&]() __attribute__((always_inline)) {  // for phase C, from LDS
+        if (kslot == 0) {
+#pragma unroll
+            for (int i = 0; i < TB; ++i) shl[i] = sh[i];
+        }
+    };
+
+    // The end cotangent for phase B is staged in LDS during the pre-pass (the first kPre elements
+    // of each lane fetched before the pre-pass's loads and written after them).
+    const float* dhT_row = a.dh_T ? a.dh_T + int64_t(b) * N * d : nullptr;
+    constexpr int kPre = 4;
+    auto dh_elem = [&](int e) __attribute__((always_inline)) -> float {
+        return dhT_row ? dhT_row[int64_t(e / S) * d + slice * S + e % S] : 0.0f;
+    };
+
     // R at the chunk's end (its later side): the end-state cotangent, then the later chunks'
     double R_in = a.dq_T ? double(a.dq_T[int64_t(b) * d + col]) : 0.0;
     double R_out = 0.0;  // R after the chunk (its position t_begin)
-    if (W > 1) {
-        // pre-pass: each chunk's own sum (restarted at its resets, processed latest first)
+    bool pad_lane = false;
+    if (RES || W > 1) {
+        // pre-pass: each chunk's own sum (restarted at its resets, latest position first)
         double Rl = 0.0;
         bool hasr = false;
+        float dhv[kPre];
+#pragma unroll
+        for (int q = 0; q < kPre; ++q) {
+            const int e = q * kWave * W + gl;
+            dhv[q] = dh_elem(min(e, NS - 1));
+        }
+        __builtin_amdgcn_sched_barrier(0);
         for (int sb = nsb - 1; sb >= 0; --sb) {
             const int tb0 = t_begin + sb * TB;
             const int n = min(TB, t_end - tb0);
@@ -576,77 +798,13 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
         }
         if (kslot == 0) rl[w * S + x] = Rl;
         if (lane == 0) rf[w] = hasr ? 1 : 0;
-        __syncthreads();
-        for (int j = W - 1; j > w; --j) R_in = (rf[j] ? 0.0 : R_in) + rl[j * S + x];
-        R_out = (hasr ? 0.0 : R_in) + Rl;
-    }
-
-    // the sub-block in registers: (1 - b), the A update's constant term, dsel + share, and the
-    // output factors dc = p1 g, db = p2 g (activation derivatives folded in)
-    float omb[TB], e2[TB], e3[TB], p1[TB], p2[TB];
-    int cl[TB];
-    // positions' shares and A-update terms from the running R (latest position first)
-    auto fetch_a = [&](int tb0, int n, double& R) {
-        const int tl = t_end - 1;
-        IN gv[TB], dv[TB];
-        int32_t cv[TB];
-        uint8_t vb[TB];
 #pragma unroll
-        for (int i = 0; i < TB; ++i) {
-            const int t = uniform(min(tb0 + i, tl));
-            const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
-            gv[i] = bload<IN>(rg, vy, sy);
-            dv[i] = bload<IN>(rds, vy, sy);
-            cv[i] = bload<int32_t>(rc, vc, uint32_t(t) * K * sizeof(Raw));
-            if constexpr (kWide) vb[i] = bload<uint8_t>(rv, vv, uint32_t(t) * K);
+        for (int q = 0; q < kPre; ++q) {
+            const int e = q * kWave * W + gl;
+            if (e < NS) dhs[e] = dhv[q];
         }
-        fetch_q(tb0);
-#pragma unroll
-        for (int i = TB - 1; i >= 0; --i) {
-            float share = 0.0f;
-            if (i < n) {
-                R += double(qb[i]);
-                share = static_cast<float>(divn(R));
-                R += double(qa[i]);
-                if ((rmask >> i) & 1u) R = 0.0;
-            }
-            const float bg = ACT ? fast_sigmoid(to_f32(gv[i])) : to_f32(gv[i]);
-            const float ds = to_f32(dv[i]);
-            omb[i] = 1.0f - bg;
-            e2[i] = omb[i] * ds - bg * share;
-            e3[i] = ds + share;
-            p1[i] = bg;  // the gate, until fetch_c folds the candidate in
-            int c = cv[i];
-            if constexpr (kWide) c = vb[i] ? c : -1;
-            cl[i] = active ? c : -2;
-        }
-    };
-    auto fetch_c = [&](int tb0) {
-        const int tl = t_end - 1;
-        IN yv[TB], hv[TB];
-#pragma unroll
-        for (int i = 0; i < TB; ++i) {
-            const uint32_t sy = uint32_t(uniform(min(tb0 + i, tl))) * kd * sizeof(IN);
-            yv[i] = bload<IN>(ry, vy, sy);
-            hv[i] = bload<IN>(rho, vy, sy);
-        }
-#pragma unroll
-        for (int i = 0; i < TB; ++i) {
-            const float bg = p1[i];
-            const float c = ACT ? fast_tanh(to_f32(yv[i])) : to_f32(yv[i]);
-            const float diff = c - to_f32(hv[i]);
-            if constexpr (ACT) {
-                p1[i] = bg * (1.0f - c * c);         // tanh'
-                p2[i] = diff * (omb[i] * bg);        // sigmoid'
-            } else {
-                p2[i] = diff;
-            }
-        }
-    };
-
-    double R = R_in;
-    if (W > 1) {
-        // phase A: the chunk's per-cell maps A_before = mu A_after + nu, latest position first
+        for (int e = kPre * kWave * W + gl; e < NS; e += kWave * W) dhs[e] = dh_elem(e);
+        // phase A: the chunk's per-cell maps A_before = mu A_after + nu, from the identity
         for (int e0 = 0; e0 < NS; e0 += kWave) {
             const int e = e0 + lane;
             if (e < NS) {
@@ -654,87 +812,146 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                 st2[e] = 0.0f;
             }
         }
+        __syncthreads();
+        for (int j = W - 1; j > w; --j) R_in = (rf[j] ? 0.0 : R_in) + rl[j * S + x];
+        R_out = (hasr ? 0.0 : R_in) + Rl;
+        double R = R_in;
         for (int sb = nsb - 1; sb >= 0; --sb) {
             const int tb0 = t_begin + sb * TB;
             const int n = min(TB, t_end - tb0);
-            fetch_a(tb0, n, R);
+            if (!RES) fetch_q(tb0);
+            fetch_a(tb0);
+            shares(n, R);
+            pad_lane = false;
 #pragma unroll
             for (int i = TB - 1; i >= 0; --i) {
-                if (i < n) {
-                    const int ci = cl[i];
-                    const int ri = (ci > 0 ? ci : 0) * S + x;
-                    const float mu = st[ri], nu = st2[ri];
-                    const int wi = ci >= 0 ? ci * S + x : NS;
-                    st[wi] = omb[i] * mu;
-                    st2[wi] = omb[i] * nu + e2[i];
-                    if ((rmask >> i) & 1u) {  // nothing before the boundary reaches past it
-                        lds_zero(st, NS, lane);
-                        lds_zero(st2, NS, lane);
-                    }
+                pad_lane |= prep(i, i < n);  // the loads of position i arrive in order
+                float& mu = lds_at(lds, ca[i]);
+                float& nu = lds_at(lds, ca[i] + boff);
+                const float vm = mu, vn = nu;
+                mu = omb[i] * vm;
+                nu = omb[i] * (vn + dsv[i]) - (1.0f - omb[i]) * sh[i];
+                if (rmask != 0u && ((rmask >> i) & 1u)) {  // nothing before it reaches past t
+                    lds_zero(st, NS, lane);
+                    lds_zero(st2, NS, lane);
                 }
             }
         }
+        if (RES) {  // the replay's own inputs, in flight during phase B (not earlier: registers)
+            keep_shares();
+            __builtin_amdgcn_sched_barrier(0);
+            fetch_c(t_begin);
+        }
         __syncthreads();
-        // phase B: every chunk's end cotangent (into its mu's place), latest chunk first
-        const float* dhT_row = a.dh_T ? a.dh_T + int64_t(b) * N * d : nullptr;
-        for (int e0 = 0; e0 < NS; e0 += kWave * W) {
-            const int e = e0 + gl;
-            if (e < NS) {
-                float A = dhT_row ? dhT_row[int64_t(e / S) * d + slice * S + e % S] : 0.0f;
+        // phase B: every chunk's end cotangent (into its mu's place), latest chunk first, chunk
+        // by chunk over all of the lane's elements
+        for (int g0 = 0; g0 < NS; g0 += kWave * W * kPre) {  // groups of kPre elements per lane
+            float A[kPre];
 #pragma unroll
-                for (int j = kMaxChunks - 1; j >= 0; --j) {
-                    if (j < W) {
-                        float* sj = lds + j * a.region;
-                        const float mu = sj[e], nu = sj[NS + 1 + e];
-                        sj[e] = A;
-                        A = mu * A + nu;
+            for (int q = 0; q < kPre; ++q) A[q] = dhs[min(g0 + q * kWave * W + gl, NS - 1)];
+#pragma unroll
+            for (int j = kMaxChunks - 1; j >= 0; --j) {
+                if (j < W) {
+                    float* sj = lds + j * a.region;
+                    float mu[kPre], nu[kPre];
+#pragma unroll
+                    for (int q = 0; q < kPre; ++q) {
+                        const int e = min(g0 + q * kWave * W + gl, NS);  // NS: the dummy
+                        mu[q] = sj[e];
+                        nu[q] = sj[NS + 1 + e];
+                    }
+#pragma unroll
+                    for (int q = 0; q < kPre; ++q) {  // past the end: the dummy word
+                        const int e = g0 + q * kWave * W + gl;
+                        sj[min(e, NS)] = A[q];
+                        A[q] = mu[q] * A[q] + nu[q];
                     }
                 }
             }
         }
         __syncthreads();
-        R = R_in;
     } else {
-        const float* dhT_row = a.dh_T ? a.dh_T + int64_t(b) * N * d : nullptr;
         for (int e0 = 0; e0 < NS; e0 += kWave) {
             const int e = e0 + lane;
-            if (e < NS) st[e] = dhT_row ? dhT_row[int64_t(e / S) * d + slice * S + e % S] : 0.0f;
+            if (e < NS) st[e] = dh_elem(e);
         }
     }
+    if (lane == 0) st[NS] = 0.0f;  // the dummy: idle lanes read it as a zero cotangent
 
     // phase C: the replay with the outputs, latest position first
-    for (int sb = nsb - 1; sb >= 0; --sb) {
-        const int tb0 = t_begin + sb * TB;
-        const int n = min(TB, t_end - tb0);
-        if (W == 1 || nsb > 1) fetch_a(tb0, n, R);
-        fetch_c(tb0);
+    const rsrc_t rdy = make_rsrc(static_cast<IN*>(a.dy) + base, row_bytes);
+    const rsrc_t rdg = make_rsrc(static_cast<IN*>(a.dg) + base, row_bytes);
+    auto block = [&](int tb0, int n) __attribute__((always_inline)) {
+        const bool pad = ballot(pad_lane) != 0u;
+        auto steps = [&](auto full_c, auto reset_c, auto pad_c) __attribute__((always_inline)) {
+            constexpr bool kFull = decltype(full_c)::value;
+            constexpr bool kReset = decltype(reset_c)::value;
+            constexpr bool kPad = decltype(pad_c)::value;
 #pragma unroll
-        for (int i = TB - 1; i >= 0; --i) {
-            if (i < n) {
-                const int ci = cl[i];
-                const bool ok = ci >= 0;
-                const float aold = st[(ci > 0 ? ci : 0) * S + x];
-                const float gg = aold + e3[i];
-                st[ok ? ci * S + x : NS] = omb[i] * aold + e2[i];
-                const uint32_t so = uint32_t(tb0 + i) * kd * sizeof(IN);
-                bstore_f32<IN>(ok ? p1[i] * gg : 0.0f, rdy, vy, so);
-                bstore_f32<IN>(ok ? p2[i] * gg : 0.0f, rdg, vy, so);
-                if ((rmask >> i) & 1u) lds_zero(st, NS, lane);
+            for (int i = TB - 1; i >= 0; --i) {
+                if (kFull || i < n) {
+                    float& A = lds_at(lds, ca[i]);
+                    const float share = shl[i];
+                    const float carried = A + dsv[i];
+                    const float gg = carried + share;
+                    const float bg = 1.0f - omb[i];
+                    A = omb[i] * carried - bg * share;
+                    const float c = ACT ? fast_tanh(to_f32(yv[i])) : to_f32(yv[i]);
+                    const float diff = c - to_f32(hv[i]);
+                    float dc, db;
+                    if constexpr (ACT) {
+                        dc = bg * (1.0f - c * c) * gg;   // tanh'
+                        db = diff * (omb[i] * bg) * gg;  // sigmoid'
+                    } else {
+                        dc = bg * gg;
+                        db = diff * gg;
+                    }
+                    if (kPad) {  // exact zeros on padded slots, whatever their inputs hold
+                        const bool ok = ca[i] != dummy;
+                        dc = ok ? dc : 0.0f;
+                        db = ok ? db : 0.0f;
+                    }
+                    const uint32_t so = uint32_t(tb0 + i) * kd * sizeof(IN);
+                    bstore_f32<IN>(dc, rdy, vy, so);
+                    bstore_f32<IN>(db, rdg, vy, so);
+                    if (kReset && ((rmask >> i) & 1u)) lds_zero(st, NS, lane);
+                }
             }
+        };
+        if (n == TB && rmask == 0u && !pad) steps(std::true_type{}, std::false_type{}, std::false_type{});
+        else steps(std::false_type{}, std::true_type{}, std::true_type{});
+    };
+    double R = R_in;
+    if constexpr (RES) {
+        block(t_begin, t_end - t_begin);  // the chunk is in registers since phase A
+    } else {
+        for (int sb = nsb - 1; sb >= 0; --sb) {
+            const int tb0 = t_begin + sb * TB;
+            const int n = min(TB, t_end - tb0);
+            fetch_q(tb0);
+            fetch_a(tb0);
+            shares(n, R);
+            keep_shares();
+            pad_lane = false;
+#pragma unroll
+            for (int i = TB - 1; i >= 0; --i) pad_lane |= prep(i, i < n);
+            fetch_c(tb0);
+            block(tb0, n);
         }
     }
-    if (W == 1) R_out = R;
+    if (!RES && W == 1) R_out = R;
 
     // the carried-state gradient: A and R after position 0
     if (w == 0) {
-        if (a.dh0) {
-            float* dh0_row = a.dh0 + int64_t(b) * N * d;
+        if (float* const dh0 = a.dh0) {
+            float* dh0_row = dh0 + int64_t(b) * N * d;
             for (int e0 = 0; e0 < NS; e0 += kWave) {
                 const int e = e0 + lane;
                 if (e < NS) dh0_row[int64_t(e / S) * d + slice * S + e % S] = st[e];
             }
         }
-        if (a.dq0 && kslot == 0) a.dq0[int64_t(b) * d + col] = static_cast<float>(R_out);
+        float* const dq0 = a.dq0;
+        if (dq0 && kslot == 0) dq0[int64_t(b) * d + col] = static_cast<float>(R_out);
     }
 }
 
@@ -858,8 +1075,8 @@ hipError_t allow_lds(K kernel, size_t lds) {
 
 template <typename IN, typename OUT, typename SLOT, int S>
 hipError_t launch_fwd_s(const FwdArgs& a, size_t lds, hipStream_t st) {
-    constexpr int TB = sizeof(typename SLOT::Raw) == 8 ? 16 : 32;
-    auto k = fwd_chunk<IN, OUT, SLOT, S, TB>;
+    auto k = (a.W > 1 && a.Tc <= kResTB) ? fwd_chunk<IN, OUT, SLOT, S, kResTB, true>
+                                         : fwd_chunk<IN, OUT, SLOT, S, kStreamTB, false>;
     hipError_t e = allow_lds(k, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k, sweep_grid(a.B, a.d / S), dim3(kWave * a.W), lds, st, a);
@@ -880,8 +1097,8 @@ hipError_t launch_fwd(const FwdArgs& a, int S, size_t lds, hipStream_t st) {
 
 template <typename IN, typename SLOT, bool ACT, int S>
 hipError_t launch_bwd_s(const BwdArgs& a, size_t lds, hipStream_t st) {
-    constexpr int TB = 16;
-    auto k = bwd_chunk<IN, SLOT, ACT, S, TB>;
+    auto k = (a.W > 1 && a.Tc <= kResTB) ? bwd_chunk<IN, SLOT, ACT, S, kResTB, true>
+                                         : bwd_chunk<IN, SLOT, ACT, S, kStreamTB, false>;
     hipError_t e = allow_lds(k, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k, sweep_grid(a.B, a.d / S), dim3(kWave * a.W), lds, st, a);

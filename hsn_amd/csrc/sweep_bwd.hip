@@ -72,7 +72,7 @@ extern "C" int hsn_win_backward(const void* y, const void* gate_pre, const void*
     HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
                 HSN_ERR_UNSUPPORTED_DTYPE, "hsn_win_backward: io_dtype must be f32 or bf16");
     HSN_REQUIRE(check_elems({int64_t(B) * T * K * d, int64_t(B) * N * d}) &&
-                    int64_t(T) * K * d <= INT32_MAX,
+                    int64_t(T) * K * d * 4 < (int64_t(1) << 31),
                 HSN_ERR_SIZE_OVERFLOW,
                 "hsn_win_backward: a tensor is too large");
     Geometry g;
@@ -142,7 +142,7 @@ extern "C" int hsn_win_recurrence(const float* c, const float* b, const float* h
     HSN_REQUIRE(B >= 1 && T >= 1 && N >= 1 && d >= 1 && K >= 1, HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_recurrence: bad dimensions");
     HSN_REQUIRE(check_elems({int64_t(B) * T * K * d, int64_t(B) * N * d}) &&
-                    int64_t(T) * K * d <= INT32_MAX,
+                    int64_t(T) * K * d * 4 < (int64_t(1) << 31),
                 HSN_ERR_SIZE_OVERFLOW,
                 "hsn_win_recurrence: a tensor is too large");
     Geometry g;

@@ -47,7 +47,7 @@ extern "C" int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype
     HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
                 HSN_ERR_UNSUPPORTED_DTYPE, "hsn_win_forward: io_dtype must be f32 or bf16");
     HSN_REQUIRE(check_elems({int64_t(B) * T * K * d, int64_t(B) * N * d}) &&
-                    int64_t(T) * K * d <= INT32_MAX,
+                    int64_t(T) * K * d * 4 < (int64_t(1) << 31),
                 HSN_ERR_SIZE_OVERFLOW,
                 "hsn_win_forward: a tensor is too large");
     Geometry g;
