@@ -4,8 +4,10 @@
 
 A step is one window of the configuration, inputs resident in HBM: the router
 (``hsn_win_route``), the forward sweep (``hsn_win_forward``) and the backward with the
-carried-state gradient (``hsn_win_backward``). ``value`` is positions/s over the K timed steps
-(B*T positions per step, bracketed by synchronisations). Each kernel's average duration is
+carried-state gradient (``hsn_win_backward``). The step is captured once as a HIP graph and
+``value`` is positions/s over K timed replays (B*T positions per step, bracketed by
+synchronisations); ``--no-graph`` times eager launches instead (``ms_per_step_eager`` is always
+reported). Each kernel's average duration is
 measured with HIP events recorded on the stream the kernels run on (torch's current stream);
 ``roofline`` reports the dominant kernel's algorithmic bytes per launch (the byte model of
 ``hsn_amd.workload.byte_model``) over its average duration against the 8 TB/s HBM peak.
@@ -38,6 +40,14 @@ def _args():
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-h-max", action="store_true", help="do not produce the row maxima")
+    p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                   help="after the timed steps, copy a buffer of MIB MiB three times (outside "
+                        "the timed region): the reference kernel for scaling rocprofv3's "
+                        "FETCH_SIZE / WRITE_SIZE counters")
+    p.add_argument("--no-graph", action="store_true",
+                   help="time eager launches instead of replays of the captured step")
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="repeat the CPU baseline's sample until this much time has passed")
     return p.parse_args()
 
 
@@ -53,9 +63,9 @@ def _traffic(workload: str):
         return None
 
 
-def _cpu_baseline(cfg, seed):
+def _cpu_baseline(cfg, seed, min_seconds):
     """The CPU oracle on one full window of the configuration (or a prefix of its positions for
-    the large configurations), on all host cores."""
+    the large configurations), on all host cores, repeated until ``min_seconds`` have passed."""
     import torch
 
     from hsn_amd.workload import make_cotangents, make_window
@@ -72,22 +82,28 @@ def _cpu_baseline(cfg, seed):
     short = {k: (v[:, :2] if k in ("logits", "y", "gate_pre", "reset") else v) for k, v in w.items()}
     O.window_forward(short["logits"], short["y"], short["gate_pre"], short["reset"], w["h0"], w["q0"],
                      w["age0"], w["pos0"], w["cost"], **kw)
+    reps = 0
     t0 = time.perf_counter()
-    f = O.window_forward(w["logits"], w["y"], w["gate_pre"], w["reset"], w["h0"], w["q0"],
-                         w["age0"], w["pos0"], w["cost"], **kw)
-    O.window_backward(w["y"], w["gate_pre"], f["h_old"], f["cells"], f["valid"], w["reset"],
-                      sample.N, c["d_q_pre"], c["d_q_post"],
-                      torch.where(f["valid"][..., None], c["d_h_sel"].float(), 0.0).to(c["d_h_sel"].dtype),
-                      c["d_h_T"], c["d_q_T"])
-    secs = time.perf_counter() - t0
-    positions = sample.B * sample.T
+    while True:
+        f = O.window_forward(w["logits"], w["y"], w["gate_pre"], w["reset"], w["h0"], w["q0"],
+                             w["age0"], w["pos0"], w["cost"], **kw)
+        O.window_backward(w["y"], w["gate_pre"], f["h_old"], f["cells"], f["valid"], w["reset"],
+                          sample.N, c["d_q_pre"], c["d_q_post"],
+                          torch.where(f["valid"][..., None], c["d_h_sel"].float(),
+                                      0.0).to(c["d_h_sel"].dtype),
+                          c["d_h_T"], c["d_q_T"])
+        reps += 1
+        secs = time.perf_counter() - t0
+        if secs >= min_seconds:
+            break
+    positions = sample.B * sample.T * reps
     return {
         "value": positions / secs,
         "unit": "positions/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{sample.B} rows x {sample.T} positions of the {cfg.name} window, fwd+bwd, "
-                  f"the repository's PyTorch-CPU oracle ({secs:.2f} s)",
+        "sample": f"{reps} x ({sample.B} rows x {sample.T} positions of the {cfg.name} window), "
+                  f"fwd+bwd, the repository's PyTorch-CPU oracle ({secs:.1f} s)",
     }
 
 
@@ -135,13 +151,37 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # per-kernel durations: eager steps with events between the launches
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(events[i])
     torch.cuda.synchronize()
-    secs = time.perf_counter() - t0
+    eager_secs = time.perf_counter() - t0
+    # the job: the step captured once as a HIP graph (its outputs in the graph's pool) and
+    # replayed K times, so the host's per-launch work is out of the loop
+    secs = eager_secs
+    graphed = False
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        capture = torch.cuda.Stream()
+        capture.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(capture):
+            step()  # warm the capture stream's allocator
+        torch.cuda.current_stream().wait_stream(capture)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        secs = time.perf_counter() - t0
+        graphed = True
     per_kernel = {"route": 0.0, "forward": 0.0, "backward": 0.0}
     for ev in events:
         per_kernel["route"] += ev[0].elapsed_time(ev[1])
@@ -186,13 +226,22 @@ def main() -> int:
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": None if traffic is None else traffic.get(dominant),
         },
+        "timing": "HIP graph replays of the captured step" if graphed else "eager launches",
+        "ms_per_step_eager": eager_secs / args.steps * 1e3,
         "kernels_ms": per_kernel,
         "kernels_gbs": {k: algo[k] / (per_kernel[k] * 1e-3) / 1e9 for k in per_kernel},
         "window_gbs": window_gbs,
         "window_frac": window_gbs / HBM_PEAK_GBS,
     }
+    if args.calibrate_copy > 0:  # outside the timed region: a plain copy of known size
+        src = torch.ones(args.calibrate_copy * (1 << 20) // 4, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["calibration_copy_bytes"] = args.calibrate_copy * (1 << 20)
     if not args.no_cpu:
-        result["cpu_baseline"] = _cpu_baseline(cfg, args.seed)
+        result["cpu_baseline"] = _cpu_baseline(cfg, args.seed, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0
 

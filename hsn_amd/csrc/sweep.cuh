@@ -1066,11 +1066,21 @@ inline DivN make_divn(int N) {
     return v;
 }
 
+// Raise a kernel's dynamic-LDS limit to the full 160 KiB once per process and device (not a
+// stream operation, and never repeated inside a stream capture).
 template <typename K>
 hipError_t allow_lds(K kernel, size_t lds) {
     if (lds <= 64 * 1024) return hipSuccess;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    constexpr int kMaxDevices = 64;
+    static bool done[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev >= 0 && dev < kMaxDevices && done[dev]) return hipSuccess;
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsMax));
+    if (e == hipSuccess && dev >= 0 && dev < kMaxDevices) done[dev] = true;
+    return e;
 }
 
 template <typename IN, typename OUT, typename SLOT, int S>

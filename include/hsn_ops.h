@@ -5,10 +5,9 @@
  * Same function names, argument order, dtype codes and status codes as the reference's ABI
  * (kernels/include/hsn_ops.h:64-77,85-99,155-187), so a host that binds that header binds this
  * library unchanged. Conventions as there: dense row-major tensors, int32_t indices, one float
- * dtype per call (f32 or bf16 here; f16 is HSN_ERR_UNSUPPORTED_DTYPE), fp32 accumulation with
- * one rounding per output, outputs written in full, `stream` a hipStream_t, functions return
+ * dtype per call (f32, f16 or bf16), fp32 accumulation with one rounding per output, outputs written in full, `stream` a hipStream_t, functions return
  * once the work is enqueued. Tolerances against the reference's golden vectors: f32 1e-5,
- * bf16 1e-2 (atol = rtol).
+ * f16 and bf16 1e-2 (atol = rtol).
  */
 #ifndef HSN_OPS_H
 #define HSN_OPS_H
