@@ -4,7 +4,7 @@
 // 8-lane half row (row_half_mirror) and the rotation by 8 (row_ror:8), so groups of up to 16
 // lanes reduce with one v_*_dpp instruction per step and no LDS traffic; each step combines a
 // lane with its partner symmetrically, so every lane of the group ends with the bit-identical
-// result. Wider groups (32, 64 lanes) take the LDS-permute shuffle for the remaining steps.
+// result. Wider groups (32, 64 lanes) join rows with gfx950's permlane swaps.
 #pragma once
 
 #include "common.cuh"
@@ -28,6 +28,31 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
         __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, false));
 }
 
+// The partner row of every lane (gfx950 v_permlane16_swap / v_permlane32_swap, no LDS): the
+// swap of a value with itself returns, in every lane, {the value in the even row, the value in
+// the odd row} of the lane's pair of 16-lane rows (lanes l and l^16), resp. of its pair of
+// 32-lane halves (lanes l and l^32). Both lanes of a pair get the same two operands in the same
+// order, so a combination of them is bit-identical in both.
+struct RowPair {
+    uint32_t lo, hi;
+};
+__device__ __forceinline__ RowPair pair16(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return {static_cast<uint32_t>(r[0]), static_cast<uint32_t>(r[1])};
+}
+__device__ __forceinline__ RowPair pair32(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return {static_cast<uint32_t>(r[0]), static_cast<uint32_t>(r[1])};
+}
+__device__ __forceinline__ float sum16(float v) {
+    const RowPair r = pair16(__float_as_uint(v));
+    return __uint_as_float(r.lo) + __uint_as_float(r.hi);
+}
+__device__ __forceinline__ float sum32(float v) {
+    const RowPair r = pair32(__float_as_uint(v));
+    return __uint_as_float(r.lo) + __uint_as_float(r.hi);
+}
+
 // Sum over each aligned group of L lanes; every lane of a group gets the group's sum.
 template <int L>
 __device__ __forceinline__ float group_sum(float v) {
@@ -36,8 +61,8 @@ __device__ __forceinline__ float group_sum(float v) {
     if constexpr (L >= 4) v += dpp_f32<dpp::kXor2>(v);
     if constexpr (L >= 8) v += dpp_f32<dpp::kHalfMirror>(v);
     if constexpr (L >= 16) v += dpp_f32<dpp::kRor8>(v);
-    if constexpr (L >= 32) v += __shfl_xor(v, 16, kWave);
-    if constexpr (L >= 64) v += __shfl_xor(v, 32, kWave);
+    if constexpr (L >= 32) v = sum16(v);
+    if constexpr (L >= 64) v = sum32(v);
     return v;
 }
 
@@ -50,8 +75,14 @@ __device__ __forceinline__ uint32_t group_max(uint32_t v) {
     if constexpr (L >= 4) v = umax(v, dpp_u32<dpp::kXor2>(v));
     if constexpr (L >= 8) v = umax(v, dpp_u32<dpp::kHalfMirror>(v));
     if constexpr (L >= 16) v = umax(v, dpp_u32<dpp::kRor8>(v));
-    if constexpr (L >= 32) v = umax(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 16, kWave)));
-    if constexpr (L >= 64) v = umax(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 32, kWave)));
+    if constexpr (L >= 32) {
+        const RowPair r = pair16(v);
+        v = umax(r.lo, r.hi);
+    }
+    if constexpr (L >= 64) {
+        const RowPair r = pair32(v);
+        v = umax(r.lo, r.hi);
+    }
     return v;
 }
 

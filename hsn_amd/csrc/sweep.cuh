@@ -94,6 +94,8 @@ __device__ __forceinline__ void col_sums(float (&v)[M]) {
 #pragma unroll
         for (int i = 0; i < M; ++i) {
             if (m == 8) v[i] += dpp_f32<dpp::kRor8>(v[i]);  // xor 8 inside a 16-lane row
+            else if (m == 16) v[i] = sum16(v[i]);
+            else if (m == 32) v[i] = sum32(v[i]);
             else v[i] += __shfl_xor(v[i], m, kWave);
         }
     }
@@ -149,12 +151,13 @@ struct FwdArgs {
 };
 
 // LDS words of the forward: per wavefront the state slice h [N*S] (alpha in phase A) with a
-// dummy word, and when chunked beta [N*S] with a dummy; then the ages' last-selection table
-// [N+1], the column-sum partials [W][W][S], two flags per chunk and, when chunked, the start
-// state [N*S] staged for phase B.
+// dummy word, and beta [N*S] with a dummy (the cells' maxima in phase C); then the ages'
+// last-selection table [N+1], the column-sum partials [W][W][S], two flags per chunk and, when
+// chunked, the start state [N*S] staged for phase B.
 inline int fwd_region(int N, int S, int W) {  // a multiple of 4 words: 16-byte aligned slices
+    (void)W;
     const int ns = N * S + 1;
-    return ((W > 1 ? 2 * ns : ns) + 3) & ~3;
+    return (2 * ns + 3) & ~3;
 }
 inline size_t fwd_lds_bytes(int N, int S, int W) {
     const size_t h0_stage = W > 1 ? size_t(N) * S : 0;  // the start state, for phase B
@@ -166,11 +169,15 @@ __device__ __forceinline__ float& lds_at(float* lds, uint32_t byte) {
     return *reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + byte);
 }
 
+__device__ __forceinline__ uint32_t& lds_at_u(float* lds, uint32_t byte) {
+    return *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(lds) + byte);
+}
+
 constexpr uint32_t kNoCell = 0xffffffffu;  // no tracked cell
 
 // RES: the whole chunk is one register sub-block (W > 1, Tc <= TB): phase C replays what phase A
 // loaded. Otherwise every phase streams its sub-blocks from memory.
-template <typename IN, typename OUT, typename SLOT, int S, int TB, bool RES>
+template <typename IN, typename OUT, typename SLOT, int S, int TB, bool RES, bool CM>
 __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     using Raw = typename SLOT::Raw;
     constexpr bool kWide = sizeof(Raw) == 8;
@@ -202,7 +209,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     const int t_end = min(T, t_begin + a.Tc);
     const int nsb = RES ? 1 : (t_end - t_begin + TB - 1) / TB;
     const bool track_age = slice == 0 && a.age_T != nullptr;
-    const bool want_max = a.h_max != nullptr;
+    const bool want_max = CM || a.h_max != nullptr;  // CM: launched only with the maxima
     const uint32_t qbytes = uint32_t(T) * d * sizeof(OUT);
     const DivN divn = a.divn;
 
@@ -237,21 +244,29 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     uint32_t rmask = 0u;
     float omb[TB], bcv[TB];
     uint32_t ca[TB];
-    auto fetch = [&](int tb0) __attribute__((always_inline)) {
-        const int tl = t_end - 1;
-#pragma unroll
-        for (int i = 0; i < TB; ++i) {
-            const int t = uniform(min(tb0 + i, tl));
-            const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
-            yv[i] = bload<IN>(ry, vy, sy);
-            gv[i] = bload<IN>(rg, vy, sy);
-            cv[i] = bload<int32_t>(rc, vc, uint32_t(t) * K * sizeof(Raw));
-            if constexpr (kWide) vb[i] = bload<uint8_t>(rv, vv, uint32_t(t) * K);
-        }
+    // the loads of position i of the sub-block at tb0 (clamped into the chunk, so every load is
+    // unconditional and the compiler's wait counts are exact)
+    auto fetch_at = [&](int i, int tb0) __attribute__((always_inline)) {
+        const int t = uniform(min(tb0 + i, t_end - 1));
+        const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
+        yv[i] = bload<IN>(ry, vy, sy);
+        gv[i] = bload<IN>(rg, vy, sy);
+        cv[i] = bload<int32_t>(rc, vc, uint32_t(t) * K * sizeof(Raw));
+        if constexpr (kWide) vb[i] = bload<uint8_t>(rv, vv, uint32_t(t) * K);
+    };
+    // the sub-block's resets as a bit mask of its positions
+    auto fetch_rst = [&](int tb0) __attribute__((always_inline)) {
         const bool rin = lane < TB && tb0 + lane < t_end;
         const uint8_t r = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
         rmask = static_cast<uint32_t>(ballot(r != 0));
     };
+    auto fetch = [&](int tb0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < TB; ++i) fetch_at(i, tb0);
+        fetch_rst(tb0);
+    };
+    // positions whose loads are in flight ahead of the one being composed in phase A
+    constexpr int kAhead = kWide ? 12 : 16;
     // returns whether the lane's slot is padded
     auto prep = [&](int i, bool in_block) __attribute__((always_inline)) -> bool {
         int c = cv[i];
@@ -276,29 +291,28 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
         return h0_row[int64_t(e / S) * d + slice * S + e % S];
     };
     if (RES || W > 1) {
-        // phase A: the chunk's per-cell maps, alpha (st) and beta (st2), from the identity
-        for (int e0 = 0; e0 < NS; e0 += kWave) {
-            const int e = e0 + lane;
-            if (e < NS) {
-                st[e] = 1.0f;
-                st2[e] = 0.0f;
-            }
-        }
+        // phase A: the chunk's per-cell maps, alpha (st) and beta (st2).
+        // The loads are software-pipelined, kAhead positions ahead of the one being composed, so
+        // the composition overlaps the sub-block's later loads (issuing them all first would
+        // hold the wavefront at issue until most of them had returned). A reset makes what
+        // came before it irrelevant to the chunk's map: the maps restart from zero at the
+        // sub-block's last reset and only the positions from there are composed.
         bool any_reset = false;
         for (int sb = 0; sb < nsb; ++sb) {
             const int tb0 = t_begin + sb * TB;
             const int n = min(TB, t_end - tb0);
+            fetch_rst(tb0);  // the oldest load: waiting for it waits for nothing else
             if (sb == 0) {
 #pragma unroll
                 for (int q = 0; q < kPre; ++q) {
                     const int e = q * kWave * W + gl;
                     h0v[q] = h0_elem(min(e, NS - 1));
                 }
-                __builtin_amdgcn_sched_barrier(0);
             }
-            fetch(tb0);
+#pragma unroll
+            for (int i = 0; i < kAhead && i < TB; ++i) fetch_at(i, tb0);
+            __builtin_amdgcn_sched_barrier(0);
             if (sb == 0) {
-                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int q = 0; q < kPre; ++q) {
                     const int e = q * kWave * W + gl;
@@ -307,19 +321,29 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
                 for (int e = kPre * kWave * W + gl; e < NS; e += kWave * W) h0s[e] = h0_elem(e);
             }
             any_reset |= rmask != 0u;
+            const int start = rmask != 0u ? 31 - __builtin_clz(rmask) : 0;
+            if (sb == 0 || rmask != 0u) {
+                const float a0 = sb == 0 && rmask == 0u ? 1.0f : 0.0f;
+                for (int e0 = 0; e0 < NS; e0 += kWave) {
+                    const int e = e0 + lane;
+                    if (e < NS) {
+                        st[e] = a0;
+                        st2[e] = 0.0f;
+                    }
+                }
+            }
             pad_lane = false;
 #pragma unroll
             for (int i = 0; i < TB; ++i) {
+                if (i + kAhead < TB) fetch_at(i + kAhead, tb0);
                 pad_lane |= prep(i, i < n);  // the loads of position i arrive in order
-                if (rmask != 0u && ((rmask >> i) & 1u)) {  // the state restarts from zero at t
-                    lds_zero(st, NS, lane);
-                    lds_zero(st2, NS, lane);
+                if (i >= start) {
+                    float& al = lds_at(lds, ca[i]);
+                    float& be = lds_at(lds, ca[i] + boff);
+                    const float va = al, vbe = be;
+                    al = omb[i] * va;
+                    be = omb[i] * vbe + bcv[i];
                 }
-                float& al = lds_at(lds, ca[i]);
-                float& be = lds_at(lds, ca[i] + boff);
-                const float va = al, vbe = be;
-                al = omb[i] * va;
-                be = omb[i] * vbe + bcv[i];
             }
         }
         if (lane == 0) rflag[w] = any_reset ? 1 : 0;
@@ -381,10 +405,50 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     if (lane == 0) st[NS] = 0.0f;  // the dummy: idle lanes read it as a zero state
 
     // phase C: the replay with the outputs.
-    // The slice's max |h| (bits, NaN above +inf) is M, held by the tracked cell (cw: its word in
-    // this lane's column, kNoCell when none). A position changes it only when a new value
-    // exceeds it or the tracked cell is written; otherwise M stands.
+    // The slice's max |h| per position (bits, NaN above +inf), two ways:
+    //  CM (N <= 256): every cell's max over the slice's columns, cm[c], lives in the beta
+    //     region (free in phase C) as 256 words, those past N zero. Each position writes its
+    //     cells' new maxima (a DPP max over the slot's lanes, stored by the slot's first lane;
+    //     the other lanes store to words of their own past the cells, so no two lanes of a store
+    //     share a word) and every lane reads the cells lane, lane+64, lane+128 and lane+192
+    //     (consecutive words across the lanes: no bank conflict); its maximum per position stays
+    //     in a register, and one batched wavefront reduction after the steps gives every
+    //     position's slice maximum. No branch, whatever the data.
+    //  otherwise: M, held by the tracked cell (cw: its word in this lane's column, kNoCell when
+    //     none); a position changes it only when a new value exceeds it or the tracked cell is
+    //     written, and then leaves the steps for a rescan or a raise.
     uint32_t M = 0u, cw = kNoCell;
+    constexpr int kLgS = S == 1 ? 0 : S == 2 ? 1 : S == 4 ? 2 : S == 8 ? 3 : 4;
+    constexpr int kCmCells = 256;
+    uint32_t* const cmw = reinterpret_cast<uint32_t*>(st2);  // [256] + the dummy N's + [64]
+    const uint32_t cm_base = rb + boff;
+    // a slot's cm word from its state word: cell c = (ca - rb) >> (2 + lg S) (the dummy gives N,
+    // a cell past the real ones: its padded and idle lanes store zero there)
+    const uint32_t cm_own = cm_base + uint32_t(kCmCells + 1 + lane) * 4u;
+    const uint32_t cm_rd = cm_base + uint32_t(lane) * 4u;
+    auto cm_init = [&]() __attribute__((always_inline)) {
+        for (int c0 = 0; c0 < kCmCells; c0 += kWave) {
+            const int c = c0 + lane;
+            uint32_t m = 0u;
+            if (c < N) {
+                if constexpr (S % 4 == 0) {
+#pragma unroll
+                    for (int q = 0; q < S; q += 4) {
+                        const float4 v = *reinterpret_cast<const float4*>(st + c * S + q);
+                        m = umax(umax(m, umax(abs_bits(v.x), abs_bits(v.y))),
+                                 umax(abs_bits(v.z), abs_bits(v.w)));
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < S; ++q) m = umax(m, abs_bits(st[c * S + q]));
+                }
+            }
+            cmw[c] = m;
+        }
+    };
+    auto cm_zero = [&]() __attribute__((always_inline)) {
+        for (int c0 = 0; c0 < kCmCells; c0 += kWave) cmw[c0 + lane] = 0u;
+    };
     auto rescan = [&]() __attribute__((always_inline)) {  // the max and a cell holding it, over the whole slice
         constexpr int U = 8;  // reads in flight per lane (the dummy word NS reads as zero)
         uint32_t best = 0u;
@@ -438,61 +502,114 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
         M = m;
         cw = cell_x + uint32_t(x) * 4u;
     };
-    if (want_max) rescan();
+    if constexpr (CM) cm_init();
+    else if (want_max) rescan();
 
     int lr = -1;  // the chunk's last reset
     const rsrc_t rho = out_rsrc(a.h_old, a.o_row, row_elems * sizeof(OUT));
     const rsrc_t rhs = out_rsrc(a.h_sel, a.o_row, row_elems * sizeof(OUT));
     const rsrc_t rqa = out_rsrc(a.q_pre, a.qo_row, qbytes);
     const rsrc_t rqb = out_rsrc(a.q_post, a.qo_row, qbytes);
-    // One sub-block of phase C: the steps, specialised for a full block without resets or
-    // padded slots (the common case) and general otherwise; then the summaries, the slice maxima
-    // and the cells' last selections.
+    // One sub-block of phase C: the steps, then the summaries, the slice maxima and the cells'
+    // last selections.
+    //
+    // The steps run straight through the unrolled positions. A position that needs more than the
+    // update (a reset before it, a change of the tracked maximum after it) leaves the unrolled
+    // code for the one handler after it, which re-enters at the next position to do. The rare
+    // work is compiled once instead of once per position, so the hot path is contiguous code
+    // (an inlined copy per position put a jump over cold code, and an instruction-cache miss,
+    // into every step).
     auto block = [&](int tb0, int n) __attribute__((always_inline)) {
         const bool pad = ballot(pad_lane) != 0u;
         float delta[TB];
-        uint32_t hmv = 0u;
-        auto steps = [&](auto full_c, auto reset_c, auto pad_c) __attribute__((always_inline)) {
-            constexpr bool kFull = decltype(full_c)::value;
-            constexpr bool kReset = decltype(reset_c)::value;
-            constexpr bool kPad = decltype(pad_c)::value;
+        uint32_t lmv[TB];  // CM: this lane's cells' maximum after each position
 #pragma unroll
-            for (int i = 0; i < TB; ++i) {
-                delta[i] = 0.0f;
-                if (kFull || i < n) {
-                    const int t = tb0 + i;
-                    if (kReset && ((rmask >> i) & 1u)) {  // a boundary: h, q and ages restart
-                        lds_zero(st, NS, lane);
-                        M = 0u;
-                        cw = kNoCell;
-                        lr = t;
-                    }
-                    const bool ok = !kPad || ca[i] != dummy;
-                    const float hold = lds_at(lds, kPad && !ok ? x0 : ca[i]);
-                    const float hnew = omb[i] * hold + bcv[i];
-                    lds_at(lds, ca[i]) = kPad && !ok ? 0.0f : hnew;
-                    const uint32_t so = uint32_t(t) * kd * sizeof(OUT);
-                    bstore_f32<OUT>(hold, rho, vo, so);
-                    float hs = hnew;
-                    if (kPad && ballot(active && !ok)) {  // a padded slot shows cell 0 after
-                        const float c0 = lds_at(lds, x0);
-                        hs = ok ? hnew : c0;
-                    }
-                    bstore_f32<OUT>(hs, rhs, vo, so);
-                    delta[i] = kPad && !ok ? 0.0f : hnew - hold;
-                    if (want_max) {
-                        const uint32_t av = kPad && !ok ? 0u : abs_bits(hnew);
-                        if (ballot(av > M || ca[i] == cw)) {
-                            if (ballot(ca[i] == cw)) rescan();  // the tracked cell changed
-                            else raise(av, ca[i]);
+        for (int i = 0; i < TB; ++i) {
+            delta[i] = 0.0f;
+            lmv[i] = 0u;
+        }
+        uint32_t hmv = 0u;
+        const uint32_t live = n >= 32 ? 0xffffffffu : (1u << n) - 1u;
+        const uint32_t so0 = uint32_t(tb0) * kd * sizeof(OUT);
+        const uint32_t sstep = kd * sizeof(OUT);
+        auto steps = [&](auto pad_c) __attribute__((always_inline)) {
+            constexpr bool kPad = decltype(pad_c)::value;
+            uint32_t todo = live;
+            uint32_t rpend = rmask & live;  // resets not applied yet
+            for (;;) {
+                int ev = -1;
+                bool ev_reset = false;
+                uint32_t ev_av = 0u, ev_ca = 0u;
+#pragma unroll
+                for (int i = 0; i < TB; ++i) {
+                    if ((todo >> i) & 1u) {
+                        if (unlikely((rpend >> i) & 1u)) {  // a boundary before position i
+                            ev = i;
+                            ev_reset = true;
+                            break;
                         }
-                        hmv = lane == i ? M : hmv;
+                        const bool ok = !kPad || ca[i] != dummy;
+                        const float hold = lds_at(lds, kPad && !ok ? x0 : ca[i]);
+                        const float hnew = omb[i] * hold + bcv[i];
+                        lds_at(lds, ca[i]) = kPad && !ok ? 0.0f : hnew;
+                        const uint32_t so = so0 + uint32_t(i) * sstep;
+                        bstore_f32<OUT>(hold, rho, vo, so);
+                        float hs = hnew;
+                        if (kPad) {  // a padded slot shows cell 0 after the update
+                            const float c0 = lds_at(lds, x0);
+                            hs = ok ? hnew : c0;
+                        }
+                        bstore_f32<OUT>(hs, rhs, vo, so);
+                        delta[i] = kPad && !ok ? 0.0f : hnew - hold;
+                        if constexpr (CM) {
+                            const uint32_t av = kPad && !ok ? 0u : abs_bits(hnew);
+                            const uint32_t cma = x == 0 ? cm_base + (((ca[i] - rb) >> (2 + kLgS)) << 2) : cm_own;
+                            lds_at_u(lds, cma) = group_max<S>(av);
+                            const uint32_t m0 = lds_at_u(lds, cm_rd), m1 = lds_at_u(lds, cm_rd + 256u);
+                            const uint32_t m2 = lds_at_u(lds, cm_rd + 512u), m3 = lds_at_u(lds, cm_rd + 768u);
+                            lmv[i] = umax(umax(m0, m1), umax(m2, m3));
+                        } else if (want_max) {
+                            const uint32_t av = kPad && !ok ? 0u : abs_bits(hnew);
+                            if (unlikely(ballot(av > M || ca[i] == cw) != 0u)) {
+                                ev = i;
+                                ev_av = av;
+                                ev_ca = ca[i];
+                                break;
+                            }
+                            hmv = lane == i ? M : hmv;
+                        }
                     }
+                }
+                if (ev < 0) break;
+                if (ev_reset) {  // h, q and ages restart; position ev runs next
+                    lds_zero(st, NS, lane);
+                    if constexpr (CM) cm_zero();
+                    M = 0u;
+                    cw = kNoCell;
+                    lr = tb0 + ev;
+                    rpend &= ~(1u << ev);
+                    todo = live & ~((1u << ev) - 1u);
+                } else {  // position ev is done but for its maximum
+                    if (ballot(ev_ca == cw)) rescan();  // the tracked cell changed
+                    else raise(ev_av, ev_ca);
+                    hmv = lane == ev ? M : hmv;
+                    todo = live & ~((2u << ev) - 1u);
                 }
             }
         };
-        if (n == TB && rmask == 0u && !pad) steps(std::true_type{}, std::false_type{}, std::false_type{});
-        else steps(std::false_type{}, std::true_type{}, std::true_type{});
+        if (pad) steps(std::true_type{});
+        else steps(std::false_type{});
+        if constexpr (CM) {  // every position's slice maximum, lane i holding position i's
+#pragma unroll
+            for (int i = 0; i < TB; ++i) {
+                uint32_t v = group_max<16>(lmv[i]);
+                RowPair r = pair16(v);
+                v = umax(r.lo, r.hi);
+                r = pair32(v);
+                v = umax(r.lo, r.hi);
+                hmv = lane == i ? v : hmv;
+            }
+        }
 
         // the summary before and after each position: q' = q + sum_k (h' - h)[k] / N, written by
         // one lane per column
@@ -831,7 +948,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                 const float vm = mu, vn = nu;
                 mu = omb[i] * vm;
                 nu = omb[i] * (vn + dsv[i]) - (1.0f - omb[i]) * sh[i];
-                if (rmask != 0u && ((rmask >> i) & 1u)) {  // nothing before it reaches past t
+                if (unlikely(rmask != 0u && ((rmask >> i) & 1u))) {  // nothing before it reaches past t
                     lds_zero(st, NS, lane);
                     lds_zero(st2, NS, lane);
                 }
@@ -914,7 +1031,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                     const uint32_t so = uint32_t(tb0 + i) * kd * sizeof(IN);
                     bstore_f32<IN>(dc, rdy, vy, so);
                     bstore_f32<IN>(db, rdg, vy, so);
-                    if (kReset && ((rmask >> i) & 1u)) lds_zero(st, NS, lane);
+                    if (kReset && unlikely((rmask >> i) & 1u)) lds_zero(st, NS, lane);
                 }
             }
         };
@@ -1085,8 +1202,13 @@ hipError_t allow_lds(K kernel, size_t lds) {
 
 template <typename IN, typename OUT, typename SLOT, int S>
 hipError_t launch_fwd_s(const FwdArgs& a, size_t lds, hipStream_t st) {
-    auto k = (a.W > 1 && a.Tc <= kResTB) ? fwd_chunk<IN, OUT, SLOT, S, kResTB, true>
-                                         : fwd_chunk<IN, OUT, SLOT, S, kStreamTB, false>;
+    const bool res = a.W > 1 && a.Tc <= kResTB;
+    // see fwd_chunk's phase C: 256 cells' maxima, a dummy and 64 words more fit the beta region
+    const bool cm = a.h_max != nullptr && a.N <= 256 && a.N * S >= 321;
+    auto k = res ? (cm ? fwd_chunk<IN, OUT, SLOT, S, kResTB, true, true>
+                       : fwd_chunk<IN, OUT, SLOT, S, kResTB, true, false>)
+                 : (cm ? fwd_chunk<IN, OUT, SLOT, S, kStreamTB, false, true>
+                       : fwd_chunk<IN, OUT, SLOT, S, kStreamTB, false, false>);
     hipError_t e = allow_lds(k, lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k, sweep_grid(a.B, a.d / S), dim3(kWave * a.W), lds, st, a);
