@@ -59,24 +59,38 @@ def hipcc() -> str:
     return found
 
 
-def _compile(src: Path) -> Path:
+def _stamp(src: Path) -> str:
+    """Digest of what an object depends on: the source, every header and the flags."""
+    h = hashlib.sha256(" ".join(HIP_FLAGS).encode())
+    for path in [src, *headers()]:
+        h.update(path.read_bytes())
+    return h.hexdigest()
+
+
+def _compile(src: Path, incremental: bool = False) -> Path:
     obj = BUILD / (src.name + ".o")
+    stamp = BUILD / (src.name + ".stamp")
+    digest = _stamp(src)
+    if incremental and obj.is_file() and stamp.is_file() and stamp.read_text() == digest:
+        return obj
     cmd = [hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr[-6000:]}")
+    stamp.write_text(digest)
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile and link the library; returns its path."""
+def build(verbose: bool = False, incremental: bool = False) -> Path:
+    """Compile and link the library; returns its path. ``incremental`` reuses an object whose
+    source, headers and flags are unchanged since it was compiled (the default compiles all)."""
     BUILD.mkdir(exist_ok=True)
     srcs = sources()
     jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4)), 16)
     with concurrent.futures.ThreadPoolExecutor(max_workers=max(jobs, 1)) as pool:
-        objs = list(pool.map(_compile, srcs))
+        objs = list(pool.map(lambda src: _compile(src, incremental), srcs))
     tmp = LIBRARY.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -113,5 +127,5 @@ def stale() -> str | None:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv[1:])
     sys.exit(0)

@@ -97,35 +97,63 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
     const IO* logits = static_cast<const IO*>(a.logits) + b * a.l_row + p * a.l_pos;
     const bool scale_cost = a.lambda > 0.0f;
 
+    // The cost table in lanes (lane j holds cost[j], j < M <= 64), loaded with the logits so
+    // the position waits for memory once: cost[u] for a lane's own u is a shuffle, called with
+    // every lane active.
+    const float cost_lane = lane < M ? a.cost[lane] : 0.0f;
+    auto cost_of = [&](int u) __attribute__((always_inline)) -> float {
+        return M <= kWave ? __shfl(cost_lane, u, kWave) : a.cost[u];
+    };
+
     // scores, units and sort keys of this lane's cells
     float sc[NPL];
     int unit[NPL];
     uint32_t key[NPL];
     int slot_of[NPL];  // 1 + the scored slot that took the cell, 0 if none
+    if (M == 1) {  // one unit: every cell's logit read at once (cells past N read cell N-1)
+        IO raw[NPL];
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-        const int n = lane * NPL + i;
-        sc[i] = -INFINITY;
-        unit[i] = 0;
-        key[i] = 0u;  // below every real key: never chosen
-        slot_of[i] = 0;
-        if (n < N) {
-            const IO* row = logits + static_cast<int64_t>(n) * a.width;
-            float best = to_f32(row[0]);
-            if (scale_cost) best = __fsub_rn(best, __fmul_rn(a.lambda, a.cost[0]));
-            int arg = 0;
-            for (int j = 1; j < M; ++j) {
-                float s = to_f32(row[j]);
-                if (scale_cost) s = __fsub_rn(s, __fmul_rn(a.lambda, a.cost[j]));
-                // amax / argmax: the first maximiser, a NaN counts as the maximum (first NaN)
-                if (best == best && (s > best || s != s)) {
-                    best = s;
-                    arg = j;
+        for (int i = 0; i < NPL; ++i) {
+            const int n = min(lane * NPL + i, N - 1);
+            raw[i] = logits[static_cast<int64_t>(n) * a.width];
+        }
+        const float lc = scale_cost ? __fmul_rn(a.lambda, a.cost[0]) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int n = lane * NPL + i;
+            float best = to_f32(raw[i]);
+            if (scale_cost) best = __fsub_rn(best, lc);
+            sc[i] = n < N ? best : -INFINITY;
+            unit[i] = 0;
+            key[i] = n < N ? (n < R ? kKeyPosInf : score_key(best)) : 0u;  // 0: never chosen
+            slot_of[i] = 0;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int n = lane * NPL + i;
+            sc[i] = -INFINITY;
+            unit[i] = 0;
+            key[i] = 0u;  // below every real key: never chosen
+            slot_of[i] = 0;
+            if (n < N) {
+                const IO* row = logits + static_cast<int64_t>(n) * a.width;
+                float best = to_f32(row[0]);
+                if (scale_cost) best = __fsub_rn(best, __fmul_rn(a.lambda, a.cost[0]));
+                int arg = 0;
+                for (int j = 1; j < M; ++j) {
+                    float s = to_f32(row[j]);
+                    if (scale_cost) s = __fsub_rn(s, __fmul_rn(a.lambda, a.cost[j]));
+                    // amax / argmax: the first maximiser, a NaN counts as the maximum (first NaN)
+                    if (best == best && (s > best || s != s)) {
+                        best = s;
+                        arg = j;
+                    }
                 }
+                sc[i] = best;
+                unit[i] = arg;
+                key[i] = n < R ? kKeyPosInf : score_key(best);
             }
-            sc[i] = best;
-            unit[i] = arg;
-            key[i] = n < R ? kKeyPosInf : score_key(best);
         }
     }
 
@@ -182,7 +210,8 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
     // the budget: per-slot cost, prefix sums accumulated in double in slot order and rounded to
     // fp32 per slot (torch's CPU cumsum of fp32), then the shared cost and the limit in fp32
     const bool is_slot = lane < K;
-    const float per_slot = is_slot ? __fadd_rn(a.overhead, a.cost[my_unit]) : 0.0f;
+    const float my_cost = cost_of(is_slot ? my_unit : 0);
+    const float per_slot = is_slot ? __fadd_rn(a.overhead, my_cost) : 0.0f;
     double acc = 0.0;
     for (int j = 0; j < K; ++j) {
         const float v = readlane(per_slot, j);
@@ -271,7 +300,8 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
                 }
             }
             // the budget guarantee: over the limit after the probes, keep the scored selection
-            const float cost_k = ok ? __fadd_rn(a.overhead, a.cost[new_unit]) : 0.0f;
+            const float new_cost = cost_of(ok ? new_unit : 0);
+            const float cost_k = ok ? __fadd_rn(a.overhead, new_cost) : 0.0f;
             float spent = 0.0f;
             for (int j = 0; j < K; ++j) spent = __fadd_rn(spent, readlane(cost_k, j));
             over = __fadd_rn(a.shared, spent) > a.limit;

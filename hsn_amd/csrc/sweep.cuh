@@ -809,27 +809,27 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
         const uint8_t r = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
         rmask = static_cast<uint32_t>(ballot(r != 0));
     };
-    auto fetch_a = [&](int tb0) __attribute__((always_inline)) {  // the gate, the selection cotangent and the decisions
-        const int tl = t_end - 1;
-#pragma unroll
-        for (int i = 0; i < TB; ++i) {
-            const int t = uniform(min(tb0 + i, tl));
-            const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
-            gv[i] = bload<IN>(rg, vy, sy);
-            dv[i] = bload<IN>(rds, vy, sy);
-            cv[i] = bload<int32_t>(rc, vc, uint32_t(t) * K * sizeof(Raw));
-            if constexpr (kWide) vb[i] = bload<uint8_t>(rv, vv, uint32_t(t) * K);
-        }
+    // the gate, the selection cotangent and the decision of position i of the sub-block at tb0
+    auto fetch_a_at = [&](int i, int tb0) __attribute__((always_inline)) {
+        const int t = uniform(min(tb0 + i, t_end - 1));
+        const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
+        gv[i] = bload<IN>(rg, vy, sy);
+        dv[i] = bload<IN>(rds, vy, sy);
+        cv[i] = bload<int32_t>(rc, vc, uint32_t(t) * K * sizeof(Raw));
+        if constexpr (kWide) vb[i] = bload<uint8_t>(rv, vv, uint32_t(t) * K);
     };
-    auto fetch_c = [&](int tb0) __attribute__((always_inline)) {  // the candidate and the gathered old state
+    // the candidate and the gathered old state, latest position first (phase C's order)
+    auto fetch_c = [&](int tb0) __attribute__((always_inline)) {
         const int tl = t_end - 1;
 #pragma unroll
-        for (int i = 0; i < TB; ++i) {
+        for (int i = TB - 1; i >= 0; --i) {
             const uint32_t sy = uint32_t(uniform(min(tb0 + i, tl))) * kd * sizeof(IN);
             yv[i] = bload<IN>(ry, vy, sy);
             hv[i] = bload<IN>(rho, vy, sy);
         }
     };
+    // positions whose loads are in flight ahead of the one being composed in phase A
+    constexpr int kAhead = kWide ? 12 : 16;
 
     // The summary cotangent R is a running sum of 2T cotangents; it is accumulated in fp64 (its
     // chunked sums would otherwise round differently from a sequential fp32 sum by about
@@ -887,20 +887,28 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     double R_out = 0.0;  // R after the chunk (its position t_begin)
     bool pad_lane = false;
     if (RES || W > 1) {
-        // pre-pass: each chunk's own sum (restarted at its resets, latest position first)
+        // pre-pass: each chunk's own sum (restarted at its resets, latest position first). The
+        // first kAhead positions of phase A (resident kernels) are fetched with it, so their
+        // loads are in flight through the pre-pass and its barrier.
         double Rl = 0.0;
         bool hasr = false;
         float dhv[kPre];
-#pragma unroll
-        for (int q = 0; q < kPre; ++q) {
-            const int e = q * kWave * W + gl;
-            dhv[q] = dh_elem(min(e, NS - 1));
-        }
-        __builtin_amdgcn_sched_barrier(0);
         for (int sb = nsb - 1; sb >= 0; --sb) {
             const int tb0 = t_begin + sb * TB;
             const int n = min(TB, t_end - tb0);
             fetch_q(tb0);
+            if (sb == nsb - 1) {
+#pragma unroll
+                for (int q = 0; q < kPre; ++q) {
+                    const int e = q * kWave * W + gl;
+                    dhv[q] = dh_elem(min(e, NS - 1));
+                }
+            }
+            if (RES) {
+#pragma unroll
+                for (int i = TB - 1; i >= TB - kAhead && i >= 0; --i) fetch_a_at(i, tb0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = TB - 1; i >= 0; --i) {
                 if (i < n) {
@@ -921,36 +929,45 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
             if (e < NS) dhs[e] = dhv[q];
         }
         for (int e = kPre * kWave * W + gl; e < NS; e += kWave * W) dhs[e] = dh_elem(e);
-        // phase A: the chunk's per-cell maps A_before = mu A_after + nu, from the identity
-        for (int e0 = 0; e0 < NS; e0 += kWave) {
-            const int e = e0 + lane;
-            if (e < NS) {
-                st[e] = 1.0f;
-                st2[e] = 0.0f;
-            }
-        }
         __syncthreads();
         for (int j = W - 1; j > w; --j) R_in = (rf[j] ? 0.0 : R_in) + rl[j * S + x];
         R_out = (hasr ? 0.0 : R_in) + Rl;
+        // phase A: the chunk's per-cell maps A_before = mu A_after + nu, latest position first,
+        // the loads kAhead positions ahead. A reset at t cuts what comes after it from what comes
+        // before: the maps restart from zero at the sub-block's earliest reset, and only the
+        // positions before it are composed (the later ones are still prepared for phase C).
         double R = R_in;
         for (int sb = nsb - 1; sb >= 0; --sb) {
             const int tb0 = t_begin + sb * TB;
             const int n = min(TB, t_end - tb0);
-            if (!RES) fetch_q(tb0);
-            fetch_a(tb0);
+            if (!RES) {
+                fetch_q(tb0);
+#pragma unroll
+                for (int i = TB - 1; i >= TB - kAhead && i >= 0; --i) fetch_a_at(i, tb0);
+            }
             shares(n, R);
+            const int stop = rmask != 0u ? __builtin_ctz(rmask) : TB;  // compose positions < stop
+            if (sb == nsb - 1 || rmask != 0u) {
+                const float m0 = sb == nsb - 1 && rmask == 0u ? 1.0f : 0.0f;
+                for (int e0 = 0; e0 < NS; e0 += kWave) {
+                    const int e = e0 + lane;
+                    if (e < NS) {
+                        st[e] = m0;
+                        st2[e] = 0.0f;
+                    }
+                }
+            }
             pad_lane = false;
 #pragma unroll
             for (int i = TB - 1; i >= 0; --i) {
+                if (i - kAhead >= 0) fetch_a_at(i - kAhead, tb0);
                 pad_lane |= prep(i, i < n);  // the loads of position i arrive in order
-                float& mu = lds_at(lds, ca[i]);
-                float& nu = lds_at(lds, ca[i] + boff);
-                const float vm = mu, vn = nu;
-                mu = omb[i] * vm;
-                nu = omb[i] * (vn + dsv[i]) - (1.0f - omb[i]) * sh[i];
-                if (unlikely(rmask != 0u && ((rmask >> i) & 1u))) {  // nothing before it reaches past t
-                    lds_zero(st, NS, lane);
-                    lds_zero(st2, NS, lane);
+                if (i < stop) {
+                    float& mu = lds_at(lds, ca[i]);
+                    float& nu = lds_at(lds, ca[i] + boff);
+                    const float vm = mu, vn = nu;
+                    mu = omb[i] * vm;
+                    nu = omb[i] * (vn + dsv[i]) - (1.0f - omb[i]) * sh[i];
                 }
             }
         }
@@ -998,15 +1015,20 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     // phase C: the replay with the outputs, latest position first
     const rsrc_t rdy = make_rsrc(static_cast<IN*>(a.dy) + base, row_bytes);
     const rsrc_t rdg = make_rsrc(static_cast<IN*>(a.dg) + base, row_bytes);
+    // One sub-block of phase C, straight through the positions; a reset leaves the unrolled code
+    // for the one zeroing after it and re-enters at the next (earlier) position, so the hot path
+    // is contiguous code (the forward's phase C does the same).
     auto block = [&](int tb0, int n) __attribute__((always_inline)) {
         const bool pad = ballot(pad_lane) != 0u;
-        auto steps = [&](auto full_c, auto reset_c, auto pad_c) __attribute__((always_inline)) {
-            constexpr bool kFull = decltype(full_c)::value;
-            constexpr bool kReset = decltype(reset_c)::value;
+        const uint32_t live = n >= 32 ? 0xffffffffu : (1u << n) - 1u;
+        auto steps = [&](auto pad_c) __attribute__((always_inline)) {
             constexpr bool kPad = decltype(pad_c)::value;
+            uint32_t todo = live;
+            for (;;) {
+                int ev = -1;
 #pragma unroll
             for (int i = TB - 1; i >= 0; --i) {
-                if (kFull || i < n) {
+                if ((todo >> i) & 1u) {
                     float& A = lds_at(lds, ca[i]);
                     const float share = shl[i];
                     const float carried = A + dsv[i];
@@ -1031,12 +1053,19 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                     const uint32_t so = uint32_t(tb0 + i) * kd * sizeof(IN);
                     bstore_f32<IN>(dc, rdy, vy, so);
                     bstore_f32<IN>(db, rdg, vy, so);
-                    if (kReset && unlikely((rmask >> i) & 1u)) lds_zero(st, NS, lane);
+                    if (unlikely((rmask >> i) & 1u)) {  // nothing before it reaches past t
+                        ev = i;
+                        break;
+                    }
                 }
             }
+                if (ev < 0) break;
+                lds_zero(st, NS, lane);
+                todo &= (1u << ev) - 1u;
+            }
         };
-        if (n == TB && rmask == 0u && !pad) steps(std::true_type{}, std::false_type{}, std::false_type{});
-        else steps(std::false_type{}, std::true_type{}, std::true_type{});
+        if (pad) steps(std::true_type{});
+        else steps(std::false_type{});
     };
     double R = R_in;
     if constexpr (RES) {
@@ -1046,7 +1075,8 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
             const int tb0 = t_begin + sb * TB;
             const int n = min(TB, t_end - tb0);
             fetch_q(tb0);
-            fetch_a(tb0);
+#pragma unroll
+            for (int i = TB - 1; i >= 0; --i) fetch_a_at(i, tb0);
             shares(n, R);
             keep_shares();
             pad_lane = false;
@@ -1248,5 +1278,17 @@ hipError_t launch_bwd(const BwdArgs& a, int S, size_t lds, hipStream_t st) {
     }
     return hipErrorInvalidValue;
 }
+
+// The kernels of each storage type are instantiated in a translation unit of their own
+// (sweep_inst_*.hip), so they compile in parallel; every other unit only declares them.
+#ifndef HSN_SWEEP_INSTANTIATE
+extern template hipError_t launch_fwd<float, float, Packed32>(const FwdArgs&, int, size_t, hipStream_t);
+extern template hipError_t launch_fwd<bf16_t, bf16_t, Packed32>(const FwdArgs&, int, size_t, hipStream_t);
+extern template hipError_t launch_fwd<float, float, Cells64>(const FwdArgs&, int, size_t, hipStream_t);
+extern template hipError_t launch_fwd<bf16_t, float, Cells64>(const FwdArgs&, int, size_t, hipStream_t);
+extern template hipError_t launch_bwd<float, Packed32, true>(const BwdArgs&, int, size_t, hipStream_t);
+extern template hipError_t launch_bwd<bf16_t, Packed32, true>(const BwdArgs&, int, size_t, hipStream_t);
+extern template hipError_t launch_bwd<float, Cells64, false>(const BwdArgs&, int, size_t, hipStream_t);
+#endif
 
 }  // namespace hsn
