@@ -341,16 +341,174 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
     }
 }
 
+// The decision of one position without probes, for NPL <= 4: the same selection as `decide`,
+// with each lane's cells sorted once. A lane's entries (key, cell, score, unit) are put in the
+// selection's order (key descending, cell ascending: a strict total order, so a five-comparator
+// network sorts them exactly) and kept in LDS; a round's winner is the lane whose head is the
+// wavefront's largest (the first such lane: the smaller cell), and it only writes its head to
+// the round's slot and reads its next entry, instead of rescanning its cells.
+template <int NPL, typename IO, typename IDX>
+__device__ void decide_sorted(const RouteArgs& a, int b, int p, uint4* ent, uint4* tab) {
+    static_assert(NPL == 1 || NPL == 2 || NPL == 4, "NPL");
+    const int lane = lane_id();
+    const int N = a.N, M = a.M, K = a.K, R = a.reserved;
+    const IO* logits = static_cast<const IO*>(a.logits) + b * a.l_row + p * a.l_pos;
+    const bool scale_cost = a.lambda > 0.0f;
+    const float cost_lane = lane < M ? a.cost[lane] : 0.0f;
+    auto cost_of = [&](int u) __attribute__((always_inline)) -> float {
+        return M <= kWave ? __shfl(cost_lane, u, kWave) : a.cost[u];
+    };
+
+    float sc[NPL];
+    int unit[NPL], nn[NPL];
+    uint32_t key[NPL];
+    if (M == 1) {
+        IO raw[NPL];
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) raw[i] = logits[int64_t(min(lane * NPL + i, N - 1)) * a.width];
+        const float lc = scale_cost ? __fmul_rn(a.lambda, a.cost[0]) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int n = lane * NPL + i;
+            float best = to_f32(raw[i]);
+            if (scale_cost) best = __fsub_rn(best, lc);
+            sc[i] = n < N ? best : -INFINITY;
+            unit[i] = 0;
+            key[i] = n < N ? (n < R ? kKeyPosInf : score_key(best)) : 0u;
+            nn[i] = n;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int n = lane * NPL + i;
+            sc[i] = -INFINITY;
+            unit[i] = 0;
+            key[i] = 0u;
+            nn[i] = n;
+            if (n < N) {
+                const IO* row = logits + static_cast<int64_t>(n) * a.width;
+                float best = to_f32(row[0]);
+                if (scale_cost) best = __fsub_rn(best, __fmul_rn(a.lambda, a.cost[0]));
+                int arg = 0;
+                for (int j = 1; j < M; ++j) {
+                    float s = to_f32(row[j]);
+                    if (scale_cost) s = __fsub_rn(s, __fmul_rn(a.lambda, a.cost[j]));
+                    if (best == best && (s > best || s != s)) {
+                        best = s;
+                        arg = j;
+                    }
+                }
+                sc[i] = best;
+                unit[i] = arg;
+                key[i] = n < R ? kKeyPosInf : score_key(best);
+            }
+        }
+    }
+    auto ce = [&](int i, int j) __attribute__((always_inline)) {  // the earlier entry first
+        // bitwise, not short-circuit: compares and selects, no branch
+        const bool sw = (key[i] < key[j]) | ((key[i] == key[j]) & (nn[i] > nn[j]));
+        const uint32_t k = key[i];
+        const int c = nn[i], u = unit[i];
+        const float v = sc[i];
+        key[i] = sw ? key[j] : k;
+        key[j] = sw ? k : key[j];
+        nn[i] = sw ? nn[j] : c;
+        nn[j] = sw ? c : nn[j];
+        unit[i] = sw ? unit[j] : u;
+        unit[j] = sw ? u : unit[j];
+        sc[i] = sw ? sc[j] : v;
+        sc[j] = sw ? v : sc[j];
+    };
+    if constexpr (NPL == 2) ce(0, 1);
+    if constexpr (NPL == 4) {
+        ce(0, 1);
+        ce(2, 3);
+        ce(0, 2);
+        ce(1, 3);
+        ce(1, 2);
+    }
+    uint4* const mine = ent + lane * NPL;
+#pragma unroll
+    for (int i = 1; i < NPL; ++i)
+        mine[i] = make_uint4(key[i], uint32_t(nn[i]), __float_as_uint(sc[i]), uint32_t(unit[i]));
+
+    // K rounds: the wavefront's largest head, its first lane; the winner moves to its next entry
+    uint4 head = make_uint4(key[0], uint32_t(nn[0]), __float_as_uint(sc[0]), uint32_t(unit[0]));
+    int ptr = 0;
+    uint32_t srec = 0u;  // per entry (8 bits each): 1 + the slot that took it, 0 if none
+    for (int r = 0; r < K; ++r) {
+        const uint32_t wk = wave_reduce_u32(head.x, [](uint32_t x, uint32_t y) { return x > y ? x : y; }, 0u);
+        const int src = __builtin_ctzll(ballot(head.x == wk));
+        if (lane == src) {
+            tab[r] = head;
+            srec |= uint32_t(r + 1) << (8 * ptr);
+            ++ptr;
+            head = ptr < NPL ? mine[ptr] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    __builtin_amdgcn_wave_barrier();  // the slot table's writes before its reads (one wavefront)
+    const bool is_slot = lane < K;
+    const uint4 e = is_slot ? tab[lane] : make_uint4(0u, 0u, 0u, 0u);
+    const int my_cell = static_cast<int>(e.y);
+    const float my_score = __uint_as_float(e.z);
+    const int my_unit = (a.fixed_units && lane < R) ? lane % M : static_cast<int>(e.w);
+
+    // the budget (as decide)
+    const float my_cost = cost_of(is_slot ? my_unit : 0);
+    const float per_slot = is_slot ? __fadd_rn(a.overhead, my_cost) : 0.0f;
+    double acc = 0.0;
+    for (int j = 0; j < K; ++j) {
+        const float v = readlane(per_slot, j);
+        if (j <= lane) acc += static_cast<double>(v);
+    }
+    const float cumulative = __fadd_rn(a.shared, static_cast<float>(acc));
+    const bool ok = is_slot && cumulative <= a.limit;
+    const uint64_t vmask = ballot(ok);
+
+    // the threshold (as decide)
+    float low = (ok && my_cell >= R) ? my_score : INFINITY;
+    low = wave_nan_min(low);
+    float high = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const uint32_t so = (srec >> (8 * i)) & 0xffu;
+        const bool sel = so > 0u && ((vmask >> (so - 1u)) & 1ull);
+        if (nn[i] < N && !sel) high = nan_max(high, sc[i]);
+    }
+    high = wave_nan_max(high);
+    const float th = 0.5f * (low + high);
+
+    if (is_slot) {
+        const int64_t o = b * a.o_row + p * a.o_pos + lane;
+        store_index<IDX>(a.cells, o, ok ? my_cell : 0);
+        store_index<IDX>(a.units, o, ok ? my_unit : 0);
+        a.valid[o] = ok ? 1 : 0;
+        a.refreshed[o] = 0;
+        if (a.slots) a.slots[o] = ok ? my_cell : -1;
+    }
+    if (lane == 0) {
+        a.theta[b * a.th_row + p * a.th_pos] = th;
+        if (a.h_max_zero) a.h_max_zero[static_cast<int64_t>(b) * a.P + p] = 0.0f;
+    }
+}
+
 // Whole window without probes: a wavefront per (row, position), four per workgroup.
 template <int NPL, typename IO, typename IDX>
 __global__ __launch_bounds__(256) void route_parallel(RouteArgs a) {
-    const int wave = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const int wv = uniform(threadIdx.x / kWave);  // uniform: the position's offsets stay scalar
+    const int wave = blockIdx.x * (blockDim.x / kWave) + wv;
     if (wave >= a.B * a.P) return;
     const int b = wave / a.P, p = wave - b * a.P;
-    int64_t ages[NPL];
+    if constexpr (NPL <= 4) {
+        __shared__ uint4 ent[4][kWave * NPL];
+        __shared__ uint4 tab[4][kWave];
+        decide_sorted<NPL, IO, IDX>(a, b, p, ent[wv], tab[wv]);
+    } else {
+        int64_t ages[NPL];
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) ages[i] = 0;
-    decide<NPL, IO, IDX>(a, b, p, ages, false);
+        for (int i = 0; i < NPL; ++i) ages[i] = 0;
+        decide<NPL, IO, IDX>(a, b, p, ages, false);
+    }
 }
 
 // With probes (or the per-position form): one wavefront walks a row's positions in order.
