@@ -724,12 +724,13 @@ struct BwdArgs {
 };
 
 // LDS words of the backward: per wavefront the cotangent slice A [N*S] (mu in phase A) with a
-// dummy word, and when chunked nu [N*S] with a dummy; then the chunks' summary-cotangent sums
-// [W][S] (fp64), reset flags [W], per wavefront the shares of a sub-block [S][TB] and, when
-// chunked, the end cotangent [N*S] staged for phase B.
+// dummy word, and nu [N*S] with a dummy (the cells' tags in phase C); then the chunks'
+// summary-cotangent sums [W][S] (fp64), reset flags [W], per wavefront the shares of a sub-block
+// [S][TB] and, when chunked, the end cotangent [N*S] staged for phase B.
 inline int bwd_region(int N, int S, int W) {  // a multiple of 4 words
+    (void)W;  // phase C keeps the cells' tags in the nu region, chunked or not
     const int ns = N * S + 1;
-    return ((W > 1 ? 2 * ns : ns) + 3) & ~3;
+    return (2 * ns + 3) & ~3;
 }
 inline size_t bwd_lds_bytes(int N, int S, int W) {
     const size_t dh_stage = W > 1 ? size_t(N) * S : 0;  // the end cotangent, for phase B
@@ -818,18 +819,22 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
         cv[i] = bload<int32_t>(rc, vc, uint32_t(t) * K * sizeof(Raw));
         if constexpr (kWide) vb[i] = bload<uint8_t>(rv, vv, uint32_t(t) * K);
     };
-    // the candidate and the gathered old state, latest position first (phase C's order)
-    auto fetch_c = [&](int tb0) __attribute__((always_inline)) {
+    // the candidate and the gathered old state of positions [lo, hi) of the sub-block, latest
+    // position first (phase C's order)
+    auto fetch_c = [&](int tb0, int lo = 0, int hi = TB) __attribute__((always_inline)) {
         const int tl = t_end - 1;
 #pragma unroll
         for (int i = TB - 1; i >= 0; --i) {
-            const uint32_t sy = uint32_t(uniform(min(tb0 + i, tl))) * kd * sizeof(IN);
-            yv[i] = bload<IN>(ry, vy, sy);
-            hv[i] = bload<IN>(rho, vy, sy);
+            if (i >= lo && i < hi) {
+                const uint32_t sy = uint32_t(uniform(min(tb0 + i, tl))) * kd * sizeof(IN);
+                yv[i] = bload<IN>(ry, vy, sy);
+                hv[i] = bload<IN>(rho, vy, sy);
+            }
         }
     };
-    // positions whose loads are in flight ahead of the one being composed in phase A
-    constexpr int kAhead = kWide ? 12 : 16;
+    // positions whose loads are in flight ahead of the one being composed in phase A (fewer than
+    // the forward's: this kernel keeps more per position in registers)
+    constexpr int kAhead = kWide ? 8 : 12;
 
     // The summary cotangent R is a running sum of 2T cotangents; it is accumulated in fp64 (its
     // chunked sums would otherwise round differently from a sequential fp32 sum by about
@@ -946,6 +951,8 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                 for (int i = TB - 1; i >= TB - kAhead && i >= 0; --i) fetch_a_at(i, tb0);
             }
             shares(n, R);
+            keep_shares();  // phase A reads them back from LDS (registers are scarce here)
+            __builtin_amdgcn_wave_barrier();
             const int stop = rmask != 0u ? __builtin_ctz(rmask) : TB;  // compose positions < stop
             if (sb == nsb - 1 || rmask != 0u) {
                 const float m0 = sb == nsb - 1 && rmask == 0u ? 1.0f : 0.0f;
@@ -967,14 +974,14 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                     float& nu = lds_at(lds, ca[i] + boff);
                     const float vm = mu, vn = nu;
                     mu = omb[i] * vm;
-                    nu = omb[i] * (vn + dsv[i]) - (1.0f - omb[i]) * sh[i];
+                    nu = omb[i] * (vn + dsv[i]) - (1.0f - omb[i]) * shl[i];
                 }
             }
         }
-        if (RES) {  // the replay's own inputs, in flight during phase B (not earlier: registers)
-            keep_shares();
+        if (RES) {  // the replay's first inputs, in flight during phase B (the rest after it:
+                    // registers)
             __builtin_amdgcn_sched_barrier(0);
-            fetch_c(t_begin);
+            fetch_c(t_begin, TB / 2, TB);
         }
         __syncthreads();
         // phase B: every chunk's end cotangent (into its mu's place), latest chunk first, chunk
@@ -1011,30 +1018,44 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
         }
     }
     if (lane == 0) st[NS] = 0.0f;  // the dummy: idle lanes read it as a zero cotangent
+    if constexpr (RES) fetch_c(t_begin, 0, TB / 2);  // the replay's later inputs
 
     // phase C: the replay with the outputs, latest position first
     const rsrc_t rdy = make_rsrc(static_cast<IN*>(a.dy) + base, row_bytes);
     const rsrc_t rdg = make_rsrc(static_cast<IN*>(a.dg) + base, row_bytes);
-    // One sub-block of phase C, straight through the positions; a reset leaves the unrolled code
-    // for the one zeroing after it and re-enters at the next (earlier) position, so the hot path
-    // is contiguous code (the forward's phase C does the same).
+    // Resets without a branch: every cell's word in the (now free) nu region tags the position
+    // of its last update in this replay (the chunk's start state: t_end), and rcur is the
+    // latest reset passed (positions run latest first; t_end + 1: none yet). A reset at t zeroes
+    // the cotangent of every cell after position t is replayed, so a cell's value counts only
+    // if it was updated after the latest reset passed: tag < rcur, else it reads as zero.
+    int* const tagw = reinterpret_cast<int*>(st2);
+    const uint32_t tag_base = rb + boff;
+    constexpr int kLgS = S == 1 ? 0 : S == 2 ? 1 : S == 4 ? 2 : S == 8 ? 3 : 4;
+    for (int c0 = 0; c0 <= N; c0 += kWave)
+        if (c0 + lane <= N) tagw[c0 + lane] = t_end;
+    int rcur = t_end + 1;
+    // One sub-block of phase C, straight through the positions (no branch: the registers of a
+    // position are free once it is replayed).
     auto block = [&](int tb0, int n) __attribute__((always_inline)) {
         const bool pad = ballot(pad_lane) != 0u;
-        const uint32_t live = n >= 32 ? 0xffffffffu : (1u << n) - 1u;
         auto steps = [&](auto pad_c) __attribute__((always_inline)) {
             constexpr bool kPad = decltype(pad_c)::value;
-            uint32_t todo = live;
-            for (;;) {
-                int ev = -1;
 #pragma unroll
             for (int i = TB - 1; i >= 0; --i) {
-                if ((todo >> i) & 1u) {
-                    float& A = lds_at(lds, ca[i]);
+                if (i < n) {
+                    const int t = tb0 + i;
+                    // the slot's cell's tag (the dummy's for padded and idle lanes: cell N)
+                    const uint32_t ta = tag_base + (((ca[i] - rb) >> (2 + kLgS)) << 2);
+                    float& Aref = lds_at(lds, ca[i]);
+                    const float Ar = Aref;
+                    const int tg = *reinterpret_cast<const int*>(reinterpret_cast<const char*>(lds) + ta);
+                    const float A = tg < rcur ? Ar : 0.0f;
                     const float share = shl[i];
                     const float carried = A + dsv[i];
                     const float gg = carried + share;
                     const float bg = 1.0f - omb[i];
-                    A = omb[i] * carried - bg * share;
+                    Aref = omb[i] * carried - bg * share;
+                    *reinterpret_cast<int*>(reinterpret_cast<char*>(lds) + ta) = t;
                     const float c = ACT ? fast_tanh(to_f32(yv[i])) : to_f32(yv[i]);
                     const float diff = c - to_f32(hv[i]);
                     float dc, db;
@@ -1050,18 +1071,11 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                         dc = ok ? dc : 0.0f;
                         db = ok ? db : 0.0f;
                     }
-                    const uint32_t so = uint32_t(tb0 + i) * kd * sizeof(IN);
+                    const uint32_t so = uint32_t(t) * kd * sizeof(IN);
                     bstore_f32<IN>(dc, rdy, vy, so);
                     bstore_f32<IN>(db, rdg, vy, so);
-                    if (unlikely((rmask >> i) & 1u)) {  // nothing before it reaches past t
-                        ev = i;
-                        break;
-                    }
+                    rcur = ((rmask >> i) & 1u) ? t : rcur;  // nothing before it reaches past t
                 }
-            }
-                if (ev < 0) break;
-                lds_zero(st, NS, lane);
-                todo &= (1u << ev) - 1u;
             }
         };
         if (pad) steps(std::true_type{});
@@ -1094,7 +1108,8 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
             float* dh0_row = dh0 + int64_t(b) * N * d;
             for (int e0 = 0; e0 < NS; e0 += kWave) {
                 const int e = e0 + lane;
-                if (e < NS) dh0_row[int64_t(e / S) * d + slice * S + e % S] = st[e];
+                if (e < NS)  // a cell last updated before the latest reset passed reads as zero
+                    dh0_row[int64_t(e / S) * d + slice * S + e % S] = tagw[e / S] < rcur ? st[e] : 0.0f;
             }
         }
         float* const dq0 = a.dq0;
