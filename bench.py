@@ -4,11 +4,12 @@
 
 A step is one window of the configuration, inputs resident in HBM: the router
 (``hsn_win_route``), the forward sweep (``hsn_win_forward``) and the backward with the
-carried-state gradient (``hsn_win_backward``). The step is captured once as a HIP graph and
-``value`` is positions/s over K timed replays (B*T positions per step, bracketed by
-synchronisations); ``--no-graph`` times eager launches instead (``ms_per_step_eager`` is always
-reported). Each kernel's average duration is
-measured with HIP events recorded on the stream the kernels run on (torch's current stream);
+carried-state gradient (``hsn_win_backward``). ``value`` is positions/s over K timed steps
+launched eagerly as a PyTorch loop calls them (B*T positions per step, bracketed by
+synchronisations); ``--graph`` times K replays of the step captured as a HIP graph instead
+(``ms_per_step_graph`` is reported either way unless ``--no-graph``). Each kernel's average
+duration is measured with HIP events recorded on the stream the kernels run on (torch's current
+stream), over K eager steps queued behind device copies so that the kernels run back to back;
 ``roofline`` reports the dominant kernel's algorithmic bytes per launch (the byte model of
 ``hsn_amd.workload.byte_model``) over its average duration against the 8 TB/s HBM peak.
 ``cpu_baseline`` times the repository's CPU oracle (the reference's profile:cpu algorithm) on a
@@ -44,8 +45,10 @@ def _args():
                    help="after the timed steps, copy a buffer of MIB MiB three times (outside "
                         "the timed region): the reference kernel for scaling rocprofv3's "
                         "FETCH_SIZE / WRITE_SIZE counters")
+    p.add_argument("--graph", action="store_true",
+                   help="value from replays of the step captured as a HIP graph")
     p.add_argument("--no-graph", action="store_true",
-                   help="time eager launches instead of replays of the captured step")
+                   help="skip the graph capture and its replays")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="repeat the CPU baseline's sample until this much time has passed")
     return p.parse_args()
@@ -151,18 +154,30 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    # per-kernel durations: eager steps with events between the launches
+    # eager steps as the host issues them (host work per launch included)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    eager_secs = time.perf_counter() - t0
+    # per-kernel durations: eager steps with events between the launches, queued behind a few
+    # milliseconds of plain device copies so the host has issued every launch before the GPU
+    # reaches them (the kernels then run back to back and an event pair brackets one kernel's
+    # execution, not the host's launch latency)
+    busy = torch.empty(64 << 20, device=dev)
+    busy_dst = torch.empty_like(busy)
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    for _ in range(2 * args.steps + 8):  # about 0.1 ms each, ahead of the host's issue rate
+        busy_dst.copy_(busy)
     for i in range(args.steps):
         step(events[i])
     torch.cuda.synchronize()
-    eager_secs = time.perf_counter() - t0
-    # the job: the step captured once as a HIP graph (its outputs in the graph's pool) and
-    # replayed K times, so the host's per-launch work is out of the loop
+    del busy, busy_dst
+    # the step captured once as a HIP graph (its outputs in the graph's pool) and replayed K
+    # times: the host's per-launch work is out of the loop, the graph launch's is in it
     secs = eager_secs
-    graphed = False
+    graph_secs = None
     if not args.no_graph:
         graph = torch.cuda.CUDAGraph()
         capture = torch.cuda.Stream()
@@ -180,8 +195,10 @@ def main() -> int:
         for _ in range(args.steps):
             graph.replay()
         torch.cuda.synchronize()
-        secs = time.perf_counter() - t0
-        graphed = True
+        graph_secs = time.perf_counter() - t0
+    graphed = args.graph and graph_secs is not None
+    if graphed:
+        secs = graph_secs
     per_kernel = {"route": 0.0, "forward": 0.0, "backward": 0.0}
     for ev in events:
         per_kernel["route"] += ev[0].elapsed_time(ev[1])
@@ -228,6 +245,7 @@ def main() -> int:
         },
         "timing": "HIP graph replays of the captured step" if graphed else "eager launches",
         "ms_per_step_eager": eager_secs / args.steps * 1e3,
+        "ms_per_step_graph": None if graph_secs is None else graph_secs / args.steps * 1e3,
         "kernels_ms": per_kernel,
         "kernels_gbs": {k: algo[k] / (per_kernel[k] * 1e-3) / 1e9 for k in per_kernel},
         "window_gbs": window_gbs,
