@@ -244,10 +244,11 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     uint32_t rmask = 0u;
     float omb[TB], bcv[TB];
     uint32_t ca[TB];
-    // the loads of position i of the sub-block at tb0 (clamped into the chunk, so every load is
-    // unconditional and the compiler's wait counts are exact)
+    // the loads of position i of the sub-block at tb0, unconditional (the compiler's wait counts
+    // stay exact). Not clamped: the row's resources bound them, so a position past the chunk
+    // reads data the preparation ignores and one past the row reads zeros.
     auto fetch_at = [&](int i, int tb0) __attribute__((always_inline)) {
-        const int t = uniform(min(tb0 + i, t_end - 1));
+        const int t = tb0 + i;
         const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
         yv[i] = bload<IN>(ry, vy, sy);
         gv[i] = bload<IN>(rg, vy, sy);
@@ -267,14 +268,17 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     };
     // positions whose loads are in flight ahead of the one being composed in phase A
     constexpr int kAhead = kWide ? 12 : 16;
-    // returns whether the lane's slot is padded
+    // returns whether the lane's slot is padded (the activations are computed for every lane,
+    // then selected: a conditional tanh would cost a divergent branch per position)
     auto prep = [&](int i, bool in_block) __attribute__((always_inline)) -> bool {
         int c = cv[i];
         if constexpr (kWide) c = vb[i] ? c : -1;
         const bool ok = in_block && active && c >= 0;
         const float bg = fast_sigmoid(to_f32(gv[i]));
+        const float cand = fast_tanh(to_f32(yv[i]));
+        const float bc = bg * cand;
         omb[i] = ok ? 1.0f - bg : 1.0f;
-        bcv[i] = ok ? bg * fast_tanh(to_f32(yv[i])) : 0.0f;
+        bcv[i] = ok ? bc : 0.0f;
         ca[i] = ok ? rb + uint32_t(c * S + x) * 4u : dummy;
         return in_block && active && c < 0;
     };
@@ -333,18 +337,23 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
                 }
             }
             pad_lane = false;
+            auto compose = [&](auto full_c) __attribute__((always_inline)) {
+                constexpr bool kFull = decltype(full_c)::value;  // n == TB: no position test
 #pragma unroll
-            for (int i = 0; i < TB; ++i) {
-                if (i + kAhead < TB) fetch_at(i + kAhead, tb0);
-                pad_lane |= prep(i, i < n);  // the loads of position i arrive in order
-                if (i >= start) {
-                    float& al = lds_at(lds, ca[i]);
-                    float& be = lds_at(lds, ca[i] + boff);
-                    const float va = al, vbe = be;
-                    al = omb[i] * va;
-                    be = omb[i] * vbe + bcv[i];
+                for (int i = 0; i < TB; ++i) {
+                    if (i + kAhead < TB) fetch_at(i + kAhead, tb0);
+                    pad_lane |= prep(i, kFull || i < n);  // the loads of position i arrive in order
+                    if (i >= start) {
+                        float& al = lds_at(lds, ca[i]);
+                        float& be = lds_at(lds, ca[i] + boff);
+                        const float va = al, vbe = be;
+                        al = omb[i] * va;
+                        be = omb[i] * vbe + bcv[i];
+                    }
                 }
-            }
+            };
+            if (n == TB) compose(std::true_type{});
+            else compose(std::false_type{});
         }
         if (lane == 0) rflag[w] = any_reset ? 1 : 0;
         __syncthreads();
