@@ -267,7 +267,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
         fetch_rst(tb0);
     };
     // positions whose loads are in flight ahead of the one being composed in phase A
-    constexpr int kAhead = kWide ? 12 : 16;
+    constexpr int kAhead = kWide ? 12 : 8;
     // returns whether the lane's slot is padded (the activations are computed for every lane,
     // then selected: a conditional tanh would cost a divergent branch per position)
     auto prep = [&](int i, bool in_block) __attribute__((always_inline)) -> bool {
