@@ -108,11 +108,12 @@ __device__ __forceinline__ float nan_max(float a, float b) {
 
 // A total order on fp32 scores as a stable descending sort sees them: NaN above +inf (all NaNs
 // equal), -0 equal to +0, otherwise the numeric order. Larger key = earlier in the order.
+// Selects only (no branch): a negative score flips every bit, a non-negative one sets the top bit.
 __device__ __forceinline__ uint32_t score_key(float s) {
-    if (s != s) return 0xffffffffu;
-    uint32_t u = __float_as_uint(s);
-    if (u == 0x80000000u) u = 0u;  // -0 sorts with +0
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    const uint32_t u0 = __float_as_uint(s);
+    const uint32_t u = u0 == 0x80000000u ? 0u : u0;  // -0 sorts with +0
+    const uint32_t k = u ^ (static_cast<uint32_t>(static_cast<int32_t>(u) >> 31) | 0x80000000u);
+    return s != s ? 0xffffffffu : k;
 }
 constexpr uint32_t kKeyPosInf = 0xff800000u;  // score_key(+inf)
 

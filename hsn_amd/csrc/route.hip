@@ -13,7 +13,24 @@
 // whole window is one launch with a wavefront per (row, position); with probes the ages evolve
 // with the decisions and one wavefront walks a row's positions in order, its ages in VGPRs.
 #include "common.cuh"
+#include "bufio.cuh"
 #include "dpp.cuh"
+
+#include <type_traits>
+
+// The CPU path rounds every product and sum on its own (scores - lambda * cost is a multiply,
+// then a subtract): no fused multiply-adds anywhere in the router.
+#pragma clang fp contract(off)
+
+namespace hsn {
+namespace {
+// one rounding each (written here, below the pragma: the header's mul_rn and friends carry
+// their own contraction state into the caller when inlined)
+__device__ __forceinline__ float mul_rn(float x, float y) { return x * y; }
+__device__ __forceinline__ float sub_rn(float x, float y) { return x - y; }
+__device__ __forceinline__ float add_rn(float x, float y) { return x + y; }
+}  // namespace
+}  // namespace hsn
 
 namespace hsn {
 namespace {
@@ -117,12 +134,12 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
             const int n = min(lane * NPL + i, N - 1);
             raw[i] = logits[static_cast<int64_t>(n) * a.width];
         }
-        const float lc = scale_cost ? __fmul_rn(a.lambda, a.cost[0]) : 0.0f;
+        const float lc = scale_cost ? mul_rn(a.lambda, a.cost[0]) : 0.0f;
 #pragma unroll
         for (int i = 0; i < NPL; ++i) {
             const int n = lane * NPL + i;
             float best = to_f32(raw[i]);
-            if (scale_cost) best = __fsub_rn(best, lc);
+            if (scale_cost) best = sub_rn(best, lc);
             sc[i] = n < N ? best : -INFINITY;
             unit[i] = 0;
             key[i] = n < N ? (n < R ? kKeyPosInf : score_key(best)) : 0u;  // 0: never chosen
@@ -139,11 +156,11 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
             if (n < N) {
                 const IO* row = logits + static_cast<int64_t>(n) * a.width;
                 float best = to_f32(row[0]);
-                if (scale_cost) best = __fsub_rn(best, __fmul_rn(a.lambda, a.cost[0]));
+                if (scale_cost) best = sub_rn(best, mul_rn(a.lambda, a.cost[0]));
                 int arg = 0;
                 for (int j = 1; j < M; ++j) {
                     float s = to_f32(row[j]);
-                    if (scale_cost) s = __fsub_rn(s, __fmul_rn(a.lambda, a.cost[j]));
+                    if (scale_cost) s = sub_rn(s, mul_rn(a.lambda, a.cost[j]));
                     // amax / argmax: the first maximiser, a NaN counts as the maximum (first NaN)
                     if (best == best && (s > best || s != s)) {
                         best = s;
@@ -211,13 +228,13 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
     // fp32 per slot (torch's CPU cumsum of fp32), then the shared cost and the limit in fp32
     const bool is_slot = lane < K;
     const float my_cost = cost_of(is_slot ? my_unit : 0);
-    const float per_slot = is_slot ? __fadd_rn(a.overhead, my_cost) : 0.0f;
+    const float per_slot = is_slot ? add_rn(a.overhead, my_cost) : 0.0f;
     double acc = 0.0;
     for (int j = 0; j < K; ++j) {
         const float v = readlane(per_slot, j);
         if (j <= lane) acc += static_cast<double>(v);
     }
-    const float cumulative = __fadd_rn(a.shared, static_cast<float>(acc));
+    const float cumulative = add_rn(a.shared, static_cast<float>(acc));
     const bool ok = is_slot && cumulative <= a.limit;
     const uint64_t vmask = ballot(ok);
     const int n_valid = __popcll(vmask);
@@ -301,10 +318,10 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
             }
             // the budget guarantee: over the limit after the probes, keep the scored selection
             const float new_cost = cost_of(ok ? new_unit : 0);
-            const float cost_k = ok ? __fadd_rn(a.overhead, new_cost) : 0.0f;
+            const float cost_k = ok ? add_rn(a.overhead, new_cost) : 0.0f;
             float spent = 0.0f;
-            for (int j = 0; j < K; ++j) spent = __fadd_rn(spent, readlane(cost_k, j));
-            over = __fadd_rn(a.shared, spent) > a.limit;
+            for (int j = 0; j < K; ++j) spent = add_rn(spent, readlane(cost_k, j));
+            over = add_rn(a.shared, spent) > a.limit;
             if (!over) {
                 out_cell = new_cell;
                 out_unit = new_unit;
@@ -341,40 +358,85 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
     }
 }
 
+// NaN-propagating wavefront amin / amax (torch's: NaN when any lane holds one). A ballot finds a
+// NaN; the min / max tree (the fold order of wave_nan_min / wave_nan_max) does the rest, so the
+// result equals theirs bit for bit at a third of the instructions.
+__device__ __forceinline__ float wave_amin(float v) {
+    const bool any_nan = ballot(v != v) != 0u;
+    const float m = wave_reduce_f32(v, [](float x, float y) { return fminf(x, y); }, INFINITY);
+    return any_nan ? __int_as_float(0x7fc00000) : m;
+}
+__device__ __forceinline__ float wave_amax(float v) {
+    const bool any_nan = ballot(v != v) != 0u;
+    const float m = wave_reduce_f32(v, [](float x, float y) { return fmaxf(x, y); }, -INFINITY);
+    return any_nan ? __int_as_float(0x7fc00000) : m;
+}
+
+// A lane's NPL consecutive logits as one buffer load (the row's resource bounds it).
+template <int NPL, typename IO>
+__device__ __forceinline__ void load_run(IO (&raw)[NPL], rsrc_t r, uint32_t voff) {
+    constexpr int kBytes = NPL * static_cast<int>(sizeof(IO));
+    if constexpr (kBytes == 16) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+        __builtin_memcpy(raw, &v, 16);
+    } else if constexpr (kBytes == 8) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0);
+        __builtin_memcpy(raw, &v, 8);
+    } else if constexpr (kBytes == 4) {
+        const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);
+        __builtin_memcpy(raw, &v, 4);
+    } else {
+        const uint16_t v = __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
+        __builtin_memcpy(raw, &v, 2);
+    }
+}
+
 // The decision of one position without probes, for NPL <= 4: the same selection as `decide`,
 // with each lane's cells sorted once. A lane's entries (key, cell, score, unit) are put in the
 // selection's order (key descending, cell ascending: a strict total order, so a five-comparator
-// network sorts them exactly) and kept in LDS; a round's winner is the lane whose head is the
-// wavefront's largest (the first such lane: the smaller cell), and it only writes its head to
-// the round's slot and reads its next entry, instead of rescanning its cells.
-template <int NPL, typename IO, typename IDX>
+// network sorts them exactly); the head is in registers and the rest in LDS. A round's winner
+// is the lane whose head is the wavefront's largest (the first such lane: the smaller cell), and
+// it only writes its head to the round's slot and reads its next entry, instead of rescanning
+// its cells. kOne (one unit, M = 1): every slot costs the same, so the budget's running sum is
+// a product, and a contiguous logits row is one vector load per lane.
+template <int NPL, bool kOne, typename IO, typename IDX>
 __device__ void decide_sorted(const RouteArgs& a, int b, int p, uint4* ent, uint4* tab) {
     static_assert(NPL == 1 || NPL == 2 || NPL == 4, "NPL");
     const int lane = lane_id();
     const int N = a.N, M = a.M, K = a.K, R = a.reserved;
     const IO* logits = static_cast<const IO*>(a.logits) + b * a.l_row + p * a.l_pos;
     const bool scale_cost = a.lambda > 0.0f;
-    const float cost_lane = lane < M ? a.cost[lane] : 0.0f;
-    auto cost_of = [&](int u) __attribute__((always_inline)) -> float {
-        return M <= kWave ? __shfl(cost_lane, u, kWave) : a.cost[u];
-    };
 
     float sc[NPL];
     int unit[NPL], nn[NPL];
     uint32_t key[NPL];
-    if (M == 1) {
+    // kOne: the one unit's cost, loaded with the logits so the position waits for memory once
+    const float cost0 = kOne ? a.cost[0] : 0.0f;
+    if constexpr (kOne) {
         IO raw[NPL];
+        constexpr uint32_t kRun = NPL * sizeof(IO);
+        const bool vec = a.width == 1 && N % NPL == 0 &&
+                         (reinterpret_cast<uintptr_t>(logits) & (kRun - 1)) == 0;
+        if (vec) {  // lanes past the row read zeros (kOob); their cells are masked below
+            const rsrc_t r = make_rsrc(logits, uint32_t(N) * sizeof(IO));
+            load_run<NPL, IO>(raw, r, lane * NPL < N ? uint32_t(lane) * kRun : kOob);
+        } else {
 #pragma unroll
-        for (int i = 0; i < NPL; ++i) raw[i] = logits[int64_t(min(lane * NPL + i, N - 1)) * a.width];
-        const float lc = scale_cost ? __fmul_rn(a.lambda, a.cost[0]) : 0.0f;
+            for (int i = 0; i < NPL; ++i)
+                raw[i] = logits[int64_t(min(lane * NPL + i, N - 1)) * a.width];
+        }
+        const float lc = scale_cost ? mul_rn(a.lambda, cost0) : 0.0f;
 #pragma unroll
         for (int i = 0; i < NPL; ++i) {
             const int n = lane * NPL + i;
             float best = to_f32(raw[i]);
-            if (scale_cost) best = __fsub_rn(best, lc);
+            if (scale_cost) best = sub_rn(best, lc);
+            // masks, not a conditional: the compiler would branch around the key otherwise
+            const uint32_t in = 0u - static_cast<uint32_t>(n < N);
+            const uint32_t rsv = 0u - static_cast<uint32_t>(n < R);
             sc[i] = n < N ? best : -INFINITY;
             unit[i] = 0;
-            key[i] = n < N ? (n < R ? kKeyPosInf : score_key(best)) : 0u;
+            key[i] = ((score_key(best) & ~rsv) | (kKeyPosInf & rsv)) & in;
             nn[i] = n;
         }
     } else {
@@ -388,11 +450,11 @@ __device__ void decide_sorted(const RouteArgs& a, int b, int p, uint4* ent, uint
             if (n < N) {
                 const IO* row = logits + static_cast<int64_t>(n) * a.width;
                 float best = to_f32(row[0]);
-                if (scale_cost) best = __fsub_rn(best, __fmul_rn(a.lambda, a.cost[0]));
+                if (scale_cost) best = sub_rn(best, mul_rn(a.lambda, a.cost[0]));
                 int arg = 0;
                 for (int j = 1; j < M; ++j) {
                     float s = to_f32(row[j]);
-                    if (scale_cost) s = __fsub_rn(s, __fmul_rn(a.lambda, a.cost[j]));
+                    if (scale_cost) s = sub_rn(s, mul_rn(a.lambda, a.cost[j]));
                     if (best == best && (s > best || s != s)) {
                         best = s;
                         arg = j;
@@ -404,9 +466,12 @@ __device__ void decide_sorted(const RouteArgs& a, int b, int p, uint4* ent, uint
             }
         }
     }
-    auto ce = [&](int i, int j) __attribute__((always_inline)) {  // the earlier entry first
-        // bitwise, not short-circuit: compares and selects, no branch
-        const bool sw = (key[i] < key[j]) | ((key[i] == key[j]) & (nn[i] > nn[j]));
+    // the earlier entry first; bitwise, not short-circuit: compares and selects, no branch. Where
+    // the entry at i is known to hold the smaller cell (kTie false), equal keys keep their places.
+    auto ce = [&](int i, int j, auto tie_c) __attribute__((always_inline)) {
+        constexpr bool kTie = decltype(tie_c)::value;
+        bool sw = key[i] < key[j];
+        if constexpr (kTie) sw = sw | ((key[i] == key[j]) & (nn[i] > nn[j]));
         const uint32_t k = key[i];
         const int c = nn[i], u = unit[i];
         const float v = sc[i];
@@ -414,36 +479,43 @@ __device__ void decide_sorted(const RouteArgs& a, int b, int p, uint4* ent, uint
         key[j] = sw ? k : key[j];
         nn[i] = sw ? nn[j] : c;
         nn[j] = sw ? c : nn[j];
-        unit[i] = sw ? unit[j] : u;
-        unit[j] = sw ? u : unit[j];
+        if constexpr (!kOne) {
+            unit[i] = sw ? unit[j] : u;
+            unit[j] = sw ? u : unit[j];
+        }
         sc[i] = sw ? sc[j] : v;
         sc[j] = sw ? v : sc[j];
     };
-    if constexpr (NPL == 2) ce(0, 1);
+    // Cells n = lane*NPL + i start in order of i. The first four comparators of the network
+    // compare an entry from {0, 1} with one from {2, 3} (or 0 with 1, 2 with 3), the smaller
+    // cell always at the lower place; only the last one can see either order.
+    if constexpr (NPL == 2) ce(0, 1, std::false_type{});
     if constexpr (NPL == 4) {
-        ce(0, 1);
-        ce(2, 3);
-        ce(0, 2);
-        ce(1, 3);
-        ce(1, 2);
+        ce(0, 1, std::false_type{});
+        ce(2, 3, std::false_type{});
+        ce(0, 2, std::false_type{});
+        ce(1, 3, std::false_type{});
+        ce(1, 2, std::true_type{});
     }
+    // entries 1 .. NPL-1 at mine[0 .. NPL-2], an empty entry (key 0: never the largest) last
     uint4* const mine = ent + lane * NPL;
 #pragma unroll
     for (int i = 1; i < NPL; ++i)
-        mine[i] = make_uint4(key[i], uint32_t(nn[i]), __float_as_uint(sc[i]), uint32_t(unit[i]));
+        mine[i - 1] = make_uint4(key[i], uint32_t(nn[i]), __float_as_uint(sc[i]), uint32_t(unit[i]));
+    mine[NPL - 1] = make_uint4(0u, 0u, 0u, 0u);
 
     // K rounds: the wavefront's largest head, its first lane; the winner moves to its next entry
     uint4 head = make_uint4(key[0], uint32_t(nn[0]), __float_as_uint(sc[0]), uint32_t(unit[0]));
-    int ptr = 0;
-    uint32_t srec = 0u;  // per entry (8 bits each): 1 + the slot that took it, 0 if none
-    for (int r = 0; r < K; ++r) {
+    int ptr = 0;            // this lane's entries given to slots
+    uint32_t srec = 0u;     // per entry (8 bits each): 1 + the slot that took it, 0 if none
+    for (int r = 0; r < K; r = uniform(r + 1)) {
         const uint32_t wk = wave_reduce_u32(head.x, [](uint32_t x, uint32_t y) { return x > y ? x : y; }, 0u);
         const int src = __builtin_ctzll(ballot(head.x == wk));
         if (lane == src) {
             tab[r] = head;
             srec |= uint32_t(r + 1) << (8 * ptr);
             ++ptr;
-            head = ptr < NPL ? mine[ptr] : make_uint4(0u, 0u, 0u, 0u);
+            head = mine[min(ptr, NPL) - 1];
         }
     }
     __builtin_amdgcn_wave_barrier();  // the slot table's writes before its reads (one wavefront)
@@ -451,31 +523,49 @@ __device__ void decide_sorted(const RouteArgs& a, int b, int p, uint4* ent, uint
     const uint4 e = is_slot ? tab[lane] : make_uint4(0u, 0u, 0u, 0u);
     const int my_cell = static_cast<int>(e.y);
     const float my_score = __uint_as_float(e.z);
-    const int my_unit = (a.fixed_units && lane < R) ? lane % M : static_cast<int>(e.w);
 
-    // the budget (as decide)
-    const float my_cost = cost_of(is_slot ? my_unit : 0);
-    const float per_slot = is_slot ? __fadd_rn(a.overhead, my_cost) : 0.0f;
-    double acc = 0.0;
-    for (int j = 0; j < K; ++j) {
-        const float v = readlane(per_slot, j);
-        if (j <= lane) acc += static_cast<double>(v);
+    // the budget (as decide): the running sum of the slots' costs in double, as the CPU cumsum
+    int my_unit = 0;
+    float cumulative;
+    if constexpr (kOne) {
+        // every slot costs ps: the sum over slots 0..lane is (lane + 1) * ps, exact in double
+        // (a float times at most 64), as the running sum is
+        const float ps = add_rn(a.overhead, cost0);
+        cumulative = add_rn(a.shared, static_cast<float>(static_cast<double>(ps) * (lane + 1)));
+    } else {
+        my_unit = (a.fixed_units && lane < R) ? lane % M : static_cast<int>(e.w);
+        const float my_cost = is_slot ? a.cost[my_unit] : 0.0f;
+        const float per_slot = is_slot ? add_rn(a.overhead, my_cost) : 0.0f;
+        double acc = 0.0;
+        for (int j = 0; j < K; ++j) {
+            const float v = readlane(per_slot, j);
+            if (j <= lane) acc += static_cast<double>(v);
+        }
+        cumulative = add_rn(a.shared, static_cast<float>(acc));
     }
-    const float cumulative = __fadd_rn(a.shared, static_cast<float>(acc));
     const bool ok = is_slot && cumulative <= a.limit;
     const uint64_t vmask = ballot(ok);
 
     // the threshold (as decide)
-    float low = (ok && my_cell >= R) ? my_score : INFINITY;
-    low = wave_nan_min(low);
+    const float low = wave_amin((ok && my_cell >= R) ? my_score : INFINITY);
+    const uint64_t full = K >= kWave ? ~0ull : (1ull << K) - 1ull;
+    const bool all_valid = vmask == full;  // then an entry is selected when it was taken
     float high = -INFINITY;
+    bool high_nan = false;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
-        const uint32_t so = (srec >> (8 * i)) & 0xffu;
-        const bool sel = so > 0u && ((vmask >> (so - 1u)) & 1ull);
-        if (nn[i] < N && !sel) high = nan_max(high, sc[i]);
+        bool sel;
+        if (all_valid) {
+            sel = i < ptr;
+        } else {
+            const uint32_t so = (srec >> (8 * i)) & 0xffu;
+            sel = so > 0u && ((vmask >> (so - 1u)) & 1ull);
+        }
+        const bool out = (nn[i] < N) & !sel;
+        high = fmaxf(high, out ? sc[i] : -INFINITY);
+        high_nan = high_nan | (out & (sc[i] != sc[i]));
     }
-    high = wave_nan_max(high);
+    high = wave_amax(high_nan ? __int_as_float(0x7fc00000) : high);
     const float th = 0.5f * (low + high);
 
     if (is_slot) {
@@ -502,7 +592,8 @@ __global__ __launch_bounds__(256) void route_parallel(RouteArgs a) {
     if constexpr (NPL <= 4) {
         __shared__ uint4 ent[4][kWave * NPL];
         __shared__ uint4 tab[4][kWave];
-        decide_sorted<NPL, IO, IDX>(a, b, p, ent[wv], tab[wv]);
+        if (a.M == 1) decide_sorted<NPL, true, IO, IDX>(a, b, p, ent[wv], tab[wv]);
+        else decide_sorted<NPL, false, IO, IDX>(a, b, p, ent[wv], tab[wv]);
     } else {
         int64_t ages[NPL];
 #pragma unroll
