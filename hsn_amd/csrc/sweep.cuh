@@ -177,6 +177,25 @@ constexpr uint32_t kNoCell = 0xffffffffu;  // no tracked cell
 
 // RES: the whole chunk is one register sub-block (W > 1, Tc <= TB): phase C replays what phase A
 // loaded. Otherwise every phase streams its sub-blocks from memory.
+// A row's state [N*S] out of LDS by the whole workgroup: element e = i*stride + t (t the thread),
+// U elements a thread per pass, all read before any is stored (one LDS wait a pass).
+template <int S, int U, typename Rd, typename Wr>
+__device__ __forceinline__ void write_state(int NS, int t, int stride, Rd rd, Wr wr) {
+    for (int e0 = t; e0 < NS; e0 += U * stride) {
+        float v[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int e = e0 + j * stride;
+            v[j] = e < NS ? rd(e) : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int e = e0 + j * stride;
+            if (e < NS) wr(e, v[j]);
+        }
+    }
+}
+
 template <typename IN, typename OUT, typename SLOT, int S, int TB, bool RES, bool CM>
 __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     using Raw = typename SLOT::Raw;
@@ -234,6 +253,9 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     if (track_age)
         for (int n0 = 0; n0 <= N; n0 += kWave * W)
             if (n0 + gl <= N) last[n0 + gl] = -1;
+    // the first pass of the ages' starting values, loaded now: the ages are the kernel's last work
+    const int64_t* const age0_row = track_age ? a.age0 + b * a.a0_row : nullptr;
+    const int64_t age0_first = track_age && gl < N ? age0_row[gl] : 0;
 
     // A sub-block: the raw loads, then per position (1 - b), b*c and the LDS byte address of
     // the slot's (cell, column) word. Padded and idle lanes get the identity update (1, 0) on
@@ -666,35 +688,40 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
         }
     }
 
-    // the end state (zeroed when the caller's next record resets this row)
+    // the end state (zeroed when the caller's next record resets this row). h is the last
+    // chunk's state, in wave W-1's region; every wavefront writes a share of it (wave W-1 alone,
+    // an LDS wait per store, made the kernel's tail).
     const uint8_t* const clear_p = a.clear;
     const bool clear = clear_p ? clear_p[b * a.c_row] != 0 : false;
-    if (w == W - 1) {
-        if (float* const hT = a.h_T) {
-            float* hT_row = hT + b * a.hT_row;
-            for (int e0 = 0; e0 < NS; e0 += kWave) {
-                const int e = e0 + lane;
-                if (e < NS) hT_row[int64_t(e / S) * d + slice * S + e % S] = clear ? 0.0f : st[e];
-            }
-        }
-        float* const qT = a.q_T;
-        if (qT && kslot == 0) qT[b * a.qT_row + col] = clear ? 0.0f : q_run;
-    }
-    if (track_age) {
-        if (lane == 0) rlast[w] = lr;
+    float* const hT = a.h_T;
+    if (hT || track_age) {  // uniform in the workgroup
+        if (track_age && lane == 0) rlast[w] = lr;
         __syncthreads();
+    }
+    if (hT) {
+        const float* const stl = lds + (W - 1) * a.region;
+        float* const hT_row = hT + b * a.hT_row;
+        write_state<S, 4>(NS, gl, kWave * W, [&](int e) __attribute__((always_inline)) {
+            return clear ? 0.0f : stl[e];
+        }, [&](int e, float v) __attribute__((always_inline)) {
+            hT_row[int64_t(e / S) * d + slice * S + e % S] = v;
+        });
+    }
+    float* const qT = a.q_T;
+    if (w == W - 1 && qT && kslot == 0) qT[b * a.qT_row + col] = clear ? 0.0f : q_run;
+    if (track_age) {
         int last_reset = -1;
         for (int j = 0; j < W; ++j) last_reset = max(last_reset, rlast[j]);
-        const int64_t* age0_row = a.age0 + b * a.a0_row;
         int64_t* ageT_row = a.age_T + b * a.aT_row;
         for (int n0 = 0; n0 < N; n0 += kWave * W) {
             const int n = n0 + gl;
             if (n < N) {
                 const int ls = last[n];
+                const int64_t a0 = n0 == 0 ? age0_first : age0_row[n];
                 int64_t age;
                 if (ls >= 0 && ls >= last_reset) age = (T - 1) - ls;
                 else if (last_reset >= 0) age = T - last_reset;
-                else age = age0_row[n] + T;
+                else age = a0 + T;
                 ageT_row[n] = clear ? 0 : age;
             }
         }
@@ -1111,19 +1138,25 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     }
     if (!RES && W == 1) R_out = R;
 
-    // the carried-state gradient: A and R after position 0
-    if (w == 0) {
-        if (float* const dh0 = a.dh0) {
-            float* dh0_row = dh0 + int64_t(b) * N * d;
-            for (int e0 = 0; e0 < NS; e0 += kWave) {
-                const int e = e0 + lane;
-                if (e < NS)  // a cell last updated before the latest reset passed reads as zero
-                    dh0_row[int64_t(e / S) * d + slice * S + e % S] = tagw[e / S] < rcur ? st[e] : 0.0f;
-            }
-        }
-        float* const dq0 = a.dq0;
-        if (dq0 && kslot == 0) dq0[int64_t(b) * d + col] = static_cast<float>(R_out);
+    // the carried-state gradient: A and R after position 0. A is wave 0's state; every
+    // wavefront writes a share of it (wave 0 alone, an LDS wait per store, made the kernel's tail),
+    // and wave 0 passes its latest reset in its region's dummy word.
+    if (float* const dh0 = a.dh0) {
+        if (w == 0 && lane == 0) reinterpret_cast<int*>(st)[NS] = rcur;
+        __syncthreads();
+        const float* const st0 = lds;
+        const int* const tag0 = reinterpret_cast<const int*>(lds + NS + 1);
+        const int rcur0 = reinterpret_cast<const int*>(lds)[NS];
+        float* const dh0_row = dh0 + int64_t(b) * N * d;
+        write_state<S, 4>(NS, gl, kWave * W, [&](int e) __attribute__((always_inline)) {
+            // a cell last updated before the latest reset passed reads as zero
+            return tag0[e / S] < rcur0 ? st0[e] : 0.0f;
+        }, [&](int e, float v) __attribute__((always_inline)) {
+            dh0_row[int64_t(e / S) * d + slice * S + e % S] = v;
+        });
     }
+    float* const dq0 = a.dq0;
+    if (w == 0 && dq0 && kslot == 0) dq0[int64_t(b) * d + col] = static_cast<float>(R_out);
 }
 
 // ------------------------------------------------------------------------------------------
