@@ -277,16 +277,22 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
         cv[i] = bload<int32_t>(rc, vc, uint32_t(t) * K * sizeof(Raw));
         if constexpr (kWide) vb[i] = bload<uint8_t>(rv, vv, uint32_t(t) * K);
     };
-    // the sub-block's resets as a bit mask of its positions
+    // the sub-block's resets (lane i: position tb0 + i), loaded before its other inputs and
+    // turned into a bit mask of its positions after they are issued: the ballot waits for the
+    // oldest load only, not for a round trip before the others go out
+    uint8_t rbyte = 0;
     auto fetch_rst = [&](int tb0) __attribute__((always_inline)) {
         const bool rin = lane < TB && tb0 + lane < t_end;
-        const uint8_t r = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
-        rmask = static_cast<uint32_t>(ballot(r != 0));
+        rbyte = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
+    };
+    auto rst_mask = [&]() __attribute__((always_inline)) {
+        rmask = static_cast<uint32_t>(ballot(rbyte != 0));
     };
     auto fetch = [&](int tb0) __attribute__((always_inline)) {
+        fetch_rst(tb0);
 #pragma unroll
         for (int i = 0; i < TB; ++i) fetch_at(i, tb0);
-        fetch_rst(tb0);
+        rst_mask();
     };
     // positions whose loads are in flight ahead of the one being composed in phase A
     constexpr int kAhead = kWide ? 12 : 8;
@@ -338,6 +344,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
 #pragma unroll
             for (int i = 0; i < kAhead && i < TB; ++i) fetch_at(i, tb0);
             __builtin_amdgcn_sched_barrier(0);
+            rst_mask();
             if (sb == 0) {
 #pragma unroll
                 for (int q = 0; q < kPre; ++q) {
@@ -834,7 +841,12 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     int32_t cv[TB];
     uint8_t vb[TB];
     uint32_t rmask = 0u;
-    auto fetch_q = [&](int tb0) __attribute__((always_inline)) {  // the summary cotangents and the reset mask
+    // the summary cotangents and the resets (lane i: position tb0 + i; loaded first, turned into
+    // a bit mask of the positions by rst_mask once the sub-block's other loads are issued)
+    uint8_t rbyte = 0;
+    auto fetch_q = [&](int tb0) __attribute__((always_inline)) {
+        const bool rin = lane < TB && tb0 + lane < t_end;
+        rbyte = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
         const int tl = t_end - 1;
 #pragma unroll
         for (int i = 0; i < TB; ++i) {
@@ -842,9 +854,9 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
             qa[i] = to_f32(bload<IN>(rqa, vq, sq));
             qb[i] = to_f32(bload<IN>(rqb, vq, sq));
         }
-        const bool rin = lane < TB && tb0 + lane < t_end;
-        const uint8_t r = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
-        rmask = static_cast<uint32_t>(ballot(r != 0));
+    };
+    auto rst_mask = [&]() __attribute__((always_inline)) {
+        rmask = static_cast<uint32_t>(ballot(rbyte != 0));
     };
     // the gate, the selection cotangent and the decision of position i of the sub-block at tb0
     auto fetch_a_at = [&](int i, int tb0) __attribute__((always_inline)) {
@@ -950,6 +962,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                 for (int i = TB - 1; i >= TB - kAhead && i >= 0; --i) fetch_a_at(i, tb0);
             }
             __builtin_amdgcn_sched_barrier(0);
+            rst_mask();
 #pragma unroll
             for (int i = TB - 1; i >= 0; --i) {
                 if (i < n) {
@@ -985,6 +998,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                 fetch_q(tb0);
 #pragma unroll
                 for (int i = TB - 1; i >= TB - kAhead && i >= 0; --i) fetch_a_at(i, tb0);
+                rst_mask();
             }
             shares(n, R);
             keep_shares();  // phase A reads them back from LDS (registers are scarce here)
@@ -1127,6 +1141,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
             fetch_q(tb0);
 #pragma unroll
             for (int i = TB - 1; i >= 0; --i) fetch_a_at(i, tb0);
+            rst_mask();
             shares(n, R);
             keep_shares();
             pad_lane = false;
