@@ -833,10 +833,15 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     const uint32_t vy = active ? uint32_t(kslot * d + col) * sizeof(IN) : kOob;
     const uint32_t vc = active ? uint32_t(kslot) * sizeof(Raw) : kOob;
     const uint32_t vv = active ? uint32_t(kslot) : kOob;
-    const uint32_t vq = uint32_t(col) * sizeof(IN);  // every lane reads its column's cotangent
 
-    // raw loads of a sub-block
-    float qa[TB], qb[TB];
+    // raw loads of a sub-block. The summary cotangents are transposed: lane (g, x) = (lane / S,
+    // lane % S) holds positions g*kQP .. g*kQP + kQP - 1 of column x, so a sub-block takes
+    // 2*kQP loads instead of one per position at every slot (the same column's value, eight times
+    // over at S = 8, and enough loads to fill a wavefront's 63 in flight with phase A's prologue).
+    constexpr int kQG = kWave / S;                               // position groups
+    constexpr int kQP = TB * S >= kWave ? TB * S / kWave : 1;    // positions per group
+    const int qg = lane / S;
+    float qa[kQP], qb[kQP];
     IN gv[TB], dv[TB], yv[TB], hv[TB];
     int32_t cv[TB];
     uint8_t vb[TB];
@@ -847,12 +852,13 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     auto fetch_q = [&](int tb0) __attribute__((always_inline)) {
         const bool rin = lane < TB && tb0 + lane < t_end;
         rbyte = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
-        const int tl = t_end - 1;
+        const uint32_t sq = uint32_t(tb0) * d * sizeof(IN);
 #pragma unroll
-        for (int i = 0; i < TB; ++i) {
-            const uint32_t sq = uint32_t(uniform(min(tb0 + i, tl))) * d * sizeof(IN);
-            qa[i] = to_f32(bload<IN>(rqa, vq, sq));
-            qb[i] = to_f32(bload<IN>(rqb, vq, sq));
+        for (int j = 0; j < kQP; ++j) {  // past the row: the resource reads zeros (masked anyway)
+            const int i = qg * kQP + j;
+            const uint32_t v = i < TB ? uint32_t(i * d + col) * sizeof(IN) : kOob;
+            qa[j] = to_f32(bload<IN>(rqa, v, sq));
+            qb[j] = to_f32(bload<IN>(rqb, v, sq));
         }
     };
     auto rst_mask = [&]() __attribute__((always_inline)) {
@@ -884,27 +890,83 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     // the forward's: this kernel keeps more per position in registers)
     constexpr int kAhead = kWide ? 8 : 12;
 
-    // The summary cotangent R is a running sum of 2T cotangents; it is accumulated in fp64 (its
+    // The summary cotangent R is a running sum of 2T cotangents, latest position first: R += qb,
+    // the position's share is R/N, R += qa, and a reset zeroes R. It is accumulated in fp64 (its
     // chunked sums would otherwise round differently from a sequential fp32 sum by about
-    // sqrt(2T) ulps of its largest partial), and every position's share R/N is rounded to fp32.
-    float sh[TB];
-    auto shares = [&](int n, double& R) __attribute__((always_inline)) {  // latest position first, through the resets
+    // sqrt(2T) ulps of its largest partial), and every share is rounded to fp32.
+    // A run of positions maps R to (rs ? 0 : R) + c. Each lane composes its own positions' map,
+    // and a scan over the position groups (later groups first: shuffles of the column's lanes)
+    // gives every lane the map of the positions after its own. The running sum is a few
+    // dependent adds instead of one per position.
+    auto lane_map = [&](int n, bool& rs, double& c) __attribute__((always_inline)) {
+        rs = false;
+        c = 0.0;
+#pragma unroll
+        for (int j = kQP - 1; j >= 0; --j) {
+            const int i = qg * kQP + j;
+            if (i < n) {
+                c += double(qb[j]);
+                c += double(qa[j]);
+                if ((rmask >> i) & 1u) {
+                    c = 0.0;
+                    rs = true;
+                }
+            }
+        }
+    };
+    // inclusive: the map of the groups g .. kQG-1 (applied latest first)
+    auto scan_maps = [&](bool& rs, double& c) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 1; k < kQG; k <<= 1) {
+            const double cu = __shfl_down(c, k * S, kWave);
+            const int ru = __shfl_down(rs ? 1 : 0, k * S, kWave);
+            if (qg + k < kQG) {
+                c = rs ? c : cu + c;
+                rs = rs || ru != 0;
+            }
+        }
+    };
+    // the column's whole run (group 0's inclusive map), in every lane of the column
+    auto run_map = [&](bool rs, double c, bool& rs0, double& c0) __attribute__((always_inline)) {
+        c0 = __shfl(c, x, kWave);
+        rs0 = __shfl(rs ? 1 : 0, x, kWave) != 0;
+    };
+    // the sub-block's shares into LDS (shl: this column's [TB]), and R carried past it
+    auto shares = [&](int n, double& R) __attribute__((always_inline)) {
+        bool rs;
+        double c;
+        lane_map(n, rs, c);
+        scan_maps(rs, c);
+        bool rs0;
+        double c0;
+        run_map(rs, c, rs0, c0);
+        // exclusive: the map of the groups after this one
+        double ce = __shfl_down(c, S, kWave);
+        int re = __shfl_down(rs ? 1 : 0, S, kWave);
+        if (qg + 1 >= kQG) {
+            ce = 0.0;
+            re = 0;
+        }
+        double Rg = (re ? 0.0 : R) + ce;
         const double inv = double(divn.inv), nf = double(divn.n);
         auto run = [&](auto pow2_c) __attribute__((always_inline)) {
             constexpr bool kPow2 = decltype(pow2_c)::value;
 #pragma unroll
-            for (int i = TB - 1; i >= 0; --i) {
-                sh[i] = 0.0f;
+            for (int j = kQP - 1; j >= 0; --j) {
+                const int i = qg * kQP + j;
+                float sh = 0.0f;
                 if (i < n) {
-                    R += double(qb[i]);
-                    sh[i] = static_cast<float>(kPow2 ? R * inv : R / nf);
-                    R += double(qa[i]);
-                    if ((rmask >> i) & 1u) R = 0.0;
+                    Rg += double(qb[j]);
+                    sh = static_cast<float>(kPow2 ? Rg * inv : Rg / nf);
+                    Rg += double(qa[j]);
+                    if ((rmask >> i) & 1u) Rg = 0.0;
                 }
+                if (i < TB) shl[i] = sh;
             }
         };
         if (divn.pow2) run(std::true_type{});
         else run(std::false_type{});
+        R = (rs0 ? 0.0 : R) + c0;
     };
     // per position: (1 - b), the selection cotangent and the LDS byte address of the slot's word.
     // Padded and idle lanes get the identity update (1, no cotangent) on the dummy word.
@@ -919,12 +981,6 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
         dsv[i] = ok ? to_f32(dv[i]) : 0.0f;
         ca[i] = ok ? rb + uint32_t(c * S + x) * 4u : dummy;
         return in_block && active && c < 0;
-    };
-    auto keep_shares = [&]() __attribute__((always_inline)) {  // for phase C, from LDS
-        if (kslot == 0) {
-#pragma unroll
-            for (int i = 0; i < TB; ++i) shl[i] = sh[i];
-        }
     };
 
     // The end cotangent for phase B is staged in LDS during the pre-pass (the first kPre elements
@@ -963,17 +1019,13 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
             }
             __builtin_amdgcn_sched_barrier(0);
             rst_mask();
-#pragma unroll
-            for (int i = TB - 1; i >= 0; --i) {
-                if (i < n) {
-                    Rl += double(qb[i]);
-                    Rl += double(qa[i]);
-                    if ((rmask >> i) & 1u) {
-                        Rl = 0.0;
-                        hasr = true;
-                    }
-                }
-            }
+            bool rs, rs0;
+            double c, c0;
+            lane_map(n, rs, c);
+            scan_maps(rs, c);
+            run_map(rs, c, rs0, c0);
+            Rl = (rs0 ? 0.0 : Rl) + c0;
+            hasr = hasr || rs0;
         }
         if (kslot == 0) rl[w * S + x] = Rl;
         if (lane == 0) rf[w] = hasr ? 1 : 0;
@@ -1000,8 +1052,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                 for (int i = TB - 1; i >= TB - kAhead && i >= 0; --i) fetch_a_at(i, tb0);
                 rst_mask();
             }
-            shares(n, R);
-            keep_shares();  // phase A reads them back from LDS (registers are scarce here)
+            shares(n, R);  // phase A reads them back from LDS (registers are scarce here)
             __builtin_amdgcn_wave_barrier();
             const int stop = rmask != 0u ? __builtin_ctz(rmask) : TB;  // compose positions < stop
             if (sb == nsb - 1 || rmask != 0u) {
@@ -1143,7 +1194,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
             for (int i = TB - 1; i >= 0; --i) fetch_a_at(i, tb0);
             rst_mask();
             shares(n, R);
-            keep_shares();
+            __builtin_amdgcn_wave_barrier();
             pad_lane = false;
 #pragma unroll
             for (int i = TB - 1; i >= 0; --i) pad_lane |= prep(i, i < n);
