@@ -875,16 +875,15 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
     };
     // the candidate and the gathered old state of positions [lo, hi) of the sub-block, latest
     // position first (phase C's order)
+    auto fetch_c_at = [&](int i, int tb0) __attribute__((always_inline)) {
+        const uint32_t sy = uint32_t(uniform(min(tb0 + i, t_end - 1))) * kd * sizeof(IN);
+        yv[i] = bload<IN>(ry, vy, sy);
+        hv[i] = bload<IN>(rho, vy, sy);
+    };
     auto fetch_c = [&](int tb0, int lo = 0, int hi = TB) __attribute__((always_inline)) {
-        const int tl = t_end - 1;
 #pragma unroll
-        for (int i = TB - 1; i >= 0; --i) {
-            if (i >= lo && i < hi) {
-                const uint32_t sy = uint32_t(uniform(min(tb0 + i, tl))) * kd * sizeof(IN);
-                yv[i] = bload<IN>(ry, vy, sy);
-                hv[i] = bload<IN>(rho, vy, sy);
-            }
-        }
+        for (int i = TB - 1; i >= 0; --i)
+            if (i >= lo && i < hi) fetch_c_at(i, tb0);
     };
     // positions whose loads are in flight ahead of the one being composed in phase A (fewer than
     // the forward's: this kernel keeps more per position in registers)
@@ -1069,6 +1068,9 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
 #pragma unroll
             for (int i = TB - 1; i >= 0; --i) {
                 if (i - kAhead >= 0) fetch_a_at(i - kAhead, tb0);
+                // RES: the last kAhead steps have no loads of their own left to issue; the
+                // replay's latest inputs go out there instead (through the barrier and phase B)
+                else if (RES && TB - kAhead + i >= TB / 2) fetch_c_at(TB - kAhead + i, tb0);
                 pad_lane |= prep(i, i < n);  // the loads of position i arrive in order
                 if (i < stop) {
                     float& mu = lds_at(lds, ca[i]);
@@ -1079,10 +1081,10 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                 }
             }
         }
-        if (RES) {  // the replay's first inputs, in flight during phase B (the rest after it:
-                    // registers)
+        if (RES) {  // the rest of the replay's first inputs, in flight during phase B (the
+                    // earlier half after it: registers)
             __builtin_amdgcn_sched_barrier(0);
-            fetch_c(t_begin, TB / 2, TB);
+            fetch_c(t_begin, TB / 2, TB - kAhead);
         }
         __syncthreads();
         // phase B: every chunk's end cotangent (into its mu's place), latest chunk first, chunk
