@@ -101,6 +101,48 @@ __device__ __forceinline__ void col_sums(float (&v)[M]) {
     }
 }
 
+// The column sums of a sub-block's per-position values, scattered: v[0..M) holds lane l's values
+// of positions 0..M-1; on return v[0..P) holds the sums over the column's lanes (equal lane % S)
+// of positions base .. base+P-1, P = M*S/64 (M*S >= 64). Recursive halving, from the lanes
+// 32 apart down to S apart: at each step a lane keeps the lower or the upper half of its
+// positions (by the step's lane bit) and adds its partner's copy of that half. The gfx950 row
+// swaps exchange a pair of halves in one instruction, so the whole reduction is about as many
+// instructions as positions (an all-lanes reduction of every position is S..32 steps each).
+template <int S, int M>
+__device__ __forceinline__ void col_scatter(float (&v)[M], int lane, int& base) {
+    static_assert(M * S >= kWave, "at least one position per lane");
+    base = 0;
+    int c = M;
+#pragma unroll
+    for (int m = 32; m >= S; m >>= 1) {
+        const int h = c / 2;
+        const bool up = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < M / 2; ++i) {
+            if (i < h) {
+                const float a = v[i], b = v[h + i];
+                if (m == 32 || m == 16) {
+                    // the lower row's lanes end with their a and the partner's a, the upper
+                    // row's with the partner's b and their b
+                    const auto r = m == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(a),
+                                                                              __float_as_uint(b),
+                                                                              false, false)
+                                           : __builtin_amdgcn_permlane16_swap(__float_as_uint(a),
+                                                                              __float_as_uint(b),
+                                                                              false, false);
+                    v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+                } else {
+                    const float send = up ? a : b;
+                    const float recv = m == 8 ? dpp_f32<dpp::kRor8>(send) : __shfl_xor(send, m, kWave);
+                    v[i] = (up ? b : a) + recv;
+                }
+            }
+        }
+        base += up ? h : 0;
+        c = h;
+    }
+}
+
 // Zero `count` words of LDS from `p` with the wavefront (a uniform trip count).
 __device__ __forceinline__ void lds_zero(float* p, int count, int lane) {
     for (int e0 = 0; e0 < count; e0 += kWave)
@@ -649,8 +691,70 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
             }
         }
 
-        // the summary before and after each position: q' = q + sum_k (h' - h)[k] / N, written by
-        // one lane per column
+        // the summary before and after each position: q' = q + sum_k (h' - h)[k] / N
+        if constexpr (TB * S >= kWave) {
+            // scattered: lane (g, x) = (lane / S, lane % S) sums, and stores, positions
+            // base .. base+kP-1 of column x (a full-width store per kP positions instead of a
+            // column's eight lanes per position). A run of positions maps q to (rs ? 0 : q) + c
+            // (a reset zeroes q before its position); a scan over the groups, earlier first,
+            // gives each lane the map of the positions before its own.
+            constexpr int kP = TB * S / kWave;
+            constexpr int kG = kWave / S;
+            int base;
+            col_scatter<S, TB>(delta, lane, base);
+            float ctb[kP];
+            if (divn.pow2) {
+#pragma unroll
+                for (int j = 0; j < kP; ++j) ctb[j] = delta[j] * divn.inv;
+            } else {
+#pragma unroll
+                for (int j = 0; j < kP; ++j) ctb[j] = delta[j] / divn.n;
+            }
+            bool rs = false;
+            float c = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kP; ++j) {
+                const int i = base + j;
+                if (i < n) {
+                    if ((rmask >> i) & 1u) {
+                        c = 0.0f;
+                        rs = true;
+                    }
+                    c += ctb[j];
+                }
+            }
+            const int g = lane / S;
+#pragma unroll
+            for (int k = 1; k < kG; k <<= 1) {  // inclusive over the groups 0..g
+                const float ce = __shfl_up(c, k * S, kWave);
+                const int re = __shfl_up(rs ? 1 : 0, k * S, kWave);
+                if (g >= k) {
+                    c = rs ? c : ce + c;
+                    rs = rs || re != 0;
+                }
+            }
+            float cx = __shfl_up(c, S, kWave);
+            int rx = __shfl_up(rs ? 1 : 0, S, kWave);
+            if (g == 0) {
+                cx = 0.0f;
+                rx = 0;
+            }
+            const float c_all = __shfl(c, (kG - 1) * S + x, kWave);
+            const bool rs_all = __shfl(rs ? 1 : 0, (kG - 1) * S + x, kWave) != 0;
+            float q = (rx ? 0.0f : q_run) + cx;
+            const uint32_t qstep = uint32_t(d) * sizeof(OUT);
+            const uint32_t sq = uint32_t(tb0) * qstep;
+#pragma unroll
+            for (int j = 0; j < kP; ++j) {
+                const int i = base + j;
+                const uint32_t vq = i < n ? uint32_t(i) * qstep + uint32_t(col) * sizeof(OUT) : kOob;
+                if (i < n && ((rmask >> i) & 1u)) q = 0.0f;
+                bstore_f32<OUT>(q, rqa, vq, sq);
+                q = i < n ? q + ctb[j] : q;
+                bstore_f32<OUT>(q, rqb, vq, sq);
+            }
+            q_run = (rs_all ? 0.0f : q_run) + c_all;
+        } else {
         col_sums<S>(delta);
         auto summaries = [&](auto pow2_c, auto reset_c) __attribute__((always_inline)) {
             constexpr bool kPow2 = decltype(pow2_c)::value;
@@ -671,6 +775,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
             if (divn.pow2 && rmask == 0u) summaries(std::true_type{}, std::false_type{});
             else if (divn.pow2) summaries(std::true_type{}, std::true_type{});
             else summaries(std::false_type{}, std::true_type{});
+        }
         }
         if (want_max && lane < n)  // lane i sends position tb0 + i's slice max
             atomicMax(reinterpret_cast<unsigned int*>(a.h_max + b * a.hm_row) + (tb0 + lane),
