@@ -238,6 +238,47 @@ __device__ __forceinline__ void write_state(int NS, int t, int stride, Rd rd, Wr
     }
 }
 
+// The wavefront maximum of each of M per-position values, scattered the same way: lane l ends
+// with position l / (64/M) (64/M lanes per position, all with the same value). Halving from the
+// lanes 32 apart (row swaps) down to 2*(64/M)... then a plain exchange for the last steps; the
+// partners inside 8 lanes are the half-mirror and quad permutations (each pairs lanes across
+// the step's bit, with the same positions so far).
+template <int M>
+__device__ __forceinline__ uint32_t max_scatter(uint32_t (&v)[M], int lane) {
+    static_assert(M >= 1 && M <= kWave && (M & (M - 1)) == 0, "M");
+    int c = M;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        auto xchg = [&](uint32_t u) __attribute__((always_inline)) -> uint32_t {
+            if (m == 8) return dpp_u32<dpp::kRor8>(u);
+            if (m == 4) return dpp_u32<dpp::kHalfMirror>(u);
+            if (m == 2) return dpp_u32<dpp::kXor2>(u);
+            return dpp_u32<dpp::kXor1>(u);
+        };
+        if (c > 1) {
+            const int h = c / 2;
+            const bool up = (lane & m) != 0;
+#pragma unroll
+            for (int i = 0; i < M / 2; ++i) {
+                if (i < h) {
+                    const uint32_t a = v[i], b = v[h + i];
+                    if (m == 32 || m == 16) {
+                        const auto r = m == 32 ? __builtin_amdgcn_permlane32_swap(a, b, false, false)
+                                               : __builtin_amdgcn_permlane16_swap(a, b, false, false);
+                        v[i] = umax(static_cast<uint32_t>(r[0]), static_cast<uint32_t>(r[1]));
+                    } else {
+                        v[i] = umax(up ? b : a, xchg(up ? a : b));
+                    }
+                }
+            }
+            c = h;
+        } else {
+            v[0] = umax(v[0], xchg(v[0]));
+        }
+    }
+    return v[0];
+}
+
 template <typename IN, typename OUT, typename SLOT, int S, int TB, bool RES, bool CM>
 __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     using Raw = typename SLOT::Raw;
@@ -679,17 +720,8 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
         };
         if (pad) steps(std::true_type{});
         else steps(std::false_type{});
-        if constexpr (CM) {  // every position's slice maximum, lane i holding position i's
-#pragma unroll
-            for (int i = 0; i < TB; ++i) {
-                uint32_t v = group_max<16>(lmv[i]);
-                RowPair r = pair16(v);
-                v = umax(r.lo, r.hi);
-                r = pair32(v);
-                v = umax(r.lo, r.hi);
-                hmv = lane == i ? v : hmv;
-            }
-        }
+        // CM: every position's slice maximum, lane l holding position l / (64 / TB)'s
+        if constexpr (CM) hmv = max_scatter<TB>(lmv, lane);
 
         // the summary before and after each position: q' = q + sum_k (h' - h)[k] / N
         if constexpr (TB * S >= kWave) {
@@ -777,9 +809,16 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
             else summaries(std::false_type{}, std::true_type{});
         }
         }
-        if (want_max && lane < n)  // lane i sends position tb0 + i's slice max
+        if constexpr (CM) {  // the first lane of each position's group sends its slice max
+            constexpr int kDup = kWave / TB;
+            const int pos = lane / kDup;
+            if (lane % kDup == 0 && pos < n)
+                atomicMax(reinterpret_cast<unsigned int*>(a.h_max + b * a.hm_row) + (tb0 + pos),
+                          hmv);
+        } else if (want_max && lane < n) {  // lane i sends position tb0 + i's slice max
             atomicMax(reinterpret_cast<unsigned int*>(a.h_max + b * a.hm_row) + (tb0 + lane),
                       hmv);
+        }
         if (track_age && x == 0) {  // the cells' last selection (idle and padded: the dummy N)
 #pragma unroll
             for (int i = 0; i < TB; ++i)
