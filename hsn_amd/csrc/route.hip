@@ -358,18 +358,35 @@ __device__ void decide(const RouteArgs& a, int b, int p, int64_t (&ages)[NPL], b
     }
 }
 
-// NaN-propagating wavefront amin / amax (torch's: NaN when any lane holds one). A ballot finds a
-// NaN; the min / max tree (the fold order of wave_nan_min / wave_nan_max) does the rest, so the
-// result equals theirs bit for bit at a third of the instructions.
-__device__ __forceinline__ float wave_amin(float v) {
-    const bool any_nan = ballot(v != v) != 0u;
-    const float m = wave_reduce_f32(v, [](float x, float y) { return fminf(x, y); }, INFINITY);
-    return any_nan ? __int_as_float(0x7fc00000) : m;
+// The order-preserving signed-integer image of a non-NaN float (an involution): non-negative
+// floats keep their bits and negative ones flip their magnitude bits, so -0 (-1) sorts just
+// below +0 (0) and a float min / max is a signed-integer one.
+__device__ __forceinline__ int32_t ford(float f) {
+    const int32_t u = __float_as_int(f);
+    return u ^ ((u >> 31) & 0x7fffffff);
 }
-__device__ __forceinline__ float wave_amax(float v) {
-    const bool any_nan = ballot(v != v) != 0u;
-    const float m = wave_reduce_f32(v, [](float x, float y) { return fmaxf(x, y); }, -INFINITY);
-    return any_nan ? __int_as_float(0x7fc00000) : m;
+__device__ __forceinline__ float ford_inv(int32_t k) {
+    return __int_as_float(k ^ ((k >> 31) & 0x7fffffff));
+}
+// NaN-propagating wavefront amin / amax (torch's: NaN when any lane holds one) of float images:
+// a ballot finds a NaN, the rest is a signed-integer min / max, one DPP instruction a step (a
+// float tree needs the neighbour's value canonicalised first). Of -0 and +0 the min is -0 and
+// the max +0, whichever lane holds them.
+__device__ __forceinline__ float wave_amin_k(int32_t k, bool nan) {
+    const bool any_nan = ballot(nan) != 0u;
+    const uint32_t m = wave_reduce_u32(
+        static_cast<uint32_t>(k),
+        [](uint32_t x, uint32_t y) { return static_cast<int32_t>(x) < static_cast<int32_t>(y) ? x : y; },
+        static_cast<uint32_t>(ford(INFINITY)));
+    return any_nan ? __int_as_float(0x7fc00000) : ford_inv(static_cast<int32_t>(m));
+}
+__device__ __forceinline__ float wave_amax_k(int32_t k, bool nan) {
+    const bool any_nan = ballot(nan) != 0u;
+    const uint32_t m = wave_reduce_u32(
+        static_cast<uint32_t>(k),
+        [](uint32_t x, uint32_t y) { return static_cast<int32_t>(x) > static_cast<int32_t>(y) ? x : y; },
+        static_cast<uint32_t>(ford(-INFINITY)));
+    return any_nan ? __int_as_float(0x7fc00000) : ford_inv(static_cast<int32_t>(m));
 }
 
 // A lane's NPL consecutive logits as one buffer load (the row's resource bounds it).
@@ -547,10 +564,11 @@ __device__ void decide_sorted(const RouteArgs& a, int b, int p, uint4* ent, uint
     const uint64_t vmask = ballot(ok);
 
     // the threshold (as decide)
-    const float low = wave_amin((ok && my_cell >= R) ? my_score : INFINITY);
+    const bool in_low = ok && my_cell >= R;
+    const float low = wave_amin_k(in_low ? ford(my_score) : ford(INFINITY), in_low && my_score != my_score);
     const uint64_t full = K >= kWave ? ~0ull : (1ull << K) - 1ull;
     const bool all_valid = vmask == full;  // then an entry is selected when it was taken
-    float high = -INFINITY;
+    int32_t hk = ford(-INFINITY);
     bool high_nan = false;
 #pragma unroll
     for (int i = 0; i < NPL; ++i) {
@@ -562,10 +580,10 @@ __device__ void decide_sorted(const RouteArgs& a, int b, int p, uint4* ent, uint
             sel = so > 0u && ((vmask >> (so - 1u)) & 1ull);
         }
         const bool out = (nn[i] < N) & !sel;
-        high = fmaxf(high, out ? sc[i] : -INFINITY);
+        hk = max(hk, out ? ford(sc[i]) : ford(-INFINITY));
         high_nan = high_nan | (out & (sc[i] != sc[i]));
     }
-    high = wave_amax(high_nan ? __int_as_float(0x7fc00000) : high);
+    const float high = wave_amax_k(hk, high_nan);
     const float th = 0.5f * (low + high);
 
     if (is_slot) {
