@@ -1263,6 +1263,9 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                 }
             }
         }
+        // the replay's later inputs, issued before the barrier: a stall at issue (the earlier
+        // half is still in flight) then overlaps the wait for the other chunks
+        if constexpr (RES) fetch_c(t_begin, 0, TB / 2);
         __syncthreads();
     } else {
         for (int e0 = 0; e0 < NS; e0 += kWave) {
@@ -1271,7 +1274,6 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
         }
     }
     if (lane == 0) st[NS] = 0.0f;  // the dummy: idle lanes read it as a zero cotangent
-    if constexpr (RES) fetch_c(t_begin, 0, TB / 2);  // the replay's later inputs
 
     // phase C: the replay with the outputs, latest position first
     const rsrc_t rdy = make_rsrc(static_cast<IN*>(a.dy) + base, row_bytes);
