@@ -455,12 +455,6 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
                 for (int i = 0; i < TB; ++i) {
                     if (i + kAhead < TB) fetch_at(i + kAhead, tb0);
                     pad_lane |= prep(i, kFull || i < n);  // the loads of position i arrive in order
-                    // RES: the cells' last selection for the ages here, where the position's
-                    // cell is first known and the LDS waits on memory (in the replay it would
-                    // hold only slice 0's workgroups up, behind the replay's own LDS traffic)
-                    if constexpr (RES)
-                        if (track_age && x == 0 && (kFull || i < n))
-                            atomicMax(&last[(ca[i] - rb) / (4u * S)], tb0 + i);
                     if (i >= start) {
                         float& al = lds_at(lds, ca[i]);
                         float& be = lds_at(lds, ca[i] + boff);
@@ -825,7 +819,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
             atomicMax(reinterpret_cast<unsigned int*>(a.h_max + b * a.hm_row) + (tb0 + lane),
                       hmv);
         }
-        if (!RES && track_age && x == 0) {  // the cells' last selection (idle and padded: the dummy N)
+        if (track_age && x == 0) {  // the cells' last selection (idle and padded: the dummy N)
 #pragma unroll
             for (int i = 0; i < TB; ++i)
                 if (i < n) atomicMax(&last[(ca[i] - rb) / (4u * S)], tb0 + i);
