@@ -87,6 +87,11 @@ ROUTE_CASES = [
     (1, 3, 4096, 1, 32, dict(), torch.bfloat16, "zipf"),
     (2, 3, 33, 2, 33, dict(limit=0.75), torch.float32, "zeros"),
     (2, 2, 64, 1, 64, dict(), torch.float32, "plain"),
+    # one unit: N % 4 != 0 at four cells a lane (scalar loads) with a cost term (the product and
+    # the difference rounded apart); bf16 runs of two and four cells a lane (vector loads)
+    (2, 4, 130, 1, 8, dict(lambda_cost=0.05), torch.float32, "ties"),
+    (2, 4, 100, 1, 6, dict(reserved=2), torch.bfloat16, "nan"),
+    (2, 3, 200, 1, 8, dict(), torch.bfloat16, "plain"),
 ]
 
 
