@@ -114,7 +114,8 @@ def main() -> int:
     args = _args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the window path "
-              "shards over rows with no exchange, see DESIGN.md", file=sys.stderr)
+              "shards over rows (each GPU owns whole rows, no exchange), so one GPU's rate "
+              "times N is the job's", file=sys.stderr)
         return 2
     import torch
 
