@@ -142,7 +142,7 @@ def main() -> int:
         if ev:
             ev[1].record()
         out = window.forward(w["y"], w["gate_pre"], w["reset"], slots, w["h0"], w["q0"],
-                             w["age0"], w["pos0"], N, h_max=h_max)
+                             w["age0"], w["pos0"], N, h_max=h_max, h_max_zeroed=True)
         if ev:
             ev[2].record()
         grads = window.backward(w["y"], w["gate_pre"], out["h_old"], slots, w["reset"], N,

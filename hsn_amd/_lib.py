@@ -34,6 +34,7 @@ P, I, F, L = c_void_p, c_int, c_float, c_int64
 SIGNATURES: dict[str, list] = {
     "hsn_win_abi_version": [],
     "hsn_win_last_error": [],
+    "hsn_win_supports": [I, I, I, I, I, I],
     "hsn_win_route": [P, I, L, P, P, P, P, P, I, P, P, P, P, P, I, I, I, I, I, I, I, F, F, F, F, I,
                       I, P],
     "hsn_win_select": [P, I, L, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, F, F, F, F, I, I, P],
@@ -81,6 +82,18 @@ def call(name: str, *args) -> None:
     if status != HSN_OK:
         message = lib.hsn_win_last_error().decode(errors="replace")
         raise RuntimeError(f"{name}: {STATUS.get(status, status)}: {message}")
+
+
+OP_FORWARD, OP_BACKWARD, OP_RECURRENCE, OP_CELL_UPDATE, OP_ROUTE = 0, 1, 2, 3, 4
+
+
+def unsupported(op: int, B: int, T: int, N: int, d: int, K: int) -> str | None:
+    """Why entry point ``op`` does not take this shape (``None``: it does), from the library's
+    own geometry (``hsn_win_supports``; host arithmetic only, no GPU)."""
+    lib = library()
+    if lib.hsn_win_supports(op, B, T, N, d, K) == HSN_OK:
+        return None
+    return lib.hsn_win_last_error().decode(errors="replace")
 
 
 def ptr(t) -> int | None:

@@ -707,8 +707,11 @@ extern "C" int hsn_win_route(const void* logits, int io_dtype, int64_t width, co
                 "hsn_win_route: need K <= N and K <= 64");
     HSN_REQUIRE(N <= 64 * kWave, HSN_ERR_INVALID_ARGUMENT, "hsn_win_route: N above 4096");
     HSN_REQUIRE(width >= M, HSN_ERR_INVALID_ARGUMENT, "hsn_win_route: width < M");
-    HSN_REQUIRE(reserved >= 0 && reserved <= K, HSN_ERR_INVALID_ARGUMENT,
-                "hsn_win_route: reserved must lie in [0, K]");
+    // the router's own checks (python/hsn/model/router.py:1328-1339)
+    HSN_REQUIRE(reserved >= 0 && (reserved == 0 || reserved < K), HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_route: reserved must be 0 or lie in [1, K)");
+    HSN_REQUIRE(!reserved_units || reserved > 0, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_route: reserved_units needs reserved > 0");
     HSN_REQUIRE(index_bits == 32 || index_bits == 64, HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_route: index_bits must be 32 or 64");
     HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
@@ -759,8 +762,11 @@ extern "C" int hsn_win_select(const void* logits, int io_dtype, int64_t width, c
     HSN_REQUIRE(width >= M, HSN_ERR_INVALID_ARGUMENT, "hsn_win_select: width < M");
     HSN_REQUIRE(t >= 0 && t < n_out && (!probes || (age && t < n_age)), HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_select: record t outside the tapes (or probes without ages)");
-    HSN_REQUIRE(reserved >= 0 && reserved <= K, HSN_ERR_INVALID_ARGUMENT,
-                "hsn_win_select: reserved must lie in [0, K]");
+    // the router's own checks (python/hsn/model/router.py:1328-1339)
+    HSN_REQUIRE(reserved >= 0 && (reserved == 0 || reserved < K), HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_select: reserved must be 0 or lie in [1, K)");
+    HSN_REQUIRE(!reserved_units || reserved > 0, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_select: reserved_units needs reserved > 0");
     HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
                 HSN_ERR_UNSUPPORTED_DTYPE, "hsn_win_select: logits must be f32 or bf16");
     RouteArgs a{};

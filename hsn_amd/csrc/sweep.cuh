@@ -456,10 +456,12 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
                     if (i + kAhead < TB) fetch_at(i + kAhead, tb0);
                     pad_lane |= prep(i, kFull || i < n);  // the loads of position i arrive in order
                     if (i >= start) {
+                        // alpha's sign bit marks a cell written in the chunk (a plain 1 or the
+                        // restart's 0 is unwritten): -(omb |alpha|), free input modifiers
                         float& al = lds_at(lds, ca[i]);
                         float& be = lds_at(lds, ca[i] + boff);
                         const float va = al, vbe = be;
-                        al = omb[i] * va;
+                        al = -omb[i] * fabsf(va);
                         be = omb[i] * vbe + bcv[i];
                     }
                 }
@@ -470,9 +472,15 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
         if (lane == 0) rflag[w] = any_reset ? 1 : 0;
         __syncthreads();
 
-        // phase B: every chunk's start state (into its alpha's place), and its column sums.
-        // Chunk by chunk over all of the lane's elements, so each chunk's reads are in flight
-        // together (a chunk's store may alias the next chunk's reads as far as the compiler knows).
+        // phase B: every chunk's start state (into its alpha's place), and the summary's change
+        // over each chunk. Chunk by chunk over all of the lane's elements, so each chunk's reads
+        // are in flight together (a chunk's store may alias the next chunk's reads as far as the
+        // compiler knows). A chunk that resets ends at beta whatever its start (a select, not
+        // 0 * h: a NaN in the start state must not cross the reset, as the reference's
+        // masked_fill). The summary moves only by the deltas of written cells (q' = q + sum of
+        // the slots' deltas / N), so a chunk adds the sum of its written cells' end - start, or,
+        // after a reset, restarts from the sum of its end state: an unwritten NaN or inf cell
+        // reaches neither.
         float ps[kMaxChunks];
 #pragma unroll
         for (int j = 0; j < kMaxChunks; ++j) ps[j] = 0.0f;
@@ -484,6 +492,7 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
             for (int j = 0; j < kMaxChunks; ++j) {
                 if (j < W) {
                     float* sj = lds + j * a.region;
+                    const bool rj = rflag[j] != 0;
                     float al[kPre], be[kPre];
 #pragma unroll
                     for (int q = 0; q < kPre; ++q) {
@@ -495,8 +504,10 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
                     for (int q = 0; q < kPre; ++q) {  // past the end: the dummy word
                         const int e = g0 + q * kWave * W + gl;
                         sj[min(e, NS)] = h[q];
-                        ps[j] += e < NS ? h[q] : 0.0f;
-                        h[q] = al[q] * h[q] + be[q];
+                        const float hn = rj ? be[q] : fabsf(al[q]) * h[q] + be[q];
+                        const float dq = rj ? hn : (signbit(al[q]) ? hn - h[q] : 0.0f);
+                        ps[j] += e < NS ? dq : 0.0f;
+                        h[q] = hn;
                     }
                 }
             }
@@ -507,15 +518,13 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
             if (j < W && lane < S) part[(w * W + j) * S + lane] = ps[j];
         __syncthreads();
         if (w > 0) {
-            float cs_w = 0.0f, cs_0 = 0.0f;
-            for (int wp = 0; wp < W; ++wp) {
-                cs_w += part[(wp * W + w) * S + x];
-                cs_0 += part[(wp * W) * S + x];
+            float q = q_run;  // q0, then the summary at each earlier chunk's end
+            for (int j = 0; j < w; ++j) {
+                float cs = 0.0f;
+                for (int wp = 0; wp < W; ++wp) cs += part[(wp * W + j) * S + x];
+                q = (rflag[j] != 0 ? 0.0f : q) + divn(cs);
             }
-            bool reset_before = false;
-            for (int j = 0; j < w; ++j) reset_before |= rflag[j] != 0;
-            // q - sum_n h[n] / N is constant between resets, zero after one
-            q_run = (reset_before ? 0.0f : q_run - divn(cs_0)) + divn(cs_w);
+            q_run = q;
         }
     } else {
         for (int e0 = 0; e0 < NS; e0 += kWave) {
@@ -1248,11 +1257,12 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
                         mu[q] = sj[e];
                         nu[q] = sj[NS + 1 + e];
                     }
+                    const bool rj = rf[j] != 0;  // a reset in the chunk: A before it is nu
 #pragma unroll
                     for (int q = 0; q < kPre; ++q) {  // past the end: the dummy word
                         const int e = g0 + q * kWave * W + gl;
                         sj[min(e, NS)] = A[q];
-                        A[q] = mu[q] * A[q] + nu[q];
+                        A[q] = rj ? nu[q] : mu[q] * A[q] + nu[q];  // a select: no 0 * NaN
                     }
                 }
             }
@@ -1378,6 +1388,12 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
 // quantity of the round, computed from inputs only), an epilogue applies the norm's VJP.
 // ------------------------------------------------------------------------------------------
 
+// The RMS workspace: [slots, d] of the storage type, then [slots] fp32 of 1/rms at a 16-byte
+// aligned offset.
+inline size_t rms_inv_offset(int64_t slots, int d, size_t elem) {
+    return (size_t(slots) * size_t(d) * elem + 15) & ~size_t(15);
+}
+
 // ynorm[s, x] = y[s, x] * inv[s] * w[x],  inv[s] = rsqrt(mean_x y^2 + eps): a wavefront per slot
 template <typename IN>
 __global__ __launch_bounds__(256) void rms_prologue(const IN* y, const float* w, IN* ynorm,
@@ -1484,21 +1500,15 @@ inline DivN make_divn(int N) {
     return v;
 }
 
-// Raise a kernel's dynamic-LDS limit to the full 160 KiB once per process and device (not a
-// stream operation, and never repeated inside a stream capture).
+// Raise a kernel's dynamic-LDS limit to the full 160 KiB once per (kernel, device) and process
+// (not a stream operation, and never repeated inside a stream capture). Every instantiation is
+// its own kernel, so the record is keyed by the kernel's address.
+hipError_t allow_lds_raw(const void* kernel, size_t lds);
+
 template <typename K>
 hipError_t allow_lds(K kernel, size_t lds) {
     if (lds <= 64 * 1024) return hipSuccess;
-    constexpr int kMaxDevices = 64;
-    static bool done[kMaxDevices] = {};
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    if (dev >= 0 && dev < kMaxDevices && done[dev]) return hipSuccess;
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, int(kLdsMax));
-    if (e == hipSuccess && dev >= 0 && dev < kMaxDevices) done[dev] = true;
-    return e;
+    return allow_lds_raw(reinterpret_cast<const void*>(kernel), lds);
 }
 
 template <typename IN, typename OUT, typename SLOT, int S>

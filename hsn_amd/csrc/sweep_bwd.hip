@@ -85,7 +85,7 @@ extern "C" int hsn_win_backward(const void* y, const void* gate_pre, const void*
     const void* pre = y;
     float* inv = nullptr;
     if (cand_norm) {  // the normalised candidate input (the forward's, recomputed)
-        inv = reinterpret_cast<float*>(static_cast<char*>(rms_scratch) + nslots * d * elem);
+        inv = reinterpret_cast<float*>(static_cast<char*>(rms_scratch) + rms_inv_offset(nslots, d, elem));
         const int blocks = static_cast<int>((nslots + 3) / 4);
         if (io_dtype == HSN_DTYPE_F32)
             hipLaunchKernelGGL((rms_prologue<float>), dim3(blocks), dim3(256), 0, st,

@@ -8,12 +8,12 @@ using namespace hsn;
 namespace {
 
 // The RMS candidate's prologue: writes the normalised candidate input into the workspace
-// (layout: [slots, d] of the storage type, then [slots] fp32 of 1/rms) and returns it.
+// (layout: rms_inv_offset) and returns it.
 const void* rms_normalise(const void* y, int io_dtype, const float* cand_w, float cand_eps,
                           void* scratch, int64_t slots, int d, hipStream_t st) {
     const int blocks = static_cast<int>((slots + 3) / 4);
     const size_t elem = io_dtype == HSN_DTYPE_F32 ? 4 : 2;
-    float* inv = reinterpret_cast<float*>(static_cast<char*>(scratch) + slots * d * elem);
+    float* inv = reinterpret_cast<float*>(static_cast<char*>(scratch) + rms_inv_offset(slots, d, elem));
     if (io_dtype == HSN_DTYPE_F32)
         hipLaunchKernelGGL((rms_prologue<float>), dim3(blocks), dim3(256), 0, st,
                            static_cast<const float*>(y), cand_w, static_cast<float*>(scratch), inv,
@@ -138,5 +138,40 @@ extern "C" int hsn_win_cell_update(const void* y, const void* gate, int io_dtype
         HSN_HIP((launch_fwd<float, float, Cells64>(a, g.S, lds, st)));
     else
         HSN_HIP((launch_fwd<bf16_t, float, Cells64>(a, g.S, lds, st)));
+    HSN_ABI_END
+}
+
+extern "C" int hsn_win_supports(int op, int B, int T, int N, int d, int K) {
+    HSN_ABI_BEGIN
+    HSN_REQUIRE(B >= 1 && T >= 1 && N >= 1 && d >= 1 && K >= 1, HSN_ERR_INVALID_ARGUMENT,
+                "dimensions must be >= 1");
+    Geometry g;
+    switch (op) {
+        case HSN_OP_FORWARD:
+        case HSN_OP_CELL_UPDATE: {
+            const int t = op == HSN_OP_FORWARD ? T : 1;
+            HSN_REQUIRE(K <= N, HSN_ERR_INVALID_ARGUMENT, "K exceeds N");
+            HSN_REQUIRE(choose_geometry(B, t, N, d, K, fwd_lds_bytes, g),
+                        HSN_ERR_INVALID_ARGUMENT,
+                        "no state slice fits the LDS with one slot per lane (N or K too large)");
+            break;
+        }
+        case HSN_OP_BACKWARD:
+        case HSN_OP_RECURRENCE:
+            HSN_REQUIRE(op == HSN_OP_RECURRENCE || K <= N, HSN_ERR_INVALID_ARGUMENT,
+                        "K exceeds N");
+            HSN_REQUIRE(choose_geometry(B, T, N, d, K, bwd_lds_bytes, g),
+                        HSN_ERR_INVALID_ARGUMENT,
+                        "no cotangent slice fits the LDS with one slot per lane (N or K too large)");
+            break;
+        case HSN_OP_ROUTE:
+            HSN_REQUIRE(K <= N, HSN_ERR_INVALID_ARGUMENT, "K exceeds N");
+            HSN_REQUIRE(K <= kWave, HSN_ERR_INVALID_ARGUMENT, "K above 64 (one lane per slot)");
+            HSN_REQUIRE(N <= 64 * kWave, HSN_ERR_INVALID_ARGUMENT,
+                        "N above 4096 (64 cells per lane)");
+            break;
+        default:
+            HSN_REQUIRE(false, HSN_ERR_INVALID_ARGUMENT, "unknown op");
+    }
     HSN_ABI_END
 }

@@ -19,15 +19,9 @@ from torch import Tensor
 from .. import _lib
 from .._lib import DTYPE_BF16, DTYPE_F32, call, ptr, stream_of
 from ..state import CellGraphState
+from ..window import check_reserved, rms_scratch_bytes
 
 _prepared: set[int] = set()
-
-#: LDS per workgroup on gfx950
-_MAX_LDS_BYTES = 160 * 1024
-#: the router's limits: one 64-lane wavefront per position, cells 64 per lane at most
-_MAX_SELECT_CELLS = 4096
-_MAX_SELECT_K = 64
-
 
 def available() -> bool:
     """Library presence and freshness only: never initialises the GPU."""
@@ -44,10 +38,6 @@ def prepared(device: torch.device) -> bool:
     return device.type == "cuda" and (device.index or 0) in _prepared
 
 
-def _slice_fits(n_cells: int, extra_per_cell: int = 0) -> bool:
-    return n_cells * (4 + extra_per_cell) <= _MAX_LDS_BYTES
-
-
 # --------------------------------------------------------------------------------------------
 # the backward recurrence (reference window.py:108-192)
 # --------------------------------------------------------------------------------------------
@@ -62,7 +52,7 @@ def _recurrence(c, b, h_old, cells, valid, reset, n_cells, d_q_pre, d_q_post, d_
             return None
     B, T, K, d = (int(n) for n in c.shape)
     N = int(n_cells)
-    if not _slice_fits(N):
+    if _lib.unsupported(_lib.OP_RECURRENCE, B, T, N, d, K) is not None:
         return None
     dc = torch.empty(B, T, K, d, dtype=torch.float32, device=c.device)
     db = torch.empty_like(dc)
@@ -129,6 +119,7 @@ def _io(t: Tensor) -> int:
 def _launch_select(logits, width, n_units, age, cost, cells, units, valid, theta, refreshed, t,
                    n_out, n_age, B, N, k, age_max, probes, lambda_cost, cell_overhead,
                    shared_cost, limit, reserved, reserved_units):
+    check_reserved(int(k), reserved, bool(reserved_units))
     call("hsn_win_select", ptr(logits), _io(logits), int(width), ptr(age) if probes else None,
          ptr(cost), ptr(cells), ptr(units), ptr(valid), ptr(theta), ptr(refreshed), B, N,
          int(n_units), int(k), int(t), int(n_out), int(n_age), int(age_max), int(bool(probes)),
@@ -217,14 +208,10 @@ def _select_fold_fake(scored, age, cost, cells, units, valid, theta, refreshed, 
 
 
 def select_unsupported(n_cells: int, k: int, n_units: int = 1) -> Optional[str]:
-    """Why :func:`select` cannot take a model of this shape (``None``: it can)."""
-    if n_cells > _MAX_SELECT_CELLS:
-        return f"model.n_cells={n_cells}: at most {_MAX_SELECT_CELLS} cells (64 per lane)"
-    if k > n_cells:
-        return f"k_select={k} exceeds model.n_cells={n_cells}"
-    if k > _MAX_SELECT_K:
-        return f"k_select={k}: one lane per slot of a 64-lane wavefront"
-    return None
+    """Why :func:`select` cannot take a model of this shape (``None``: it can), by the
+    library's own checks (reference window.py:557-565)."""
+    why = _lib.unsupported(_lib.OP_ROUTE, 1, 1, int(n_cells), 1, int(k))
+    return None if why is None else f"model.n_cells={n_cells}, k_select={k}: {why}"
 
 
 def select(logits: Tensor, age: Tensor, cost_table: Tensor, *, k: int, age_max: int, probes: bool,
@@ -269,7 +256,8 @@ def _launch_update(y, gate, cand_w, cand_norm, cand_eps, h, q, age, pos, cells, 
     scratch = None
     if cand_norm:
         elem = 4 if y.dtype == torch.float32 else 2
-        scratch = torch.empty(B * K * (d * elem + 4), dtype=torch.uint8, device=y.device)
+        scratch = torch.empty(rms_scratch_bytes(B * K, d, elem), dtype=torch.uint8,
+                              device=y.device)
     call("hsn_win_cell_update", ptr(y), ptr(gate), _io(y), ptr(cand_w) if cand_norm else None,
          int(bool(cand_norm)), float(cand_eps), ptr(scratch), ptr(h), ptr(q), ptr(age), ptr(pos),
          ptr(cells), ptr(valid), ptr(h_next), ptr(q_next), ptr(age_next), ptr(pos_next),
@@ -327,14 +315,10 @@ def _update_tape_fake(y, gate, tape_h, tape_q, tape_age, cells, valid, cand_w, r
 
 
 def cell_update_unsupported(n_cells: int, d: int, k: int) -> Optional[str]:
-    """Why :func:`cell_update` cannot take a model of this shape (``None``: it can)."""
-    if k > n_cells:
-        return f"k_select={k} exceeds model.n_cells={n_cells}"
-    if k > 8 * 64:
-        return f"k_select={k}: at most 8 slots per lane"
-    if not _slice_fits(n_cells, 8):
-        return f"model.n_cells={n_cells}: the state slice does not fit the LDS"
-    return None
+    """Why :func:`cell_update` cannot take a model of this shape (``None``: it can), by the
+    library's own geometry (reference window.py:626-640)."""
+    why = _lib.unsupported(_lib.OP_CELL_UPDATE, 1, 1, int(n_cells), int(d), int(k))
+    return None if why is None else f"model.n_cells={n_cells}, d={d}, k_select={k}: {why}"
 
 
 def _cand(cell):

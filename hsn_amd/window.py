@@ -30,6 +30,7 @@ BUDGET_SLACK = 1e-5
 __all__ = [
     "BUDGET_SLACK",
     "RouteConfig",
+    "check_reserved",
     "route",
     "forward",
     "backward",
@@ -54,6 +55,20 @@ class RouteConfig:
     limit: float = 1.0 + BUDGET_SLACK
     reserved: int = 0
     reserved_units: bool = False
+
+    def __post_init__(self):
+        check_reserved(self.k, self.reserved, self.reserved_units)
+
+
+def check_reserved(k: int, reserved: int, reserved_units: bool) -> None:
+    """The router's checks of the fast cells (``python/hsn/model/router.py:1328-1339``):
+    ``reserved`` an int in ``[0, k)``, and ``reserved_units`` only with ``reserved > 0``."""
+    if isinstance(reserved, bool) or not isinstance(reserved, int) or reserved < 0:
+        raise ValueError(f"reserved must be an int >= 0, got {reserved!r}")
+    if reserved and reserved >= k:
+        raise ValueError(f"reserved={reserved} must be < k_max={k}")
+    if not reserved and reserved_units:
+        raise ValueError("reserved_units needs reserved > 0")
 
 
 def _io_code(dtype: torch.dtype) -> int:
@@ -124,19 +139,27 @@ def pack_slots(cells: Tensor, valid: Tensor) -> Tensor:
     return torch.where(valid, cells.to(torch.int32), torch.full_like(cells, -1, dtype=torch.int32))
 
 
+def rms_scratch_bytes(slots: int, d: int, elem: int) -> int:
+    """Bytes of the RMS candidate's workspace: ``[slots, d]`` of the storage type, then
+    ``[slots]`` fp32 at the next 16-byte boundary (``include/hsn_window.h``)."""
+    return ((slots * d * elem + 15) & ~15) + 4 * slots
+
+
 def _rms_scratch(slots: int, d: int, io: torch.dtype, dev) -> Tensor:
     elem = 4 if io == torch.float32 else 2
-    return torch.empty(slots * (d * elem + 4), dtype=torch.uint8, device=dev)
+    return torch.empty(rms_scratch_bytes(slots, d, elem), dtype=torch.uint8, device=dev)
 
 
 def forward(y: Tensor, gate_pre: Tensor, reset: Tensor, slots: Tensor, h0: Tensor, q0: Tensor,
             age0: Tensor, pos0: Tensor, n_cells: int, *, cand_norm: bool = False,
             cand_w: Optional[Tensor] = None, cand_eps: float = 1e-6,
-            h_max: Optional[Tensor] = None) -> dict:
+            h_max: Optional[Tensor] = None, h_max_zeroed: bool = False) -> dict:
     """The forward sweep from given decisions (``slots [B,T,K]`` int32, see :func:`route`).
     Returns ``q_pre, q_post [B,T,d]``,
     ``h_sel, h_old [B,T,K,d]`` (storage dtype), the end state ``h [B,N,d], q [B,d]`` (fp32),
-    ``age [B,N], pos [B]`` (int64) and ``h_max [B,T]`` when a zeroed buffer is passed."""
+    ``age [B,N], pos [B]`` (int64) and, when a buffer ``h_max [B,T]`` is passed, the row maxima
+    in it. The sweep max-reduces into that buffer, so it is zeroed here first unless
+    ``h_max_zeroed`` says :func:`route` already did (its ``h_max_zero``)."""
     B, T, K, d = (int(s) for s in y.shape)
     N = int(n_cells)
     dev, io = y.device, y.dtype
@@ -166,6 +189,8 @@ def forward(y: Tensor, gate_pre: Tensor, reset: Tensor, slots: Tensor, h0: Tenso
     }
     if h_max is not None:
         _check(h_max, "h_max", (B, T), torch.float32, dev)
+        if not h_max_zeroed:
+            h_max.zero_()
         out["h_max"] = h_max
     call("hsn_win_forward", ptr(y), ptr(gate_pre), _io_code(io), ptr(cand_w) if cand_norm else None,
          int(bool(cand_norm)), float(cand_eps), ptr(scratch), ptr(reset), ptr(slots),
@@ -234,7 +259,7 @@ def window_forward(logits: Tensor, y: Tensor, gate_pre: Tensor, reset: Tensor, h
                                                          age0=age0, h_max_zero=h_max,
                                                          with_slots=True)
     out = forward(y, gate_pre, reset, slots, h0, q0, age0, pos0, N, cand_norm=cand_norm,
-                  cand_w=cand_w, cand_eps=cand_eps, h_max=h_max)
+                  cand_w=cand_w, cand_eps=cand_eps, h_max=h_max, h_max_zeroed=True)
     out.update(cells=cells, units=units, valid=valid, theta=theta, refreshed=refreshed,
                slots=slots)
     return out

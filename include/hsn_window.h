@@ -50,6 +50,21 @@ int hsn_win_abi_version(void);
 const char* hsn_win_last_error(void);
 
 /*
+ * Whether an entry point takes a shape, decided on the host by the launchers' own checks and
+ * geometry (no GPU work, no launch): HSN_OK, or HSN_ERR_INVALID_ARGUMENT with the reason in
+ * hsn_win_last_error(). This is what the Python wrappers consult to decline (return None) as
+ * the reference's wrappers do (python/hsn/kernels/window.py:119-128,557-565,626-640).
+ *   op: HSN_OP_FORWARD, HSN_OP_BACKWARD, HSN_OP_RECURRENCE, HSN_OP_CELL_UPDATE, HSN_OP_ROUTE
+ *   (hsn_win_route and hsn_win_select); T is ignored for the per-position ops.
+ */
+#define HSN_OP_FORWARD 0
+#define HSN_OP_BACKWARD 1
+#define HSN_OP_RECURRENCE 2
+#define HSN_OP_CELL_UPDATE 3
+#define HSN_OP_ROUTE 4
+int hsn_win_supports(int op, int B, int T, int N, int d, int K);
+
+/*
  * Router: the hard top-k decision of every position of a window.
  * Replaces the per-position `hsn_win_select` launches of the fused sweep
  * (reference kernels/cuda/hsn_window.cu:533-749, wrapper python/hsn/kernels/window.py:356-423)
@@ -103,7 +118,8 @@ int hsn_win_select(const void* logits, int io_dtype, int64_t width, const int64_
  * python/hsn/kernels/native.py:244-303; python/hsn/model/state.py:267-324).
  *   y, gate_pre [B,T,K,d] io_dtype: candidate input and write-gate pre-activation
  *   c = tanh(y) (cand_norm 0) or tanh(y * rsqrt(mean_d(y^2) + cand_eps) * cand_w) (cand_norm 1,
- *   cand_w [d] f32, rms_scratch a workspace of B*T*K*(d*sizeof(io) + 4) bytes); b = sigmoid
+ *   cand_w [d] f32, rms_scratch a workspace of R(B*T*K) bytes, R(s) = align16(s*d*sizeof(io)) + 4*s);
+ *   b = sigmoid
  *   reset [B,T] u8; slots [B,T,K] int32 (hsn_win_route's packed decision: cell or -1)
  *   h0 [B,N,d], q0 [B,d] f32; age0 [B,N], pos0 [B] int64
  * Outputs (each optional): q_pre, q_post [B,T,d] io_dtype (summary before / after each
@@ -170,7 +186,7 @@ int hsn_win_recurrence_dense(const float* c, const float* b, const float* h_old,
  * kernels/cuda/hsn_window.cu:751-954 `hsn_win_cell_update`, wrappers cell_update_op /
  * update_tape_op (python/hsn/kernels/window.py:605-760).
  *   y [B,K,d], gate [B,K,d] io_dtype (the round's products); cand_w [d] f32 (cand_norm 1;
- *   rms_scratch a workspace of B*K*(d*sizeof(io) + 4) bytes)
+ *   rms_scratch a workspace of R(B*K) bytes, R as in hsn_win_forward)
  *   h [B,n_state,N,d], q [B,n_state,d] f32, age [B,n_state,N] int64: record t read
  *   pos [B] int64 (optional), cells [B,n_slot,K] int64, valid [B,n_slot,K] u8: record t
  *   h_next, q_next, age_next: record t_out written (may be the buffers above, t_out != t);

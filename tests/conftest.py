@@ -55,3 +55,20 @@ def _single_thread_torch():
 
     torch.set_num_threads(int(os.environ.get("HSN_TEST_THREADS", "4")))
     yield
+
+
+def nan_state_window(N=16, d=8, K=2, T=6, seed=31):
+    """A window whose start state holds a NaN in a cell no slot ever writes (its logits are
+    -inf), with a reset at position 3 of row 1: row 0's maxima are NaN throughout, row 1's until
+    the reset and finite from there."""
+    import torch
+
+    from hsn_amd.workload import CONFIGS, make_window
+
+    cfg = CONFIGS["tiny"].scaled(B=2, T=T, N=N, d=d, K=K, h0_sigma=0.3, reset_at=((1, 3),))
+    w = make_window(cfg, seed)
+    quiet = N - 2
+    w["logits"][:, :, quiet] = float("-inf")
+    w["h0"][:, quiet, d // 2] = float("nan")
+    w["q0"] = torch.where(torch.isnan(w["h0"]), torch.zeros_like(w["h0"]), w["h0"]).mean(dim=1)
+    return cfg, w, quiet

@@ -1,0 +1,227 @@
+"""The drop-in boundary's contract on the GPU, as the reference's kernel tests check it:
+``torch.library.opcheck`` of every custom op (schema, fake tensor, autograd registration,
+mutation annotations), the first dispatch of every op on a fresh thread
+(``tests/kernels/test_p2_10_cuda.py:100-131``), and the tape forms walked over a block of
+positions against the plain per-position ops bit for bit, with resets at the block's first,
+interior and last positions and two in a row (``tests/kernels/test_p2_10_window.py:453-537``).
+GPU only.
+"""
+
+from __future__ import annotations
+
+from concurrent.futures import ThreadPoolExecutor
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def mods(cuda_device):
+    from hsn_amd.kernels import ops, window
+
+    assert window.available(), "the HIP library must be built for the GPU tests"
+    window.prepare(0)
+    return ops, window
+
+
+def _cases(dev):
+    """Small inputs for every custom op: name -> (op, args, differentiable argument names)."""
+    from hsn_amd.kernels import ops, window
+
+    g = torch.Generator().manual_seed(5)
+    B, N, d, K, M, n = 3, 12, 8, 3, 2, 4
+    f = lambda *s: torch.randn(*s, generator=g).to(dev)  # noqa: E731
+    idx = torch.stack([torch.randperm(N, generator=g)[:K] for _ in range(B)]).to(dev)
+    valid = torch.ones(B, K, dtype=torch.int32, device=dev)
+    valid[1, 2] = 0
+    logits = f(B, N, M)
+    age = torch.randint(0, 5, (B, N), generator=g).to(dev)
+    tape_age = torch.randint(0, 5, (B, n + 1, N), generator=g).to(dev)
+    cost = torch.tensor([0.03125, 0.0625], device=dev)
+    sel = (2, True, 0.0, 0.0, 0.0, 1.0 + 1e-5, 0, False)  # age_max .. reserved_units
+
+    def tapes():
+        return (torch.zeros(B, n, K, dtype=torch.int64, device=dev),
+                torch.zeros(B, n, K, dtype=torch.int64, device=dev),
+                torch.zeros(B, n, K, dtype=torch.bool, device=dev),
+                torch.zeros(B, n, device=dev),
+                torch.zeros(B, n, K, dtype=torch.bool, device=dev))
+
+    h = f(B, N, d) * 0.3
+    q = h.mean(dim=1)
+    cells64 = idx.clone()
+    valid_b = valid.bool()
+    cells64[~valid_b] = 0
+    y, gate = f(B, K, d), f(B, K, d) + 2.0
+    w = torch.rand(d, generator=g).to(dev) + 0.5
+    pos = torch.randint(0, 9, (B,), generator=g).to(dev)
+    th = torch.zeros(B, n + 1, N, d, device=dev)
+    th[:, 1] = h
+    tq = torch.zeros(B, n + 1, d, device=dev)
+    tq[:, 1] = q
+    ta = torch.zeros(B, n + 1, N, dtype=torch.int64, device=dev)
+    ta[:, 1] = age
+    dec_c = torch.zeros(B, n, K, dtype=torch.int64, device=dev)
+    dec_v = torch.zeros(B, n, K, dtype=torch.bool, device=dev)
+    dec_c[:, 1], dec_v[:, 1] = cells64, valid_b
+    reset = torch.zeros(B, n, dtype=torch.bool, device=dev)
+    reset[2, 2] = True
+    c, b = f(B, K, d).tanh(), torch.sigmoid(f(B, K, d))
+    return {
+        "gather_concat": (ops.gather_concat, (f(B, d), f(B, d), f(B, N, d), f(B, K, d), idx),
+                          (0, 1, 2, 3)),
+        "gather_concat_backward": (ops.gather_concat_backward, (f(B, K, 4 * d), idx, N), ()),
+        "gated_delta_update": (ops.gated_delta_update,
+                               (h.clone(), q.clone(), age.to(torch.int32), idx, valid, c, b), ()),
+        "gated_delta_update_functional": (ops.gated_delta_update_functional,
+                                          (h.clone(), q.clone(), age, idx, valid, c, b),
+                                          (0, 1, 5, 6)),
+        "gated_delta_update_state": (ops.gated_delta_update_state,
+                                     (h.clone(), q.clone(), age, idx, valid, c, b), (0, 1, 5, 6)),
+        "gated_delta_update_backward": (ops.gated_delta_update_backward,
+                                        (idx, valid, c, b, h[:, :K].contiguous(), f(B, N, d),
+                                         f(B, d)), ()),
+        "window_select": (window.select_op, (logits, age, cost, K) + sel, ()),
+        "window_select_tape": (window.select_tape_op, (logits, tape_age, cost) + tapes() + (1,) + sel,
+                               ()),
+        "window_select_fold": (window.select_fold_op,
+                               (torch.cat([logits.reshape(B * N, M), f(B * N, 3)], 1), tape_age,
+                                cost) + tapes() + (1, M) + sel, ()),
+        "window_cell_update": (window.cell_update_op,
+                               (y, gate, h, q, age, pos, cells64, valid_b, w, True, 1e-6), ()),
+        "window_update_tape": (window.update_tape_op,
+                               (y, gate, th, tq, ta, dec_c, dec_v, w, reset,
+                                torch.zeros(B, n, K, d, device=dev), torch.zeros(B, n, device=dev),
+                                torch.zeros(B, n, d, device=dev), 1, True, 1e-6), ()),
+    }
+
+
+OP_NAMES = ["gather_concat", "gather_concat_backward", "gated_delta_update",
+            "gated_delta_update_functional", "gated_delta_update_state",
+            "gated_delta_update_backward", "window_select", "window_select_tape",
+            "window_select_fold", "window_cell_update", "window_update_tape"]
+
+
+def _clone(args):
+    return tuple(a.clone() if isinstance(a, torch.Tensor) else a for a in args)
+
+
+@pytest.mark.parametrize("name", OP_NAMES)
+def test_opcheck_each_op(mods, cuda_device, name):
+    op, args, grads = _cases(cuda_device)[name]
+    args = list(_clone(args))
+    for i in grads:
+        args[i] = args[i].detach().requires_grad_(True)
+    torch.library.opcheck(op, tuple(args))
+
+
+def _outputs(res):
+    if res is None:
+        return ()
+    return tuple(res) if isinstance(res, (tuple, list)) else (res,)
+
+
+@pytest.mark.parametrize("name", OP_NAMES)
+def test_first_dispatch_on_a_fresh_thread(mods, cuda_device, name):
+    """The library is prepared on the main thread; a thread that never called it gets the same
+    results (its own last-error slot, the device's current stream), and the mutated inputs of
+    the in-place and tape ops too."""
+    op, args, _ = _cases(cuda_device)[name]
+    a_main = _clone(args)
+    want = _outputs(op(*a_main))
+    torch.cuda.synchronize()
+
+    def first_call():
+        a = _clone(args)
+        out = _outputs(op(*a))
+        torch.cuda.synchronize()
+        return out, a
+
+    with ThreadPoolExecutor(max_workers=1) as pool:
+        got, a_thread = pool.submit(first_call).result(timeout=60)
+    for x, y in zip(got, want):
+        assert torch.equal(x, y)
+    for x, y in zip(a_thread, a_main):  # in-place and tape outputs
+        if isinstance(x, torch.Tensor):
+            assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("cand_norm", ["rms", "none"])
+def test_tape_ops_write_what_the_plain_ops_return(mods, cuda_device, cand_norm):
+    """``select_tape`` / ``update_tape`` over a block of positions against ``select`` /
+    ``cell_update`` and ``CellGraphState.reset`` position by position (the same kernels, so bit
+    for bit): record ``t`` of the decision tape; record ``t + 1`` of the state tape with the next
+    position's reset applied (resets at the block's first, interior and last positions, and two
+    in a row); the summary, slots and maxima before that reset; a last record that is never
+    reset; and no record written but the position's own (the tapes start as a sentinel)."""
+    from hsn_amd.state import CandidateSpec, CellGraphState
+    from hsn_amd.window import BUDGET_SLACK
+
+    _, window = mods
+    dev = cuda_device
+    g = torch.Generator().manual_seed(23)
+    B, n, N, M, d, K = 5, 6, 24, 3, 8, 4
+    cost = torch.tensor([0.03125, 0.0234375, 0.0390625], device=dev)
+    cell = (CandidateSpec.rms((torch.rand(d, generator=g) + 0.5).to(dev))
+            if cand_norm == "rms" else CandidateSpec.plain(d, dev))
+    state = CellGraphState.make(h=(torch.rand(B, N, d, generator=g) * 1.6 - 0.8).to(dev),
+                                q=torch.zeros(B, d, device=dev),
+                                age=torch.zeros(B, N, dtype=torch.int64, device=dev),
+                                pos=torch.zeros(B, dtype=torch.int64, device=dev))
+    state = state._replace(q=state.h.mean(dim=1))
+    for _ in range(4):
+        state = state.tick((torch.rand(B, N, generator=g) < 0.5).to(dev))
+    reset = torch.zeros(B, n, dtype=torch.bool)
+    reset[0, 0] = True
+    reset[1, 3] = True
+    reset[2, n - 1] = True
+    reset[3, 1] = reset[3, 2] = True
+    reset = reset.to(dev)
+    sentinel = 7.0
+    tape_h = torch.full((B, n + 1, N, d), sentinel, device=dev)
+    tape_q = torch.full((B, n + 1, d), sentinel, device=dev)
+    tape_age = torch.full((B, n + 1, N), 7, dtype=torch.int64, device=dev)
+    cells = torch.full((B, n, K), 7, dtype=torch.int64, device=dev)
+    units = torch.full((B, n, K), 7, dtype=torch.int64, device=dev)
+    valid = torch.zeros((B, n, K), dtype=torch.bool, device=dev)
+    refreshed = torch.zeros((B, n, K), dtype=torch.bool, device=dev)
+    theta = torch.full((B, n), sentinel, device=dev)
+    h_sel = torch.full((B, n, K, d), sentinel, device=dev)
+    h_max = torch.full((B, n), sentinel, device=dev)
+    qs = torch.full((B, n, d), sentinel, device=dev)
+    first = state.reset(reset[:, 0])
+    tape_h[:, 0], tape_q[:, 0], tape_age[:, 0] = first.h, first.q, first.age
+    keys = dict(age_max=2, probes=True, lambda_cost=0.0, cell_overhead=0.0, shared_cost=0.0,
+                limit=0.1 * (1.0 + BUDGET_SLACK))
+    fired = padded = 0
+    for t in range(n):
+        pre = state.reset(reset[:, t])
+        assert torch.equal(tape_h[:, t], pre.h) and torch.equal(tape_q[:, t], pre.q)
+        assert torch.equal(tape_age[:, t], pre.age)
+        logits = torch.randn(B, N, M, generator=g).to(dev)
+        want = window.select(logits, pre.age, cost, k=K, **keys)
+        window.select_tape(logits, tape_age, cost, cells, units, valid, theta, refreshed, t=t,
+                           **keys)
+        got = (cells[:, t], units[:, t], valid[:, t], theta[:, t], refreshed[:, t])
+        for a, b in zip(got, want):
+            assert torch.equal(a, b)
+        assert bool((cells[:, t + 1:] == 7).all()) and bool((theta[:, t + 1:] == 7).all())
+        fired += int(refreshed[:, t].sum())
+        padded += int((~valid[:, t]).sum())
+        y = torch.randn(B, K, d, generator=g).to(dev)
+        gate = torch.randn(B, K, d, generator=g).to(dev)
+        after, slots, top = window.cell_update(cell, y, gate, pre, want[0], want[2])
+        window.update_tape(cell, y, gate, tape_h, tape_q, tape_age, cells, valid, reset, h_sel,
+                           h_max, qs, t=t)
+        nxt = after.reset(reset[:, t + 1]) if t + 1 < n else after
+        assert torch.equal(tape_h[:, t + 1], nxt.h) and torch.equal(tape_q[:, t + 1], nxt.q)
+        assert torch.equal(tape_age[:, t + 1], nxt.age)
+        assert torch.equal(qs[:, t], after.q) and torch.equal(h_sel[:, t], slots)
+        assert torch.equal(h_max[:, t], top)
+        assert bool((tape_h[:, t + 2:] == sentinel).all())
+        assert bool((qs[:, t + 1:] == sentinel).all())
+        assert torch.equal(tape_h[:, t], pre.h)  # the record it read is untouched
+        state = after
+    assert fired > 0 and padded > 0  # probes and padded slots were exercised

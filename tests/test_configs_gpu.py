@@ -1,6 +1,6 @@
-"""The benchmark contract's larger configurations on the GPU at their real per-row shapes: bf16
-(N=1024, K=16), the TBPTT segment (N=512, d=128, carried over windows) and the skewed window
-(N=4096, K=32, Zipf-biased logits). GPU only.
+"""The benchmark contract's five configurations on the GPU at their full sizes: tiny (exactly as
+stated), bf16 (N=1024, K=16), the TBPTT segment (N=512, d=128, carried over windows) and the
+skewed window (N=4096, K=32, Zipf-biased logits). GPU only.
 
 Each test checks size-independent properties on every row: the decisions of spaced positions
 equal the oracle's router; q stays the mean of h; the backward is linear in its cotangents
@@ -8,7 +8,8 @@ equal the oracle's router; q stays the mean of h; the backward is linear in its 
 against the oracle's full window. The TBPTT tests check the carried state and its gradient:
 two windows with the state carried (forward) and the next window's d_h0, d_q0 fed back as the
 end cotangent (backward, the reference's segment semantics) equal one window of twice the
-length. Bars as in test_window_gpu: decisions bit-exact, fp32 1e-5, bf16 2e-2.
+length, and one row of that segment equals the oracle's long window. Config 1 runs exactly as
+the contract states it. Bars as in test_window_gpu: decisions bit-exact, fp32 1e-5, bf16 2e-2.
 """
 
 from __future__ import annotations
@@ -102,12 +103,53 @@ def test_bf16_config_full_size(dev):
     _check_config(dev, CONFIGS["bf16"], seed=31, row=5, every=64, tol=BF16_TOL)
 
 
-def test_skewed_config_rows(dev):
-    """Config 5's rows at their real shape (T1024 N4096 d64 K32, bf16, Zipf-biased logits), 32
-    of the 256 rows: rows are independent, and the full batch only widens the grid."""
+def test_skewed_config_full_size(dev):
+    """Config 5 at its full size: B256 T1024 N4096 d64 K32, bf16 storage, Zipf-biased logits
+    (65,536 router wavefronts over 2.1 GB of logits); the properties on every row, one row
+    against the oracle."""
     from hsn_amd.workload import CONFIGS
 
-    _check_config(dev, CONFIGS["skewed"].scaled(B=32), seed=51, row=3, every=64, tol=BF16_TOL)
+    _check_config(dev, CONFIGS["skewed"], seed=51, row=3, every=128, tol=BF16_TOL)
+
+
+def test_tiny_config_exactly(dev):
+    """Config 1 as the benchmark contract states it: B2 T8 N16 d16 K2, fp32, zero start state,
+    one reset at row 1, position 4; forward and backward with the carried state against the
+    oracle's whole window."""
+    from hsn_amd.workload import CONFIGS, make_cotangents, make_window
+
+    cfg_w = CONFIGS["tiny"]
+    w = make_window(cfg_w, 1)
+    assert not bool(w["h0"].any()) and w["reset"].nonzero().tolist() == [[1, 4]]
+    cot = make_cotangents(cfg_w, 1)
+    D, C = _put(w, dev), _put(cot, dev)
+    got = _forward(w, D, _route_cfg(k=cfg_w.K))
+    want = O.window_forward(w["logits"], w["y"], w["gate_pre"], w["reset"], w["h0"], w["q0"],
+                            w["age0"], w["pos0"], w["cost"], k=cfg_w.K)
+    for name in ("cells", "units"):
+        assert torch.equal(got[name].cpu().long(), want[name]), name
+    for name in ("valid", "theta", "age", "pos"):
+        assert torch.equal(got[name].cpu(), want[name]), name
+    for name in ("q_pre", "q_post", "h_old", "h_sel", "h_max", "h", "q"):
+        _close(got[name], want[name], F32_TOL, name)
+    gb = _backward(w, got, D, C, cfg_w.N)
+    wb = O.window_backward(w["y"], w["gate_pre"], want["h_old"], want["cells"], want["valid"],
+                           w["reset"], cfg_w.N, cot["d_q_pre"], cot["d_q_post"], cot["d_h_sel"],
+                           cot["d_h_T"], cot["d_q_T"])
+    for name, g_, w_ in zip(("dy", "dgate", "d_h0"), gb[:3], wb[:3]):
+        _close(g_, w_, F32_TOL, name)
+    _close(gb[3], _d_q0_exact(w["reset"], cot["d_q_pre"], cot["d_q_post"], cot["d_q_T"],
+                              cfg_w.N), F32_TOL, "d_q0")
+    # row 1 restarts at position 4: its state before that position is zero
+    assert bool((got["q_pre"][1, 4] == 0).all())
+
+
+def test_tbptt_config_rows_match_oracle(dev):
+    """Config 4 (B128 T128 N512 d128 K8, fp32): one window, the properties on every row and one
+    row against the oracle's window, forward and backward."""
+    from hsn_amd.workload import CONFIGS
+
+    _check_config(dev, CONFIGS["tbptt"], seed=43, row=17, every=16, tol=F32_TOL)
 
 
 def _cat(a, b, key):
@@ -156,6 +198,26 @@ def test_tbptt_two_windows_equal_one(dev):
         _close(bl[i][:, T:], b1[i], F32_TOL, name + " window 1")
     _close(bl[2], b0[2], F32_TOL, "d_h0")
     _close(bl[3], b0[3], F32_TOL, "d_q0")
+
+    # one row of the segment against the oracle's long window, forward and backward
+    r = 9
+    row = lambda t: t[[r]]  # noqa: E731
+    want = O.window_forward(row(wl["logits"]), row(wl["y"]), row(wl["gate_pre"]),
+                            row(wl["reset"]), row(wl["h0"]), row(wl["q0"]), row(wl["age0"]),
+                            row(wl["pos0"]), wl["cost"], k=cfg_w.K)
+    for name in ("cells", "theta"):
+        assert torch.equal(torch.cat([g0[name][[r]], g1[name][[r]]], 1).cpu().to(want[name].dtype),
+                           want[name]), name
+    for name in ("q_pre", "q_post", "h_old", "h_sel", "h_max"):
+        _close(torch.cat([g0[name][[r]], g1[name][[r]]], 1), want[name], F32_TOL, name + " row")
+    _close(g1["h"][[r]], want["h"], F32_TOL, "h_T row")
+    CLc = {k: (None if v is None else row(v.cpu())) for k, v in CL.items()}
+    wb = O.window_backward(row(wl["y"]), row(wl["gate_pre"]), want["h_old"], want["cells"],
+                           want["valid"], row(wl["reset"]), cfg_w.N, CLc["d_q_pre"],
+                           CLc["d_q_post"], CLc["d_h_sel"], CLc["d_h_T"], CLc["d_q_T"])
+    _close(torch.cat([b0[0][[r]], b1[0][[r]]], 1), wb[0], F32_TOL, "dy row")
+    _close(torch.cat([b0[1][[r]], b1[1][[r]]], 1), wb[1], F32_TOL, "dgate row")
+    _close(b0[2][[r]], wb[2], F32_TOL, "d_h0 row")
 
 
 def test_tbptt_sixteen_window_segment(dev):

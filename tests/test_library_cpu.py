@@ -9,6 +9,7 @@ import subprocess
 from pathlib import Path
 
 import pytest
+import torch
 
 ROOT = Path(__file__).resolve().parents[1]
 
@@ -75,6 +76,34 @@ def test_argument_errors_return_status_without_a_gpu():
     # a NULL required pointer
     status = lib.hsn_gated_delta_update(None, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, None)
     assert status == 1
+    # the router's fast cells (router.py:1328-1339): reserved == K, and reserved_units alone
+    status = lib.hsn_win_route(1, 0, 1, 1, None, None, 1, 1, 32, 1, 1, 1, None, None, 1, 1, 8, 1,
+                               4, 0, 0, 0.0, 0.0, 0.0, 1.0, 4, 0, None)
+    assert status == 1 and b"reserved" in lib.hsn_win_last_error()
+    status = lib.hsn_win_select(1, 0, 1, None, 1, 1, 1, 1, 1, 1, 1, 8, 1, 4, 0, 1, 1, 0, 0, 0.0,
+                                0.0, 0.0, 1.0, 0, 1, None)
+    assert status == 1 and b"reserved_units" in lib.hsn_win_last_error()
+
+
+@pytest.mark.parametrize("reserved,units,ok", [(0, False, True), (3, True, True), (4, False, False),
+                                               (5, False, False), (0, True, False),
+                                               (-1, False, False), (True, False, False)])
+def test_reserved_cells_follow_the_router_rules(reserved, units, ok):
+    """``reserved`` must be an int in [0, k) and ``reserved_units`` needs reserved > 0, in the
+    window path's settings, the per-position wrappers and the oracle alike (ValueError)."""
+    from hsn_amd.window import RouteConfig
+    from oracle import hsn_oracle as O
+
+    logits = torch.zeros(1, 8, 2)
+    cost = torch.full((2,), 1 / 16)
+    if ok:
+        RouteConfig(k=4, reserved=reserved, reserved_units=units)
+        O.router_select(logits, None, cost, k=4, reserved=reserved, reserved_units=units)
+    else:
+        with pytest.raises(ValueError):
+            RouteConfig(k=4, reserved=reserved, reserved_units=units)
+        with pytest.raises(ValueError):
+            O.router_select(logits, None, cost, k=4, reserved=reserved, reserved_units=units)
 
 
 def test_product_path_fails_loudly_without_the_library(monkeypatch):
@@ -89,3 +118,31 @@ def test_product_path_fails_loudly_without_the_library(monkeypatch):
     finally:
         monkeypatch.undo()
         _lib.library.cache_clear()
+
+
+def test_decline_predicates_follow_the_library_geometry():
+    """The Python decline checks ask the library's own launch geometry (``hsn_win_supports``),
+    so a shape the kernels cannot take declines (``None`` / a reason) instead of raising at
+    launch: K = 65 and N = 20460 in the recurrence, K = 65 in the update, N = 4097 in the router
+    (the reference's convention, python/hsn/kernels/window.py:119-128)."""
+    from hsn_amd import _lib, build
+    from hsn_amd.kernels import window as W
+
+    if build.stale() is not None:
+        pytest.skip("library not built here")
+    assert _lib.unsupported(_lib.OP_RECURRENCE, 2, 16, 256, 64, 8) is None
+    assert _lib.unsupported(_lib.OP_RECURRENCE, 2, 16, 256, 64, 65) is not None
+    assert _lib.unsupported(_lib.OP_RECURRENCE, 2, 16, 20460, 64, 8) is not None
+    assert _lib.unsupported(_lib.OP_FORWARD, 32, 256, 256, 64, 8) is None
+    assert _lib.unsupported(_lib.OP_BACKWARD, 32, 256, 256, 64, 8) is None
+    assert W.cell_update_unsupported(256, 64, 8) is None
+    assert W.cell_update_unsupported(256, 64, 65) is not None
+    assert W.cell_update_unsupported(16, 8, 17) is not None
+    assert W.select_unsupported(4096, 32) is None
+    assert W.select_unsupported(4097, 8) is not None
+    assert W.select_unsupported(256, 65) is not None
+    # a shape the launcher refuses is exactly one hsn_win_supports refuses
+    lib = _lib.library()
+    status = lib.hsn_win_recurrence(1, 1, 1, 1, 1, 1, None, None, None, None, None, 1, 1, None,
+                                    None, 2, 4, 65, 64, 256, None)
+    assert status == 1 and b"LDS" in lib.hsn_win_last_error()

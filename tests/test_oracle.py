@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import load_golden
+from conftest import load_golden, nan_state_window
 from oracle import hsn_oracle as O
 
 F64 = torch.float64
@@ -443,3 +443,98 @@ def test_planted_mistake_fails_the_pin():
     got_c, _ = broken(s["c"].detach(), s["b"].detach(), torch.stack(h_old, 1), s["cells"],
                       s["valid"], s["reset"], N, s["w_pre"], s["w_post"], None)
     assert not torch.allclose(got_c, want_c)
+
+
+# --------------------------------------------------------------------------------------------
+# the RMS candidate: tanh(RMSNorm(y)) with torch's nn.RMSNorm(d, eps=1e-6) (the reference's
+# python/hsn/model/cell.py:206-212,480-484), pinned by its published definition, a closed form,
+# an invariant and finite differences; planted mistakes must fail these pins
+# --------------------------------------------------------------------------------------------
+
+
+def _rms_rows(seed=21, d=12):
+    """Rows of several magnitudes: unit scale, large, and small enough that eps dominates."""
+    g = torch.Generator().manual_seed(seed)
+    y = torch.randn(6, d, generator=g, dtype=F64)
+    y[2] *= 40.0
+    y[3] *= 1e-3  # mean(y^2) ~ 1e-6: eps = 1e-6 matters here
+    y[4] *= 3e-4
+    w = torch.rand(d, generator=g, dtype=F64) + 0.5
+    return y, w
+
+
+def _rms_pins_hold(cand, eps=1e-6) -> bool:
+    """Every pin of the RMS candidate against a candidate function ``cand(y, w, eps)``:
+
+    1. torch's documented RMSNorm, ``y / sqrt(mean(y^2) + eps) * weight`` (eps inside the root,
+       the mean over the last dimension, the gain after the normalisation), in float64;
+    2. the constant row ``y = c * 1``: ``tanh(c / sqrt(c^2 + eps) * w)``;
+    3. with a unit gain and ``eps = 0``, ``atanh(candidate)`` has mean square exactly 1 per row.
+    """
+    y, w = _rms_rows()
+    ok = True
+    want = torch.tanh(y / torch.sqrt((y * y).sum(-1, keepdim=True) / y.shape[-1] + eps) * w)
+    ok &= bool(torch.allclose(cand(y, w, eps), want, atol=1e-12, rtol=1e-12))
+    for c in (0.7, -2.5, 1e-3, -3e-4):
+        row = torch.full((1, y.shape[-1]), c, dtype=F64)
+        closed = torch.tanh(torch.tensor(c, dtype=F64) / math.sqrt(c * c + eps) * w)
+        ok &= bool(torch.allclose(cand(row, w, eps)[0], closed, atol=1e-12, rtol=1e-12))
+    pre = torch.atanh(cand(y[:2], torch.ones_like(w), 0.0))
+    ok &= bool(torch.allclose((pre * pre).mean(-1), torch.ones(2, dtype=F64), atol=1e-10))
+    return ok
+
+
+def test_rms_candidate_pins():
+    assert _rms_pins_hold(lambda y, w, eps: O.candidate(y, True, w, eps))
+
+
+def test_rms_candidate_planted_mistakes_fail_the_pins():
+    """Plausible mistakes in the candidate each fail at least one pin."""
+    def norm(y, w, eps, *, inside=True, mean=True, gain=True, gain_first=False):
+        x = y * w if gain_first else y
+        ms = (x * x).mean(-1, keepdim=True) if mean else (x * x).sum(-1, keepdim=True)
+        den = torch.sqrt(ms + eps) if inside else torch.sqrt(ms) + eps
+        out = x / den
+        return torch.tanh(out * w if (gain and not gain_first) else out)
+
+    mistakes = {
+        "eps 1e-5": lambda y, w, eps: norm(y, w, 1e-5),
+        "eps outside the root": lambda y, w, eps: norm(y, w, eps, inside=False),
+        "sum for mean": lambda y, w, eps: norm(y, w, eps, mean=False),
+        "gain dropped": lambda y, w, eps: norm(y, w, eps, gain=False),
+        "gain before the norm": lambda y, w, eps: norm(y, w, eps, gain_first=True),
+    }
+    assert _rms_pins_hold(lambda y, w, eps: norm(y, w, eps))  # the correct form passes
+    for name, bad in mistakes.items():
+        assert not _rms_pins_hold(bad), f"the pins miss the mistake: {name}"
+
+
+def test_rms_candidate_gradient_matches_finite_differences():
+    """The oracle's d(candidate)/d(y, w) (autograd, which the window backward's d_cand_w uses)
+    against central finite differences in float64."""
+    y, w = _rms_rows(seed=22, d=5)
+    y = y[[0, 2, 3]].clone().requires_grad_(True)
+    w = w.clone().requires_grad_(True)
+    assert torch.autograd.gradcheck(lambda a, b: O.candidate(a, True, b, 1e-6), (y, w),
+                                    eps=1e-7, atol=1e-6, rtol=1e-5)
+
+
+# --------------------------------------------------------------------------------------------
+# the row maximum h_max: NaN-propagating (the reference's test_p2_10_window.py:540-560)
+# --------------------------------------------------------------------------------------------
+
+
+def test_h_max_propagates_a_nan_in_an_unwritten_cell():
+    cfg, w, quiet = nan_state_window()
+    out = O.window_forward(w["logits"], w["y"], w["gate_pre"], w["reset"], w["h0"], w["q0"],
+                           w["age0"], w["pos0"], w["cost"], k=cfg.K)
+    assert not bool((out["cells"] == quiet).any()), "the NaN cell must stay unwritten"
+    hm = out["h_max"]
+    assert bool(torch.isnan(hm[0]).all())
+    assert bool(torch.isnan(hm[1, :3]).all()) and bool(torch.isfinite(hm[1, 3:]).all())
+    # the NaN never reaches the summaries or the written slots
+    for key in ("q_pre", "q_post", "h_old", "h_sel"):
+        assert bool(torch.isfinite(out[key]).all()), key
+    # a plain max (NaN-ignoring, as a careless reduction would be) fails this pin
+    finite = torch.nan_to_num(out["h"], nan=0.0).abs().flatten(1).amax(1)
+    assert not bool(torch.isnan(finite).any())

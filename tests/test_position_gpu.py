@@ -155,6 +155,9 @@ def test_cell_update_matches_oracle(win, cuda_device, case):
     D = [t.to(cuda_device) for t in (y, gate, h, q, age, pos, cells, valid, w)]
     got = win.cell_update_op(*D, rms, 1e-6)
     _close(got[0], want[0], "h")
+    # cells no valid slot names are copied bit for bit (test_p2_10_window.py:272,442)
+    untouched = ~O.selection_mask(cells, valid, h.shape[1])
+    assert torch.equal(got[0].cpu()[untouched], h[untouched]), "unselected cells"
     _close(got[1], want[1], "q")
     assert torch.equal(got[2].cpu(), want[2]), "age"
     assert torch.equal(got[3].cpu(), want[3]), "pos"
@@ -191,6 +194,8 @@ def test_update_tape_writes_the_next_record(win, cuda_device):
                        T[6], T[7], T[8], t, True, 1e-6)
     keep = torch.tensor([True] + [False] + [True] * (B - 2))
     _close(T[0][keep, t + 1], want[0][keep], "h record t+1")
+    untouched = ~O.selection_mask(cells, valid, N) & keep[:, None]
+    assert torch.equal(T[0][:, t + 1].cpu()[untouched], h[untouched]), "unselected cells"
     assert bool((T[0][1, t + 1] == 0).all()), "the reset row restarts at zero"
     _close(T[1][keep, t + 1], want[1][keep], "q record t+1")
     assert torch.equal(T[2][keep, t + 1].cpu(), want[2][keep]), "age record t+1"
@@ -199,3 +204,19 @@ def test_update_tape_writes_the_next_record(win, cuda_device):
     _close(T[7][:, t], want[5], "h_max")
     _close(T[8][:, t], want[1], "qs (before the reset)")
     _close(T[0][:, t], h, "record t unchanged")
+
+
+@pytest.mark.parametrize("N,d", [(256, 64), (300, 16)])
+def test_cell_update_h_max_propagates_a_nan(win, cuda_device, N, d):
+    """One position's row maximum is NaN when a cell no slot writes holds a NaN, and the NaN
+    stays in its cell (test_p2_10_window.py:540-560)."""
+    c = dict(B=2, N=N, d=d, K=4)
+    h, q, age, pos, cells, valid, y, gate, w = _update_inputs(c, 900 + N)
+    quiet = int(torch.ones(N).index_fill(0, cells[0], 0).nonzero()[0])
+    h[0, quiet, d // 2] = float("nan")
+    want = O.cell_update(y, gate, h, q, age, pos, cells, valid)
+    D = [t.to(cuda_device) for t in (y, gate, h, q, age, pos, cells, valid, w)]
+    got = win.cell_update_op(*D, False, 1e-6)
+    assert bool(torch.isnan(got[5][0].cpu())) and bool(torch.isnan(want[5][0]))
+    _close(got[5][1], want[5][1], "finite row")
+    assert torch.equal(torch.isnan(got[0].cpu()), torch.isnan(want[0]))

@@ -181,6 +181,7 @@ WINDOW_CASES = [
     dict(B=8, T=300, N=64, d=64, K=8, io="f32"),  # chunks longer than a register sub-block
     dict(B=256, T=70, N=32, d=64, K=8, io="f32"),  # one chunk per row, several sub-blocks
     dict(B=3, T=5, N=16, d=4, K=4, io="f32"),  # fewer positions than chunks per row
+    dict(B=3, T=7, N=20, d=7, K=3, io="bf16", rms=True),  # odd d and odd B*T*K: RMS workspace
 ]
 
 
@@ -248,6 +249,46 @@ def test_window_forward_and_backward_match_oracle(dev, case):
         _close(gb[4], wb[4], tol * 10, "d_cand_w")  # a sum over every slot of the window
     zero_pad = ~want["valid"]
     assert bool((gb[0].cpu()[zero_pad] == 0).all()) and bool((gb[1].cpu()[zero_pad] == 0).all())
+
+
+@pytest.mark.parametrize("N,d", [(256, 64), (300, 16), (16, 8)])
+def test_forward_h_max_propagates_a_nan_in_an_unwritten_cell(dev, N, d):
+    """A NaN in a start-state cell no slot writes makes the row maximum NaN until a reset clears
+    the row (the reference's test_p2_10_window.py:540-560), on both of the forward's maxima
+    paths: per-cell maxima in LDS (N <= 256) and the tracked maximum with rescans (N > 256)."""
+    from conftest import nan_state_window
+    from hsn_amd import window
+
+    cfg, w, quiet = nan_state_window(N=N, d=d, K=4, T=12)
+    want = O.window_forward(w["logits"], w["y"], w["gate_pre"], w["reset"], w["h0"], w["q0"],
+                            w["age0"], w["pos0"], w["cost"], k=cfg.K)
+    D = {k: v.to(dev) for k, v in w.items()}
+    got = window.window_forward(D["logits"], D["y"], D["gate_pre"], D["reset"], D["h0"], D["q0"],
+                                D["age0"], D["pos0"], D["cost"], _route_cfg(k=cfg.K))
+    assert torch.equal(got["cells"].cpu().long(), want["cells"])
+    hm = got["h_max"].cpu()
+    assert torch.equal(torch.isnan(hm), torch.isnan(want["h_max"]))
+    assert bool(torch.isnan(hm[0]).all()) and bool(torch.isnan(hm[1, :3]).all())
+    _close(hm[1, 3:], want["h_max"][1, 3:], F32_TOL, "h_max after the reset")
+    for name in ("q_pre", "q_post", "h_old"):
+        _close(got[name], want[name], F32_TOL, name)
+    assert torch.equal(torch.isnan(got["h"].cpu()), torch.isnan(want["h"]))
+
+
+def test_forward_zeroes_a_row_maximum_buffer_it_is_given(dev):
+    """``forward(h_max=buf)`` max-reduces into ``buf``: it zeroes it first, so a buffer holding
+    garbage (here larger than every maximum) gives the same maxima as the routed window."""
+    from hsn_amd import window
+
+    c = WINDOW_CASES[4]
+    cfg_w, w, cot, cost, cfg, _ = _window_case(c, 404)
+    D = {k: v.to(dev) for k, v in w.items()}
+    ref = window.window_forward(D["logits"], D["y"], D["gate_pre"], D["reset"], D["h0"], D["q0"],
+                                D["age0"], D["pos0"], cost.to(dev), cfg)
+    buf = torch.full((c["B"], c["T"]), 1e30, device=dev)
+    out = window.forward(D["y"], D["gate_pre"], D["reset"], ref["slots"], D["h0"], D["q0"],
+                         D["age0"], D["pos0"], c["N"], h_max=buf)
+    assert torch.equal(out["h_max"], ref["h_max"]) and out["h_max"] is buf
 
 
 def test_backward_without_optional_cotangents(dev):
