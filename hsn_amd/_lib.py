@@ -40,6 +40,8 @@ SIGNATURES: dict[str, list] = {
     "hsn_win_select": [P, I, L, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, F, F, F, F, I, I, P],
     "hsn_win_forward": [P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I,
                         I, P],
+    "hsn_win_forward_noalloc": [P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I,
+                                I, I, I, I, P],
     "hsn_win_backward": [P, P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I,
                          P],
     "hsn_win_recurrence": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P],

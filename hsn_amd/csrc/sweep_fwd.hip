@@ -1,5 +1,8 @@
 // Entry points of the forward sweep: the whole window (hsn_win_forward) and the reference's
 // per-position end of round (hsn_win_cell_update), over the kernels of sweep.cuh.
+#include <mutex>
+#include <string>
+
 #include "sweep.cuh"
 #include "abi_util.h"
 
@@ -10,46 +13,51 @@ namespace {
 // The RMS candidate's prologue: writes the normalised candidate input into the workspace
 // (layout: rms_inv_offset) and returns it.
 const void* rms_normalise(const void* y, int io_dtype, const float* cand_w, float cand_eps,
-                          void* scratch, int64_t slots, int d, hipStream_t st) {
+                          void* ws, int64_t slots, int d, hipStream_t st) {
     const int blocks = static_cast<int>((slots + 3) / 4);
     const size_t elem = io_dtype == HSN_DTYPE_F32 ? 4 : 2;
-    float* inv = reinterpret_cast<float*>(static_cast<char*>(scratch) + rms_inv_offset(slots, d, elem));
+    float* inv = reinterpret_cast<float*>(static_cast<char*>(ws) + rms_inv_offset(slots, d, elem));
     if (io_dtype == HSN_DTYPE_F32)
         hipLaunchKernelGGL((rms_prologue<float>), dim3(blocks), dim3(256), 0, st,
-                           static_cast<const float*>(y), cand_w, static_cast<float*>(scratch), inv,
+                           static_cast<const float*>(y), cand_w, static_cast<float*>(ws), inv,
                            slots, d, cand_eps);
     else
         hipLaunchKernelGGL((rms_prologue<bf16_t>), dim3(blocks), dim3(256), 0, st,
-                           static_cast<const bf16_t*>(y), cand_w, static_cast<bf16_t*>(scratch),
+                           static_cast<const bf16_t*>(y), cand_w, static_cast<bf16_t*>(ws),
                            inv, slots, d, cand_eps);
-    return scratch;
+    return ws;
 }
 
-}  // namespace
-
-extern "C" int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype,
-                               const float* cand_w, int cand_norm, float cand_eps,
-                               void* rms_scratch, const uint8_t* reset, const int32_t* slots,
-                               const float* h0, const float* q0, const int64_t* age0,
-                               const int64_t* pos0, void* q_pre, void* q_post, void* h_sel,
-                               void* h_old, float* h_max, float* h_T, float* q_T, int64_t* age_T,
-                               int64_t* pos_T, int B, int T, int N, int d, int K, void* stream) {
-    HSN_ABI_BEGIN
+// The checks every forward entry point makes before it touches the RMS workspace.
+void forward_checks(const char* fn, const void* y, const void* gate_pre, int io_dtype,
+                    const float* cand_w, int cand_norm, const uint8_t* reset,
+                    const int32_t* slots, const float* h0, const float* q0, const int64_t* age0,
+                    const int64_t* pos0, int64_t* age_T, int64_t* pos_T, int B, int T, int N,
+                    int d, int K) {
+    const std::string f(fn);
     HSN_REQUIRE(y && gate_pre && reset && slots && h0 && q0, HSN_ERR_INVALID_ARGUMENT,
-                "hsn_win_forward: a required pointer is NULL");
+                f + ": a required pointer is NULL");
     HSN_REQUIRE(B >= 1 && T >= 1 && N >= 1 && d >= 1 && K >= 1 && K <= N,
-                HSN_ERR_INVALID_ARGUMENT, "hsn_win_forward: bad dimensions");
-    HSN_REQUIRE(!age_T || age0, HSN_ERR_INVALID_ARGUMENT, "hsn_win_forward: age_T needs age0");
+                HSN_ERR_INVALID_ARGUMENT, f + ": bad dimensions");
+    HSN_REQUIRE(!age_T || age0, HSN_ERR_INVALID_ARGUMENT, f + ": age_T needs age0");
     HSN_REQUIRE(!pos_T || (pos0 && age_T), HSN_ERR_INVALID_ARGUMENT,
-                "hsn_win_forward: pos_T needs pos0 and age_T");
-    HSN_REQUIRE(!cand_norm || (cand_w && rms_scratch), HSN_ERR_INVALID_ARGUMENT,
-                "hsn_win_forward: the RMS candidate needs cand_w and rms_scratch");
+                f + ": pos_T needs pos0 and age_T");
+    HSN_REQUIRE(!cand_norm || cand_w, HSN_ERR_INVALID_ARGUMENT,
+                f + ": the RMS candidate needs cand_w");
     HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
-                HSN_ERR_UNSUPPORTED_DTYPE, "hsn_win_forward: io_dtype must be f32 or bf16");
+                HSN_ERR_UNSUPPORTED_DTYPE, f + ": io_dtype must be f32 or bf16");
     HSN_REQUIRE(check_elems({int64_t(B) * T * K * d, int64_t(B) * N * d}) &&
                     int64_t(T) * K * d * 4 < (int64_t(1) << 31),
-                HSN_ERR_SIZE_OVERFLOW,
-                "hsn_win_forward: a tensor is too large");
+                HSN_ERR_SIZE_OVERFLOW, f + ": a tensor is too large");
+}
+
+// The forward sweep after the checks; `rms_scratch` is the RMS candidate's workspace.
+void forward_launch(const void* y, const void* gate_pre, int io_dtype, const float* cand_w,
+                    int cand_norm, float cand_eps, void* rms_scratch, const uint8_t* reset,
+                    const int32_t* slots, const float* h0, const float* q0, const int64_t* age0,
+                    const int64_t* pos0, void* q_pre, void* q_post, void* h_sel, void* h_old,
+                    float* h_max, float* h_T, float* q_T, int64_t* age_T, int64_t* pos_T, int B,
+                    int T, int N, int d, int K, void* stream) {
     Geometry g;
     HSN_REQUIRE(choose_geometry(B, T, N, d, K, fwd_lds_bytes, g), HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_forward: the state slice does not fit the LDS (N too large)");
@@ -76,6 +84,84 @@ extern "C" int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype
         HSN_HIP((launch_fwd<float, float, Packed32>(a, g.S, lds, st)));
     else
         HSN_HIP((launch_fwd<bf16_t, bf16_t, Packed32>(a, g.S, lds, st)));
+}
+
+}  // namespace
+
+extern "C" int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype,
+                               const float* cand_w, int cand_norm, float cand_eps,
+                               void* rms_scratch, const uint8_t* reset, const int32_t* slots,
+                               const float* h0, const float* q0, const int64_t* age0,
+                               const int64_t* pos0, void* q_pre, void* q_post, void* h_sel,
+                               void* h_old, float* h_max, float* h_T, float* q_T, int64_t* age_T,
+                               int64_t* pos_T, int B, int T, int N, int d, int K, void* stream) {
+    HSN_ABI_BEGIN
+    forward_checks("hsn_win_forward", y, gate_pre, io_dtype, cand_w, cand_norm, reset, slots, h0,
+                   q0, age0, pos0, age_T, pos_T, B, T, N, d, K);
+    HSN_REQUIRE(!cand_norm || rms_scratch, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_forward: the RMS candidate needs rms_scratch");
+    forward_launch(y, gate_pre, io_dtype, cand_w, cand_norm, cand_eps, rms_scratch, reset, slots,
+                   h0, q0, age0, pos0, q_pre, q_post, h_sel, h_old, h_max, h_T, q_T, age_T,
+                   pos_T, B, T, N, d, K, stream);
+    HSN_ABI_END
+}
+
+namespace {
+
+// The workspace of hsn_win_forward_noalloc, owned by the library: every device the library runs
+// on holds its own copy for the life of the process. Host code never uses the symbol itself
+// (its host-side name is a stand-in, not a device address): each device's address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+void* device_scratch() {
+    int dev = 0;
+    HSN_HIP(hipGetDevice(&dev));
+    HSN_REQUIRE(dev >= 0 && dev < kMaxDevices, HSN_ERR_BACKEND,
+                "hsn_win_forward_noalloc: device index above 63");
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        HSN_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        HSN_REQUIRE(p != nullptr, HSN_ERR_BACKEND,
+                    "hsn_win_forward_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int hsn_win_forward_noalloc(const void* y, const void* gate_pre, int io_dtype,
+                                       const float* cand_w, int cand_norm, float cand_eps,
+                                       const uint8_t* reset, const int32_t* slots,
+                                       const float* h0, const float* q0, const int64_t* age0,
+                                       const int64_t* pos0, void* q_pre, void* q_post,
+                                       void* h_sel, void* h_old, float* h_max, float* h_T,
+                                       float* q_T, int64_t* age_T, int64_t* pos_T, int B, int T,
+                                       int N, int d, int K, void* stream) {
+    HSN_ABI_BEGIN
+    forward_checks("hsn_win_forward_noalloc", y, gate_pre, io_dtype, cand_w, cand_norm, reset,
+                   slots, h0, q0, age0, pos0, age_T, pos_T, B, T, N, d, K);
+    void* ws = nullptr;
+    if (cand_norm) {  // the RMS candidate's workspace: the library's array, within its size
+        const size_t elem = io_dtype == HSN_DTYPE_F32 ? 4 : 2;
+        const int64_t n_slots = int64_t(B) * T * K;
+        const size_t need = rms_inv_offset(n_slots, d, elem) + 4 * size_t(n_slots);
+        HSN_REQUIRE(need <= kNoAllocScratchBytes, HSN_ERR_SIZE_OVERFLOW,
+                    "hsn_win_forward_noalloc: the RMS workspace of B*T*K slots needs " +
+                        std::to_string(need) + " bytes, above the library's " +
+                        std::to_string(kNoAllocScratchBytes) + "-byte scratch array");
+        ws = device_scratch();
+    }
+    forward_launch(y, gate_pre, io_dtype, cand_w, cand_norm, cand_eps, ws, reset, slots, h0, q0,
+                   age0, pos0, q_pre, q_post, h_sel, h_old, h_max, h_T, q_T, age_T, pos_T, B, T,
+                   N, d, K, stream);
     HSN_ABI_END
 }
 

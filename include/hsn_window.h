@@ -136,6 +136,25 @@ int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype, const flo
                     int T, int N, int d, int K, void* stream);
 
 /*
+ * hsn_win_forward without the workspace argument: an entry point that allocates nothing and
+ * takes no workspace. It has no counterpart in the reference; it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). The RMS candidate's workspace is a device array of 32 MiB that the library
+ * owns (one per GPU, held until the process ends): calls with cand_norm 1 take at most
+ * R(B*T*K) <= 32 MiB (R as in hsn_win_forward; about 129,000 slots of d = 64 in fp32) and
+ * return HSN_ERR_SIZE_OVERFLOW above it. Every call on a GPU shares that GPU's array, so calls
+ * that overlap on one GPU (other streams or threads) race; calls ordered on one stream do not.
+ * Arguments, outputs and results are those of hsn_win_forward.
+ */
+int hsn_win_forward_noalloc(const void* y, const void* gate_pre, int io_dtype,
+                            const float* cand_w, int cand_norm, float cand_eps,
+                            const uint8_t* reset, const int32_t* slots, const float* h0,
+                            const float* q0, const int64_t* age0, const int64_t* pos0,
+                            void* q_pre, void* q_post, void* h_sel, void* h_old, float* h_max,
+                            float* h_T, float* q_T, int64_t* age_T, int64_t* pos_T, int B, int T,
+                            int N, int d, int K, void* stream);
+
+/*
  * Backward of the window with the activations fused and the carried-state gradient: the
  * reverse recurrence of python/hsn/train/split.py:128-174 (A [N,d], R [d] resident on chip),
  * seeded with the end-state cotangent (python/hsn/train/state_gradient.py:402-416), the VJPs

@@ -146,3 +146,18 @@ def test_decline_predicates_follow_the_library_geometry():
     status = lib.hsn_win_recurrence(1, 1, 1, 1, 1, 1, None, None, None, None, None, 1, 1, None,
                                     None, 2, 4, 65, 64, 256, None)
     assert status == 1 and b"LDS" in lib.hsn_win_last_error()
+
+
+def test_noalloc_forward_rejects_a_workspace_above_its_array_without_a_gpu():
+    """The no-allocation forward checks the RMS workspace against its 32 MiB array before any
+    HIP call: 1,048,576 slots of d = 64 (260 MiB) return HSN_ERR_SIZE_OVERFLOW."""
+    from hsn_amd import _lib, build
+
+    if build.stale() is not None:
+        pytest.skip("library not built here")
+    lib = _lib.library()
+    status = lib.hsn_win_forward_noalloc(1, 1, 0, 1, 1, 1e-6, 1, 1, 1, 1, None, None, None, None,
+                                         None, None, None, None, None, None, None, 16, 4096, 256,
+                                         64, 16, None)
+    assert status == 5
+    assert b"scratch array" in lib.hsn_win_last_error()
