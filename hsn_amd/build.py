@@ -27,13 +27,14 @@ MANIFEST = PKG / "libhsn_amd.json"
 ARCH = "gfx950"
 
 #: hipcc flags. Packed fp32 arithmetic is switched off (the compiler would otherwise form
-#: v_pk_* fp32 ops from scalar code); -ffp-contract=fast lets a*b+c fuse where written apart.
+#: v_pk_* fp32 ops from scalar code); a*b+c may fuse where written apart, except where a file
+#: says `#pragma clang fp contract(off)` (the router: the CPU path rounds every operation).
 HIP_FLAGS = [
     "-O3",
     "-std=c++17",
     f"--offload-arch={ARCH}",
     "-fPIC",
-    "-ffp-contract=fast",
+    "-ffp-contract=fast-honor-pragmas",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]

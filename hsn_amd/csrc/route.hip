@@ -408,6 +408,29 @@ __device__ __forceinline__ void load_run(IO (&raw)[NPL], rsrc_t r, uint32_t voff
     }
 }
 
+// A lane's NPL consecutive logits, any multiple of 16 bytes or a power of two below, as vector
+// buffer loads (a lane past the row reads zeros).
+template <int NPL, typename IO>
+__device__ __forceinline__ void load_block(IO (&raw)[NPL], rsrc_t r, uint32_t voff) {
+    constexpr int kBytes = NPL * static_cast<int>(sizeof(IO));
+    if constexpr (kBytes <= 16) {
+        load_run<NPL, IO>(raw, r, voff);
+    } else {
+        static_assert(kBytes % 16 == 0, "whole 16-byte runs");
+        constexpr int kPer = 16 / static_cast<int>(sizeof(IO));
+#pragma unroll
+        for (int c = 0; c < kBytes / 16; ++c) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16u * c, 0, 0);
+            __builtin_memcpy(&raw[c * kPer], &v, 16);
+        }
+    }
+}
+
+// The float of a score key below the NaN key (score_key's inverse; the key of -0 is +0's).
+__device__ __forceinline__ float key_score(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
+
 // The decision of one position without probes, for NPL <= 4: the same selection as `decide`,
 // with each lane's cells sorted once. A lane's entries (key, cell, score, unit) are put in the
 // selection's order (key descending, cell ascending: a strict total order, so a five-comparator
@@ -600,24 +623,266 @@ __device__ void decide_sorted(const RouteArgs& a, int b, int p, uint4* ent, uint
     }
 }
 
-// Whole window without probes: a wavefront per (row, position), four per workgroup.
-template <int NPL, typename IO, typename IDX>
+// The decision of one position without probes, any NPL: a threshold, then an exact order of
+// the few cells at or above it.
+//  1. Every lane's largest key; L = the largest 16-bit key prefix that at least Kc = K + 1 (K
+//     when K = N) lanes' maxima reach, by 16 steps of ballot and popcount. The Kc-th largest
+//     lane maximum is at most the Kc-th largest key overall (a subset's Kc-th largest is at most
+//     the set's), so every cell of the top Kc, reserved and NaN keys included, has a key >= L.
+//  2. The candidates, every cell with key >= L (about Kc and a few more), go to LDS, compacted
+//     with ballot and mbcnt. More than 64 (heavy ties) take K rounds of a wavefront argmax over
+//     the keys in registers instead.
+//  3. Each candidate's rank is its count of candidates before it in the selection's order (key
+//     descending, cell ascending): the stable order exactly. Rank k < K is slot k.
+//  4. The budget as `decide`; theta's highest unselected score is the largest of the unselected
+//     candidates (NaN-propagating) and of the keys below L (no NaN there: a NaN key is the
+//     largest), whose float is exact but for -0 reading as +0, which changes no threshold (a zero
+//     below L means every selected score is positive).
+// VALU work per position is about 10 per cell and 6 per candidate, against 16 per slot for the
+// K rounds of a wavefront argmax.
+template <int NPL, bool kOne, typename IO, typename IDX>
+__device__ void decide_select(const RouteArgs& a, int b, int p, uint4* cand, uint4* tab,
+                              uint64_t* ord) {
+    const int lane = lane_id();
+    const int N = a.N, M = a.M, K = a.K, R = a.reserved;
+    const IO* logits = static_cast<const IO*>(a.logits) + b * a.l_row + p * a.l_pos;
+    const bool scale_cost = a.lambda > 0.0f;
+
+    // kOne keeps the raw logits and recomputes a score where one is needed (a candidate, the
+    // pool): scores, keys and logits together would hold three registers per cell
+    constexpr int kS = kOne ? 1 : NPL;
+    float scv[kS];
+    int unit[kS];
+    IO raw[kOne ? NPL : 1];
+    uint32_t key[NPL];
+    const float cost0 = kOne ? a.cost[0] : 0.0f;
+    const float lc = kOne && scale_cost ? mul_rn(a.lambda, cost0) : 0.0f;
+    if constexpr (kOne) {
+        constexpr uint32_t kRun = NPL * sizeof(IO);
+        const bool vec = a.width == 1 && N % NPL == 0 &&
+                         (reinterpret_cast<uintptr_t>(logits) & (kRun >= 16 ? 15 : kRun - 1)) == 0;
+        if (vec) {  // lanes past the row read zeros (kOob); their cells are masked below
+            const rsrc_t r = make_rsrc(logits, uint32_t(N) * sizeof(IO));
+            load_block<NPL, IO>(raw, r, lane * NPL < N ? uint32_t(lane) * kRun : kOob);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NPL; ++i)
+                raw[i] = logits[int64_t(min(lane * NPL + i, N - 1)) * a.width];
+        }
+    }
+    auto score = [&](int i) __attribute__((always_inline)) -> float {
+        if constexpr (kOne) {
+            const float v = to_f32(raw[i]);
+            return scale_cost ? sub_rn(v, lc) : v;
+        } else {
+            return scv[i];
+        }
+    };
+    auto unit_of = [&](int i) __attribute__((always_inline)) -> int {
+        if constexpr (kOne) return 0;
+        else return unit[i];
+    };
+    if constexpr (kOne) {
+        if (N == kWave * NPL && R == 0 && !scale_cost) {  // uniform: every lane full, no masks
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) key[i] = score_key(to_f32(raw[i]));
+        } else {
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                const int n = lane * NPL + i;
+                const uint32_t in = 0u - static_cast<uint32_t>(n < N);
+                const uint32_t rsv = 0u - static_cast<uint32_t>(n < R);
+                key[i] = ((score_key(score(i)) & ~rsv) | (kKeyPosInf & rsv)) & in;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int n = lane * NPL + i;
+            scv[i] = -INFINITY;
+            unit[i] = 0;
+            key[i] = 0u;
+            if (n < N) {
+                const IO* row = logits + static_cast<int64_t>(n) * a.width;
+                float best = to_f32(row[0]);
+                if (scale_cost) best = sub_rn(best, mul_rn(a.lambda, a.cost[0]));
+                int arg = 0;
+                for (int j = 1; j < M; ++j) {
+                    float s = to_f32(row[j]);
+                    if (scale_cost) s = sub_rn(s, mul_rn(a.lambda, a.cost[j]));
+                    if (best == best && (s > best || s != s)) {
+                        best = s;
+                        arg = j;
+                    }
+                }
+                scv[i] = best;
+                unit[i] = arg;
+                key[i] = n < R ? kKeyPosInf : score_key(best);
+            }
+        }
+    }
+
+    // 1. the threshold prefix from the lanes' maxima
+    uint32_t hb = 0u;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) hb = umax(hb, key[i]);
+    const int Kc = K < N ? K + 1 : K;
+    const uint32_t top = hb >> 16;
+    uint32_t pfx = 0u;
+#pragma unroll
+    for (int bit = 15; bit >= 0; --bit) {
+        const uint32_t c = pfx | (1u << bit);
+        pfx = __popcll(ballot(top >= c)) >= Kc ? c : pfx;
+    }
+    const uint32_t L = pfx > 0u ? pfx << 16 : 1u;  // 1: every real key (a cell past N has key 0)
+
+    // 2. the candidates into LDS, and the largest key below L
+    uint32_t below = 0u;
+    int C = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const bool c = key[i] >= L;
+        below = umax(below, c ? 0u : key[i]);
+        const uint64_t m = ballot(c);
+        if (m != 0u) {  // uniform
+            const int at = C + lanes_below(m);
+            if (c && at < kWave) {
+                const uint32_t n = uint32_t(lane * NPL + i);
+                cand[at] = make_uint4(key[i], n, __float_as_uint(score(i)), uint32_t(unit_of(i)));
+                ord[at] = (uint64_t(key[i]) << 32) | ~n;  // the selection's order as one integer
+            }
+            C += __popcll(m);
+        }
+    }
+    // Theta's highest unselected score over the cells outside the slot table (`pool`: a signed
+    // image, `pool_nan`); the table's slots past the budget join it below.
+    int32_t pool;
+    bool pool_nan;
+    if (C <= kWave) {
+        __builtin_amdgcn_wave_barrier();  // the candidates' writes before their reads
+        const bool is_c = lane < C;
+        const uint4 me = is_c ? cand[lane] : make_uint4(0u, 0xffffffffu, 0u, 0u);
+        // 3. each candidate's place in the selection's order: (key, ~cell) as one unsigned
+        // integer, the other candidates' read by broadcast from LDS, four a step (the slots past
+        // C hold 0, below every candidate)
+        const uint64_t mine = (uint64_t(me.x) << 32) | ~me.y;
+        if (lane >= C) ord[lane] = 0u;
+        __builtin_amdgcn_wave_barrier();
+        int rank = 0;
+        for (int j = 0; j < C; j = uniform(j + 4)) {
+            const uint64_t o0 = ord[j], o1 = ord[j + 1], o2 = ord[j + 2], o3 = ord[j + 3];
+            rank += static_cast<int>(o0 > mine) + static_cast<int>(o1 > mine) +
+                    static_cast<int>(o2 > mine) + static_cast<int>(o3 > mine);
+        }
+        if (is_c && rank < K) tab[rank] = me;
+        const bool out = is_c && rank >= K;
+        const float cs = __uint_as_float(me.z);
+        pool = max(out ? ford(cs) : ford(-INFINITY), below != 0u ? ford(key_score(below)) : ford(-INFINITY));
+        pool_nan = out && cs != cs;
+    } else {
+        // Heavy ties: K rounds of a wavefront argmax over the keys in registers (the largest
+        // key, the lowest cell of it: cells are in blocks, so the first lane and its first
+        // entry); the winner's entry leaves the pool.
+        uint32_t bk = 0u;
+        int bi = 0;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const bool gt = key[i] > bk;
+            bk = gt ? key[i] : bk;
+            bi = gt ? i : bi;
+        }
+        for (int r = 0; r < K; r = uniform(r + 1)) {
+            const uint32_t wk = wave_reduce_u32(bk, [](uint32_t x, uint32_t y) { return x > y ? x : y; }, 0u);
+            const int src = __builtin_ctzll(ballot(bk == wk));
+            if (lane == src) {
+#pragma unroll
+                for (int i = 0; i < NPL; ++i) {
+                    if (i == bi) {
+                        tab[r] = make_uint4(key[i], uint32_t(lane * NPL + i), __float_as_uint(score(i)),
+                                            uint32_t(unit_of(i)));
+                        key[i] = 0u;
+                    }
+                }
+                bk = 0u;
+                bi = 0;
+#pragma unroll
+                for (int i = 0; i < NPL; ++i) {
+                    const bool gt = key[i] > bk;
+                    bk = gt ? key[i] : bk;
+                    bi = gt ? i : bi;
+                }
+            }
+        }
+        pool = ford(-INFINITY);
+        pool_nan = false;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {  // every real cell still in the pool
+            const bool out = key[i] != 0u;
+            const float si = score(i);
+            pool = max(pool, out ? ford(si) : ford(-INFINITY));
+            pool_nan = pool_nan | (out & (si != si));
+        }
+    }
+    __builtin_amdgcn_wave_barrier();  // the slot table's writes before its reads
+    const bool is_slot = lane < K;
+    const uint4 e = is_slot ? tab[lane] : make_uint4(0u, 0u, 0u, 0u);
+    const int my_cell = static_cast<int>(e.y);
+    const float my_score = __uint_as_float(e.z);
+
+    // 4. the budget (as decide)
+    int my_unit = 0;
+    float cumulative;
+    if constexpr (kOne) {
+        const float ps = add_rn(a.overhead, cost0);
+        cumulative = add_rn(a.shared, static_cast<float>(static_cast<double>(ps) * (lane + 1)));
+    } else {
+        my_unit = (a.fixed_units && lane < R) ? lane % M : static_cast<int>(e.w);
+        const float my_cost = is_slot ? a.cost[my_unit] : 0.0f;
+        const float per_slot = is_slot ? add_rn(a.overhead, my_cost) : 0.0f;
+        double acc = 0.0;
+        for (int j = 0; j < K; ++j) {
+            const float v = readlane(per_slot, j);
+            if (j <= lane) acc += static_cast<double>(v);
+        }
+        cumulative = add_rn(a.shared, static_cast<float>(acc));
+    }
+    const bool ok = is_slot && cumulative <= a.limit;
+
+    // the threshold: the lowest selected scored slot, the highest unselected cell (the pool and
+    // the table's slots past the budget)
+    const bool in_low = ok && my_cell >= R;
+    const float low = wave_amin_k(in_low ? ford(my_score) : ford(INFINITY), in_low && my_score != my_score);
+    const bool cut = is_slot && !ok;
+    const int32_t hk = max(pool, cut ? ford(my_score) : ford(-INFINITY));
+    const float high = wave_amax_k(hk, pool_nan | (cut && my_score != my_score));
+    const float th = 0.5f * (low + high);
+
+    if (is_slot) {
+        const int64_t o = b * a.o_row + p * a.o_pos + lane;
+        store_index<IDX>(a.cells, o, ok ? my_cell : 0);
+        store_index<IDX>(a.units, o, ok ? my_unit : 0);
+        a.valid[o] = ok ? 1 : 0;
+        a.refreshed[o] = 0;
+        if (a.slots) a.slots[o] = ok ? my_cell : -1;
+    }
+    if (lane == 0) {
+        a.theta[b * a.th_row + p * a.th_pos] = th;
+        if (a.h_max_zero) a.h_max_zero[static_cast<int64_t>(b) * a.P + p] = 0.0f;
+    }
+}
+
+// Whole window without probes: a wavefront per (row, position), four per workgroup; kOne
+// (one unit) is a kernel of its own, so its register budget is not the multi-unit one.
+template <int NPL, bool kOne, typename IO, typename IDX>
 __global__ __launch_bounds__(256) void route_parallel(RouteArgs a) {
     const int wv = uniform(threadIdx.x / kWave);  // uniform: the position's offsets stay scalar
-    const int wave = blockIdx.x * (blockDim.x / kWave) + wv;
-    if (wave >= a.B * a.P) return;
-    const int b = wave / a.P, p = wave - b * a.P;
-    if constexpr (NPL <= 4) {
-        __shared__ uint4 ent[4][kWave * NPL];
-        __shared__ uint4 tab[4][kWave];
-        if (a.M == 1) decide_sorted<NPL, true, IO, IDX>(a, b, p, ent[wv], tab[wv]);
-        else decide_sorted<NPL, false, IO, IDX>(a, b, p, ent[wv], tab[wv]);
-    } else {
-        int64_t ages[NPL];
-#pragma unroll
-        for (int i = 0; i < NPL; ++i) ages[i] = 0;
-        decide<NPL, IO, IDX>(a, b, p, ages, false);
-    }
+    const int p = blockIdx.x * (blockDim.x / kWave) + wv;
+    const int b = blockIdx.y;
+    if (p >= a.P) return;
+    __shared__ uint4 cand[4][kWave];
+    __shared__ uint4 tab[4][kWave];
+    __shared__ uint64_t ord[4][kWave + 4];
+    decide_select<NPL, kOne, IO, IDX>(a, b, p, cand[wv], tab[wv], ord[wv]);
 }
 
 // With probes (or the per-position form): one wavefront walks a row's positions in order.
@@ -656,9 +921,13 @@ hipError_t launch_route(const RouteArgs& a, bool sequential, hipStream_t stream)
             hipLaunchKernelGGL((route_sequential<V, IO, IDX>), dim3(a.B), dim3(kWave), 0,      \
                                stream, a);                                                     \
         } else {                                                                               \
-            const int waves = a.B * a.P;                                                       \
-            hipLaunchKernelGGL((route_parallel<V, IO, IDX>), dim3((waves + 3) / 4), dim3(256),  \
-                               0, stream, a);                                                  \
+            const dim3 grid((a.P + 3) / 4, a.B);                                               \
+            if (a.M == 1)                                                                      \
+                hipLaunchKernelGGL((route_parallel<V, true, IO, IDX>), grid, dim3(256), 0,     \
+                                   stream, a);                                                 \
+            else                                                                               \
+                hipLaunchKernelGGL((route_parallel<V, false, IO, IDX>), grid, dim3(256), 0,    \
+                                   stream, a);                                                 \
         }                                                                                      \
         return hipGetLastError();                                                              \
     }
