@@ -35,15 +35,18 @@ SIGNATURES: dict[str, list] = {
     "hsn_win_abi_version": [],
     "hsn_win_last_error": [],
     "hsn_win_supports": [I, I, I, I, I, I],
+    "hsn_win_set_path": [I],
+    "hsn_win_path": [I, I, I, I, I, I, I, P],
+    "hsn_win_workspace_bytes": [I, I, I, I, I, I, I, I, P],
     "hsn_win_route": [P, I, L, P, P, P, P, P, I, P, P, P, P, P, I, I, I, I, I, I, I, F, F, F, F, I,
                       I, P],
     "hsn_win_select": [P, I, L, P, P, P, P, P, P, P, I, I, I, I, I, I, I, I, I, F, F, F, F, I, I, P],
-    "hsn_win_forward": [P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I,
-                        I, P],
+    "hsn_win_forward": [P, P, I, P, I, F, P, L, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I,
+                        I, I, P],
     "hsn_win_forward_noalloc": [P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I,
                                 I, I, I, I, P],
-    "hsn_win_backward": [P, P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I,
-                         P],
+    "hsn_win_backward": [P, P, P, I, P, I, F, P, L, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I,
+                         I, P],
     "hsn_win_recurrence": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P],
     "hsn_win_recurrence_dense": [P, P, P, P, P, P, P, P, I, I, I, I, P],
     "hsn_win_cell_update": [P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I,
@@ -96,6 +99,32 @@ def unsupported(op: int, B: int, T: int, N: int, d: int, K: int) -> str | None:
     if lib.hsn_win_supports(op, B, T, N, d, K) == HSN_OK:
         return None
     return lib.hsn_win_last_error().decode(errors="replace")
+
+
+PATHS = {"auto": 0, "slice": 1, "chain": 2}
+PATH_NAMES = {v: k for k, v in PATHS.items()}
+
+
+def set_path(path: str) -> None:
+    """Fix the sweeps' design for later forward / backward calls of this process: ``"auto"``
+    (the default), ``"slice"`` (time-chunked slices in LDS) or ``"chain"`` (cell chains)."""
+    call("hsn_win_set_path", PATHS[path])
+
+
+def path_for(op: int, B: int, T: int, N: int, d: int, K: int, io_code: int) -> str:
+    """The design a forward / backward call of this shape takes (``"slice"`` or ``"chain"``)."""
+    out = ctypes.c_int(0)
+    call("hsn_win_path", op, B, T, N, d, K, io_code, ctypes.byref(out))
+    return PATH_NAMES[out.value]
+
+
+def workspace_bytes(op: int, B: int, T: int, N: int, d: int, K: int, io_code: int,
+                    cand_norm: bool) -> int:
+    """Bytes of the workspace a forward / backward call of this shape needs (host arithmetic)."""
+    out = ctypes.c_int64(0)
+    call("hsn_win_workspace_bytes", op, B, T, N, d, K, io_code, int(bool(cand_norm)),
+         ctypes.byref(out))
+    return int(out.value)
 
 
 def ptr(t) -> int | None:

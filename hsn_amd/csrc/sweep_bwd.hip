@@ -1,8 +1,11 @@
 // Entry points of the backward recurrence: the whole window with the activations fused and the
 // carried state (hsn_win_backward), the reference's recurrence from c and b
 // (hsn_win_recurrence) and the dense-fallback rows' recurrence (hsn_win_recurrence_dense).
+#include <string>
+
 #include "sweep.cuh"
 #include "abi_util.h"
+#include "chain_host.h"
 
 using namespace hsn;
 
@@ -57,34 +60,37 @@ void fill_common(BwdArgs& a, const void* y, const void* g, const void* h_old, co
 
 extern "C" int hsn_win_backward(const void* y, const void* gate_pre, const void* h_old,
                                 int io_dtype, const float* cand_w, int cand_norm, float cand_eps,
-                                void* rms_scratch, const int32_t* slots, const uint8_t* reset,
-                                const void* d_q_pre, const void* d_q_post, const void* d_h_sel,
-                                const float* d_h_T, const float* d_q_T, void* dy, void* dgate,
-                                float* d_h0, float* d_q0, float* d_cand_w, int B, int T, int N,
-                                int d, int K, void* stream) {
+                                void* workspace, int64_t workspace_bytes, const int32_t* slots,
+                                const uint8_t* reset, const void* d_q_pre, const void* d_q_post,
+                                const void* d_h_sel, const float* d_h_T, const float* d_q_T,
+                                void* dy, void* dgate, float* d_h0, float* d_q0, float* d_cand_w,
+                                int B, int T, int N, int d, int K, void* stream) {
     HSN_ABI_BEGIN
     HSN_REQUIRE(y && gate_pre && h_old && slots && reset && dy && dgate, HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_backward: a required pointer is NULL");
     HSN_REQUIRE(B >= 1 && T >= 1 && N >= 1 && d >= 1 && K >= 1 && K <= N,
                 HSN_ERR_INVALID_ARGUMENT, "hsn_win_backward: bad dimensions");
-    HSN_REQUIRE(!cand_norm || (cand_w && rms_scratch), HSN_ERR_INVALID_ARGUMENT,
-                "hsn_win_backward: the RMS candidate needs cand_w and rms_scratch");
+    HSN_REQUIRE(!cand_norm || cand_w, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_backward: the RMS candidate needs cand_w");
     HSN_REQUIRE(io_dtype == HSN_DTYPE_F32 || io_dtype == HSN_DTYPE_BF16,
                 HSN_ERR_UNSUPPORTED_DTYPE, "hsn_win_backward: io_dtype must be f32 or bf16");
     HSN_REQUIRE(check_elems({int64_t(B) * T * K * d, int64_t(B) * N * d}) &&
                     int64_t(T) * K * d * 4 < (int64_t(1) << 31),
                 HSN_ERR_SIZE_OVERFLOW,
                 "hsn_win_backward: a tensor is too large");
-    Geometry g;
-    HSN_REQUIRE(choose_geometry(B, T, N, d, K, bwd_lds_bytes, g), HSN_ERR_INVALID_ARGUMENT,
-                "hsn_win_backward: the cotangent slice does not fit the LDS (N too large)");
-    const size_t lds = bwd_lds_bytes(N, g.S, g.W);
-    hipStream_t st = as_stream(stream);
-    const int64_t nslots = int64_t(B) * T * K;
     const size_t elem = io_dtype == HSN_DTYPE_F32 ? 4 : 2;
+    const WorkspaceLayout L = workspace_layout(HSN_OP_BACKWARD, B, T, N, d, K, elem, cand_norm);
+    HSN_REQUIRE(L.bytes == 0 || (workspace && workspace_bytes >= int64_t(L.bytes)),
+                HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_backward: the workspace must hold " + std::to_string(L.bytes) +
+                    " bytes (hsn_win_workspace_bytes)");
+    hipStream_t st = as_stream(stream);
+    char* ws = static_cast<char*>(workspace);
+    const int64_t nslots = int64_t(B) * T * K;
     const void* pre = y;
     float* inv = nullptr;
     if (cand_norm) {  // the normalised candidate input (the forward's, recomputed)
+        void* rms_scratch = ws + L.rms;
         inv = reinterpret_cast<float*>(static_cast<char*>(rms_scratch) + rms_inv_offset(nslots, d, elem));
         const int blocks = static_cast<int>((nslots + 3) / 4);
         if (io_dtype == HSN_DTYPE_F32)
@@ -98,14 +104,23 @@ extern "C" int hsn_win_backward(const void* y, const void* gate_pre, const void*
         HSN_HIP(hipGetLastError());
         pre = rms_scratch;
     }
-    BwdArgs a{};
-    fill_common(a, pre, gate_pre, h_old, d_h_sel, d_q_pre, d_q_post, reset, d_h_T, d_q_T, dy,
-                dgate, d_h0, d_q0, B, T, N, d, K, g);
-    a.cells = slots, a.valid = nullptr;
-    if (io_dtype == HSN_DTYPE_F32)
-        HSN_HIP((launch_bwd<float, Packed32, true>(a, g.S, lds, st)));
-    else
-        HSN_HIP((launch_bwd<bf16_t, Packed32, true>(a, g.S, lds, st)));
+    if (L.chain) {
+        chain_backward(pre, gate_pre, h_old, io_dtype, slots, reset, d_q_pre, d_q_post, d_h_sel,
+                       d_h_T, d_q_T, dy, dgate, d_h0, d_q0, B, T, N, d, K, ws, L, st);
+    } else {
+        Geometry g;
+        HSN_REQUIRE(choose_geometry(B, T, N, d, K, bwd_lds_bytes, g), HSN_ERR_INVALID_ARGUMENT,
+                    "hsn_win_backward: the cotangent slice does not fit the LDS (N too large)");
+        const size_t lds = bwd_lds_bytes(N, g.S, g.W);
+        BwdArgs a{};
+        fill_common(a, pre, gate_pre, h_old, d_h_sel, d_q_pre, d_q_post, reset, d_h_T, d_q_T, dy,
+                    dgate, d_h0, d_q0, B, T, N, d, K, g);
+        a.cells = slots, a.valid = nullptr;
+        if (io_dtype == HSN_DTYPE_F32)
+            HSN_HIP((launch_bwd<float, Packed32, true>(a, g.S, lds, st)));
+        else
+            HSN_HIP((launch_bwd<bf16_t, Packed32, true>(a, g.S, lds, st)));
+    }
     if (cand_norm) {  // the norm's VJP: dy holds dL/dpre
         const int blocks = static_cast<int>((nslots + 3) / 4);
         if (io_dtype == HSN_DTYPE_F32) {

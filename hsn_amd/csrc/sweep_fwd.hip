@@ -5,6 +5,7 @@
 
 #include "sweep.cuh"
 #include "abi_util.h"
+#include "chain_host.h"
 
 using namespace hsn;
 
@@ -51,22 +52,28 @@ void forward_checks(const char* fn, const void* y, const void* gate_pre, int io_
                 HSN_ERR_SIZE_OVERFLOW, f + ": a tensor is too large");
 }
 
-// The forward sweep after the checks; `rms_scratch` is the RMS candidate's workspace.
+// The forward after the checks, on the path the layout names; `ws` is the workspace.
 void forward_launch(const void* y, const void* gate_pre, int io_dtype, const float* cand_w,
-                    int cand_norm, float cand_eps, void* rms_scratch, const uint8_t* reset,
-                    const int32_t* slots, const float* h0, const float* q0, const int64_t* age0,
-                    const int64_t* pos0, void* q_pre, void* q_post, void* h_sel, void* h_old,
-                    float* h_max, float* h_T, float* q_T, int64_t* age_T, int64_t* pos_T, int B,
-                    int T, int N, int d, int K, void* stream) {
+                    int cand_norm, float cand_eps, char* ws, const WorkspaceLayout& L,
+                    const uint8_t* reset, const int32_t* slots, const float* h0, const float* q0,
+                    const int64_t* age0, const int64_t* pos0, void* q_pre, void* q_post,
+                    void* h_sel, void* h_old, float* h_max, float* h_T, float* q_T,
+                    int64_t* age_T, int64_t* pos_T, int B, int T, int N, int d, int K,
+                    void* stream) {
+    hipStream_t st = as_stream(stream);
+    if (cand_norm) {
+        y = rms_normalise(y, io_dtype, cand_w, cand_eps, ws + L.rms, int64_t(B) * T * K, d, st);
+        HSN_HIP(hipGetLastError());
+    }
+    if (L.chain) {
+        chain_forward(y, gate_pre, io_dtype, reset, slots, h0, q0, age0, pos0, q_pre, q_post,
+                      h_sel, h_old, h_max, h_T, q_T, age_T, pos_T, B, T, N, d, K, ws, L, st);
+        return;
+    }
     Geometry g;
     HSN_REQUIRE(choose_geometry(B, T, N, d, K, fwd_lds_bytes, g), HSN_ERR_INVALID_ARGUMENT,
                 "hsn_win_forward: the state slice does not fit the LDS (N too large)");
     const size_t lds = fwd_lds_bytes(N, g.S, g.W);
-    hipStream_t st = as_stream(stream);
-    if (cand_norm) {
-        y = rms_normalise(y, io_dtype, cand_w, cand_eps, rms_scratch, int64_t(B) * T * K, d, st);
-        HSN_HIP(hipGetLastError());
-    }
     FwdArgs a{};
     a.y = y, a.g = gate_pre, a.y_row = int64_t(T) * K * d;
     a.reset = reset, a.r_row = T, a.clear = nullptr, a.c_row = 0;
@@ -90,19 +97,24 @@ void forward_launch(const void* y, const void* gate_pre, int io_dtype, const flo
 
 extern "C" int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype,
                                const float* cand_w, int cand_norm, float cand_eps,
-                               void* rms_scratch, const uint8_t* reset, const int32_t* slots,
-                               const float* h0, const float* q0, const int64_t* age0,
-                               const int64_t* pos0, void* q_pre, void* q_post, void* h_sel,
-                               void* h_old, float* h_max, float* h_T, float* q_T, int64_t* age_T,
-                               int64_t* pos_T, int B, int T, int N, int d, int K, void* stream) {
+                               void* workspace, int64_t workspace_bytes, const uint8_t* reset,
+                               const int32_t* slots, const float* h0, const float* q0,
+                               const int64_t* age0, const int64_t* pos0, void* q_pre,
+                               void* q_post, void* h_sel, void* h_old, float* h_max, float* h_T,
+                               float* q_T, int64_t* age_T, int64_t* pos_T, int B, int T, int N,
+                               int d, int K, void* stream) {
     HSN_ABI_BEGIN
     forward_checks("hsn_win_forward", y, gate_pre, io_dtype, cand_w, cand_norm, reset, slots, h0,
                    q0, age0, pos0, age_T, pos_T, B, T, N, d, K);
-    HSN_REQUIRE(!cand_norm || rms_scratch, HSN_ERR_INVALID_ARGUMENT,
-                "hsn_win_forward: the RMS candidate needs rms_scratch");
-    forward_launch(y, gate_pre, io_dtype, cand_w, cand_norm, cand_eps, rms_scratch, reset, slots,
-                   h0, q0, age0, pos0, q_pre, q_post, h_sel, h_old, h_max, h_T, q_T, age_T,
-                   pos_T, B, T, N, d, K, stream);
+    const WorkspaceLayout L = workspace_layout(HSN_OP_FORWARD, B, T, N, d, K,
+                                               io_dtype == HSN_DTYPE_F32 ? 4 : 2, cand_norm);
+    HSN_REQUIRE(L.bytes == 0 || (workspace && workspace_bytes >= int64_t(L.bytes)),
+                HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_forward: the workspace must hold " + std::to_string(L.bytes) +
+                    " bytes (hsn_win_workspace_bytes)");
+    forward_launch(y, gate_pre, io_dtype, cand_w, cand_norm, cand_eps,
+                   static_cast<char*>(workspace), L, reset, slots, h0, q0, age0, pos0, q_pre,
+                   q_post, h_sel, h_old, h_max, h_T, q_T, age_T, pos_T, B, T, N, d, K, stream);
     HSN_ABI_END
 }
 
@@ -148,20 +160,17 @@ extern "C" int hsn_win_forward_noalloc(const void* y, const void* gate_pre, int 
     HSN_ABI_BEGIN
     forward_checks("hsn_win_forward_noalloc", y, gate_pre, io_dtype, cand_w, cand_norm, reset,
                    slots, h0, q0, age0, pos0, age_T, pos_T, B, T, N, d, K);
-    void* ws = nullptr;
-    if (cand_norm) {  // the RMS candidate's workspace: the library's array, within its size
-        const size_t elem = io_dtype == HSN_DTYPE_F32 ? 4 : 2;
-        const int64_t n_slots = int64_t(B) * T * K;
-        const size_t need = rms_inv_offset(n_slots, d, elem) + 4 * size_t(n_slots);
-        HSN_REQUIRE(need <= kNoAllocScratchBytes, HSN_ERR_SIZE_OVERFLOW,
-                    "hsn_win_forward_noalloc: the RMS workspace of B*T*K slots needs " +
-                        std::to_string(need) + " bytes, above the library's " +
-                        std::to_string(kNoAllocScratchBytes) + "-byte scratch array");
-        ws = device_scratch();
-    }
-    forward_launch(y, gate_pre, io_dtype, cand_w, cand_norm, cand_eps, ws, reset, slots, h0, q0,
-                   age0, pos0, q_pre, q_post, h_sel, h_old, h_max, h_T, q_T, age_T, pos_T, B, T,
-                   N, d, K, stream);
+    // the workspace hsn_win_forward would take: the library's array, within its size
+    const WorkspaceLayout L = workspace_layout(HSN_OP_FORWARD, B, T, N, d, K,
+                                               io_dtype == HSN_DTYPE_F32 ? 4 : 2, cand_norm);
+    HSN_REQUIRE(L.bytes <= kNoAllocScratchBytes, HSN_ERR_SIZE_OVERFLOW,
+                "hsn_win_forward_noalloc: the workspace of this shape needs " +
+                    std::to_string(L.bytes) + " bytes, above the library's " +
+                    std::to_string(kNoAllocScratchBytes) + "-byte scratch array");
+    char* ws = L.bytes ? static_cast<char*>(device_scratch()) : nullptr;
+    forward_launch(y, gate_pre, io_dtype, cand_w, cand_norm, cand_eps, ws, L, reset, slots, h0,
+                   q0, age0, pos0, q_pre, q_post, h_sel, h_old, h_max, h_T, q_T, age_T, pos_T, B,
+                   T, N, d, K, stream);
     HSN_ABI_END
 }
 
@@ -231,24 +240,19 @@ extern "C" int hsn_win_supports(int op, int B, int T, int N, int d, int K) {
     HSN_ABI_BEGIN
     HSN_REQUIRE(B >= 1 && T >= 1 && N >= 1 && d >= 1 && K >= 1, HSN_ERR_INVALID_ARGUMENT,
                 "dimensions must be >= 1");
-    Geometry g;
+    const char* why = nullptr;
     switch (op) {
         case HSN_OP_FORWARD:
-        case HSN_OP_CELL_UPDATE: {
-            const int t = op == HSN_OP_FORWARD ? T : 1;
+        case HSN_OP_BACKWARD:  // either path (the one the call would take)
             HSN_REQUIRE(K <= N, HSN_ERR_INVALID_ARGUMENT, "K exceeds N");
-            HSN_REQUIRE(choose_geometry(B, t, N, d, K, fwd_lds_bytes, g),
-                        HSN_ERR_INVALID_ARGUMENT,
-                        "no state slice fits the LDS with one slot per lane (N or K too large)");
+            choose_path(op, B, T, N, d, K, 4);
             break;
-        }
-        case HSN_OP_BACKWARD:
+        case HSN_OP_CELL_UPDATE:
+            HSN_REQUIRE(K <= N, HSN_ERR_INVALID_ARGUMENT, "K exceeds N");
+            HSN_REQUIRE(slice_takes(op, B, 1, N, d, K, &why), HSN_ERR_INVALID_ARGUMENT, why);
+            break;
         case HSN_OP_RECURRENCE:
-            HSN_REQUIRE(op == HSN_OP_RECURRENCE || K <= N, HSN_ERR_INVALID_ARGUMENT,
-                        "K exceeds N");
-            HSN_REQUIRE(choose_geometry(B, T, N, d, K, bwd_lds_bytes, g),
-                        HSN_ERR_INVALID_ARGUMENT,
-                        "no cotangent slice fits the LDS with one slot per lane (N or K too large)");
+            HSN_REQUIRE(slice_takes(op, B, T, N, d, K, &why), HSN_ERR_INVALID_ARGUMENT, why);
             break;
         case HSN_OP_ROUTE:
             HSN_REQUIRE(K <= N, HSN_ERR_INVALID_ARGUMENT, "K exceeds N");

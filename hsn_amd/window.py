@@ -145,9 +145,12 @@ def rms_scratch_bytes(slots: int, d: int, elem: int) -> int:
     return ((slots * d * elem + 15) & ~15) + 4 * slots
 
 
-def _rms_scratch(slots: int, d: int, io: torch.dtype, dev) -> Tensor:
-    elem = 4 if io == torch.float32 else 2
-    return torch.empty(rms_scratch_bytes(slots, d, elem), dtype=torch.uint8, device=dev)
+def _workspace(op: int, B: int, T: int, N: int, d: int, K: int, io: torch.dtype,
+               cand_norm: bool, dev) -> tuple[Optional[Tensor], int]:
+    """The workspace of a forward / backward call (``None`` where the call needs none) and its
+    size, as the library reports it for the path the call takes."""
+    n = _lib.workspace_bytes(op, B, T, N, d, K, _io_code(io), cand_norm)
+    return (torch.empty(n, dtype=torch.uint8, device=dev) if n else None), n
 
 
 def forward(y: Tensor, gate_pre: Tensor, reset: Tensor, slots: Tensor, h0: Tensor, q0: Tensor,
@@ -171,12 +174,11 @@ def forward(y: Tensor, gate_pre: Tensor, reset: Tensor, slots: Tensor, h0: Tenso
     _check(q0, "q0", (B, d), torch.float32, dev)
     _check(age0, "age0", (B, N), torch.int64, dev)
     _check(pos0, "pos0", (B,), torch.int64, dev)
-    scratch = None
     if cand_norm:
         if cand_w is None:
             raise ValueError("cand_norm needs cand_w")
         _check(cand_w, "cand_w", (d,), torch.float32, dev)
-        scratch = _rms_scratch(B * T * K, d, io, dev)
+    ws, ws_bytes = _workspace(_lib.OP_FORWARD, B, T, N, d, K, io, cand_norm, dev)
     out = {
         "q_pre": torch.empty(B, T, d, dtype=io, device=dev),
         "q_post": torch.empty(B, T, d, dtype=io, device=dev),
@@ -193,7 +195,7 @@ def forward(y: Tensor, gate_pre: Tensor, reset: Tensor, slots: Tensor, h0: Tenso
             h_max.zero_()
         out["h_max"] = h_max
     call("hsn_win_forward", ptr(y), ptr(gate_pre), _io_code(io), ptr(cand_w) if cand_norm else None,
-         int(bool(cand_norm)), float(cand_eps), ptr(scratch), ptr(reset), ptr(slots),
+         int(bool(cand_norm)), float(cand_eps), ptr(ws), ws_bytes, ptr(reset), ptr(slots),
          ptr(h0), ptr(q0), ptr(age0), ptr(pos0), ptr(out["q_pre"]), ptr(out["q_post"]),
          ptr(out["h_sel"]), ptr(out["h_old"]), ptr(h_max), ptr(out["h"]), ptr(out["q"]),
          ptr(out["age"]), ptr(out["pos"]), B, T, N, d, K, stream_of(dev))
@@ -228,20 +230,20 @@ def backward(y: Tensor, gate_pre: Tensor, h_old: Tensor, slots: Tensor,
         _check(d_h_T, "d_h_T", (B, N, d), torch.float32, dev)
     if d_q_T is not None:
         _check(d_q_T, "d_q_T", (B, d), torch.float32, dev)
-    scratch = d_w = None
+    d_w = None
     if cand_norm:
         if cand_w is None:
             raise ValueError("cand_norm needs cand_w")
         _check(cand_w, "cand_w", (d,), torch.float32, dev)
-        scratch = _rms_scratch(B * T * K, d, io, dev)
         d_w = torch.empty(d, dtype=torch.float32, device=dev)
+    ws, ws_bytes = _workspace(_lib.OP_BACKWARD, B, T, N, d, K, io, cand_norm, dev)
     dy = torch.empty_like(y)
     dgate = torch.empty_like(y)
     d_h0 = torch.empty(B, N, d, dtype=torch.float32, device=dev)
     d_q0 = torch.empty(B, d, dtype=torch.float32, device=dev)
     call("hsn_win_backward", ptr(y), ptr(gate_pre), ptr(h_old), _io_code(io),
-         ptr(cand_w) if cand_norm else None, int(bool(cand_norm)), float(cand_eps), ptr(scratch),
-         ptr(slots), ptr(reset), ptr(d_q_pre), ptr(d_q_post), ptr(d_h_sel),
+         ptr(cand_w) if cand_norm else None, int(bool(cand_norm)), float(cand_eps), ptr(ws),
+         ws_bytes, ptr(slots), ptr(reset), ptr(d_q_pre), ptr(d_q_post), ptr(d_h_sel),
          ptr(d_h_T), ptr(d_q_T), ptr(dy), ptr(dgate), ptr(d_h0), ptr(d_q0), ptr(d_w), B, T, N, d, K,
          stream_of(dev))
     return dy, dgate, d_h0, d_q0, d_w

@@ -43,7 +43,7 @@ extern "C" {
 #endif
 
 /* ABI version of this header (bumped on any signature or semantic change). */
-#define HSN_WINDOW_ABI_VERSION 1
+#define HSN_WINDOW_ABI_VERSION 2
 int hsn_win_abi_version(void);
 
 /* The last error message of the calling thread ("" if none); valid until the next call. */
@@ -63,6 +63,37 @@ const char* hsn_win_last_error(void);
 #define HSN_OP_CELL_UPDATE 3
 #define HSN_OP_ROUTE 4
 int hsn_win_supports(int op, int B, int T, int N, int d, int K);
+
+/*
+ * The two designs of the window's sweeps. No counterpart in the reference (its fused sweep is
+ * one design); these choose between this library's two, which compute the same outputs to the
+ * parity tolerance:
+ *   HSN_PATH_SLICE  time-chunked slices of the state resident in LDS (a workgroup per row and
+ *                   column slice): the fastest where a wavefront's piece of a slot row is a
+ *                   full 32-byte sector (d / S columns per wavefront, S * K <= 64);
+ *   HSN_PATH_CHAIN  cell chains (a wavefront per cell walks the cell's events in time; whole
+ *                   slot rows per load and store; the summary by a scan over time): any N, K
+ *                   up to 255, d up to 256.
+ * hsn_win_set_path fixes the path of every later hsn_win_forward / hsn_win_forward_noalloc /
+ * hsn_win_backward call of the process (HSN_PATH_AUTO, the default: the slices where their
+ * piece is a full sector, else the chains). hsn_win_path reports the path a call of `op`
+ * (HSN_OP_FORWARD or HSN_OP_BACKWARD) would take, or the reason neither takes the shape.
+ */
+#define HSN_PATH_AUTO 0
+#define HSN_PATH_SLICE 1
+#define HSN_PATH_CHAIN 2
+int hsn_win_set_path(int path);
+int hsn_win_path(int op, int B, int T, int N, int d, int K, int io_dtype, int* path);
+
+/*
+ * The workspace hsn_win_forward / hsn_win_backward need, in bytes (0: none), for `op`
+ * HSN_OP_FORWARD or HSN_OP_BACKWARD on the path the call takes: the RMS candidate's normalised
+ * input (cand_norm 1) and, on the chain path, the row lists, the per-position sums and the
+ * forward's per-slot deltas. No counterpart in the reference (its sweep keeps the state in
+ * shared memory and allocates through torch).
+ */
+int hsn_win_workspace_bytes(int op, int B, int T, int N, int d, int K, int io_dtype,
+                            int cand_norm, int64_t* bytes);
 
 /*
  * Router: the hard top-k decision of every position of a window.
@@ -118,8 +149,9 @@ int hsn_win_select(const void* logits, int io_dtype, int64_t width, const int64_
  * python/hsn/kernels/native.py:244-303; python/hsn/model/state.py:267-324).
  *   y, gate_pre [B,T,K,d] io_dtype: candidate input and write-gate pre-activation
  *   c = tanh(y) (cand_norm 0) or tanh(y * rsqrt(mean_d(y^2) + cand_eps) * cand_w) (cand_norm 1,
- *   cand_w [d] f32, rms_scratch a workspace of R(B*T*K) bytes, R(s) = align16(s*d*sizeof(io)) + 4*s);
- *   b = sigmoid
+ *   cand_w [d] f32); b = sigmoid
+ *   workspace: workspace_bytes >= what hsn_win_workspace_bytes(HSN_OP_FORWARD, ...) reports
+ *   (may be NULL where that is 0)
  *   reset [B,T] u8; slots [B,T,K] int32 (hsn_win_route's packed decision: cell or -1)
  *   h0 [B,N,d], q0 [B,d] f32; age0 [B,N], pos0 [B] int64
  * Outputs (each optional): q_pre, q_post [B,T,d] io_dtype (summary before / after each
@@ -129,7 +161,8 @@ int hsn_win_select(const void* logits, int io_dtype, int64_t width, const int64_
  * hsn_win_route zeroes it), h_T [B,N,d], q_T [B,d] f32, age_T [B,N], pos_T [B] int64.
  */
 int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype, const float* cand_w,
-                    int cand_norm, float cand_eps, void* rms_scratch, const uint8_t* reset,
+                    int cand_norm, float cand_eps, void* workspace, int64_t workspace_bytes,
+                    const uint8_t* reset,
                     const int32_t* slots, const float* h0, const float* q0, const int64_t* age0,
                     const int64_t* pos0, void* q_pre, void* q_post, void* h_sel, void* h_old,
                     float* h_max, float* h_T, float* q_T, int64_t* age_T, int64_t* pos_T, int B,
@@ -139,12 +172,13 @@ int hsn_win_forward(const void* y, const void* gate_pre, int io_dtype, const flo
  * hsn_win_forward without the workspace argument: an entry point that allocates nothing and
  * takes no workspace. It has no counterpart in the reference; it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc). The RMS candidate's workspace is a device array of 32 MiB that the library
- * owns (one per GPU, held until the process ends): calls with cand_norm 1 take at most
- * R(B*T*K) <= 32 MiB (R as in hsn_win_forward; about 129,000 slots of d = 64 in fp32) and
- * return HSN_ERR_SIZE_OVERFLOW above it. Every call on a GPU shares that GPU's array, so calls
- * that overlap on one GPU (other streams or threads) race; calls ordered on one stream do not.
- * Arguments, outputs and results are those of hsn_win_forward.
+ * forbid hipMalloc). The workspace hsn_win_forward would take (hsn_win_workspace_bytes, on the
+ * same path) is a device array of 32 MiB that the library owns (one per GPU, held until the
+ * process ends): shapes whose workspace exceeds it return HSN_ERR_SIZE_OVERFLOW (the slice
+ * path needs one only for the RMS candidate: about 129,000 slots of d = 64 in fp32; the chain
+ * path about 4 (d + 1 + d / K) bytes per slot). Every call on a GPU shares that GPU's array,
+ * so calls that overlap on one GPU (other streams or threads) race; calls ordered on one
+ * stream do not. Arguments, outputs and results are those of hsn_win_forward.
  */
 int hsn_win_forward_noalloc(const void* y, const void* gate_pre, int io_dtype,
                             const float* cand_w, int cand_norm, float cand_eps,
@@ -164,10 +198,12 @@ int hsn_win_forward_noalloc(const void* y, const void* gate_pre, int io_dtype,
  *   d_q_pre, d_q_post [B,T,d], d_h_sel [B,T,K,d] io_dtype (optional: absent = zero)
  *   d_h_T [B,N,d], d_q_T [B,d] f32 (optional: absent = zero)
  * Outputs: dy, dgate [B,T,K,d] io_dtype (exact zeros on padded slots); d_h0 [B,N,d], d_q0 [B,d]
- * f32 (optional); d_cand_w [d] f32 (cand_norm 1; rms_scratch as hsn_win_forward's).
+ * f32 (optional); d_cand_w [d] f32 (cand_norm 1).
+ *   workspace: workspace_bytes >= what hsn_win_workspace_bytes(HSN_OP_BACKWARD, ...) reports.
  */
 int hsn_win_backward(const void* y, const void* gate_pre, const void* h_old, int io_dtype,
-                     const float* cand_w, int cand_norm, float cand_eps, void* rms_scratch,
+                     const float* cand_w, int cand_norm, float cand_eps, void* workspace,
+                     int64_t workspace_bytes,
                      const int32_t* slots, const uint8_t* reset, const void* d_q_pre,
                      const void* d_q_post, const void* d_h_sel, const float* d_h_T,
                      const float* d_q_T, void* dy, void* dgate, float* d_h0, float* d_q0,
@@ -205,7 +241,7 @@ int hsn_win_recurrence_dense(const float* c, const float* b, const float* h_old,
  * kernels/cuda/hsn_window.cu:751-954 `hsn_win_cell_update`, wrappers cell_update_op /
  * update_tape_op (python/hsn/kernels/window.py:605-760).
  *   y [B,K,d], gate [B,K,d] io_dtype (the round's products); cand_w [d] f32 (cand_norm 1;
- *   rms_scratch a workspace of R(B*K) bytes, R as in hsn_win_forward)
+ *   rms_scratch a workspace of R(B*K) bytes, R(s) = align16(s*d*sizeof(io)) + 4*s)
  *   h [B,n_state,N,d], q [B,n_state,d] f32, age [B,n_state,N] int64: record t read
  *   pos [B] int64 (optional), cells [B,n_slot,K] int64, valid [B,n_slot,K] u8: record t
  *   h_next, q_next, age_next: record t_out written (may be the buffers above, t_out != t);

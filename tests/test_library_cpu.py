@@ -43,7 +43,7 @@ def test_library_is_current_and_exports_every_declared_symbol():
     assert _declared() <= exported, _declared() - exported
     assert set(_lib.SIGNATURES) == _declared()
     lib = _lib.library()  # loads without a GPU
-    assert lib.hsn_win_abi_version() == 1
+    assert lib.hsn_win_abi_version() == 2
 
 
 def test_status_codes_match_the_reference_abi():
@@ -70,7 +70,7 @@ def test_argument_errors_return_status_without_a_gpu():
     assert status == 1
     assert b"K <= N" in lib.hsn_win_last_error()
     # f16 is not a window storage type
-    status = lib.hsn_win_forward(1, 1, 1, None, 0, 0.0, None, 1, 1, 1, 1, None, None, None, None,
+    status = lib.hsn_win_forward(1, 1, 1, None, 0, 0.0, None, 0, 1, 1, 1, 1, None, None, None, None,
                                  None, None, None, None, None, None, None, 1, 1, 4, 4, 2, None)
     assert status == 2
     # a NULL required pointer
@@ -135,6 +135,18 @@ def test_decline_predicates_follow_the_library_geometry():
     assert _lib.unsupported(_lib.OP_RECURRENCE, 2, 16, 20460, 64, 8) is not None
     assert _lib.unsupported(_lib.OP_FORWARD, 32, 256, 256, 64, 8) is None
     assert _lib.unsupported(_lib.OP_BACKWARD, 32, 256, 256, 64, 8) is None
+    # K = 65 leaves no slice with a slot per lane; the cell chains take it, unless the slices
+    # are forced
+    for op in (_lib.OP_FORWARD, _lib.OP_BACKWARD):
+        assert _lib.unsupported(op, 2, 16, 256, 64, 65) is None
+        try:
+            _lib.set_path("slice")
+            assert "slice path" in _lib.unsupported(op, 2, 16, 256, 64, 65)
+            _lib.set_path("chain")
+            assert "chain path" in _lib.unsupported(op, 2, 16, 512, 64, 257)
+        finally:
+            _lib.set_path("auto")
+    assert _lib.unsupported(_lib.OP_FORWARD, 2, 16, 14000, 64, 8) is not None  # neither
     assert W.cell_update_unsupported(256, 64, 8) is None
     assert W.cell_update_unsupported(256, 64, 65) is not None
     assert W.cell_update_unsupported(16, 8, 17) is not None
@@ -148,9 +160,70 @@ def test_decline_predicates_follow_the_library_geometry():
     assert status == 1 and b"LDS" in lib.hsn_win_last_error()
 
 
+def _align(n: int) -> int:
+    return (n + 255) // 256 * 256
+
+
+@pytest.mark.parametrize("name", ["ref", "bf16", "tbptt", "skewed", "tiny"])
+def test_workspace_and_path_follow_the_shape(name):
+    """The path a forward / backward call takes and the workspace it needs, host arithmetic
+    only: the slices where a wavefront's piece of a slot row is a full 32-byte sector (ref,
+    tbptt: 8 fp32 columns), the cell chains where it would be narrower (bf16: 4 bf16 columns,
+    skewed: 2); the chain workspace is the row lists (B(N+1) + BTK int32), the per-position
+    sums (BTd fp32) and, in the forward, the per-slot deltas (BTKd fp32), each 256-aligned,
+    then the RMS candidate's input."""
+    from hsn_amd import _lib, build
+    from hsn_amd.window import rms_scratch_bytes
+    from hsn_amd.workload import CONFIGS
+
+    if build.stale() is not None:
+        pytest.skip("library not built here")
+    c = CONFIGS[name]
+    io = _lib.DTYPE_BF16 if c.io == "bf16" else _lib.DTYPE_F32
+    elem = 2 if c.io == "bf16" else 4
+    want = "chain" if name in ("bf16", "skewed") else "slice"
+    B, T, N, d, K = c.B, c.T, c.N, c.d, c.K
+    rms = _align(rms_scratch_bytes(B * T * K, d, elem))
+    for op in (_lib.OP_FORWARD, _lib.OP_BACKWARD):
+        assert _lib.path_for(op, B, T, N, d, K, io) == want
+        chain = 0
+        if want == "chain":
+            chain = _align(B * (N + 1) * 4) + _align(B * T * K * 4) + _align(B * T * d * 4)
+            if op == _lib.OP_FORWARD:
+                chain += _align(B * T * K * d * 4)
+        assert _lib.workspace_bytes(op, B, T, N, d, K, io, False) == chain
+        assert _lib.workspace_bytes(op, B, T, N, d, K, io, True) == chain + rms
+    try:  # a forced path changes the answer where both paths take the shape
+        _lib.set_path("chain")
+        assert _lib.path_for(_lib.OP_FORWARD, B, T, N, d, K, io) == "chain"
+        _lib.set_path("slice")
+        assert _lib.path_for(_lib.OP_FORWARD, B, T, N, d, K, io) == "slice"
+    finally:
+        _lib.set_path("auto")
+    lib = _lib.library()
+    assert lib.hsn_win_set_path(3) == 1 and b"path" in lib.hsn_win_last_error()
+
+
+def test_forward_rejects_a_short_workspace_without_a_gpu():
+    """A workspace below what hsn_win_workspace_bytes reports is refused before any launch."""
+    from hsn_amd import _lib, build
+
+    if build.stale() is not None:
+        pytest.skip("library not built here")
+    lib = _lib.library()
+    B, T, N, d, K = 2, 8, 64, 64, 16  # bf16: the chain path, a workspace is needed
+    need = _lib.workspace_bytes(_lib.OP_FORWARD, B, T, N, d, K, _lib.DTYPE_BF16, False)
+    assert need > 0
+    status = lib.hsn_win_forward(1, 1, _lib.DTYPE_BF16, None, 0, 0.0, 1, need - 1, 1, 1, 1, 1,
+                                 None, None, None, None, None, None, None, None, None, None,
+                                 None, B, T, N, d, K, None)
+    assert status == 1 and b"workspace must hold" in lib.hsn_win_last_error()
+
+
 def test_noalloc_forward_rejects_a_workspace_above_its_array_without_a_gpu():
-    """The no-allocation forward checks the RMS workspace against its 32 MiB array before any
-    HIP call: 1,048,576 slots of d = 64 (260 MiB) return HSN_ERR_SIZE_OVERFLOW."""
+    """The no-allocation forward checks its workspace against its 32 MiB array before any HIP
+    call: 1,048,576 slots of d = 64 (the RMS input alone is 260 MiB) return
+    HSN_ERR_SIZE_OVERFLOW."""
     from hsn_amd import _lib, build
 
     if build.stale() is not None:

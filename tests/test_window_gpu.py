@@ -29,6 +29,16 @@ def dev(cuda_device):
     return cuda_device
 
 
+@pytest.fixture(params=["slice", "chain"])
+def path(request, dev):
+    """Each forward / backward test runs on both sweep designs (the library's path setting)."""
+    from hsn_amd import _lib
+
+    _lib.set_path(request.param)
+    yield request.param
+    _lib.set_path("auto")
+
+
 def _close(got, want, tol, what=""):
     got = got.detach().float().cpu()
     want = want.detach().float().cpu()
@@ -182,6 +192,9 @@ WINDOW_CASES = [
     dict(B=256, T=70, N=32, d=64, K=8, io="f32"),  # one chunk per row, several sub-blocks
     dict(B=3, T=5, N=16, d=4, K=4, io="f32"),  # fewer positions than chunks per row
     dict(B=3, T=7, N=20, d=7, K=3, io="bf16", rms=True),  # odd d and odd B*T*K: RMS workspace
+    dict(B=2, T=200, N=8, d=100, K=4, io="f32"),  # long chains: several event windows per cell
+    # hot cells (Zipf bias) whose events overflow a chain group's staged list; padded slots
+    dict(B=2, T=256, N=512, d=16, K=16, io="bf16", bias="zipf", limit=0.02),
 ]
 
 
@@ -191,7 +204,7 @@ def _window_case(c, seed):
     M = c.get("M", 1)
     cfg_w = CONFIGS["tiny"].scaled(B=c["B"], T=c["T"], N=c["N"], d=c["d"], K=c["K"], M=M,
                                    h0_sigma=0.3, reset_p=0.08, reset_at=((0, 3),),
-                                   io=c["io"])
+                                   io=c["io"], logit_bias=c.get("bias", "none"))
     w = make_window(cfg_w, seed)
     cot = make_cotangents(cfg_w, seed, carried=True)
     cost = torch.full((M,), 1.0 / (c["N"] * M)) if M == 1 else torch.tensor([0.03125, 0.0625])
@@ -205,7 +218,7 @@ def _valid_mask(t, valid):
 
 
 @pytest.mark.parametrize("case", range(len(WINDOW_CASES)))
-def test_window_forward_and_backward_match_oracle(dev, case):
+def test_window_forward_and_backward_match_oracle(dev, path, case):
     from hsn_amd import window
 
     c = WINDOW_CASES[case]
@@ -252,7 +265,7 @@ def test_window_forward_and_backward_match_oracle(dev, case):
 
 
 @pytest.mark.parametrize("N,d", [(256, 64), (300, 16), (16, 8)])
-def test_forward_h_max_propagates_a_nan_in_an_unwritten_cell(dev, N, d):
+def test_forward_h_max_propagates_a_nan_in_an_unwritten_cell(dev, path, N, d):
     """A NaN in a start-state cell no slot writes makes the row maximum NaN until a reset clears
     the row (the reference's test_p2_10_window.py:540-560), on both of the forward's maxima
     paths: per-cell maxima in LDS (N <= 256) and the tracked maximum with rescans (N > 256)."""
@@ -275,7 +288,7 @@ def test_forward_h_max_propagates_a_nan_in_an_unwritten_cell(dev, N, d):
     assert torch.equal(torch.isnan(got["h"].cpu()), torch.isnan(want["h"]))
 
 
-def test_forward_zeroes_a_row_maximum_buffer_it_is_given(dev):
+def test_forward_zeroes_a_row_maximum_buffer_it_is_given(dev, path):
     """``forward(h_max=buf)`` max-reduces into ``buf``: it zeroes it first, so a buffer holding
     garbage (here larger than every maximum) gives the same maxima as the routed window."""
     from hsn_amd import window
@@ -291,7 +304,7 @@ def test_forward_zeroes_a_row_maximum_buffer_it_is_given(dev):
     assert torch.equal(out["h_max"], ref["h_max"]) and out["h_max"] is buf
 
 
-def test_backward_without_optional_cotangents(dev):
+def test_backward_without_optional_cotangents(dev, path):
     from hsn_amd import window
 
     c = dict(B=2, T=12, N=24, d=8, K=4, io="f32", limit=0.2)
@@ -315,6 +328,50 @@ def test_backward_without_optional_cotangents(dev):
                    f"d_q0 {present}")
         else:
             assert bool((gb[3] == 0).all())
+
+
+@pytest.mark.parametrize("io", ["f32", "bf16"])
+def test_chain_takes_more_slots_than_a_wavefront(dev, io):
+    """K = 80 slots per position, more than a wavefront's lanes: the slices (a slot per lane)
+    and the router decline it, the cell chains take up to 255. The oracle's decisions, packed,
+    through the forward and the backward against the oracle; a budget of 0.3 leaves 20 padded
+    slots per position."""
+    from hsn_amd import _lib, window
+
+    c = dict(B=2, T=12, N=200, d=32, K=80, io=io, limit=0.3)
+    cfg_w, w, cot, cost, cfg, _ = _window_case(c, 91)
+    B, T, N, d, K = c["B"], c["T"], c["N"], c["d"], c["K"]
+    code = _lib.DTYPE_F32 if io == "f32" else _lib.DTYPE_BF16
+    assert _lib.path_for(_lib.OP_FORWARD, B, T, N, d, K, code) == "chain"
+    assert _lib.path_for(_lib.OP_BACKWARD, B, T, N, d, K, code) == "chain"
+    tol = BF16_TOL if io == "bf16" else F32_TOL
+    want = O.window_forward(w["logits"], w["y"], w["gate_pre"], w["reset"], w["h0"], w["q0"],
+                            w["age0"], w["pos0"], cost, **_oracle_route_kwargs(cfg))
+    assert 0 < int((~want["valid"]).sum()) < want["valid"].numel()
+    D = {k: v.to(dev) for k, v in w.items()}
+    slots = window.pack_slots(want["cells"], want["valid"]).to(dev)
+    h_max = torch.empty(B, T, device=dev)
+    got = window.forward(D["y"], D["gate_pre"], D["reset"], slots, D["h0"], D["q0"], D["age0"],
+                         D["pos0"], N, h_max=h_max)
+    for name in ("q_pre", "q_post", "h_old", "h_max"):
+        _close(got[name], want[name], tol, name)
+    _close(got["h_sel"], want["h_sel"], tol, "h_sel")  # padded slots show cell 0 after the update
+    _close(got["h"], want["h"], tol, "h_T")
+    _close(got["q"], want["q"], tol, "q_T")
+    assert torch.equal(got["age"].cpu(), want["age"]) and torch.equal(got["pos"].cpu(), want["pos"])
+    d_h_sel = _valid_mask(cot["d_h_sel"], want["valid"])
+    wb = O.window_backward(w["y"], w["gate_pre"], want["h_old"], want["cells"], want["valid"],
+                           w["reset"], N, cot["d_q_pre"], cot["d_q_post"], d_h_sel, cot["d_h_T"],
+                           cot["d_q_T"])
+    gb = window.backward(D["y"], D["gate_pre"], want["h_old"].to(dev), slots, D["reset"], N,
+                         cot["d_q_pre"].to(dev), cot["d_q_post"].to(dev), d_h_sel.to(dev),
+                         cot["d_h_T"].to(dev), cot["d_q_T"].to(dev))
+    for name, g_, w_ in zip(("dy", "dgate", "d_h0"), gb[:3], wb[:3]):
+        _close(g_, w_, tol, name)
+    _close(gb[3], _d_q0_exact(w["reset"], cot["d_q_pre"], cot["d_q_post"], cot["d_q_T"], N), tol,
+           "d_q0")
+    zero_pad = ~want["valid"]
+    assert bool((gb[0].cpu()[zero_pad] == 0).all()) and bool((gb[1].cpu()[zero_pad] == 0).all())
 
 
 @pytest.mark.parametrize("shape", [(3, 7, 5, 3, 4), (1, 1, 2, 1, 1), (4, 50, 300, 8, 64),
@@ -477,7 +534,7 @@ def _two_window_objective(w1, w2, y1, g1, h0, q0, y2, g2, cost, wq, wh):
 # --------------------------------------------------------------------------------------------
 
 
-def test_ref_shape_window_rows_match_oracle(dev):
+def test_ref_shape_window_rows_match_oracle(dev, path):
     """The metric's configuration (B32 T256 N256 d64 K8 fp32) on the GPU; rows are independent,
     so rows 0 and 17 are checked against the oracle run on those rows alone, and size-independent
     properties on all rows: q stays the mean of h (q0 = mean h0 and every update moves q by the

@@ -1,7 +1,7 @@
-"""The entry point that allocates nothing (``hsn_win_forward_noalloc``: the RMS candidate's
-workspace is the library's own device array) against ``hsn_win_forward`` with a caller
-workspace, through the C ABI, on two calls in a row, the second with a smaller window. The
-same kernels run on the same inputs, so every output is bit-identical. GPU only."""
+"""The entry point that allocates nothing (``hsn_win_forward_noalloc``: its workspace is the
+library's own device array) against ``hsn_win_forward`` with a caller workspace, through the C
+ABI, on two calls in a row, the second with a smaller window, on each sweep design. The same
+kernels run on the same inputs, so every output is bit-identical. GPU only."""
 
 from __future__ import annotations
 
@@ -43,7 +43,7 @@ def _call(name, dev, w, slots, cand_w, out, dims, io, workspace=None):
     code = _lib.DTYPE_F32 if io == "f32" else _lib.DTYPE_BF16
     head = [ptr(w["y"]), ptr(w["gate_pre"]), code, ptr(cand_w), 1, 1e-6]
     if name == "hsn_win_forward":
-        head.append(ptr(workspace))
+        head += [ptr(workspace), 0 if workspace is None else workspace.numel()]
     tail = [ptr(w["reset"]), ptr(slots), ptr(w["h0"]), ptr(w["q0"]), ptr(w["age0"]),
             ptr(w["pos0"]), ptr(out["q_pre"]), ptr(out["q_post"]), ptr(out["h_sel"]),
             ptr(out["h_old"]), ptr(out["h_max"]), ptr(out["h"]), ptr(out["q"]), ptr(out["age"]),
@@ -51,20 +51,27 @@ def _call(name, dev, w, slots, cand_w, out, dims, io, workspace=None):
     _lib.call(name, *head, *tail)
 
 
+@pytest.mark.parametrize("path", ["slice", "chain"])
 @pytest.mark.parametrize("io", ["f32", "bf16"])
-def test_noalloc_forward_equals_the_forward_with_a_workspace(cuda_device, io):
-    from hsn_amd.window import rms_scratch_bytes
+def test_noalloc_forward_equals_the_forward_with_a_workspace(cuda_device, io, path):
+    from hsn_amd import _lib
 
     dev = cuda_device
-    for dims, seed in (((6, 40, 64, 32, 8), 3), ((2, 9, 20, 7, 3), 4)):  # second call smaller
-        B, T, N, d, K = dims
-        w, slots, cand_w = _window(dev, B, T, N, d, K, io, seed)
-        elem = 4 if io == "f32" else 2
-        ws = torch.empty(rms_scratch_bytes(B * T * K, d, elem), dtype=torch.uint8, device=dev)
-        want = _outputs(dev, B, T, N, d, K, io)
-        _call("hsn_win_forward", dev, w, slots, cand_w, want, dims, io, ws)
-        got = _outputs(dev, B, T, N, d, K, io)
-        _call("hsn_win_forward_noalloc", dev, w, slots, cand_w, got, dims, io)
-        torch.cuda.synchronize()
-        for name in want:
-            assert torch.equal(got[name], want[name]), (name, dims, io)
+    code = _lib.DTYPE_F32 if io == "f32" else _lib.DTYPE_BF16
+    try:
+        _lib.set_path(path)
+        for dims, seed in (((6, 40, 64, 32, 8), 3), ((2, 9, 20, 7, 3), 4)):  # second smaller
+            B, T, N, d, K = dims
+            assert _lib.path_for(_lib.OP_FORWARD, B, T, N, d, K, code) == path
+            w, slots, cand_w = _window(dev, B, T, N, d, K, io, seed)
+            n = _lib.workspace_bytes(_lib.OP_FORWARD, B, T, N, d, K, code, True)
+            ws = torch.empty(n, dtype=torch.uint8, device=dev)
+            want = _outputs(dev, B, T, N, d, K, io)
+            _call("hsn_win_forward", dev, w, slots, cand_w, want, dims, io, ws)
+            got = _outputs(dev, B, T, N, d, K, io)
+            _call("hsn_win_forward_noalloc", dev, w, slots, cand_w, got, dims, io)
+            torch.cuda.synchronize()
+            for name in want:
+                assert torch.equal(got[name], want[name]), (name, dims, io, path)
+    finally:
+        _lib.set_path("auto")
