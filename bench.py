@@ -39,6 +39,8 @@ def _args():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--config", default="ref")
     p.add_argument("--seed", type=int, default=1)
+    p.add_argument("--path", choices=["auto", "slice", "chain"], default="auto",
+                   help="the sweeps' design (auto: the library's choice by shape)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-h-max", action="store_true", help="do not produce the row maxima")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -125,8 +127,14 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("no GPU visible", file=sys.stderr)
         return 1
+    from hsn_amd import _lib
+
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
+    _lib.set_path(args.path)
+    io_code = _lib.DTYPE_BF16 if cfg.io == "bf16" else _lib.DTYPE_F32
+    paths = {op: _lib.path_for(code, cfg.B, cfg.T, cfg.N, cfg.d, cfg.K, io_code)
+             for op, code in (("forward", _lib.OP_FORWARD), ("backward", _lib.OP_BACKWARD))}
     w = {k: v.to(dev) for k, v in make_window(cfg, args.seed).items()}
     cot = make_cotangents(cfg, args.seed, carried=True)
     cot = {k: (None if v is None else v.to(dev)) for k, v in cot.items()}
@@ -234,7 +242,7 @@ def main() -> int:
         "data": "synthetic (seeded workload generator, hsn_amd/workload.py)",
         "config": {"workload": cfg.name, "shape": describe(cfg), "B": B, "T": T, "N": N, "d": d,
                    "K": K, "M": cfg.M, "storage": cfg.io, "h_max": not args.no_h_max,
-                   "parallelism": "single GPU"},
+                   "sweep_path": paths, "parallelism": "single GPU"},
         "roofline": {
             "bound": "hbm",
             "kernel": dominant,

@@ -4,7 +4,9 @@
 // element with a 32-bit voffset and the position with a uniform soffset (an SGPR), so a load or
 // a store costs no per-lane address arithmetic. Raw buffers check voffset against the size: a
 // voffset past it (kOob) reads 0 and drops a store, which masks inactive lanes without a branch,
-// and a resource of size 0 (an absent optional tensor) reads zeros and drops every store.
+// and a resource of size 0 (an absent optional tensor) reads zeros and drops every store. The
+// soffset is not part of that check on this architecture family: every soffset stays inside the
+// tensor's row, and only the voffset masks.
 #pragma once
 
 #include "common.cuh"

@@ -11,11 +11,11 @@
 //                 of positions from a bit per position per cell (popcount below t):
 //                 deterministic.
 //   chain_fwd     (row, group of cells; a wavefront per cell): h_old, h_sel, the end state, the
-//                 ages, each valid slot's delta h_sel - h_old in fp32 where the summary needs
-//                 it; the row maximum of |h| per position from each cell's value on the
-//                 intervals between its events (LDS atomic max, then one global atomic max per
-//                 position and group).
-//   summary_delta (row, position): D[t] = the sum of the valid slots' deltas.
+//                 ages, each valid slot's delta h_sel - h_old in fp32 where the rows are bf16
+//                 or omitted; the row maximum of |h| per position from each cell's value on the
+//                 intervals between its events (LDS atomic max), a table per group.
+//   summary_delta (row, position): D[t] = the sum of the valid slots' deltas; the row maximum,
+//                 the largest of the groups'.
 //   summary_scan_fwd (row, 64 columns): q before and after every position, a scan over time
 //                 of D / N with the resets.
 //   summary_scan_bwd (row, 64 columns): the summary cotangent R, a reverse scan in fp64, as the
@@ -52,18 +52,20 @@ constexpr int kEvWin = 64;  // events per window: one event per lane
 // ------------------------------------------------------------------------------------------
 
 constexpr int kListThreads = 1024;
+constexpr int kListU = 8;  // slots per thread and block of positions
 
 // positions per block of the rank pass (a multiple of 32): a bit per position per cell in at most
-// 64 KiB, and at most 2048 slots unless one word of positions has more
+// 64 KiB, and at most 2048 slots unless one word of positions has more (32 K <= 8160 slots, within
+// the kListU * kListThreads a block's threads hold)
 __host__ __device__ inline int list_block(int N, int T, int K) {
     int P = 32;
     while (P < T && int64_t(N) * (2 * P / 32) * 4 <= 65536 && 2 * P * K <= 2048) P *= 2;
     return P;
 }
 // the scan partials' words: the 16 wavefronts' and the row's total, or a prefix per word of the
-// block's padded-slot bits
+// block's padded-slot bits and their total
 __host__ __device__ inline int list_partials(int P, int K) {
-    const int pkw = (P * K + 31) / 32;
+    const int pkw = (P * K + 31) / 32 + 1;
     return pkw > 65 ? pkw : 65;
 }
 __host__ __device__ inline int list_words(int N, int T, int K) {  // LDS words of row_lists
@@ -100,9 +102,17 @@ __global__ __launch_bounds__(kListThreads) void row_lists(ListArgs a) {
     for (int c = tid; c < N; c += kListThreads) cnt[c] = 0;
     if (tid == 0) misc[0] = 0;
     __syncthreads();
-    for (int64_t i = tid; i < int64_t(T) * K; i += kListThreads) {
-        const int c = slot_cell(a.slots, row + i, N);
-        if (c >= 0) atomicAdd(&cnt[c], 1);
+    const int n_slots = T * K;
+    for (int i0 = tid; i0 < n_slots; i0 += kListThreads * kListU) {  // kListU loads in flight
+        int cs[kListU];
+#pragma unroll
+        for (int u = 0; u < kListU; ++u) {
+            const int i = i0 + u * kListThreads;
+            cs[u] = i < n_slots ? slot_cell(a.slots, row + i, N) : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < kListU; ++u)
+            if (cs[u] >= 0) atomicAdd(&cnt[cs[u]], 1);
     }
     __syncthreads();
     // exclusive scan of the counts (a chunk of cells per thread, then the chunks' prefix)
@@ -139,31 +149,56 @@ __global__ __launch_bounds__(kListThreads) void row_lists(ListArgs a) {
     const int n_valid = wsum[kListThreads / 64];
     if (tid == 0) a.ptr[int64_t(b) * (N + 1) + N] = n_valid;
     int32_t* ev = a.ev + row;
+    // blocks of P positions (P * K <= kListU * kListThreads slots): a thread's slots of the next
+    // block are loaded while the current one is ranked
+    int cur[kListU], nxt[kListU];
+    auto fetch = [&](int t0, int (&cs)[kListU]) __attribute__((always_inline)) {
+        const int n = min(P, T - t0) * K;
+#pragma unroll
+        for (int u = 0; u < kListU; ++u) {
+            const int i = tid + u * kListThreads;
+            cs[u] = t0 < T && i < n ? slot_cell(a.slots, row + int64_t(t0) * K + i, N) : -2;
+        }
+    };
+    fetch(0, cur);
     for (int t0 = 0; t0 < T; t0 += P) {
         const int pn = min(P, T - t0);
+        fetch(t0 + P, nxt);
         __syncthreads();
         for (int i = tid; i < N * PW; i += kListThreads) mask[i] = 0u;
         for (int i = tid; i < PKW; i += kListThreads) pmask[i] = 0u;
         __syncthreads();
-        for (int i = tid; i < pn * K; i += kListThreads) {
+#pragma unroll
+        for (int u = 0; u < kListU; ++u) {
+            const int i = tid + u * kListThreads, c = cur[u];
+            if (c == -2) continue;  // past the block
             const int tl = i / K;
-            const int c = slot_cell(a.slots, row + int64_t(t0) * K + i, N);
             if (c >= 0) atomicOr(&mask[c * PW + (tl >> 5)], 1u << (tl & 31));
             else atomicOr(&pmask[i >> 5], 1u << (i & 31));
         }
         __syncthreads();
-        if (tid == 0) {  // the padded slots' prefix per word, in wsum
+        if (tid < 64) {  // the padded slots' exclusive prefix per word, in wsum (wavefront 0)
             int acc = 0;
-            for (int w = 0; w < PKW; ++w) {
-                wsum[w] = acc;
-                acc += __popc(pmask[w]);
+            for (int w0 = 0; w0 < PKW; w0 += 64) {
+                const int w = w0 + tid;
+                const int v = w < PKW ? __popc(pmask[w]) : 0;
+                int incl = v;
+                for (int o = 1; o < 64; o <<= 1) {
+                    const int u = __shfl_up(incl, o, 64);
+                    if (tid >= o) incl += u;
+                }
+                if (w < PKW) wsum[w] = acc + incl - v;
+                acc += __shfl(incl, 63, 64);
             }
+            if (tid == 0) wsum[PKW] = acc;  // the block's padded slots
         }
         __syncthreads();
         const int pad0 = misc[0];
-        for (int i = tid; i < pn * K; i += kListThreads) {
+#pragma unroll
+        for (int u = 0; u < kListU; ++u) {
+            const int i = tid + u * kListThreads, c = cur[u];
+            if (c == -2) continue;
             const int tl = i / K, k = i - tl * K;
-            const int c = slot_cell(a.slots, row + int64_t(t0) * K + i, N);
             const int t = t0 + tl;
             if (c >= 0) {
                 int rank = cnt[c];
@@ -176,17 +211,16 @@ __global__ __launch_bounds__(kListThreads) void row_lists(ListArgs a) {
                 ev[n_valid + pad0 + r] = (t << 8) | k;
             }
         }
+        (void)pn;
         __syncthreads();
         for (int c = tid; c < N; c += kListThreads) {
             int v = 0;
             for (int w = 0; w < PW; ++w) v += __popc(mask[c * PW + w]);
             cnt[c] += v;
         }
-        if (tid == 0) {
-            int v = 0;
-            for (int w = 0; w < PKW; ++w) v += __popc(pmask[w]);
-            misc[0] = pad0 + v;
-        }
+        if (tid == 0) misc[0] = pad0 + wsum[PKW];
+#pragma unroll
+        for (int u = 0; u < kListU; ++u) cur[u] = nxt[u];
     }
 }
 
@@ -292,7 +326,8 @@ struct FwdArgs {
     void* h_old;           // [B, T, K, d] io (optional)
     void* h_sel;           // (optional)
     float* delta;          // [B, T, K, d] fp32: h_sel - h_old of the valid slots (optional)
-    float* h_max;          // [B, T], zero on entry (optional)
+    uint32_t* hm_groups;   // [B, T, G]: each group's row maximum per position, |h| bits
+                           // (optional: with the row maxima)
     float* h_T;            // [B, N, d] (optional)
     int64_t* age_T;        // [B, N] (optional)
     int64_t* pos_T;        // [B] (optional)
@@ -326,7 +361,7 @@ __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
     int* next = reinterpret_cast<int*>(hm + T);          // [1]
     int* cptr = next + 1;                                // [C + 1]
     int* cev = cptr + a.C + 1;                           // [stage]
-    const bool want_max = a.h_max != nullptr;
+    const bool want_max = a.hm_groups != nullptr;
     const int c_begin = g * a.C, c_end = min(N, c_begin + a.C);
     const int nc = c_end - c_begin;
     const int32_t* ptr = a.ptr + int64_t(b) * (N + 1);
@@ -493,11 +528,11 @@ __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
         }
     }
     if (a.pos_T && g == 0 && tid == 0) a.pos_T[b] = lrT >= 0 ? int64_t(T - lrT) : a.pos0[b] + T;
-    if (want_max) {
+    if (want_max) {  // the group's maxima, reduced over the groups by summary_delta
         __syncthreads();
-        unsigned int* hmr = reinterpret_cast<unsigned int*>(a.h_max + int64_t(b) * T);
-        for (int p = tid; p < T; p += kChainThreads)
-            if (hm[p]) atomicMax(hmr + p, hm[p]);
+        const int G = gridDim.y;
+        uint32_t* hg = a.hm_groups + int64_t(b) * T * G + g;
+        for (int p = tid; p < T; p += kChainThreads) hg[int64_t(p) * G] = hm[p];
     }
 }
 
@@ -511,12 +546,14 @@ struct DeltaArgs {
     const float* delta;   // [B, T, K, d] fp32 (not PAIR)
     const int32_t* slots; // [B, T, K]
     float* D;             // [B, T, d]
-    int B, T, N, d, K;
+    const uint32_t* hm_groups;  // [B, T, G] (optional)
+    float* h_max;         // [B, T]: the maximum over the groups (with hm_groups)
+    int B, T, N, d, K, G;
 };
 
 // A wavefront per (row, position), lanes over the columns: D[t] = the sum over the position's
-// valid slots, in slot order, of h_sel - h_old (PAIR: fp32 outputs, the forward's own values)
-// or of the forward's fp32 deltas.
+// valid slots, in slot order, of h_sel - h_old as stored (PAIR: fp32 rows, the forward's own
+// values) or of the chains' fp32 deltas (bf16 rows, or an omitted h_old / h_sel).
 template <typename IO, int V, bool PAIR>
 __global__ __launch_bounds__(256) void summary_delta(DeltaArgs a) {
     const int pos = blockIdx.x * 4 + uniform(threadIdx.x / 64);
@@ -568,6 +605,13 @@ __global__ __launch_bounds__(256) void summary_delta(DeltaArgs a) {
 #pragma unroll
     for (int v = 0; v < V; ++v)
         if (lane + 64 * v < d) Dp[lane + 64 * v] = D[v];
+    if (a.hm_groups) {  // the row maximum: the largest of the groups' (|h| bits, NaN above inf)
+        const uint32_t* hg = a.hm_groups + (int64_t(b) * a.T + pos) * a.G;
+        uint32_t m = 0u;
+        for (int g = lane; g < a.G; g += 64) m = umax(m, hg[g]);
+        m = wave_max_from_groups<1>(m);
+        if (lane == 0) a.h_max[int64_t(b) * a.T + pos] = __uint_as_float(m);
+    }
 }
 
 constexpr int kScanWaves = 16;
@@ -597,7 +641,8 @@ struct ScanArgs {
 // into its start value and replays its positions in the reference's order per position
 // (python/hsn/kernels/native.py:302 with state.py:267-283): q_pre[t] = (reset[t] ? 0 : q),
 // q_post[t] = q_pre[t] + D[t] / N. Rows of [., T, d] tensors are buffer resources: a lane's
-// column is its voffset, the position a uniform soffset.
+// column is its voffset, the position a uniform soffset (kept inside the row: only the voffset
+// masks an access).
 template <typename IO>
 __global__ __launch_bounds__(64 * kScanWaves) void summary_scan_fwd(ScanArgs a) {
     __shared__ int rss[kScanWaves];
@@ -621,8 +666,10 @@ __global__ __launch_bounds__(64 * kScanWaves) void summary_scan_fwd(ScanArgs a) 
         const int t0 = r0 + w * kR;
         float Dv[kR];
 #pragma unroll
-        for (int j = 0; j < kR; ++j)  // past T: the soffset runs out of the buffer, reads 0
-            Dv[j] = bload<float>(rD, vo4, uint32_t(min(t0 + j, T)) * d * 4u);
+        for (int j = 0; j < kR; ++j) {  // past T: the lane offset masks the load (reads 0)
+            const bool in = t0 + j < T;
+            Dv[j] = bload<float>(rD, in ? vo4 : kOob, uint32_t(in ? t0 + j : 0) * d * 4u);
+        }
         const uint32_t rsm = static_cast<uint32_t>(ballot(
             lane < kR && t0 + lane < T && a.reset != nullptr && a.reset[int64_t(b) * T + t0 + lane] != 0));
         float c = 0.0f;
@@ -640,12 +687,14 @@ __global__ __launch_bounds__(64 * kScanWaves) void summary_scan_fwd(ScanArgs a) 
         for (int j = w; j < kScanWaves; ++j) qe = (rss[j] ? 0.0f : qe) + cx[j][lane];
         float qq = qs;
 #pragma unroll
-        for (int j = 0; j < kR; ++j) {
-            const uint32_t so = uint32_t(min(t0 + j, T)) * d * sizeof(IO);
+        for (int j = 0; j < kR; ++j) {  // past T: the lane offset drops the stores
+            const bool in = t0 + j < T;
+            const uint32_t so = uint32_t(in ? t0 + j : 0) * d * sizeof(IO);
+            const uint32_t vj = in ? vo : kOob;
             if ((rsm >> j) & 1u) qq = 0.0f;
-            bstore_f32<IO>(qq, rqa, vo, so);
+            bstore_f32<IO>(qq, rqa, vj, so);
             qq = qq + divn(Dv[j]);
-            bstore_f32<IO>(qq, rqb, vo, so);
+            bstore_f32<IO>(qq, rqb, vj, so);
         }
         q = qe;
         __syncthreads();  // before the next round reuses the exchange
@@ -682,10 +731,11 @@ __global__ __launch_bounds__(64 * kScanWaves) void summary_scan_bwd(ScanArgs a) 
         const int t0 = rr * span + w * kR;
         float va[kR], vb[kR];
 #pragma unroll
-        for (int j = 0; j < kR; ++j) {  // past T: the soffset runs out of the buffers, reads 0
-            const uint32_t so = uint32_t(min(t0 + j, T)) * d * sizeof(IO);
-            va[j] = to_f32(bload<IO>(rpa, vo, so));
-            vb[j] = to_f32(bload<IO>(rpb, vo, so));
+        for (int j = 0; j < kR; ++j) {  // past T: the lane offset masks the loads (reads 0)
+            const bool in = t0 + j < T;
+            const uint32_t so = uint32_t(in ? t0 + j : 0) * d * sizeof(IO);
+            va[j] = to_f32(bload<IO>(rpa, in ? vo : kOob, so));
+            vb[j] = to_f32(bload<IO>(rpb, in ? vo : kOob, so));
         }
         const uint32_t rsm = static_cast<uint32_t>(ballot(
             lane < kR && t0 + lane < T && a.reset != nullptr && a.reset[int64_t(b) * T + t0 + lane] != 0));
@@ -707,7 +757,8 @@ __global__ __launch_bounds__(64 * kScanWaves) void summary_scan_bwd(ScanArgs a) 
 #pragma unroll
         for (int j = kR - 1; j >= 0; --j) {
             Rr += double(vb[j]);
-            bstore(static_cast<float>(divn(Rr)), rsh, vo4, uint32_t(min(t0 + j, T)) * d * 4u);
+            const bool in = t0 + j < T;
+            bstore(static_cast<float>(divn(Rr)), rsh, in ? vo4 : kOob, uint32_t(in ? t0 + j : 0) * d * 4u);
             Rr += double(va[j]);
             if ((rsm >> j) & 1u) Rr = 0.0;
         }

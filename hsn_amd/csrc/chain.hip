@@ -105,6 +105,9 @@ WorkspaceLayout workspace_layout(int op, int B, int T, int N, int d, int K, size
         if (op == HSN_OP_FORWARD) {
             L.delta = at;
             at = align_up(at + size_t(slots) * d * 4);
+            const int C = chain_cells(B, N);
+            L.hmax = at;
+            at = align_up(at + size_t(B) * T * ((N + C - 1) / C) * 4);
         }
     }
     L.rms = at;
@@ -191,7 +194,8 @@ void chain_forward(const void* y, const void* gate_pre, int io_dtype, const uint
     int32_t* ptr = reinterpret_cast<int32_t*>(ws + L.ptr);
     int32_t* ev = reinterpret_cast<int32_t*>(ws + L.ev);
     float* D = reinterpret_cast<float*>(ws + L.sum);
-    // the summary reads the fp32 outputs themselves; else the chains' fp32 deltas
+    // the summary reads the fp32 rows themselves; else the chains' fp32 deltas (bf16 rows are
+    // rounded: summing them would leave q off the mean of h by up to a rounding of |h|)
     const bool pair = io_dtype == HSN_DTYPE_F32 && h_sel && h_old;
     float* delta = pair ? nullptr : reinterpret_cast<float*>(ws + L.delta);
     build_lists(slots, ptr, ev, B, T, N, K, st);
@@ -199,13 +203,15 @@ void chain_forward(const void* y, const void* gate_pre, int io_dtype, const uint
     fa.y = y, fa.g = gate_pre, fa.ptr = ptr, fa.ev = ev, fa.reset = reset;
     fa.h0 = h0, fa.age0 = age0, fa.pos0 = pos0;
     fa.h_old = h_old, fa.h_sel = h_sel, fa.delta = delta;
-    fa.h_max = h_max, fa.h_T = h_T, fa.age_T = age_T, fa.pos_T = pos_T;
+    uint32_t* hm_groups = h_max ? reinterpret_cast<uint32_t*>(ws + L.hmax) : nullptr;
+    fa.hm_groups = hm_groups, fa.h_T = h_T, fa.age_T = age_T, fa.pos_T = pos_T;
     fa.B = B, fa.T = T, fa.N = N, fa.d = d, fa.K = K;
     fa.C = chain_cells(B, N), fa.stage = chain_stage(T, N, K, fa.C);
     const size_t lds = size_t(chain::chain_words(T, fa.C, fa.stage)) * 4;
     chain::DeltaArgs da{};
     da.h_old = h_old, da.h_sel = h_sel, da.delta = delta, da.slots = slots, da.D = D;
-    da.B = B, da.T = T, da.N = N, da.d = d, da.K = K;
+    da.hm_groups = hm_groups, da.h_max = h_max;
+    da.B = B, da.T = T, da.N = N, da.d = d, da.K = K, da.G = (N + fa.C - 1) / fa.C;
     chain::ScanArgs sa{};
     sa.D = D, sa.q0 = q0, sa.q_pre = q_pre, sa.q_post = q_post, sa.q_T = q_T;
     sa.reset = reset, sa.B = B, sa.T = T, sa.d = d, sa.divn = make_divn(N);

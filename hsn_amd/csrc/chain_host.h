@@ -13,10 +13,11 @@ enum PathCode : int { kPathAuto = 0, kPathSlice = 1, kPathChain = 2 };
 
 // The workspace of hsn_win_forward / hsn_win_backward, byte offsets into it (256-aligned):
 // the RMS candidate's normalised input (both paths), and on the chain path the row lists, the
-// per-position sums (the forward's D, the backward's share) and the forward's per-slot deltas.
+// per-position sums (the forward's D, the backward's share), the forward's fp32 per-slot deltas
+// (used with bf16 rows, or where the caller omits h_old or h_sel) and its per-group row maxima.
 struct WorkspaceLayout {
     bool chain = false;
-    size_t ptr = 0, ev = 0, sum = 0, delta = 0, rms = 0, bytes = 0;
+    size_t ptr = 0, ev = 0, sum = 0, delta = 0, hmax = 0, rms = 0, bytes = 0;
 };
 
 int path_setting();

@@ -36,17 +36,12 @@ __device__ __forceinline__ float from_f32<float>(float x) {
 }
 
 // Round-to-nearest-even narrowing of an fp32 to bf16 (the IEEE rounding every framework uses
-// for this cast); a NaN stays a quiet NaN with its sign.
+// for this cast): gfx950's v_cvt_pk_bf16_f32, one instruction under the default round-to-nearest
+// mode with fp32 denormals kept; a NaN stays a NaN.
 template <>
 __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
-    const uint32_t u = __float_as_uint(x);
     bf16_t r;
-    if ((u & 0x7fffffffu) > 0x7f800000u) {
-        r.bits = static_cast<uint16_t>((u >> 16) | 0x0040u);
-    } else {
-        const uint32_t lsb = (u >> 16) & 1u;
-        r.bits = static_cast<uint16_t>((u + 0x7fffu + lsb) >> 16);
-    }
+    r.bits = __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
     return r;
 }
 

@@ -350,10 +350,10 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void fwd_chunk(FwdArgs a) {
     float omb[TB], bcv[TB];
     uint32_t ca[TB];
     // the loads of position i of the sub-block at tb0, unconditional (the compiler's wait counts
-    // stay exact). Not clamped: the row's resources bound them, so a position past the chunk
-    // reads data the preparation ignores and one past the row reads zeros.
+    // stay exact). A position past the chunk reads data the preparation ignores; one past the
+    // row is clamped to the row's last position (the soffset must stay inside the row).
     auto fetch_at = [&](int i, int tb0) __attribute__((always_inline)) {
-        const int t = tb0 + i;
+        const int t = uniform(min(tb0 + i, T - 1));
         const uint32_t sy = uint32_t(t) * kd * sizeof(IN);
         yv[i] = bload<IN>(ry, vy, sy);
         gv[i] = bload<IN>(rg, vy, sy);
@@ -1007,9 +1007,9 @@ __global__ __launch_bounds__(kWave* kMaxChunks) void bwd_chunk(BwdArgs a) {
         rbyte = bload<uint8_t>(rr, rin ? uint32_t(lane) : kOob, uint32_t(tb0));
         const uint32_t sq = uint32_t(tb0) * d * sizeof(IN);
 #pragma unroll
-        for (int j = 0; j < kQP; ++j) {  // past the row: the resource reads zeros (masked anyway)
+        for (int j = 0; j < kQP; ++j) {  // past the row: masked by the lane offset (reads 0)
             const int i = qg * kQP + j;
-            const uint32_t v = i < TB ? uint32_t(i * d + col) * sizeof(IN) : kOob;
+            const uint32_t v = i < TB && tb0 + i < a.T ? uint32_t(i * d + col) * sizeof(IN) : kOob;
             qa[j] = to_f32(bload<IN>(rqa, v, sq));
             qb[j] = to_f32(bload<IN>(rqb, v, sq));
         }

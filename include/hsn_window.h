@@ -88,8 +88,9 @@ int hsn_win_path(int op, int B, int T, int N, int d, int K, int io_dtype, int* p
 /*
  * The workspace hsn_win_forward / hsn_win_backward need, in bytes (0: none), for `op`
  * HSN_OP_FORWARD or HSN_OP_BACKWARD on the path the call takes: the RMS candidate's normalised
- * input (cand_norm 1) and, on the chain path, the row lists, the per-position sums and the
- * forward's per-slot deltas. No counterpart in the reference (its sweep keeps the state in
+ * input (cand_norm 1) and, on the chain path, the row lists, the per-position sums, the
+ * forward's fp32 per-slot deltas (used with bf16 rows, or where h_old or h_sel is omitted) and
+ * its row-maximum table per workgroup of cells. No counterpart in the reference (its sweep keeps the state in
  * shared memory and allocates through torch).
  */
 int hsn_win_workspace_bytes(int op, int B, int T, int N, int d, int K, int io_dtype,

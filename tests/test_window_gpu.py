@@ -330,6 +330,38 @@ def test_backward_without_optional_cotangents(dev, path):
             assert bool((gb[3] == 0).all())
 
 
+def test_bf16_storage_rounds_like_torch(dev, path):
+    """The bf16 narrowing of the kernels (gfx950's v_cvt_pk_bf16_f32) against torch's
+    round-to-nearest-even cast, bit for bit: every cell is written at position 0 (K = N), so
+    h_old[:, 0] is the cast of h0's rows, here ties to even in both directions, denormals, the
+    largest finite value (rounds to inf), infinities and signed zeros; a NaN stays a NaN."""
+    from hsn_amd import window
+
+    B, T, N, d, K = 2, 2, 16, 64, 16
+    g = torch.Generator().manual_seed(8)
+    one = 1.0
+    special = torch.tensor([one + 2.0 ** -8, one + 3 * 2.0 ** -8, -(one + 2.0 ** -8),
+                            -(one + 3 * 2.0 ** -8), 1e-40, -1e-40, 2.0 ** -133, 3.4028234663852886e38,
+                            -3.4028234663852886e38, float("inf"), float("-inf"), 0.0, -0.0,
+                            float("nan"), one + 2.0 ** -9, 0.1], dtype=torch.float32)
+    h0 = torch.randn(B, N, d, generator=g)
+    h0[:, :, :16] = special  # every cell's first 16 columns
+    h0[1, :, 16:32] = torch.randn(N, 16, generator=g) * 1e-39  # denormals of every kind
+    y = torch.randn(B, T, K, d, generator=g).to(torch.bfloat16)
+    gate = torch.randn(B, T, K, d, generator=g).to(torch.bfloat16)
+    cells = torch.arange(N).expand(B, T, N).contiguous()
+    slots = window.pack_slots(cells, torch.ones(B, T, K, dtype=torch.bool)).to(dev)
+    reset = torch.zeros(B, T, dtype=torch.bool, device=dev)
+    out = window.forward(y.to(dev), gate.to(dev), reset, slots, h0.to(dev),
+                         torch.zeros(B, d, device=dev), torch.zeros(B, N, dtype=torch.int64, device=dev),
+                         torch.zeros(B, dtype=torch.int64, device=dev), N)
+    got = out["h_old"][:, 0].cpu()
+    want = h0.to(torch.bfloat16)
+    nan = torch.isnan(want)
+    assert torch.equal(torch.isnan(got), nan)
+    assert torch.equal(got.view(torch.int16)[~nan], want.view(torch.int16)[~nan])
+
+
 @pytest.mark.parametrize("io", ["f32", "bf16"])
 def test_chain_takes_more_slots_than_a_wavefront(dev, io):
     """K = 80 slots per position, more than a wavefront's lanes: the slices (a slot per lane)
