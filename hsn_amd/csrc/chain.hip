@@ -80,13 +80,17 @@ int choose_path(int op, int B, int T, int N, int d, int K, size_t elem) {
     }
     if (!c_ok) return kPathSlice;
     if (!s_ok) return kPathChain;
-    // both take it: the slices where a wavefront's piece of a slot row is a full 32-byte
-    // sector, the chains where it would be narrower (K large against d)
+    // both take it: the slices where a wavefront's piece of a slot row is a full 32-byte sector
+    // and the state slice (N * S words) leaves room for chunks of the row in LDS; the chains
+    // where the piece would be narrower (K large against d) or the slice large (N large). Measured
+    // on MI355X: slices at B32 T256 N256 d64 K8 fp32 (S 8, 68 against 95 us per step), chains at
+    // B64 T512 N1024 d64 K16 bf16 (S 4: 0.45 against 1.62 ms) and B128 T128 N512 d128 K8 fp32
+    // (S 8, N S 4096: 0.31 against 0.43 ms).
     Geometry g;
     const bool fwd = op == HSN_OP_FORWARD;
     if (fwd) choose_geometry(B, T, N, d, K, fwd_lds_bytes, g);
     else choose_geometry(B, T, N, d, K, bwd_lds_bytes, g);
-    return size_t(g.S) * elem >= 32 ? kPathSlice : kPathChain;
+    return size_t(g.S) * elem >= 32 && int64_t(N) * g.S <= 2048 ? kPathSlice : kPathChain;
 }
 
 WorkspaceLayout workspace_layout(int op, int B, int T, int N, int d, int K, size_t elem,

@@ -76,7 +76,7 @@ int hsn_win_supports(int op, int B, int T, int N, int d, int K);
  *                   up to 255, d up to 256.
  * hsn_win_set_path fixes the path of every later hsn_win_forward / hsn_win_forward_noalloc /
  * hsn_win_backward call of the process (HSN_PATH_AUTO, the default: the slices where their
- * piece is a full sector, else the chains). hsn_win_path reports the path a call of `op`
+ * piece is a full sector and N * S <= 2048, else the chains). hsn_win_path reports the path a call of `op`
  * (HSN_OP_FORWARD or HSN_OP_BACKWARD) would take, or the reason neither takes the shape.
  */
 #define HSN_PATH_AUTO 0

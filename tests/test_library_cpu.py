@@ -167,9 +167,10 @@ def _align(n: int) -> int:
 @pytest.mark.parametrize("name", ["ref", "bf16", "tbptt", "skewed", "tiny"])
 def test_workspace_and_path_follow_the_shape(name):
     """The path a forward / backward call takes and the workspace it needs, host arithmetic
-    only: the slices where a wavefront's piece of a slot row is a full 32-byte sector (ref,
-    tbptt: 8 fp32 columns), the cell chains where it would be narrower (bf16: 4 bf16 columns,
-    skewed: 2); the chain workspace is the row lists (B(N+1) + BTK int32), the per-position
+    only: the slices where a wavefront's piece of a slot row is a full 32-byte sector and the
+    state slice N * S is at most 2048 words (ref: 8 fp32 columns of 256 cells), the cell chains
+    where the piece would be narrower (bf16: 4 bf16 columns, skewed: 2) or the slice larger
+    (tbptt: 8 columns of 512 cells); the chain workspace is the row lists (B(N+1) + BTK int32), the per-position
     sums (BTd fp32) and, in the forward, the per-slot deltas (BTKd fp32) and a row-maximum
     table per workgroup of cells (BTG words, 1 <= G <= N / 16), each 256-aligned, then the RMS
     candidate's input."""
@@ -182,7 +183,7 @@ def test_workspace_and_path_follow_the_shape(name):
     c = CONFIGS[name]
     io = _lib.DTYPE_BF16 if c.io == "bf16" else _lib.DTYPE_F32
     elem = 2 if c.io == "bf16" else 4
-    want = "chain" if name in ("bf16", "skewed") else "slice"
+    want = "chain" if name in ("bf16", "skewed", "tbptt") else "slice"
     B, T, N, d, K = c.B, c.T, c.N, c.d, c.K
     rms = _align(rms_scratch_bytes(B * T * K, d, elem))
     for op in (_lib.OP_FORWARD, _lib.OP_BACKWARD):
