@@ -53,6 +53,10 @@ SIGNATURES: dict[str, list] = {
                             I, I, I, I, I, P],
     "hsn_gather_concat": [P, P, P, P, P, P, I, I, I, I, I, P],
     "hsn_gather_concat_bwd": [P, P, P, P, P, P, I, I, I, I, I, I, P],
+    "hsn_grouped_unit_mlp_fwd": [P, P, P, P, P, P, P, P, I, I, I, I, I, P],
+    "hsn_grouped_unit_mlp_bwd": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, P],
+    "hsn_csr_messages": [P, P, P, P, P, P, P, I, I, I, I, I, I, P],
+    "hsn_csr_messages_bwd": [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P],
     "hsn_gated_delta_update": [P, P, P, P, P, P, P, P, I, I, I, I, I, P],
     "hsn_gated_delta_update_bwd": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P],
 }

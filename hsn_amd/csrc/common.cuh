@@ -45,6 +45,12 @@ __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
     return r;
 }
 
+__device__ __forceinline__ float to_f32(_Float16 x) { return static_cast<float>(x); }
+template <>
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float x) {
+    return static_cast<_Float16>(x);
+}
+
 template <typename T>
 __device__ __forceinline__ float load_f32(const T* p, int64_t i) {
     return to_f32(p[i]);

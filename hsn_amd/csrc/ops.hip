@@ -9,12 +9,6 @@
 
 namespace hsn {
 
-__device__ __forceinline__ float to_f32(_Float16 x) { return static_cast<float>(x); }
-template <>
-__device__ __forceinline__ _Float16 from_f32<_Float16>(float x) {
-    return static_cast<_Float16>(x);
-}
-
 namespace {
 
 // grad_h = G (the copy the slot pass then overwrites), or zero when G is NULL.

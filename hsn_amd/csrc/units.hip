@@ -1,0 +1,698 @@
+// The remaining ops of the reference's sparse-round ABI (kernels/include/hsn_ops.h:101-153): the
+// grouped unit MLP and the CSR neighbour messages, forward and backward, for f32 / f16 / bf16
+// storage with fp32 arithmetic and one rounding per output.
+//
+// The products run on the matrix cores: v_mfma_f32_16x16x4_f32 tiles (a 16x4 by 4x16 product per
+// instruction, fp32 in and out), the operands widened from the storage dtype on load, so f16 and
+// bf16 inputs multiply exactly and accumulate in fp32. Lane l of a wavefront supplies A[l % 16][l
+// / 16] and B[l / 16][l % 16] and receives D[4 (l / 16) + r][l % 16] in its r-th result
+// register. A workgroup is four wavefronts side by side over 64 output columns.
+//
+// The ABI takes no workspace, so nothing is staged between launches: the grouped MLP finds each
+// unit's pairs by scanning unit_idx (a wavefront-wide ballot per 64 pairs), and its backward
+// recomputes the hidden cotangent dz1 tile by tile where it is consumed. Every sum runs in a fixed
+// order (no atomics), so all results are reproducible run to run whatever `deterministic` says.
+// CSR entries outside [0, N) / [0, E] contribute nothing (never an out-of-bounds access); the
+// graph's well-formedness is the caller's, as for the reference's GPU path.
+#include <algorithm>
+
+#include "common.cuh"
+
+#include "../../include/hsn_ops.h"
+#include "abi_util.h"
+
+namespace hsn {
+namespace units {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+constexpr float kRsqrt2 = 0.70710678118654752f;
+constexpr float kRsqrt2Pi = 0.39894228040143268f;
+
+// The exact GELU x/2 (1 + erf(x / sqrt 2)) and its derivative Phi(x) + x phi(x)
+// (kernels/include/hsn_ops.h:104-113), from the device library's erff / expf.
+__device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erff(x * kRsqrt2)); }
+__device__ __forceinline__ float gelu_grad(float x) {
+    return 0.5f * (1.0f + erff(x * kRsqrt2)) + x * expf(-0.5f * x * x) * kRsqrt2Pi;
+}
+
+// The next (up to) 16 pairs p >= cur of unit j, in order: lane i < n holds the i-th, `cur`
+// advances past them. Every lane of the wavefront computes the same n and cur.
+struct Chunk {
+    int n;
+    int row;  // lane's pair (lane < n), else -1
+};
+__device__ __forceinline__ Chunk next_pairs(const int32_t* unit_idx, int P, int j, int& cur) {
+    const int lane = lane_id();
+    int n = 0, row = -1;
+    while (n < 16 && cur < P) {
+        const int p = cur + lane;
+        uint64_t m = ballot(p < P && unit_idx[p] == j);
+        int last = -1;
+        while (m != 0ull && n < 16) {
+            const int bit = __builtin_ctzll(m);
+            m &= m - 1ull;
+            if (lane == n) row = cur + bit;
+            ++n;
+            last = bit;
+        }
+        cur = m != 0ull ? cur + last + 1 : cur + 64;  // stopped early: resume after the last taken
+    }
+    return Chunk{n, row};
+}
+
+// The pair of A-row `i` of the chunk (or -1). A cross-lane read: call it with every lane active
+// (a lane outside the exec mask does not supply its value).
+__device__ __forceinline__ int pair_of(const Chunk& c, int i) { return __shfl(c.row, i, kWave); }
+
+// dz1 = (grad_out W2[j]^T) * gelu'(z1) for the chunk's pairs and hidden columns [h0, h0 + 64)
+// (each wavefront its 16), into LDS dz[16][64]; with `act`, gelu(z1) too. Rows past the chunk and
+// columns past H hold zeros.
+template <typename T>
+__device__ __forceinline__ void dz_tile(const T* grad_out, const T* W2j, const T* hidden,
+                                        const Chunk& c, int h0, int d, int H, float (*dz)[64],
+                                        float (*act)[64]) {
+    const int lane = lane_id(), w = threadIdx.x >> 6, lr = lane & 15, lq = lane >> 4;
+    const int h = h0 + 16 * w + lr;
+    const bool hin = h < H;
+    const int pa = pair_of(c, lr);
+    const T* go = grad_out + int64_t(pa < 0 ? 0 : pa) * d;
+    const T* w2 = W2j + int64_t(hin ? h : 0) * d;  // W2[j][h][:]: B[k][h] = W2[j][h][k]
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr int U = 4;
+    for (int k0 = 0; k0 < d; k0 += 4 * U) {
+        float a[U], b[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = k0 + 4 * u + lq;
+            const int kc = k < d ? k : d - 1;
+            a[u] = pa >= 0 && k < d ? load_f32(go, kc) : 0.0f;
+            b[u] = hin && k < d ? load_f32(w2, kc) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc = mfma(a[u], b[u], acc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = 4 * lq + r;
+        const int p = pair_of(c, row);
+        const float z = p >= 0 && hin ? load_f32(hidden, int64_t(p) * H + h) : 0.0f;
+        const bool ok = p >= 0 && hin;
+        dz[row][16 * w + lr] = ok ? acc[r] * gelu_grad(z) : 0.0f;
+        if (act) act[row][16 * w + lr] = ok ? gelu(z) : 0.0f;
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// grouped_unit_mlp forward: (M, S) workgroups, unit j's chunks s, s + S, ... of 16 pairs
+// ------------------------------------------------------------------------------------------
+
+// For a chunk: per hidden tile of 64 columns, z1 = v W1[j] + b1[j] (saved pre-GELU, rounded once
+// to the storage dtype), gelu(z1) in fp32 into LDS, and out += gelu(z1) W2[j][tile] accumulated
+// in registers over the tiles; out = that + b2[j]. Layer 2 reads the fp32 activation, not the
+// rounded copy, as the reference's two kernels do through an fp32 buffer.
+template <typename T>
+__global__ __launch_bounds__(256) void mlp_fwd(const T* v, const int32_t* unit_idx, const T* W1,
+                                               const T* b1, const T* W2, const T* b2, T* hidden,
+                                               T* out, int P, int d, int H) {
+    __shared__ float act[16][64];
+    const int j = blockIdx.x, s = blockIdx.y, S = gridDim.y;
+    const int lane = lane_id(), w = threadIdx.x >> 6, lr = lane & 15, lq = lane >> 4;
+    const int in = 4 * d;
+    const T* W1j = W1 + int64_t(j) * in * H;
+    const T* W2j = W2 + int64_t(j) * H * d;
+    int cur = 0, chunk = 0;
+    for (;;) {
+        const Chunk c = next_pairs(unit_idx, P, j, cur);
+        if (c.n == 0) break;
+        if (chunk++ % S != s) continue;
+        const int pa = pair_of(c, lr);
+        const T* vr = v + int64_t(pa < 0 ? 0 : pa) * in;
+        v4f oacc[4];  // out columns 16 (w + 4 t) + lr, t < 4 (d <= 256)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) oacc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int h0 = 0; h0 < H; h0 += 64) {
+            const int hc = h0 + 16 * w + lr;
+            const bool hin = hc < H;
+            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            constexpr int U = 8;
+            for (int k0 = 0; k0 < in; k0 += 4 * U) {
+                float a[U], b[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int k = k0 + 4 * u + lq;
+                    const int kc = k < in ? k : in - 1;
+                    a[u] = pa >= 0 && k < in ? load_f32(vr, kc) : 0.0f;
+                    b[u] = hin && k < in ? load_f32(W1j, int64_t(kc) * H + hc) : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) acc = mfma(a[u], b[u], acc);
+            }
+            const float bias = hin ? load_f32(b1, int64_t(j) * H + hc) : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 4 * lq + r;
+                const int p = pair_of(c, row);
+                const float z = acc[r] + bias;
+                const bool ok = p >= 0 && hin;
+                if (ok) store_f32(hidden, int64_t(p) * H + hc, z);
+                act[row][16 * w + lr] = ok ? gelu(z) : 0.0f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int oc = 16 * (w + 4 * t) + lr;
+                if (16 * (w + 4 * t) < d) {  // uniform in the wavefront
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) {
+                        const int k = 4 * q + lq;
+                        const float av = act[lr][k];
+                        const float bv = h0 + k < H && oc < d ? load_f32(W2j, int64_t(h0 + k) * d + oc) : 0.0f;
+                        oacc[t] = mfma(av, bv, oacc[t]);
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        int prow[4];  // the output rows' pairs (a cross-lane read: every lane takes part)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) prow[r] = pair_of(c, 4 * lq + r);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int oc = 16 * (w + 4 * t) + lr;
+            if (oc < d) {
+                const float bias = load_f32(b2, int64_t(j) * d + oc);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (prow[r] >= 0) store_f32(out, int64_t(prow[r]) * d + oc, oacc[t][r] + bias);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// grouped_unit_mlp backward
+// ------------------------------------------------------------------------------------------
+
+// (H / 64, M, 4d / 64) workgroups: unit j's hidden columns [h0, h0 + 64) and input rows
+// [i0, i0 + 64): grad_W1[j][i0.., h0..] = sum_p v[p]^T dz1[p]; the first input block also
+// grad_W2[j][h0.., :] = sum_p gelu(z1[p])^T grad_out[p] and grad_b1[j][h0..]; the first of all
+// grad_b2[j]. A unit without pairs gets zeros.
+template <typename T>
+__global__ __launch_bounds__(256) void mlp_dw(const T* v, const int32_t* unit_idx, const T* W2,
+                                              const T* hidden, const T* grad_out, T* grad_W1,
+                                              T* grad_b1, T* grad_W2, T* grad_b2, int P, int d,
+                                              int H) {
+    __shared__ float dz[16][64];
+    __shared__ float act[16][64];
+    const int j = blockIdx.y, lane = lane_id(), w = threadIdx.x >> 6, lr = lane & 15,
+              lq = lane >> 4, tid = threadIdx.x;
+    const int in = 4 * d;
+    const int h0 = blockIdx.x * 64, i0 = blockIdx.z * 64;
+    const bool first_in = blockIdx.z == 0;
+    const T* W2j = W2 + int64_t(j) * H * d;
+    constexpr int kMaxD16 = 16;  // d <= 256: 16 column tiles of grad_W2 per wavefront
+    const int nd = (d + 15) / 16;
+    v4f gw1[4], gw2[kMaxD16];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) gw1[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < kMaxD16; ++t) gw2[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    float gb1 = 0.0f;  // thread tid < 64: column h0 + tid
+    float gb2[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // first workgroup: columns tid + 256 u
+    int cur = 0;
+    for (;;) {
+        const Chunk c = next_pairs(unit_idx, P, j, cur);
+        if (c.n == 0) break;
+        dz_tile<T>(grad_out, W2j, hidden, c, h0, d, H, dz, first_in ? act : nullptr);
+        __syncthreads();
+        // grad_W1[i][h] += sum_k v[p_k][i] dz[k][h]: A = v^T (rows i, k = pairs), B = dz
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int k = 4 * s + lq;  // the pair
+            const int p = pair_of(c, k);
+            const float bv = dz[k][16 * w + lr];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int i = i0 + 16 * t + lr;
+                const float av = p >= 0 && i < in ? load_f32(v, int64_t(p) * in + i) : 0.0f;
+                gw1[t] = mfma(av, bv, gw1[t]);
+            }
+        }
+        if (first_in) {
+            // grad_W2[h][o] += sum_k gelu(z1)[k][h] grad_out[p_k][o]: A = act^T, B = grad_out
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int k = 4 * s + lq;
+                const int p = pair_of(c, k);
+                const float av = act[k][16 * w + lr];
+#pragma unroll
+                for (int t = 0; t < kMaxD16; ++t) {
+                    if (t < nd) {
+                        const int o = 16 * t + lr;
+                        const float bv = p >= 0 && o < d ? load_f32(grad_out, int64_t(p) * d + o) : 0.0f;
+                        gw2[t] = mfma(av, bv, gw2[t]);
+                    }
+                }
+            }
+            if (tid < 64)
+                for (int k = 0; k < c.n; ++k) gb1 += dz[k][tid];
+            if (blockIdx.x == 0) {
+                for (int k = 0; k < c.n; ++k) {
+                    const int p = pair_of(c, k);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int o = tid + 256 * u;
+                        if (o < d) gb2[u] += load_f32(grad_out, int64_t(p) * d + o);
+                    }
+                }
+            }
+        }
+        __syncthreads();  // before the next chunk rewrites the tiles
+    }
+    const int h = h0 + 16 * w + lr;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = i0 + 16 * t + 4 * lq + r;
+            if (i < in && h < H) store_f32(grad_W1, (int64_t(j) * in + i) * H + h, gw1[t][r]);
+        }
+    if (first_in) {
+#pragma unroll
+        for (int t = 0; t < kMaxD16; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int hr = h0 + 16 * w + 4 * lq + r, o = 16 * t + lr;
+                if (t < nd && hr < H && o < d)
+                    store_f32(grad_W2, (int64_t(j) * H + hr) * d + o, gw2[t][r]);
+            }
+        if (tid < 64 && h0 + tid < H) store_f32(grad_b1, int64_t(j) * H + h0 + tid, gb1);
+        if (blockIdx.x == 0)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int o = tid + 256 * u;
+                if (o < d) store_f32(grad_b2, int64_t(j) * d + o, gb2[u]);
+            }
+    }
+}
+
+// (4d / 64, M) workgroups: grad_v[p][i0..] = sum_h dz1[p][h] W1[j][i][h], dz1 recomputed per
+// hidden tile of 64.
+template <typename T>
+__global__ __launch_bounds__(256) void mlp_dv(const int32_t* unit_idx, const T* W1, const T* W2,
+                                              const T* hidden, const T* grad_out, T* grad_v,
+                                              int P, int d, int H) {
+    __shared__ float dz[16][64];
+    const int j = blockIdx.y, lane = lane_id(), w = threadIdx.x >> 6, lr = lane & 15,
+              lq = lane >> 4;
+    const int in = 4 * d;
+    const int i = blockIdx.x * 64 + 16 * w + lr;
+    const bool iin = i < in;
+    const T* W1r = W1 + (int64_t(j) * in + (iin ? i : 0)) * H;  // W1[j][i][:]
+    const T* W2j = W2 + int64_t(j) * H * d;
+    int cur = 0;
+    for (;;) {
+        const Chunk c = next_pairs(unit_idx, P, j, cur);
+        if (c.n == 0) break;
+        v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int h0 = 0; h0 < H; h0 += 64) {
+            dz_tile<T>(grad_out, W2j, hidden, c, h0, d, H, dz, nullptr);
+            __syncthreads();
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const int h = h0 + 4 * s + lq;
+                const float av = dz[lr][4 * s + lq];
+                const float bv = iin && h < H ? load_f32(W1r, h) : 0.0f;
+                acc = mfma(av, bv, acc);
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int p = pair_of(c, 4 * lq + r);
+            if (p >= 0 && iin) store_f32(grad_v, int64_t(p) * in + i, acc[r]);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// csr_messages
+// ------------------------------------------------------------------------------------------
+
+struct Csr {
+    const int32_t* indptr;   // [N + 1]
+    const int32_t* indices;  // [E]
+    int N, E;
+    // the edge range of row i, clamped into [0, E] (empty for a row outside [0, N))
+    __device__ __forceinline__ void range(int i, int& e0, int& e1) const {
+        if (i < 0 || i >= N) {
+            e0 = e1 = 0;
+            return;
+        }
+        e0 = min(max(indptr[i], 0), E);
+        e1 = min(max(indptr[i + 1], e0), E);
+    }
+};
+
+// S[s][c] = sum_e a[e] h[r_s, indices[e], c] for 16 slots from s0 and columns [c0, c0 + nc),
+// into LDS (row stride `ld`); every thread of the workgroup takes (slot, column) pairs and walks
+// its slot's edges in order.
+template <typename T>
+__device__ __forceinline__ void gather_sums(const T* h, const T* a, const int32_t* cell_idx,
+                                            const Csr& g, int s0, int BK, int K, int d, int c0,
+                                            int nc, float* S, int ld) {
+    for (int x = threadIdx.x; x < 16 * nc; x += blockDim.x) {
+        const int s = x / nc, cc = x - s * nc;
+        const int flat = s0 + s, col = c0 + cc;
+        float sum = 0.0f;
+        if (flat < BK && col < d) {
+            const int r = flat / K;
+            int e0, e1;
+            g.range(cell_idx[flat], e0, e1);
+            for (int e = e0; e < e1; ++e) {
+                const int src = g.indices[e];
+                if (src >= 0 && src < g.N)
+                    sum += load_f32(a, e) * load_f32(h, (int64_t(r) * g.N + src) * d + col);
+            }
+        }
+        S[s * ld + cc] = sum;
+    }
+}
+
+// (BK / 16, d / 64) workgroups: m[s][o] = sum_c V[o][c] S[s][c] for 16 slots (S in LDS).
+template <typename T>
+__global__ __launch_bounds__(256) void csr_fwd(const T* h, const Csr g, const T* a, const T* V,
+                                               const int32_t* cell_idx, T* m, int B, int K,
+                                               int d) {
+    extern __shared__ float S[];  // [16][d]
+    const int lane = lane_id(), w = threadIdx.x >> 6, lr = lane & 15, lq = lane >> 4;
+    const int BK = B * K, s0 = blockIdx.x * 16;
+    gather_sums<T>(h, a, cell_idx, g, s0, BK, K, d, 0, d, S, d);
+    __syncthreads();
+    const int o = blockIdx.y * 64 + 16 * w + lr;
+    const bool oin = o < d;
+    const T* Vr = V + int64_t(oin ? o : 0) * d;  // B[c][o] = V[o][c]
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < d; k0 += 4) {
+        const int k = k0 + lq;
+        const float av = k < d ? S[lr * d + k] : 0.0f;
+        const float bv = oin && k < d ? load_f32(Vr, k) : 0.0f;
+        acc = mfma(av, bv, acc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int flat = s0 + 4 * lq + r;
+        if (flat < BK && oin) store_f32(m, int64_t(flat) * d + o, acc[r]);
+    }
+}
+
+// (d / 64, d / 16) workgroups: grad_V[o][c] = sum_s grad_m[s][o] S[s][c] over every slot s, in
+// chunks of 16 slots (S for the workgroup's 64 columns in LDS).
+template <typename T>
+__global__ __launch_bounds__(256) void csr_dV(const T* h, const Csr g, const T* a,
+                                              const int32_t* cell_idx, const T* grad_m, T* grad_V,
+                                              int B, int K, int d) {
+    __shared__ float S[16 * 64];
+    const int lane = lane_id(), w = threadIdx.x >> 6, lr = lane & 15, lq = lane >> 4;
+    const int BK = B * K;
+    const int c0 = blockIdx.x * 64, o0 = blockIdx.y * 16;
+    const int nc = min(64, d - c0);
+    const int o = o0 + lr;  // A row
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < BK; s0 += 16) {
+        gather_sums<T>(h, a, cell_idx, g, s0, BK, K, d, c0, nc, S, 64);
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int s = 4 * q + lq;  // k: the slot
+            const int flat = s0 + s;
+            const float av = flat < BK && o < d ? load_f32(grad_m, int64_t(flat) * d + o) : 0.0f;
+            const int cc = 16 * w + lr;
+            const float bv = cc < nc ? S[s * 64 + cc] : 0.0f;
+            acc = mfma(av, bv, acc);
+        }
+        __syncthreads();
+    }
+    const int c = c0 + 16 * w + lr;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int orow = o0 + 4 * lq + r;
+        if (orow < d && c < d) store_f32(grad_V, int64_t(orow) * d + c, acc[r]);
+    }
+}
+
+// (B, d / 64) wavefronts: row r's grad_h for 64 columns, one lane per column, in blocks of
+// kDhCells source cells accumulated in LDS: every slot in order adds a[e] (V^T grad_m[r, k])[c]
+// to the source cell of each of its edges, in edge order, so every sum has a fixed order.
+constexpr int kDhCells = 128;
+template <typename T>
+__global__ __launch_bounds__(64) void csr_dh(const Csr g, const T* a, const T* V,
+                                             const int32_t* cell_idx, const T* grad_m, T* grad_h,
+                                             int K, int d) {
+    __shared__ float acc[kDhCells][64];
+    const int r = blockIdx.x, lane = lane_id(), c = blockIdx.y * 64 + lane;
+    const bool cin = c < d;
+    T* gh = grad_h + int64_t(r) * g.N * d;
+    for (int n0 = 0; n0 < g.N; n0 += kDhCells) {
+        for (int n = 0; n < kDhCells; ++n) acc[n][lane] = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            const int flat = r * K + k;
+            int e0, e1;
+            g.range(cell_idx[flat], e0, e1);
+            bool any = false;  // an edge of this slot with its source in the block
+            for (int e = e0; e < e1 && !any; ++e) {
+                const int src = g.indices[e];
+                any = src >= n0 && src < n0 + kDhCells && src < g.N;
+            }
+            if (!any) continue;
+            float u = 0.0f;  // (V^T grad_m[r, k])[c]
+            if (cin)
+                for (int o = 0; o < d; ++o)
+                    u += load_f32(V, int64_t(o) * d + c) * load_f32(grad_m, int64_t(flat) * d + o);
+            for (int e = e0; e < e1; ++e) {
+                const int src = g.indices[e];
+                if (src >= n0 && src < n0 + kDhCells && src < g.N)
+                    acc[src - n0][lane] += load_f32(a, e) * u;
+            }
+        }
+        if (cin)
+            for (int n = n0; n < min(g.N, n0 + kDhCells); ++n)
+                store_f32(gh, int64_t(n) * d + c, acc[n - n0][lane]);
+    }
+}
+
+// A wavefront per edge e (target row i, source j): grad_a[e] = sum over the slots (r, k) that
+// selected row i, in order, of grad_m[r, k] . (V h[r, j]).
+template <typename T>
+__global__ __launch_bounds__(256) void csr_da(const T* h, const Csr g, const T* V,
+                                              const int32_t* cell_idx, const T* grad_m, T* grad_a,
+                                              int B, int K, int d) {
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6), lane = lane_id();
+    if (e >= g.E) return;
+    // the target row: the last i with indptr[i] <= e (binary search; a malformed CSR may give
+    // a row whose range excludes e, which then contributes nothing)
+    int lo = 0, hi = g.N;  // indptr[lo] <= e < indptr[hi] when well formed
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (g.indptr[mid] <= e) lo = mid;
+        else hi = mid;
+    }
+    int e0, e1;
+    g.range(lo, e0, e1);
+    const int src = g.indices[e];
+    float acc = 0.0f;
+    if (e >= e0 && e < e1 && src >= 0 && src < g.N) {
+        for (int flat = 0; flat < B * K; ++flat) {
+            if (cell_idx[flat] != lo) continue;  // uniform
+            const int r = flat / K;
+            const T* hr = h + (int64_t(r) * g.N + src) * d;
+            const T* gm = grad_m + int64_t(flat) * d;
+            for (int o = lane; o < d; o += 64) {  // lane o: grad_m[o] (V h)[o]
+                float vh = 0.0f;
+                for (int cc = 0; cc < d; ++cc) vh += load_f32(V, int64_t(o) * d + cc) * load_f32(hr, cc);
+                acc += load_f32(gm, o) * vh;
+            }
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+    if (lane == 0) store_f32(grad_a, e, acc);
+}
+
+}  // namespace units
+}  // namespace hsn
+
+using namespace hsn;
+
+namespace {
+
+template <template <typename> class Fn, typename... Args>
+void by_dtype(int dtype, Args&&... args) {
+    if (dtype == HSN_DTYPE_F32) Fn<float>::run(args...);
+    else if (dtype == HSN_DTYPE_F16) Fn<_Float16>::run(args...);
+    else Fn<bf16_t>::run(args...);
+}
+
+void check_dtype(int dtype, const char* who) {
+    HSN_REQUIRE(dtype == HSN_DTYPE_F32 || dtype == HSN_DTYPE_F16 || dtype == HSN_DTYPE_BF16,
+                HSN_ERR_UNSUPPORTED_DTYPE, std::string(who) + ": unknown dtype code");
+}
+
+void check_units(int P, int M, int d, int H, const char* who) {
+    HSN_REQUIRE(P >= 1 && M >= 1 && d >= 1 && H >= 1, HSN_ERR_INVALID_ARGUMENT,
+                std::string(who) + ": dimensions must be >= 1");
+    HSN_REQUIRE(d <= 256, HSN_ERR_INVALID_ARGUMENT, std::string(who) + ": d above 256");
+    HSN_REQUIRE(int64_t(M) * 4 * d * H <= INT32_MAX && int64_t(P) * H <= INT32_MAX &&
+                    int64_t(P) * 4 * d <= INT32_MAX,
+                HSN_ERR_SIZE_OVERFLOW, std::string(who) + ": an element count exceeds INT32_MAX");
+}
+
+void check_csr(int B, int N, int d, int K, int E, const char* who) {
+    HSN_REQUIRE(B >= 1 && N >= 1 && d >= 1 && K >= 1 && E >= 0, HSN_ERR_INVALID_ARGUMENT,
+                std::string(who) + ": dimensions must be >= 1 (E >= 0)");
+    HSN_REQUIRE(d <= 1024, HSN_ERR_INVALID_ARGUMENT, std::string(who) + ": d above 1024");
+    HSN_REQUIRE(int64_t(B) * N * d <= INT32_MAX && int64_t(B) * K * d <= INT32_MAX &&
+                    int64_t(d) * d <= INT32_MAX && N < INT32_MAX,
+                HSN_ERR_SIZE_OVERFLOW, std::string(who) + ": an element count exceeds INT32_MAX");
+}
+
+inline dim3 tiles(int n, int per) { return dim3((n + per - 1) / per); }
+
+template <typename T>
+struct RunMlp {
+    static void run(const void* v, const int32_t* idx, const void* W1, const void* b1,
+                    const void* W2, const void* b2, void* hidden, void* out, int P, int M, int d,
+                    int H, hipStream_t st) {
+        const int S = std::min((P + 15) / 16, 64);  // chunk slots per unit
+        hipLaunchKernelGGL((units::mlp_fwd<T>), dim3(M, S), dim3(256), 0, st,
+                           static_cast<const T*>(v), idx, static_cast<const T*>(W1),
+                           static_cast<const T*>(b1), static_cast<const T*>(W2),
+                           static_cast<const T*>(b2), static_cast<T*>(hidden),
+                           static_cast<T*>(out), P, d, H);
+    }
+};
+
+template <typename T>
+struct RunMlpBwd {
+    static void run(const void* v, const int32_t* idx, const void* W1, const void* W2,
+                    const void* hidden, const void* dout, void* dv, void* dW1, void* db1,
+                    void* dW2, void* db2, int P, int M, int d, int H, hipStream_t st) {
+        hipLaunchKernelGGL((units::mlp_dw<T>), dim3((H + 63) / 64, M, (4 * d + 63) / 64),
+                           dim3(256), 0, st, static_cast<const T*>(v), idx,
+                           static_cast<const T*>(W2), static_cast<const T*>(hidden),
+                           static_cast<const T*>(dout), static_cast<T*>(dW1),
+                           static_cast<T*>(db1), static_cast<T*>(dW2), static_cast<T*>(db2), P, d,
+                           H);
+        hipLaunchKernelGGL((units::mlp_dv<T>), dim3((4 * d + 63) / 64, M), dim3(256), 0, st, idx,
+                           static_cast<const T*>(W1), static_cast<const T*>(W2),
+                           static_cast<const T*>(hidden), static_cast<const T*>(dout),
+                           static_cast<T*>(dv), P, d, H);
+    }
+};
+
+template <typename T>
+struct RunCsr {
+    static void run(const void* h, const int32_t* indptr, const int32_t* indices, const void* a,
+                    const void* V, const int32_t* idx, void* m, int B, int N, int d, int K, int E,
+                    hipStream_t st) {
+        const units::Csr g{indptr, indices, N, E};
+        hipLaunchKernelGGL((units::csr_fwd<T>), dim3((B * K + 15) / 16, (d + 63) / 64),
+                           dim3(256), size_t(16) * d * 4, st, static_cast<const T*>(h), g,
+                           static_cast<const T*>(a), static_cast<const T*>(V), idx,
+                           static_cast<T*>(m), B, K, d);
+    }
+};
+
+template <typename T>
+struct RunCsrBwd {
+    static void run(const void* h, const int32_t* indptr, const int32_t* indices, const void* a,
+                    const void* V, const int32_t* idx, const void* dm, void* dh, void* da,
+                    void* dV, int B, int N, int d, int K, int E, hipStream_t st) {
+        const units::Csr g{indptr, indices, N, E};
+        hipLaunchKernelGGL((units::csr_dh<T>), dim3(B, (d + 63) / 64), dim3(64), 0, st, g,
+                           static_cast<const T*>(a), static_cast<const T*>(V), idx,
+                           static_cast<const T*>(dm), static_cast<T*>(dh), K, d);
+        if (E > 0)
+            hipLaunchKernelGGL((units::csr_da<T>), dim3((E + 3) / 4), dim3(256), 0, st,
+                               static_cast<const T*>(h), g, static_cast<const T*>(V), idx,
+                               static_cast<const T*>(dm), static_cast<T*>(da), B, K, d);
+        hipLaunchKernelGGL((units::csr_dV<T>), dim3((d + 63) / 64, (d + 15) / 16), dim3(256), 0,
+                           st, static_cast<const T*>(h), g, static_cast<const T*>(a), idx,
+                           static_cast<const T*>(dm), static_cast<T*>(dV), B, K, d);
+    }
+};
+
+}  // namespace
+
+extern "C" int hsn_grouped_unit_mlp_fwd(const void* v, const int32_t* unit_idx, const void* W1,
+                                        const void* b1, const void* W2, const void* b2,
+                                        void* hidden_saved, void* out, int P, int M, int d, int H,
+                                        int dtype, void* stream) {
+    HSN_ABI_BEGIN
+    check_units(P, M, d, H, "hsn_grouped_unit_mlp_fwd");
+    check_dtype(dtype, "hsn_grouped_unit_mlp_fwd");
+    HSN_REQUIRE(v && unit_idx && W1 && b1 && W2 && b2 && hidden_saved && out,
+                HSN_ERR_INVALID_ARGUMENT, "hsn_grouped_unit_mlp_fwd: a pointer is NULL");
+    by_dtype<RunMlp>(dtype, v, unit_idx, W1, b1, W2, b2, hidden_saved, out, P, M, d, H,
+                     as_stream(stream));
+    HSN_HIP(hipGetLastError());
+    HSN_ABI_END
+}
+
+extern "C" int hsn_grouped_unit_mlp_bwd(const void* v, const int32_t* unit_idx, const void* W1,
+                                        const void* W2, const void* hidden_saved,
+                                        const void* grad_out, void* grad_v, void* grad_W1,
+                                        void* grad_b1, void* grad_W2, void* grad_b2, int P, int M,
+                                        int d, int H, int dtype, int deterministic,
+                                        void* stream) {
+    HSN_ABI_BEGIN
+    check_units(P, M, d, H, "hsn_grouped_unit_mlp_bwd");
+    check_dtype(dtype, "hsn_grouped_unit_mlp_bwd");
+    HSN_REQUIRE(deterministic == 0 || deterministic == 1, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_grouped_unit_mlp_bwd: deterministic must be 0 or 1");
+    HSN_REQUIRE(v && unit_idx && W1 && W2 && hidden_saved && grad_out && grad_v && grad_W1 &&
+                    grad_b1 && grad_W2 && grad_b2,
+                HSN_ERR_INVALID_ARGUMENT, "hsn_grouped_unit_mlp_bwd: a pointer is NULL");
+    HSN_REQUIRE(M <= 65535, HSN_ERR_INVALID_ARGUMENT, "hsn_grouped_unit_mlp_bwd: M above 65535");
+    by_dtype<RunMlpBwd>(dtype, v, unit_idx, W1, W2, hidden_saved, grad_out, grad_v, grad_W1,
+                        grad_b1, grad_W2, grad_b2, P, M, d, H, as_stream(stream));
+    HSN_HIP(hipGetLastError());
+    HSN_ABI_END
+}
+
+extern "C" int hsn_csr_messages(const void* h, const int32_t* indptr, const int32_t* indices,
+                                const void* a, const void* V, const int32_t* cell_idx, void* m,
+                                int B, int N, int d, int K, int E, int dtype, void* stream) {
+    HSN_ABI_BEGIN
+    check_csr(B, N, d, K, E, "hsn_csr_messages");
+    check_dtype(dtype, "hsn_csr_messages");
+    HSN_REQUIRE(h && indptr && V && cell_idx && m && (E == 0 || (indices && a)),
+                HSN_ERR_INVALID_ARGUMENT, "hsn_csr_messages: a pointer is NULL");
+    by_dtype<RunCsr>(dtype, h, indptr, indices, a, V, cell_idx, m, B, N, d, K, E,
+                     as_stream(stream));
+    HSN_HIP(hipGetLastError());
+    HSN_ABI_END
+}
+
+extern "C" int hsn_csr_messages_bwd(const void* h, const int32_t* indptr, const int32_t* indices,
+                                    const void* a, const void* V, const int32_t* cell_idx,
+                                    const void* grad_m, void* grad_h, void* grad_a, void* grad_V,
+                                    int B, int N, int d, int K, int E, int dtype,
+                                    int deterministic, void* stream) {
+    HSN_ABI_BEGIN
+    check_csr(B, N, d, K, E, "hsn_csr_messages_bwd");
+    check_dtype(dtype, "hsn_csr_messages_bwd");
+    HSN_REQUIRE(deterministic == 0 || deterministic == 1, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_csr_messages_bwd: deterministic must be 0 or 1");
+    HSN_REQUIRE(h && indptr && V && cell_idx && grad_m && grad_h && grad_V &&
+                    (E == 0 || (indices && a && grad_a)),
+                HSN_ERR_INVALID_ARGUMENT, "hsn_csr_messages_bwd: a pointer is NULL");
+    by_dtype<RunCsrBwd>(dtype, h, indptr, indices, a, V, cell_idx, grad_m, grad_h, grad_a, grad_V,
+                        B, N, d, K, E, as_stream(stream));
+    HSN_HIP(hipGetLastError());
+    HSN_ABI_END
+}

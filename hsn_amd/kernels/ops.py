@@ -1,12 +1,14 @@
-"""The four-op numerical ABI of the sparse round on the HIP library: the gather of the selected
-cells' state into the cell input and the gated delta update, with their backwards.
+"""The numerical ABI of the sparse round on the HIP library: the gather of the selected cells'
+state into the cell input, the grouped unit MLP, the CSR neighbour messages and the gated delta
+update, with their backwards.
 
-Mirrors the reference's custom ops (python/hsn/kernels/ops.py:91-130 for the gather,
-:224-300 for the update): the same op names (``hsn::gather_concat``,
-``hsn::gather_concat_backward``, ``hsn::gated_delta_update`` in place on ``h, q, age``,
-``hsn::gated_delta_update_functional``, ``hsn::gated_delta_update_state``,
-``hsn::gated_delta_update_backward``), schemas, mutation sets, fakes and autograd
-registrations. Each op is one call of ``include/hsn_ops.h`` on torch's current stream; inputs are
+Mirrors the reference's custom ops (python/hsn/kernels/ops.py:91-130 for the gather, :133-180
+for the unit MLP, :183-221 for the messages, :224-300 for the update): the same op names
+(``hsn::gather_concat``, ``hsn::gather_concat_backward``, ``hsn::grouped_unit_mlp``,
+``hsn::grouped_unit_mlp_backward``, ``hsn::csr_messages``, ``hsn::csr_messages_backward``,
+``hsn::gated_delta_update`` in place on ``h, q, age``, ``hsn::gated_delta_update_functional``,
+``hsn::gated_delta_update_state``, ``hsn::gated_delta_update_backward``), schemas, mutation
+sets, fakes and autograd registrations. Each op is one call of ``include/hsn_ops.h`` on torch's current stream; inputs are
 made contiguous and indices int32 as that ABI takes them. There is no other implementation:
 without the library every op raises.
 """
@@ -24,6 +26,10 @@ __all__ = [
     "available",
     "gather_concat",
     "gather_concat_backward",
+    "grouped_unit_mlp",
+    "grouped_unit_mlp_backward",
+    "csr_messages",
+    "csr_messages_backward",
     "gated_delta_update",
     "gated_delta_update_functional",
     "gated_delta_update_state",
@@ -202,3 +208,119 @@ def _update_grad(ctx: Any, G: Tensor, g: Tensor, dage: Tensor, dold: Tensor) -> 
 
 gated_delta_update_functional.register_autograd(_update_grad, setup_context=_update_setup)
 gated_delta_update_state.register_autograd(_update_grad, setup_context=_update_setup)
+
+
+# --------------------------------------------------------------------------------------------
+# the grouped unit MLP (reference python/hsn/kernels/ops.py:133-180)
+# --------------------------------------------------------------------------------------------
+
+
+@torch.library.custom_op("hsn::grouped_unit_mlp", mutates_args=(), device_types="cuda")
+def grouped_unit_mlp(v: Tensor, idx: Tensor, w1: Tensor, b1: Tensor, w2: Tensor,
+                     b2: Tensor) -> tuple[Tensor, Tensor]:
+    """``(out [P,d], hidden [P,H])``: unit ``idx[p]`` on pair ``p``, ``hidden`` the saved
+    pre-GELU ``z1`` (reference hsn_ops.h:101-112)."""
+    P, M, d, H = v.shape[0], w1.shape[0], w2.shape[2], w1.shape[2]
+    v, idx, w1, b1, w2, b2 = (v.contiguous(), _i32(idx), w1.contiguous(), b1.contiguous(),
+                              w2.contiguous(), b2.contiguous())
+    out, hidden = v.new_empty((P, d)), v.new_empty((P, H))
+    call("hsn_grouped_unit_mlp_fwd", ptr(v), ptr(idx), ptr(w1), ptr(b1), ptr(w2), ptr(b2),
+         ptr(hidden), ptr(out), P, M, d, H, _code(v), stream_of(v.device))
+    return out, hidden
+
+
+@grouped_unit_mlp.register_fake
+def _mlp_fake(v, idx, w1, b1, w2, b2):
+    return v.new_empty((v.shape[0], w2.shape[2])), v.new_empty((v.shape[0], w1.shape[2]))
+
+
+@torch.library.custom_op("hsn::grouped_unit_mlp_backward", mutates_args=(), device_types="cuda")
+def grouped_unit_mlp_backward(v: Tensor, idx: Tensor, w1: Tensor, w2: Tensor, hidden: Tensor,
+                              dout: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """``(dv, dw1, db1, dw2, db2)`` from the saved ``z1`` (reference hsn_ops.h:114-130)."""
+    P, M, d, H = v.shape[0], w1.shape[0], w2.shape[2], w1.shape[2]
+    v, idx, w1, w2, hidden, dout = (v.contiguous(), _i32(idx), w1.contiguous(), w2.contiguous(),
+                                    hidden.contiguous(), dout.contiguous())
+    dv, dw1, dw2 = torch.empty_like(v), torch.empty_like(w1), torch.empty_like(w2)
+    db1, db2 = w1.new_empty((M, H)), w2.new_empty((M, d))
+    call("hsn_grouped_unit_mlp_bwd", ptr(v), ptr(idx), ptr(w1), ptr(w2), ptr(hidden), ptr(dout),
+         ptr(dv), ptr(dw1), ptr(db1), ptr(dw2), ptr(db2), P, M, d, H, _code(v), 1,
+         stream_of(v.device))
+    return dv, dw1, db1, dw2, db2
+
+
+@grouped_unit_mlp_backward.register_fake
+def _mlp_bwd_fake(v, idx, w1, w2, hidden, dout):
+    return (torch.empty_like(v), torch.empty_like(w1), w1.new_empty((w1.shape[0], w1.shape[2])),
+            torch.empty_like(w2), w2.new_empty((w2.shape[0], w2.shape[2])))
+
+
+def _mlp_setup(ctx: Any, inputs: tuple[Any, ...], output: tuple[Tensor, Tensor]) -> None:
+    v, idx, w1, _, w2, _ = inputs
+    ctx.save_for_backward(v, idx, w1, w2, output[1])
+    ctx.mark_non_differentiable(output[1])
+
+
+def _mlp_grad(ctx: Any, dout: Tensor, dhidden: Tensor) -> tuple[Any, ...]:
+    dv, dw1, db1, dw2, db2 = grouped_unit_mlp_backward(*ctx.saved_tensors, dout.contiguous())
+    return dv, None, dw1, db1, dw2, db2
+
+
+grouped_unit_mlp.register_autograd(_mlp_grad, setup_context=_mlp_setup)
+
+
+# --------------------------------------------------------------------------------------------
+# the CSR neighbour messages (reference python/hsn/kernels/ops.py:183-221)
+# --------------------------------------------------------------------------------------------
+
+
+@torch.library.custom_op("hsn::csr_messages", mutates_args=(), device_types="cuda")
+def csr_messages(h: Tensor, indptr: Tensor, indices: Tensor, a: Tensor, V: Tensor,
+                 idx: Tensor) -> Tensor:
+    """``m [B,K,d]``: ``m[r,k] = sum_e a[e] (V h[r, indices[e]])`` over the edges of row
+    ``idx[r,k]`` (reference hsn_ops.h:132-143)."""
+    B, N, d = h.shape
+    K, E = idx.shape[1], a.numel()
+    h, indptr, indices, a, V, idx = (h.contiguous(), _i32(indptr), _i32(indices), a.contiguous(),
+                                     V.contiguous(), _i32(idx))
+    m = h.new_empty((B, K, d))
+    call("hsn_csr_messages", ptr(h), ptr(indptr), ptr(indices), ptr(a), ptr(V), ptr(idx), ptr(m),
+         B, N, d, K, E, _code(h), stream_of(h.device))
+    return m
+
+
+@csr_messages.register_fake
+def _messages_fake(h, indptr, indices, a, V, idx):
+    return h.new_empty((*idx.shape, h.shape[2]))
+
+
+@torch.library.custom_op("hsn::csr_messages_backward", mutates_args=(), device_types="cuda")
+def csr_messages_backward(h: Tensor, indptr: Tensor, indices: Tensor, a: Tensor, V: Tensor,
+                          idx: Tensor, dm: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """``(dh, da, dV)`` of the messages (reference hsn_ops.h:145-153)."""
+    B, N, d = h.shape
+    K, E = idx.shape[1], a.numel()
+    h, indptr, indices, a, V, idx, dm = (h.contiguous(), _i32(indptr), _i32(indices),
+                                         a.contiguous(), V.contiguous(), _i32(idx),
+                                         dm.contiguous())
+    dh, da, dV = torch.empty_like(h), torch.empty_like(a), torch.empty_like(V)
+    call("hsn_csr_messages_bwd", ptr(h), ptr(indptr), ptr(indices), ptr(a), ptr(V), ptr(idx),
+         ptr(dm), ptr(dh), ptr(da), ptr(dV), B, N, d, K, E, _code(h), 1, stream_of(h.device))
+    return dh, da, dV
+
+
+@csr_messages_backward.register_fake
+def _messages_bwd_fake(h, indptr, indices, a, V, idx, dm):
+    return torch.empty_like(h), torch.empty_like(a), torch.empty_like(V)
+
+
+def _messages_setup(ctx: Any, inputs: tuple[Any, ...], output: Tensor) -> None:
+    ctx.save_for_backward(*inputs)
+
+
+def _messages_grad(ctx: Any, dm: Tensor) -> tuple[Any, ...]:
+    dh, da, dV = csr_messages_backward(*ctx.saved_tensors, dm.contiguous())
+    return dh, None, None, da, dV, None
+
+
+csr_messages.register_autograd(_messages_grad, setup_context=_messages_setup)

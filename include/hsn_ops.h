@@ -1,10 +1,11 @@
 /*
- * hsn_ops.h -- the four-op numerical C ABI of HSN's sparse round, the two ops on the window
- * hot path (the gated delta update and the gather of the selected cells), for MI355X.
+ * hsn_ops.h -- the numerical C ABI of HSN's sparse round for MI355X: the two ops on the window
+ * hot path (the gated delta update and the gather of the selected cells) and the cell round's
+ * grouped unit MLP and CSR neighbour messages.
  *
  * Same function names, argument order, dtype codes and status codes as the reference's ABI
- * (kernels/include/hsn_ops.h:64-77,85-99,155-187), so a host that binds that header binds this
- * library unchanged. Conventions as there: dense row-major tensors, int32_t indices, one float
+ * (kernels/include/hsn_ops.h:64-187), so a host that binds that header binds this library
+ * unchanged. Conventions as there: dense row-major tensors, int32_t indices, one float
  * dtype per call (f32, f16 or bf16), fp32 accumulation with one rounding per output, outputs written in full, `stream` a hipStream_t, functions return
  * once the work is enqueued. Tolerances against the reference's golden vectors: f32 1e-5,
  * f16 and bf16 1e-2 (atol = rtol).
@@ -50,6 +51,57 @@ int hsn_gather_concat(const void* u, const void* eps, const void* h, const void*
 int hsn_gather_concat_bwd(const void* grad_v, const int32_t* cell_idx, void* grad_u,
                           void* grad_eps, void* grad_h, void* grad_m, int B, int N, int d, int K,
                           int dtype, int deterministic, void* stream);
+
+/*
+ * The grouped unit MLP (reference hsn_ops.h:101-112): unit j = unit_idx[p] in [0,M) on pair p,
+ *   z1[p,:] = v[p,:] W1[j] + b1[j,:] (saved as hidden_saved [P,H], pre-GELU),
+ *   out[p,:] = gelu(z1[p,:]) W2[j] + b2[j,:], gelu(x) = x/2 (1 + erf(x / sqrt 2)).
+ * v [P,4d]; unit_idx [P]; W1 [M,4d,H] ([in, out]); b1 [M,H]; W2 [M,H,d]; b2 [M,d]; out [P,d];
+ * d <= 256. The products run on the matrix cores (fp32 16x16x4 tiles, operands widened from
+ * the storage dtype).
+ */
+int hsn_grouped_unit_mlp_fwd(const void* v, const int32_t* unit_idx, const void* W1,
+                             const void* b1, const void* W2, const void* b2, void* hidden_saved,
+                             void* out, int P, int M, int d, int H, int dtype, void* stream);
+
+/*
+ * Its backward (reference hsn_ops.h:114-130), from grad_out [P,d] and the saved z1:
+ *   dz1 = (grad_out W2[j]^T) * gelu'(z1); grad_v = dz1 W1[j]^T;
+ *   grad_W1[j] = sum_p v^T dz1, grad_b1[j] = sum_p dz1; grad_W2[j] = sum_p gelu(z1)^T grad_out,
+ *   grad_b2[j] = sum_p grad_out; units without a pair get zeros.
+ * dz1 is recomputed where it is consumed (the ABI has no workspace); every sum has a fixed
+ * order, so `deterministic` holds either way.
+ */
+int hsn_grouped_unit_mlp_bwd(const void* v, const int32_t* unit_idx, const void* W1,
+                             const void* W2, const void* hidden_saved, const void* grad_out,
+                             void* grad_v, void* grad_W1, void* grad_b1, void* grad_W2,
+                             void* grad_b2, int P, int M, int d, int H, int dtype,
+                             int deterministic, void* stream);
+
+/*
+ * The CSR neighbour messages (reference hsn_ops.h:132-143): i = cell_idx[r,k],
+ *   m[r,k,:] = sum_{e in [indptr[i], indptr[i+1])} a[e] (V h[r, indices[e], :]),
+ * V [d,d] as [d_out, d_in]. h [B,N,d]; indptr [N+1]; indices, a [E]; cell_idx [B,K] (repeats
+ * allowed); m [B,K,d]; d <= 1024. Computed as V (sum_e a[e] h[r, indices[e]]) on the matrix
+ * cores. Entries outside [0,N) / [0,E] contribute nothing (no out-of-bounds access); the CSR's
+ * well-formedness is the caller's, as on the reference's GPU path (HSN_ERR_BAD_GRAPH is not
+ * detected on the device).
+ */
+int hsn_csr_messages(const void* h, const int32_t* indptr, const int32_t* indices, const void* a,
+                     const void* V, const int32_t* cell_idx, void* m, int B, int N, int d, int K,
+                     int E, int dtype, void* stream);
+
+/*
+ * Its backward (reference hsn_ops.h:145-153), from grad_m [B,K,d]: over every slot (r,k) and
+ * edge e of its row, source j = indices[e]:
+ *   grad_h[r,j,:] = sum a[e] (V^T grad_m[r,k,:]); grad_V = sum a[e] grad_m[r,k,:] (outer)
+ *   h[r,j,:]; grad_a[e] = sum grad_m[r,k,:] . (V h[r,j,:]).
+ * Every sum has a fixed order (no atomics), so `deterministic` holds either way.
+ */
+int hsn_csr_messages_bwd(const void* h, const int32_t* indptr, const int32_t* indices,
+                         const void* a, const void* V, const int32_t* cell_idx,
+                         const void* grad_m, void* grad_h, void* grad_a, void* grad_V, int B,
+                         int N, int d, int K, int E, int dtype, int deterministic, void* stream);
 
 /*
  * The gated delta update, in place on h, q, age (reference hsn_ops.h:155-171): for every valid

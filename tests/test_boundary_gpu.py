@@ -69,10 +69,26 @@ def _cases(dev):
     reset = torch.zeros(B, n, dtype=torch.bool, device=dev)
     reset[2, 2] = True
     c, b = f(B, K, d).tanh(), torch.sigmoid(f(B, K, d))
+    deg = torch.tensor([2, 0, 1, 3, 1, 0, 2, 1, 1, 0, 2, 1])
+    indptr = torch.cat([torch.zeros(1, dtype=torch.int64), deg.cumsum(0)]).to(torch.int32)
+    csr = (indptr.to(dev), torch.randint(0, N, (int(indptr[-1]),), generator=g,
+                                         dtype=torch.int32).to(dev),
+           torch.rand(int(indptr[-1]), generator=g).to(dev))
     return {
         "gather_concat": (ops.gather_concat, (f(B, d), f(B, d), f(B, N, d), f(B, K, d), idx),
                           (0, 1, 2, 3)),
         "gather_concat_backward": (ops.gather_concat_backward, (f(B, K, 4 * d), idx, N), ()),
+        "grouped_unit_mlp": (ops.grouped_unit_mlp,
+                             (f(5, 4 * d), torch.tensor([0, 1, 1, 0, 1], device=dev),
+                              f(3, 4 * d, 6), f(3, 6), f(3, 6, d), f(3, d)), (0, 2, 3, 4, 5)),
+        "grouped_unit_mlp_backward": (ops.grouped_unit_mlp_backward,
+                                      (f(5, 4 * d), torch.tensor([0, 1, 1, 0, 1], device=dev),
+                                       f(3, 4 * d, 6), f(3, 6, d), f(5, 6), f(5, d)), ()),
+        "csr_messages": (ops.csr_messages,
+                         (f(B, N, d), csr[0], csr[1], csr[2], f(d, d), idx), (0, 3, 4)),
+        "csr_messages_backward": (ops.csr_messages_backward,
+                                  (f(B, N, d), csr[0], csr[1], csr[2], f(d, d), idx, f(B, K, d)),
+                                  ()),
         "gated_delta_update": (ops.gated_delta_update,
                                (h.clone(), q.clone(), age.to(torch.int32), idx, valid, c, b), ()),
         "gated_delta_update_functional": (ops.gated_delta_update_functional,
@@ -98,7 +114,9 @@ def _cases(dev):
     }
 
 
-OP_NAMES = ["gather_concat", "gather_concat_backward", "gated_delta_update",
+OP_NAMES = ["gather_concat", "gather_concat_backward", "grouped_unit_mlp",
+            "grouped_unit_mlp_backward", "csr_messages", "csr_messages_backward",
+            "gated_delta_update",
             "gated_delta_update_functional", "gated_delta_update_state",
             "gated_delta_update_backward", "window_select", "window_select_tape",
             "window_select_fold", "window_cell_update", "window_update_tape"]

@@ -27,7 +27,9 @@ def test_headers_declare_the_hot_path_entry_points():
     for expected in ("hsn_win_route", "hsn_win_select", "hsn_win_forward", "hsn_win_backward",
                      "hsn_win_recurrence", "hsn_win_recurrence_dense", "hsn_win_cell_update",
                      "hsn_gated_delta_update", "hsn_gated_delta_update_bwd", "hsn_gather_concat",
-                     "hsn_gather_concat_bwd", "hsn_win_abi_version", "hsn_win_last_error"):
+                     "hsn_gather_concat_bwd", "hsn_grouped_unit_mlp_fwd",
+                     "hsn_grouped_unit_mlp_bwd", "hsn_csr_messages", "hsn_csr_messages_bwd",
+                     "hsn_win_abi_version", "hsn_win_last_error"):
         assert expected in names
 
 

@@ -1,6 +1,6 @@
-"""The four-op ABI (gather of the selected cells, gated delta update, their backwards) on the GPU
-against the reference's golden vectors, through the custom ops of ``hsn_amd.kernels.ops``.
-GPU only.
+"""The sparse round's op ABI (gather of the selected cells, grouped unit MLP, CSR messages, gated
+delta update, their backwards) on the GPU against the reference's golden vectors and the CPU
+oracle, through the custom ops of ``hsn_amd.kernels.ops``. GPU only.
 
 The vectors' inputs lie on an f16/bf16-exact grid and their outputs come from the reference's
 f64 oracle rounded once to f32, so one vector serves every dtype: f32 within 1e-5, f16 and bf16
@@ -107,3 +107,121 @@ def test_inplace_update_rejects_a_strided_state(ops, cuda_device):
     with pytest.raises(ValueError, match="contiguous"):
         ops.gated_delta_update(h, D["q"].clone(), D["age"].clone(), D["cell_idx"], D["valid"],
                                D["c"], D["b"])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("size", SIZES)
+def test_grouped_unit_mlp_matches_golden(ops, cuda_device, size, dtype):
+    """Forward and backward against the vectors (the odd one has a unit without pairs: zero
+    gradients); in f16 / bf16 the saved z1 is the storage dtype's, as the ABI stores it."""
+    v = load_golden(f"{size}_grouped_unit_mlp.safetensors")
+    D = _put(v, cuda_device, dtype)
+    out, hidden = ops.grouped_unit_mlp(D["v"], D["unit_idx"], D["W1"], D["b1"], D["W2"], D["b2"])
+    _close(hidden, v["hidden_saved"], dtype, "hidden_saved")
+    _close(out, v["out"], dtype, "out")
+    got = ops.grouped_unit_mlp_backward(D["v"], D["unit_idx"], D["W1"], D["W2"],
+                                        D["hidden_saved"], D["grad_out"])
+    for name, g_ in zip(("grad_v", "grad_W1", "grad_b1", "grad_W2", "grad_b2"), got):
+        _close(g_, v[name], dtype, name)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("size", SIZES)
+def test_csr_messages_match_golden(ops, cuda_device, size, dtype):
+    """Forward and backward against the vectors: repeated slots (tiny: cell 1 twice in row 1) and
+    edges of rows no slot selects (their grad_a is exactly zero)."""
+    v = load_golden(f"{size}_csr_messages.safetensors")
+    D = _put(v, cuda_device, dtype)
+    m = ops.csr_messages(D["h"], D["indptr"], D["indices"], D["a"], D["V"], D["cell_idx"])
+    _close(m, v["m"], dtype, "m")
+    gh, ga, gV = ops.csr_messages_backward(D["h"], D["indptr"], D["indices"], D["a"], D["V"],
+                                           D["cell_idx"], D["grad_m"])
+    for name, g_ in zip(("grad_h", "grad_a", "grad_V"), (gh, ga, gV)):
+        _close(g_, v[name], dtype, name)
+    assert bool((ga.cpu()[v["grad_a"] == 0] == 0).all())
+
+
+def test_unit_mlp_and_messages_autograd_match_golden(ops, cuda_device):
+    """The custom ops' autograd registrations give the vectors' gradients."""
+    v = load_golden("odd_grouped_unit_mlp.safetensors")
+    D = _put(v, cuda_device, torch.float32)
+    leaves = [D[k].clone().requires_grad_(True) for k in ("v", "W1", "b1", "W2", "b2")]
+    out, _ = ops.grouped_unit_mlp(leaves[0], D["unit_idx"], *leaves[1:])
+    grads = torch.autograd.grad(out, leaves, D["grad_out"])
+    for name, g_ in zip(("grad_v", "grad_W1", "grad_b1", "grad_W2", "grad_b2"), grads):
+        _close(g_, v[name], torch.float32, name)
+    v = load_golden("odd_csr_messages.safetensors")
+    D = _put(v, cuda_device, torch.float32)
+    h, a, V = (D[k].clone().requires_grad_(True) for k in ("h", "a", "V"))
+    m = ops.csr_messages(h, D["indptr"], D["indices"], a, V, D["cell_idx"])
+    for name, g_ in zip(("grad_h", "grad_a", "grad_V"),
+                        torch.autograd.grad(m, (h, a, V), D["grad_m"])):
+        _close(g_, v[name], torch.float32, name)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_unit_mlp_and_messages_match_oracle_on_ragged_shapes(ops, cuda_device, dtype):
+    """Shapes the vectors leave open: units with more than 16 pairs (several row chunks), one
+    unit without pairs, H and 4d off the 64-column tiles, d past one tile; a CSR with empty rows,
+    self loops, repeated slots and d = 100 (two column tiles). Inputs rounded to the storage
+    dtype first, the oracle run on them in float64."""
+    from oracle import hsn_oracle as O
+
+    g = torch.Generator().manual_seed(41)
+    tol = TOL[dtype]
+    P, M, d, H = 70, 5, 24, 200
+    rnd = lambda *s: (torch.randn(*s, generator=g) * 0.5).to(dtype)  # noqa: E731
+    v, W1, b1, W2, b2 = rnd(P, 4 * d), rnd(M, 4 * d, H), rnd(M, H), rnd(M, H, d), rnd(M, d)
+    idx = torch.randint(0, M - 1, (P,), generator=g, dtype=torch.int32)  # unit M-1 unused
+    dout = rnd(P, d)
+    f64 = lambda t: t.double()  # noqa: E731
+    want_out, want_h = O.grouped_unit_mlp(f64(v), idx, f64(W1), f64(b1), f64(W2), f64(b2))
+    dev = cuda_device
+    out, hidden = ops.grouped_unit_mlp(v.to(dev), idx.to(dev), W1.to(dev), b1.to(dev),
+                                       W2.to(dev), b2.to(dev))
+    _close(hidden, want_h, dtype, "hidden")
+    _close(out, want_out, dtype, "out")
+    want = O.grouped_unit_mlp_bwd(f64(v), idx, f64(W1), f64(W2), f64(hidden.cpu()), f64(dout))
+    got = ops.grouped_unit_mlp_backward(v.to(dev), idx.to(dev), W1.to(dev), W2.to(dev), hidden,
+                                        dout.to(dev))
+    for name, g_, w_ in zip(("dv", "dW1", "db1", "dW2", "db2"), got, want):
+        _close(g_, w_, dtype, name)
+    assert bool((got[1][M - 1] == 0).all()) and bool((got[3][M - 1] == 0).all())
+    B, N, K, d = 3, 50, 7, 100
+    deg = torch.randint(0, 4, (N,), generator=g)
+    deg[[3, 17]] = 0  # empty rows
+    indptr = torch.cat([torch.zeros(1, dtype=torch.int64), deg.cumsum(0)]).to(torch.int32)
+    E = int(indptr[-1])
+    indices = torch.randint(0, N, (E,), generator=g, dtype=torch.int32)
+    indices[0] = 0  # a self loop where row 0 has an edge
+    a = torch.rand(E, generator=g).to(dtype)
+    h, V = rnd(B, N, d), rnd(d, d)
+    cell_idx = torch.randint(0, N, (B, K), generator=g, dtype=torch.int32)
+    cell_idx[0, 1] = cell_idx[0, 0]  # a repeated slot
+    cell_idx[1, 2] = 3  # an empty row
+    gm = rnd(B, K, d)
+    want_m = O.csr_messages(f64(h), indptr, indices, f64(a), f64(V), cell_idx)
+    m = ops.csr_messages(h.to(dev), indptr.to(dev), indices.to(dev), a.to(dev), V.to(dev),
+                         cell_idx.to(dev))
+    _close(m, want_m, dtype, "m")
+    assert bool((m[1, 2] == 0).all())
+    want = O.csr_messages_bwd(f64(h), indptr, indices, f64(a), f64(V), cell_idx, f64(gm))
+    got = ops.csr_messages_backward(h.to(dev), indptr.to(dev), indices.to(dev), a.to(dev),
+                                    V.to(dev), cell_idx.to(dev), gm.to(dev))
+    for name, g_, w_ in zip(("dh", "da", "dV"), got, want):
+        _close(g_, w_, dtype, name)
+
+
+def test_unit_mlp_and_messages_are_reproducible(ops, cuda_device):
+    """Every sum has a fixed order: two runs agree bit for bit."""
+    v = load_golden("ref_grouped_unit_mlp.safetensors")
+    D = _put(v, cuda_device, torch.float32)
+    args = (D["v"], D["unit_idx"], D["W1"], D["W2"], D["hidden_saved"], D["grad_out"])
+    first = ops.grouped_unit_mlp_backward(*args)
+    second = ops.grouped_unit_mlp_backward(*args)
+    assert all(torch.equal(x, y) for x, y in zip(first, second))
+    v = load_golden("ref_csr_messages.safetensors")
+    D = _put(v, cuda_device, torch.float32)
+    args = (D["h"], D["indptr"], D["indices"], D["a"], D["V"], D["cell_idx"], D["grad_m"])
+    first, second = ops.csr_messages_backward(*args), ops.csr_messages_backward(*args)
+    assert all(torch.equal(x, y) for x, y in zip(first, second))

@@ -55,6 +55,71 @@ def test_gather_concat_matches_golden_vectors(size):
     _close(gm, v["grad_m"])
 
 
+@pytest.mark.parametrize("size", ["tiny", "ref", "odd"])
+def test_grouped_unit_mlp_matches_golden_vectors(size):
+    """The reference's f64 Rust oracle's vectors for the grouped unit MLP (inputs on a
+    bf16-exact grid, outputs rounded once to f32); the odd vector has a unit without pairs, whose
+    gradients are zero."""
+    v = load_golden(f"{size}_grouped_unit_mlp.safetensors")
+    out, hidden = O.grouped_unit_mlp(v["v"], v["unit_idx"], v["W1"], v["b1"], v["W2"], v["b2"])
+    _close(out, v["out"])
+    _close(hidden, v["hidden_saved"])
+    got = O.grouped_unit_mlp_bwd(v["v"], v["unit_idx"], v["W1"], v["W2"], v["hidden_saved"],
+                                 v["grad_out"])
+    for g_, name in zip(got, ("grad_v", "grad_W1", "grad_b1", "grad_W2", "grad_b2")):
+        _close(g_, v[name])
+    if size == "odd":
+        absent = sorted(set(range(v["W1"].shape[0])) - set(v["unit_idx"].tolist()))
+        assert absent and bool((v["grad_W1"][absent] == 0).all())
+
+
+@pytest.mark.parametrize("size", ["tiny", "ref", "odd"])
+def test_csr_messages_match_golden_vectors(size):
+    """The reference's vectors for the CSR messages: repeated slots (tiny: cell 1 twice in row 1)
+    and edges whose row no slot selects (their grad_a is zero)."""
+    v = load_golden(f"{size}_csr_messages.safetensors")
+    m = O.csr_messages(v["h"], v["indptr"], v["indices"], v["a"], v["V"], v["cell_idx"])
+    _close(m, v["m"])
+    gh, ga, gV = O.csr_messages_bwd(v["h"], v["indptr"], v["indices"], v["a"], v["V"],
+                                    v["cell_idx"], v["grad_m"])
+    _close(gh, v["grad_h"])
+    _close(ga, v["grad_a"])
+    _close(gV, v["grad_V"])
+
+
+def test_unit_and_message_backwards_equal_autograd():
+    """Both backwards against float64 autograd of their forwards, on random inputs with a unit
+    no pair uses, an empty CSR row and repeated slots."""
+    g = torch.Generator().manual_seed(12)
+    P, M, d, H = 9, 4, 3, 5
+    v = torch.randn(P, 4 * d, generator=g, dtype=F64, requires_grad=True)
+    idx = torch.tensor([0, 2, 2, 0, 1, 2, 0, 1, 2])  # unit 3 unused
+    W1 = torch.randn(M, 4 * d, H, generator=g, dtype=F64, requires_grad=True)
+    b1 = torch.randn(M, H, generator=g, dtype=F64, requires_grad=True)
+    W2 = torch.randn(M, H, d, generator=g, dtype=F64, requires_grad=True)
+    b2 = torch.randn(M, d, generator=g, dtype=F64, requires_grad=True)
+    out, hidden = O.grouped_unit_mlp(v, idx, W1, b1, W2, b2)
+    gout = torch.randn(P, d, generator=g, dtype=F64)
+    want = torch.autograd.grad((out * gout).sum(), (v, W1, b1, W2, b2))
+    got = O.grouped_unit_mlp_bwd(v.detach(), idx, W1.detach(), W2.detach(), hidden.detach(), gout)
+    for a, b in zip(got, want):
+        torch.testing.assert_close(a, b, atol=1e-12, rtol=1e-12)
+    B, N, K = 2, 5, 3
+    h = torch.randn(B, N, d, generator=g, dtype=F64, requires_grad=True)
+    indptr = torch.tensor([0, 2, 2, 5, 6, 7], dtype=torch.int32)  # row 1 empty
+    indices = torch.tensor([1, 3, 0, 2, 4, 4, 1], dtype=torch.int32)
+    a = torch.rand(7, generator=g, dtype=F64, requires_grad=True)
+    V = torch.randn(d, d, generator=g, dtype=F64, requires_grad=True)
+    cell_idx = torch.tensor([[1, 2, 2], [0, 4, 1]], dtype=torch.int32)
+    m = O.csr_messages(h, indptr, indices, a, V, cell_idx)
+    gm = torch.randn(B, K, d, generator=g, dtype=F64)
+    want = torch.autograd.grad((m * gm).sum(), (h, a, V))
+    got = O.csr_messages_bwd(h.detach(), indptr, indices, a.detach(), V.detach(), cell_idx, gm)
+    for x, y in zip(got, want):
+        torch.testing.assert_close(x, y, atol=1e-12, rtol=1e-12)
+    assert bool((m[0, 0] == 0).all())  # the empty row's message
+
+
 def test_golden_tiny_vector_has_padded_repeat():
     """The tiny vector holds the case the dummy row exists for: a padded slot repeating a valid
     slot's cell (``cell_idx=[[0,1],[2,2]]``, ``valid=[[1,1],[1,0]]``)."""
