@@ -51,6 +51,7 @@ SIGNATURES: dict[str, list] = {
     "hsn_win_recurrence_dense": [P, P, P, P, P, P, P, P, I, I, I, I, P],
     "hsn_win_cell_update": [P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I,
                             I, I, I, I, I, P],
+    "hsn_win_fold_row": [P, I, P, I, I, P, I, I, P, P, I, I, I, I, I, I, I, P],
     "hsn_gather_concat": [P, P, P, P, P, P, I, I, I, I, I, P],
     "hsn_gather_concat_bwd": [P, P, P, P, P, P, I, I, I, I, I, I, P],
     "hsn_grouped_unit_mlp_fwd": [P, P, P, P, P, P, P, P, I, I, I, I, I, P],

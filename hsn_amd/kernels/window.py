@@ -314,6 +314,46 @@ def _update_tape_fake(y, gate, tape_h, tape_q, tape_age, cells, valid, cand_w, r
     return None
 
 
+@torch.library.custom_op(
+    "hsn::window_update_fold",
+    mutates_args=("tape_h", "tape_q", "tape_age", "tape_hsel", "h_max", "qs", "x"),
+    device_types="cuda")
+def update_fold_op(y: Tensor, gate: Tensor, tape_h: Tensor, tape_q: Tensor, tape_age: Tensor,
+                   cells: Tensor, valid: Tensor, cand_w: Tensor, reset: Tensor, tape_hsel: Tensor,
+                   h_max: Tensor, qs: Tensor, x: Tensor, z: Tensor, context: Tensor, t: int,
+                   cand_norm: bool, cand_eps: float, n_fast: int = 0) -> None:
+    """:func:`update_tape_op` on the round's products as they are (reference window.py:765-853):
+    ``y [B,K,d]`` and ``gate [B*K,d]`` (a strided view of a wider product allowed) in fp32 or
+    bf16, widened to fp32 before the round (exact), then record ``t + 1`` of
+    ``x [n,B,d_z+d+d_c(+d)]`` (when ``t + 1 < n``) becomes ``[z; q; context(; f)]`` of position
+    ``t + 1`` (``hsn_win_fold_row``): ``q`` after the round and the next reset, ``f`` the mean of
+    cells ``0 .. n_fast-1`` of that record's state, each value rounded to ``x``'s dtype."""
+    B, n_state, N, d = (int(n) for n in tape_h.shape)
+    n, K = int(cells.shape[1]), int(cells.shape[2])
+    d_z, d_c = int(z.shape[2]), int(context.shape[2])
+    if tuple(x.shape) != (n, B, d_z + d + d_c + (d if n_fast else 0)):
+        raise ValueError(f"x must be [n, B, d_z + d + d_c (+ d)], got {tuple(x.shape)}")
+    if not 0 <= n_fast <= N:
+        raise ValueError(f"n_fast must lie in [0, {N}], got {n_fast}")
+    if not x.is_contiguous() or not z.is_contiguous() or not context.is_contiguous():
+        raise ValueError("x, z and context must be contiguous")
+    y32 = y.float().contiguous()
+    gate32 = gate.float().reshape(B, K, d).contiguous()
+    _launch_update(y32, gate32, cand_w, cand_norm, cand_eps, tape_h, tape_q, tape_age, None, cells,
+                   valid, tape_h, tape_q, tape_age, None, tape_hsel, h_max, reset, qs, B, N, d, K, t,
+                   n_state, n, t + 1)
+    if t + 1 < n:
+        call("hsn_win_fold_row", ptr(x), _io(x), ptr(z), _io(z), d_z, ptr(context), _io(context),
+             d_c, ptr(tape_q), ptr(tape_h), int(n_fast), B, N, d, n, n_state, t + 1,
+             stream_of(x.device))
+
+
+@update_fold_op.register_fake
+def _update_fold_fake(y, gate, tape_h, tape_q, tape_age, cells, valid, cand_w, reset, tape_hsel,
+                      h_max, qs, x, z, context, t, cand_norm, cand_eps, n_fast=0):
+    return None
+
+
 def cell_update_unsupported(n_cells: int, d: int, k: int) -> Optional[str]:
     """Why :func:`cell_update` cannot take a model of this shape (``None``: it can), by the
     library's own geometry (reference window.py:626-640)."""
@@ -344,6 +384,16 @@ def cell_update(cell, y: Tensor, gate: Tensor, state: CellGraphState, cells: Ten
         state.age.contiguous(), state.pos.contiguous(), cells.contiguous(), valid.contiguous(), w,
         cand_norm, eps)
     return CellGraphState.make(h=h, q=q, age=age, pos=pos), h_sel, h_max
+
+
+def update_fold(cell, y, gate, tape_h, tape_q, tape_age, cells, valid, reset, tape_hsel, h_max, qs,
+                x, z, context, *, t: int, n_fast: int = 0) -> None:
+    """:func:`update_tape` from the round's products as they are, with the next position's
+    input of the first product written into ``x`` (:func:`update_fold_op`; reference
+    window.py:1099-1143)."""
+    cand_norm, w, eps = _cand(cell)
+    update_fold_op(y, gate, tape_h, tape_q, tape_age, cells, valid, w, reset, tape_hsel, h_max, qs,
+                   x, z, context, t, cand_norm, eps, n_fast)
 
 
 def update_tape(cell, y, gate, tape_h, tape_q, tape_age, cells, valid, reset, tape_hsel, h_max, qs,

@@ -258,6 +258,22 @@ int hsn_win_cell_update(const void* y, const void* gate, int io_dtype, const flo
                         float* h_max, const uint8_t* reset, float* q_post, int B, int N, int d,
                         int K, int t, int n_state, int n_slot, int t_out, void* stream);
 
+/*
+ * The folded sweep's row (reference kernels/cuda/hsn_window.cu:770-779,887-920, the extra output
+ * of update_fold_op, python/hsn/kernels/window.py:765-853): after hsn_win_cell_update has
+ * written record t_next of the state tape, the next position's input row of the first product,
+ *   x[t_next, b, :] = [z[b, t_next, :]; q[b, t_next, :]; context[b, t_next, :] (; f[b, :])],
+ * every value rounded once to x_dtype (round to nearest even for bf16); f, present when
+ * n_fast = F > 0, is the mean of cells 0 .. F-1 of state record t_next, summed in cell order
+ * (the fast readout, model.fast_readout).
+ *   x [n, B, d_z + d + d_c (+ d)] x_dtype (f32 or bf16); z [B, n, d_z] z_dtype; context
+ *   [B, n, d_c] c_dtype; tape_q [B, n_state, d], tape_h [B, n_state, N, d] f32; 1 <= t_next < n.
+ */
+int hsn_win_fold_row(void* x, int x_dtype, const void* z, int z_dtype, int d_z,
+                     const void* context, int c_dtype, int d_c, const float* tape_q,
+                     const float* tape_h, int n_fast, int B, int N, int d, int n, int n_state,
+                     int t_next, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

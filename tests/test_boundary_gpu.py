@@ -69,6 +69,7 @@ def _cases(dev):
     reset = torch.zeros(B, n, dtype=torch.bool, device=dev)
     reset[2, 2] = True
     c, b = f(B, K, d).tanh(), torch.sigmoid(f(B, K, d))
+    wide = f(B * K, d + 3)  # a wider product: the gate is its last d columns (a strided view)
     deg = torch.tensor([2, 0, 1, 3, 1, 0, 2, 1, 1, 0, 2, 1])
     indptr = torch.cat([torch.zeros(1, dtype=torch.int64), deg.cumsum(0)]).to(torch.int32)
     csr = (indptr.to(dev), torch.randint(0, N, (int(indptr[-1]),), generator=g,
@@ -107,6 +108,12 @@ def _cases(dev):
                                 cost) + tapes() + (1, M) + sel, ()),
         "window_cell_update": (window.cell_update_op,
                                (y, gate, h, q, age, pos, cells64, valid_b, w, True, 1e-6), ()),
+        "window_update_fold": (window.update_fold_op,
+                               (y.to(torch.bfloat16), wide[:, 3:], th, tq, ta, dec_c, dec_v, w,
+                                reset, torch.zeros(B, n, K, d, device=dev),
+                                torch.zeros(B, n, device=dev), torch.zeros(B, n, d, device=dev),
+                                torch.zeros(n, B, 5 + 2 * d + 3, dtype=torch.bfloat16, device=dev),
+                                f(B, n, 5), f(B, n, 3).to(torch.bfloat16), 1, True, 1e-6, 2), ()),
         "window_update_tape": (window.update_tape_op,
                                (y, gate, th, tq, ta, dec_c, dec_v, w, reset,
                                 torch.zeros(B, n, K, d, device=dev), torch.zeros(B, n, device=dev),
@@ -119,7 +126,8 @@ OP_NAMES = ["gather_concat", "gather_concat_backward", "grouped_unit_mlp",
             "gated_delta_update",
             "gated_delta_update_functional", "gated_delta_update_state",
             "gated_delta_update_backward", "window_select", "window_select_tape",
-            "window_select_fold", "window_cell_update", "window_update_tape"]
+            "window_select_fold", "window_cell_update", "window_update_tape",
+            "window_update_fold"]
 
 
 def _clone(args):
@@ -243,3 +251,66 @@ def test_tape_ops_write_what_the_plain_ops_return(mods, cuda_device, cand_norm):
         assert torch.equal(tape_h[:, t], pre.h)  # the record it read is untouched
         state = after
     assert fired > 0 and padded > 0  # probes and padded slots were exercised
+
+
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n_fast", [0, 3])
+def test_update_fold_is_update_tape_and_the_next_row(mods, cuda_device, x_dtype, n_fast):
+    """``update_fold`` on the products as they are (bf16 ``y``, an fp32 gate that is a strided
+    view of a wider product) writes exactly what ``update_tape`` writes from their fp32 copies,
+    and record ``t + 1`` of ``x`` is ``[z; q; context(; f)]`` of position ``t + 1`` rounded to
+    ``x``'s dtype: ``q`` after the next reset (set on row 1), ``f`` the mean of the first
+    ``n_fast`` cells summed in cell order; at the last record ``x`` is left alone
+    (reference window.py:765-853)."""
+    _, window = mods
+    dev = cuda_device
+    g = torch.Generator().manual_seed(61)
+    B, n, N, d, K, d_z, d_c = 3, 4, 20, 16, 4, 6, 5
+    f = lambda *s: torch.randn(*s, generator=g).to(dev)  # noqa: E731
+    w = (torch.rand(d, generator=g) + 0.5).to(dev)
+    th, tq = f(B, n + 1, N, d) * 0.4, f(B, n + 1, d) * 0.1
+    ta = torch.randint(0, 5, (B, n + 1, N), generator=g).to(dev)
+    dec_c = torch.stack([torch.stack([torch.randperm(N, generator=g)[:K] for _ in range(n)])
+                         for _ in range(B)]).to(dev)
+    dec_v = torch.ones(B, n, K, dtype=torch.bool, device=dev)
+    dec_v[2, :, 1] = False
+    reset = torch.zeros(B, n, dtype=torch.bool, device=dev)
+    reset[1, 2] = True
+    z = f(B, n, d_z).to(torch.bfloat16)
+    ctx = f(B, n, d_c)
+    width = d_z + d + d_c + (d if n_fast else 0)
+    for t in (1, n - 1):
+        y = f(B, K, d).to(torch.bfloat16)
+        wide = f(B * K, d + 7)
+        gate = wide[:, 7:]
+        outs = []
+        for fold in (False, True):
+            tapes = [th.clone(), tq.clone(), ta.clone()]
+            rec = [torch.full((B, n, K, d), 7.0, device=dev), torch.full((B, n), 7.0, device=dev),
+                   torch.full((B, n, d), 7.0, device=dev)]
+            x = torch.full((n, B, width), 7.0, device=dev).to(x_dtype)
+            if fold:
+                window.update_fold_op(y, gate, *tapes, dec_c, dec_v, w, reset, *rec, x, z, ctx, t,
+                                      True, 1e-6, n_fast)
+            else:
+                window.update_tape_op(y.float(), gate.contiguous().reshape(B, K, d), *tapes, dec_c,
+                                      dec_v, w, reset, *rec, t, True, 1e-6)
+            outs.append((tapes, rec, x))
+        for a, b_ in zip(outs[0][0] + outs[0][1], outs[1][0] + outs[1][1]):
+            assert torch.equal(a, b_)
+        x = outs[1][2]
+        if t + 1 < n:
+            h1, q1 = outs[0][0][0][:, t + 1].cpu(), outs[0][0][1][:, t + 1].cpu()
+            parts = [z[:, t + 1].float().cpu(), q1, ctx[:, t + 1].cpu()]
+            if n_fast:
+                s = torch.zeros(B, d)
+                for cell in range(n_fast):
+                    s = s + h1[:, cell]
+                parts.append(s / n_fast)
+            want = torch.cat(parts, dim=1).to(x_dtype)
+            assert torch.equal(x[t + 1].cpu(), want)
+            assert bool((q1[1] == 0).all())  # the reset of row 1 at position t + 1 = 2
+            others = [r for r in range(n) if r != t + 1]
+            assert bool((x[others].float() == 7.0).all())
+        else:
+            assert bool((x.float() == 7.0).all())
