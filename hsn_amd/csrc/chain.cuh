@@ -287,11 +287,29 @@ inline dim3 chain_grid(int B, int G) {
 }
 
 // LDS words of a chain workgroup: nr [T + 2], the reset bits [TW], their word table [TW + 1],
-// the row maxima [T], the next cell to take, the group's list starts [C + 1] and its staged
-// events [stage].
+// the row maxima [T], the next cell to take, the group's list starts [C + 1], its staged events
+// [stage] and its cells in the order they are taken [C].
 __host__ __device__ inline int chain_words(int T, int C, int stage) {
     const int TW = (T + 31) / 32;
-    return (T + 2) + TW + (TW + 1) + T + 1 + (C + 1) + stage;
+    return (T + 2) + TW + (TW + 1) + T + 1 + (C + 1) + stage + C;
+}
+
+// The group's cells heaviest first (most events; ties by cell), into order[0 .. nc): the
+// wavefronts take cells in this order, so the long chains start first and the workgroup's
+// wavefronts finish together (a workgroup holds its CU slot until its last wavefront ends).
+// cptr must be visible to every thread; ends with a barrier.
+__device__ __forceinline__ void heavy_first(const int* cptr, int nc, int* order, int tid,
+                                            int nthreads) {
+    for (int i = tid; i < nc; i += nthreads) {
+        const int ni = cptr[i + 1] - cptr[i];
+        int rank = 0;
+        for (int j = 0; j < nc; ++j) {
+            const int nj = cptr[j + 1] - cptr[j];
+            rank += (nj > ni || (nj == ni && j < i)) ? 1 : 0;
+        }
+        order[rank] = i;
+    }
+    __syncthreads();
 }
 
 // The wavefront maximum of the bit patterns of |h| over the cell's columns (a NaN above +inf).
@@ -307,7 +325,9 @@ __device__ __forceinline__ uint32_t cell_abs_max(const float (&h)[V], int lane, 
 __device__ __forceinline__ void max_interval(uint32_t* hm, int p0, int p1, uint32_t val,
                                              int lane) {
     if (val == 0u) return;
-    for (int p = p0 + lane; p < p1; p += 64) atomicMax(&hm[p], val);
+    if (p0 + lane < p1) atomicMax(&hm[p0 + lane], val);
+    if (p1 - p0 > 64)  // uniform; the intervals are mostly shorter than a wavefront
+        for (int p = p0 + 64 + lane; p < p1; p += 64) atomicMax(&hm[p], val);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -346,7 +366,7 @@ __device__ __forceinline__ void fetch_rows(IO (&yv)[V], IO (&gv)[V], rsrc_t ry, 
     }
 }
 
-template <typename IO, int V, int NB>
+template <typename IO, int V, int NB, bool DELTA>
 __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
     extern __shared__ uint32_t lds_u[];
     int b, g;
@@ -361,6 +381,7 @@ __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
     int* next = reinterpret_cast<int*>(hm + T);          // [1]
     int* cptr = next + 1;                                // [C + 1]
     int* cev = cptr + a.C + 1;                           // [stage]
+    int* order = cev + a.stage;                          // [C]
     const bool want_max = a.hm_groups != nullptr;
     const int c_begin = g * a.C, c_end = min(N, c_begin + a.C);
     const int nc = c_end - c_begin;
@@ -375,6 +396,7 @@ __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
     if (tid == 0) next[0] = 0;
     const int lrT = reset_table(a.reset ? a.reset + int64_t(b) * T : nullptr, T, nr, rbits, nx,
                                 tid, kChainThreads);
+    heavy_first(cptr, nc, order, tid, kChainThreads);
     const int64_t slot0 = int64_t(b) * T * K;
     const uint32_t row_bytes = uint32_t(T) * K * d * sizeof(IO);
     const rsrc_t ry = make_rsrc(static_cast<const IO*>(a.y) + slot0 * d, row_bytes);
@@ -397,9 +419,10 @@ __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
     const int pad_begin = ptr[N];
 
     for (;;) {
-        int ci = lane == 0 ? atomicAdd(next, 1) : 0;
-        ci = __builtin_amdgcn_readfirstlane(ci);
-        if (ci >= nc) break;
+        int slot = lane == 0 ? atomicAdd(next, 1) : 0;
+        slot = __builtin_amdgcn_readfirstlane(slot);
+        if (slot >= nc) break;
+        const int ci = uniform(order[slot]);
         const int c = c_begin + ci;
         const int e_beg = uniform(cptr[ci]), e_end = uniform(cptr[ci + 1]);
         float h[V];
@@ -457,7 +480,7 @@ __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
                 const float hn = (1.0f - bg) * hold + bg * cand;
                 bstore_f32<IO>(hold, rho, voff[v], so);
                 bstore_f32<IO>(hn, rhs, voff[v], so);
-                bstore(hn - hold, rdl, voff4[v], uint32_t(t * K + (q & 255)) * srow4);
+                if constexpr (DELTA) bstore(hn - hold, rdl, voff4[v], uint32_t(t * K + (q & 255)) * srow4);
                 hold_last[v] = hold;
                 h[v] = hn;
             }
@@ -807,6 +830,7 @@ __global__ __launch_bounds__(kChainThreads) void chain_bwd(BwdArgs a) {
     int* next = nx + TW + 1 + T;  // the layout of chain_fwd (no row maxima used)
     int* cptr = next + 1;
     int* cev = cptr + a.C + 1;
+    int* order = cev + a.stage;
     const int c_begin = g * a.C, c_end = min(N, c_begin + a.C);
     const int nc = c_end - c_begin;
     const int32_t* ptr = a.ptr + int64_t(b) * (N + 1);
@@ -817,6 +841,7 @@ __global__ __launch_bounds__(kChainThreads) void chain_bwd(BwdArgs a) {
     for (int i = tid; i < nst; i += kChainThreads) cev[i] = ev[pc0 + i];
     if (tid == 0) next[0] = 0;
     reset_table(a.reset ? a.reset + int64_t(b) * T : nullptr, T, nr, rbits, nx, tid, kChainThreads);
+    heavy_first(cptr, nc, order, tid, kChainThreads);
     const int64_t slot0 = int64_t(b) * T * K;
     const uint32_t row_bytes = uint32_t(T) * K * d * sizeof(IO);
     const rsrc_t ry = make_rsrc(static_cast<const IO*>(a.y) + slot0 * d, row_bytes);
@@ -843,9 +868,10 @@ __global__ __launch_bounds__(kChainThreads) void chain_bwd(BwdArgs a) {
         float r[NB][V];
     };
     for (;;) {
-        int ci = lane == 0 ? atomicAdd(next, 1) : 0;
-        ci = __builtin_amdgcn_readfirstlane(ci);
-        if (ci >= nc) break;
+        int slot = lane == 0 ? atomicAdd(next, 1) : 0;
+        slot = __builtin_amdgcn_readfirstlane(slot);
+        if (slot >= nc) break;
+        const int ci = uniform(order[slot]);
         const int c = c_begin + ci;
         const int e_beg = uniform(cptr[ci]), e_end = uniform(cptr[ci + 1]);
         const bool staged = e_end - pc0 <= nst;

@@ -133,7 +133,7 @@ void build_lists(const int32_t* slots, int32_t* ptr, int32_t* ev, int B, int T, 
 
 template <typename IO, int V>
 void launch_chain_fwd(const chain::FwdArgs& a, size_t lds, hipStream_t st) {
-    auto k = chain::chain_fwd<IO, V, 8>;
+    auto k = a.delta ? chain::chain_fwd<IO, V, 8, true> : chain::chain_fwd<IO, V, 8, false>;
     HSN_HIP(allow_lds(k, lds));
     hipLaunchKernelGGL(k, chain::chain_grid(a.B, (a.N + a.C - 1) / a.C),
                        dim3(chain::kChainThreads), lds, st, a);
