@@ -321,13 +321,16 @@ __device__ __forceinline__ uint32_t cell_abs_max(const float (&h)[V], int lane, 
     return wave_max_from_groups<1>(m);
 }
 
-// The row maxima over positions [p0, p1) from one cell's value (bits).
+// The row maxima over positions [p0, p1) from one cell's value (bits): the first 64 positions
+// inline (intervals are mostly shorter than a wavefront), the rest out of line.
+__device__ __attribute__((noinline)) void max_interval_tail(uint32_t* hm, int p0, int p1,
+                                                           uint32_t val, int lane) {
+    for (int p = p0 + lane; p < p1; p += 64) atomicMax(&hm[p], val);
+}
 __device__ __forceinline__ void max_interval(uint32_t* hm, int p0, int p1, uint32_t val,
                                              int lane) {
-    if (val == 0u) return;
     if (p0 + lane < p1) atomicMax(&hm[p0 + lane], val);
-    if (p1 - p0 > 64)  // uniform; the intervals are mostly shorter than a wavefront
-        for (int p = p0 + 64 + lane; p < p1; p += 64) atomicMax(&hm[p], val);
+    if (unlikely(uniform(p1 - p0) > 64)) max_interval_tail(hm, p0 + 64, p1, val, lane);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -366,7 +369,7 @@ __device__ __forceinline__ void fetch_rows(IO (&yv)[V], IO (&gv)[V], rsrc_t ry, 
     }
 }
 
-template <typename IO, int V, int NB, bool DELTA>
+template <typename IO, int V, int NB, bool DELTA, bool HMAX>
 __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
     extern __shared__ uint32_t lds_u[];
     int b, g;
@@ -382,7 +385,7 @@ __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
     int* cptr = next + 1;                                // [C + 1]
     int* cev = cptr + a.C + 1;                           // [stage]
     int* order = cev + a.stage;                          // [C]
-    const bool want_max = a.hm_groups != nullptr;
+    constexpr bool want_max = HMAX;
     const int c_begin = g * a.C, c_end = min(N, c_begin + a.C);
     const int nc = c_end - c_begin;
     const int32_t* ptr = a.ptr + int64_t(b) * (N + 1);
@@ -465,13 +468,14 @@ __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
             }
         };
         const bool pad_here = c == 0 && pad_begin < n_slots;
-        auto update = [&](int q, int nrq, const IO (&yv)[V], const IO (&gv)[V])
-                          __attribute__((always_inline)) {
-            const int t = q >> 8;
-            const uint32_t so = uint32_t(t * K + (q & 255)) * srow;
+        // one event: position t, its slot's byte offsets (so: storage rows, so4: fp32 rows) and
+        // the first reset after t
+        auto update = [&](auto pad_c, int t, uint32_t so, uint32_t so4, int nrq, const IO (&yv)[V],
+                          const IO (&gv)[V]) __attribute__((always_inline)) {
+            constexpr bool kPad = decltype(pad_c)::value;
             const bool zero = nrprev <= t;  // a reset since the cell's last event
-            if (want_max) max_interval(hm, s, min(t, nrprev), vprev, lane);
-            if (pad_here) flush(t);
+            if constexpr (want_max) max_interval(hm, s, min(t, nrprev), vprev, lane);
+            if constexpr (kPad) flush(t);
 #pragma unroll
             for (int v = 0; v < V; ++v) {
                 const float hold = zero ? 0.0f : h[v];
@@ -480,33 +484,37 @@ __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
                 const float hn = (1.0f - bg) * hold + bg * cand;
                 bstore_f32<IO>(hold, rho, voff[v], so);
                 bstore_f32<IO>(hn, rhs, voff[v], so);
-                if constexpr (DELTA) bstore(hn - hold, rdl, voff4[v], uint32_t(t * K + (q & 255)) * srow4);
-                hold_last[v] = hold;
+                if constexpr (DELTA) bstore(hn - hold, rdl, voff4[v], so4);
+                if constexpr (kPad) hold_last[v] = hold;
                 h[v] = hn;
             }
-            if (want_max) vprev = cell_abs_max<V>(h, lane, d);
+            if constexpr (want_max) vprev = cell_abs_max<V>(h, lane, d);
             s = t;
             tprev = t;
             nrprev = nrq;
-            if (pad_here) flush(t + 1);
+            if constexpr (kPad) flush(t + 1);
         };
-        // windows of 64 events (one per lane), in batches of NB with two batches in flight
-        auto walk = [&](auto staged_c) __attribute__((always_inline)) {
+        // windows of 64 events (one per lane), in batches of NB with two batches in flight; a
+        // window's positions, slot offsets and next resets are computed for all its events at
+        // once (lane i: event i) and read per event with readlane
+        auto walk = [&](auto staged_c, auto pad_c) __attribute__((always_inline)) {
             constexpr bool kStaged = decltype(staged_c)::value;
             for (int w0 = e_beg; w0 < e_end; w0 += kEvWin) {
                 const int m = min(kEvWin, e_end - w0);
                 int evw;
                 if constexpr (kStaged) evw = lane < m ? cev[w0 - pc0 + lane] : 0;
                 else evw = lane < m ? ev[w0 + lane] : 0;
-                const int nrw = lane < m ? nr[(evw >> 8) + 1] : T;
+                const int tw = evw >> 8;
+                const int slw = tw * K + (evw & 255);
+                const uint32_t sow = uint32_t(slw) * srow;
+                const uint32_t so4w = uint32_t(slw) * srow4;
+                const int nrw = lane < m ? nr[tw + 1] : T;
                 IO ya[NB][V], ga[NB][V], yb[NB][V], gb[NB][V];
                 auto fetch = [&](int j, IO (&yv)[NB][V], IO (&gv)[NB][V])
                                  __attribute__((always_inline)) {
 #pragma unroll
                     for (int i = 0; i < NB; ++i) {
-                        const int idx = min(j + i, kEvWin - 1);
-                        const int q = __builtin_amdgcn_readlane(evw, idx);
-                        const uint32_t so = uint32_t((q >> 8) * K + (q & 255)) * srow;
+                        const uint32_t so = __builtin_amdgcn_readlane(sow, min(j + i, kEvWin - 1));
                         fetch_rows<IO, V>(yv[i], gv[i], ry, rg, voff, so, j + i < m);
                     }
                 };
@@ -516,7 +524,9 @@ __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
                     for (int i = 0; i < NB; ++i) {
                         if (j + i < m) {
                             const int idx = j + i;
-                            update(__builtin_amdgcn_readlane(evw, idx),
+                            update(pad_c, __builtin_amdgcn_readlane(tw, idx),
+                                   __builtin_amdgcn_readlane(sow, idx),
+                                   DELTA ? __builtin_amdgcn_readlane(so4w, idx) : 0u,
                                    __builtin_amdgcn_readlane(nrw, idx), yv[i], gv[i]);
                         }
                     }
@@ -531,8 +541,9 @@ __global__ __launch_bounds__(kChainThreads) void chain_fwd(FwdArgs a) {
                 }
             }
         };
-        if (!pad_here && e_end - pc0 <= nst) walk(std::true_type{});
-        else walk(std::false_type{});
+        if (pad_here) walk(std::false_type{}, std::true_type{});
+        else if (e_end - pc0 <= nst) walk(std::true_type{}, std::false_type{});
+        else walk(std::false_type{}, std::false_type{});
         if (pad_here) flush(T);
         if (want_max) max_interval(hm, s, min(T, nrprev), vprev, lane);
         const bool cleared = nrprev < T;  // a reset after the cell's last event
@@ -896,17 +907,20 @@ __global__ __launch_bounds__(kChainThreads) void chain_bwd(BwdArgs a) {
                 int evw;
                 if constexpr (kStaged) evw = lane < m ? cev[w0 - pc0 + lane] : 0;
                 else evw = lane < m ? ev[w0 + lane] : 0;
-                const int nrw = lane < m ? nr[(evw >> 8) + 1] : T;
+                // the window's positions, slot offsets, share offsets and next resets, for all
+                // its events at once (lane i: event i), read per event with readlane
+                const int tw = evw >> 8;
+                const uint32_t sow = uint32_t(tw * K + (evw & 255)) * srow;
+                const uint32_t stw = uint32_t(tw) * srow4;
+                const int nrw = lane < m ? nr[tw + 1] : T;
                 Rows ra, rb;
                 // batch j holds window indices [j - NB + 1, j], fetched latest first
                 auto fetch = [&](int j, Rows& r) __attribute__((always_inline)) {
 #pragma unroll
                     for (int i = 0; i < NB; ++i) {
                         const int idx = j - i;
-                        const int q = __builtin_amdgcn_readlane(evw, max(idx, 0));
-                        const int t = q >> 8;
-                        const uint32_t so = uint32_t(t * K + (q & 255)) * srow;
-                        const uint32_t st = uint32_t(t) * srow4;
+                        const uint32_t so = __builtin_amdgcn_readlane(sow, max(idx, 0));
+                        const uint32_t st = __builtin_amdgcn_readlane(stw, max(idx, 0));
                         const bool in = idx >= 0;
 #pragma unroll
                         for (int v = 0; v < V; ++v) {
@@ -924,10 +938,9 @@ __global__ __launch_bounds__(kChainThreads) void chain_bwd(BwdArgs a) {
                     for (int i = 0; i < NB; ++i) {
                         const int idx = j - i;
                         if (idx >= 0) {
-                            const int q = __builtin_amdgcn_readlane(evw, idx);
+                            const int t = __builtin_amdgcn_readlane(tw, idx);
                             const int nrq = __builtin_amdgcn_readlane(nrw, idx);
-                            const int t = q >> 8;
-                            const uint32_t so = uint32_t(t * K + (q & 255)) * srow;
+                            const uint32_t so = __builtin_amdgcn_readlane(sow, idx);
                             const bool zero = nrq <= tnext && tnext < T;  // a reset in (t, tnext]
 #pragma unroll
                             for (int v = 0; v < V; ++v) {

@@ -133,7 +133,11 @@ void build_lists(const int32_t* slots, int32_t* ptr, int32_t* ev, int B, int T, 
 
 template <typename IO, int V>
 void launch_chain_fwd(const chain::FwdArgs& a, size_t lds, hipStream_t st) {
-    auto k = a.delta ? chain::chain_fwd<IO, V, 8, true> : chain::chain_fwd<IO, V, 8, false>;
+    constexpr int NB = 4;  // measured: 4 ahead of 8 and 16 (most cells hold a few events)
+    auto k = a.delta ? (a.hm_groups ? chain::chain_fwd<IO, V, NB, true, true>
+                                    : chain::chain_fwd<IO, V, NB, true, false>)
+                     : (a.hm_groups ? chain::chain_fwd<IO, V, NB, false, true>
+                                    : chain::chain_fwd<IO, V, NB, false, false>);
     HSN_HIP(allow_lds(k, lds));
     hipLaunchKernelGGL(k, chain::chain_grid(a.B, (a.N + a.C - 1) / a.C),
                        dim3(chain::kChainThreads), lds, st, a);
