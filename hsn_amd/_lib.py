@@ -106,7 +106,7 @@ def unsupported(op: int, B: int, T: int, N: int, d: int, K: int) -> str | None:
     return lib.hsn_win_last_error().decode(errors="replace")
 
 
-PATHS = {"auto": 0, "slice": 1, "chain": 2}
+PATHS = {"auto": 0, "slice": 1, "chain": 2, "strip": 3}
 PATH_NAMES = {v: k for k, v in PATHS.items()}
 
 

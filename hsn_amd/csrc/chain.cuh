@@ -85,7 +85,7 @@ __device__ __forceinline__ int slot_cell(const int32_t* slots, int64_t i, int N)
     return c >= 0 && c < N ? c : -1;
 }
 
-__global__ __launch_bounds__(kListThreads) void row_lists(ListArgs a) {
+static __global__ __launch_bounds__(kListThreads) void row_lists(ListArgs a) {
     extern __shared__ uint32_t lds_u[];
     const int b = blockIdx.x;
     const int tid = threadIdx.x;

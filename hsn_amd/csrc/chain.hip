@@ -68,9 +68,16 @@ bool chain_takes(int B, int T, int N, int d, int K, const char** why) {
 int choose_path(int op, int B, int T, int N, int d, int K, size_t elem) {
     const char* why_s = nullptr;
     const char* why_c = nullptr;
+    const char* why_p = nullptr;
     const int setting = path_setting();
-    const bool s_ok = setting != kPathChain && slice_takes(op, B, T, N, d, K, &why_s);
-    const bool c_ok = setting != kPathSlice && chain_takes(B, T, N, d, K, &why_c);
+    const bool any = setting == kPathAuto;
+    const bool s_ok = (any || setting == kPathSlice) && slice_takes(op, B, T, N, d, K, &why_s);
+    const bool c_ok = (any || setting == kPathChain) && chain_takes(B, T, N, d, K, &why_c);
+    if (setting == kPathStrip) {  // the strips only where asked for (see below)
+        if (!strip_takes(op, B, T, N, d, K, &why_p))
+            throw AbiError{HSN_ERR_INVALID_ARGUMENT, std::string("(strip path) ") + why_p};
+        return kPathStrip;
+    }
     if (!s_ok && !c_ok) {
         std::string msg;
         if (setting == kPathSlice) msg = std::string("(slice path) ") + why_s;
@@ -80,7 +87,13 @@ int choose_path(int op, int B, int T, int N, int d, int K, size_t elem) {
     }
     if (!c_ok) return kPathSlice;
     if (!s_ok) return kPathChain;
-    // both take it: the slices where a wavefront's piece of a slot row is a full 32-byte sector
+    // The strips are never the automatic choice: measured on MI355X at B32 T256 N256 d64 K8 fp32
+    // they take 30 + 35 us (forward + backward) against the slices' 30 + 29, and at B128 T128
+    // N512 d128 K8 fp32 0.44 ms against the chains' 0.31: their walk moves its bytes near the
+    // bandwidth the slices reach, but each of the 256 (one per CU) or more workgroups first builds
+    // the row's lists and afterwards sums and scans the row in LDS, phases that move no HBM bytes
+    // and run on every CU at once.
+    // Both slices and chains take it: the slices where a wavefront's piece of a slot row is a full 32-byte sector
     // and the state slice (N * S words) leaves room for chunks of the row in LDS; the chains
     // where the piece would be narrower (K large against d) or the slice large (N large). Measured
     // on MI355X: slices at B32 T256 N256 d64 K8 fp32 (S 8, 68 against 95 us per step), chains at
@@ -96,7 +109,9 @@ int choose_path(int op, int B, int T, int N, int d, int K, size_t elem) {
 WorkspaceLayout workspace_layout(int op, int B, int T, int N, int d, int K, size_t elem,
                                  int cand_norm) {
     WorkspaceLayout L;
-    L.chain = choose_path(op, B, T, N, d, K, elem) == kPathChain;
+    const int path = choose_path(op, B, T, N, d, K, elem);
+    L.chain = path == kPathChain;
+    L.strip = path == kPathStrip;
     const int64_t slots = int64_t(B) * T * K;
     size_t at = 0;
     if (L.chain) {
@@ -254,8 +269,9 @@ void chain_backward(const void* y, const void* gate_pre, const void* h_old, int 
 
 extern "C" int hsn_win_set_path(int path) {
     HSN_ABI_BEGIN
-    HSN_REQUIRE(path == hsn::kPathAuto || path == hsn::kPathSlice || path == hsn::kPathChain,
-                HSN_ERR_INVALID_ARGUMENT, "hsn_win_set_path: path must be 0 (auto), 1 or 2");
+    HSN_REQUIRE(path == hsn::kPathAuto || path == hsn::kPathSlice || path == hsn::kPathChain ||
+                    path == hsn::kPathStrip,
+                HSN_ERR_INVALID_ARGUMENT, "hsn_win_set_path: path must be 0 (auto), 1, 2 or 3");
     hsn::set_path_setting(path);
     HSN_ABI_END
 }

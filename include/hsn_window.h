@@ -65,23 +65,29 @@ const char* hsn_win_last_error(void);
 int hsn_win_supports(int op, int B, int T, int N, int d, int K);
 
 /*
- * The two designs of the window's sweeps. No counterpart in the reference (its fused sweep is
- * one design); these choose between this library's two, which compute the same outputs to the
+ * The three designs of the window's sweeps. No counterpart in the reference (its fused sweep is
+ * one design); these choose between this library's three, which compute the same outputs to the
  * parity tolerance:
  *   HSN_PATH_SLICE  time-chunked slices of the state resident in LDS (a workgroup per row and
- *                   column slice): the fastest where a wavefront's piece of a slot row is a
- *                   full 32-byte sector (d / S columns per wavefront, S * K <= 64);
+ *                   column slice): a wavefront's piece of a slot row is S columns, S * K <= 64;
  *   HSN_PATH_CHAIN  cell chains (a wavefront per cell walks the cell's events in time; whole
  *                   slot rows per load and store; the summary by a scan over time): any N, K
- *                   up to 255, d up to 256.
+ *                   up to 255, d up to 256;
+ *   HSN_PATH_STRIP  column strips (a workgroup per row and 8 columns holds the row's event
+ *                   lists, the per-slot summary deltas and the scan in LDS; the cells' chains in
+ *                   pairs of lanes, 4 columns per lane): one kernel per direction and no
+ *                   workspace; d a multiple of 4, K up to 255, T * K <= 8192 and the lists
+ *                   within the LDS.
  * hsn_win_set_path fixes the path of every later hsn_win_forward / hsn_win_forward_noalloc /
- * hsn_win_backward call of the process (HSN_PATH_AUTO, the default: the slices where their
- * piece is a full sector and N * S <= 2048, else the chains). hsn_win_path reports the path a call of `op`
- * (HSN_OP_FORWARD or HSN_OP_BACKWARD) would take, or the reason neither takes the shape.
+ * hsn_win_backward call of the process (HSN_PATH_AUTO, the default: the slices where their piece
+ * is a full sector and N * S <= 2048, else the chains; the strips only when set, being slower on
+ * the measured shapes). hsn_win_path reports the path a call of `op` (HSN_OP_FORWARD or
+ * HSN_OP_BACKWARD) would take, or the reason none takes the shape.
  */
 #define HSN_PATH_AUTO 0
 #define HSN_PATH_SLICE 1
 #define HSN_PATH_CHAIN 2
+#define HSN_PATH_STRIP 3
 int hsn_win_set_path(int path);
 int hsn_win_path(int op, int B, int T, int N, int d, int K, int io_dtype, int* path);
 

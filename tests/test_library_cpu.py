@@ -206,8 +206,22 @@ def test_workspace_and_path_follow_the_shape(name):
         assert _lib.path_for(_lib.OP_FORWARD, B, T, N, d, K, io) == "slice"
     finally:
         _lib.set_path("auto")
+    # the strips, only when set: no workspace but the RMS input's; the forward holds a position's
+    # K * 8 deltas per row in LDS, so the bf16 and skewed rows (T K = 8192, 32768) do not fit
+    try:
+        _lib.set_path("strip")
+        for op in (_lib.OP_FORWARD, _lib.OP_BACKWARD):
+            why = _lib.unsupported(op, B, T, N, d, K)
+            if name in ("ref", "tbptt", "tiny"):
+                assert why is None and _lib.path_for(op, B, T, N, d, K, io) == "strip"
+                assert _lib.workspace_bytes(op, B, T, N, d, K, io, False) == 0
+                assert _lib.workspace_bytes(op, B, T, N, d, K, io, True) == rms
+            elif op == _lib.OP_FORWARD:
+                assert "strip path" in why
+    finally:
+        _lib.set_path("auto")
     lib = _lib.library()
-    assert lib.hsn_win_set_path(3) == 1 and b"path" in lib.hsn_win_last_error()
+    assert lib.hsn_win_set_path(4) == 1 and b"path" in lib.hsn_win_last_error()
 
 
 def test_forward_rejects_a_short_workspace_without_a_gpu():
