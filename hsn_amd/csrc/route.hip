@@ -623,6 +623,63 @@ __device__ void decide_sorted(const RouteArgs& a, int b, int p, uint4* ent, uint
     }
 }
 
+// The slot table's budget, threshold and outputs (steps 4 and on of decide_select): `tab` holds
+// the K slots in the selection's order, `pool` / `pool_nan` theta's highest unselected score
+// over the cells outside the table.
+template <bool kOne, typename IDX>
+__device__ __forceinline__ void finish_select(const RouteArgs& a, int b, int p, const uint4* tab,
+                                              int32_t pool, bool pool_nan, float cost0) {
+    const int lane = lane_id();
+    const int K = a.K, R = a.reserved, M = a.M;
+    (void)M;
+    __builtin_amdgcn_wave_barrier();  // the slot table's writes before its reads
+    const bool is_slot = lane < K;
+    const uint4 e = is_slot ? tab[lane] : make_uint4(0u, 0u, 0u, 0u);
+    const int my_cell = static_cast<int>(e.y);
+    const float my_score = __uint_as_float(e.z);
+
+    // 4. the budget (as decide)
+    int my_unit = 0;
+    float cumulative;
+    if constexpr (kOne) {
+        const float ps = add_rn(a.overhead, cost0);
+        cumulative = add_rn(a.shared, static_cast<float>(static_cast<double>(ps) * (lane + 1)));
+    } else {
+        my_unit = (a.fixed_units && lane < R) ? lane % M : static_cast<int>(e.w);
+        const float my_cost = is_slot ? a.cost[my_unit] : 0.0f;
+        const float per_slot = is_slot ? add_rn(a.overhead, my_cost) : 0.0f;
+        double acc = 0.0;
+        for (int j = 0; j < K; ++j) {
+            const float v = readlane(per_slot, j);
+            if (j <= lane) acc += static_cast<double>(v);
+        }
+        cumulative = add_rn(a.shared, static_cast<float>(acc));
+    }
+    const bool ok = is_slot && cumulative <= a.limit;
+
+    // the threshold: the lowest selected scored slot, the highest unselected cell (the pool and
+    // the table's slots past the budget)
+    const bool in_low = ok && my_cell >= R;
+    const float low = wave_amin_k(in_low ? ford(my_score) : ford(INFINITY), in_low && my_score != my_score);
+    const bool cut = is_slot && !ok;
+    const int32_t hk = max(pool, cut ? ford(my_score) : ford(-INFINITY));
+    const float high = wave_amax_k(hk, pool_nan | (cut && my_score != my_score));
+    const float th = 0.5f * (low + high);
+
+    if (is_slot) {
+        const int64_t o = b * a.o_row + p * a.o_pos + lane;
+        store_index<IDX>(a.cells, o, ok ? my_cell : 0);
+        store_index<IDX>(a.units, o, ok ? my_unit : 0);
+        a.valid[o] = ok ? 1 : 0;
+        a.refreshed[o] = 0;
+        if (a.slots) a.slots[o] = ok ? my_cell : -1;
+    }
+    if (lane == 0) {
+        a.theta[b * a.th_row + p * a.th_pos] = th;
+        if (a.h_max_zero) a.h_max_zero[static_cast<int64_t>(b) * a.P + p] = 0.0f;
+    }
+}
+
 // The decision of one position without probes, any NPL: a threshold, then an exact order of
 // the few cells at or above it.
 //  1. Every lane's largest key; L = the largest 16-bit key prefix that at least Kc = K + 1 (K
@@ -823,52 +880,185 @@ __device__ void decide_select(const RouteArgs& a, int b, int p, uint4* cand, uin
             pool_nan = pool_nan | (out & (si != si));
         }
     }
-    __builtin_amdgcn_wave_barrier();  // the slot table's writes before its reads
-    const bool is_slot = lane < K;
-    const uint4 e = is_slot ? tab[lane] : make_uint4(0u, 0u, 0u, 0u);
-    const int my_cell = static_cast<int>(e.y);
-    const float my_score = __uint_as_float(e.z);
+    finish_select<kOne, IDX>(a, b, p, tab, pool, pool_nan, cost0);
+}
 
-    // 4. the budget (as decide)
-    int my_unit = 0;
-    float cumulative;
-    if constexpr (kOne) {
-        const float ps = add_rn(a.overhead, cost0);
-        cumulative = add_rn(a.shared, static_cast<float>(static_cast<double>(ps) * (lane + 1)));
-    } else {
-        my_unit = (a.fixed_units && lane < R) ? lane % M : static_cast<int>(e.w);
-        const float my_cost = is_slot ? a.cost[my_unit] : 0.0f;
-        const float per_slot = is_slot ? add_rn(a.overhead, my_cost) : 0.0f;
-        double acc = 0.0;
-        for (int j = 0; j < K; ++j) {
-            const float v = readlane(per_slot, j);
-            if (j <= lane) acc += static_cast<double>(v);
+// The decision of one position without probes for one unit and wide rows (NPL >= 16): the
+// selection of decide_select with every key recomputed from the lane's packed logits where a pass
+// needs it instead of held in registers (a key and a logit per cell would take two registers per
+// cell: at N = 4096 more than one wavefront's share of a SIMD), and the heavy-ties path's taken
+// cells in a bit mask. kUni: every lane full, no reserved cells, no cost term (the key of a cell
+// is its logit's).
+template <int NPL, bool kUni, typename IO, typename IDX>
+__device__ void decide_lean_body(const RouteArgs& a, int b, int p, uint4* cand, uint4* tab,
+                                 uint64_t* ord) {
+    static_assert(NPL >= 16 && NPL <= 64, "NPL");
+    constexpr int kW = NPL * static_cast<int>(sizeof(IO)) / 4;  // packed words per lane
+    static_assert(kW % 4 == 0, "whole 16-byte loads");
+    const int lane = lane_id();
+    const int N = a.N, K = a.K, R = a.reserved;
+    const IO* logits = static_cast<const IO*>(a.logits) + b * a.l_row + p * a.l_pos;
+    const bool scale_cost = a.lambda > 0.0f;
+    const float cost0 = a.cost[0];
+    const float lc = scale_cost ? mul_rn(a.lambda, cost0) : 0.0f;
+    const int n0 = lane * NPL;
+    uint32_t w[kW];
+    {
+        constexpr uint32_t kRun = NPL * sizeof(IO);
+        const bool vec = a.width == 1 && N % NPL == 0 &&
+                         (reinterpret_cast<uintptr_t>(logits) & 15) == 0;
+        if (vec) {  // lanes past the row read zeros (kOob); their cells are masked below
+            const rsrc_t r = make_rsrc(logits, uint32_t(N) * sizeof(IO));
+            const uint32_t vo = n0 < N ? uint32_t(lane) * kRun : kOob;
+#pragma unroll
+            for (int c = 0; c < kW / 4; ++c) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, vo + 16u * c, 0, 0);
+                __builtin_memcpy(&w[4 * c], &v, 16);
+            }
+        } else {
+            IO raw[NPL];
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) raw[i] = logits[int64_t(min(n0 + i, N - 1)) * a.width];
+            __builtin_memcpy(w, raw, sizeof(raw));
         }
-        cumulative = add_rn(a.shared, static_cast<float>(acc));
     }
-    const bool ok = is_slot && cumulative <= a.limit;
+    auto val = [&](int i) __attribute__((always_inline)) -> float {
+        if constexpr (sizeof(IO) == 4) return __uint_as_float(w[i]);
+        else return __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+    };
+    auto score = [&](int i) __attribute__((always_inline)) -> float {
+        const float v = val(i);
+        return scale_cost ? sub_rn(v, lc) : v;
+    };
+    const int n_in = min(max(N - n0, 0), NPL), n_rsv = min(max(R - n0, 0), NPL);
+    auto key = [&](int i) __attribute__((always_inline)) -> uint32_t {
+        if constexpr (kUni) {
+            return score_key(val(i));
+        } else {
+            const uint32_t in = 0u - static_cast<uint32_t>(i < n_in);
+            const uint32_t rsv = 0u - static_cast<uint32_t>(i < n_rsv);
+            return ((score_key(score(i)) & ~rsv) | (kKeyPosInf & rsv)) & in;
+        }
+    };
 
-    // the threshold: the lowest selected scored slot, the highest unselected cell (the pool and
-    // the table's slots past the budget)
-    const bool in_low = ok && my_cell >= R;
-    const float low = wave_amin_k(in_low ? ford(my_score) : ford(INFINITY), in_low && my_score != my_score);
-    const bool cut = is_slot && !ok;
-    const int32_t hk = max(pool, cut ? ford(my_score) : ford(-INFINITY));
-    const float high = wave_amax_k(hk, pool_nan | (cut && my_score != my_score));
-    const float th = 0.5f * (low + high);
+    // the words may change at each block of 16 cells (an empty asm): the compiler computes a
+    // block's keys within the block instead of all of them up front
+    auto fence = [&](int i) __attribute__((always_inline)) {
+        if ((i & 15) == 0) {
+#pragma unroll
+            for (int c = 0; c < kW; ++c) asm volatile("" : "+v"(w[c]));
+        }
+    };
+    // 1. the threshold prefix from the lanes' maxima
+    uint32_t hb = 0u;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        fence(i);
+        hb = umax(hb, key(i));
+    }
+    const int Kc = K < N ? K + 1 : K;
+    const uint32_t top = hb >> 16;
+    uint32_t pfx = 0u;
+#pragma unroll
+    for (int bit = 15; bit >= 0; --bit) {
+        const uint32_t c = pfx | (1u << bit);
+        pfx = __popcll(ballot(top >= c)) >= Kc ? c : pfx;
+    }
+    const uint32_t L = pfx > 0u ? pfx << 16 : 1u;  // 1: every real key (a cell past N has key 0)
 
-    if (is_slot) {
-        const int64_t o = b * a.o_row + p * a.o_pos + lane;
-        store_index<IDX>(a.cells, o, ok ? my_cell : 0);
-        store_index<IDX>(a.units, o, ok ? my_unit : 0);
-        a.valid[o] = ok ? 1 : 0;
-        a.refreshed[o] = 0;
-        if (a.slots) a.slots[o] = ok ? my_cell : -1;
+    // 2. the candidates into LDS, and the largest key below L (the keys computed again)
+    uint32_t below = 0u;
+    int C = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        fence(i);
+        const uint32_t k = key(i);
+        const bool c = k >= L;
+        below = umax(below, c ? 0u : k);
+        const uint64_t m = ballot(c);
+        if (m != 0u) {  // uniform
+            const int at = C + lanes_below(m);
+            if (c && at < kWave) {
+                const uint32_t n = uint32_t(n0 + i);
+                cand[at] = make_uint4(k, n, __float_as_uint(score(i)), 0u);
+                ord[at] = (uint64_t(k) << 32) | ~n;  // the selection's order as one integer
+            }
+            C += __popcll(m);
+        }
     }
-    if (lane == 0) {
-        a.theta[b * a.th_row + p * a.th_pos] = th;
-        if (a.h_max_zero) a.h_max_zero[static_cast<int64_t>(b) * a.P + p] = 0.0f;
+    int32_t pool;
+    bool pool_nan;
+    if (C <= kWave) {
+        __builtin_amdgcn_wave_barrier();  // the candidates' writes before their reads
+        const bool is_c = lane < C;
+        const uint4 me = is_c ? cand[lane] : make_uint4(0u, 0xffffffffu, 0u, 0u);
+        // 3. each candidate's place in the selection's order (as decide_select)
+        const uint64_t mine = (uint64_t(me.x) << 32) | ~me.y;
+        if (lane >= C) ord[lane] = 0u;
+        __builtin_amdgcn_wave_barrier();
+        int rank = 0;
+        for (int j = 0; j < C; j = uniform(j + 4)) {
+            const uint64_t o0 = ord[j], o1 = ord[j + 1], o2 = ord[j + 2], o3 = ord[j + 3];
+            rank += static_cast<int>(o0 > mine) + static_cast<int>(o1 > mine) +
+                    static_cast<int>(o2 > mine) + static_cast<int>(o3 > mine);
+        }
+        if (is_c && rank < K) tab[rank] = me;
+        const bool out = is_c && rank >= K;
+        const float cs = __uint_as_float(me.z);
+        pool = max(out ? ford(cs) : ford(-INFINITY), below != 0u ? ford(key_score(below)) : ford(-INFINITY));
+        pool_nan = out && cs != cs;
+    } else {
+        // Heavy ties: K rounds of a wavefront argmax (as decide_select), the lane's best among
+        // its cells not yet taken found by a pass over its keys
+        uint64_t taken = 0ull;
+        uint32_t bk = 0u;
+        int bi = 0;
+        float bs = 0.0f;
+        auto best = [&]() __attribute__((always_inline)) {
+            bk = 0u;
+            bi = 0;
+            bs = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NPL; ++i) {
+                fence(i);
+                const uint32_t k = ((taken >> i) & 1ull) ? 0u : key(i);
+                const bool gt = k > bk;
+                bk = gt ? k : bk;
+                bi = gt ? i : bi;
+                bs = gt ? score(i) : bs;
+            }
+        };
+        best();
+        for (int r = 0; r < K; r = uniform(r + 1)) {
+            const uint32_t wk = wave_reduce_u32(bk, [](uint32_t x, uint32_t y) { return x > y ? x : y; }, 0u);
+            const int src = __builtin_ctzll(ballot(bk == wk));
+            if (lane == src) {
+                tab[r] = make_uint4(bk, uint32_t(n0 + bi), __float_as_uint(bs), 0u);
+                taken |= 1ull << bi;
+                best();
+            }
+        }
+        pool = ford(-INFINITY);
+        pool_nan = false;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {  // every real cell still in the pool
+            fence(i);
+            const bool out = i < n_in && !((taken >> i) & 1ull);
+            const float si = score(i);
+            pool = max(pool, out ? ford(si) : ford(-INFINITY));
+            pool_nan = pool_nan | (out & (si != si));
+        }
     }
+    finish_select<true, IDX>(a, b, p, tab, pool, pool_nan, cost0);
+}
+
+template <int NPL, typename IO, typename IDX>
+__device__ __forceinline__ void decide_lean(const RouteArgs& a, int b, int p, uint4* cand,
+                                            uint4* tab, uint64_t* ord) {
+    if (a.N == kWave * NPL && a.reserved == 0 && !(a.lambda > 0.0f))
+        decide_lean_body<NPL, true, IO, IDX>(a, b, p, cand, tab, ord);
+    else
+        decide_lean_body<NPL, false, IO, IDX>(a, b, p, cand, tab, ord);
 }
 
 // Whole window without probes: a wavefront per (row, position), four per workgroup; kOne
@@ -882,7 +1072,10 @@ __global__ __launch_bounds__(256) void route_parallel(RouteArgs a) {
     __shared__ uint4 cand[4][kWave];
     __shared__ uint4 tab[4][kWave];
     __shared__ uint64_t ord[4][kWave + 4];
-    decide_select<NPL, kOne, IO, IDX>(a, b, p, cand[wv], tab[wv], ord[wv]);
+    if constexpr (kOne && NPL >= 16)
+        decide_lean<NPL, IO, IDX>(a, b, p, cand[wv], tab[wv], ord[wv]);
+    else
+        decide_select<NPL, kOne, IO, IDX>(a, b, p, cand[wv], tab[wv], ord[wv]);
 }
 
 // With probes (or the per-position form): one wavefront walks a row's positions in order.
