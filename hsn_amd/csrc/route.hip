@@ -1078,6 +1078,211 @@ __global__ __launch_bounds__(256) void route_parallel(RouteArgs a) {
         decide_select<NPL, kOne, IO, IDX>(a, b, p, cand[wv], tab[wv], ord[wv]);
 }
 
+// Whole window without probes, one unit, a workgroup per (row, position) for rows too wide for a
+// wavefront's registers (N > 1024): 256 threads of CPT consecutive cells each (thread t holds
+// cells t*CPT ..), the selection of decide_select across the workgroup:
+//  1. every thread's largest key into LDS; L, the largest 16-bit key prefix that at least Kc of
+//     the 256 thread maxima reach (each wavefront computes it from the same 256 values);
+//  2. each wavefront compacts its cells with key >= L into its own LDS segment;
+//  3. wavefront 0 ranks the candidates (at most 64 in all) and finishes as decide_select; more
+//     than 64 (heavy ties) take K rounds of a workgroup argmax (the largest key, the lowest cell:
+//     the first wavefront, lane and cell holding it).
+template <int CPT, typename IO, typename IDX>
+__global__ __launch_bounds__(256) void route_block(RouteArgs a) {
+    static_assert(CPT >= 1 && CPT <= 16, "CPT");
+    constexpr int kT = 256, kWv = kT / kWave;
+    constexpr int kW = (CPT * static_cast<int>(sizeof(IO)) + 3) / 4;  // packed words per thread
+    __shared__ uint32_t smax[kT];
+    __shared__ uint4 cand[kWv][kWave];
+    __shared__ uint64_t ord[kWave + 4];
+    __shared__ uint4 tab[kWave];
+    __shared__ int wcnt[kWv];
+    __shared__ uint32_t wbelow[kWv];
+    __shared__ uint4 wbest[kWv];
+    __shared__ int32_t wpool[kWv];
+    __shared__ int wnan[kWv];
+    const int p = blockIdx.x, b = blockIdx.y;
+    const int tid = threadIdx.x, lane = lane_id(), wv = uniform(tid / kWave);
+    const int N = a.N, K = a.K, R = a.reserved;
+    const IO* logits = static_cast<const IO*>(a.logits) + b * a.l_row + p * a.l_pos;
+    const bool scale_cost = a.lambda > 0.0f;
+    const float cost0 = a.cost[0];
+    const float lc = scale_cost ? mul_rn(a.lambda, cost0) : 0.0f;
+    const int n0 = tid * CPT;
+    uint32_t w[kW];
+    {
+        constexpr uint32_t kRun = CPT * sizeof(IO);
+        const bool vec = kRun % 16 == 0 && a.width == 1 && N % CPT == 0 &&
+                         (reinterpret_cast<uintptr_t>(logits) & 15) == 0;
+        if (vec) {  // threads past the row read zeros (kOob); their cells are masked below
+            const rsrc_t r = make_rsrc(logits, uint32_t(N) * sizeof(IO));
+            const uint32_t vo = n0 < N ? uint32_t(tid) * kRun : kOob;
+#pragma unroll
+            for (int c = 0; c < kW / 4; ++c) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, vo + 16u * c, 0, 0);
+                __builtin_memcpy(&w[4 * c], &v, 16);
+            }
+        } else {
+            IO raw[kW * 4 / sizeof(IO)] = {};
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) raw[i] = logits[int64_t(min(n0 + i, N - 1)) * a.width];
+            __builtin_memcpy(w, raw, kW * 4);
+        }
+    }
+    auto score = [&](int i) __attribute__((always_inline)) -> float {
+        float v;
+        if constexpr (sizeof(IO) == 4) v = __uint_as_float(w[i]);
+        else v = __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+        return scale_cost ? sub_rn(v, lc) : v;
+    };
+    const int n_in = min(max(N - n0, 0), CPT), n_rsv = min(max(R - n0, 0), CPT);
+    uint32_t key[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const uint32_t in = 0u - static_cast<uint32_t>(i < n_in);
+        const uint32_t rsv = 0u - static_cast<uint32_t>(i < n_rsv);
+        key[i] = ((score_key(score(i)) & ~rsv) | (kKeyPosInf & rsv)) & in;
+    }
+
+    // 1. the threshold prefix from the threads' maxima
+    uint32_t hb = 0u;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) hb = umax(hb, key[i]);
+    smax[tid] = hb >> 16;
+    __syncthreads();
+    const int Kc = K < N ? K + 1 : K;
+    uint32_t tops[kWv];
+#pragma unroll
+    for (int j = 0; j < kWv; ++j) tops[j] = smax[lane + kWave * j];
+    uint32_t pfx = 0u;
+#pragma unroll
+    for (int bit = 15; bit >= 0; --bit) {
+        const uint32_t c = pfx | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < kWv; ++j) cnt += __popcll(ballot(tops[j] >= c));
+        pfx = cnt >= Kc ? c : pfx;
+    }
+    const uint32_t L = pfx > 0u ? pfx << 16 : 1u;
+
+    // 2. each wavefront's candidates into its LDS segment, and its largest key below L
+    uint32_t below = 0u;
+    int C = 0;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const bool c = key[i] >= L;
+        below = umax(below, c ? 0u : key[i]);
+        const uint64_t m = ballot(c);
+        if (m != 0u) {  // uniform
+            const int at = C + lanes_below(m);
+            if (c && at < kWave)
+                cand[wv][at] = make_uint4(key[i], uint32_t(n0 + i), __float_as_uint(score(i)), 0u);
+            C += __popcll(m);
+        }
+    }
+    below = wave_reduce_u32(below, [](uint32_t x, uint32_t y) { return x > y ? x : y; }, 0u);
+    if (lane == 0) {
+        wcnt[wv] = C;
+        wbelow[wv] = below;
+    }
+    __syncthreads();
+    int Ct = 0;
+    uint32_t bel = 0u;
+#pragma unroll
+    for (int j = 0; j < kWv; ++j) {
+        Ct += wcnt[j];
+        bel = umax(bel, wbelow[j]);
+    }
+    if (Ct <= kWave) {
+        if (wv != 0) return;
+        // 3. wavefront 0: candidate `lane` from the segments, its place in the selection's order
+        int seg = 0, base = 0, off = 0;  // the segment holding candidate `lane`, its start
+#pragma unroll
+        for (int j = 0; j + 1 < kWv; ++j) {
+            off += wcnt[j];  // the start of segment j + 1 (the starts never decrease)
+            const bool past = lane >= off;
+            seg = past ? j + 1 : seg;
+            base = past ? off : base;
+        }
+        const bool is_c = lane < Ct;
+        const uint4 me = is_c ? cand[seg][lane - base] : make_uint4(0u, 0xffffffffu, 0u, 0u);
+        const uint64_t mine = (uint64_t(me.x) << 32) | ~me.y;
+        ord[lane] = is_c ? mine : 0u;
+        __builtin_amdgcn_wave_barrier();
+        int rank = 0;
+        for (int j = 0; j < Ct; j = uniform(j + 4)) {
+            const uint64_t o0 = ord[j], o1 = ord[j + 1], o2 = ord[j + 2], o3 = ord[j + 3];
+            rank += static_cast<int>(o0 > mine) + static_cast<int>(o1 > mine) +
+                    static_cast<int>(o2 > mine) + static_cast<int>(o3 > mine);
+        }
+        if (is_c && rank < K) tab[rank] = me;
+        const bool out = is_c && rank >= K;
+        const float cs = __uint_as_float(me.z);
+        const int32_t pool = max(out ? ford(cs) : ford(-INFINITY),
+                                 bel != 0u ? ford(key_score(bel)) : ford(-INFINITY));
+        finish_select<true, IDX>(a, b, p, tab, pool, out && cs != cs, cost0);
+        return;
+    }
+    // heavy ties: K rounds of a workgroup argmax, the taken cells in a bit mask
+    uint32_t taken = 0u;
+    for (int r = 0; r < K; ++r) {
+        uint32_t bk = 0u;
+        int bi = 0;
+        float bs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const uint32_t k = ((taken >> i) & 1u) ? 0u : key[i];
+            const bool gt = k > bk;
+            bk = gt ? k : bk;
+            bi = gt ? i : bi;
+            bs = gt ? score(i) : bs;
+        }
+        const uint32_t wk = wave_reduce_u32(bk, [](uint32_t x, uint32_t y) { return x > y ? x : y; }, 0u);
+        const int src = __builtin_ctzll(ballot(bk == wk));
+        if (lane == src) wbest[wv] = make_uint4(wk, uint32_t(n0 + bi), __float_as_uint(bs), 0u);
+        __syncthreads();
+        int wsel = 0;
+        uint32_t kmax = wbest[0].x;
+#pragma unroll
+        for (int j = 1; j < kWv; ++j) {
+            const bool gt = wbest[j].x > kmax;  // equal keys: the earlier wavefront (lower cells)
+            kmax = gt ? wbest[j].x : kmax;
+            wsel = gt ? j : wsel;
+        }
+        if (wv == wsel && lane == src) taken |= 1u << bi;
+        if (tid == 0) tab[r] = wbest[wsel];
+        __syncthreads();
+    }
+    int32_t pk = ford(-INFINITY);
+    bool pn = false;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {  // every real cell still in the pool
+        const bool out = i < n_in && !((taken >> i) & 1u);
+        const float si = score(i);
+        pk = max(pk, out ? ford(si) : ford(-INFINITY));
+        pn = pn | (out & (si != si));
+    }
+    pk = static_cast<int32_t>(wave_reduce_u32(
+        static_cast<uint32_t>(pk),
+        [](uint32_t x, uint32_t y) { return static_cast<int32_t>(x) > static_cast<int32_t>(y) ? x : y; },
+        static_cast<uint32_t>(ford(-INFINITY))));
+    const bool wn = ballot(pn) != 0u;
+    if (lane == 0) {
+        wpool[wv] = pk;
+        wnan[wv] = wn ? 1 : 0;
+    }
+    __syncthreads();
+    if (wv != 0) return;
+    int32_t pool = wpool[0];
+    bool pool_nan = wnan[0] != 0;
+#pragma unroll
+    for (int j = 1; j < kWv; ++j) {
+        pool = max(pool, wpool[j]);
+        pool_nan = pool_nan || wnan[j] != 0;
+    }
+    finish_select<true, IDX>(a, b, p, tab, pool, pool_nan, cost0);
+}
+
 // With probes (or the per-position form): one wavefront walks a row's positions in order.
 // Window form (a.age0): ages start at age0, a reset at p zeroes them before p reads them, and
 // each decision ticks them. Per-position form (a.age): the ages of record a.age_rec, P = 1.
@@ -1108,6 +1313,10 @@ __global__ __launch_bounds__(64) void route_sequential(RouteArgs a) {
 template <typename IO, typename IDX>
 hipError_t launch_route(const RouteArgs& a, bool sequential, hipStream_t stream) {
     const int npl = (a.N + kWave - 1) / kWave;
+    if (!sequential && a.M == 1 && a.N > 1024) {  // a workgroup per position (N <= 4096)
+        hipLaunchKernelGGL((route_block<16, IO, IDX>), dim3(a.P, a.B), dim3(256), 0, stream, a);
+        return hipGetLastError();
+    }
 #define HSN_ROUTE_CASE(V)                                                                      \
     if (npl <= V) {                                                                            \
         if (sequential) {                                                                      \

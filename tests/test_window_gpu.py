@@ -113,7 +113,7 @@ ROUTE_CASES = [
     (2, 4, 130, 1, 8, dict(lambda_cost=0.05), torch.float32, "ties"),
     (2, 4, 100, 1, 6, dict(reserved=2), torch.bfloat16, "nan"),
     (2, 3, 200, 1, 8, dict(), torch.bfloat16, "plain"),
-    # one unit, eight or more cells a lane (keys recomputed from the logits in each pass): a row
+    # one unit, sixteen or more cells a lane (keys recomputed from the logits in each pass): a row
     # not a multiple of the lane block (scalar loads) with half-integer ties; reserved cells with
     # a cost term and NaN / inf; every logit +-0 (more than 64 candidates: the argmax rounds);
     # fp32 at 4096 cells and 64 slots
@@ -121,6 +121,10 @@ ROUTE_CASES = [
     (2, 3, 1000, 1, 16, dict(reserved=3, lambda_cost=0.05), torch.bfloat16, "nan"),
     (2, 2, 512, 1, 20, dict(limit=0.7), torch.float32, "zeros"),
     (1, 2, 4096, 1, 64, dict(), torch.float32, "ties"),
+    # one unit, more than 1024 cells (a workgroup per position): a partial last block with
+    # reserved cells, a cost term and NaN / inf; every logit +-0 across the four wavefronts
+    (2, 3, 2000, 1, 24, dict(reserved=4, lambda_cost=0.05), torch.bfloat16, "nan"),
+    (1, 2, 3000, 1, 16, dict(limit=0.6), torch.float32, "zeros"),
 ]
 
 
