@@ -25,6 +25,8 @@ import sys
 import time
 from pathlib import Path
 
+import numpy as np
+
 ROOT = Path(__file__).resolve().parent
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
@@ -53,7 +55,22 @@ def _args():
                    help="skip the graph capture and its replays")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="repeat the CPU baseline's sample until this much time has passed")
+    p.add_argument("--trainer", choices=sorted(TRAINER_LISTS), default=None,
+                   help="measure the trainer's AdamW pass (hsn_tr_adamw) over a synthetic "
+                        "parameter list instead of the window (not the headline line)")
     return p.parse_args()
+
+
+#: Synthetic parameter lists for ``--trainer``: (tensor sizes, what they stand for). "model" is
+#: the size of the reference's trained models (about 2 M parameters: weights, biases, gains);
+#: "large" 256 M parameters in 64 tensors, where the pass is HBM-bound.
+TRAINER_LISTS = {
+    "model": ([64 * 64] * 48 + [256 * 64] * 96 + [64] * 48 + [256 * 128] * 6, "1.97 M in 198"),
+    "large": ([1 << 22] * 64, "256 M in 64"),
+}
+#: Algorithmic HBM bytes per element of the AdamW pass: reads param, grad, exp_avg, exp_avg_sq
+#: and writes param, exp_avg, exp_avg_sq, 4 bytes each.
+TRAINER_BYTES_PER_ELEMENT = 28
 
 
 def _traffic(workload: str):
@@ -112,6 +129,125 @@ def _cpu_baseline(cfg, seed, min_seconds):
     }
 
 
+def _trainer_main(args) -> int:
+    """The AdamW pass (``hsn_tr_adamw``) against the PyTorch multi-tensor sequence it replaces
+    (the reference's ``LazyAdamW._dense_steps``) over one synthetic parameter list, on the same
+    device. A step is one optimiser step over the whole list; ``value`` is elements/s of the
+    pass (eager launches, host work included); the roofline is the pass's kernel time from HIP
+    events on its stream (the launches queued behind device copies so they run back to back)."""
+    import torch
+
+    from hsn_amd import trainer
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    sizes, what = TRAINER_LISTS[args.trainer]
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+
+    def make():
+        return [torch.randn(n, device=dev, generator=gen) for n in sizes]
+
+    params, grads, exp_avgs = make(), make(), make()
+    exp_avg_sqs = [g.square() for g in make()]
+    hyper = dict(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01)
+    elements = sum(sizes)
+
+    def pass_step(step):
+        assert trainer.adamw(params, grads, exp_avgs, exp_avg_sqs, step=step, **hyper)
+
+    def torch_step(step):
+        lr, b1, b2 = hyper["lr"], hyper["beta1"], hyper["beta2"]
+        torch._foreach_mul_(params, 1 - lr * hyper["weight_decay"])
+        torch._foreach_lerp_(exp_avgs, grads, 1 - b1)
+        torch._foreach_mul_(exp_avg_sqs, b2)
+        torch._foreach_addcmul_(exp_avg_sqs, grads, grads, value=1 - b2)
+        denoms = torch._foreach_sqrt(exp_avg_sqs)
+        torch._foreach_div_(denoms, (1 - b2**step) ** 0.5)
+        torch._foreach_add_(denoms, hyper["eps"])
+        torch._foreach_addcdiv_(params, exp_avgs, denoms, value=-lr / (1 - b1**step))
+
+    def timed(fn):
+        for i in range(args.warmup):
+            fn(i + 1)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            fn(args.warmup + i + 1)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / args.steps
+
+    pass_secs = timed(pass_step)
+    torch_secs = timed(torch_step)
+    busy = torch.empty(64 << 20, device=dev)
+    busy_dst = torch.empty_like(busy)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for _ in range(args.steps + 8):
+        busy_dst.copy_(busy)
+    for i, (a, b) in enumerate(events):
+        a.record()
+        pass_step(i + 1)
+        b.record()
+    torch.cuda.synchronize()
+    kernel_ms = sum(a.elapsed_time(b) for a, b in events) / args.steps
+    achieved = elements * TRAINER_BYTES_PER_ELEMENT / (kernel_ms * 1e-3) / 1e9
+    launches = -(-len([n for n in sizes if n]) // 48)
+    result = {
+        "metric": f"trainer AdamW pass elements/sec ({args.trainer} parameter list, 1 GPU)",
+        "value": elements / pass_secs,
+        "unit": "elements/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": pass_secs * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded normal parameters, gradients and moments)",
+        "config": {"workload": f"trainer_adamw_{args.trainer}", "tensors": len(sizes),
+                   "elements": elements, "list": what, "launches_per_step": launches,
+                   "parallelism": "single GPU"},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "tr_pass<kAdamW>",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+        },
+        "kernel_ms": kernel_ms,
+        "torch_foreach_ms_per_step": torch_secs * 1e3,
+        "speedup_vs_torch_foreach": torch_secs / pass_secs,
+    }
+    if not args.no_cpu:  # the oracle's restatement on a bounded sample, one host thread
+        from oracle import hsn_oracle as O
+
+        rng = np.random.default_rng(args.seed)
+        n = 1 << 20
+        p, g, m = (rng.standard_normal(n).astype(np.float32) for _ in range(3))
+        v = np.square(rng.standard_normal(n)).astype(np.float32)
+        coefs = [1 - 1e-5, 0.1, 0.999, 0.001, 1 / 0.001**0.5, 1e-8, -1e-2]
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            p, m, v = O.tr_adamw(p, g, m, v, coefs, True)
+            reps += 1
+            secs = time.perf_counter() - t0
+            if secs >= args.cpu_seconds:
+                break
+        result["cpu_baseline"] = {
+            "value": n * reps / secs, "unit": "elements/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} x AdamW over {n} elements, the repository's numpy oracle "
+                      f"({secs:.1f} s)",
+        }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     args = _args()
     if args.gpus != 1:
@@ -119,6 +255,8 @@ def main() -> int:
               "shards over rows (each GPU owns whole rows, no exchange), so one GPU's rate "
               "times N is the job's", file=sys.stderr)
         return 2
+    if args.trainer:
+        return _trainer_main(args)
     import torch
 
     from hsn_amd import window

@@ -1,4 +1,5 @@
-"""The C ABI of ``libhsn_amd.so`` (``include/hsn_window.h``, ``include/hsn_ops.h``) via ctypes.
+"""The C ABI of ``libhsn_amd.so`` (``include/hsn_window.h``, ``include/hsn_ops.h``,
+``include/hsn_trainer.h``) via ctypes.
 
 The library is the product: every operator in :mod:`hsn_amd` reaches the GPU through these
 entry points, and nothing here falls back to another implementation. :func:`library` raises a
@@ -60,6 +61,13 @@ SIGNATURES: dict[str, list] = {
     "hsn_csr_messages_bwd": [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, I, P],
     "hsn_gated_delta_update": [P, P, P, P, P, P, P, P, I, I, I, I, I, P],
     "hsn_gated_delta_update_bwd": [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P],
+    "hsn_tr_adamw": [P, P, P, P, P, I, I, P, P],
+    "hsn_tr_adamw_units": [P, P, P, P, P, I, I, I, P, F, F, P],
+    "hsn_tr_lerp": [P, P, P, I, F, P],
+    "hsn_tr_scale64": [P, P, I, P, P],
+    "hsn_tr_copy": [P, P, P, I, P],
+    "hsn_tr_limit_squares": [P, P, P, P, P, I, P],
+    "hsn_tr_limit_project": [P, P, P, P, P, I, P],
 }
 
 _lock = threading.Lock()

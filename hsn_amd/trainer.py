@@ -1,0 +1,229 @@
+"""The trainer's per-step passes after ``backward()`` as single launches on MI355X
+(``include/hsn_trainer.h``; the reference's ``python/hsn/kernels/trainer.py``).
+
+The optimiser step (``hsn.train.lazy_adam``), the float64 clip's scaling (``grad_norm``), the
+update caps (``update_limit``) and the weight average (``weight_ema``) each walk a list of tensors
+with a few elementwise operations; here each is one pass over the whole list. Same functions,
+arguments and return convention as the reference: ``True`` when the pass ran, ``False`` when it did
+not, having touched nothing (the tensors are not contiguous fp32 tensors on one ROCm device, the
+list is empty, or the passes are switched off by :func:`set_enabled` or ``HSN_TRAINER_KERNELS=0``);
+the caller then runs its PyTorch operations, which each pass equals bit for bit. A missing or stale
+HIP library raises (there is no other implementation here).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from collections.abc import Sequence
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+__all__ = [
+    "MAX_UNITS",
+    "adamw",
+    "adamw_units",
+    "copy",
+    "enabled",
+    "lerp",
+    "limit_project",
+    "limit_squares",
+    "ready",
+    "scale64",
+    "set_enabled",
+]
+
+#: The most units a stacked unit tensor may have (reference ``HSN_TR_UNITS``).
+MAX_UNITS = 64
+
+_enabled = os.environ.get("HSN_TRAINER_KERNELS", "1") != "0"
+
+
+def set_enabled(flag: bool) -> bool:
+    """Switch the passes on or off for this process; returns the previous setting."""
+    global _enabled
+    previous = _enabled
+    _enabled = bool(flag)
+    return previous
+
+
+def enabled() -> bool:
+    return _enabled
+
+
+def ready(device: torch.device) -> bool:
+    """Whether the passes run on ``device``: switched on and a ROCm device. The library must be
+    built and current (else ``RuntimeError``)."""
+    if not _enabled or device.type != "cuda":
+        return False
+    _lib.library()
+    return True
+
+
+def _fits(rows: Sequence[Sequence[Tensor]]) -> bool:
+    first = rows[0]
+    if not first or any(len(row) != len(first) for row in rows):
+        return False
+    device = first[0].device
+    for row in rows:
+        for t in row:
+            if t.dtype != torch.float32 or not t.is_contiguous() or t.device != device:
+                return False
+    for j, t in enumerate(first):
+        if any(row[j].numel() != t.numel() for row in rows):
+            return False
+    return ready(device)
+
+
+def _pointers(row: Sequence[Tensor]):
+    return (ctypes.c_void_p * len(row))(*[t.data_ptr() for t in row])
+
+
+def _numels(row: Sequence[Tensor]):
+    return (ctypes.c_int64 * len(row))(*[t.numel() for t in row])
+
+
+def adamw(
+    params: Sequence[Tensor],
+    grads: Sequence[Tensor],
+    exp_avgs: Sequence[Tensor],
+    exp_avg_sqs: Sequence[Tensor],
+    *,
+    lr: float,
+    beta1: float,
+    beta2: float,
+    eps: float,
+    weight_decay: float,
+    step: int,
+) -> bool:
+    """``LazyAdamW._dense_steps`` as one pass: the AdamW step of ordinary tensors at the step
+    count ``step`` (already advanced); the coefficients from the same host arithmetic (reference
+    ``python/hsn/kernels/trainer.py:111-144``)."""
+    rows = (params, grads, exp_avgs, exp_avg_sqs)
+    if not _fits(rows):
+        return False
+    bias_correction1 = 1 - beta1**step
+    bias_correction2 = 1 - beta2**step
+    step_size = lr / bias_correction1
+    bias_correction2_sqrt = bias_correction2**0.5
+    coefs = (ctypes.c_float * 7)(
+        1 - lr * weight_decay,
+        1 - beta1,
+        beta2,
+        1 - beta2,
+        1.0 / bias_correction2_sqrt,  # torch divides a tensor list by a scalar this way
+        eps,
+        -step_size,
+    )
+    device = params[0].device
+    _lib.call("hsn_tr_adamw", *[_pointers(r) for r in rows], _numels(params), len(params),
+              int(weight_decay != 0), coefs, _lib.stream_of(device))
+    return True
+
+
+def adamw_units(
+    params: Sequence[Tensor],
+    grads: Sequence[Tensor],
+    exp_avgs: Sequence[Tensor],
+    exp_avg_sqs: Sequence[Tensor],
+    *,
+    n_units: int,
+    active: Sequence[bool],
+    decay: Sequence[float],
+    lerp_weight: Sequence[float],
+    beta2_factor: Sequence[float],
+    bias_correction2_sqrt: Sequence[float],
+    step_size: Sequence[float],
+    beta2: float,
+    eps: float,
+    weight_decay: float,
+) -> bool:
+    """``LazyAdamW._unit_step`` as one pass for stacked unit tensors ``[n_units, ...]`` that
+    share their per-unit coefficients (each a sequence of ``n_units`` values: the coefficient
+    tensors of ``_unit_step``; reference ``trainer.py:147-191``)."""
+    rows = (params, grads, exp_avgs, exp_avg_sqs)
+    if n_units > MAX_UNITS or n_units < 1 or any(p.dim() == 0 or p.shape[0] != n_units for p in params):
+        return False
+    if not _fits(rows):
+        return False
+    table = [[1.0 if flag else 0.0 for flag in active], decay, lerp_weight, beta2_factor,
+             bias_correction2_sqrt, step_size]
+    if any(len(row) != n_units for row in table):
+        return False
+    coefs = (ctypes.c_float * (6 * n_units))(*[float(v) for row in table for v in row])
+    device = params[0].device
+    _lib.call("hsn_tr_adamw_units", *[_pointers(r) for r in rows], _numels(params), len(params),
+              n_units, int(weight_decay != 0), coefs, 1 - beta2, eps, _lib.stream_of(device))
+    return True
+
+
+def lerp(selfs: Sequence[Tensor], ends: Sequence[Tensor], weight: float) -> bool:
+    """``torch._foreach_lerp_(selfs, ends, weight)`` as one pass."""
+    if not _fits((selfs, ends)):
+        return False
+    _lib.call("hsn_tr_lerp", _pointers(selfs), _pointers(ends), _numels(selfs), len(selfs),
+              float(weight), _lib.stream_of(selfs[0].device))
+    return True
+
+
+def scale64(grads: Sequence[Tensor], coefficient: Tensor) -> bool:
+    """``grad.copy_((grad.double() * coefficient).float())`` for every gradient as one pass;
+    ``coefficient`` is a one-element float64 tensor on the gradients' device."""
+    if not _fits((grads,)):
+        return False
+    if (coefficient.dtype != torch.float64 or coefficient.numel() != 1
+            or coefficient.device != grads[0].device):
+        return False
+    _lib.call("hsn_tr_scale64", _pointers(grads), _numels(grads), len(grads),
+              coefficient.data_ptr(), _lib.stream_of(grads[0].device))
+    return True
+
+
+def copy(dsts: Sequence[Tensor], srcs: Sequence[Tensor]) -> bool:
+    """``torch._foreach_copy_(dsts, srcs)`` for fp32 tensors as one pass."""
+    if not _fits((dsts, srcs)):
+        return False
+    _lib.call("hsn_tr_copy", _pointers(dsts), _pointers(srcs), _numels(dsts), len(dsts),
+              _lib.stream_of(dsts[0].device))
+    return True
+
+
+def limit_squares(
+    params: Sequence[Tensor],
+    olds: Sequence[Tensor],
+    old_squares: Sequence[Tensor],
+    delta_squares: Sequence[Tensor],
+) -> bool:
+    """The squares ``UpdateLimiter.apply`` sums for its two norms: ``old ** 2`` and
+    ``(param - old) ** 2`` of every tensor, into the given buffers."""
+    rows = (params, olds, old_squares, delta_squares)
+    if not _fits(rows):
+        return False
+    _lib.call("hsn_tr_limit_squares", *[_pointers(r) for r in rows], _numels(params),
+              len(params), _lib.stream_of(params[0].device))
+    return True
+
+
+def limit_project(
+    params: Sequence[Tensor],
+    olds: Sequence[Tensor],
+    applied_squares: Sequence[Tensor],
+    groups: Sequence[Tensor],
+) -> bool:
+    """The projection of ``UpdateLimiter.apply``: ``param = old + (param - old) * scale`` on the
+    tensors of a clipped group (``groups[j]`` holds tensor ``j``'s group as two fp32 values on the
+    device, ``[scale, clipped]``), and the squares of the applied step ``(param - old) ** 2``."""
+    if len(groups) != len(params) or any(
+            g.dtype != torch.float32 or g.numel() != 2 or not g.is_contiguous() for g in groups):
+        return False
+    if not _fits((params, olds, applied_squares)):
+        return False
+    if any(g.device != params[0].device for g in groups):
+        return False
+    _lib.call("hsn_tr_limit_project", _pointers(params), _pointers(olds),
+              _pointers(applied_squares), _pointers(groups), _numels(params), len(params),
+              _lib.stream_of(params[0].device))
+    return True

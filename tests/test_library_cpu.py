@@ -29,7 +29,9 @@ def test_headers_declare_the_hot_path_entry_points():
                      "hsn_gated_delta_update", "hsn_gated_delta_update_bwd", "hsn_gather_concat",
                      "hsn_gather_concat_bwd", "hsn_grouped_unit_mlp_fwd",
                      "hsn_grouped_unit_mlp_bwd", "hsn_csr_messages", "hsn_csr_messages_bwd",
-                     "hsn_win_abi_version", "hsn_win_last_error"):
+                     "hsn_win_abi_version", "hsn_win_last_error", "hsn_tr_adamw",
+                     "hsn_tr_adamw_units", "hsn_tr_lerp", "hsn_tr_scale64", "hsn_tr_copy",
+                     "hsn_tr_limit_squares", "hsn_tr_limit_project"):
         assert expected in names
 
 
@@ -85,6 +87,41 @@ def test_argument_errors_return_status_without_a_gpu():
     status = lib.hsn_win_select(1, 0, 1, None, 1, 1, 1, 1, 1, 1, 1, 8, 1, 4, 0, 1, 1, 0, 0, 0.0,
                                 0.0, 0.0, 1.0, 0, 1, None)
     assert status == 1 and b"reserved_units" in lib.hsn_win_last_error()
+
+
+def test_trainer_pass_arguments_are_checked_before_any_launch():
+    """The trainer passes' list checks run on the host: a bad unit count, a tensor that is not a
+    whole number of units, a NULL pointer of a non-empty tensor and a negative size return
+    HSN_ERR_INVALID_ARGUMENT with a message; a list of empty tensors (whose pointers may be NULL,
+    as torch's are) is nothing to do and returns HSN_OK without a launch."""
+    import ctypes
+
+    from hsn_amd import _lib, build
+
+    if build.stale() is not None:
+        pytest.skip("library not built here")
+    lib = _lib.library()
+
+    def ptrs(*values):
+        return (ctypes.c_void_p * len(values))(*values)
+
+    def sizes(*values):
+        return (ctypes.c_int64 * len(values))(*values)
+
+    fake = 0x10000  # never dereferenced: every case below fails its checks first
+    rows = [ptrs(fake) for _ in range(4)]
+    coefs = (ctypes.c_float * (6 * 65))()
+    assert lib.hsn_tr_adamw_units(*rows, sizes(130), 1, 65, 1, coefs, 0.001, 1e-8, None) == 1
+    assert b"n_units" in lib.hsn_win_last_error()
+    assert lib.hsn_tr_adamw_units(*rows, sizes(10), 1, 3, 1, coefs, 0.001, 1e-8, None) == 1
+    assert b"whole number" in lib.hsn_win_last_error()
+    assert lib.hsn_tr_lerp(ptrs(fake), ptrs(None), sizes(5), 1, 0.5, None) == 1
+    assert b"NULL" in lib.hsn_win_last_error()
+    assert lib.hsn_tr_copy(ptrs(fake), ptrs(fake), sizes(-1), 1, None) == 1
+    assert b"negative" in lib.hsn_win_last_error()
+    assert lib.hsn_tr_scale64(ptrs(fake), sizes(4), 1, None, None) == 1
+    assert b"coefficient" in lib.hsn_win_last_error()
+    assert lib.hsn_tr_lerp(ptrs(None, None), ptrs(None, None), sizes(0, 0), 2, 0.5, None) == 0
 
 
 @pytest.mark.parametrize("reserved,units,ok", [(0, False, True), (3, True, True), (4, False, False),

@@ -603,3 +603,151 @@ def test_h_max_propagates_a_nan_in_an_unwritten_cell():
     # a plain max (NaN-ignoring, as a careless reduction would be) fails this pin
     finite = torch.nan_to_num(out["h"], nan=0.0).abs().flatten(1).amax(1)
     assert not bool(torch.isnan(finite).any())
+
+
+# ------------------------------------------------------------------------------------------------
+# The trainer passes' oracle (fma32 and the tr_* restatements)
+# ------------------------------------------------------------------------------------------------
+
+def _round32(x):
+    """The float32 nearest (ties to even) to the exact rational x (a Fraction), as numpy float32."""
+    import numpy as np
+    from fractions import Fraction
+
+    if x == 0:
+        return np.float32(0.0)
+    sign = -1 if x < 0 else 1
+    ax = abs(x)
+    e = ax.numerator.bit_length() - ax.denominator.bit_length()
+    if Fraction(2) ** e > ax:
+        e -= 1
+    quantum = Fraction(2) ** (max(e, -126) - 23)  # subnormals below 2^-126
+    q = ax / quantum
+    n = q.numerator // q.denominator
+    rest = q - n
+    if rest > Fraction(1, 2) or (rest == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    v = n * quantum
+    if v >= Fraction(2) ** 128:
+        return np.float32(sign * np.inf)
+    return np.float32(sign * float(v))
+
+
+def _bits(x):
+    import numpy as np
+
+    return np.asarray(x, np.float32).view(np.int32)
+
+
+def test_fma32_rounds_once_like_exact_arithmetic():
+    """fma32 against the exact rational a * b + c rounded once: random operands over many
+    magnitudes, planted float32 midpoints with no tail (ties to even) and with a tail of either
+    sign, signed zeros, subnormal results and an overflow."""
+    import numpy as np
+    from fractions import Fraction
+
+    rng = np.random.default_rng(11)
+    n = 3000
+    a = (rng.standard_normal(n) * 10.0 ** rng.integers(-20, 20, n)).astype(np.float32)
+    b = (rng.standard_normal(n) * 10.0 ** rng.integers(-20, 20, n)).astype(np.float32)
+    c = (rng.standard_normal(n) * 10.0 ** rng.integers(-20, 20, n)).astype(np.float32)
+    half = np.float32(2.0 ** -12)
+    tail = np.float32(2.0 ** -12 * (1 + 2.0 ** -23))
+    extra = [
+        (half, half, 1.0),        # 1 + 2^-24 exactly: a tie, to the even 1
+        (tail, half, 1.0),        # above the midpoint: up to 1 + 2^-23
+        (-tail, half, 1.0),       # below 1 - 2^-25 ... down from the midpoint below 1
+        (half, half, 1.0 + 2.0 ** -23),  # a tie whose even neighbour is above
+        (0.0, 3.0, -0.0), (-0.0, 3.0, -0.0), (0.0, -3.0, 0.0),
+        (1e-30, 1e-15, 0.0),      # a subnormal product
+        (3e-39, 0.5, 1e-45),      # subnormal operands
+        (1e30, 1e10, -1.0),       # overflow
+    ]
+    a = np.concatenate([a, np.float32([e[0] for e in extra])])
+    b = np.concatenate([b, np.float32([e[1] for e in extra])])
+    c = np.concatenate([c, np.float32([e[2] for e in extra])])
+    got = O.fma32(a, b, c)
+    for i in range(a.size):
+        exact = Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i]))
+        want = _round32(exact)
+        if exact == 0:  # the sign of an exact zero: -0 only from -0 + -0
+            want = np.float32(-0.0) if (np.signbit(a[i] * b[i]) and np.signbit(c[i])) else np.float32(0.0)
+        assert _bits(got[i]) == _bits(want), (a[i], b[i], c[i], got[i], want)
+
+
+def test_lerp_oracle_hits_its_end_points_and_rounds_each_branch_once():
+    import numpy as np
+    from fractions import Fraction
+
+    rng = np.random.default_rng(12)
+    s = rng.standard_normal(500).astype(np.float32)
+    e = rng.standard_normal(500).astype(np.float32)
+    assert np.array_equal(_bits(O.tr_lerp(s, e, 0.0)), _bits(s))
+    assert np.array_equal(_bits(O.tr_lerp(s, e, 1.0)), _bits(e))
+    for w in (np.float32(0.1), np.float32(0.49), np.float32(0.5), np.float32(0.99)):
+        got = O.tr_lerp(s, e, w)
+        diff = (e - s).astype(np.float32)
+        for i in range(s.size):
+            if w < 0.5:
+                exact = Fraction(float(s[i])) + Fraction(float(w)) * Fraction(float(diff[i]))
+            else:
+                one_minus = np.float32(1.0) - w
+                exact = Fraction(float(e[i])) - Fraction(float(diff[i])) * Fraction(float(one_minus))
+            assert _bits(got[i]) == _bits(_round32(exact)), (w, i)
+
+
+def test_plain_trainer_passes_equal_torch_cpu_operations():
+    """The passes with no fused operation against torch's CPU operations bit for bit: the float64
+    clip's scaling, the update caps' squares and projection."""
+    import numpy as np
+
+    g = torch.Generator().manual_seed(13)
+    p = torch.randn(4000, generator=g)
+    old = torch.randn(4000, generator=g)
+    p[:4] = torch.tensor([0.0, -0.0, 1e-42, 3e30])
+    coef = torch.tensor(0.3713, dtype=torch.float64)
+    want = (p.double() * coef).float()
+    assert np.array_equal(_bits(O.tr_scale64(p.numpy(), float(coef))), _bits(want.numpy()))
+    sq_old, sq_delta = O.tr_limit_squares(p.numpy(), old.numpy())
+    assert np.array_equal(_bits(sq_old), _bits(old.square().numpy()))
+    assert np.array_equal(_bits(sq_delta), _bits((p - old).square().numpy()))
+    for clipped in (True, False):
+        scale = torch.tensor(0.625)
+        want_p = torch.where(torch.tensor(clipped), old + (p - old) * scale, p)
+        got_p, got_sq = O.tr_limit_project(p.numpy(), old.numpy(), 0.625, clipped)
+        assert np.array_equal(_bits(got_p), _bits(want_p.numpy()))
+        assert np.array_equal(_bits(got_sq), _bits((want_p - old).square().numpy()))
+
+
+def test_adamw_oracle_first_steps_reduce_to_their_closed_forms():
+    """From an all-zero state the first step's moments are single roundings: m = (1 - beta1) g
+    (the lerp from 0) and, with beta2 = 0, v = g^2; with beta1 = 0 the lerp's weight is 1 and m is
+    g itself. A zero gradient from a zero state leaves the weight at its decayed value."""
+    import numpy as np
+
+    rng = np.random.default_rng(14)
+    p = rng.standard_normal(800).astype(np.float32)
+    g = rng.standard_normal(800).astype(np.float32)
+    z = np.zeros_like(p)
+    lr, eps, wd = 2.5e-3, 1e-8, 0.01
+    for beta1, beta2 in ((0.9, 0.0), (0.0, 0.0)):
+        coefs = [1 - lr * wd, 1 - beta1, beta2, 1 - beta2, 1.0 / (1 - beta2) ** 0.5, eps,
+                 -lr / (1 - beta1)]
+        _, m, v = O.tr_adamw(p, g, z, z, coefs, True)
+        assert np.array_equal(_bits(m), _bits(np.float32(1 - beta1) * g))
+        assert np.array_equal(_bits(v), _bits(g * g))
+    coefs = [1 - lr * wd, 0.1, 0.999, 0.001, 1.0 / 0.001 ** 0.5, eps, -lr / 0.1]
+    p1, m, v = O.tr_adamw(p, z, z, z, coefs, True)
+    assert np.array_equal(_bits(p1), _bits(p * np.float32(1 - lr * wd)))
+    assert not m.any() and not v.any()
+    # the unit form with every unit active and equal coefficients is the dense form
+    M = 8
+    pu = p.reshape(M, -1)
+    table = np.float32([[1.0] * M, [coefs[0]] * M, [coefs[1]] * M, [coefs[2]] * M,
+                        [0.001 ** 0.5] * M, [lr / 0.1] * M])
+    gu = g.reshape(M, -1)
+    pd, md, vd = O.tr_adamw(p, g, z, z, [coefs[0], coefs[1], coefs[2], coefs[3],
+                                         np.float32(1.0) / np.float32(0.001 ** 0.5), eps, -lr / 0.1], True)
+    pu1, mu, vu = O.tr_adamw_units(pu, gu, z.reshape(M, -1), z.reshape(M, -1), table, 0.001, eps, True)
+    assert np.array_equal(_bits(mu.reshape(-1)), _bits(md))
+    assert np.array_equal(_bits(vu.reshape(-1)), _bits(vd))
