@@ -361,3 +361,39 @@ def test_passes_decline_what_they_cannot_take(dev):
     torch.cuda.synchronize()
     _same_bits(a, keep, "declined passes leave the tensors alone")
     assert trainer.lerp([a], [b], 0.5)  # and the same call runs once switched back on
+
+
+def test_adamw_pass_replays_in_a_graph(dev):
+    """The pass captured in a HIP graph (its pointer table and coefficients fixed at capture) and
+    replayed three times, with eager work and synchronisations between the replays: every replay
+    equals the PyTorch sequence at the same step count."""
+    from hsn_amd import trainer
+
+    gen = torch.Generator().manual_seed(606)
+    sizes = (5, 1024, 3000, 70001)
+    lr, betas, eps, wd, step = 1e-3, (0.9, 0.999), 1e-8, 0.02, 4
+    rows = [[torch.randn(n, generator=gen).to(dev) for n in sizes] for _ in range(4)]
+    for v in rows[3]:
+        v.abs_()
+    theirs = [[t.clone() for t in row] for row in rows]
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        assert trainer.adamw(*rows, lr=lr, beta1=betas[0], beta2=betas[1], eps=eps,
+                             weight_decay=wd, step=step)
+    torch.cuda.synchronize()
+    # capture records the launch without running it: the state is still the initial one
+    for r in (0, 2, 3):
+        for got, want in zip(rows[r], theirs[r]):
+            _same_bits(got, want, "capture ran nothing")
+    for replay in range(3):
+        graph.replay()
+        _dense_reference(*theirs, step, lr, betas, eps, wd)
+        torch.cuda.synchronize()
+        for r, name in ((0, "param"), (2, "exp_avg"), (3, "exp_avg_sq")):
+            for j, (got, want) in enumerate(zip(rows[r], theirs[r])):
+                _same_bits(got, want, f"replay {replay} {name}[{j}]")
+        for g in rows[1]:  # eager work between replays: new gradients in place
+            g.mul_(-0.5)
+        for g in theirs[1]:
+            g.mul_(-0.5)
