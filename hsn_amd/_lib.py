@@ -1,5 +1,5 @@
 """The C ABI of ``libhsn_amd.so`` (``include/hsn_window.h``, ``include/hsn_ops.h``,
-``include/hsn_trainer.h``) via ctypes.
+``include/hsn_trainer.h``, ``include/hsn_sweep.h``) via ctypes.
 
 The library is the product: every operator in :mod:`hsn_amd` reaches the GPU through these
 entry points, and nothing here falls back to another implementation. :func:`library` raises a
@@ -68,6 +68,10 @@ SIGNATURES: dict[str, list] = {
     "hsn_tr_copy": [P, P, P, I, P],
     "hsn_tr_limit_squares": [P, P, P, P, P, I, P],
     "hsn_tr_limit_project": [P, P, P, P, P, I, P],
+    "hsn_win_back_check": [P],
+    "hsn_win_back_head": [P, I, P],
+    "hsn_win_back_mid": [P, I, P],
+    "hsn_win_back_tail": [P, I, P],
 }
 
 _lock = threading.Lock()

@@ -31,7 +31,8 @@ def test_headers_declare_the_hot_path_entry_points():
                      "hsn_grouped_unit_mlp_bwd", "hsn_csr_messages", "hsn_csr_messages_bwd",
                      "hsn_win_abi_version", "hsn_win_last_error", "hsn_tr_adamw",
                      "hsn_tr_adamw_units", "hsn_tr_lerp", "hsn_tr_scale64", "hsn_tr_copy",
-                     "hsn_tr_limit_squares", "hsn_tr_limit_project"):
+                     "hsn_tr_limit_squares", "hsn_tr_limit_project", "hsn_win_back_check",
+                     "hsn_win_back_head", "hsn_win_back_mid", "hsn_win_back_tail"):
         assert expected in names
 
 
@@ -87,6 +88,27 @@ def test_argument_errors_return_status_without_a_gpu():
     status = lib.hsn_win_select(1, 0, 1, None, 1, 1, 1, 1, 1, 1, 1, 8, 1, 4, 0, 1, 1, 0, 0, 0.0,
                                 0.0, 0.0, 1.0, 0, 1, None)
     assert status == 1 and b"reserved_units" in lib.hsn_win_last_error()
+
+
+def test_reverse_sweep_check_follows_the_kernels_limits():
+    """``back_unsupported`` is the library's own check (no GPU): the ref model's sweep is taken;
+    d above 256, a row table over 64 KiB of LDS, fp16 products and an unknown activation are
+    not, each with its reason."""
+    import torch
+
+    from hsn_amd import build
+    from hsn_amd.state_sweep import SweepShape, back_unsupported
+
+    if build.stale() is not None:
+        pytest.skip("library not built here")
+    ref = SweepShape(B=32, T=256, K=8, N=256, d=64, H=512, M=8, n_fast=0, n_read=0, in_dim=256,
+                     d_out=8)
+    assert back_unsupported(ref) is None
+    assert back_unsupported(ref, product_dtype=torch.bfloat16) is None
+    assert "256" in back_unsupported(ref._replace(d=300))
+    assert "LDS" in back_unsupported(ref._replace(N=8000))
+    assert "bf16" in back_unsupported(ref, product_dtype=torch.float16)
+    assert "activation" in back_unsupported(ref, activation="softplus")
 
 
 def test_trainer_pass_arguments_are_checked_before_any_launch():
