@@ -55,6 +55,11 @@ def _args():
                    help="skip the graph capture and its replays")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="repeat the CPU baseline's sample until this much time has passed")
+    p.add_argument("--sweep", choices=["ref", "tiny"], default=None,
+                   help="measure the state-gradient reverse sweep (hsn_amd.state_sweep) at this "
+                        "workload instead of the window (not the headline line)")
+    p.add_argument("--products", choices=["bf16", "f32"], default="bf16",
+                   help="the reverse sweep's product dtype (bf16: autocast's)")
     p.add_argument("--trainer", choices=sorted(TRAINER_LISTS), default=None,
                    help="measure the trainer's AdamW pass (hsn_tr_adamw) over a synthetic "
                         "parameter list instead of the window (not the headline line)")
@@ -248,6 +253,140 @@ def _trainer_main(args) -> int:
     return 0
 
 
+def _sweep_main(args) -> int:
+    """The state-gradient reverse sweep over one synthetic window of the workload: a step is one
+    window's sweep (T positions of head, product, middle, product, tail) replayed from its
+    captured HIP graph, inputs resident; ``value`` is positions/s (B x T per window). Each part's
+    duration comes from HIP events between the parts of eager windows queued behind device
+    copies; the roofline is the dominant part's against its bound (the products: the all-units
+    GEMMs' FLOPs against the MFMA peak of the product dtype; the glue: its bytes against HBM)."""
+    import torch
+
+    from hsn_amd.state_sweep import ReverseSweep, SweepRunner, sweep_shape
+    from hsn_amd.workload import SWEEP_CONFIGS, make_sweep_window
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    shape_kw = SWEEP_CONFIGS[args.sweep]
+    product = torch.bfloat16 if args.products == "bf16" else torch.float32
+    wargs, wkw = make_sweep_window(**shape_kw, seed=args.seed, device=dev, product_dtype=product)
+    runner = SweepRunner(graph=True)
+    assert runner(*wargs, **wkw) is not None, "the runner declined the workload"
+    (sweep,) = runner.sweeps.values()
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        sweep.run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        sweep.run()
+    torch.cuda.synchronize()
+    graph_secs = (time.perf_counter() - t0) / args.steps
+    s = sweep.shape
+    # per part: eager windows with events between the parts, behind a queue of device copies
+    windows = max(1, min(args.steps, 3))
+    busy = torch.empty(64 << 20, device=dev)
+    busy_dst = torch.empty_like(busy)
+    import ctypes
+
+    from hsn_amd import _lib
+
+    parts = ("head", "act product", "middle", "dv product", "tail")
+    events = []
+    torch.cuda.synchronize()
+    for _ in range(windows * s.T // 4 + 8):
+        busy_dst.copy_(busy)
+    stream = _lib.stream_of(dev)
+    ref = ctypes.byref(sweep._struct)
+    for _ in range(windows):
+        for t in range(s.T - 1, -1, -1):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+            ev[0].record()
+            _lib.call("hsn_win_back_head", ref, t, stream)
+            ev[1].record()
+            torch.mm(sweep.op1, sweep.w2_t, out=sweep.act)
+            ev[2].record()
+            _lib.call("hsn_win_back_mid", ref, t, stream)
+            ev[3].record()
+            torch.mm(sweep.op2, sweep.w1_state_t, out=sweep.dv)
+            ev[4].record()
+            _lib.call("hsn_win_back_tail", ref, t, stream)
+            ev[5].record()
+            events.append(ev)
+    torch.cuda.synchronize()
+    del busy, busy_dst
+    per_part = {p: sum(ev[i].elapsed_time(ev[i + 1]) for ev in events) / (windows * s.T)
+                for i, p in enumerate(parts)}  # ms per position
+    rows = s.B * s.K
+    esize = 2 if product == torch.bfloat16 else 4
+    flops = {"act product": 2.0 * rows * s.M * s.d * s.H,
+             "dv product": 2.0 * rows * (s.M * s.H + s.d) * 2 * s.d}
+    peak_tf = 2500.0 if product == torch.bfloat16 else 157.3
+    touched = min(s.N, s.K * (int(shape_kw["D"]) + 1))  # cells a row's tail reads and writes
+    glue_bytes = {  # algorithmic bytes per position
+        # c, b, h_old, d_h_sel, y, gate_pre read, A read and written, dc, db written (fp32);
+        # op1's block cleared and written, op2's gate columns written
+        "head": rows * s.d * (11 * 4 + 3 * esize),
+        # hidden and act read, op2's block cleared and written
+        "middle": rows * s.H * 4 * esize,
+        # dv read, h_old and m V read (fp32), the touched cells' rows of A read and written
+        "tail": rows * s.d * (2 * esize + 2 * 4) + s.B * touched * s.d * 8,
+    }
+    dominant = max(per_part, key=per_part.get)
+    if dominant in flops:
+        achieved = flops[dominant] / (per_part[dominant] * 1e-3) / 1e12
+        roof = {"bound": "mfma", "kernel": dominant, "achieved": achieved, "peak": peak_tf,
+                "unit": "TFLOP/s", "frac": achieved / peak_tf, "traffic": None}
+    else:
+        achieved = glue_bytes[dominant] / (per_part[dominant] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "kernel": dominant, "achieved": achieved, "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None}
+    positions = s.B * s.T
+    result = {
+        "metric": f"state-gradient reverse sweep positions/sec ({args.sweep} model, 1 GPU)",
+        "value": positions / graph_secs,
+        "unit": "positions/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": graph_secs * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if product == torch.bfloat16 else "f32",
+        "data": "synthetic (hsn_amd/workload.py make_sweep_window)",
+        "config": {"workload": f"sweep_{args.sweep}", **shape_kw, "products": args.products,
+                   "timing": "HIP graph replay of the window's sweep", "parallelism": "single GPU"},
+        "roofline": roof,
+        "parts_us_per_position": {k: v * 1e3 for k, v in per_part.items()},
+        "position_us_graph": graph_secs / s.T * 1e6,
+    }
+    if not args.no_cpu:  # the oracle on a bounded sample: 2 rows x 8 positions, one thread
+        from oracle import state_gradient as O
+
+        torch.set_num_threads(1)
+        sample = dict(shape_kw, B=2, T=8)
+        cargs, _ = make_sweep_window(**sample, seed=args.seed)
+        record = dict(cargs[12], hidden=cargs[12]["hidden"].float())
+        consts = O.CellConstants(*cargs[13])
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            O.state_gradient_backward(*cargs[:12], record, consts)
+            reps += 1
+            secs = time.perf_counter() - t0
+            if secs >= args.cpu_seconds:
+                break
+        result["cpu_baseline"] = {
+            "value": 2 * 8 * reps / secs, "unit": "positions/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} x (2 rows x 8 positions of the {args.sweep} model), the "
+                      f"repository's PyTorch-CPU oracle ({secs:.1f} s)",
+        }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     args = _args()
     if args.gpus != 1:
@@ -257,6 +396,8 @@ def main() -> int:
         return 2
     if args.trainer:
         return _trainer_main(args)
+    if args.sweep:
+        return _sweep_main(args)
     import torch
 
     from hsn_amd import window

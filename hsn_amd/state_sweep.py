@@ -30,6 +30,7 @@ from . import _lib
 
 __all__ = [
     "ACTIVATION_CODES",
+    "CellConstants",
     "ReverseSweep",
     "SweepRunner",
     "SweepShape",
@@ -40,6 +41,32 @@ __all__ = [
 
 #: ``model.activation`` as the kernels' code (include/hsn_sweep.h HSN_ACT_*).
 ACTIVATION_CODES: dict[str, int] = {"gelu": 0, "relu": 1, "silu": 2, "tanh": 3}
+
+
+class CellConstants(NamedTuple):
+    """What the sweep reads of the cell's weights: the fields of the reference's
+    ``hsn.train.state_gradient.CellConstants`` (state_gradient.py:134-156), which the runner
+    takes as well. ``w_out [d, d]`` (y = F @ w_out.T), ``cand_gain [d]`` or None, ``cand_eps``,
+    ``w2 [M, H, d]``, ``w1_state [M, 2d, H]`` (the first layer at the state columns), ``b1 [M,
+    H]``, ``gate_state [d, 2d]``, ``gate_bias [d]``, ``norm_gain_state [2d]`` or None,
+    ``in_dim``, ``v [d, d]`` (V h = h @ v.T), ``edge_weights [N, D]``, ``pad_src [N, D]``,
+    ``activation``, ``pad_mask [N, D]``."""
+
+    w_out: Tensor
+    cand_gain: Optional[Tensor]
+    cand_eps: float
+    w2: Tensor
+    w1_state: Tensor
+    b1: Tensor
+    gate_state: Tensor
+    gate_bias: Tensor
+    norm_gain_state: Optional[Tensor]
+    in_dim: int
+    v: Tensor
+    edge_weights: Tensor
+    pad_src: Tensor
+    activation: str
+    pad_mask: Optional[Tensor] = None
 
 
 class SweepShape(NamedTuple):

@@ -168,3 +168,53 @@ def _check_byte_model() -> None:  # pragma: no cover - used interactively
         bm = byte_model(cfg)
         print(name, round(bm["forward"]), round(bm["backward"]), round(bm["total"]),
               bm["window_bytes"] / 1e6, math.floor(8e12 / bm["total"] / 1e6))
+
+
+#: The reverse sweep's workloads. "ref" is the reference's model at its ref shape (B 32, K 8,
+#: d 64, M 8 units of H 512 over a 256-position window of 256 cells; the cell input is
+#: [u; eps; h; m], 4d wide; 8 message sources a cell).
+SWEEP_CONFIGS = {
+    "ref": dict(B=32, T=256, K=8, N=256, d=64, H=512, M=8, D=8),
+    "tiny": dict(B=2, T=8, K=3, N=16, d=8, H=16, M=2, D=3),
+}
+
+
+def make_sweep_window(B: int, T: int, K: int, N: int, d: int, H: int, M: int, D: int, *,
+                      seed: int = 0, device="cpu", product_dtype=torch.float32):
+    """Synthetic arguments of the state-gradient sweep (``state_gradient_backward``'s, for
+    ``hsn_amd.state_sweep.SweepRunner``): seeded values of a window's shape: distinct cells per
+    position (one slot in 16 padded), units, a few resets, candidates and gates in their ranges,
+    a random cell (both norms, GELU) and message graph. Returns ``(args, kwargs)``."""
+    from .state_sweep import CellConstants
+
+    g = torch.Generator().manual_seed(seed)
+    f32 = torch.float32
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(device)
+
+    n = 4 * d
+    cells = torch.argsort(torch.rand(B, T, N, generator=g), dim=-1)[..., :K]
+    valid = torch.rand(B, T, K, generator=g) >= 1.0 / 16
+    units = torch.randint(0, M, (B, T, K), generator=g)
+    reset = torch.rand(B, T, generator=g) < 1.0 / 64
+    pad_src = torch.randint(0, N, (N, D), generator=g)
+    pad_mask = torch.rand(N, D, generator=g) < 0.9
+    consts = CellConstants(
+        w_out=rnd(d, d, scale=d ** -0.5), cand_gain=1.0 + rnd(d, scale=0.1), cand_eps=1e-6,
+        w2=rnd(M, H, d, scale=H ** -0.5), w1_state=rnd(M, 2 * d, H, scale=n ** -0.5),
+        b1=rnd(M, H, scale=0.1), gate_state=rnd(d, 2 * d, scale=n ** -0.5),
+        gate_bias=rnd(d, scale=0.1), norm_gain_state=1.0 + rnd(2 * d, scale=0.1), in_dim=n,
+        v=rnd(d, d, scale=d ** -0.5),
+        edge_weights=torch.where(pad_mask.to(device), rnd(N, D, scale=0.3), torch.zeros((), device=device)),
+        pad_src=pad_src.to(device), activation="gelu", pad_mask=pad_mask.to(device))
+    c = torch.tanh(rnd(B, T, K, d))
+    b = torch.sigmoid(rnd(B, T, K, d))
+    record = {
+        "y": rnd(B, T, K, d), "alpha": torch.ones(B, T, K, dtype=f32, device=device),
+        "hidden": rnd(B, T, K, H).to(product_dtype), "gate_pre": rnd(B, T, K, d),
+        "m": rnd(B, T, K, d, scale=0.5), "rms": 0.5 + torch.rand(B, T, K, generator=g).to(device),
+    }
+    args = (c, b, rnd(B, T, K, d, scale=0.5), cells.to(device), units.to(device), valid.to(device),
+            reset.to(device), N, rnd(B, T, d), rnd(B, T, d), rnd(B, T, K, d), None, record, consts)
+    return args, dict(n_read=0)
