@@ -60,6 +60,9 @@ def _args():
                         "workload instead of the window (not the headline line)")
     p.add_argument("--products", choices=["bf16", "f32"], default="bf16",
                    help="the reverse sweep's product dtype (bf16: autocast's)")
+    p.add_argument("--three-steps", action="store_true",
+                   help="the reverse sweep's three glue steps around all-units GEMMs instead of "
+                        "the fused step")
     p.add_argument("--trainer", choices=sorted(TRAINER_LISTS), default=None,
                    help="measure the trainer's AdamW pass (hsn_tr_adamw) over a synthetic "
                         "parameter list instead of the window (not the headline line)")
@@ -272,7 +275,7 @@ def _sweep_main(args) -> int:
     shape_kw = SWEEP_CONFIGS[args.sweep]
     product = torch.bfloat16 if args.products == "bf16" else torch.float32
     wargs, wkw = make_sweep_window(**shape_kw, seed=args.seed, device=dev, product_dtype=product)
-    runner = SweepRunner(graph=True)
+    runner = SweepRunner(graph=True, fused=False if args.three_steps else None)
     assert runner(*wargs, **wkw) is not None, "the runner declined the workload"
     (sweep,) = runner.sweeps.values()
     torch.cuda.synchronize()
@@ -293,7 +296,8 @@ def _sweep_main(args) -> int:
 
     from hsn_amd import _lib
 
-    parts = ("head", "act product", "middle", "dv product", "tail")
+    parts = (("cell step", "tail") if sweep.fused else
+             ("head", "act product", "middle", "dv product", "tail"))
     events = []
     torch.cuda.synchronize()
     for _ in range(windows * s.T // 4 + 8):
@@ -302,7 +306,15 @@ def _sweep_main(args) -> int:
     ref = ctypes.byref(sweep._struct)
     for _ in range(windows):
         for t in range(s.T - 1, -1, -1):
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(parts) + 1)]
+            if sweep.fused:
+                ev[0].record()
+                _lib.call("hsn_win_back_cell", ref, t, stream)
+                ev[1].record()
+                _lib.call("hsn_win_back_cell_tail", ref, t, stream)
+                ev[2].record()
+                events.append(ev)
+                continue
             ev[0].record()
             _lib.call("hsn_win_back_head", ref, t, stream)
             ev[1].record()
@@ -321,8 +333,10 @@ def _sweep_main(args) -> int:
                 for i, p in enumerate(parts)}  # ms per position
     rows = s.B * s.K
     esize = 2 if product == torch.bfloat16 else 4
-    flops = {"act product": 2.0 * rows * s.M * s.d * s.H,
-             "dv product": 2.0 * rows * (s.M * s.H + s.d) * 2 * s.d}
+    flops = {"act product": 2.0 * rows * s.M * s.d * s.H,  # the all-units GEMMs
+             "dv product": 2.0 * rows * (s.M * s.H + s.d) * 2 * s.d,
+             # the fused step multiplies each slot's own unit blocks only
+             "cell step": 2.0 * rows * (s.d * s.H + (s.H + s.d) * 2 * s.d)}
     peak_tf = 2500.0 if product == torch.bfloat16 else 157.3
     touched = min(s.N, s.K * (int(shape_kw["D"]) + 1))  # cells a row's tail reads and writes
     glue_bytes = {  # algorithmic bytes per position
@@ -361,6 +375,7 @@ def _sweep_main(args) -> int:
                    "timing": "HIP graph replay of the window's sweep", "parallelism": "single GPU"},
         "roofline": roof,
         "parts_us_per_position": {k: v * 1e3 for k, v in per_part.items()},
+        "fused_step": sweep.fused,
         "position_us_graph": graph_secs / s.T * 1e6,
     }
     if not args.no_cpu:  # the oracle on a bounded sample: 2 rows x 8 positions, one thread

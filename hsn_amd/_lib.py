@@ -72,6 +72,9 @@ SIGNATURES: dict[str, list] = {
     "hsn_win_back_head": [P, I, P],
     "hsn_win_back_mid": [P, I, P],
     "hsn_win_back_tail": [P, I, P],
+    "hsn_win_back_cell_check": [P],
+    "hsn_win_back_cell": [P, I, P],
+    "hsn_win_back_cell_tail": [P, I, P],
 }
 
 _lock = threading.Lock()

@@ -23,6 +23,7 @@
 #include "../../include/hsn_sweep.h"
 #include "abi_util.h"
 #include "common.cuh"
+#include "dpp.cuh"
 
 #pragma clang fp contract(off)
 
@@ -44,11 +45,8 @@ __device__ __forceinline__ void st(void* p, int64_t i, float v) {
     static_cast<P*>(p)[i] = from_f32<P>(v);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += wave_shfl_xor(v, m);
-    return v;
-}
+// The wavefront's sum in every lane: DPP within the rows, permlane swaps across them (no LDS).
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
 
 // state_gradient.activation_grad: the derivative of the cell's activation at x.
 __device__ __forceinline__ float act_grad(int code, float x) {
@@ -282,8 +280,549 @@ __global__ __launch_bounds__(kBackThreads) void back_tail(hsn_back_sweep s, int 
         A[int64_t(n) * d + x] = a;
     }
     if (blockIdx.x == 0)
-        for (int x = tid; x < d; x += kBackThreads)
+        for (int x = tid; x < d; x += kBackThreads) {
             s.R[int64_t(row) * d + x] = s.R[int64_t(row) * d + x] + s.d_q_pre[bt * d + x];
+        }
+}
+
+// ------------------------------------------------------------------------------------------
+// back_cell: head, both products and middle for 16 slots of one unit on the matrix cores
+// ------------------------------------------------------------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+constexpr int kCellRows = 16;  // slots per workgroup: the MFMA tile's rows
+constexpr int kCellCols = 16;  // dv columns per workgroup: one MFMA tile's columns
+constexpr int kCellThreads = 512;
+constexpr int kCellWaves = kCellThreads / kWave;
+constexpr int kCellMaxCpl = 2;  // d <= 128 on the fused step
+constexpr int kDvChunk = 4;     // dv reduction steps whose loads a wavefront issues together
+
+// act column tiles whose loads a wavefront issues together: at most 64 registers of weights
+template <typename P, int CPL>
+constexpr int act_tiles() {
+    return sizeof(P) == 2 ? 4 : (CPL == 1 ? 4 : 2);
+}
+
+// The MFMA tile of a product dtype. Lane l supplies A[l % 16][kq .. kq + kPer) and
+// B[kq .. kq + kPer)[l % 16] with kq = kPer (l / 16), and receives D[4 (l / 16) + r][l % 16] in
+// result register r; a step covers kStep of the reduction index (the lane layout checked on the
+// card for both instructions).
+template <typename P>
+struct Tile;
+template <>
+struct Tile<bf16_t> {  // v_mfma_f32_16x16x32_bf16
+    static constexpr int kPer = 8, kStep = 32;
+    typedef bf8 frag;
+    static __device__ __forceinline__ frag lds(const bf16_t* p) {
+        return *reinterpret_cast<const bf8*>(p);
+    }
+    static __device__ __forceinline__ frag glb(const bf16_t* p, bool ok) {
+        if (!ok) return frag{};
+        return *reinterpret_cast<const bf8*>(p);
+    }
+    static __device__ __forceinline__ v4f mma(frag a, frag b, v4f c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct Tile<float> {  // v_mfma_f32_16x16x4_f32
+    static constexpr int kPer = 1, kStep = 4;
+    typedef float frag;
+    static __device__ __forceinline__ frag lds(const float* p) { return *p; }
+    static __device__ __forceinline__ frag glb(const float* p, bool ok) { return ok ? *p : 0.0f; }
+    static __device__ __forceinline__ v4f mma(frag a, frag b, v4f c) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
+};
+
+// The activation's derivative with the activation fixed at compile time (one branch of code).
+template <int ACT>
+__device__ __forceinline__ float act_grad_t(float x) {
+    if constexpr (ACT == HSN_ACT_GELU) {
+        const float cdf = 0.5f * (1.0f + erff(x / 1.41421356237309515f));
+        return cdf + x * expf(-0.5f * x * x) / 2.50662827463100024f;
+    } else if constexpr (ACT == HSN_ACT_RELU) {
+        return x > 0.0f ? 1.0f : 0.0f;
+    } else if constexpr (ACT == HSN_ACT_SILU) {
+        const float sg = 1.0f / (1.0f + expf(-x));
+        return sg * (1.0f + x * (1.0f - sg));
+    } else {
+        const float th = tanhf(x);
+        return 1.0f - th * th;
+    }
+}
+
+__host__ __device__ inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+constexpr int kCellMaxSlots = 4096;  // B K on the fused step: the position's slots in LDS
+
+struct CellLds {
+    int rows, meta, sig_part, sig_gate, sig_row, red, ucache, ccache, du, dh, du_stride,
+        dh_stride, bytes;
+};
+template <typename P>
+__host__ __device__ inline CellLds cell_lds(int d, int H, int BK) {
+    constexpr int kStep = sizeof(P) == 2 ? 32 : 4;
+    CellLds L;
+    L.du_stride = round_up(d, kStep) + 8;  // + 8 elements: consecutive rows off the same banks
+    L.dh_stride = round_up(H + d, kStep) + 8;
+    L.rows = 0;                                            // int [16]
+    L.meta = L.rows + 4 * kCellRows;                       // int [4]
+    L.sig_part = L.meta + 16;                              // float [8][16]
+    L.sig_gate = L.sig_part + 4 * kCellWaves * kCellRows;  // float [16]
+    L.sig_row = L.sig_gate + 4 * kCellRows;                // float [16]
+    L.red = L.sig_row + 4 * kCellRows;                     // float [8][64][4]
+    L.ucache = L.red + 4 * kCellWaves * kWave * 4;         // uint8 [B K]: each slot's unit
+    L.ccache = round_up(L.ucache + BK, 16);                // int [B K]: each slot's cell
+    L.du = L.ccache + 4 * BK;                              // P [16][du_stride]
+    L.dh = L.du + round_up(static_cast<int>(sizeof(P)) * kCellRows * L.du_stride, 16);
+    L.bytes = L.dh + static_cast<int>(sizeof(P)) * kCellRows * L.dh_stride;
+    return L;
+}
+
+template <typename P>
+__device__ __forceinline__ float round_p(float v) {
+    return to_f32(from_f32<P>(v));
+}
+
+__device__ __forceinline__ int64_t slot_at(const hsn_back_sweep& s, int t, int q) {
+    return (int64_t(q / s.K) * s.T + t) * s.K + q % s.K;
+}
+
+// Grid (ceil(B K / 16) + M, 1, 2d / 16): the row tiles of every unit's slots at position t (in
+// slot order q = b K + k), 16 slots a tile, laid end to end unit after unit (at most
+// ceil(B K / 16) + M of them; a workgroup past the last exits); workgroup (i, 0, ct) takes row
+// tile i and dv's columns 16 ct .. 16 ct + 15. Every workgroup of a row tile computes the head and
+// act of its slots (act is a quarter of the FLOPs); the ct = 0 one writes their dc, db, sigma and
+// carry. A is only read here.
+//
+// Latency is what bounds a position (a few MB of traffic, microseconds of arithmetic): the
+// position's units and cells come into LDS in one round trip, then every load of the head, of
+// act's first batch (weights, hidden values, biases) and of dv's weights is issued before the
+// head's arithmetic, and the reductions are DPP / permlane (no LDS round trips).
+template <typename P, int CPL, int ACT>
+__global__ __launch_bounds__(kCellThreads) void back_cell(hsn_back_sweep s, int t) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    using TL = Tile<P>;
+    using frag = typename TL::frag;
+    constexpr int kActSteps = TL::kStep == 32 ? 2 * CPL : 16 * CPL;  // d <= 64 CPL
+    constexpr int kActTiles = act_tiles<P, CPL>();
+    constexpr int R = kCellRows / kCellWaves;  // head rows per wavefront
+    const int ct = blockIdx.z;
+    const bool lead = ct == 0;
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int lr = lane & 15, lq = lane >> 4;
+    const int d = s.d, K = s.K, N = s.N, H = s.H, M = s.M;
+    const int BK = s.B * K;
+    const CellLds L = cell_lds<P>(d, H, BK);
+    int* rows = reinterpret_cast<int*>(lds + L.rows);
+    int* meta = reinterpret_cast<int*>(lds + L.meta);
+    float* sig_part = reinterpret_cast<float*>(lds + L.sig_part);
+    float* sig_gate = reinterpret_cast<float*>(lds + L.sig_gate);
+    float* sig_row = reinterpret_cast<float*>(lds + L.sig_row);
+    float* red = reinterpret_cast<float*>(lds + L.red);
+    uint8_t* ucache = lds + L.ucache;
+    int* ccache = reinterpret_cast<int*>(lds + L.ccache);
+    P* du = reinterpret_cast<P*>(lds + L.du);
+    P* dh = reinterpret_cast<P*>(lds + L.dh);
+
+    // ---- the position's units and cells; which unit's which row tile this workgroup takes ----
+    for (int q = tid; q < BK; q += kCellThreads) {
+        const int64_t slot = slot_at(s, t, q);
+        ucache[q] = static_cast<uint8_t>(min(max(s.units[slot], 0), M - 1));
+        const int cell = s.slots[slot];
+        ccache[q] = cell >= 0 && cell < N ? cell : -1;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int tiles_before = 0, unit = -1, tile = 0;
+        for (int j = 0; j < M && unit < 0; ++j) {
+            int cnt = 0;
+            for (int q0 = 0; q0 < BK; q0 += kWave)
+                cnt += __popcll(ballot(q0 + lane < BK && ucache[q0 + lane] == j));
+            const int tiles = (cnt + kCellRows - 1) / kCellRows;
+            if (static_cast<int>(blockIdx.x) < tiles_before + tiles) {
+                unit = j;
+                tile = blockIdx.x - tiles_before;
+            }
+            tiles_before += tiles;
+        }
+        if (lane < kCellRows) rows[lane] = -1;
+        if (unit >= 0) {
+            const int first = tile * kCellRows;
+            int base = 0;
+            for (int q0 = 0; q0 < BK && base < first + kCellRows; q0 += kWave) {
+                const int q = q0 + lane;
+                const bool mine = q < BK && ucache[q] == unit;
+                const uint64_t m = ballot(mine);
+                const int rank = base + lanes_below(m);
+                if (mine && rank >= first && rank < first + kCellRows) rows[rank - first] = q;
+                base += __popcll(m);
+            }
+        }
+        if (lane == 0) meta[0] = unit;
+    }
+    __syncthreads();
+    const int j = meta[0];
+    if (j < 0) return;  // past the last tile (uniform)
+
+    // ---- every load up to the products: the head's rows, act's first batch, dv's weights ----
+    float vb[R][CPL], vc[R][CPL], vh[R][CPL], vs[R][CPL], vy[R][CPL], vg[R][CPL];
+    float va[R][CPL], vf[R][CPL], vr[R][CPL], gain[CPL], gbias[CPL];
+    int64_t slotv[R];
+    bool okv[R], fastv[R];
+    float alv[R];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int x = lane + c * kWave;
+        gain[c] = x < d && s.cand_norm ? s.cand_gain[x] : 0.0f;
+        gbias[c] = x < d ? s.gate_bias[x] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int q = rows[R * wave + i];
+        slotv[i] = q >= 0 ? slot_at(s, t, q) : 0;
+        const int cell = q >= 0 ? ccache[q] : -1;
+        okv[i] = cell >= 0;
+        fastv[i] = okv[i] && cell < s.n_read;
+        alv[i] = q >= 0 ? s.alpha[slotv[i]] : 0.0f;
+        const int b = q >= 0 ? q / K : 0;
+        const int64_t bt = int64_t(b) * s.T + t;
+        const int64_t base = slotv[i] * d;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int x = lane + c * kWave;
+            const bool in = q >= 0 && x < d;
+            vb[i][c] = in ? s.b[base + x] : 0.0f;
+            vc[i][c] = in ? s.c[base + x] : 0.0f;
+            vh[i][c] = in ? s.h_old[base + x] : 0.0f;
+            vs[i][c] = in ? s.d_h_sel[base + x] : 0.0f;
+            vg[i][c] = in ? s.gate_pre[base + x] : 0.0f;
+            vy[i][c] = in && s.cand_norm ? s.y[base + x] : 0.0f;
+            va[i][c] = in && okv[i] ? s.A[(int64_t(b) * N + cell) * d + x] : 0.0f;
+            vf[i][c] = in && fastv[i] ? s.d_h_fast[(bt * s.n_read + cell) * d + x] : 0.0f;
+            vr[i][c] = in ? s.R[int64_t(b) * d + x] + s.d_q_post[bt * d + x] : 0.0f;
+        }
+    }
+    int qrow[4];
+    bool okrow[4];
+    int64_t srow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        qrow[i] = rows[4 * lq + i];
+        srow[i] = qrow[i] >= 0 ? slot_at(s, t, qrow[i]) : 0;
+        okrow[i] = qrow[i] >= 0 && ccache[qrow[i]] >= 0;
+    }
+    const int ka = round_up(d, TL::kStep);
+    const int steps = ka / TL::kStep;
+    const P* w2 = static_cast<const P*>(s.w2f) + int64_t(j) * H * d;
+    const P* hidden = static_cast<const P*>(s.hidden);
+    frag bf[kActTiles][kActSteps];
+    float hid[kActTiles][4], bias[kActTiles];
+    auto load_act = [&](int c00) {
+#pragma unroll
+        for (int u = 0; u < kActTiles; ++u) {
+            const int h = c00 + 16 * kCellWaves * u + lr;
+            const bool hin = h < H;
+#pragma unroll
+            for (int st = 0; st < kActSteps; ++st) {
+                const int kq = st * TL::kStep + TL::kPer * lq;
+                bf[u][st] = TL::glb(w2 + int64_t(hin ? h : 0) * d + kq,
+                                    st < steps && hin && kq < d);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                hid[u][i] = okrow[i] && hin ? to_f32(hidden[srow[i] * H + h]) : 0.0f;
+            bias[u] = hin ? s.b1[int64_t(j) * H + h] : 0.0f;
+        }
+    };
+    load_act(16 * wave);
+    const int kt = H + d;
+    const int dv_steps = round_up(kt, TL::kStep) / TL::kStep;
+    const int col = ct * kCellCols + lr;
+    const bool cin = col < 2 * d;
+    const P* w1 = static_cast<const P*>(s.w1f) + (int64_t(j) * 2 * d + (cin ? col : 0)) * kt;
+    frag bv[kDvChunk];
+    auto load_dv = [&](int s0) {
+#pragma unroll
+        for (int u = 0; u < kDvChunk; ++u) {
+            const int st = s0 + u * kCellWaves;
+            const int kq = st * TL::kStep + TL::kPer * lq;
+            bv[u] = TL::glb(w1 + kq, st < dv_steps && cin && kq < kt);
+        }
+    };
+    load_dv(wave);
+
+    // ---- head: the carry, dc / db, the candidate's and the gate's backward ----
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int r = R * wave + i;
+        const int q = rows[r];
+        P* du_row = du + r * L.du_stride;
+        P* dg_row = dh + r * L.dh_stride + H;
+        const bool ok = okv[i];
+        float dgv[CPL], scaled[CPL];
+        float sum_yy = 0.0f, sum_ys = 0.0f, sum_gate = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int x = lane + c * kWave;
+            dgv[c] = scaled[c] = 0.0f;
+            if (q < 0 || x >= d) continue;
+            const float bx = vb[i][c], cx = vc[i][c];
+            float dc = 0.0f, db = 0.0f;
+            if (ok) {
+                float a = va[i][c];
+                if (fastv[i]) a = a + vf[i][c];  // the decoder's read of a fast cell
+                const float carried = a + vs[i][c];
+                const float share = vr[i][c] / static_cast<float>(N);
+                const float g = carried + share;
+                dc = bx * g;
+                db = (cx - vh[i][c]) * g;
+                if (lead) s.carry[int64_t(q) * d + x] = (1.0f - bx) * carried - bx * share;
+            }
+            if (lead) {
+                s.dc[slotv[i] * d + x] = dc;
+                s.db[slotv[i] * d + x] = db;
+            }
+            const float dz = dc * (1.0f - cx * cx);
+            if (s.cand_norm) {
+                scaled[c] = gain[c] * (alv[i] * dz);
+                sum_yy += vy[i][c] * vy[i][c];
+                sum_ys += vy[i][c] * scaled[c];
+            } else {
+                scaled[c] = alv[i] * dz;
+            }
+            const float dg = db * bx * (1.0f - bx);
+            dgv[c] = ok ? dg : 0.0f;
+            if (ok) sum_gate += dgv[c] * (vg[i][c] - gbias[c]);
+        }
+        float rho = 0.0f, mean_ys = 0.0f;
+        if (s.cand_norm) {
+            sum_yy = wave_sum(sum_yy);
+            sum_ys = wave_sum(sum_ys);
+            rho = 1.0f / sqrtf(sum_yy / static_cast<float>(d) + s.cand_eps);
+            mean_ys = sum_ys / static_cast<float>(d);
+        }
+        sum_gate = wave_sum(sum_gate);
+        if (lane == 0) sig_gate[r] = ok ? sum_gate : 0.0f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int x = lane + c * kWave;
+            if (x >= d) continue;
+            float v = scaled[c];
+            if (s.cand_norm) v = rho * scaled[c] - rho * rho * rho * vy[i][c] * mean_ys;
+            du_row[x] = from_f32<P>(ok ? v : 0.0f);
+            dg_row[x] = from_f32<P>(dgv[c]);
+        }
+        for (int x = d + lane; x < L.du_stride; x += kWave) du_row[x] = from_f32<P>(0.0f);
+        for (int x = d + lane; x < L.dh_stride - H; x += kWave) dg_row[x] = from_f32<P>(0.0f);
+    }
+    __syncthreads();
+
+    // ---- act = du . (W_out W2_j^T); dh = act'(hidden) act; sigma's hidden part ----
+    float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c00 = 16 * wave; c00 < H; c00 += 16 * kCellWaves * kActTiles) {
+        if (c00 != 16 * wave) load_act(c00);  // the first batch is in flight already
+#pragma unroll
+        for (int u = 0; u < kActTiles; ++u) {
+            const int h = c00 + 16 * kCellWaves * u + lr;
+            const bool hin = h < H;
+            v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int st = 0; st < kActSteps; ++st)
+                if (st < steps)
+                    acc = TL::mma(
+                        TL::lds(du + lr * L.du_stride + st * TL::kStep + TL::kPer * lq),
+                        bf[u][st], acc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float v = 0.0f;
+                if (okrow[i] && hin) {
+                    v = round_p<P>(acc[i]) * act_grad_t<ACT>(hid[u][i]);
+                    part[i] += v * (hid[u][i] - bias[u]);
+                }
+                if (hin) dh[(4 * lq + i) * L.dh_stride + h] = from_f32<P>(v);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // the 16 lanes of a row group hold the same rows
+        const float v = group_sum<16>(part[i]);
+        if (lr == 0) sig_part[wave * kCellRows + 4 * lq + i] = v;
+    }
+    // the ds epilogue's operands, in flight under the dv product
+    float rms4[4], st4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        rms4[i] = 0.0f;
+        st4[i] = 0.0f;
+        if (wave == 0 && s.cell_norm && qrow[i] >= 0 && cin) {
+            rms4[i] = s.rms[srow[i]];
+            st4[i] = col < d ? s.h_old[srow[i] * d + col] : s.mv[srow[i] * d + col - d];
+        }
+    }
+    __syncthreads();
+    if (tid < kCellRows) {
+        float sg = sig_gate[tid];
+        for (int w = 0; w < kCellWaves; ++w) sg = sg + sig_part[w * kCellRows + tid];
+        sig_row[tid] = sg;
+        if (lead && rows[tid] >= 0) s.sigma[rows[tid]] = sg;
+    }
+
+    // ---- dv's column tile ct = [dh ; dg] . w1f_j; the reduction split over the wavefronts ----
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = wave; s0 < dv_steps; s0 += kCellWaves * kDvChunk) {
+        if (s0 != wave) load_dv(s0);  // the first chunk is in flight already
+#pragma unroll
+        for (int u = 0; u < kDvChunk; ++u) {
+            const int st = s0 + u * kCellWaves;
+            if (st < dv_steps)
+                acc = TL::mma(TL::lds(dh + lr * L.dh_stride + st * TL::kStep + TL::kPer * lq),
+                              bv[u], acc);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * kWave + lane) * 4 + i] = acc[i];
+    __syncthreads();
+    if (wave == 0) {
+        // the product's value as the reference's product dtype stores it, then the cell norm's
+        // backward: ds = r dv - (r^2 / in_dim) sigma [h_old ; m V] (ds = dv without the norm)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v = red[lane * 4 + i];
+            for (int w = 1; w < kCellWaves; ++w) v = v + red[(w * kWave + lane) * 4 + i];
+            if (qrow[i] < 0 || !cin) continue;
+            v = round_p<P>(v);
+            if (s.cell_norm) {
+                const float r = rms4[i];
+                const float back = (r * r / static_cast<float>(s.in_dim)) * sig_row[4 * lq + i];
+                v = r * v - back * st4[i];
+            }
+            s.ds[int64_t(qrow[i]) * 2 * d + col] = okrow[i] ? v : 0.0f;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// back_cell_tail: the tail after back_cell, a wavefront per touched cell
+// ------------------------------------------------------------------------------------------
+constexpr int kCellTailCells = 32;  // cells per workgroup
+
+struct CellTailLds {
+    int slot_of, flag, list, count, ds, bytes;
+};
+__host__ __device__ inline CellTailLds cell_tail_lds(int N, int K, int d) {
+    CellTailLds L;
+    L.slot_of = 0;                                // int [N]
+    L.flag = L.slot_of + 4 * N;                   // int [32]
+    L.list = L.flag + 4 * kCellTailCells;         // int [32]
+    L.count = L.list + 4 * kCellTailCells;        // int
+    L.ds = round_up(L.count + 4, 16);             // float [K][2d]
+    L.bytes = L.ds + 4 * K * 2 * d;
+    return L;
+}
+
+// Grid (N / 32, B): workgroup (i, b) updates row b's cells 32 i .. 32 i + 31 that position t
+// touches (the selected cells, their message sources, the fast-read cells). Per such cell n and
+// column x, in this order: a = carry of n's slot if n is selected, else A[n] (+ d_h_fast if n is
+// a fast-read cell); + ds_h of n's slot; + the edge weight times ds_m of each selected target of
+// n, in n's out-adjacency order. Then R = (R + d_q_post) + d_q_pre, and a reset zeroes the row.
+template <int CPL>
+__global__ __launch_bounds__(kBackThreads) void back_cell_tail(hsn_back_sweep s, int t) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int row = blockIdx.y;
+    const int cell0 = blockIdx.x * kCellTailCells;
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int d = s.d, K = s.K, N = s.N;
+    const int64_t bt = int64_t(row) * s.T + t;
+    float* A = s.A + int64_t(row) * N * d;
+    const int cell_end = min(cell0 + kCellTailCells, N);
+    if (s.reset[bt] != 0) {  // the row restarts: its cotangent before position t is zero
+        for (int64_t i = int64_t(cell0) * d + tid; i < int64_t(cell_end) * d; i += kBackThreads)
+            A[i] = 0.0f;
+        if (blockIdx.x == 0)
+            for (int x = tid; x < d; x += kBackThreads) s.R[int64_t(row) * d + x] = 0.0f;
+        return;
+    }
+    const CellTailLds L = cell_tail_lds(N, K, d);
+    int* slot_of = reinterpret_cast<int*>(lds + L.slot_of);
+    int* flag = reinterpret_cast<int*>(lds + L.flag);
+    int* list = reinterpret_cast<int*>(lds + L.list);
+    int* count = reinterpret_cast<int*>(lds + L.count);
+    float* ds = reinterpret_cast<float*>(lds + L.ds);
+    for (int n = tid; n < N; n += kBackThreads) slot_of[n] = -1;
+    if (tid < kCellTailCells) flag[tid] = cell0 + tid < min(s.n_read, cell_end) ? 1 : 0;
+    __syncthreads();
+    for (int k = wave; k < K; k += kBackWaves) {
+        const int cell = s.slots[bt * K + k];
+        const bool ok = cell >= 0 && cell < N;
+        const float* dsrow = s.ds + (int64_t(row) * K + k) * 2 * d;
+        for (int x = lane; x < 2 * d; x += kWave) ds[k * 2 * d + x] = dsrow[x];
+        if (!ok) continue;
+        if (lane == 0) {
+            slot_of[cell] = k;
+            if (cell >= cell0 && cell < cell_end) flag[cell - cell0] = 1;
+        }
+        for (int e = lane; e < s.d_in; e += kWave) {
+            const int src = s.in_src[int64_t(cell) * s.d_in + e];
+            if (src >= cell0 && src < cell_end) flag[src - cell0] = 1;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const bool f = lane < kCellTailCells && flag[lane] != 0;
+        const uint64_t m = ballot(f);
+        if (f) list[lanes_below(m)] = cell0 + lane;
+        if (lane == 0) *count = __popcll(m);
+    }
+    __syncthreads();
+    const int touched = *count;
+    for (int i = wave; i < touched; i += kBackWaves) {
+        const int n = list[i];
+        const int own = slot_of[n];
+        float a[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int x = lane + c * kWave;
+            if (x >= d) continue;
+            a[c] = own >= 0 ? s.carry[(int64_t(row) * K + own) * d + x] : A[int64_t(n) * d + x];
+            if (own < 0 && n < s.n_read) a[c] = a[c] + s.d_h_fast[(bt * s.n_read + n) * d + x];
+            if (own >= 0) a[c] = a[c] + ds[own * 2 * d + x];
+        }
+        for (int j0 = 0; j0 < s.d_out; j0 += kWave) {
+            // lane e: out-edge j0 + e of n, its target's slot (or -1) and weight
+            int ke = -1;
+            float we = 0.0f;
+            if (j0 + lane < s.d_out) {
+                const int target = s.out_tgt[int64_t(n) * s.d_out + j0 + lane];
+                if (target >= 0 && target < N) ke = slot_of[target];
+                we = s.out_w[int64_t(n) * s.d_out + j0 + lane];
+            }
+            const int jn = min(kWave, s.d_out - j0);
+            for (int e = 0; e < jn; ++e) {
+                const int kj = __shfl(ke, e, kWave);
+                const float wj = __shfl(we, e, kWave);
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    const int x = lane + c * kWave;
+                    if (x >= d) continue;
+                    const float add = kj >= 0 ? wj * ds[kj * 2 * d + d + x] : 0.0f;
+                    a[c] = a[c] + add;
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int x = lane + c * kWave;
+            if (x < d) A[int64_t(n) * d + x] = a[c];
+        }
+    }
+    if (blockIdx.x == 0)
+        for (int x = tid; x < d; x += kBackThreads) {
+            const float r = s.R[int64_t(row) * d + x] + s.d_q_post[bt * d + x];
+            s.R[int64_t(row) * d + x] = r + s.d_q_pre[bt * d + x];
+        }
 }
 
 void back_check(const hsn_back_sweep* s) {
@@ -320,6 +859,29 @@ void back_check(const hsn_back_sweep* s) {
                           s->op1, s->op2, s->act, s->dv, s->dc, s->db};
     for (const void* p : need)
         HSN_REQUIRE(p != nullptr, HSN_ERR_INVALID_ARGUMENT, "reverse sweep: a buffer is NULL");
+}
+
+void cell_check(const hsn_back_sweep* s) {
+    back_check(s);
+    HSN_REQUIRE(s->d % 8 == 0 && s->H % 8 == 0, HSN_ERR_INVALID_ARGUMENT,
+                "fused reverse sweep step: d and H must be multiples of 8");
+    HSN_REQUIRE(s->d <= kCellMaxCpl * kWave, HSN_ERR_INVALID_ARGUMENT,
+                "fused reverse sweep step: d above 128");
+    HSN_REQUIRE(int64_t(s->B) * s->K <= kCellMaxSlots && s->M <= 256, HSN_ERR_INVALID_ARGUMENT,
+                "fused reverse sweep step: more than 4096 slots a position, or more than 256 "
+                "units");
+    const int BK = s->B * s->K;
+    const int lds = s->product_dtype == HSN_DTYPE_BF16 ? cell_lds<bf16_t>(s->d, s->H, BK).bytes
+                                                       : cell_lds<float>(s->d, s->H, BK).bytes;
+    HSN_REQUIRE(lds <= kMaxLds, HSN_ERR_INVALID_ARGUMENT,
+                "fused reverse sweep step: 16 slots' operand rows exceed 64 KiB of LDS");
+    HSN_REQUIRE(s->w2f != nullptr && s->w1f != nullptr && s->carry != nullptr &&
+                    s->ds != nullptr,
+                HSN_ERR_INVALID_ARGUMENT,
+                "fused reverse sweep step: w2f / w1f / carry / ds is NULL");
+    HSN_REQUIRE(cell_tail_lds(s->N, s->K, s->d).bytes <= kMaxLds, HSN_ERR_INVALID_ARGUMENT,
+                "fused reverse sweep step: the tail's slot table and slot terms (4 N + 8 K d "
+                "bytes) exceed 64 KiB of LDS");
 }
 
 void check_t(const hsn_back_sweep* s, int t) {
@@ -376,11 +938,84 @@ extern "C" int hsn_win_back_tail(const hsn_back_sweep* sweep, int t, void* strea
                     static_cast<unsigned>(s.B));
     const size_t lds = static_cast<size_t>(tail_lds(s.N, s.K, s.d).bytes);
     if (s.product_dtype == HSN_DTYPE_BF16)
-        hipLaunchKernelGGL(back_tail<bf16_t>, grid, dim3(kBackThreads), lds, as_stream(stream), s,
-                           t);
+        hipLaunchKernelGGL((back_tail<bf16_t>), grid, dim3(kBackThreads), lds,
+                           as_stream(stream), s, t);
     else
-        hipLaunchKernelGGL(back_tail<float>, grid, dim3(kBackThreads), lds, as_stream(stream), s,
-                           t);
+        hipLaunchKernelGGL((back_tail<float>), grid, dim3(kBackThreads), lds,
+                           as_stream(stream), s, t);
+    HSN_HIP(hipGetLastError());
+    HSN_ABI_END
+}
+
+extern "C" int hsn_win_back_cell_check(const hsn_back_sweep* sweep) {
+    HSN_ABI_BEGIN
+    cell_check(sweep);
+    HSN_ABI_END
+}
+
+template <typename P, int CPL>
+void launch_cell(const hsn_back_sweep& s, int t, dim3 grid, size_t lds, hipStream_t st) {
+    switch (s.activation) {
+        case HSN_ACT_GELU:
+            hipLaunchKernelGGL((back_cell<P, CPL, HSN_ACT_GELU>), grid, dim3(kCellThreads), lds, st,
+                               s, t);
+            break;
+        case HSN_ACT_RELU:
+            hipLaunchKernelGGL((back_cell<P, CPL, HSN_ACT_RELU>), grid, dim3(kCellThreads), lds, st,
+                               s, t);
+            break;
+        case HSN_ACT_SILU:
+            hipLaunchKernelGGL((back_cell<P, CPL, HSN_ACT_SILU>), grid, dim3(kCellThreads), lds, st,
+                               s, t);
+            break;
+        default:
+            hipLaunchKernelGGL((back_cell<P, CPL, HSN_ACT_TANH>), grid, dim3(kCellThreads), lds, st,
+                               s, t);
+    }
+}
+
+extern "C" int hsn_win_back_cell(const hsn_back_sweep* sweep, int t, void* stream) {
+    HSN_ABI_BEGIN
+    cell_check(sweep);
+    check_t(sweep, t);
+    const hsn_back_sweep s = *sweep;
+    const int64_t rows = int64_t(s.B) * s.K;
+    const dim3 grid(static_cast<unsigned>((rows + kCellRows - 1) / kCellRows + s.M), 1u,
+                    static_cast<unsigned>((2 * s.d + kCellCols - 1) / kCellCols));
+    const int cpl = (s.d + kWave - 1) / kWave;
+    const bool bf = s.product_dtype == HSN_DTYPE_BF16;
+    const int BK = s.B * s.K;
+    const size_t lds = static_cast<size_t>(bf ? cell_lds<bf16_t>(s.d, s.H, BK).bytes
+                                              : cell_lds<float>(s.d, s.H, BK).bytes);
+    hipStream_t st = as_stream(stream);
+    if (bf) {
+        if (cpl == 1) launch_cell<bf16_t, 1>(s, t, grid, lds, st);
+        else launch_cell<bf16_t, 2>(s, t, grid, lds, st);
+    } else {
+        if (cpl == 1) launch_cell<float, 1>(s, t, grid, lds, st);
+        else launch_cell<float, 2>(s, t, grid, lds, st);
+    }
+    HSN_HIP(hipGetLastError());
+    HSN_ABI_END
+}
+
+extern "C" int hsn_win_back_cell_tail(const hsn_back_sweep* sweep, int t, void* stream) {
+    HSN_ABI_BEGIN
+    cell_check(sweep);
+    check_t(sweep, t);
+    const hsn_back_sweep s = *sweep;
+    const dim3 grid(static_cast<unsigned>((s.N + kCellTailCells - 1) / kCellTailCells),
+                    static_cast<unsigned>(s.B));
+    const size_t lds = static_cast<size_t>(cell_tail_lds(s.N, s.K, s.d).bytes);
+    const int cpl = (s.d + kWave - 1) / kWave;
+    hipStream_t st = as_stream(stream);
+#define HSN_TAIL(C) \
+    hipLaunchKernelGGL((back_cell_tail<C>), grid, dim3(kBackThreads), lds, st, s, t)
+    if (cpl == 1) HSN_TAIL(1);
+    else if (cpl == 2) HSN_TAIL(2);
+    else if (cpl == 3) HSN_TAIL(3);
+    else HSN_TAIL(4);
+#undef HSN_TAIL
     HSN_HIP(hipGetLastError());
     HSN_ABI_END
 }

@@ -131,7 +131,7 @@ class _Struct(ctypes.Structure):
             "A", "R", "sigma", "c", "b", "h_old", "y", "gate_pre", "mv", "alpha", "rms", "hidden",
             "slots", "units", "reset", "d_q_pre", "d_q_post", "d_h_sel", "d_h_fast", "cand_gain",
             "gate_bias", "b1", "out_tgt", "out_w", "in_src", "op1", "op2", "act", "dv", "dc",
-            "db")]
+            "db", "w2f", "w1f", "carry", "ds")]
 
 
 def _product_code(dtype: torch.dtype) -> int:
@@ -172,7 +172,8 @@ class ReverseSweep:
 
     def __init__(self, shape: SweepShape, consts: Any, *, device: torch.device,
                  state_dtype: torch.dtype = torch.float32,
-                 product_dtype: torch.dtype = torch.float32, limits: Any = None) -> None:
+                 product_dtype: torch.dtype = torch.float32, limits: Any = None,
+                 fused: Optional[bool] = None) -> None:
         B, T, K, N, d, H, M, F, n_read, n, d_out = shape
         if device.type != "cuda":
             raise ValueError("the reverse sweep's kernels run on a ROCm device")
@@ -224,6 +225,10 @@ class ReverseSweep:
         self.op1, self.op2 = torch.zeros(rows, M * d, **prod), torch.zeros(rows, M * H + d, **prod)
         self.act, self.dv = torch.zeros(rows, H, **prod), torch.zeros(rows, 2 * d, **prod)
         self.dc, self.db = torch.zeros(B, T, K, d, **f32), torch.zeros(B, T, K, d, **f32)
+        self.w2f = torch.zeros(M, H, d, **prod)
+        self.w1f = torch.zeros(M, 2 * d, H + d, **prod)
+        self.carry = torch.zeros(rows, d, **f32)
+        self.ds = torch.zeros(rows, 2 * d, **f32)
         self._graph: Optional[torch.cuda.CUDAGraph] = None
         s = _Struct()
         for name, value in (("B", B), ("T", T), ("K", K), ("N", N), ("d", d), ("H", H), ("M", M),
@@ -236,11 +241,20 @@ class ReverseSweep:
         for name in ("A", "R", "sigma", "c", "b", "h_old", "y", "gate_pre", "mv", "alpha", "rms",
                      "hidden", "slots", "units", "reset", "d_q_pre", "d_q_post", "d_h_sel",
                      "cand_gain", "gate_bias", "b1", "out_tgt", "out_w", "in_src", "op1", "op2",
-                     "act", "dv", "dc", "db"):
+                     "act", "dv", "dc", "db", "w2f", "w1f", "carry", "ds"):
             setattr(s, name, getattr(self, name).data_ptr())
         s.d_h_fast = self.d_h_fast.data_ptr() if n_read else None
         self._struct = s
         _lib.call("hsn_win_back_check", ctypes.byref(s))
+        lib = _lib.library()
+        takes_fused = lib.hsn_win_back_cell_check(ctypes.byref(s)) == _lib.HSN_OK
+        if fused and not takes_fused:
+            raise ValueError("the fused step does not take this sweep: "
+                             + lib.hsn_win_last_error().decode(errors="replace"))
+        #: One launch for the head, both products and the middle (``hsn_win_back_cell``), with
+        #: only each unit's own blocks multiplied; else the reference's three glue steps around
+        #: two all-units GEMMs.
+        self.fused = takes_fused if fused is None else bool(fused)
 
     # -- loading a window ------------------------------------------------------------------------
 
@@ -254,7 +268,7 @@ class ReverseSweep:
         w_out = consts.w_out.to(self.device, torch.float32)
         w2 = consts.w2.to(self.device, torch.float32)  # [M, H, d]
         w2_t = w2.permute(0, 2, 1).reshape(M, d, H)
-        self.w2_t.copy_(torch.matmul(w_out, w2_t).reshape(M * d, H))
+        self.w2_t.copy_(torch.matmul(w_out, w2_t).reshape(M * d, H))  # row j d + k
         w1 = consts.w1_state.to(self.device, torch.float32)  # [M, 2d, H]
         w1_t = torch.cat([w1.permute(0, 2, 1).reshape(M * H, 2 * d),
                           consts.gate_state.to(self.device, torch.float32)], dim=0)
@@ -268,7 +282,13 @@ class ReverseSweep:
             gain = gain.to(self.device, torch.float32)
             fold[:d, :d] = torch.diag(gain[:d])
             fold[d:, d:] = gain[d:, None] * v
-        self.w1_state_t.copy_(w1_t @ fold)
+        folded = w1_t @ fold  # [M H + d, 2d]
+        self.w1_state_t.copy_(folded)
+        second = torch.matmul(w_out, w2_t)  # [M, d, H]: unit j's W_out W2_j^T
+        self.w2f.copy_(second.transpose(1, 2))
+        gate_rows = folded[M * H:]
+        self.w1f.copy_(torch.cat([folded[:M * H].reshape(M, H, 2 * d),
+                                  gate_rows.expand(M, d, 2 * d)], dim=1).transpose(1, 2))
         if consts.cand_gain is not None:
             self.cand_gain.copy_(consts.cand_gain)
         self.gate_bias.copy_(consts.gate_bias)
@@ -380,9 +400,14 @@ class ReverseSweep:
         self.op2.zero_()
 
     def step(self, t: int) -> None:
-        """Position ``t``: the three glue steps and the two transposed products between them."""
+        """Position ``t``: the fused step and its tail, or the three glue steps and the two
+        transposed products between them."""
         stream = _lib.stream_of(self.device)
         ref = ctypes.byref(self._struct)
+        if self.fused:
+            _lib.call("hsn_win_back_cell", ref, t, stream)
+            _lib.call("hsn_win_back_cell_tail", ref, t, stream)
+            return
         _lib.call("hsn_win_back_head", ref, t, stream)
         torch.mm(self.op1, self.w2_t, out=self.act)
         _lib.call("hsn_win_back_mid", ref, t, stream)
@@ -396,8 +421,9 @@ class SweepRunner:
     HIP graph captured at the shape's first window. Called with ``state_gradient_backward``'s
     arguments; returns ``None`` for what it does not take, and the caller keeps its PyTorch sweep."""
 
-    def __init__(self, *, graph: bool = True) -> None:
+    def __init__(self, *, graph: bool = True, fused: Optional[bool] = None) -> None:
         self.graph = graph
+        self.fused = fused
         self.sweeps: dict[tuple, ReverseSweep] = {}
         #: Windows swept, and how many of them captured a graph.
         self.calls = 0
@@ -433,7 +459,7 @@ class SweepRunner:
         sweep = self.sweeps.get(key)
         if sweep is None:
             sweep = ReverseSweep(shape, consts, device=device, state_dtype=c.dtype,
-                                 product_dtype=product_dtype)
+                                 product_dtype=product_dtype, fused=self.fused)
             self.sweeps[key] = sweep
         sweep.load(c, b, h_old, cells, units, valid, reset, d_q_pre, d_q_post, d_h_sel, d_h_fast,
                    record, consts)

@@ -96,6 +96,13 @@ typedef struct hsn_back_sweep {
     /* what the sweep returns */
     float* dc; /* [B, T, K, d] */
     float* db; /* [B, T, K, d] */
+    /* the fused step's weights (hsn_win_back_cell), in product_dtype, each unit's matrix with
+     * its reduction index contiguous: w2f [M, H, d] holds (W_out W2_j^T)^T, w1f [M, 2 d, H + d]
+     * holds ([W1_s; G_s]^T blockdiag(diag(g_h), diag(g_m) V))^T restricted to unit j's rows */
+    const void* w2f;
+    const void* w1f;
+    float* carry; /* [B K, d]: the fused step's (1 - b) carried - b R / N per slot, for its tail */
+    float* ds;    /* [B K, 2 d]: the fused step's cell-norm backward [ds_h ; ds_m] per slot */
 } hsn_back_sweep;
 
 /* Whether the glue steps take this sweep (sizes, dtypes, LDS): HSN_OK, or an error status with
@@ -111,6 +118,25 @@ int hsn_win_back_mid(const hsn_back_sweep* sweep, int t, void* stream);
 
 /* The tail of position t (hsn_win_back_tail; state_sweep.py tail_reference). */
 int hsn_win_back_tail(const hsn_back_sweep* sweep, int t, void* stream);
+
+/*
+ * No counterpart in the reference: the head, both products and the middle of position t as one
+ * launch on the matrix cores. A workgroup takes 16 slots of one unit (the slots of unit j in slot
+ * order), runs the head on them, then act = du . (W_out W2_j^T) and dv = [dh ; dg] . w1f_j on
+ * v_mfma tiles (bf16 in, fp32 accumulation; fp32 tiles for fp32 products) with only the unit's
+ * own blocks (the all-units layout multiplies M times as much, mostly zeros), writing dc, db,
+ * sigma, each slot's carry and its cell-norm backward ds (A itself is only read). The operands op1 / op2 and act are not
+ * used; values are rounded to product_dtype where the reference's products store them. Follow it
+ * with hsn_win_back_cell_tail (not hsn_win_back_tail): the tail writes the selected cells' rows
+ * of A from the carry, R, and the unselected fast-read cells. hsn_win_back_cell_check says whether a sweep takes this step
+ * (d % 8 == 0, H % 8 == 0 and its LDS).
+ */
+int hsn_win_back_cell_check(const hsn_back_sweep* sweep);
+int hsn_win_back_cell(const hsn_back_sweep* sweep, int t, void* stream);
+
+/* The tail after hsn_win_back_cell: hsn_win_back_tail's work, plus R += d_q_post[t] (before its
+ * d_q_pre[t]) and the decoder's cotangent of the fast-read cells no slot selected. */
+int hsn_win_back_cell_tail(const hsn_back_sweep* sweep, int t, void* stream);
 
 #ifdef __cplusplus
 }

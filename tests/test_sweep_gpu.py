@@ -65,60 +65,74 @@ CASES = {
 }
 
 
-@pytest.mark.parametrize("name", sorted(CASES))
-def test_sweep_matches_oracle(dev, name):
+def _run(args, kw, fused, graph=False):
+    """The runner on one window with the fused step forced on or off; skips where the fused step
+    does not take the shape."""
     from hsn_amd.state_sweep import SweepRunner
 
-    print(f"case {name}", flush=True)
+    try:
+        return SweepRunner(graph=graph, fused=fused)(*args, **kw)
+    except ValueError as e:
+        if fused and "fused step" in str(e):
+            pytest.skip(str(e))
+        raise
+
+
+@pytest.fixture(params=[True, False], ids=["fused", "three_steps"])
+def fused(request):
+    """Every sweep test runs the fused step (hsn_win_back_cell) and the three glue steps around
+    the all-units GEMMs."""
+    return request.param
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_sweep_matches_oracle(dev, name, fused):
+    print(f"case {name} fused={fused}", flush=True)
     p = sweep_problem(**CASES[name])
     want_dc, want_db = sweep_oracle(p)
     args, kw = _args(p, dev)
-    out = SweepRunner(graph=False)(*args, **kw)
+    out = _run(args, kw, fused)
     assert out is not None, "the runner declined a shape it takes"
     _close(out[0], want_dc, F32_TOL, f"{name} dL/dc")
     _close(out[1], want_db, F32_TOL, f"{name} dL/db")
 
 
-@pytest.mark.parametrize("name", ["norms_gelu", "model_shape"])
-def test_sweep_with_bf16_products(dev, name):
+@pytest.mark.parametrize("name", ["norms_gelu", "model_shape", "fast_read_resets", "wide_d"])
+def test_sweep_with_bf16_products(dev, name, fused):
     """Autocast's sweep: the hidden record, the operands and the products in bf16 (fp32
     accumulation), the state's cotangent in fp32."""
-    from hsn_amd.state_sweep import SweepRunner
-
-    print(f"case {name} bf16", flush=True)
+    print(f"case {name} bf16 fused={fused}", flush=True)
     p = sweep_problem(**CASES[name])
     want_dc, want_db = sweep_oracle(p)
     args, kw = _args(p, dev, torch.bfloat16)
-    out = SweepRunner(graph=False)(*args, **kw)
+    out = _run(args, kw, fused)
     assert out is not None
     _close(out[0], want_dc, BF16_TOL, f"{name} bf16 dL/dc")
     _close(out[1], want_db, BF16_TOL, f"{name} bf16 dL/db")
 
 
-def test_fixed_unit_slots_take_the_same_sweep(dev):
-    """Leading slots with a fixed unit (``n_fast``) are swept in the all-units layout: the same
-    values as without the distinction."""
-    from hsn_amd.state_sweep import SweepRunner
-
+def test_fixed_unit_slots_take_the_same_sweep(dev, fused):
+    """Leading slots with a fixed unit (``n_fast``) are swept like the others: the same values as
+    without the distinction."""
     p = sweep_problem(B=2, T=8, K=4, N=20, d=16, H=24, M=4, seed=11)
     args, kw = _args(p, dev)
-    plain = SweepRunner(graph=False)(*args, **kw)
-    fixed = SweepRunner(graph=False)(*args, n_fast=2, **kw)
+    plain = _run(args, kw, fused)
+    fixed = _run(args, dict(kw, n_fast=2), fused)
     assert plain is not None and fixed is not None
     assert torch.equal(plain[0], fixed[0]) and torch.equal(plain[1], fixed[1])
 
 
-def test_graph_replays_equal_the_eager_sweep(dev):
+def test_graph_replays_equal_the_eager_sweep(dev, fused):
     """One runner captures the shape's graph at its first window and replays it for the next
     ones (new values loaded between replays, eager work in between): every window equals an
     eager sweep of the same window bit for bit, and the oracle."""
     from hsn_amd.state_sweep import SweepRunner
 
-    graphed = SweepRunner(graph=True)
-    eager = SweepRunner(graph=False)
+    graphed = SweepRunner(graph=True, fused=fused)
+    eager = SweepRunner(graph=False, fused=fused)
     cell = None
     for seed in (21, 22, 23):
-        p = sweep_problem(B=3, T=10, K=4, N=30, d=16, H=32, M=3, seed=seed)
+        p = sweep_problem(B=3, T=10, K=4, N=30, d=16, H=32, M=3, seed=seed, n_read=2)
         cell = p["consts"] if cell is None else cell
         p["consts"] = cell  # one model: its weights and message graph stay between windows
         args, kw = _args(p, dev)
