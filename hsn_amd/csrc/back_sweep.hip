@@ -28,6 +28,9 @@
 #pragma clang fp contract(off)
 
 namespace hsn {
+// Raise a kernel's dynamic-LDS limit to 160 KiB once per (kernel, device) (runtime.cpp).
+hipError_t allow_lds_raw(const void* kernel, size_t lds);
+
 namespace {
 
 constexpr int kBackThreads = 256;
@@ -35,6 +38,7 @@ constexpr int kBackWaves = kBackThreads / kWave;
 constexpr int kMaxColsPerLane = 4;  // d <= 256
 constexpr int kTailCells = 64;      // cells per tail workgroup
 constexpr int kMaxLds = 64 * 1024;
+constexpr int kCellMaxLds = 160 * 1024;  // the fused step raises its kernels' dynamic-LDS limit
 
 template <typename P>
 __device__ __forceinline__ float ld(const void* p, int64_t i) {
@@ -336,16 +340,25 @@ struct Tile<float> {  // v_mfma_f32_16x16x4_f32
     }
 };
 
-// The activation's derivative with the activation fixed at compile time (one branch of code).
+// The activation's derivative with the activation fixed at compile time (one branch of code),
+// with products by reciprocal constants and exp from the hardware's exp2 (a few ulps; the exact
+// divisions and the correctly rounded expf cost more instructions than the rest of the step's
+// epilogue): Phi(x) + x phi(x) for the exact GELU, s (1 + x (1 - s)) for SiLU, 1 - tanh^2.
+constexpr float kRsqrt2f = 0.70710678118654752f;
+constexpr float kRsqrt2Pif = 0.39894228040143268f;
+constexpr float kLog2ef = 1.44269504088896341f;
+__device__ __forceinline__ float exp_fast(float x) {
+    return __builtin_amdgcn_exp2f(x * kLog2ef);
+}
 template <int ACT>
 __device__ __forceinline__ float act_grad_t(float x) {
     if constexpr (ACT == HSN_ACT_GELU) {
-        const float cdf = 0.5f * (1.0f + erff(x / 1.41421356237309515f));
-        return cdf + x * expf(-0.5f * x * x) / 2.50662827463100024f;
+        const float cdf = 0.5f * (1.0f + erff(x * kRsqrt2f));
+        return cdf + x * (exp_fast(-0.5f * x * x) * kRsqrt2Pif);
     } else if constexpr (ACT == HSN_ACT_RELU) {
         return x > 0.0f ? 1.0f : 0.0f;
     } else if constexpr (ACT == HSN_ACT_SILU) {
-        const float sg = 1.0f / (1.0f + expf(-x));
+        const float sg = __builtin_amdgcn_rcpf(1.0f + exp_fast(-x));
         return sg * (1.0f + x * (1.0f - sg));
     } else {
         const float th = tanhf(x);
@@ -358,7 +371,7 @@ __host__ __device__ inline int round_up(int x, int m) { return (x + m - 1) / m *
 constexpr int kCellMaxSlots = 4096;  // B K on the fused step: the position's slots in LDS
 
 struct CellLds {
-    int rows, meta, sig_part, sig_gate, sig_row, red, ucache, ccache, du, dh, du_stride,
+    int rows, meta, sig_part, sig_gate, sig_row, red, ucache, ccache, hid, du, dh, du_stride,
         dh_stride, bytes;
 };
 template <typename P>
@@ -375,7 +388,8 @@ __host__ __device__ inline CellLds cell_lds(int d, int H, int BK) {
     L.red = L.sig_row + 4 * kCellRows;                     // float [8][64][4]
     L.ucache = L.red + 4 * kCellWaves * kWave * 4;         // uint8 [B K]: each slot's unit
     L.ccache = round_up(L.ucache + BK, 16);                // int [B K]: each slot's cell
-    L.du = L.ccache + 4 * BK;                              // P [16][du_stride]
+    L.hid = round_up(L.ccache + 4 * BK, 16);               // P [16][H]: the rows' hidden values
+    L.du = round_up(L.hid + static_cast<int>(sizeof(P)) * kCellRows * H, 16);  // P [16][du_stride]
     L.dh = L.du + round_up(static_cast<int>(sizeof(P)) * kCellRows * L.du_stride, 16);
     L.bytes = L.dh + static_cast<int>(sizeof(P)) * kCellRows * L.dh_stride;
     return L;
@@ -424,6 +438,7 @@ __global__ __launch_bounds__(kCellThreads) void back_cell(hsn_back_sweep s, int 
     float* red = reinterpret_cast<float*>(lds + L.red);
     uint8_t* ucache = lds + L.ucache;
     int* ccache = reinterpret_cast<int*>(lds + L.ccache);
+    P* hid_lds = reinterpret_cast<P*>(lds + L.hid);
     P* du = reinterpret_cast<P*>(lds + L.du);
     P* dh = reinterpret_cast<P*>(lds + L.dh);
 
@@ -518,8 +533,35 @@ __global__ __launch_bounds__(kCellThreads) void back_cell(hsn_back_sweep s, int 
     const int steps = ka / TL::kStep;
     const P* w2 = static_cast<const P*>(s.w2f) + int64_t(j) * H * d;
     const P* hidden = static_cast<const P*>(s.hidden);
+    // the tile's hidden rows, 16 bytes a thread per load (H * sizeof(P) % 16 == 0: H % 8 == 0)
+    constexpr int kHidPer = 16 / static_cast<int>(sizeof(P));
+    constexpr int kHidLoads = 2;  // per thread per batch
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    const int hid_chunks = kCellRows * H / kHidPer;
+    u4 hv[kHidLoads];
+    auto load_hid = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < kHidLoads; ++u) {
+            const int c = c0 + u * kCellThreads + tid;
+            hv[u] = u4{0u, 0u, 0u, 0u};
+            if (c < hid_chunks) {
+                const int r = c / (H / kHidPer), e = (c % (H / kHidPer)) * kHidPer;
+                const int q = rows[r];
+                if (q >= 0 && ccache[q] >= 0)
+                    hv[u] = *reinterpret_cast<const u4*>(hidden + slot_at(s, t, q) * H + e);
+            }
+        }
+    };
+    auto store_hid = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < kHidLoads; ++u) {
+            const int c = c0 + u * kCellThreads + tid;
+            if (c < hid_chunks) *reinterpret_cast<u4*>(hid_lds + c * kHidPer) = hv[u];
+        }
+    };
+    load_hid(0);
     frag bf[kActTiles][kActSteps];
-    float hid[kActTiles][4], bias[kActTiles];
+    float bias[kActTiles];
     auto load_act = [&](int c00) {
 #pragma unroll
         for (int u = 0; u < kActTiles; ++u) {
@@ -531,9 +573,6 @@ __global__ __launch_bounds__(kCellThreads) void back_cell(hsn_back_sweep s, int 
                 bf[u][st] = TL::glb(w2 + int64_t(hin ? h : 0) * d + kq,
                                     st < steps && hin && kq < d);
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                hid[u][i] = okrow[i] && hin ? to_f32(hidden[srow[i] * H + h]) : 0.0f;
             bias[u] = hin ? s.b1[int64_t(j) * H + h] : 0.0f;
         }
     };
@@ -618,6 +657,11 @@ __global__ __launch_bounds__(kCellThreads) void back_cell(hsn_back_sweep s, int 
         for (int x = d + lane; x < L.du_stride; x += kWave) du_row[x] = from_f32<P>(0.0f);
         for (int x = d + lane; x < L.dh_stride - H; x += kWave) dg_row[x] = from_f32<P>(0.0f);
     }
+    store_hid(0);  // the first batch was in flight under the head
+    for (int c0 = kHidLoads * kCellThreads; c0 < hid_chunks; c0 += kHidLoads * kCellThreads) {
+        load_hid(c0);
+        store_hid(c0);
+    }
     __syncthreads();
 
     // ---- act = du . (W_out W2_j^T); dh = act'(hidden) act; sigma's hidden part ----
@@ -639,8 +683,9 @@ __global__ __launch_bounds__(kCellThreads) void back_cell(hsn_back_sweep s, int 
             for (int i = 0; i < 4; ++i) {
                 float v = 0.0f;
                 if (okrow[i] && hin) {
-                    v = round_p<P>(acc[i]) * act_grad_t<ACT>(hid[u][i]);
-                    part[i] += v * (hid[u][i] - bias[u]);
+                    const float hv1 = to_f32(hid_lds[(4 * lq + i) * H + h]);
+                    v = round_p<P>(acc[i]) * act_grad_t<ACT>(hv1);
+                    part[i] += v * (hv1 - bias[u]);
                 }
                 if (hin) dh[(4 * lq + i) * L.dh_stride + h] = from_f32<P>(v);
             }
@@ -800,9 +845,9 @@ __global__ __launch_bounds__(kBackThreads) void back_cell_tail(hsn_back_sweep s,
                 we = s.out_w[int64_t(n) * s.d_out + j0 + lane];
             }
             const int jn = min(kWave, s.d_out - j0);
-            for (int e = 0; e < jn; ++e) {
-                const int kj = __shfl(ke, e, kWave);
-                const float wj = __shfl(we, e, kWave);
+            for (int e = 0; e < jn; ++e) {  // e is uniform: scalar reads, no LDS
+                const int kj = __builtin_amdgcn_readlane(ke, e);
+                const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(we), e));
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
                     const int x = lane + c * kWave;
@@ -873,8 +918,8 @@ void cell_check(const hsn_back_sweep* s) {
     const int BK = s->B * s->K;
     const int lds = s->product_dtype == HSN_DTYPE_BF16 ? cell_lds<bf16_t>(s->d, s->H, BK).bytes
                                                        : cell_lds<float>(s->d, s->H, BK).bytes;
-    HSN_REQUIRE(lds <= kMaxLds, HSN_ERR_INVALID_ARGUMENT,
-                "fused reverse sweep step: 16 slots' operand rows exceed 64 KiB of LDS");
+    HSN_REQUIRE(lds <= kCellMaxLds, HSN_ERR_INVALID_ARGUMENT,
+                "fused reverse sweep step: 16 slots' operand rows exceed 160 KiB of LDS");
     HSN_REQUIRE(s->w2f != nullptr && s->w1f != nullptr && s->carry != nullptr &&
                     s->ds != nullptr,
                 HSN_ERR_INVALID_ARGUMENT,
@@ -953,24 +998,27 @@ extern "C" int hsn_win_back_cell_check(const hsn_back_sweep* sweep) {
     HSN_ABI_END
 }
 
+template <typename P, int CPL, int ACT>
+void launch_cell_act(const hsn_back_sweep& s, int t, dim3 grid, size_t lds, hipStream_t st) {
+    if (lds > static_cast<size_t>(kMaxLds))
+        HSN_HIP(allow_lds_raw(reinterpret_cast<const void*>(back_cell<P, CPL, ACT>), lds));
+    hipLaunchKernelGGL((back_cell<P, CPL, ACT>), grid, dim3(kCellThreads), lds, st, s, t);
+}
+
 template <typename P, int CPL>
 void launch_cell(const hsn_back_sweep& s, int t, dim3 grid, size_t lds, hipStream_t st) {
     switch (s.activation) {
         case HSN_ACT_GELU:
-            hipLaunchKernelGGL((back_cell<P, CPL, HSN_ACT_GELU>), grid, dim3(kCellThreads), lds, st,
-                               s, t);
+            launch_cell_act<P, CPL, HSN_ACT_GELU>(s, t, grid, lds, st);
             break;
         case HSN_ACT_RELU:
-            hipLaunchKernelGGL((back_cell<P, CPL, HSN_ACT_RELU>), grid, dim3(kCellThreads), lds, st,
-                               s, t);
+            launch_cell_act<P, CPL, HSN_ACT_RELU>(s, t, grid, lds, st);
             break;
         case HSN_ACT_SILU:
-            hipLaunchKernelGGL((back_cell<P, CPL, HSN_ACT_SILU>), grid, dim3(kCellThreads), lds, st,
-                               s, t);
+            launch_cell_act<P, CPL, HSN_ACT_SILU>(s, t, grid, lds, st);
             break;
         default:
-            hipLaunchKernelGGL((back_cell<P, CPL, HSN_ACT_TANH>), grid, dim3(kCellThreads), lds, st,
-                               s, t);
+            launch_cell_act<P, CPL, HSN_ACT_TANH>(s, t, grid, lds, st);
     }
 }
 
