@@ -25,8 +25,10 @@ void clear_last_error();
 
 inline hipStream_t as_stream(void* stream) { return static_cast<hipStream_t>(stream); }
 
-// Every element count must fit an int32 index in the kernels' per-row arithmetic, and the
-// total must fit int64 (always true for real tensors); the bound is the reference ABI's.
+// The window entry points' bound on a whole tensor's element count: 64 * INT32_MAX (the kernels
+// index across rows in int64 and within a row in int32). It is looser than the reference ABI's
+// bound, every count <= INT32_MAX (kernels/include/hsn_ops.h:21-23), which the hsn_ops.h entry
+// points (ops.hip, units.hip) check themselves.
 inline bool check_elems(std::initializer_list<int64_t> counts) {
     for (int64_t c : counts)
         if (c < 0 || c > static_cast<int64_t>(INT32_MAX) * 64) return false;
