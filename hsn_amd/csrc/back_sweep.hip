@@ -755,106 +755,105 @@ __global__ __launch_bounds__(kCellThreads) void back_cell(hsn_back_sweep s, int 
 constexpr int kCellTailCells = 32;  // cells per workgroup
 
 struct CellTailLds {
-    int slot_of, flag, list, count, ds, bytes;
+    int slot_of, ds, carry, bytes;
 };
-__host__ __device__ inline CellTailLds cell_tail_lds(int N, int K, int d) {
+__host__ __device__ inline CellTailLds cell_tail_lds(int N, int K, int d, int d_out) {
+    (void)d_out;
     CellTailLds L;
-    L.slot_of = 0;                                // int [N]
-    L.flag = L.slot_of + 4 * N;                   // int [32]
-    L.list = L.flag + 4 * kCellTailCells;         // int [32]
-    L.count = L.list + 4 * kCellTailCells;        // int
-    L.ds = round_up(L.count + 4, 16);             // float [K][2d]
-    L.bytes = L.ds + 4 * K * 2 * d;
+    L.slot_of = 0;                           // int [N]
+    L.ds = round_up(L.slot_of + 4 * N, 16);  // float [K][2d]
+    L.carry = L.ds + 4 * K * 2 * d;          // float [K][d]
+    L.bytes = L.carry + 4 * K * d;
     return L;
 }
 
-// Grid (N / 32, B): workgroup (i, b) updates row b's cells 32 i .. 32 i + 31 that position t
-// touches (the selected cells, their message sources, the fast-read cells). Per such cell n and
-// column x, in this order: a = carry of n's slot if n is selected, else A[n] (+ d_h_fast if n is
-// a fast-read cell); + ds_h of n's slot; + the edge weight times ds_m of each selected target of
-// n, in n's out-adjacency order. Then R = (R + d_q_post) + d_q_pre, and a reset zeroes the row.
+// Grid (N / 32, B): workgroup (i, b) updates row b's cells 32 i .. 32 i + 31, a wavefront per
+// cell (cells w, w + 4, ...), a lane per column and per out-edge. Every load it needs is issued at
+// once (its cells' rows of A and out-edges, the position's slots, carries and ds rows, the fast
+// reads, R); then each cell resolves its out-edges' target slots in one LDS read across lanes and
+// skips itself when nothing touches it. Per touched cell n and column x, in this order: a = the
+// carry of n's slot if n is selected, else A[n] (+ d_h_fast if n is a fast-read cell); + ds_h of
+// n's slot; + the edge weight times ds_m of each selected target of n, in n's out-adjacency
+// order. Then R = (R + d_q_post) + d_q_pre, and a reset zeroes the row.
 template <int CPL>
 __global__ __launch_bounds__(kBackThreads) void back_cell_tail(hsn_back_sweep s, int t) {
     extern __shared__ __align__(16) unsigned char lds[];
+    constexpr int kCellsPerWave = kCellTailCells / kBackWaves;
     const int row = blockIdx.y;
     const int cell0 = blockIdx.x * kCellTailCells;
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-    const int d = s.d, K = s.K, N = s.N;
+    const int d = s.d, K = s.K, N = s.N, D = s.d_out;
     const int64_t bt = int64_t(row) * s.T + t;
     float* A = s.A + int64_t(row) * N * d;
-    const int cell_end = min(cell0 + kCellTailCells, N);
-    if (s.reset[bt] != 0) {  // the row restarts: its cotangent before position t is zero
-        for (int64_t i = int64_t(cell0) * d + tid; i < int64_t(cell_end) * d; i += kBackThreads)
-            A[i] = 0.0f;
-        if (blockIdx.x == 0)
-            for (int x = tid; x < d; x += kBackThreads) s.R[int64_t(row) * d + x] = 0.0f;
-        return;
-    }
-    const CellTailLds L = cell_tail_lds(N, K, d);
+    const CellTailLds L = cell_tail_lds(N, K, d, D);
     int* slot_of = reinterpret_cast<int*>(lds + L.slot_of);
-    int* flag = reinterpret_cast<int*>(lds + L.flag);
-    int* list = reinterpret_cast<int*>(lds + L.list);
-    int* count = reinterpret_cast<int*>(lds + L.count);
     float* ds = reinterpret_cast<float*>(lds + L.ds);
+    float* carry = reinterpret_cast<float*>(lds + L.carry);
     for (int n = tid; n < N; n += kBackThreads) slot_of[n] = -1;
-    if (tid < kCellTailCells) flag[tid] = cell0 + tid < min(s.n_read, cell_end) ? 1 : 0;
-    __syncthreads();
-    for (int k = wave; k < K; k += kBackWaves) {
-        const int cell = s.slots[bt * K + k];
-        const bool ok = cell >= 0 && cell < N;
-        const float* dsrow = s.ds + (int64_t(row) * K + k) * 2 * d;
-        for (int x = lane; x < 2 * d; x += kWave) ds[k * 2 * d + x] = dsrow[x];
-        if (!ok) continue;
-        if (lane == 0) {
-            slot_of[cell] = k;
-            if (cell >= cell0 && cell < cell_end) flag[cell - cell0] = 1;
-        }
-        for (int e = lane; e < s.d_in; e += kWave) {
-            const int src = s.in_src[int64_t(cell) * s.d_in + e];
-            if (src >= cell0 && src < cell_end) flag[src - cell0] = 1;
-        }
+    // ---- every load at once ----
+    const bool reset = s.reset[bt] != 0;
+    int cell_k = -1;
+    if (tid < K) {
+        const int c = s.slots[bt * K + tid];
+        cell_k = c >= 0 && c < N ? c : -1;
     }
-    __syncthreads();
-    if (wave == 0) {
-        const bool f = lane < kCellTailCells && flag[lane] != 0;
-        const uint64_t m = ballot(f);
-        if (f) list[lanes_below(m)] = cell0 + lane;
-        if (lane == 0) *count = __popcll(m);
+    float av[kCellsPerWave][CPL], fv[kCellsPerWave][CPL], ew[kCellsPerWave];
+    int et[kCellsPerWave];
+#pragma unroll
+    for (int ci = 0; ci < kCellsPerWave; ++ci) {
+        const int n = cell0 + wave + ci * kBackWaves;
+        const bool in = n < N;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int x = lane + c * kWave;
+            av[ci][c] = in && x < d ? A[int64_t(n) * d + x] : 0.0f;
+            fv[ci][c] = in && x < d && n < s.n_read
+                            ? s.d_h_fast[(bt * s.n_read + n) * d + x] : 0.0f;
+        }
+        et[ci] = in && lane < D ? s.out_tgt[int64_t(n) * D + lane] : -1;
+        ew[ci] = in && lane < D ? s.out_w[int64_t(n) * D + lane] : 0.0f;
     }
+    for (int i = tid; i < K * 2 * d; i += kBackThreads)
+        ds[i] = s.ds[int64_t(row) * K * 2 * d + i];
+    for (int i = tid; i < K * d; i += kBackThreads) carry[i] = s.carry[int64_t(row) * K * d + i];
+    float rv = 0.0f;
+    if (blockIdx.x == 0 && tid < d)
+        rv = (s.R[int64_t(row) * d + tid] + s.d_q_post[bt * d + tid]) + s.d_q_pre[bt * d + tid];
     __syncthreads();
-    const int touched = *count;
-    for (int i = wave; i < touched; i += kBackWaves) {
-        const int n = list[i];
+    if (cell_k >= 0) slot_of[cell_k] = tid;
+    __syncthreads();
+    // ---- the cells' rows ----
+#pragma unroll
+    for (int ci = 0; ci < kCellsPerWave; ++ci) {
+        const int n = cell0 + wave + ci * kBackWaves;
+        if (n >= N) continue;  // uniform per wavefront
+        if (reset) {  // the row restarts: its cotangent before position t is zero
+#pragma unroll
+            for (int c = 0; c < CPL; ++c)
+                if (lane + c * kWave < d) A[int64_t(n) * d + lane + c * kWave] = 0.0f;
+            continue;
+        }
+        const int ke = et[ci] >= 0 && et[ci] < N ? slot_of[et[ci]] : -1;  // lane e: edge e's slot
+        const uint64_t hit = ballot(ke >= 0);
         const int own = slot_of[n];
+        if (hit == 0 && own < 0 && n >= s.n_read) continue;  // nothing touches n (uniform)
         float a[CPL];
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             const int x = lane + c * kWave;
             if (x >= d) continue;
-            a[c] = own >= 0 ? s.carry[(int64_t(row) * K + own) * d + x] : A[int64_t(n) * d + x];
-            if (own < 0 && n < s.n_read) a[c] = a[c] + s.d_h_fast[(bt * s.n_read + n) * d + x];
+            a[c] = own >= 0 ? carry[own * d + x] : av[ci][c];
+            if (own < 0 && n < s.n_read) a[c] = a[c] + fv[ci][c];
             if (own >= 0) a[c] = a[c] + ds[own * 2 * d + x];
         }
-        for (int j0 = 0; j0 < s.d_out; j0 += kWave) {
-            // lane e: out-edge j0 + e of n, its target's slot (or -1) and weight
-            int ke = -1;
-            float we = 0.0f;
-            if (j0 + lane < s.d_out) {
-                const int target = s.out_tgt[int64_t(n) * s.d_out + j0 + lane];
-                if (target >= 0 && target < N) ke = slot_of[target];
-                we = s.out_w[int64_t(n) * s.d_out + j0 + lane];
-            }
-            const int jn = min(kWave, s.d_out - j0);
-            for (int e = 0; e < jn; ++e) {  // e is uniform: scalar reads, no LDS
-                const int kj = __builtin_amdgcn_readlane(ke, e);
-                const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(we), e));
+        for (uint64_t m = hit; m != 0; m &= m - 1) {  // the selected targets, in edge order
+            const int e = __builtin_ctzll(m);
+            const int kj = __builtin_amdgcn_readlane(ke, e);
+            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ew[ci]), e));
 #pragma unroll
-                for (int c = 0; c < CPL; ++c) {
-                    const int x = lane + c * kWave;
-                    if (x >= d) continue;
-                    const float add = kj >= 0 ? wj * ds[kj * 2 * d + d + x] : 0.0f;
-                    a[c] = a[c] + add;
-                }
+            for (int c = 0; c < CPL; ++c) {
+                const int x = lane + c * kWave;
+                if (x < d) a[c] = a[c] + wj * ds[kj * 2 * d + d + x];
             }
         }
 #pragma unroll
@@ -863,11 +862,7 @@ __global__ __launch_bounds__(kBackThreads) void back_cell_tail(hsn_back_sweep s,
             if (x < d) A[int64_t(n) * d + x] = a[c];
         }
     }
-    if (blockIdx.x == 0)
-        for (int x = tid; x < d; x += kBackThreads) {
-            const float r = s.R[int64_t(row) * d + x] + s.d_q_post[bt * d + x];
-            s.R[int64_t(row) * d + x] = r + s.d_q_pre[bt * d + x];
-        }
+    if (blockIdx.x == 0 && tid < d) s.R[int64_t(row) * d + tid] = reset ? 0.0f : rv;
 }
 
 void back_check(const hsn_back_sweep* s) {
@@ -924,9 +919,12 @@ void cell_check(const hsn_back_sweep* s) {
                     s->ds != nullptr,
                 HSN_ERR_INVALID_ARGUMENT,
                 "fused reverse sweep step: w2f / w1f / carry / ds is NULL");
-    HSN_REQUIRE(cell_tail_lds(s->N, s->K, s->d).bytes <= kMaxLds, HSN_ERR_INVALID_ARGUMENT,
-                "fused reverse sweep step: the tail's slot table and slot terms (4 N + 8 K d "
+    HSN_REQUIRE(cell_tail_lds(s->N, s->K, s->d, s->d_out).bytes <= kMaxLds,
+                HSN_ERR_INVALID_ARGUMENT,
+                "fused reverse sweep step: the tail's slot table and slot terms (4 N + 12 K d "
                 "bytes) exceed 64 KiB of LDS");
+    HSN_REQUIRE(s->K <= kBackThreads && s->d_out <= kWave, HSN_ERR_INVALID_ARGUMENT,
+                "fused reverse sweep step: more than 256 slots a row or 64 out-edges a cell");
 }
 
 void check_t(const hsn_back_sweep* s, int t) {
@@ -1054,7 +1052,7 @@ extern "C" int hsn_win_back_cell_tail(const hsn_back_sweep* sweep, int t, void* 
     const hsn_back_sweep s = *sweep;
     const dim3 grid(static_cast<unsigned>((s.N + kCellTailCells - 1) / kCellTailCells),
                     static_cast<unsigned>(s.B));
-    const size_t lds = static_cast<size_t>(cell_tail_lds(s.N, s.K, s.d).bytes);
+    const size_t lds = static_cast<size_t>(cell_tail_lds(s.N, s.K, s.d, s.d_out).bytes);
     const int cpl = (s.d + kWave - 1) / kWave;
     hipStream_t st = as_stream(stream);
 #define HSN_TAIL(C) \
