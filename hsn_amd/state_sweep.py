@@ -110,12 +110,14 @@ def out_adjacency(pad_src: Tensor, pad_mask: Tensor) -> tuple[Tensor, Tensor]:
 
 
 def sweep_shape(c: Tensor, record: dict[str, Tensor], consts: Any, n_cells: int, n_fast: int,
-                n_read: int) -> SweepShape:
-    """The :class:`SweepShape` of a window's sweep arguments (state_sweep.py:531-560)."""
+                n_read: int, d_out: Optional[int] = None) -> SweepShape:
+    """The :class:`SweepShape` of a window's sweep arguments (state_sweep.py:531-560); ``d_out``
+    the message graph's out-degree when the caller knows it (else computed)."""
     B, T, K, d = (int(n) for n in c.shape)
     if consts.pad_mask is None:
         raise ValueError("the reverse sweep needs the graph's padding mask (pad_mask)")
-    d_out = int(out_adjacency(consts.pad_src, consts.pad_mask)[0].shape[1])
+    if d_out is None:
+        d_out = int(out_adjacency(consts.pad_src, consts.pad_mask)[0].shape[1])
     return SweepShape(B=B, T=T, K=K, N=int(n_cells), d=d, H=int(record["hidden"].shape[-1]),
                       M=int(consts.w2.shape[0]), n_fast=int(n_fast), n_read=int(n_read),
                       in_dim=int(consts.in_dim), d_out=d_out)
@@ -425,6 +427,9 @@ class SweepRunner:
         self.graph = graph
         self.fused = fused
         self.sweeps: dict[tuple, ReverseSweep] = {}
+        # the out-degree per message graph (its pad_src tensor, kept alive with it): the graph is
+        # fixed between windows, and finding the degree takes host synchronisations
+        self._d_out: dict[int, tuple[Tensor, int]] = {}
         #: Windows swept, and how many of them captured a graph.
         self.calls = 0
         self.captures = 0
@@ -445,7 +450,11 @@ class SweepRunner:
         product_dtype = record["hidden"].dtype
         if product_dtype not in (torch.float32, torch.bfloat16):
             return None
-        shape = sweep_shape(c, record, consts, n_cells, n_fast, n_read)
+        known = self._d_out.get(id(consts.pad_src))
+        if known is None or known[0] is not consts.pad_src:
+            degree = int(out_adjacency(consts.pad_src, consts.pad_mask)[0].shape[1])
+            known = self._d_out[id(consts.pad_src)] = (consts.pad_src, degree)
+        shape = sweep_shape(c, record, consts, n_cells, n_fast, n_read, d_out=known[1])
         cand_norm = consts.cand_gain is not None
         cell_norm = consts.norm_gain_state is not None
         if back_unsupported(shape, d_in=int(consts.pad_src.shape[1]), product_dtype=product_dtype,
