@@ -1,5 +1,5 @@
 """The C ABI of ``libhsn_amd.so`` (``include/hsn_window.h``, ``include/hsn_ops.h``,
-``include/hsn_trainer.h``, ``include/hsn_sweep.h``) via ctypes.
+``include/hsn_trainer.h``, ``include/hsn_sweep.h``, ``include/hsn_round.h``) via ctypes.
 
 The library is the product: every operator in :mod:`hsn_amd` reaches the GPU through these
 entry points, and nothing here falls back to another implementation. :func:`library` raises a
@@ -75,6 +75,9 @@ SIGNATURES: dict[str, list] = {
     "hsn_win_back_cell_check": [P],
     "hsn_win_back_cell": [P, I, P],
     "hsn_win_back_cell_tail": [P, I, P],
+    "hsn_win_cell_round_check": [P],
+    "hsn_win_cell_round_workspace": [P, P],
+    "hsn_win_cell_round": [P, P],
 }
 
 _lock = threading.Lock()

@@ -11,6 +11,7 @@ update take any ``N`` whose state slice fits the 160 KiB LDS), the carried-state
 
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -403,3 +404,153 @@ def update_tape(cell, y, gate, tape_h, tape_q, tape_age, cells, valid, reset, ta
     cand_norm, w, eps = _cand(cell)
     update_tape_op(y.contiguous(), gate.contiguous(), tape_h, tape_q, tape_age, cells, valid, w,
                    reset, tape_hsel, h_max, qs, t, cand_norm, eps)
+
+
+# --------------------------------------------------------------------------------------------
+# the fused cell round (reference window.py:195-330, 1007-1048; include/hsn_round.h)
+# --------------------------------------------------------------------------------------------
+
+_ROUND_POINTERS = ("u", "eps", "h", "q", "age", "cells", "units", "valid", "alpha", "V", "edge_w",
+                   "pad_src", "norm_w", "gate_w", "gate_b", "W1", "b1", "W2", "b2", "W_out",
+                   "cand_w", "work", "h_new", "q_new", "age_new", "h_sel")
+
+
+class _Round(ctypes.Structure):
+    """``hsn_cell_round`` (include/hsn_round.h), field for field."""
+
+    _fields_ = ([(name, ctypes.c_int32) for name in ("B", "N", "d", "K", "M", "H", "D",
+                                                     "cand_norm")]
+                + [("norm_eps", ctypes.c_float), ("cand_eps", ctypes.c_float)]
+                + [(name, ctypes.c_void_p) for name in _ROUND_POINTERS])
+
+
+def _round_struct(B, N, d, K, M, H, D, cand_norm, norm_eps, cand_eps, **pointers) -> _Round:
+    s = _Round(B=B, N=N, d=d, K=K, M=M, H=H, D=D, cand_norm=int(bool(cand_norm)),
+               norm_eps=float(norm_eps), cand_eps=float(cand_eps))
+    for name in _ROUND_POINTERS:
+        setattr(s, name, pointers.get(name))
+    return s
+
+
+def _round_unsupported(B, N, d, K, M, H, D, cand_norm) -> Optional[str]:
+    """The library's own verdict on a shape (``hsn_win_cell_round_check`` on placeholder
+    pointers: the check reads no memory)."""
+    s = _round_struct(B, N, d, K, M, H, D, cand_norm, 0.0, 0.0,
+                      **{name: 256 for name in _ROUND_POINTERS})
+    lib = _lib.library()
+    if lib.hsn_win_cell_round_check(ctypes.byref(s)) == _lib.HSN_OK:
+        return None
+    return lib.hsn_win_last_error().decode(errors="replace")
+
+
+def cell_round_error(cell) -> Optional[str]:
+    """Why the fused cell round cannot run this cell, or ``None`` when it can (reference
+    window.py:202-230): the same model switches, then the library's geometry (``d`` a multiple
+    of 4 up to 256, at most 255 units; the slot count is checked per call)."""
+    d = int(cell.d)
+    if getattr(cell, "ablate_shared_u", False):
+        return ("model.ablate_shared_u: the fused round builds the 4d cell input [u; eps; h; m] "
+                "in its kernel")
+    if not available():
+        return "the HIP library is not built (hsn_amd.build.build())"
+    if getattr(cell, "cell_norm", "rms") != "rms":
+        return f"model.cell_norm={cell.cell_norm!r}: the fused round implements the RMS norm"
+    if cell.units.activation_name != "gelu":
+        return (f"model.activation={cell.units.activation_name!r}: the fused round implements "
+                "GELU")
+    if getattr(cell, "disabled_cells", None):
+        return "model.disabled_cells is a test hook of the native round"
+    if cell.V.weight.dtype != torch.float32:
+        return f"fp32 master weights only, got {cell.V.weight.dtype}"
+    pad_src = cell.graph._pad_src
+    N, D = int(pad_src.shape[0]), int(pad_src.shape[1])
+    M, _, H = (int(n) for n in cell.units.W1.shape)
+    why = _round_unsupported(1, N, d, 1, M, H, D, getattr(cell, "cand_norm_kind", "none") != "none")
+    return None if why is None else f"model.d={d}, model.hidden={H}, model.n_units={M}: {why}"
+
+
+def _need(name: str, t: Tensor, dtype: torch.dtype, shape: tuple, device) -> None:
+    if t.dtype != dtype or tuple(t.shape) != tuple(shape) or t.device != device:
+        raise ValueError(f"cell round: {name} must be {dtype} {list(shape)} on {device}, got "
+                         f"{t.dtype} {list(t.shape)} on {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"cell round: {name} must be contiguous")
+
+
+@torch.library.custom_op("hsn::window_cell_round", mutates_args=(), device_types="cuda")
+def cell_round_op(u: Tensor, eps: Tensor, h: Tensor, q: Tensor, age: Tensor, cells: Tensor,
+                  units: Tensor, valid: Tensor, alpha: Tensor, V: Tensor, edge_w: Tensor,
+                  pad_src: Tensor, norm_w: Tensor, gate_w: Tensor, gate_b: Tensor, W1: Tensor,
+                  b1: Tensor, W2: Tensor, b2: Tensor, W_out: Tensor, cand_w: Tensor,
+                  cand_norm: bool, norm_eps: float, cand_eps: float
+                  ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """The sparse round and the tick, forward only: ``(h_new, q_new, age_new, h_sel)``
+    (reference window.py:233-330; ``hsn_win_cell_round``). Contiguous fp32 / int64 / bool
+    tensors on one device, as the reference's op takes them; not differentiable."""
+    B, N, d = (int(n) for n in h.shape)
+    K = int(cells.shape[1])
+    M, n_in, H = (int(n) for n in W1.shape)
+    D = int(edge_w.shape[1])
+    dev = h.device
+    f32, i64 = torch.float32, torch.int64
+    for name, t, dtype, shape in (
+            ("u", u, f32, (B, d)), ("eps", eps, f32, (B, d)), ("h", h, f32, (B, N, d)),
+            ("q", q, f32, (B, d)), ("age", age, i64, (B, N)), ("cells", cells, i64, (B, K)),
+            ("units", units, i64, (B, K)), ("valid", valid, torch.bool, (B, K)),
+            ("alpha", alpha, f32, (B, K)), ("V", V, f32, (d, d)), ("edge_w", edge_w, f32, (N, D)),
+            ("pad_src", pad_src, i64, (N, D)), ("norm_w", norm_w, f32, (4 * d,)),
+            ("gate_w", gate_w, f32, (d, 4 * d)), ("gate_b", gate_b, f32, (d,)),
+            ("W1", W1, f32, (M, 4 * d, H)), ("b1", b1, f32, (M, H)), ("W2", W2, f32, (M, H, d)),
+            ("b2", b2, f32, (M, d)), ("W_out", W_out, f32, (d, d))):
+        _need(name, t, dtype, shape, dev)
+    if cand_norm:  # otherwise unused (the reference passes the cell norm's gain in its place)
+        _need("cand_w", cand_w, f32, (d,), dev)
+    h_new = torch.empty_like(h)
+    q_new = torch.empty_like(q)
+    age_new = torch.empty_like(age)
+    h_sel = h.new_empty((B, K, d))
+    args = dict(u=ptr(u), eps=ptr(eps), h=ptr(h), q=ptr(q), age=ptr(age), cells=ptr(cells),
+                units=ptr(units), valid=ptr(valid), alpha=ptr(alpha), V=ptr(V),
+                edge_w=ptr(edge_w) if D else None, pad_src=ptr(pad_src) if D else None,
+                norm_w=ptr(norm_w), gate_w=ptr(gate_w), gate_b=ptr(gate_b), W1=ptr(W1),
+                b1=ptr(b1), W2=ptr(W2), b2=ptr(b2), W_out=ptr(W_out),
+                cand_w=ptr(cand_w) if cand_norm else None,
+                h_new=ptr(h_new), q_new=ptr(q_new), age_new=ptr(age_new), h_sel=ptr(h_sel))
+    s = _round_struct(B, N, d, K, M, H, D, cand_norm, norm_eps, cand_eps, **args)
+    nbytes = ctypes.c_int64(0)
+    call("hsn_win_cell_round_workspace", ctypes.byref(s), ctypes.byref(nbytes))
+    work = torch.empty(int(nbytes.value), dtype=torch.uint8, device=dev)
+    s.work = ptr(work)
+    call("hsn_win_cell_round", ctypes.byref(s), stream_of(dev))
+    return h_new, q_new, age_new, h_sel
+
+
+@cell_round_op.register_fake
+def _cell_round_fake(u, eps, h, q, age, cells, units, valid, alpha, V, edge_w, pad_src, norm_w,
+                     gate_w, gate_b, W1, b1, W2, b2, W_out, cand_w, cand_norm, norm_eps, cand_eps):
+    return (torch.empty_like(h), torch.empty_like(q), torch.empty_like(age),
+            h.new_empty((*cells.shape, h.shape[2])))
+
+
+def cell_round(cell, u: Tensor, eps: Tensor, state: CellGraphState, cells: Tensor, units: Tensor,
+               valid: Tensor, edge_weights: Tensor):
+    """``PDGCell.step_sparse`` and the tick of one position as the fused op: the state after the
+    position and the selected slots' updated states ``[B, K, d]`` (cell 0 on padded slots).
+    ``cells`` / ``units`` / ``valid`` are a hard decision (``alpha`` is 1 on its valid slots),
+    ``edge_weights`` the window's padded edge weights. fp32 state, no autograd (reference
+    window.py:1007-1048)."""
+    cand_norm = getattr(cell, "cand_norm_kind", "none") != "none"
+    norm_w = cell.norm.weight
+    with torch.no_grad():
+        h_new, q_new, age_new, h_sel = cell_round_op(
+            u.contiguous(), eps.contiguous(), state.h.contiguous(), state.q.contiguous(),
+            state.age.contiguous(), cells.contiguous(), units.contiguous(), valid.contiguous(),
+            valid.to(torch.float32).contiguous(), cell.V.weight.detach(),
+            edge_weights.to(torch.float32).contiguous(), cell.graph._pad_src,
+            norm_w.detach(), cell.gate.weight.detach(), cell.gate.bias.detach(),
+            cell.units.W1.detach(), cell.units.b1.detach(), cell.units.W2.detach(),
+            cell.units.b2.detach(), cell.W_out.weight.detach(),
+            (cell.cand_norm.weight if cand_norm else norm_w).detach(),
+            cand_norm, float(getattr(cell.norm, "eps", None) or 0.0),
+            float(getattr(cell.cand_norm, "eps", None) or 0.0) if cand_norm else 0.0)
+    return CellGraphState.make(h=h_new, q=q_new, age=age_new, pos=state.pos + 1), h_sel

@@ -218,3 +218,104 @@ def make_sweep_window(B: int, T: int, K: int, N: int, d: int, H: int, M: int, D:
     args = (c, b, rnd(B, T, K, d, scale=0.5), cells.to(device), units.to(device), valid.to(device),
             reset.to(device), N, rnd(B, T, d), rnd(B, T, d), rnd(B, T, K, d), None, record, consts)
     return args, dict(n_read=0)
+
+
+# --------------------------------------------------------------------------------------------
+# the fused cell round (hsn_amd.kernels.window.cell_round)
+# --------------------------------------------------------------------------------------------
+
+#: the round's bench shape: the reverse sweep's model (B 32, K 8 slots of N 256 cells, d 64,
+#: H 512 hidden units in each of M 8 units, D 8 padded in-edges)
+ROUND_CONFIGS = {
+    "ref": dict(B=32, K=8, N=256, d=64, H=512, M=8, D=8),
+    "tiny": dict(B=2, K=3, N=16, d=8, H=16, M=2, D=3),
+}
+
+
+def make_round_cell(*, N: int, d: int, M: int, H: int, D: int, cand_norm: bool = True,
+                    seed: int = 0, device="cpu"):
+    """A cell with what the fused round reads, under the reference PDGCell's attribute names
+    (``V``, ``norm``, ``gate``, ``W_out``, ``cand_norm``, ``units.W1 / b1 / W2 / b2``,
+    ``graph._pad_src``; python/hsn/model/cell.py), seeded values away from their initial ones,
+    and the window's padded edge weights ``[N, D]`` (softmax over each cell's edges, 0 on
+    padding). Returns ``(cell, edge_weights)``."""
+    from types import SimpleNamespace
+
+    g = torch.Generator().manual_seed(seed)
+    n = 4 * d
+
+    def rnd(*shape, scale=1.0):
+        return torch.randn(*shape, generator=g) * scale
+
+    def linear(out_f, in_f, bias):
+        lin = torch.nn.Linear(in_f, out_f, bias=bias)
+        with torch.no_grad():
+            lin.weight.copy_(rnd(out_f, in_f, scale=in_f ** -0.5) + 0.2 * rnd(out_f, in_f,
+                                                                               scale=0.2))
+            if bias:
+                lin.bias.copy_(0.2 * rnd(out_f))
+        return lin.to(device)
+
+    def rms_norm(width):
+        norm = torch.nn.RMSNorm(width, eps=1e-6)
+        with torch.no_grad():
+            norm.weight.copy_(1.0 + 0.2 * rnd(width))
+        return norm.to(device)
+
+    mask = torch.rand(N, D, generator=g) < 0.75
+    if D:
+        mask[:, 0] = True
+    pad_src = torch.where(mask, torch.randint(0, N, (N, D), generator=g), torch.zeros((), dtype=torch.int64))
+    weights = torch.where(mask, torch.softmax(rnd(N, D), dim=1), torch.zeros(()))
+    units = SimpleNamespace(
+        activation_name="gelu", hidden=H,
+        W1=(rnd(M, n, H, scale=n ** -0.5)).to(device), b1=(0.2 * rnd(M, H)).to(device),
+        W2=(rnd(M, H, d, scale=H ** -0.5)).to(device), b2=(0.2 * rnd(M, d)).to(device))
+    cell = SimpleNamespace(
+        d=d, ablate_shared_u=False, cell_norm="rms", disabled_cells=(),
+        cand_norm_kind="rms" if cand_norm else "none",
+        V=linear(d, d, False), norm=rms_norm(n), gate=linear(d, n, True),
+        W_out=linear(d, d, False),
+        cand_norm=rms_norm(d) if cand_norm else torch.nn.Identity(),
+        units=units, graph=SimpleNamespace(_pad_src=pad_src.to(device)))
+    return cell, weights.to(device)
+
+
+def make_round_positions(*, B: int, K: int, N: int, d: int, M: int, T: int, seed: int = 0,
+                         pad_every: int = 16, device="cpu"):
+    """``T`` positions of inputs and hard decisions for the fused round: ``u, eps [T, B, d]``,
+    ``cells, units [T, B, K]`` (distinct cells a row), ``valid [T, B, K]`` (every
+    ``pad_every``-th slot padded: cell 0, unit 0), and a start state (states uniform in
+    [-0.8, 0.8], ``q`` their mean, small ages)."""
+    from .state import CellGraphState
+
+    g = torch.Generator().manual_seed(seed)
+    cells = torch.argsort(torch.rand(T, B, N, generator=g), dim=-1)[..., :K]
+    units = torch.randint(0, M, (T, B, K), generator=g)
+    valid = torch.ones(T, B, K, dtype=torch.bool)
+    valid.view(-1)[pad_every - 1::pad_every] = False
+    cells = torch.where(valid, cells, torch.zeros_like(cells))
+    units = torch.where(valid, units, torch.zeros_like(units))
+    h = torch.rand(B, N, d, generator=g) * 1.6 - 0.8
+    state = CellGraphState.make(h=h.to(device), q=h.mean(dim=1).to(device),
+                                age=torch.randint(0, 9, (B, N), generator=g).to(device),
+                                pos=torch.zeros(B, dtype=torch.int64, device=device))
+    return dict(u=torch.randn(T, B, d, generator=g).to(device),
+                eps=torch.randn(T, B, d, generator=g).to(device), cells=cells.to(device),
+                units=units.to(device), valid=valid.to(device), state=state)
+
+
+def round_bytes(cfg: dict, units_present: int) -> int:
+    """Algorithmic HBM bytes of one position's fused round: the state read and written once
+    (h, the ages), q, the decision and inputs, the slots' message sources, and the weights the
+    position reads once (V, the gate, W_out, the norms' gains, and each present unit's W1, W2,
+    biases). The scratch between the launches (v, gate, F's chunk shares) is not counted: it is
+    the kernels' own traffic, not the algorithm's."""
+    B, K, N, d, H, D = (cfg[k] for k in ("B", "K", "N", "d", "H", "D"))
+    n = 4 * d
+    state = B * N * d * 4 * 2 + B * N * 8 * 2 + B * d * 4 * 2  # h, age, q: read and written
+    slots = B * K * (8 + 8 + 1 + 4) + B * d * 4 * 2 + B * K * d * 4  # decision, u, eps, h_sel
+    sources = B * K * (D * (8 + 4) + (D + 1) * d * 4)  # edges, source rows and the own row
+    shared = 4 * (d * d + d * n + d + n + d * d + d) + N * D * 12
+    unit = 4 * (n * H + H + H * d + d)
+    return state + slots + sources + shared + units_present * unit

@@ -148,3 +148,45 @@ def sweep_oracle(p, consts=None, trace=None):
         p["c"], p["b"], p["h_old"], p["cells"], p["units"], p["valid"], p["reset"], p["N"],
         cot["d_q_pre"], cot["d_q_post"], cot["d_h_sel"], cot["d_h_fast"], p["record"],
         p["consts"] if consts is None else consts, trace=trace)
+
+
+def round_problem(B=4, N=32, d=64, K=4, M=8, H=512, D=4, cand_norm=True, seed=11, pad=0.0,
+                  alpha_one=True, edge_density=0.75):
+    """One position of the fused cell round (``hsn::window_cell_round``) in float64, shaped as the
+    reference's fused-round tests build it (tests/kernels/test_p2_10_window.py:185-222): weights
+    moved away from their initial values, states uniform in [-0.8, 0.8], ``q`` near their mean,
+    small ages and positions, distinct cells a row, a fraction ``pad`` of the slots padded (cell
+    0, unit 0, as the router pads), a padded message graph (weight 0, source 0 on padding).
+    Keys are ``oracle.hsn_oracle.window_cell_round``'s arguments."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    f64 = torch.float64
+
+    def rnd(*shape, scale=1.0):
+        return torch.randn(*shape, generator=g, dtype=f64) * scale
+
+    n = 4 * d
+    cells = torch.stack([torch.randperm(N, generator=g)[:K] for _ in range(B)])
+    units = torch.randint(0, M, (B, K), generator=g)
+    valid = torch.rand(B, K, generator=g) >= pad
+    cells = torch.where(valid, cells, torch.zeros_like(cells))
+    units = torch.where(valid, units, torch.zeros_like(units))
+    mask = torch.rand(N, D, generator=g) < edge_density
+    if D:
+        mask[:, 0] = True
+    pad_src = torch.where(mask, torch.randint(0, N, (N, D), generator=g), torch.zeros((), dtype=torch.int64))
+    edge_w = torch.where(mask, torch.softmax(rnd(N, D), dim=1), torch.zeros((), dtype=f64))
+    h = torch.rand(B, N, d, generator=g, dtype=f64) * 1.6 - 0.8
+    return dict(
+        u=rnd(B, d), eps=rnd(B, d), h=h, q=h.mean(dim=1) + 0.01,
+        age=torch.randint(0, 9, (B, N), generator=g), pos=torch.randint(0, 50, (B,), generator=g),
+        cells=cells, units=units, valid=valid,
+        alpha=(valid.to(f64) if alpha_one else 0.5 + torch.rand(B, K, generator=g, dtype=f64)),
+        V=rnd(d, d, scale=d ** -0.5) + 0.2 * rnd(d, d), edge_w=edge_w, pad_src=pad_src,
+        norm_w=1.0 + 0.2 * rnd(n), norm_eps=1e-6,
+        gate_w=rnd(d, n, scale=n ** -0.5) + 0.2 * rnd(d, n, scale=0.1), gate_b=0.2 * rnd(d),
+        W1=rnd(M, n, H, scale=n ** -0.5), b1=0.2 * rnd(M, H),
+        W2=rnd(M, H, d, scale=H ** -0.5), b2=0.2 * rnd(M, d),
+        W_out=rnd(d, d, scale=d ** -0.5) + 0.2 * rnd(d, d, scale=0.2),
+        cand_w=1.0 + 0.2 * rnd(d), cand_norm=cand_norm, cand_eps=1e-6)

@@ -111,6 +111,38 @@ def test_reverse_sweep_check_follows_the_kernels_limits():
     assert "activation" in back_unsupported(ref, activation="softplus")
 
 
+def test_cell_round_check_and_workspace_follow_the_kernels_limits():
+    """The fused cell round's check and scratch size are host arithmetic (no GPU): the
+    reference's cells and the sweep's model are taken; d not a multiple of 4, d above 256, more
+    than 255 units, more than 16384 slots and a NULL buffer are not, each with its reason."""
+    import ctypes
+
+    from hsn_amd import _lib, build
+    from hsn_amd.kernels import window as W
+
+    if build.stale() is not None:
+        pytest.skip("library not built here")
+    assert W._round_unsupported(32, 32, 64, 4, 8, 512, 4, True) is None
+    assert W._round_unsupported(32, 256, 64, 8, 8, 512, 8, False) is None
+    assert W._round_unsupported(7, 11, 24, 5, 3, 77, 3, True) is None
+    assert W._round_unsupported(2, 70, 256, 20, 3, 64, 0, True) is None
+    assert "multiple of 4" in W._round_unsupported(1, 8, 6, 1, 2, 8, 2, True)
+    assert "256" in W._round_unsupported(1, 8, 260, 1, 2, 8, 2, True)
+    assert "255 units" in W._round_unsupported(1, 8, 64, 1, 300, 8, 2, True)
+    assert "16384 slots" in W._round_unsupported(4096, 8, 64, 8, 2, 8, 2, True)
+    lib = _lib.library()
+    s = W._round_struct(32, 256, 64, 8, 8, 512, 8, True, 1e-6, 1e-6,
+                        **{name: 256 for name in W._ROUND_POINTERS})
+    s.W1 = None
+    assert lib.hsn_win_cell_round_check(ctypes.byref(s)) == 1
+    assert "NULL" in lib.hsn_win_last_error().decode()
+    s.W1 = 256
+    n = ctypes.c_int64(0)
+    assert lib.hsn_win_cell_round_workspace(ctypes.byref(s), ctypes.byref(n)) == 0
+    P, d = 32 * 8, 64
+    assert n.value == P * 4 * d * 4 + P * d * 4 + 8 * P * d * 4  # v, the gate, 8 chunks of F
+
+
 def test_trainer_pass_arguments_are_checked_before_any_launch():
     """The trainer passes' list checks run on the host: a bad unit count, a tensor that is not a
     whole number of units, a NULL pointer of a non-empty tensor and a negative size return

@@ -751,3 +751,95 @@ def test_adamw_oracle_first_steps_reduce_to_their_closed_forms():
     pu1, mu, vu = O.tr_adamw_units(pu, gu, z.reshape(M, -1), z.reshape(M, -1), table, 0.001, eps, True)
     assert np.array_equal(_bits(mu.reshape(-1)), _bits(md))
     assert np.array_equal(_bits(vu.reshape(-1)), _bits(vd))
+
+
+# --------------------------------------------------------------------------------------------
+# the fused cell round's contract (window_cell_round)
+# --------------------------------------------------------------------------------------------
+
+
+def _round_by_state_gradient(p):
+    """The same round from ``oracle.state_gradient.cell_round`` (the cell's equations restated
+    separately: the sources gathered and summed by hand, alpha on W_out's output) and the gated
+    update written out: ``(h', q', age', pos', h_sel)``."""
+    from oracle import state_gradient as S
+
+    B, N, d = p["h"].shape
+    K = p["cells"].shape[1]
+    D = p["pad_src"].shape[1]
+    w = S.CellWeights(
+        w1=p["W1"], b1=p["b1"], w2=p["W2"], b2=p["b2"], gate_w=p["gate_w"], gate_b=p["gate_b"],
+        norm_gain=p["norm_w"], norm_eps=p["norm_eps"],
+        cand_gain=p["cand_w"] if p["cand_norm"] else None, cand_eps=p["cand_eps"],
+        w_out=p["W_out"], v=p["V"], pad_src=p["pad_src"],
+        pad_mask=torch.ones(N, D, dtype=torch.bool), edge_weights=p["edge_w"], activation="gelu")
+    extra = torch.cat([p["u"], p["eps"]], dim=-1)[:, None, :].expand(B, K, 2 * d)
+    c, b, _ = S.cell_round(p["h"], extra, p["cells"], p["units"], p["valid"], p["alpha"], w)
+    h2 = p["h"].clone()
+    age2 = p["age"] + 1
+    for r in range(B):
+        for k in range(K):
+            if bool(p["valid"][r, k]):
+                i = int(p["cells"][r, k])
+                h2[r, i] = (1 - b[r, k]) * p["h"][r, i] + b[r, k] * c[r, k]
+                age2[r, i] = 0
+    q2 = p["q"] + (h2 - p["h"]).sum(dim=1) / N
+    safe = torch.where(p["valid"], p["cells"], torch.zeros_like(p["cells"]))
+    h_sel = torch.stack([h2[r, safe[r]] for r in range(B)])
+    return h2, q2, age2, p["pos"] + 1, h_sel
+
+
+@pytest.mark.parametrize("case", [
+    dict(),  # the reference's default cell at B=4
+    dict(pad=0.4, seed=3),  # a budget that pads slots
+    dict(cand_norm=False, B=5, seed=4),
+    dict(B=7, N=11, d=24, K=5, M=3, H=77, D=3, seed=5, pad=0.2),  # its odd sizes
+    dict(B=1, N=32, d=64, K=1, M=1, H=33, D=4, seed=6),  # one unit, one slot
+    dict(alpha_one=False, seed=7, B=3),  # alpha away from 1: its place relative to the norm
+    dict(alpha_one=False, cand_norm=False, seed=8, B=3),
+    dict(D=0, seed=9, B=2),  # no edges
+])
+def test_window_cell_round_matches_the_cell_equations(case):
+    """``window_cell_round`` (the P2.9 ops, golden-pinned, composed in the native round's order)
+    equals the cell's equations restated separately, to float64 rounding; cells no slot writes
+    keep their state bit for bit."""
+    from conftest import round_problem
+
+    p = round_problem(**case)
+    got = O.window_cell_round(**p)
+    want = _round_by_state_gradient(p)
+    for name, a, b in zip(("h", "q", "age", "pos", "h_sel"), got, want):
+        if a.dtype == torch.int64:
+            assert torch.equal(a, b), name
+        else:
+            _close(a, b, atol=1e-12, rtol=1e-12)
+    written = O.selection_mask(p["cells"], p["valid"], p["h"].shape[1])
+    assert torch.equal(got[0][~written], p["h"][~written])
+
+
+@pytest.mark.parametrize("cand_norm", [False, True])
+def test_window_cell_round_closed_form(cand_norm):
+    """With the first layer and the gate's weights zero, F is the unit's output bias and the gate
+    its bias: h' = (1 - sigmoid(gate_b)) h + sigmoid(gate_b) tanh(alpha W_out b2_j) (with the
+    candidate norm, W_out b2_j normalised first). W_out is not symmetric, so a transposed W_out
+    fails; alpha is not 1, so alpha on the wrong side of the norm fails."""
+    from conftest import round_problem
+
+    p = round_problem(B=3, N=9, d=8, K=3, M=2, H=5, D=2, cand_norm=cand_norm, alpha_one=False,
+                      seed=12)
+    p["W1"] = torch.zeros_like(p["W1"])
+    p["b1"] = torch.zeros_like(p["b1"])
+    p["gate_w"] = torch.zeros_like(p["gate_w"])
+    h2, q2, _, _, _ = O.window_cell_round(**p)
+    sg = 1.0 / (1.0 + torch.exp(-p["gate_b"]))
+    for r in range(3):
+        for k in range(3):
+            if not bool(p["valid"][r, k]):
+                continue
+            i, j, a = int(p["cells"][r, k]), int(p["units"][r, k]), float(p["alpha"][r, k])
+            y = p["W_out"] @ p["b2"][j]
+            if cand_norm:
+                y = y / torch.sqrt((y * y).mean() + p["cand_eps"]) * p["cand_w"]
+            c = torch.tanh(a * y)
+            _close(h2[r, i], (1 - sg) * p["h"][r, i] + sg * c, atol=1e-13, rtol=1e-13)
+    assert not torch.allclose(p["W_out"], p["W_out"].T)
