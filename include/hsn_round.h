@@ -67,7 +67,8 @@ typedef struct hsn_cell_round {
     const float* b2;        /* [M, d] */
     const float* W_out;     /* [d, d] */
     const float* cand_w;    /* [d] (cand_norm; else unused) */
-    void* work;             /* hsn_win_cell_round_workspace() bytes, 256-byte aligned */
+    void* work;             /* hsn_win_cell_round_workspace() bytes; work, u, eps, h and h_new
+                             * 16-byte aligned */
     /* the state after the position and the selected slots' new states */
     float* h_new;      /* [B, N, d] */
     float* q_new;      /* [B, d] */

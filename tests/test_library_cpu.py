@@ -114,7 +114,7 @@ def test_reverse_sweep_check_follows_the_kernels_limits():
 def test_cell_round_check_and_workspace_follow_the_kernels_limits():
     """The fused cell round's check and scratch size are host arithmetic (no GPU): the
     reference's cells and the sweep's model are taken; d not a multiple of 4, d above 256, more
-    than 255 units, more than 16384 slots and a NULL buffer are not, each with its reason."""
+    than 255 units, more than 8192 slots and a NULL buffer are not, each with its reason."""
     import ctypes
 
     from hsn_amd import _lib, build
@@ -129,7 +129,7 @@ def test_cell_round_check_and_workspace_follow_the_kernels_limits():
     assert "multiple of 4" in W._round_unsupported(1, 8, 6, 1, 2, 8, 2, True)
     assert "256" in W._round_unsupported(1, 8, 260, 1, 2, 8, 2, True)
     assert "255 units" in W._round_unsupported(1, 8, 64, 1, 300, 8, 2, True)
-    assert "16384 slots" in W._round_unsupported(4096, 8, 64, 8, 2, 8, 2, True)
+    assert "8192 slots" in W._round_unsupported(2048, 8, 64, 8, 2, 8, 2, True)
     lib = _lib.library()
     s = W._round_struct(32, 256, 64, 8, 8, 512, 8, True, 1e-6, 1e-6,
                         **{name: 256 for name in W._ROUND_POINTERS})
@@ -140,7 +140,7 @@ def test_cell_round_check_and_workspace_follow_the_kernels_limits():
     n = ctypes.c_int64(0)
     assert lib.hsn_win_cell_round_workspace(ctypes.byref(s), ctypes.byref(n)) == 0
     P, d = 32 * 8, 64
-    assert n.value == P * 4 * d * 4 + P * d * 4 + 8 * P * d * 4  # v, the gate, 8 chunks of F
+    assert n.value == P * d * 4 + 8 * P * d * 4  # the gate, 8 chunks of F
 
 
 def test_trainer_pass_arguments_are_checked_before_any_launch():
