@@ -65,7 +65,7 @@ __host__ __device__ inline Work work_of(int B, int K, int d, int H) {
 
 // LDS of each launch (rows padded by one float: the 16 rows of a tile fall on distinct banks).
 struct UnitsLds {
-    int ucache, ccache, count, rows, meta, cell, src, w, gain, b1, hbar, x, rms, red, act, sh, sx,
+    int ucache, ccache, count, rows, meta, cell, src, w, gain, b1, hbar, x, red, act, sh, sx,
         sr, sa, bytes;
 };
 __host__ __device__ inline UnitsLds units_lds(int P, int d, int D) {
@@ -86,8 +86,7 @@ __host__ __device__ inline UnitsLds units_lds(int P, int d, int D) {
     L.b1 = L.gain + 4 * 4 * d;                       // float [64]: the chunk's first-layer bias
     L.hbar = L.b1 + 4 * kChunk;                      // float [16][sh]: the weighted source sums
     L.x = L.hbar + 4 * kRows * L.sh;                 // float [16][sx]: the inputs, then v
-    L.rms = L.x + 4 * kRows * L.sx;                  // float [16]
-    L.red = L.rms + 4 * kRows;                       // float [4][16][sr]: the waves' hidden shares
+    L.red = L.x + 4 * kRows * L.sx;                  // float [4][16][sr]: the waves' hidden shares
     L.act = L.red + 4 * kRoundWaves * kRows * L.sr;  // float [16][sa]
     L.bytes = L.act + 4 * kRows * L.sa;
     return L;
@@ -146,6 +145,7 @@ __device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
 template <int PRE, typename Load>
 __device__ __forceinline__ v4f product(const float* a, int q, const float (&pre)[PRE],
                                        bool use_pre, Load load) {
+    auto rd = [&](int i) { return a[i]; };
     v4f acc0 = {0.0f, 0.0f, 0.0f, 0.0f};
     v4f acc1 = {0.0f, 0.0f, 0.0f, 0.0f};
     int s = 0;
@@ -154,7 +154,7 @@ __device__ __forceinline__ v4f product(const float* a, int q, const float (&pre)
         for (int b0 = 0; b0 < PRE; b0 += kBlock) {
             float av[kBlock];
 #pragma unroll
-            for (int i = 0; i < kBlock; ++i) av[i] = a[b0 + i];
+            for (int i = 0; i < kBlock; ++i) av[i] = rd(b0 + i);
 #pragma unroll
             for (int i = 0; i < kBlock; i += 2) {
                 acc0 = mfma(av[i], pre[b0 + i], acc0);
@@ -165,7 +165,7 @@ __device__ __forceinline__ v4f product(const float* a, int q, const float (&pre)
     } else if (use_pre) {  // q < PRE (register arrays take compile-time indices only)
 #pragma unroll
         for (int i = 0; i < PRE; ++i)
-            if (i < q) acc0 = mfma(a[i], pre[i], acc0);
+            if (i < q) acc0 = mfma(rd(i), pre[i], acc0);
         s = q;
     }
     const int blocks = (q - s) / kBlock;
@@ -182,7 +182,7 @@ __device__ __forceinline__ v4f product(const float* a, int q, const float (&pre)
         }
         float av[kBlock];
 #pragma unroll
-        for (int i = 0; i < kBlock; ++i) av[i] = a[s0 + i];
+        for (int i = 0; i < kBlock; ++i) av[i] = rd(s0 + i);
 #pragma unroll
         for (int i = 0; i < kBlock; i += 2) {
             acc0 = mfma(av[i], cur[i], acc0);
@@ -191,7 +191,7 @@ __device__ __forceinline__ v4f product(const float* a, int q, const float (&pre)
 #pragma unroll
         for (int i = 0; i < kBlock; ++i) cur[i] = nxt[i];
     }
-    for (int t = s + blocks * kBlock; t < q; ++t) acc0 = mfma(a[t], load(t), acc0);
+    for (int t = s + blocks * kBlock; t < q; ++t) acc0 = mfma(rd(t), load(t), acc0);
     return acc0 + acc1;
 }
 
@@ -261,7 +261,6 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
     float* b1c = reinterpret_cast<float*>(lds + L.b1);
     float* hbar = reinterpret_cast<float*>(lds + L.hbar);
     float* x = reinterpret_cast<float*>(lds + L.x);
-    float* rms = reinterpret_cast<float*>(lds + L.rms);
     float* red = reinterpret_cast<float*>(lds + L.red);
     float* act = reinterpret_cast<float*>(lds + L.act);
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
@@ -276,12 +275,27 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
 
     // ---- the position's units and cells; which unit's which row tile this workgroup takes ----
     for (int j = tid; j < M; j += kRoundThreads) count[j] = 0;
-    for (int q = tid; q < P; q += kRoundThreads) {
+    // the first slots' decisions and the norm's gain
+    const bool q_first = tid < P;
+    const uint8_t valid0 = q_first ? s.valid[tid] : uint8_t(0);
+    const int64_t cell0 = q_first ? s.cells[tid] : int64_t(-1);
+    const int64_t unit0 = q_first ? s.units[tid] : int64_t(0);
+    const float gain0 = tid < n ? s.norm_w[tid] : 0.0f;
+    if (q_first) {
+        const bool live = valid0 && cell0 >= 0 && cell0 < N;
+        const int unit = static_cast<int>(unit0 < 0 ? 0 : (unit0 >= M ? M - 1 : unit0));
+        ucache[tid] = live ? static_cast<uint8_t>(unit) : uint8_t(0xff);
+        ccache[tid] = live ? static_cast<int>(cell0) : -1;
+    }
+    for (int q = tid + kRoundThreads; q < P; q += kRoundThreads) {
         const int cell = live_cell(s, q);
         ucache[q] = cell >= 0 ? static_cast<uint8_t>(unit_of(s, q)) : uint8_t(0xff);
         ccache[q] = cell;
     }
-    // the slot-independent weights of the products before the MLP, in flight meanwhile
+    if (tid < n) gain[tid] = gain0;
+    for (int c = tid + kRoundThreads; c < n; c += kRoundThreads) gain[c] = s.norm_w[c];
+    __syncthreads();
+    // the slot-independent weights of the products before the MLP, in flight from here on
     const int colg = wave * 16 + lr;
     const bool okg = lead && wave < tiles_d && colg < d;
     float gpre[kPreGate], vpre[kPreV];
@@ -289,8 +303,6 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
     preload_row(vpre, s.V + int64_t(wave < tiles_d && colg < d ? colg : 0) * d + g * (d / 4),
                 d / 4, wave < tiles_d && colg < d);
     const float gbias = okg ? s.gate_b[colg] : 0.0f;
-    for (int c = tid; c < n; c += kRoundThreads) gain[c] = s.norm_w[c];
-    __syncthreads();
     for (int q = tid; q < P; q += kRoundThreads)  // integer counts: any order gives the same
         if (ucache[q] != 0xff) atomicAdd(&count[ucache[q]], 1);
     __syncthreads();
@@ -336,17 +348,10 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
     if (j < 0) return;  // past the last row tile (uniform)
 
     // ---- the tile's in-edges, then the unit's weights in flight while the inputs come in ----
-    for (int e = tid; e < kRows * D; e += kRoundThreads) {
-        const int cell = cell_of[e / D];
-        int64_t src = -1;
-        float w = 0.0f;
-        if (cell >= 0) {
-            src = s.pad_src[int64_t(cell) * D + e % D];
-            w = s.edge_w[int64_t(cell) * D + e % D];
-        }
-        srcs[e] = src >= 0 && src < N ? static_cast<int>(src) : -1;
-        ws[e] = w;
-    }
+    const bool e_first = tid < kRows * D;
+    const int ecell0 = e_first ? cell_of[tid / D] : -1;
+    const int64_t esrc0 = ecell0 >= 0 ? s.pad_src[int64_t(ecell0) * D + tid % D] : int64_t(-1);
+    const float ew0 = ecell0 >= 0 ? s.edge_w[int64_t(ecell0) * D + tid % D] : 0.0f;
     // first layer: wavefront w takes the reduction quarter [w n / 4, (w + 1) n / 4) of all 64
     // columns, lane group g its q1 = n / 16 steps from k = w n / 4 + g q1; a 16-byte load gives
     // four column tiles (tile t's column i is h0 + 4 i + t)
@@ -359,7 +364,7 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
 #pragma unroll
     for (int i = 0; i < kPreW1; ++i)
         w1pre[i] = i < q1 ? row4(w1 + int64_t(i) * H, c1, H, al1) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (tid < kChunk) b1c[tid] = h0 + tid < H ? s.b1[int64_t(j) * H + h0 + tid] : 0.0f;
+    const float bias1 = tid < kChunk && h0 + tid < H ? s.b1[int64_t(j) * H + h0 + tid] : 0.0f;
     // second layer: as before, a 16-column tile a wavefront over the chunk's 64 rows
     const int col2 = wave * 16 + lr;
     const bool ok2 = wave < tiles_d && col2 < d;
@@ -367,6 +372,22 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
     const float* w2 = s.W2 + (int64_t(j) * H + h0 + g * (kChunk / 4)) * d + (ok2 ? col2 : 0);
     float w2pre[kPreW2];
     preload_col(w2pre, w2, d, kChunk / 4, rows2, ok2);
+    if (e_first) {
+        srcs[tid] = esrc0 >= 0 && esrc0 < N ? static_cast<int>(esrc0) : -1;
+        ws[tid] = ew0;
+    }
+    for (int e = tid + kRoundThreads; e < kRows * D; e += kRoundThreads) {
+        const int cell = cell_of[e / D];
+        int64_t src = -1;
+        float w = 0.0f;
+        if (cell >= 0) {
+            src = s.pad_src[int64_t(cell) * D + e % D];
+            w = s.edge_w[int64_t(cell) * D + e % D];
+        }
+        srcs[e] = src >= 0 && src < N ? static_cast<int>(src) : -1;
+        ws[e] = w;
+    }
+    if (tid < kChunk) b1c[tid] = bias1;
     __syncthreads();
 
     // ---- the inputs: the state blocks and each slot's weighted source sum, four columns a thread
@@ -433,18 +454,25 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
         }
 #pragma unroll
         for (int i = 0; i < kPer; ++i) ss[i] = group_sum<kWave>(ss[i]);
-        if (lane < kPer) {
-            float mine = ss[0];
+        float scale[kPer];
 #pragma unroll
-            for (int i = 1; i < kPer; ++i) mine = lane == i ? ss[i] : mine;
-            rms[wave * kPer + lane] = rsqrtf(mine / static_cast<float>(n) + s.norm_eps);
+        for (int i = 0; i < kPer; ++i) scale[i] = rsqrtf(ss[i] / static_cast<float>(n) + s.norm_eps);
+        // v = x scale gain in place, the wavefront's own rows (reads batched ahead of the writes)
+        for (int c0 = lane; c0 < n; c0 += 4 * kWave) {
+            float t[kPer][4];
+#pragma unroll
+            for (int i = 0; i < kPer; ++i)
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    t[i][m] = c0 + m * kWave < n ? x[(wave * kPer + i) * L.sx + c0 + m * kWave] : 0.0f;
+#pragma unroll
+            for (int i = 0; i < kPer; ++i)
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    if (c0 + m * kWave < n)
+                        x[(wave * kPer + i) * L.sx + c0 + m * kWave] =
+                            t[i][m] * scale[i] * gain[c0 + m * kWave];
         }
-    }
-    __syncthreads();
-#pragma unroll 4
-    for (int e = tid; e < kRows * n; e += kRoundThreads) {
-        const int pp = e / n, c = e % n;
-        x[pp * L.sx + c] = x[pp * L.sx + c] * rms[pp] * gain[c];
     }
     __syncthreads();
 
