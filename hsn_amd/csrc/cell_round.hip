@@ -65,7 +65,7 @@ __host__ __device__ inline Work work_of(int B, int K, int d, int H) {
 
 // LDS of each launch (rows padded by one float: the 16 rows of a tile fall on distinct banks).
 struct UnitsLds {
-    int ucache, ccache, count, rows, meta, cell, src, w, gain, b1, hbar, x, red, act, sh, sx,
+    int ucache, ccache, count, rows, meta, cell, src, w, gain, b1, gb, hbar, x, red, gred, act, sh, sx,
         sr, sa, bytes;
 };
 __host__ __device__ inline UnitsLds units_lds(int P, int d, int D) {
@@ -84,10 +84,12 @@ __host__ __device__ inline UnitsLds units_lds(int P, int d, int D) {
     L.w = L.src + 4 * kRows * D;                     // float [16][D]: their edge weights
     L.gain = L.w + 4 * kRows * D;                    // float [4 d]: the cell norm's gain
     L.b1 = L.gain + 4 * 4 * d;                       // float [64]: the chunk's first-layer bias
-    L.hbar = L.b1 + 4 * kChunk;                      // float [16][sh]: the weighted source sums
+    L.gb = L.b1 + 4 * kChunk;                        // float [16]: the gate tile's bias
+    L.hbar = L.gb + 4 * 16;                          // float [16][sh]: the weighted source sums
     L.x = L.hbar + 4 * kRows * L.sh;                 // float [16][sx]: the inputs, then v
     L.red = L.x + 4 * kRows * L.sx;                  // float [4][16][sr]: the waves' hidden shares
-    L.act = L.red + 4 * kRoundWaves * kRows * L.sr;  // float [16][sa]
+    L.gred = L.red + 4 * kRoundWaves * kRows * L.sr;  // float [4][16][17]: the gate tile's shares
+    L.act = L.gred + 4 * kRoundWaves * kRows * 17;   // float [16][sa]
     L.bytes = L.act + 4 * kRows * L.sa;
     return L;
 }
@@ -227,7 +229,7 @@ __device__ __forceinline__ void preload_col(float (&pre)[PRE], const float* w, i
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
 // ---- units: the slots' inputs and their unit's MLP, 64 hidden units a workgroup -----------------
-constexpr int kPreGate = 64;  // gate weights a lane of the chunk-0 workgroup holds early (d <= 64)
+constexpr int kPreGate = 16;  // gate weights a lane holds early (its share of one gate tile)
 constexpr int kPreV = 16;     // V weights likewise
 constexpr int kPreW1 = 16;    // first-layer steps (float4: four column tiles) a lane holds early
 constexpr int kPreW2 = 16;    // second-layer weights (all of a chunk's)
@@ -263,11 +265,13 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
     float* x = reinterpret_cast<float*>(lds + L.x);
     float* red = reinterpret_cast<float*>(lds + L.red);
     float* act = reinterpret_cast<float*>(lds + L.act);
+    float* gred = reinterpret_cast<float*>(lds + L.gred);
+    float* gb = reinterpret_cast<float*>(lds + L.gb);
     const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
     const int lr = lane & 15, g = lane >> 4;
     const int chunk = blockIdx.y;
     const int h0 = chunk * kChunk;
-    const bool lead = chunk == 0;  // the workgroup that also computes its slots' gate
+    const bool lead = chunk == 0;
     const int tiles_d = (d + 15) / 16;
     const Work W = work_of(s.B, K, d, H);
     float* gate_out = reinterpret_cast<float*>(static_cast<unsigned char*>(s.work) + W.gate);
@@ -295,14 +299,23 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
     if (tid < n) gain[tid] = gain0;
     for (int c = tid + kRoundThreads; c < n; c += kRoundThreads) gain[c] = s.norm_w[c];
     __syncthreads();
-    // the slot-independent weights of the products before the MLP, in flight from here on
-    const int colg = wave * 16 + lr;
-    const bool okg = lead && wave < tiles_d && colg < d;
+    // the slot-independent weights of the products before the MLP, in flight from here on. The
+    // gate's column tiles go to the chunks (tile c to chunk c, the four wavefronts splitting its
+    // reduction) when there are as many chunks as tiles; otherwise chunk 0 computes them all.
+    const bool split_gate = static_cast<int>(gridDim.y) >= tiles_d;
+    const int gtile = split_gate && chunk < tiles_d ? chunk : -1;
+    const int qg = n / 16;                      // a lane group's steps of the split gate tile
+    const int kg = wave * (n / 4) + g * qg;     // their first reduction index
+    const int gcol = gtile * 16 + lr;
+    const bool okg = gtile >= 0 && gcol < d;
+    const float* gw = s.gate_w + int64_t(okg ? gcol : 0) * n + kg;
     float gpre[kPreGate], vpre[kPreV];
-    preload_row(gpre, s.gate_w + int64_t(okg ? colg : 0) * n + g * d, d, okg);
-    preload_row(vpre, s.V + int64_t(wave < tiles_d && colg < d ? colg : 0) * d + g * (d / 4),
-                d / 4, wave < tiles_d && colg < d);
-    const float gbias = okg ? s.gate_b[colg] : 0.0f;
+    preload_row(gpre, gw, qg, okg);
+    const int colv = wave * 16 + lr;
+    preload_row(vpre, s.V + int64_t(wave < tiles_d && colv < d ? colv : 0) * d + g * (d / 4),
+                d / 4, wave < tiles_d && colv < d);
+    const float gbias0 = gtile >= 0 && tid < 16 && gtile * 16 + tid < d ? s.gate_b[gtile * 16 + tid]
+                                                                     : 0.0f;
     for (int q = tid; q < P; q += kRoundThreads)  // integer counts: any order gives the same
         if (ucache[q] != 0xff) atomicAdd(&count[ucache[q]], 1);
     __syncthreads();
@@ -388,6 +401,7 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
         ws[e] = w;
     }
     if (tid < kChunk) b1c[tid] = bias1;
+    if (tid < 16) gb[tid] = gbias0;
     __syncthreads();
 
     // ---- the inputs: the state blocks and each slot's weighted source sum, four columns a thread
@@ -439,17 +453,32 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
     }
     __syncthreads();
 
-    // the cell norm: 1 / sqrt(mean(x^2) + eps) a slot, a wavefront four slots side by side
+    // the cell norm: 1 / sqrt(mean(x^2) + eps) a slot, a wavefront four slots side by side, then
+    // v = x scale gain in place (the wavefront's own rows; one read of each value when a row is
+    // at most four values a lane)
     {
         constexpr int kPer = kRows / kRoundWaves;
         float ss[kPer];
 #pragma unroll
         for (int i = 0; i < kPer; ++i) ss[i] = 0.0f;
-        for (int c = lane; c < n; c += kWave) {
+        const bool one_pass = n <= 4 * kWave;
+        float t[kPer][4];
+        if (one_pass) {
 #pragma unroll
-            for (int i = 0; i < kPer; ++i) {
-                const float t = x[(wave * kPer + i) * L.sx + c];
-                ss[i] += t * t;
+            for (int i = 0; i < kPer; ++i)
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const int c = lane + m * kWave;
+                    t[i][m] = c < n ? x[(wave * kPer + i) * L.sx + c] : 0.0f;
+                    ss[i] += t[i][m] * t[i][m];
+                }
+        } else {
+            for (int c = lane; c < n; c += kWave) {
+#pragma unroll
+                for (int i = 0; i < kPer; ++i) {
+                    const float v = x[(wave * kPer + i) * L.sx + c];
+                    ss[i] += v * v;
+                }
             }
         }
 #pragma unroll
@@ -457,36 +486,44 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
         float scale[kPer];
 #pragma unroll
         for (int i = 0; i < kPer; ++i) scale[i] = rsqrtf(ss[i] / static_cast<float>(n) + s.norm_eps);
-        // v = x scale gain in place, the wavefront's own rows (reads batched ahead of the writes)
-        for (int c0 = lane; c0 < n; c0 += 4 * kWave) {
-            float t[kPer][4];
+        if (one_pass) {
 #pragma unroll
             for (int i = 0; i < kPer; ++i)
 #pragma unroll
-                for (int m = 0; m < 4; ++m)
-                    t[i][m] = c0 + m * kWave < n ? x[(wave * kPer + i) * L.sx + c0 + m * kWave] : 0.0f;
+                for (int m = 0; m < 4; ++m) {
+                    const int c = lane + m * kWave;
+                    if (c < n) x[(wave * kPer + i) * L.sx + c] = t[i][m] * scale[i] * gain[c];
+                }
+        } else {
+            for (int c = lane; c < n; c += kWave) {
 #pragma unroll
-            for (int i = 0; i < kPer; ++i)
-#pragma unroll
-                for (int m = 0; m < 4; ++m)
-                    if (c0 + m * kWave < n)
-                        x[(wave * kPer + i) * L.sx + c0 + m * kWave] =
-                            t[i][m] * scale[i] * gain[c0 + m * kWave];
+                for (int i = 0; i < kPer; ++i)
+                    x[(wave * kPer + i) * L.sx + c] = x[(wave * kPer + i) * L.sx + c] * scale[i] *
+                                                      gain[c];
+            }
         }
     }
     __syncthreads();
 
-    // the gate (chunk 0): sigmoid(gate_w v + gate_b), B[k][col] = gate_w[col][k]
-    if (lead) {
+    // the gate: sigmoid(gate_w v + gate_b), B[k][col] = gate_w[col][k]
+    if (gtile >= 0) {  // this wavefront's share of the chunk's tile, summed after the hidden layer
+        const v4f acc = product(x + lr * L.sx + kg, qg, gpre, true, [&](int k) {
+            const float w = gw[k];
+            return okg ? w : 0.0f;
+        });
+#pragma unroll
+        for (int r = 0; r < 4; ++r) gred[(wave * kRows + 4 * g + r) * 17 + lr] = acc[r];
+    } else if (!split_gate && lead) {  // fewer chunks than tiles: chunk 0 takes them all
+        const float none[kBlock] = {};
         for (int tile = wave; tile < tiles_d; tile += kRoundWaves) {
             const int col = tile * 16 + lr;
             const bool ok = col < d;
             const float* grow = s.gate_w + int64_t(ok ? col : 0) * n + g * d;
-            const v4f acc = product(x + lr * L.sx + g * d, d, gpre, tile == wave, [&](int k) {
+            const v4f acc = product(x + lr * L.sx + g * d, d, none, false, [&](int k) {
                 const float w = grow[k];
                 return ok ? w : 0.0f;
             });
-            const float bias = tile == wave ? gbias : (ok ? s.gate_b[col] : 0.0f);
+            const float bias = ok ? s.gate_b[col] : 0.0f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int q = rows[4 * g + r];
@@ -539,6 +576,14 @@ __global__ __launch_bounds__(kRoundThreads) void round_units(hsn_cell_round s) {
 #pragma unroll
         for (int w = 0; w < kRoundWaves; ++w) z += red[(w * kRows + row) * L.sr + c];
         act[row * L.sa + c] = h0 + c < H ? gelu_erf(z + b1c[c]) : 0.0f;
+    }
+    if (gtile >= 0 && tid < kRows * 16) {  // the gate tile's shares in wave order
+        const int row = tid / 16, c = tid % 16;
+        const int col = gtile * 16 + c, q = rows[row];
+        float z = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kRoundWaves; ++w) z += gred[(w * kRows + row) * 17 + c];
+        if (col < d && q >= 0) gate_out[int64_t(q) * d + col] = act_sigmoid(z + gb[c]);
     }
     __syncthreads();
 
