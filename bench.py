@@ -63,6 +63,11 @@ def _args():
     p.add_argument("--three-steps", action="store_true",
                    help="the reverse sweep's three glue steps around all-units GEMMs instead of "
                         "the fused step")
+    p.add_argument("--round", choices=["ref", "tiny"], default=None,
+                   help="measure the fused cell round (hsn::window_cell_round) over a window of "
+                        "positions at this workload instead of the window (not the headline line)")
+    p.add_argument("--round-positions", type=int, default=64,
+                   help="positions a --round step runs (the state carried from one to the next)")
     p.add_argument("--trainer", choices=sorted(TRAINER_LISTS), default=None,
                    help="measure the trainer's AdamW pass (hsn_tr_adamw) over a synthetic "
                         "parameter list instead of the window (not the headline line)")
@@ -412,6 +417,135 @@ def _sweep_main(args) -> int:
     return 0
 
 
+def _round_main(args) -> int:
+    """The fused cell round over a window of T synthetic positions (the state carried from one
+    position to the next, as the forward sweep runs it): a step is the T positions' rounds, inputs
+    and decisions resident in HBM; ``value`` is positions/s (B x T per step) from replays of the
+    step captured as a HIP graph (the op allocates nothing the graph cannot hold), the eager rate
+    beside it. The roofline treats the round's two launches as one unit: the algorithmic bytes
+    of a position (``hsn_amd.workload.round_bytes``) over its device time, from HIP events on the
+    replay stream around the timed replays (the two kernels' rocprofv3 averages add up to it)."""
+    import torch
+
+    from hsn_amd.kernels.window import cell_round_op
+    from hsn_amd.workload import (ROUND_CONFIGS, make_round_cell, make_round_positions,
+                                  round_bytes)
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    cfg = ROUND_CONFIGS[args.round]
+    T = args.round_positions
+    cell, edge_w = make_round_cell(N=cfg["N"], d=cfg["d"], M=cfg["M"], H=cfg["H"], D=cfg["D"],
+                                   seed=args.seed, device=dev)
+    pos = make_round_positions(B=cfg["B"], K=cfg["K"], N=cfg["N"], d=cfg["d"], M=cfg["M"], T=T,
+                               seed=args.seed, device=dev)
+    weights = [t.detach() for t in (cell.V.weight, edge_w, cell.graph._pad_src, cell.norm.weight,
+                                    cell.gate.weight, cell.gate.bias, cell.units.W1,
+                                    cell.units.b1, cell.units.W2, cell.units.b2,
+                                    cell.W_out.weight, cell.cand_norm.weight)]
+    alpha = pos["valid"].float()
+    start = pos["state"]
+
+    def one(t, h, q, age):
+        return cell_round_op(pos["u"][t], pos["eps"][t], h, q, age, pos["cells"][t],
+                             pos["units"][t], pos["valid"][t], alpha[t], *weights, True, 1e-6,
+                             1e-6)[:3]
+
+    def step():
+        h, q, age = start.h, start.q, start.age
+        for t in range(T):
+            h, q, age = one(t, h, q, age)
+        return h
+
+    with torch.no_grad():
+        for _ in range(max(1, args.warmup)):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        eager_secs = (time.perf_counter() - t0) / args.steps
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        graph.replay()
+        torch.cuda.synchronize()
+        ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        t0 = time.perf_counter()
+        ev[0].record()
+        for _ in range(args.steps):
+            graph.replay()
+        ev[1].record()
+        torch.cuda.synchronize()
+        step_secs = (time.perf_counter() - t0) / args.steps
+    device_us = ev[0].elapsed_time(ev[1]) / (args.steps * T) * 1e3
+    # units a position reads: all M at the bench's shape (B K = 256 slots over 8 units)
+    present = int(torch.unique(pos["units"][0][pos["valid"][0]]).numel())
+    nbytes = round_bytes(cfg, present)
+    achieved = nbytes / (device_us * 1e-6) / 1e9
+    positions = cfg["B"] * T
+    result = {
+        "metric": f"fused cell round positions/sec ({args.round} model, 1 GPU)",
+        "value": positions / step_secs,
+        "unit": "positions/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_secs * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (hsn_amd/workload.py make_round_cell, make_round_positions)",
+        "config": {"workload": f"cell_round_{args.round}", **cfg, "positions": T,
+                   "timing": "HIP graph replay of the T positions' rounds",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "round_units + round_back (one position)",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "bytes_per_position": nbytes},
+        "position_us_device": device_us,
+        "position_us_wall": step_secs / T * 1e6,
+        "position_us_eager": eager_secs / T * 1e6,
+    }
+    if not args.no_cpu:  # the oracle on a bounded sample: 2 rows x 4 positions, one thread
+        from oracle import hsn_oracle as O
+
+        torch.set_num_threads(1)
+        ccell, cedge = make_round_cell(N=cfg["N"], d=cfg["d"], M=cfg["M"], H=cfg["H"],
+                                       D=cfg["D"], seed=args.seed)
+        cpos = make_round_positions(B=2, K=cfg["K"], N=cfg["N"], d=cfg["d"], M=cfg["M"], T=4,
+                                    seed=args.seed)
+        w = dict(V=ccell.V.weight.detach(), edge_w=cedge, pad_src=ccell.graph._pad_src,
+                 norm_w=ccell.norm.weight.detach(), norm_eps=1e-6,
+                 gate_w=ccell.gate.weight.detach(), gate_b=ccell.gate.bias.detach(),
+                 W1=ccell.units.W1, b1=ccell.units.b1, W2=ccell.units.W2, b2=ccell.units.b2,
+                 W_out=ccell.W_out.weight.detach(), cand_w=ccell.cand_norm.weight.detach(),
+                 cand_norm=True, cand_eps=1e-6)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            st = cpos["state"]
+            h, q, age, p_ = st.h, st.q, st.age, st.pos
+            for t in range(4):
+                h, q, age, p_, _ = O.window_cell_round(
+                    cpos["u"][t], cpos["eps"][t], h, q, age, p_, cpos["cells"][t],
+                    cpos["units"][t], cpos["valid"][t], cpos["valid"][t].float(), **w)
+            reps += 1
+            secs = time.perf_counter() - t0
+            if secs >= args.cpu_seconds:
+                break
+        result["cpu_baseline"] = {
+            "value": 2 * 4 * reps / secs, "unit": "positions/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} x (2 rows x 4 positions of the {args.round} model), the "
+                      f"repository's PyTorch-CPU oracle in fp32 ({secs:.1f} s)",
+        }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     args = _args()
     if args.gpus != 1:
@@ -423,6 +557,8 @@ def main() -> int:
         return _trainer_main(args)
     if args.sweep:
         return _sweep_main(args)
+    if args.round:
+        return _round_main(args)
     import torch
 
     from hsn_amd import window
