@@ -843,3 +843,33 @@ def test_window_cell_round_closed_form(cand_norm):
             c = torch.tanh(a * y)
             _close(h2[r, i], (1 - sg) * p["h"][r, i] + sg * c, atol=1e-13, rtol=1e-13)
     assert not torch.allclose(p["W_out"], p["W_out"].T)
+
+
+@pytest.mark.parametrize("mistake", [
+    ("alpha before the candidate norm",
+     "y = torch.nn.functional.rms_norm(F @ W_out.T", "y = torch.nn.functional.rms_norm((a * F) @ W_out.T"),
+    ("gate on the raw input", "b = gate(v @ gate_w.T", "b = gate(v_raw @ gate_w.T"),
+    ("W_out transposed", "c = torch.tanh((a * F) @ W_out.T)", "c = torch.tanh((a * F) @ W_out)"),
+    ("unit MLP on the raw input", "grouped_unit_mlp(v.reshape", "grouped_unit_mlp(v_raw.reshape"),
+], ids=lambda m: m[0].replace(" ", "_"))
+def test_window_cell_round_planted_mistakes_fail_the_pin(mistake):
+    """Each plausible mistake, planted in a copy of ``window_cell_round``'s source, moves the new
+    state away from the cell's equations on at least one of the pin's cases."""
+    import inspect
+
+    from conftest import round_problem
+
+    name, old, new = mistake
+    src = inspect.getsource(O.window_cell_round)
+    assert old in src, name
+    namespace = dict(vars(O))
+    exec(src.replace(old, new), namespace)
+    planted = namespace["window_cell_round"]
+    caught = 0
+    for case in (dict(), dict(alpha_one=False, seed=7, B=3),
+                 dict(alpha_one=False, cand_norm=False, seed=8, B=3)):
+        p = round_problem(**case)
+        got = planted(**p)[0]
+        want = _round_by_state_gradient(p)[0]
+        caught += not torch.allclose(got, want, atol=1e-12, rtol=1e-12)
+    assert caught, f"the planted mistake '{name}' passed the pin"
