@@ -114,6 +114,13 @@ def _cases(dev):
                                 torch.zeros(B, n, device=dev), torch.zeros(B, n, d, device=dev),
                                 torch.zeros(n, B, 5 + 2 * d + 3, dtype=torch.bfloat16, device=dev),
                                 f(B, n, 5), f(B, n, 3).to(torch.bfloat16), 1, True, 1e-6, 2), ()),
+        "window_cell_round": (window.cell_round_op,
+                              (f(B, d), f(B, d), h, q, age, cells64,
+                               torch.randint(0, M, (B, K), generator=g).to(dev), valid_b,
+                               valid_b.float(), f(d, d), torch.rand(N, 2, generator=g).to(dev),
+                               torch.randint(0, N, (N, 2), generator=g).to(dev), f(4 * d),
+                               f(d, 4 * d), f(d), f(M, 4 * d, 6), f(M, 6), f(M, 6, d), f(M, d),
+                               f(d, d), w, True, 1e-6, 1e-6), ()),
         "window_update_tape": (window.update_tape_op,
                                (y, gate, th, tq, ta, dec_c, dec_v, w, reset,
                                 torch.zeros(B, n, K, d, device=dev), torch.zeros(B, n, device=dev),
@@ -127,7 +134,7 @@ OP_NAMES = ["gather_concat", "gather_concat_backward", "grouped_unit_mlp",
             "gated_delta_update_functional", "gated_delta_update_state",
             "gated_delta_update_backward", "window_select", "window_select_tape",
             "window_select_fold", "window_cell_update", "window_update_tape",
-            "window_update_fold"]
+            "window_update_fold", "window_cell_round"]
 
 
 def _clone(args):
