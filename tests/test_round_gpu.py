@@ -81,6 +81,8 @@ CASES = {
     "wide_d": dict(B=4, N=40, d=128, K=6, M=4, H=200, D=5, seed=13),
     "d256_many_slots": dict(B=2, N=70, d=256, K=20, M=3, H=64, D=2, seed=14),  # >64 KiB of LDS
     "one_unit_many_slots": dict(B=64, N=64, d=32, K=16, M=1, H=96, D=4, seed=15),
+    "max_slots": dict(B=128, N=96, d=16, K=64, M=4, H=64, D=2, seed=16, pad=0.1),  # B K = 8192
+    "wide_row_slots": dict(B=2, N=80, d=128, K=64, M=2, H=64, D=3, seed=17),  # >64 KiB in back
 }
 
 
