@@ -425,11 +425,11 @@ class _Round(ctypes.Structure):
 
 
 def _round_struct(B, N, d, K, M, H, D, cand_norm, norm_eps, cand_eps, **pointers) -> _Round:
-    s = _Round(B=B, N=N, d=d, K=K, M=M, H=H, D=D, cand_norm=int(bool(cand_norm)),
-               norm_eps=float(norm_eps), cand_eps=float(cand_eps))
-    for name in _ROUND_POINTERS:
-        setattr(s, name, pointers.get(name))
-    return s
+    return _Round(B, N, d, K, M, H, D, int(bool(cand_norm)), float(norm_eps), float(cand_eps),
+                  *[pointers.get(name) for name in _ROUND_POINTERS])
+
+
+_round_work: dict[tuple, int] = {}  # scratch bytes by (B, K, d, H): host arithmetic only
 
 
 def _round_unsupported(B, N, d, K, M, H, D, cand_norm) -> Optional[str]:
@@ -469,10 +469,10 @@ def cell_round_error(cell) -> Optional[str]:
     return None if why is None else f"model.d={d}, model.hidden={H}, model.n_units={M}: {why}"
 
 
-def _need(name: str, t: Tensor, dtype: torch.dtype, shape: tuple, device) -> None:
-    if t.dtype != dtype or tuple(t.shape) != tuple(shape) or t.device != device:
-        raise ValueError(f"cell round: {name} must be {dtype} {list(shape)} on {device}, got "
-                         f"{t.dtype} {list(t.shape)} on {t.device}")
+def _need(name: str, t: Tensor, dtype: torch.dtype, shape: tuple, index: int) -> None:
+    if t.dtype is not dtype or t.shape != shape or t.get_device() != index:
+        raise ValueError(f"cell round: {name} must be {dtype} {list(shape)} on cuda:{index}, "
+                         f"got {t.dtype} {list(t.shape)} on {t.device}")
     if not t.is_contiguous():
         raise ValueError(f"cell round: {name} must be contiguous")
 
@@ -492,6 +492,7 @@ def cell_round_op(u: Tensor, eps: Tensor, h: Tensor, q: Tensor, age: Tensor, cel
     M, n_in, H = (int(n) for n in W1.shape)
     D = int(edge_w.shape[1])
     dev = h.device
+    index = h.get_device()
     f32, i64 = torch.float32, torch.int64
     for name, t, dtype, shape in (
             ("u", u, f32, (B, d)), ("eps", eps, f32, (B, d)), ("h", h, f32, (B, N, d)),
@@ -502,25 +503,29 @@ def cell_round_op(u: Tensor, eps: Tensor, h: Tensor, q: Tensor, age: Tensor, cel
             ("gate_w", gate_w, f32, (d, 4 * d)), ("gate_b", gate_b, f32, (d,)),
             ("W1", W1, f32, (M, 4 * d, H)), ("b1", b1, f32, (M, H)), ("W2", W2, f32, (M, H, d)),
             ("b2", b2, f32, (M, d)), ("W_out", W_out, f32, (d, d))):
-        _need(name, t, dtype, shape, dev)
+        _need(name, t, dtype, shape, index)
     if cand_norm:  # otherwise unused (the reference passes the cell norm's gain in its place)
-        _need("cand_w", cand_w, f32, (d,), dev)
+        _need("cand_w", cand_w, f32, (d,), index)
     h_new = torch.empty_like(h)
     q_new = torch.empty_like(q)
     age_new = torch.empty_like(age)
     h_sel = h.new_empty((B, K, d))
-    args = dict(u=ptr(u), eps=ptr(eps), h=ptr(h), q=ptr(q), age=ptr(age), cells=ptr(cells),
-                units=ptr(units), valid=ptr(valid), alpha=ptr(alpha), V=ptr(V),
-                edge_w=ptr(edge_w) if D else None, pad_src=ptr(pad_src) if D else None,
-                norm_w=ptr(norm_w), gate_w=ptr(gate_w), gate_b=ptr(gate_b), W1=ptr(W1),
-                b1=ptr(b1), W2=ptr(W2), b2=ptr(b2), W_out=ptr(W_out),
-                cand_w=ptr(cand_w) if cand_norm else None,
-                h_new=ptr(h_new), q_new=ptr(q_new), age_new=ptr(age_new), h_sel=ptr(h_sel))
-    s = _round_struct(B, N, d, K, M, H, D, cand_norm, norm_eps, cand_eps, **args)
-    nbytes = ctypes.c_int64(0)
-    call("hsn_win_cell_round_workspace", ctypes.byref(s), ctypes.byref(nbytes))
-    work = torch.empty(int(nbytes.value), dtype=torch.uint8, device=dev)
-    s.work = ptr(work)
+    key = (B, K, d, H)
+    nbytes = _round_work.get(key)
+    if nbytes is None:
+        probe = _round_struct(B, N, d, K, M, H, D, cand_norm, norm_eps, cand_eps)
+        out = ctypes.c_int64(0)
+        call("hsn_win_cell_round_workspace", ctypes.byref(probe), ctypes.byref(out))
+        nbytes = _round_work[key] = int(out.value)
+    work = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    s = _Round(B, N, d, K, M, H, D, int(bool(cand_norm)), float(norm_eps), float(cand_eps),
+               u.data_ptr(), eps.data_ptr(), h.data_ptr(), q.data_ptr(), age.data_ptr(),
+               cells.data_ptr(), units.data_ptr(), valid.data_ptr(), alpha.data_ptr(),
+               V.data_ptr(), edge_w.data_ptr() if D else None, pad_src.data_ptr() if D else None,
+               norm_w.data_ptr(), gate_w.data_ptr(), gate_b.data_ptr(), W1.data_ptr(),
+               b1.data_ptr(), W2.data_ptr(), b2.data_ptr(), W_out.data_ptr(),
+               cand_w.data_ptr() if cand_norm else None, work.data_ptr(), h_new.data_ptr(),
+               q_new.data_ptr(), age_new.data_ptr(), h_sel.data_ptr())
     call("hsn_win_cell_round", ctypes.byref(s), stream_of(dev))
     return h_new, q_new, age_new, h_sel
 

@@ -83,6 +83,7 @@ CASES = {
     "one_unit_many_slots": dict(B=64, N=64, d=32, K=16, M=1, H=96, D=4, seed=15),
     "max_slots": dict(B=128, N=96, d=16, K=64, M=4, H=64, D=2, seed=16, pad=0.1),  # B K = 8192
     "wide_row_slots": dict(B=2, N=80, d=128, K=64, M=2, H=64, D=3, seed=17),  # >64 KiB in back
+    "smallest": dict(B=3, N=9, d=4, K=2, M=2, H=5, D=1, seed=18),  # one step a lane group
 }
 
 
