@@ -8,10 +8,12 @@
 //          need: no separate routing launch) times the chunks of 64 hidden units. A workgroup
 //          finds its unit and slots, puts the unit's first-layer weights in flight, and meanwhile
 //          builds its slots' inputs itself: each slot's weighted source sum, m = V (sum), the 4d
-//          input [u; eps; h_i; m] and the cell norm (the chunk-0 workgroup also the gate's product
-//          and sigmoid). Then hidden = v W1_j + b1_j (the four wavefronts split the reduction and
-//          sum their shares in a fixed order), the GELU, and the chunk's share of F = act W2_j,
-//          stored per chunk and summed in chunk order by the next launch (no atomics).
+//          input [u; eps; h_i; m] and the cell norm. Then hidden = v W1_j + b1_j (the four
+//          wavefronts split the reduction and sum their shares in a fixed order), the GELU, and
+//          the chunk's share of F = act W2_j, stored per chunk and summed in chunk order by the
+//          next launch (no atomics). The gate's 16-column tiles go to the chunks (tile c to the
+//          chunk-c workgroup, its wavefronts splitting the reduction; chunk 0 takes every tile
+//          when there are fewer chunks than tiles).
 //   back   (row, part) workgroups: part 0 finishes F (+ b2_j), W_out, the candidate norm, tanh and
 //          the gated update of the row's slots, then q and h_sel; parts 1.. copy the row's other
 //          cells, 64 a workgroup, and tick the ages. Written cells and copied cells are disjoint,
