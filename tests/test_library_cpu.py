@@ -32,7 +32,9 @@ def test_headers_declare_the_hot_path_entry_points():
                      "hsn_win_abi_version", "hsn_win_last_error", "hsn_tr_adamw",
                      "hsn_tr_adamw_units", "hsn_tr_lerp", "hsn_tr_scale64", "hsn_tr_copy",
                      "hsn_tr_limit_squares", "hsn_tr_limit_project", "hsn_win_back_check",
-                     "hsn_win_back_head", "hsn_win_back_mid", "hsn_win_back_tail"):
+                     "hsn_win_back_head", "hsn_win_back_mid", "hsn_win_back_tail",
+                     "hsn_win_back_cell", "hsn_win_back_cell_tail", "hsn_win_cell_round",
+                     "hsn_win_cell_round_check", "hsn_win_cell_round_workspace"):
         assert expected in names
 
 
