@@ -66,6 +66,10 @@ def _args():
     p.add_argument("--round", choices=["ref", "tiny"], default=None,
                    help="measure the fused cell round (hsn::window_cell_round) over a window of "
                         "positions at this workload instead of the window (not the headline line)")
+    p.add_argument("--ops", choices=["ref", "model"], default=None,
+                   help="measure the P2.9 ops (include/hsn_ops.h) one call at a time at the "
+                        "golden vectors' ref size or the reference model's per-position size "
+                        "(not the headline line)")
     p.add_argument("--round-positions", type=int, default=64,
                    help="positions a --round step runs (the state carried from one to the next)")
     p.add_argument("--trainer", choices=sorted(TRAINER_LISTS), default=None,
@@ -417,6 +421,132 @@ def _sweep_main(args) -> int:
     return 0
 
 
+#: Sizes of ``--ops``: the golden vectors' "ref" dimensions (tests/golden MANIFEST) and the
+#: reference model's per-position round (B 32 rows, K 8 slots of N 256 cells, d 64, H 512, M 8,
+#: 8 in-edges a cell).
+OPS_SIZES = {
+    "ref": dict(B=4, K=4, N=32, d=64, E=128, P=16, M=8, H=512),
+    "model": dict(B=32, K=8, N=256, d=64, E=2048, P=256, M=8, H=512),
+}
+
+
+def _ops_main(args) -> int:
+    """The P2.9 ops (``include/hsn_ops.h``), forward and backward, one call at a time: device
+    time per call from HIP events around ``--steps`` calls queued behind device copies (so host
+    dispatch is not counted), synthetic fp32 inputs of the size's shapes. ``value`` is the
+    grouped unit MLP's forward calls/s; its roofline is against the fp32 MFMA peak (useful
+    FLOPs: 2 P (4d H + H d)). The reference's own comparison is per op against its PyTorch path
+    (``scripts/bench_kernels.py``); here the CPU oracle of the unit MLP stands beside it."""
+    import torch
+
+    from hsn_amd.kernels import ops
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda", 0)
+    z = OPS_SIZES[args.ops]
+    B, K, N, d, E, P, M, H = (z[k] for k in ("B", "K", "N", "d", "E", "P", "M", "H"))
+    g = torch.Generator().manual_seed(args.seed)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(dev)
+
+    idx = torch.stack([torch.randperm(N, generator=g)[:K] for _ in range(B)]).to(dev)
+    valid = torch.ones(B, K, dtype=torch.int32, device=dev)
+    h, q = rnd(B, N, d, scale=0.5), rnd(B, d)
+    age = torch.zeros(B, N, dtype=torch.int32, device=dev)
+    c, b = rnd(B, K, d).tanh(), torch.sigmoid(rnd(B, K, d))
+    u, eps, m = rnd(B, d), rnd(B, d), rnd(B, K, d)
+    unit = torch.randint(0, M, (P,), generator=g).to(dev)
+    v = rnd(P, 4 * d)
+    w1, b1 = rnd(M, 4 * d, H, scale=(4 * d) ** -0.5), rnd(M, H, scale=0.1)
+    w2, b2 = rnd(M, H, d, scale=H ** -0.5), rnd(M, d, scale=0.1)
+    deg = torch.full((N,), E // N, dtype=torch.int64)
+    indptr = torch.cat([torch.zeros(1, dtype=torch.int64), deg.cumsum(0)]).to(dev)
+    indices = torch.randint(0, N, (E,), generator=g).to(dev)
+    a = torch.rand(E, generator=g).to(dev)
+    V = rnd(d, d, scale=d ** -0.5)
+    out, hidden = ops.grouped_unit_mlp(v, unit, w1, b1, w2, b2)
+    calls = {
+        "gated_delta_update_functional": lambda: ops.gated_delta_update_functional(
+            h, q, age.long(), idx, valid, c, b),
+        "gated_delta_update_backward": lambda: ops.gated_delta_update_backward(
+            idx, valid, c, b, c, h, q),
+        "gather_concat": lambda: ops.gather_concat(u, eps, h, m, idx),
+        "gather_concat_backward": lambda: ops.gather_concat_backward(
+            rnd_dv, idx, N),
+        "grouped_unit_mlp": lambda: ops.grouped_unit_mlp(v, unit, w1, b1, w2, b2),
+        "grouped_unit_mlp_backward": lambda: ops.grouped_unit_mlp_backward(
+            v, unit, w1, w2, hidden, out),
+        "csr_messages": lambda: ops.csr_messages(h, indptr, indices, a, V, idx),
+        "csr_messages_backward": lambda: ops.csr_messages_backward(
+            h, indptr, indices, a, V, idx, m),
+    }
+    rnd_dv = rnd(B, K, 4 * d)
+    busy = torch.empty(64 << 20, device=dev)
+    busy_dst = torch.empty_like(busy)
+    per_call = {}
+    with torch.no_grad():
+        for name, fn in calls.items():
+            for _ in range(max(1, args.warmup)):
+                fn()
+            torch.cuda.synchronize()
+            for _ in range(args.steps // 8 + 8):
+                busy_dst.copy_(busy)
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            ev[0].record()
+            for _ in range(args.steps):
+                fn()
+            ev[1].record()
+            torch.cuda.synchronize()
+            per_call[name] = ev[0].elapsed_time(ev[1]) / args.steps * 1e3  # us
+    del busy, busy_dst
+    mlp_us = per_call["grouped_unit_mlp"]
+    flops = 2.0 * P * (4 * d * H + H * d)
+    achieved = flops / (mlp_us * 1e-6) / 1e12
+    result = {
+        "metric": f"grouped unit MLP forward calls/sec ({args.ops} size, 1 GPU)",
+        "value": 1e6 / mlp_us,
+        "unit": "calls/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": mlp_us * 1e-3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded, bench.py OPS_SIZES shapes)",
+        "config": {"workload": f"ops_{args.ops}", **z,
+                   "timing": "HIP events around the calls, queued behind device copies",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": "grouped_unit_mlp forward",
+                     "achieved": achieved, "peak": 157.3, "unit": "TFLOP/s",
+                     "frac": achieved / 157.3, "traffic": None, "flops_per_call": flops},
+        "us_per_call": per_call,
+    }
+    if not args.no_cpu:  # the oracle's unit MLP on the same size, one thread
+        from oracle import hsn_oracle as O
+
+        torch.set_num_threads(1)
+        cpu = [t.cpu() for t in (v, unit, w1, b1, w2, b2)]
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            O.grouped_unit_mlp(*cpu)
+            reps += 1
+            secs = time.perf_counter() - t0
+            if secs >= args.cpu_seconds:
+                break
+        result["cpu_baseline"] = {
+            "value": reps / secs, "unit": "calls/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} calls of the repository's PyTorch-CPU oracle grouped_unit_mlp at "
+                      f"the same size ({secs:.1f} s)",
+        }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def _round_main(args) -> int:
     """The fused cell round over a window of T synthetic positions (the state carried from one
     position to the next, as the forward sweep runs it): a step is the T positions' rounds, inputs
@@ -559,6 +689,8 @@ def main() -> int:
         return _sweep_main(args)
     if args.round:
         return _round_main(args)
+    if args.ops:
+        return _ops_main(args)
     import torch
 
     from hsn_amd import window

@@ -22,6 +22,9 @@
 #include "abi_util.h"
 
 namespace hsn {
+// Raise a kernel's dynamic-LDS limit to 160 KiB once per (kernel, device) (runtime.cpp).
+hipError_t allow_lds_raw(const void* kernel, size_t lds);
+
 namespace units {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -190,6 +193,259 @@ __global__ __launch_bounds__(256) void mlp_fwd(const T* v, const int32_t* unit_i
                 for (int r = 0; r < 4; ++r)
                     if (prow[r] >= 0) store_f32(out, int64_t(prow[r]) * d + oc, oacc[t][r] + bias);
             }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// grouped_unit_mlp forward by row tiles (d a multiple of 4, P <= 16384, M <= 4096)
+// ------------------------------------------------------------------------------------------
+
+// The row tiles of every unit's pairs (16 pairs of one unit in pair order, laid end to end unit
+// after unit; a workgroup finds its tile from LDS counts of each unit's pairs), one workgroup each,
+// all H hidden columns walked in tiles of 64. The first layer's reduction over the 4d inputs is
+// split over the four wavefronts (each lane group g a contiguous quarter of a wavefront's share);
+// a lane's 16-byte load of W1[j][k][h0 + 4 lr ..] feeds four interleaved column tiles (tile t's
+// column lr is h0 + 4 lr + t), and the next 16 steps' weights are in flight while a block's
+// products run, across the hidden tiles too. The shares are summed in wavefront order, z1 stored
+// (rounded once), gelu(z1) kept in fp32 in LDS, and out += gelu(z1) W2[j][tile] accumulated in
+// registers over the tiles, a 16-column output tile a wavefront.
+constexpr int kTileMaxSlots = 16384;
+constexpr int kTileMaxUnits = 4096;
+constexpr int kTileBlock = 8;  // reduction steps whose weights are loaded together
+
+struct TileLds {
+    int ucache, count, rows, meta, vs, red, act, b1, sv, bytes;
+};
+__host__ __device__ inline TileLds tile_lds(int P, int M, int d, int H) {
+    TileLds L;
+    L.sv = 4 * d + 1;
+    L.ucache = 0;                                         // uint16 [P]: each pair's unit
+    L.count = (2 * P + 15) / 16 * 16;                     // int [M]
+    L.rows = L.count + (4 * M + 15) / 16 * 16;            // int [16]
+    L.meta = L.rows + 64;                                 // int [4]
+    L.vs = L.meta + 16;                                   // float [16][sv]
+    L.red = L.vs + 4 * 16 * L.sv;                         // float [4][16][65]
+    L.act = L.red + 4 * 4 * 16 * 65;                      // float [16][65]
+    L.b1 = L.act + 4 * 16 * 65;                           // float [H]: the unit's first-layer bias
+    L.bytes = L.b1 + 4 * H;
+    return L;
+}
+
+// Four consecutive values of a row from column c on, widened; 0 past `cols`.
+template <typename T>
+__device__ __forceinline__ float4 row4w(const T* w, int c, int cols, bool aligned) {
+    if (aligned && c + 4 <= cols) {
+        if constexpr (sizeof(T) == 4) {
+            return *reinterpret_cast<const float4*>(w + c);
+        } else {
+            const uint2 raw = *reinterpret_cast<const uint2*>(w + c);
+            T e[4];
+            __builtin_memcpy(e, &raw, 8);
+            return make_float4(to_f32(e[0]), to_f32(e[1]), to_f32(e[2]), to_f32(e[3]));
+        }
+    }
+    return make_float4(c < cols ? to_f32(w[c]) : 0.0f, c + 1 < cols ? to_f32(w[c + 1]) : 0.0f,
+                       c + 2 < cols ? to_f32(w[c + 2]) : 0.0f,
+                       c + 3 < cols ? to_f32(w[c + 3]) : 0.0f);
+}
+
+template <typename T, bool ALIGNED>  // ALIGNED: H % 4 == 0, rows of W1 in 16-byte pieces
+__global__ __launch_bounds__(256) void mlp_fwd_tiles(const T* v, const int32_t* unit_idx,
+                                                     const T* W1, const T* b1, const T* W2,
+                                                     const T* b2, T* hidden, T* out, int P, int M,
+                                                     int d, int H) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const TileLds L = tile_lds(P, M, d, H);
+    uint16_t* ucache = reinterpret_cast<uint16_t*>(lds + L.ucache);
+    int* count = reinterpret_cast<int*>(lds + L.count);
+    int* rows = reinterpret_cast<int*>(lds + L.rows);
+    int* meta = reinterpret_cast<int*>(lds + L.meta);
+    float* vs = reinterpret_cast<float*>(lds + L.vs);
+    float* red = reinterpret_cast<float*>(lds + L.red);
+    float* act = reinterpret_cast<float*>(lds + L.act);
+    float* b1c = reinterpret_cast<float*>(lds + L.b1);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, g = lane >> 4;
+    const int n = 4 * d;
+
+    // ---- which unit's which row tile ----
+    for (int j = tid; j < M; j += 256) count[j] = 0;
+    for (int q = tid; q < P; q += 256) {
+        const int u = unit_idx[q];
+        ucache[q] = u >= 0 && u < M ? static_cast<uint16_t>(u) : uint16_t(0xffff);
+    }
+    __syncthreads();
+    for (int q = tid; q < P; q += 256)  // integer counts: any order gives the same
+        if (ucache[q] != 0xffff) atomicAdd(&count[ucache[q]], 1);
+    __syncthreads();
+    if (wave == 0) {
+        int unit = -1, tile = 0;
+        if (lane == 0) {
+            int before = 0;
+            for (int j = 0; j < M; ++j) {
+                const int t = (count[j] + 15) / 16;
+                if (static_cast<int>(blockIdx.x) < before + t) {
+                    unit = j;
+                    tile = blockIdx.x - before;
+                    break;
+                }
+                before += t;
+            }
+        }
+        unit = __builtin_amdgcn_readfirstlane(unit);
+        tile = __builtin_amdgcn_readfirstlane(tile);
+        if (lane < 16) rows[lane] = -1;
+        if (unit >= 0) {
+            const int first = tile * 16;
+            int base = 0;
+            for (int q0 = 0; q0 < P && base < first + 16; q0 += kWave) {
+                const int q = q0 + lane;
+                const bool mine = q < P && ucache[q] == unit;
+                const uint64_t m = ballot(mine);
+                const int rank = base + lanes_below(m);
+                if (mine && rank >= first && rank < first + 16) rows[rank - first] = q;
+                base += __popcll(m);
+            }
+        }
+        if (lane == 0) meta[0] = unit;
+    }
+    __syncthreads();
+    const int j = meta[0];
+    if (j < 0) return;  // past the last tile (uniform)
+
+    // ---- the tile's inputs, widened into LDS ----
+    {
+        const int n4 = n / 4;
+        const bool valign = (reinterpret_cast<uintptr_t>(v) & (4 * sizeof(T) - 1)) == 0;
+#pragma unroll 4
+        for (int e = tid; e < 16 * n4; e += 256) {
+            const int pp = e / n4, c = 4 * (e % n4);
+            const int q = rows[pp];
+            const float4 t = q >= 0 ? row4w(v + int64_t(q) * n, c, n, valign)
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float* dst = vs + pp * L.sv + c;
+            dst[0] = t.x, dst[1] = t.y, dst[2] = t.z, dst[3] = t.w;
+        }
+    }
+
+    const int q1 = n / 16;                       // a lane group's steps of its wavefront's share
+    const int k1 = wave * (n / 4) + g * q1;      // their first input row
+    constexpr bool al = ALIGNED;
+    const T* W1j = W1 + int64_t(j) * n * H;
+    const T* W2j = W2 + int64_t(j) * H * d;
+    const int tiles_h = (H + 63) / 64;
+    const int blocks = (q1 + kTileBlock - 1) / kTileBlock;  // per hidden tile
+    const int tiles_d = (d + 15) / 16;
+    v4f oacc[4];  // output column tiles wave, wave + 4, ... (d <= 256)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) oacc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto load_block = [&](float4 (&b)[kTileBlock], int ht, int bi) {
+        const int c = ht * 64 + 4 * lr;
+#pragma unroll
+        for (int i = 0; i < kTileBlock; ++i) {
+            const int s = bi * kTileBlock + i;
+            b[i] = s < q1 ? row4w(W1j + int64_t(k1 + s) * H, c, H, al)
+                          : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    // The first layer's weights stream as one sequence of blocks (`blocks` a hidden tile, tile
+    // after tile); block i + 1 is loaded while block i's products run, into the other of two
+    // buffers (no copy, so no wait on loads in flight), and a tile's last block is followed by
+    // its tail: the shares' sum, z1, the GELU and the second layer.
+    float4 bufA[kTileBlock], bufB[kTileBlock];
+    load_block(bufA, 0, 0);
+    for (int c = tid; c < H; c += 256) b1c[c] = load_f32(b1, int64_t(j) * H + c);
+    __syncthreads();  // the inputs and the bias are in LDS
+
+    v4f acc[4];
+    const float* arow = vs + lr * L.sv + k1;
+    const int total = tiles_h * blocks;
+    auto load_w2 = [&](float (&w)[16], int h0, int t) {
+        const int col = (wave + 4 * t) * 16 + lr;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int h = h0 + g * 16 + s;
+            w[s] = wave + 4 * t < tiles_d && col < d && h < H
+                       ? load_f32(W2j, int64_t(h) * d + col) : 0.0f;
+        }
+    };
+    auto step = [&](int i, float4 (&cur)[kTileBlock], float4 (&nxt)[kTileBlock]) {
+        const int ht = i / blocks, bi = i % blocks;
+        if (bi == 0) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        if (i + 1 < total) load_block(nxt, (i + 1) / blocks, (i + 1) % blocks);
+        float av[kTileBlock];
+#pragma unroll
+        for (int k = 0; k < kTileBlock; ++k) {
+            const int s = bi * kTileBlock + k;
+            av[k] = s < q1 ? arow[s] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < kTileBlock; ++k) {
+            acc[0] = mfma(av[k], cur[k].x, acc[0]);
+            acc[1] = mfma(av[k], cur[k].y, acc[1]);
+            acc[2] = mfma(av[k], cur[k].z, acc[2]);
+            acc[3] = mfma(av[k], cur[k].w, acc[3]);
+        }
+        if (bi + 1 < blocks) return;
+        // the tile's tail; its second-layer weights (the wavefront's first output tile; d <= 64:
+        // all of them) are in flight during the shares' sum
+        const int h0 = ht * 64;
+        float w2v[16];
+        load_w2(w2v, h0, 0);
+        // the wavefront's share: row 4 g + r, column 4 lr + t of the tile
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[((wave * 16) + 4 * g + r) * 65 + 4 * lr + t] = acc[t][r];
+        __syncthreads();
+        for (int e = tid; e < 16 * 64; e += 256) {  // the shares in wavefront order
+            const int row = e >> 6, c = e & 63;
+            float z = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) z += red[(w * 16 + row) * 65 + c];
+            const int q = rows[row];
+            if (h0 + c < H) z += b1c[h0 + c];
+            const bool ok = q >= 0 && h0 + c < H;
+            if (ok) store_f32(hidden, int64_t(q) * H + h0 + c, z);
+            act[row * 65 + c] = ok ? gelu(z) : 0.0f;
+        }
+        __syncthreads();
+        // out += gelu(z1) W2[j][h0 .. h0 + 63]: output tile wave + 4 t, B[k][col] = W2[j][h0 + k][col]
+        {
+            const float* ar = act + lr * 65 + g * 16;
+            float a2[16];
+#pragma unroll
+            for (int s = 0; s < 16; ++s) a2[s] = ar[s];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (wave + 4 * t < tiles_d) {  // uniform in the wavefront
+                    if (t > 0) load_w2(w2v, h0, t);
+#pragma unroll
+                    for (int s = 0; s < 16; ++s) oacc[t] = mfma(a2[s], w2v[s], oacc[t]);
+                }
+            }
+        }
+        __syncthreads();  // red and act are rewritten by the next tile
+    };
+    for (int i = 0; i < total; i += 2) {
+        step(i, bufA, bufB);
+        if (i + 1 < total) step(i + 1, bufB, bufA);
+    }
+    int prow[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) prow[r] = rows[4 * g + r];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int col = (wave + 4 * t) * 16 + lr;
+        if (wave + 4 * t < tiles_d && col < d) {
+            const float bias = load_f32(b2, int64_t(j) * d + col);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (prow[r] >= 0) store_f32(out, int64_t(prow[r]) * d + col, oacc[t][r] + bias);
         }
     }
 }
@@ -567,6 +823,22 @@ struct RunMlp {
     static void run(const void* v, const int32_t* idx, const void* W1, const void* b1,
                     const void* W2, const void* b2, void* hidden, void* out, int P, int M, int d,
                     int H, hipStream_t st) {
+        if (d % 4 == 0 && P <= units::kTileMaxSlots && M <= units::kTileMaxUnits &&
+            units::tile_lds(P, M, d, H).bytes <= 160 * 1024) {
+            const int lds = units::tile_lds(P, M, d, H).bytes;
+            auto launch = [&](auto kernel) {
+                if (lds > 64 * 1024)
+                    HSN_HIP(allow_lds_raw(reinterpret_cast<const void*>(kernel), lds));
+                hipLaunchKernelGGL(kernel, dim3((P + 15) / 16 + M), dim3(256), lds, st,
+                                   static_cast<const T*>(v), idx, static_cast<const T*>(W1),
+                                   static_cast<const T*>(b1), static_cast<const T*>(W2),
+                                   static_cast<const T*>(b2), static_cast<T*>(hidden),
+                                   static_cast<T*>(out), P, M, d, H);
+            };
+            if (H % 4 == 0) launch(&units::mlp_fwd_tiles<T, true>);
+            else launch(&units::mlp_fwd_tiles<T, false>);
+            return;
+        }
         const int S = std::min((P + 15) / 16, 64);  // chunk slots per unit
         hipLaunchKernelGGL((units::mlp_fwd<T>), dim3(M, S), dim3(256), 0, st,
                            static_cast<const T*>(v), idx, static_cast<const T*>(W1),
