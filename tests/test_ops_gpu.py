@@ -225,3 +225,29 @@ def test_unit_mlp_and_messages_are_reproducible(ops, cuda_device):
     args = (D["h"], D["indptr"], D["indices"], D["a"], D["V"], D["cell_idx"], D["grad_m"])
     first, second = ops.csr_messages_backward(*args), ops.csr_messages_backward(*args)
     assert all(torch.equal(x, y) for x, y in zip(first, second))
+
+
+@pytest.mark.parametrize("P,M,d,H", [
+    (40, 3, 6, 50),      # d not a multiple of 4: the scanning kernel
+    (64, 4, 16, 77),     # H not a multiple of 4: the row-tile kernel's unaligned loads
+    (20000, 2, 4, 8),    # more pairs than the row-tile kernel's slot table: the scanning kernel
+    (300, 6, 64, 512),   # the reference model's widths, several tiles a unit
+])
+def test_unit_mlp_forward_paths_match_oracle(ops, cuda_device, P, M, d, H):
+    """Both forward kernels (by row tiles, and the pair-scanning one for shapes the first does not
+    take) against the oracle in float64 on fp32 inputs."""
+    from oracle import hsn_oracle as O
+
+    g = torch.Generator().manual_seed(P + d)
+    rnd = lambda *s, scale=1.0: torch.randn(*s, generator=g) * scale  # noqa: E731
+    v, b1, b2 = rnd(P, 4 * d), rnd(M, H, scale=0.1), rnd(M, d, scale=0.1)
+    W1, W2 = rnd(M, 4 * d, H, scale=(4 * d) ** -0.5), rnd(M, H, d, scale=H ** -0.5)
+    idx = torch.randint(0, M, (P,), generator=g, dtype=torch.int32)
+    want_out, want_h = O.grouped_unit_mlp(v.double(), idx, W1.double(), b1.double(), W2.double(),
+                                          b2.double())
+    dev = cuda_device
+    out, hidden = ops.grouped_unit_mlp(v.to(dev), idx.to(dev), W1.to(dev), b1.to(dev),
+                                       W2.to(dev), b2.to(dev))
+    for name, got, want in (("hidden", hidden, want_h), ("out", out, want_out)):
+        err = (got.double().cpu() - want).abs() / want.abs().clamp(min=1.0)
+        assert float(err.max()) <= 1e-5, f"{name}: worst {float(err.max()):.3e} (bar 1e-5)"
