@@ -596,6 +596,190 @@ __global__ __launch_bounds__(256) void mlp_dv(const int32_t* unit_idx, const T* 
     }
 }
 
+// grad_v by row tiles (the forward's conditions): (row tile, 64-input group) workgroups. Per
+// hidden tile of 64: dz1 = (grad_out W2[j]^T) * gelu'(z1) for the tile's 16 pairs (a 16-column
+// hidden tile a wavefront, reduction over d), then grad_v[:, i0 .. i0 + 63] += dz1 W1[j]^T (a
+// 16-column input tile a wavefront, reduction over the 64 hidden units). Both weight fragments
+// are read along a lane's own row (16-byte loads), and the next hidden tile's fragments and z1
+// values are in flight during the current tile.
+struct DvLds {
+    int ucache, count, rows, meta, go, dz, z, sg, bytes;
+};
+__host__ __device__ inline DvLds dv_lds(int P, int M, int d) {
+    DvLds L;
+    L.sg = d + 1;
+    L.ucache = 0;                                 // uint16 [P]
+    L.count = (2 * P + 15) / 16 * 16;             // int [M]
+    L.rows = L.count + (4 * M + 15) / 16 * 16;    // int [16]
+    L.meta = L.rows + 64;                         // int [4]
+    L.go = L.meta + 16;                           // float [16][sg]: the rows' grad_out
+    L.dz = L.go + 4 * 16 * L.sg;                  // float [16][65]: dz1 of a hidden tile
+    L.z = L.dz + 4 * 16 * 65;                     // float [16][65]: gelu'(z1) of a hidden tile
+    L.bytes = L.z + 4 * 16 * 65;
+    return L;
+}
+
+template <typename T, bool ALIGNED>  // ALIGNED: rows of W1 and W2 in 16-byte pieces
+__global__ __launch_bounds__(256) void mlp_dv_tiles(const int32_t* unit_idx, const T* W1,
+                                                    const T* W2, const T* hidden,
+                                                    const T* grad_out, T* grad_v, int P, int M,
+                                                    int d, int H) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const DvLds L = dv_lds(P, M, d);
+    uint16_t* ucache = reinterpret_cast<uint16_t*>(lds + L.ucache);
+    int* count = reinterpret_cast<int*>(lds + L.count);
+    int* rows = reinterpret_cast<int*>(lds + L.rows);
+    int* meta = reinterpret_cast<int*>(lds + L.meta);
+    float* go = reinterpret_cast<float*>(lds + L.go);
+    float* dz = reinterpret_cast<float*>(lds + L.dz);
+    float* zg = reinterpret_cast<float*>(lds + L.z);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, g = lane >> 4;
+    const int n = 4 * d;
+
+    for (int j = tid; j < M; j += 256) count[j] = 0;
+    for (int q = tid; q < P; q += 256) {
+        const int u = unit_idx[q];
+        ucache[q] = u >= 0 && u < M ? static_cast<uint16_t>(u) : uint16_t(0xffff);
+    }
+    __syncthreads();
+    for (int q = tid; q < P; q += 256)  // integer counts: any order gives the same
+        if (ucache[q] != 0xffff) atomicAdd(&count[ucache[q]], 1);
+    __syncthreads();
+    if (wave == 0) {
+        int unit = -1, tile = 0;
+        if (lane == 0) {
+            int before = 0;
+            for (int j = 0; j < M; ++j) {
+                const int t = (count[j] + 15) / 16;
+                if (static_cast<int>(blockIdx.x) < before + t) {
+                    unit = j;
+                    tile = blockIdx.x - before;
+                    break;
+                }
+                before += t;
+            }
+        }
+        unit = __builtin_amdgcn_readfirstlane(unit);
+        tile = __builtin_amdgcn_readfirstlane(tile);
+        if (lane < 16) rows[lane] = -1;
+        if (unit >= 0) {
+            const int first = tile * 16;
+            int base = 0;
+            for (int q0 = 0; q0 < P && base < first + 16; q0 += kWave) {
+                const int q = q0 + lane;
+                const bool mine = q < P && ucache[q] == unit;
+                const uint64_t m = ballot(mine);
+                const int rank = base + lanes_below(m);
+                if (mine && rank >= first && rank < first + 16) rows[rank - first] = q;
+                base += __popcll(m);
+            }
+        }
+        if (lane == 0) meta[0] = unit;
+    }
+    __syncthreads();
+    const int j = meta[0];
+    if (j < 0) return;  // past the last tile (uniform)
+
+    const int i0 = blockIdx.y * 64;
+    const T* W1j = W1 + int64_t(j) * n * H;
+    const T* W2j = W2 + int64_t(j) * H * d;
+    const int tiles_h = (H + 63) / 64;
+    const int qd = d / 4;  // dz's reduction steps a lane group (d a multiple of 4)
+    // the rows' grad_out, widened into LDS
+    for (int e = tid; e < 16 * qd; e += 256) {
+        const int pp = e / qd, c = 4 * (e % qd);
+        const int q = rows[pp];
+        const float4 t = q >= 0 ? row4w(grad_out + int64_t(q) * d, c, d, ALIGNED)
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float* dst = go + pp * L.sg + c;
+        dst[0] = t.x, dst[1] = t.y, dst[2] = t.z, dst[3] = t.w;
+    }
+    // a hidden tile's fragments: W2[j][h][g qd ..] for this lane's hidden column h (dz), W1[j][i]
+    // [h0 + 16 g ..] for its input column i (grad_v), and z1 of 4 (row, h) pairs a thread
+    constexpr int kQd = 16;  // dz steps held in registers (d <= 64); beyond, read as they go
+    const int hcol = wave * 16 + lr;  // the wavefront's hidden column in the tile
+    const int icol = i0 + wave * 16 + lr;
+    const bool iin = icol < n;
+    struct Frag {
+        float w2[kQd];
+        float4 w1[4];
+        float z[4];
+    };
+    auto load_frag = [&](Frag& f, int ht) {
+        const int h = ht * 64 + hcol;
+        const bool hin = h < H;
+        const T* w2r = W2j + int64_t(hin ? h : 0) * d + g * qd;
+#pragma unroll
+        for (int s = 0; s < kQd; s += 4) {
+            const float4 t = hin && s < qd ? row4w(w2r, s, qd, ALIGNED)
+                                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            f.w2[s] = t.x, f.w2[s + 1] = t.y, f.w2[s + 2] = t.z, f.w2[s + 3] = t.w;
+        }
+        const T* w1r = W1j + int64_t(iin ? icol : 0) * H + ht * 64 + g * 16;
+        const int left = H - (ht * 64 + g * 16);  // this lane group's hidden units in range
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            f.w1[s] = iin ? row4w(w1r, 4 * s, left, ALIGNED) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = tid + 256 * u, row = e >> 6, c = e & 63;
+            const int q = rows[row];
+            f.z[u] = q >= 0 && ht * 64 + c < H ? load_f32(hidden, int64_t(q) * H + ht * 64 + c)
+                                               : 0.0f;
+        }
+    };
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};  // grad_v rows 4 g + r, input column icol
+    Frag fa, fb;
+    load_frag(fa, 0);
+    __syncthreads();  // grad_out is in LDS
+    auto tile = [&](int ht, Frag& cur, Frag& nxt) {
+        if (ht + 1 < tiles_h) load_frag(nxt, ht + 1);
+        // gelu'(z1) of the tile into LDS
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = tid + 256 * u, row = e >> 6, c = e & 63;
+            zg[row * 65 + c] = gelu_grad(cur.z[u]);
+        }
+        // grad_out W2[j]^T for hidden column hcol: A = grad_out rows, B[k][h] = W2[j][h][k]
+        v4f t = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float* ar = go + lr * L.sg + g * qd;
+#pragma unroll
+        for (int s = 0; s < kQd; ++s)
+            if (s < qd) t = mfma(ar[s], cur.w2[s], t);
+        for (int s = kQd; s < qd; ++s) {  // d > 64
+            const int h = ht * 64 + hcol;
+            const float w = h < H ? load_f32(W2j, int64_t(h) * d + g * qd + s) : 0.0f;
+            t = mfma(ar[s], w, t);
+        }
+        __syncthreads();  // gelu' in LDS
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 4 * g + r;
+            dz[row * 65 + hcol] = t[r] * zg[row * 65 + hcol];
+        }
+        __syncthreads();
+        // grad_v += dz1 W1[j]^T: A = dz rows (k = h), B[k][i] = W1[j][i][h0 + k]
+        const float* dr = dz + lr * 65 + g * 16;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            acc = mfma(dr[4 * s], cur.w1[s].x, acc);
+            acc = mfma(dr[4 * s + 1], cur.w1[s].y, acc);
+            acc = mfma(dr[4 * s + 2], cur.w1[s].z, acc);
+            acc = mfma(dr[4 * s + 3], cur.w1[s].w, acc);
+        }
+        __syncthreads();  // dz and zg are rewritten by the next tile
+    };
+    for (int ht = 0; ht < tiles_h; ht += 2) {
+        tile(ht, fa, fb);
+        if (ht + 1 < tiles_h) tile(ht + 1, fb, fa);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int q = rows[4 * g + r];
+        if (q >= 0 && iin) store_f32(grad_v, int64_t(q) * n + icol, acc[r]);
+    }
+}
+
 // ------------------------------------------------------------------------------------------
 // csr_messages
 // ------------------------------------------------------------------------------------------
@@ -859,6 +1043,21 @@ struct RunMlpBwd {
                            static_cast<const T*>(dout), static_cast<T*>(dW1),
                            static_cast<T*>(db1), static_cast<T*>(dW2), static_cast<T*>(db2), P, d,
                            H);
+        if (d % 4 == 0 && P <= units::kTileMaxSlots && M <= units::kTileMaxUnits &&
+            units::dv_lds(P, M, d).bytes <= 160 * 1024) {
+            const int lds = units::dv_lds(P, M, d).bytes;
+            auto launch = [&](auto kernel) {
+                if (lds > 64 * 1024)
+                    HSN_HIP(allow_lds_raw(reinterpret_cast<const void*>(kernel), lds));
+                hipLaunchKernelGGL(kernel, dim3((P + 15) / 16 + M, (4 * d + 63) / 64), dim3(256),
+                                   lds, st, idx, static_cast<const T*>(W1),
+                                   static_cast<const T*>(W2), static_cast<const T*>(hidden),
+                                   static_cast<const T*>(dout), static_cast<T*>(dv), P, M, d, H);
+            };
+            if (H % 4 == 0 && d % 16 == 0) launch(&units::mlp_dv_tiles<T, true>);
+            else launch(&units::mlp_dv_tiles<T, false>);
+            return;
+        }
         hipLaunchKernelGGL((units::mlp_dv<T>), dim3((4 * d + 63) / 64, M), dim3(256), 0, st, idx,
                            static_cast<const T*>(W1), static_cast<const T*>(W2),
                            static_cast<const T*>(hidden), static_cast<const T*>(dout),

@@ -234,8 +234,8 @@ def test_unit_mlp_and_messages_are_reproducible(ops, cuda_device):
     (300, 6, 64, 512),   # the reference model's widths, several tiles a unit
 ])
 def test_unit_mlp_forward_paths_match_oracle(ops, cuda_device, P, M, d, H):
-    """Both forward kernels (by row tiles, and the pair-scanning one for shapes the first does not
-    take) against the oracle in float64 on fp32 inputs."""
+    """Both forward kernels and both grad_v kernels (by row tiles, and the pair-scanning ones for
+    shapes the first do not take) against the oracle in float64 on fp32 inputs."""
     from oracle import hsn_oracle as O
 
     g = torch.Generator().manual_seed(P + d)
@@ -248,6 +248,16 @@ def test_unit_mlp_forward_paths_match_oracle(ops, cuda_device, P, M, d, H):
     dev = cuda_device
     out, hidden = ops.grouped_unit_mlp(v.to(dev), idx.to(dev), W1.to(dev), b1.to(dev),
                                        W2.to(dev), b2.to(dev))
-    for name, got, want in (("hidden", hidden, want_h), ("out", out, want_out)):
+    dout = rnd(P, d)
+    grads = ops.grouped_unit_mlp_backward(v.to(dev), idx.to(dev), W1.to(dev), W2.to(dev), hidden,
+                                          dout.to(dev))
+    want_g = O.grouped_unit_mlp_bwd(v.double(), idx, W1.double(), W2.double(),
+                                    hidden.double().cpu(), dout.double())
+    pairs = [("hidden", hidden, want_h), ("out", out, want_out)]
+    pairs += list(zip(("dv", "dW1", "db1", "dW2", "db2"), grads, want_g))
+    for name, got, want in pairs:
+        # the weight gradients sum over a unit's pairs in fp32: the bar grows with the square
+        # root of their count (the random walk of the roundings; 10000 pairs at P = 20000)
+        bar = 1e-5 * (max(1.0, (P / M / 64) ** 0.5) if name[1] in "Wb" else 1.0)
         err = (got.double().cpu() - want).abs() / want.abs().clamp(min=1.0)
-        assert float(err.max()) <= 1e-5, f"{name}: worst {float(err.max()):.3e} (bar 1e-5)"
+        assert float(err.max()) <= bar, f"{name}: worst {float(err.max()):.3e} (bar {bar:.1e})"
