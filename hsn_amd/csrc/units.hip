@@ -851,41 +851,6 @@ __global__ __launch_bounds__(256) void csr_fwd(const T* h, const Csr g, const T*
     }
 }
 
-// (d / 64, d / 16) workgroups: grad_V[o][c] = sum_s grad_m[s][o] S[s][c] over every slot s, in
-// chunks of 16 slots (S for the workgroup's 64 columns in LDS).
-template <typename T>
-__global__ __launch_bounds__(256) void csr_dV(const T* h, const Csr g, const T* a,
-                                              const int32_t* cell_idx, const T* grad_m, T* grad_V,
-                                              int B, int K, int d) {
-    __shared__ float S[16 * 64];
-    const int lane = lane_id(), w = threadIdx.x >> 6, lr = lane & 15, lq = lane >> 4;
-    const int BK = B * K;
-    const int c0 = blockIdx.x * 64, o0 = blockIdx.y * 16;
-    const int nc = min(64, d - c0);
-    const int o = o0 + lr;  // A row
-    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s0 = 0; s0 < BK; s0 += 16) {
-        gather_sums<T>(h, a, cell_idx, g, s0, BK, K, d, c0, nc, S, 64);
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int s = 4 * q + lq;  // k: the slot
-            const int flat = s0 + s;
-            const float av = flat < BK && o < d ? load_f32(grad_m, int64_t(flat) * d + o) : 0.0f;
-            const int cc = 16 * w + lr;
-            const float bv = cc < nc ? S[s * 64 + cc] : 0.0f;
-            acc = mfma(av, bv, acc);
-        }
-        __syncthreads();
-    }
-    const int c = c0 + 16 * w + lr;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int orow = o0 + 4 * lq + r;
-        if (orow < d && c < d) store_f32(grad_V, int64_t(orow) * d + c, acc[r]);
-    }
-}
-
 // (B, d / 64) wavefronts: row r's grad_h for 64 columns, one lane per column, in blocks of
 // kDhCells source cells accumulated in LDS: every slot in order adds a[e] (V^T grad_m[r, k])[c]
 // to the source cell of each of its edges, in edge order, so every sum has a fixed order.
@@ -963,6 +928,221 @@ __global__ __launch_bounds__(256) void csr_da(const T* h, const Csr g, const T* 
     if (lane == 0) store_f32(grad_a, e, acc);
 }
 
+
+// grad_h by (row, 64 columns, 128 source cells) workgroups with the row's work staged in LDS
+// (K <= 64). u[k] = V^T grad_m[r, k] comes first, for the 64 columns, through LDS blocks of 64
+// rows of V; then the row's edges in slot and edge order (source, weight, slot) are listed into
+// LDS kDhList at a time, each wavefront owns 32 of the 128 cells and walks the whole list, adding
+// a[e] u[k] to the cells it owns, so every cell's sum keeps the list's order. Cells no edge names
+// get zeros.
+constexpr int kDhList = 1024;
+struct DhLds {
+    int start, e0, u, src, w, slot, acc, bytes;
+};
+__host__ __device__ inline DhLds dh_lds(int K) {
+    DhLds L;
+    L.start = 0;                                // int [K + 1]
+    L.e0 = L.start + 4 * (K + 1);               // int [K]
+    L.u = (L.e0 + 4 * K + 15) & ~15;            // float [K][64]
+    L.src = L.u + 4 * 64 * K;                   // int [kDhList]
+    L.w = L.src + 4 * kDhList;                  // float [kDhList]
+    L.slot = L.w + 4 * kDhList;                 // int [kDhList]
+    L.acc = L.slot + 4 * kDhList;               // float [128][64]; first V's block and grad_m's
+    const int stage = 4 * (64 * 64 + 64 * K);   // [64][64] and [K][64]
+    L.bytes = L.acc + (stage > 4 * 128 * 64 ? stage : 4 * 128 * 64);
+    return L;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void csr_dh_rows(const Csr g, const T* a, const T* V,
+                                                   const int32_t* cell_idx, const T* grad_m,
+                                                   T* grad_h, int K, int d) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const DhLds L = dh_lds(K);
+    int* start = reinterpret_cast<int*>(lds + L.start);
+    int* se0 = reinterpret_cast<int*>(lds + L.e0);
+    float* u = reinterpret_cast<float*>(lds + L.u);
+    int* lsrc = reinterpret_cast<int*>(lds + L.src);
+    float* lw = reinterpret_cast<float*>(lds + L.w);
+    int* lslot = reinterpret_cast<int*>(lds + L.slot);
+    float* acc = reinterpret_cast<float*>(lds + L.acc);
+    float* Vs = acc;            // [64 rows o][64 columns]
+    float* gs = acc + 64 * 64;  // [K][64 rows o]
+    const int r = blockIdx.x, c0 = blockIdx.y * 64, n0 = blockIdx.z * 128;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the slots' edge ranges and their offsets in the list (an inclusive scan in wavefront 0)
+    if (wave == 0) {
+        int e0 = 0, e1 = 0;
+        if (lane < K) g.range(cell_idx[r * K + lane], e0, e1);
+        int v = e1 - e0;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_up(v, off, kWave);
+            if (lane >= off) v += t;
+        }
+        if (lane < K) {
+            se0[lane] = e0;
+            start[lane + 1] = v;
+        }
+        if (lane == 0) start[0] = 0;
+    }
+    for (int x = tid; x < K * 64; x += 256) u[x] = 0.0f;
+    for (int o0 = 0; o0 < d; o0 += 64) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int x = tid + 256 * i, oo = x >> 6, cc = x & 63;
+            Vs[x] = o0 + oo < d && c0 + cc < d ? load_f32(V, int64_t(o0 + oo) * d + c0 + cc) : 0.0f;
+        }
+        for (int x = tid; x < K * 64; x += 256) {
+            const int k = x >> 6, oo = x & 63;
+            gs[x] = o0 + oo < d ? load_f32(grad_m, (int64_t(r) * K + k) * d + o0 + oo) : 0.0f;
+        }
+        __syncthreads();
+        for (int x = tid; x < K * 64; x += 256) {  // the same thread owns u[x] every block
+            const int k = x >> 6, cc = x & 63;
+            float sum = u[x];
+#pragma unroll 8
+            for (int oo = 0; oo < 64; ++oo) sum += Vs[oo * 64 + cc] * gs[k * 64 + oo];
+            u[x] = sum;
+        }
+    }
+    __syncthreads();
+    const int total = start[K];
+    const int lo = n0 + 32 * wave, hi = min(lo + 32, g.N);
+    for (int n = lo; n < hi; ++n) acc[(n - n0) * 64 + lane] = 0.0f;
+    for (int p0 = 0; p0 < total; p0 += kDhList) {
+        const int cnt = min(kDhList, total - p0);
+        __syncthreads();  // the last block's walk is done
+        for (int x = tid; x < cnt; x += 256) {
+            const int pos = p0 + x;
+            int klo = 0, khi = K;  // start[klo] <= pos < start[khi]
+            while (khi - klo > 1) {
+                const int mid = (klo + khi) >> 1;
+                if (start[mid] <= pos) klo = mid;
+                else khi = mid;
+            }
+            const int e = se0[klo] + pos - start[klo];
+            const int src = g.indices[e];
+            lsrc[x] = src >= n0 && src < min(n0 + 128, g.N) ? src : -1;
+            lw[x] = load_f32(a, e);
+            lslot[x] = klo;
+        }
+        __syncthreads();
+        for (int i = 0; i < cnt; ++i) {  // uniform test
+            const int src = lsrc[i];
+            if (src >= lo && src < hi) acc[(src - n0) * 64 + lane] += lw[i] * u[lslot[i] * 64 + lane];
+        }
+    }
+    const int c = c0 + lane;
+    if (c < d) {
+        T* gh = grad_h + int64_t(r) * g.N * d;
+        for (int n = lo; n < hi; ++n) store_f32(gh, int64_t(n) * d + c, acc[(n - n0) * 64 + lane]);
+    }
+}
+
+// grad_V by groups of slots, (group, 16 columns, 64 rows) workgroups: the group's slots in
+// chunks of 16, S[s][c] = sum_e a[e] h[r_s, indices[e], c] gathered a (slot, column) a thread into
+// LDS, then grad_m[s]^T S[s] on MFMA, wavefront w taking rows o0 + 16 w .. + 16. With one group
+// the sum goes straight to grad_V; with more, each group's [d][d] fp32 sum goes to part[group]
+// and csr_dV_sum adds the groups in order.
+template <typename T>
+__global__ __launch_bounds__(256) void csr_dV_groups(const T* h, const Csr g, const T* a,
+                                                     const int32_t* cell_idx, const T* grad_m,
+                                                     T* grad_V, float* part, int B, int K, int d,
+                                                     int group_slots) {
+    __shared__ float S[16 * 16];
+    const int lane = lane_id(), w = threadIdx.x >> 6, lr = lane & 15, lq = lane >> 4;
+    const int BK = B * K;
+    const int sb = blockIdx.x * group_slots, se = min(BK, sb + group_slots);
+    const int c0 = blockIdx.y * 16, o = blockIdx.z * 64 + 16 * w + lr;
+    const int s = threadIdx.x >> 4, cc = threadIdx.x & 15;
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = sb; s0 < se; s0 += 16) {
+        const int flat = s0 + s, col = c0 + cc;
+        float sum = 0.0f;
+        if (flat < se && col < d) {
+            const int r = flat / K;
+            int e0, e1;
+            g.range(cell_idx[flat], e0, e1);
+            const T* hr = h + int64_t(r) * g.N * d + col;
+#pragma unroll 4
+            for (int e = e0; e < e1; ++e) {
+                const int src = g.indices[e];
+                if (src >= 0 && src < g.N) sum += load_f32(a, e) * load_f32(hr, int64_t(src) * d);
+            }
+        }
+        __syncthreads();  // the last chunk's products are done
+        S[threadIdx.x] = sum;
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int k = 4 * q + lq;
+            const float av = s0 + k < se && o < d ? load_f32(grad_m, int64_t(s0 + k) * d + o) : 0.0f;
+            acc = mfma(av, S[k * 16 + lr], acc);
+        }
+    }
+    const int c = c0 + lr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int orow = blockIdx.z * 64 + 16 * w + 4 * lq + i;
+        if (orow < d && c < d) {
+            if (part) part[int64_t(blockIdx.x) * d * d + int64_t(orow) * d + c] = acc[i];
+            else store_f32(grad_V, int64_t(orow) * d + c, acc[i]);
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void csr_dV_sum(const float* part, T* grad_V, int groups, int dd) {
+    const int x = blockIdx.x * 256 + threadIdx.x;
+    if (x >= dd) return;
+    float sum = 0.0f;
+    for (int i = 0; i < groups; ++i) sum += part[int64_t(i) * dd + x];
+    store_f32(grad_V, x, sum);
+}
+
+// grad_a with the slots' cells staged in LDS (B K <= 16384): a wavefront per edge e (target row
+// i, source j) finds the slots that selected row i in the LDS copy, in order, and adds
+// (V^T grad_m[r, k]) . h[r, j] for each, lane c taking column c (then a wavefront sum).
+template <typename T>
+__global__ __launch_bounds__(256) void csr_da_rows(const T* h, const Csr g, const T* V,
+                                                   const int32_t* cell_idx, const T* grad_m,
+                                                   T* grad_a, int B, int K, int d) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    int* cells = reinterpret_cast<int*>(lds);
+    const int BK = B * K;
+    for (int x = threadIdx.x; x < BK; x += 256) cells[x] = cell_idx[x];
+    __syncthreads();
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6), lane = lane_id();
+    if (e >= g.E) return;
+    int lo = 0, hi = g.N;  // the target row: the last i with indptr[i] <= e
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (g.indptr[mid] <= e) lo = mid;
+        else hi = mid;
+    }
+    int e0, e1;
+    g.range(lo, e0, e1);
+    const int src = g.indices[e];
+    float acc = 0.0f;
+    if (e >= e0 && e < e1 && src >= 0 && src < g.N) {
+        for (int flat = 0; flat < BK; ++flat) {
+            if (cells[flat] != lo) continue;  // uniform
+            const int r = flat / K;
+            const T* hr = h + (int64_t(r) * g.N + src) * d;
+            const T* gm = grad_m + int64_t(flat) * d;
+            for (int c = lane; c < d; c += 64) {  // lane c: (V^T grad_m)[c] h[c]
+                float ug = 0.0f;
+#pragma unroll 8
+                for (int o = 0; o < d; ++o) ug += load_f32(V, int64_t(o) * d + c) * load_f32(gm, o);
+                acc += ug * load_f32(hr, c);
+            }
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+    if (lane == 0) store_f32(grad_a, e, acc);
+}
 }  // namespace units
 }  // namespace hsn
 
@@ -1084,16 +1264,44 @@ struct RunCsrBwd {
                     const void* V, const int32_t* idx, const void* dm, void* dh, void* da,
                     void* dV, int B, int N, int d, int K, int E, hipStream_t st) {
         const units::Csr g{indptr, indices, N, E};
-        hipLaunchKernelGGL((units::csr_dh<T>), dim3(B, (d + 63) / 64), dim3(64), 0, st, g,
-                           static_cast<const T*>(a), static_cast<const T*>(V), idx,
-                           static_cast<const T*>(dm), static_cast<T*>(dh), K, d);
-        if (E > 0)
+        // grad_V first: with more than one group of slots its fp32 partial sums live in grad_h's
+        // memory (4-byte aligned and large enough), which the grad_h kernel then overwrites
+        const int BK = B * K, chunks = (BK + 15) / 16;
+        const int64_t room = reinterpret_cast<uintptr_t>(dh) % 4 == 0
+                                 ? int64_t(B) * N * d * int64_t(sizeof(T)) / (int64_t(d) * d * 4)
+                                 : 0;
+        int groups = 1, group_slots = 16 * chunks;
+        if (chunks > 1 && room >= 2) {
+            const int most = static_cast<int>(std::min<int64_t>(room, 256));
+            group_slots = 16 * ((chunks + most - 1) / most);
+            groups = (BK + group_slots - 1) / group_slots;
+        }
+        float* part = groups > 1 ? static_cast<float*>(dh) : nullptr;
+        hipLaunchKernelGGL((units::csr_dV_groups<T>), dim3(groups, (d + 15) / 16, (d + 63) / 64),
+                           dim3(256), 0, st, static_cast<const T*>(h), g,
+                           static_cast<const T*>(a), idx, static_cast<const T*>(dm),
+                           static_cast<T*>(dV), part, B, K, d, group_slots);
+        if (part)
+            hipLaunchKernelGGL((units::csr_dV_sum<T>), dim3((d * d + 255) / 256), dim3(256), 0, st,
+                               part, static_cast<T*>(dV), groups, d * d);
+        if (K <= 64)
+            hipLaunchKernelGGL((units::csr_dh_rows<T>), dim3(B, (d + 63) / 64, (N + 127) / 128),
+                               dim3(256), units::dh_lds(K).bytes, st, g, static_cast<const T*>(a),
+                               static_cast<const T*>(V), idx, static_cast<const T*>(dm),
+                               static_cast<T*>(dh), K, d);
+        else
+            hipLaunchKernelGGL((units::csr_dh<T>), dim3(B, (d + 63) / 64), dim3(64), 0, st, g,
+                               static_cast<const T*>(a), static_cast<const T*>(V), idx,
+                               static_cast<const T*>(dm), static_cast<T*>(dh), K, d);
+        if (E > 0 && int64_t(B) * K <= 16384)
+            hipLaunchKernelGGL((units::csr_da_rows<T>), dim3((E + 3) / 4), dim3(256),
+                               size_t(4) * B * K, st, static_cast<const T*>(h), g,
+                               static_cast<const T*>(V), idx, static_cast<const T*>(dm),
+                               static_cast<T*>(da), B, K, d);
+        else if (E > 0)
             hipLaunchKernelGGL((units::csr_da<T>), dim3((E + 3) / 4), dim3(256), 0, st,
                                static_cast<const T*>(h), g, static_cast<const T*>(V), idx,
                                static_cast<const T*>(dm), static_cast<T*>(da), B, K, d);
-        hipLaunchKernelGGL((units::csr_dV<T>), dim3((d + 63) / 64, (d + 15) / 16), dim3(256), 0,
-                           st, static_cast<const T*>(h), g, static_cast<const T*>(a), idx,
-                           static_cast<const T*>(dm), static_cast<T*>(dV), B, K, d);
     }
 };
 

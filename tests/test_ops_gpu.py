@@ -212,6 +212,41 @@ def test_unit_mlp_and_messages_match_oracle_on_ragged_shapes(ops, cuda_device, d
         _close(g_, w_, dtype, name)
 
 
+@pytest.mark.parametrize("B,N,K,d,deg,dtype", [
+    (32, 256, 8, 64, 8, torch.float32),    # the model's round: grad_V over 16 groups of slots
+    (32, 256, 8, 64, 8, torch.bfloat16),   # the same in bf16 (half the room for the partials)
+    (8, 40, 80, 24, 3, torch.float32),     # K above 64: the per-wavefront grad_h kernel
+    (4, 300, 64, 40, 60, torch.float32),   # rows of thousands of edges, 3 cell blocks, d off 16
+])
+def test_csr_messages_backward_paths_match_oracle(ops, cuda_device, B, N, K, d, deg, dtype):
+    """The CSR backward's kernels at the shapes that pick each path, against the float64
+    oracle on inputs rounded to the storage dtype; hubs (cells of in-degree up to 4 deg) make
+    the rows' edge lists run past one LDS block."""
+    from oracle import hsn_oracle as O
+
+    g = torch.Generator().manual_seed(B * 1000 + K)
+    rnd = lambda *s: (torch.randn(*s, generator=g) * 0.5).to(dtype)  # noqa: E731
+    degs = torch.randint(0, deg + 1, (N,), generator=g)
+    degs[: N // 10] *= 4
+    indptr = torch.cat([torch.zeros(1, dtype=torch.int64), degs.cumsum(0)]).to(torch.int32)
+    E = int(indptr[-1])
+    indices = torch.randint(0, N, (E,), generator=g, dtype=torch.int32)
+    a = torch.rand(E, generator=g).to(dtype)
+    h, V, gm = rnd(B, N, d), rnd(d, d), rnd(B, K, d)
+    cell_idx = torch.randint(0, N, (B, K), generator=g, dtype=torch.int32)
+    cell_idx[:, 0] = 0  # every row selects a hub
+    f64 = lambda t: t.double()  # noqa: E731
+    want = O.csr_messages_bwd(f64(h), indptr, indices, f64(a), f64(V), cell_idx, f64(gm))
+    dev = cuda_device
+    got = ops.csr_messages_backward(h.to(dev), indptr.to(dev), indices.to(dev), a.to(dev),
+                                    V.to(dev), cell_idx.to(dev), gm.to(dev))
+    for name, g_, w_ in zip(("dh", "da", "dV"), got, want):
+        _close(g_, w_, dtype, name)
+    again = ops.csr_messages_backward(h.to(dev), indptr.to(dev), indices.to(dev), a.to(dev),
+                                      V.to(dev), cell_idx.to(dev), gm.to(dev))
+    assert all(torch.equal(x, y) for x, y in zip(got, again))
+
+
 def test_unit_mlp_and_messages_are_reproducible(ops, cuda_device):
     """Every sum has a fixed order: two runs agree bit for bit."""
     v = load_golden("ref_grouped_unit_mlp.safetensors")
