@@ -1093,11 +1093,78 @@ __global__ __launch_bounds__(256) void csr_dV_groups(const T* h, const Csr g, co
     }
 }
 
+// U[s][c] = sum_o grad_m[s][o] V[o][c] for 16 slots and 64 columns a workgroup (MFMA, wavefront
+// w taking columns c0 + 16 w .. + 16), in fp32 for csr_da_u.
+template <typename T>
+__global__ __launch_bounds__(256) void csr_u(const T* V, const T* grad_m, float* U, int BK,
+                                             int d) {
+    const int lane = lane_id(), w = threadIdx.x >> 6, lr = lane & 15, lq = lane >> 4;
+    const int s0 = blockIdx.x * 16, c = blockIdx.y * 64 + 16 * w + lr;
+    const bool sin = s0 + lr < BK, cin = c < d;
+    const T* gm = grad_m + int64_t(sin ? s0 + lr : 0) * d;
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+    for (int o0 = 0; o0 < d; o0 += 4) {
+        const int o = o0 + lq;
+        const float av = sin && o < d ? load_f32(gm, o) : 0.0f;
+        const float bv = cin && o < d ? load_f32(V, int64_t(o) * d + c) : 0.0f;
+        acc = mfma(av, bv, acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int s = s0 + 4 * lq + i;
+        if (s < BK && cin) U[int64_t(s) * d + c] = acc[i];
+    }
+}
+
+// grad_a from U: a wavefront per edge e (target row i, source j) adds U[r, k] . h[r, j] over the
+// slots that selected row i, in order. The slots' cells and indptr are staged in LDS
+// ((B K + N + 1) ints within 64 KiB); the slots are found 64 at a time by a ballot and taken in
+// ascending order from its set bits.
+template <typename T>
+__global__ __launch_bounds__(256) void csr_da_u(const T* h, const Csr g, const float* U,
+                                                const int32_t* cell_idx, T* grad_a, int B, int K,
+                                                int d) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int BK = B * K;
+    int* cells = reinterpret_cast<int*>(lds);
+    int* ptr = cells + BK;
+    for (int x = threadIdx.x; x < BK; x += 256) cells[x] = cell_idx[x];
+    for (int x = threadIdx.x; x <= g.N; x += 256) ptr[x] = g.indptr[x];
+    __syncthreads();
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6), lane = lane_id();
+    if (e >= g.E) return;
+    int lo = 0, hi = g.N;  // the target row: the last i with indptr[i] <= e
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (ptr[mid] <= e) lo = mid;
+        else hi = mid;
+    }
+    const int e0 = min(max(ptr[lo], 0), g.E), e1 = min(max(ptr[lo + 1], e0), g.E);
+    const int src = g.indices[e];
+    float acc = 0.0f;
+    if (e >= e0 && e < e1 && src >= 0 && src < g.N) {
+        for (int f0 = 0; f0 < BK; f0 += 64) {
+            uint64_t hits = ballot(f0 + lane < BK && cells[f0 + lane] == lo);
+            while (hits) {  // uniform
+                const int flat = f0 + __builtin_ctzll(hits);
+                hits &= hits - 1;
+                const T* hr = h + (int64_t(flat / K) * g.N + src) * d;
+                const float* u = U + int64_t(flat) * d;
+                for (int c = lane; c < d; c += 64) acc += u[c] * load_f32(hr, c);
+            }
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+    if (lane == 0) store_f32(grad_a, e, acc);
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void csr_dV_sum(const float* part, T* grad_V, int groups, int dd) {
     const int x = blockIdx.x * 256 + threadIdx.x;
     if (x >= dd) return;
-    float sum = 0.0f;
+    float sum = 0.0f;  // the loads issued 8 at a time; the sum keeps the groups' order
+#pragma unroll 8
     for (int i = 0; i < groups; ++i) sum += part[int64_t(i) * dd + x];
     store_f32(grad_V, x, sum);
 }
@@ -1284,6 +1351,27 @@ struct RunCsrBwd {
         if (part)
             hipLaunchKernelGGL((units::csr_dV_sum<T>), dim3((d * d + 255) / 256), dim3(256), 0, st,
                                part, static_cast<T*>(dV), groups, d * d);
+        // grad_a next, from U = grad_m V in grad_h's memory when it fits there
+        const bool u_fits = reinterpret_cast<uintptr_t>(dh) % 4 == 0 &&
+                            int64_t(BK) * d * 4 <= int64_t(B) * N * d * int64_t(sizeof(T));
+        if (E > 0 && int64_t(BK) + N + 1 <= 16384 && u_fits) {
+            float* U = static_cast<float*>(dh);
+            hipLaunchKernelGGL((units::csr_u<T>), dim3(chunks, (d + 63) / 64), dim3(256), 0, st,
+                               static_cast<const T*>(V), static_cast<const T*>(dm), U, BK, d);
+            hipLaunchKernelGGL((units::csr_da_u<T>), dim3((E + 3) / 4), dim3(256),
+                               size_t(4) * (BK + N + 1),
+                               st, static_cast<const T*>(h), g, U, idx, static_cast<T*>(da), B,
+                               K, d);
+        } else if (E > 0 && BK <= 16384) {
+            hipLaunchKernelGGL((units::csr_da_rows<T>), dim3((E + 3) / 4), dim3(256),
+                               size_t(4) * BK, st, static_cast<const T*>(h), g,
+                               static_cast<const T*>(V), idx, static_cast<const T*>(dm),
+                               static_cast<T*>(da), B, K, d);
+        } else if (E > 0) {
+            hipLaunchKernelGGL((units::csr_da<T>), dim3((E + 3) / 4), dim3(256), 0, st,
+                               static_cast<const T*>(h), g, static_cast<const T*>(V), idx,
+                               static_cast<const T*>(dm), static_cast<T*>(da), B, K, d);
+        }
         if (K <= 64)
             hipLaunchKernelGGL((units::csr_dh_rows<T>), dim3(B, (d + 63) / 64, (N + 127) / 128),
                                dim3(256), units::dh_lds(K).bytes, st, g, static_cast<const T*>(a),
@@ -1293,15 +1381,6 @@ struct RunCsrBwd {
             hipLaunchKernelGGL((units::csr_dh<T>), dim3(B, (d + 63) / 64), dim3(64), 0, st, g,
                                static_cast<const T*>(a), static_cast<const T*>(V), idx,
                                static_cast<const T*>(dm), static_cast<T*>(dh), K, d);
-        if (E > 0 && int64_t(B) * K <= 16384)
-            hipLaunchKernelGGL((units::csr_da_rows<T>), dim3((E + 3) / 4), dim3(256),
-                               size_t(4) * B * K, st, static_cast<const T*>(h), g,
-                               static_cast<const T*>(V), idx, static_cast<const T*>(dm),
-                               static_cast<T*>(da), B, K, d);
-        else if (E > 0)
-            hipLaunchKernelGGL((units::csr_da<T>), dim3((E + 3) / 4), dim3(256), 0, st,
-                               static_cast<const T*>(h), g, static_cast<const T*>(V), idx,
-                               static_cast<const T*>(dm), static_cast<T*>(da), B, K, d);
     }
 };
 
