@@ -96,7 +96,8 @@ int hsn_csr_messages(const void* h, const int32_t* indptr, const int32_t* indice
  * edge e of its row, source j = indices[e]:
  *   grad_h[r,j,:] = sum a[e] (V^T grad_m[r,k,:]); grad_V = sum a[e] grad_m[r,k,:] (outer)
  *   h[r,j,:]; grad_a[e] = sum grad_m[r,k,:] . (V h[r,j,:]).
- * Every sum has a fixed order (no atomics), so `deterministic` holds either way.
+ * Every sum has a fixed order (no atomics), so `deterministic` holds either way. grad_h must
+ * not overlap any input: its memory holds intermediate fp32 sums before grad_h is written.
  */
 int hsn_csr_messages_bwd(const void* h, const int32_t* indptr, const int32_t* indices,
                          const void* a, const void* V, const int32_t* cell_idx,
