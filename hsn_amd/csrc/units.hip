@@ -465,6 +465,8 @@ __global__ __launch_bounds__(256) void mlp_dw(const T* v, const int32_t* unit_id
                                               int H) {
     __shared__ float dz[16][64];
     __shared__ float act[16][64];
+    __shared__ float gos[16 * 256];  // the chunk's grad_out rows, [16][d]
+    __shared__ float vs[16][64];     // the chunk's v rows at the workgroup's 64 inputs
     const int j = blockIdx.y, lane = lane_id(), w = threadIdx.x >> 6, lr = lane & 15,
               lq = lane >> 4, tid = threadIdx.x;
     const int in = 4 * d;
@@ -481,54 +483,102 @@ __global__ __launch_bounds__(256) void mlp_dw(const T* v, const int32_t* unit_id
     float gb1 = 0.0f;  // thread tid < 64: column h0 + tid
     float gb2[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // first workgroup: columns tid + 256 u
     int cur = 0;
+    const int hw = h0 + 16 * w + lr;  // the wavefront's hidden column for dz
+    const bool hwin = hw < H;
+    const T* w2h = W2j + int64_t(hwin ? hw : 0) * d;
+    const int kr = tid >> 4, kc = tid & 15;  // the thread's row and column phase when staging
     for (;;) {
         const Chunk c = next_pairs(unit_idx, P, j, cur);
         if (c.n == 0) break;
-        dz_tile<T>(grad_out, W2j, hidden, c, h0, d, H, dz, first_in ? act : nullptr);
+        // every load of the chunk in one batch: the pairs' grad_out rows and v's 64 inputs (for
+        // LDS), W2's columns (dz's B operand) and z1 of the wavefront's rows
+        const int pr = pair_of(c, kr);
+        float gr[16], vr[4], b[16], z[4];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int o = kc + 16 * i;
+            gr[i] = pr >= 0 && o < d ? load_f32(grad_out, int64_t(pr) * d + o) : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int x = i0 + kc + 16 * i;
+            vr[i] = pr >= 0 && x < in ? load_f32(v, int64_t(pr) * in + x) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int k = 4 * u + lq;
+            b[u] = hwin && k < d ? load_f32(w2h, k) : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int p = pair_of(c, 4 * lq + r);
+            z[r] = p >= 0 && hwin ? load_f32(hidden, int64_t(p) * H + hw) : 0.0f;
+        }
+        __syncthreads();  // the last chunk's reads of the tiles are done
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int o = kc + 16 * i;
+            if (o < d) gos[kr * d + o] = gr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vs[kr][kc + 16 * i] = vr[i];
+        __syncthreads();
+        // dz1 = (grad_out W2[j]^T) * gelu'(z1): A[pair][k] = grad_out rows (LDS), B[k][h] = W2
+        v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int k = 4 * u + lq;
+            acc = mfma(k < d ? gos[lr * d + k] : 0.0f, b[u], acc);
+        }
+        for (int k0 = 64; k0 < d; k0 += 64) {  // d above 64: the next blocks of W2's columns
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int k = k0 + 4 * u + lq;
+                const float bv = hwin && k < d ? load_f32(w2h, k) : 0.0f;
+                acc = mfma(k < d ? gos[lr * d + k] : 0.0f, bv, acc);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 4 * lq + r;
+            const bool ok = pair_of(c, row) >= 0 && hwin;
+            dz[row][16 * w + lr] = ok ? acc[r] * gelu_grad(z[r]) : 0.0f;
+            if (first_in) act[row][16 * w + lr] = ok ? gelu(z[r]) : 0.0f;
+        }
         __syncthreads();
         // grad_W1[i][h] += sum_k v[p_k][i] dz[k][h]: A = v^T (rows i, k = pairs), B = dz
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int k = 4 * s + lq;  // the pair
-            const int p = pair_of(c, k);
             const float bv = dz[k][16 * w + lr];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int i = i0 + 16 * t + lr;
-                const float av = p >= 0 && i < in ? load_f32(v, int64_t(p) * in + i) : 0.0f;
-                gw1[t] = mfma(av, bv, gw1[t]);
-            }
+            for (int t = 0; t < 4; ++t) gw1[t] = mfma(vs[k][16 * t + lr], bv, gw1[t]);
         }
         if (first_in) {
             // grad_W2[h][o] += sum_k gelu(z1)[k][h] grad_out[p_k][o]: A = act^T, B = grad_out
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const int k = 4 * s + lq;
-                const int p = pair_of(c, k);
                 const float av = act[k][16 * w + lr];
 #pragma unroll
                 for (int t = 0; t < kMaxD16; ++t) {
                     if (t < nd) {
                         const int o = 16 * t + lr;
-                        const float bv = p >= 0 && o < d ? load_f32(grad_out, int64_t(p) * d + o) : 0.0f;
-                        gw2[t] = mfma(av, bv, gw2[t]);
+                        gw2[t] = mfma(av, o < d ? gos[k * d + o] : 0.0f, gw2[t]);
                     }
                 }
             }
             if (tid < 64)
                 for (int k = 0; k < c.n; ++k) gb1 += dz[k][tid];
             if (blockIdx.x == 0) {
-                for (int k = 0; k < c.n; ++k) {
-                    const int p = pair_of(c, k);
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const int o = tid + 256 * u;
-                        if (o < d) gb2[u] += load_f32(grad_out, int64_t(p) * d + o);
-                    }
+                for (int u = 0; u < 4; ++u) {
+                    const int o = tid + 256 * u;
+                    if (o < d)
+                        for (int k = 0; k < c.n; ++k) gb2[u] += gos[k * d + o];
                 }
             }
         }
-        __syncthreads();  // before the next chunk rewrites the tiles
     }
     const int h = h0 + 16 * w + lr;
 #pragma unroll
