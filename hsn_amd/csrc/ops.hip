@@ -18,6 +18,10 @@ __global__ __launch_bounds__(256) void copy_or_zero(const F* src, F* dst, int64_
     if (i < n) dst[i] = src ? src[i] : from_f32<F>(0.0f);
 }
 
+// A thread per (row, column) walks the row's K slots in order, 8 at a time: the group's valid
+// flags, cells, gates and candidates are loaded first, then the group's old values of h in one
+// batch; a cell that an earlier slot of the group already updated takes that slot's stored value
+// (in-place order, as if each slot read h after the slots before it).
 template <typename F>
 __global__ __launch_bounds__(256) void gated_update_fwd(F* h, F* q, int32_t* age,
                                                         const int32_t* cell_idx,
@@ -27,23 +31,42 @@ __global__ __launch_bounds__(256) void gated_update_fwd(F* h, F* q, int32_t* age
     const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (e >= int64_t(B) * d) return;
     const int r = static_cast<int>(e / d), x = static_cast<int>(e - int64_t(r) * d);
+    constexpr int G = 8;
     float delta = 0.0f;
-    for (int k = 0; k < K; ++k) {
-        const int64_t s = int64_t(r) * K + k;
-        const int64_t o = s * d + x;
-        if (valid[s]) {
-            const int n = cell_idx[s];
-            const int64_t hi = (int64_t(r) * N + n) * d + x;
-            const float old = to_f32(h[hi]);
-            const float bv = to_f32(bgate[o]);
-            const float value = (1.0f - bv) * old + bv * to_f32(c[o]);
-            const F stored = from_f32<F>(value);
-            h[hi] = stored;
-            h_old_saved[o] = from_f32<F>(old);
-            delta += to_f32(stored) - old;
-            if (x == 0) age[int64_t(r) * N + n] = 0;
-        } else {
-            h_old_saved[o] = from_f32<F>(0.0f);
+    for (int k0 = 0; k0 < K; k0 += G) {
+        bool on[G];
+        int cell[G];
+        float cv[G], bv[G], old[G], stored[G];
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const int64_t s = int64_t(r) * K + k0 + i;
+            on[i] = k0 + i < K && valid[s] != 0;
+            cell[i] = on[i] ? cell_idx[s] : -1;
+            cv[i] = on[i] ? to_f32(c[s * d + x]) : 0.0f;
+            bv[i] = on[i] ? to_f32(bgate[s * d + x]) : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < G; ++i)
+            old[i] = on[i] ? to_f32(h[(int64_t(r) * N + cell[i]) * d + x]) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            stored[i] = 0.0f;
+            if (k0 + i >= K) continue;
+            const int64_t o = (int64_t(r) * K + k0 + i) * d + x;
+            if (on[i]) {
+                float prev = old[i];
+#pragma unroll
+                for (int t = 0; t < i; ++t)
+                    if (on[t] && cell[t] == cell[i]) prev = stored[t];  // the latest earlier slot
+                const F st = from_f32<F>((1.0f - bv[i]) * prev + bv[i] * cv[i]);
+                stored[i] = to_f32(st);
+                h[(int64_t(r) * N + cell[i]) * d + x] = st;
+                h_old_saved[o] = from_f32<F>(prev);
+                delta += stored[i] - prev;
+                if (x == 0) age[int64_t(r) * N + cell[i]] = 0;
+            } else {
+                h_old_saved[o] = from_f32<F>(0.0f);
+            }
         }
     }
     const int64_t qi = int64_t(r) * d + x;

@@ -142,8 +142,9 @@ def _update_inplace_fake(h, q, age, idx, valid, c, b):
 
 
 def _functional(h, q, age, idx, valid, c, b):
-    hn, qn = h.contiguous().clone(), q.contiguous().clone()
-    an = age.to(torch.int32).contiguous().clone()
+    hn = h.clone(memory_format=torch.contiguous_format)
+    qn = q.clone(memory_format=torch.contiguous_format)
+    an = age.to(torch.int32, copy=True, memory_format=torch.contiguous_format)
     old = _update(hn, qn, an, idx, valid, c, b)
     return hn, qn, an.to(age.dtype), old
 

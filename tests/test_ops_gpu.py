@@ -212,6 +212,50 @@ def test_unit_mlp_and_messages_match_oracle_on_ragged_shapes(ops, cuda_device, d
         _close(g_, w_, dtype, name)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gated_update_slot_groups_match_oracle_and_slot_order(ops, cuda_device, dtype):
+    """K = 19 slots (three groups of the kernel's 8) with padded slots. Rows without repeated
+    cells: against the float64 oracle. Rows with a cell repeated inside a group and across
+    groups: against 19 single-slot calls in slot order, since the ABI's update is in place and
+    each slot reads h after the slots before it."""
+    from oracle import hsn_oracle as O
+
+    g = torch.Generator().manual_seed(77)
+    B, N, K, d = 3, 40, 19, 70
+    rnd = lambda *s: (torch.randn(*s, generator=g) * 0.5).to(dtype)  # noqa: E731
+    h, q, c, b = rnd(B, N, d), rnd(B, d), rnd(B, K, d), torch.rand(B, K, d, generator=g).to(dtype)
+    age = torch.randint(0, 9, (B, N), generator=g, dtype=torch.int32)
+    cells = torch.stack([torch.randperm(N, generator=g)[:K] for _ in range(B)]).to(torch.int32)
+    valid = (torch.rand(B, K, generator=g) > 0.2).to(torch.int32)
+    dev = cuda_device
+    f64 = lambda t: t.double()  # noqa: E731
+    want = O.gated_delta_update_abi(f64(h), f64(q), age, cells, valid, f64(c), f64(b))
+    got = ops.gated_delta_update_functional(h.to(dev), q.to(dev), age.to(dev), cells.to(dev),
+                                            valid.to(dev), c.to(dev), b.to(dev))
+    for name, g_, w_ in zip(("h", "q", "age", "h_old"), got, want):
+        _close(g_, w_, dtype, name)
+    rep = cells.clone()
+    rep[0, 3] = rep[0, 1]     # inside the first group
+    rep[1, 12] = rep[1, 2]    # across groups
+    rep[2, 18] = rep[2, 9]
+    rep[2, 10] = rep[2, 9]
+    valid[:, [1, 2, 3, 9, 10, 12, 18]] = 1
+    got = ops.gated_delta_update_functional(h.to(dev), q.to(dev), age.to(dev), rep.to(dev),
+                                            valid.to(dev), c.to(dev), b.to(dev))
+    hs, qs, ages = h.to(dev), q.to(dev), age.to(dev)
+    olds = []
+    for k in range(K):
+        one = torch.zeros_like(valid)
+        one[:, k] = valid[:, k]
+        hs, qs, ages, old = ops.gated_delta_update_functional(hs, qs, ages, rep.to(dev),
+                                                              one.to(dev), c.to(dev), b.to(dev))
+        olds.append(old[:, k])
+    _close(got[0], hs.cpu(), dtype, "h")
+    _close(got[1], qs.cpu(), dtype, "q")
+    assert torch.equal(got[2].cpu(), ages.cpu())
+    _close(got[3], torch.stack(olds, 1).cpu(), dtype, "h_old")
+
+
 @pytest.mark.parametrize("B,N,K,d,deg,dtype", [
     (32, 256, 8, 64, 8, torch.float32),    # the model's round: grad_V over 16 groups of slots
     (32, 256, 8, 64, 8, torch.bfloat16),   # the same in bf16 (half the room for the partials)
