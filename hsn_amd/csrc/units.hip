@@ -874,6 +874,76 @@ __device__ __forceinline__ void gather_sums(const T* h, const T* a, const int32_
     }
 }
 
+// S as gather_sums, with the 16 slots' edges listed into LDS first when they fit (kListCap
+// entries): wavefront 0 finds the slots' ranges and their offsets, every thread lists entries
+// (source, weight), then each (slot, column) sums its slot's entries in edge order with the loads
+// of h issued 8 at a time. A longer list takes gather_sums.
+constexpr int kListCap = 1024;
+template <typename T>
+__device__ __forceinline__ void gather_sums_listed(const T* h, const T* a,
+                                                   const int32_t* cell_idx, const Csr& g, int s0,
+                                                   int BK, int K, int d, float* S) {
+    __shared__ int lstart[17], le0[16], lsrc[kListCap];
+    __shared__ float lw[kListCap];
+    const int tid = threadIdx.x, lane = lane_id();
+    if (tid < kWave) {
+        int e0 = 0, e1 = 0;
+        if (lane < 16 && s0 + lane < BK) g.range(cell_idx[s0 + lane], e0, e1);
+        int v = lane < 16 ? e1 - e0 : 0;
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+            const int t = __shfl_up(v, off, kWave);
+            if (lane >= off) v += t;
+        }
+        if (lane < 16) {
+            le0[lane] = e0;
+            lstart[lane + 1] = v;
+        }
+        if (lane == 0) lstart[0] = 0;
+    }
+    __syncthreads();
+    const int total = lstart[16];
+    if (total > kListCap) {  // uniform
+        gather_sums<T>(h, a, cell_idx, g, s0, BK, K, d, 0, d, S, d);
+        return;
+    }
+    for (int x = tid; x < total; x += blockDim.x) {
+        int lo = 0, hi = 16;  // lstart[lo] <= x < lstart[hi]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (lstart[mid] <= x) lo = mid;
+            else hi = mid;
+        }
+        const int e = le0[lo] + x - lstart[lo];
+        const int src = g.indices[e];
+        lsrc[x] = src >= 0 && src < g.N ? src : -1;
+        lw[x] = load_f32(a, e);
+    }
+    __syncthreads();
+    for (int x = tid; x < 16 * d; x += blockDim.x) {
+        const int sl = x / d, col = x - sl * d;
+        const int flat = s0 + sl;
+        float sum = 0.0f;
+        if (flat < BK) {
+            const T* hr = h + int64_t(flat / K) * g.N * d + col;
+            const int b0 = lstart[sl], b1 = lstart[sl + 1];
+            for (int j0 = b0; j0 < b1; j0 += 8) {
+                float hv[8], wv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int src = j0 + u < b1 ? lsrc[j0 + u] : -1;
+                    wv[u] = src >= 0 ? lw[j0 + u] : 0.0f;
+                    hv[u] = src >= 0 ? load_f32(hr, int64_t(src) * d) : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (j0 + u < b1 && lsrc[j0 + u] >= 0) sum += wv[u] * hv[u];
+            }
+        }
+        S[x] = sum;
+    }
+}
+
 // (BK / 16, d / 64) workgroups: m[s][o] = sum_c V[o][c] S[s][c] for 16 slots (S in LDS).
 template <typename T>
 __global__ __launch_bounds__(256) void csr_fwd(const T* h, const Csr g, const T* a, const T* V,
@@ -882,7 +952,7 @@ __global__ __launch_bounds__(256) void csr_fwd(const T* h, const Csr g, const T*
     extern __shared__ float S[];  // [16][d]
     const int lane = lane_id(), w = threadIdx.x >> 6, lr = lane & 15, lq = lane >> 4;
     const int BK = B * K, s0 = blockIdx.x * 16;
-    gather_sums<T>(h, a, cell_idx, g, s0, BK, K, d, 0, d, S, d);
+    gather_sums_listed<T>(h, a, cell_idx, g, s0, BK, K, d, S);
     __syncthreads();
     const int o = blockIdx.y * 64 + 16 * w + lr;
     const bool oin = o < d;

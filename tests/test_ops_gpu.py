@@ -263,7 +263,7 @@ def test_gated_update_slot_groups_match_oracle_and_slot_order(ops, cuda_device, 
     (4, 300, 64, 40, 60, torch.float32),   # rows of thousands of edges, 3 cell blocks, d off 16
 ])
 def test_csr_messages_backward_paths_match_oracle(ops, cuda_device, B, N, K, d, deg, dtype):
-    """The CSR backward's kernels at the shapes that pick each path, against the float64
+    """The CSR forward's and backward's kernels at the shapes that pick each path, against the float64
     oracle on inputs rounded to the storage dtype; hubs (cells of in-degree up to 4 deg) make
     the rows' edge lists run past one LDS block."""
     from oracle import hsn_oracle as O
@@ -280,8 +280,11 @@ def test_csr_messages_backward_paths_match_oracle(ops, cuda_device, B, N, K, d, 
     cell_idx = torch.randint(0, N, (B, K), generator=g, dtype=torch.int32)
     cell_idx[:, 0] = 0  # every row selects a hub
     f64 = lambda t: t.double()  # noqa: E731
-    want = O.csr_messages_bwd(f64(h), indptr, indices, f64(a), f64(V), cell_idx, f64(gm))
     dev = cuda_device
+    m = ops.csr_messages(h.to(dev), indptr.to(dev), indices.to(dev), a.to(dev), V.to(dev),
+                         cell_idx.to(dev))  # hubs: slot lists past the forward's LDS list
+    _close(m, O.csr_messages(f64(h), indptr, indices, f64(a), f64(V), cell_idx), dtype, "m")
+    want = O.csr_messages_bwd(f64(h), indptr, indices, f64(a), f64(V), cell_idx, f64(gm))
     got = ops.csr_messages_backward(h.to(dev), indptr.to(dev), indices.to(dev), a.to(dev),
                                     V.to(dev), cell_idx.to(dev), gm.to(dev))
     for name, g_, w_ in zip(("dh", "da", "dV"), got, want):
