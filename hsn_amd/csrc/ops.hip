@@ -86,21 +86,38 @@ __global__ __launch_bounds__(256) void gated_update_bwd(const int32_t* cell_idx,
     const float gq = to_f32(g[int64_t(r) * d + x]);
     const float share = gq / static_cast<float>(N);
     grad_q[int64_t(r) * d + x] = g[int64_t(r) * d + x];
-    for (int k = 0; k < K; ++k) {
-        const int64_t s = int64_t(r) * K + k;
-        const int64_t o = s * d + x;
-        if (valid[s]) {
-            const int n = cell_idx[s];
-            const int64_t hi = (int64_t(r) * N + n) * d + x;
-            const float Gn = to_f32(G[hi]);
-            const float bv = to_f32(bgate[o]);
-            const float total = Gn + share;
-            grad_h[hi] = from_f32<F>((1.0f - bv) * Gn - bv * share);
-            grad_c[o] = from_f32<F>(bv * total);
-            grad_b[o] = from_f32<F>((to_f32(c[o]) - to_f32(h_old[o])) * total);
-        } else {
-            grad_c[o] = from_f32<F>(0.0f);
-            grad_b[o] = from_f32<F>(0.0f);
+    constexpr int S = 8;  // slots a batch: every load of the batch issued before its stores
+    for (int k0 = 0; k0 < K; k0 += S) {
+        bool on[S];
+        int64_t hi[S];
+        float Gn[S], bv[S], cv[S], ov[S];
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            const int64_t s = int64_t(r) * K + k0 + i;
+            on[i] = k0 + i < K && valid[s] != 0;
+            hi[i] = on[i] ? (int64_t(r) * N + cell_idx[s]) * d + x : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            const int64_t o = (int64_t(r) * K + k0 + i) * d + x;
+            Gn[i] = on[i] ? to_f32(G[hi[i]]) : 0.0f;
+            bv[i] = on[i] ? to_f32(bgate[o]) : 0.0f;
+            cv[i] = on[i] ? to_f32(c[o]) : 0.0f;
+            ov[i] = on[i] ? to_f32(h_old[o]) : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            if (k0 + i >= K) continue;
+            const int64_t o = (int64_t(r) * K + k0 + i) * d + x;
+            if (on[i]) {
+                const float total = Gn[i] + share;
+                grad_h[hi[i]] = from_f32<F>((1.0f - bv[i]) * Gn[i] - bv[i] * share);
+                grad_c[o] = from_f32<F>(bv[i] * total);
+                grad_b[o] = from_f32<F>((cv[i] - ov[i]) * total);
+            } else {
+                grad_c[o] = from_f32<F>(0.0f);
+                grad_b[o] = from_f32<F>(0.0f);
+            }
         }
     }
 }

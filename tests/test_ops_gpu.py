@@ -234,6 +234,13 @@ def test_gated_update_slot_groups_match_oracle_and_slot_order(ops, cuda_device, 
                                             valid.to(dev), c.to(dev), b.to(dev))
     for name, g_, w_ in zip(("h", "q", "age", "h_old"), got, want):
         _close(g_, w_, dtype, name)
+    G, gq = rnd(B, N, d), rnd(B, d)  # the backward over the same three groups of slots
+    old = got[3].cpu()
+    want = O.gated_delta_update_bwd(cells, valid, f64(c), f64(b), f64(old), f64(G), f64(gq))
+    back = ops.gated_delta_update_backward(cells.to(dev), valid.to(dev), c.to(dev), b.to(dev),
+                                           old.to(dev), G.to(dev), gq.to(dev))
+    for name, g_, w_ in zip(("grad_h", "grad_q", "grad_c", "grad_b"), back, want):
+        _close(g_, w_, dtype, name)
     rep = cells.clone()
     rep[0, 3] = rep[0, 1]     # inside the first group
     rep[1, 12] = rep[1, 2]    # across groups
