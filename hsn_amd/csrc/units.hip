@@ -250,25 +250,12 @@ __device__ __forceinline__ float4 row4w(const T* w, int c, int cols, bool aligne
                        c + 3 < cols ? to_f32(w[c + 3]) : 0.0f);
 }
 
-template <typename T, bool ALIGNED>  // ALIGNED: H % 4 == 0, rows of W1 in 16-byte pieces
-__global__ __launch_bounds__(256) void mlp_fwd_tiles(const T* v, const int32_t* unit_idx,
-                                                     const T* W1, const T* b1, const T* W2,
-                                                     const T* b2, T* hidden, T* out, int P, int M,
-                                                     int d, int H) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    const TileLds L = tile_lds(P, M, d, H);
-    uint16_t* ucache = reinterpret_cast<uint16_t*>(lds + L.ucache);
-    int* count = reinterpret_cast<int*>(lds + L.count);
-    int* rows = reinterpret_cast<int*>(lds + L.rows);
-    int* meta = reinterpret_cast<int*>(lds + L.meta);
-    float* vs = reinterpret_cast<float*>(lds + L.vs);
-    float* red = reinterpret_cast<float*>(lds + L.red);
-    float* act = reinterpret_cast<float*>(lds + L.act);
-    float* b1c = reinterpret_cast<float*>(lds + L.b1);
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, g = lane >> 4;
-    const int n = 4 * d;
-
-    // ---- which unit's which row tile ----
+// The workgroup's row tile (blockIdx.x over every unit's tiles of 16 pairs, laid end to end unit
+// after unit): returns its unit, or -1 past the last tile, with its pairs in rows[16] (-1 past
+// the unit's pairs), from LDS counts of each unit's pairs. Every thread of the workgroup calls it.
+__device__ __forceinline__ int find_row_tile(const int32_t* unit_idx, int P, int M,
+                                             uint16_t* ucache, int* count, int* rows, int* meta) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     for (int j = tid; j < M; j += 256) count[j] = 0;
     for (int q = tid; q < P; q += 256) {
         const int u = unit_idx[q];
@@ -310,7 +297,29 @@ __global__ __launch_bounds__(256) void mlp_fwd_tiles(const T* v, const int32_t* 
         if (lane == 0) meta[0] = unit;
     }
     __syncthreads();
-    const int j = meta[0];
+    return meta[0];
+}
+
+template <typename T, bool ALIGNED, bool SPLIT = false>  // ALIGNED: H % 4 == 0, rows of W1 in
+// 16-byte pieces; SPLIT: one hidden tile a workgroup (blockIdx.y), z1 stored, no second layer
+__global__ __launch_bounds__(256) void mlp_fwd_tiles(const T* v, const int32_t* unit_idx,
+                                                     const T* W1, const T* b1, const T* W2,
+                                                     const T* b2, T* hidden, T* out, int P, int M,
+                                                     int d, int H) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const TileLds L = tile_lds(P, M, d, H);
+    uint16_t* ucache = reinterpret_cast<uint16_t*>(lds + L.ucache);
+    int* count = reinterpret_cast<int*>(lds + L.count);
+    int* rows = reinterpret_cast<int*>(lds + L.rows);
+    int* meta = reinterpret_cast<int*>(lds + L.meta);
+    float* vs = reinterpret_cast<float*>(lds + L.vs);
+    float* red = reinterpret_cast<float*>(lds + L.red);
+    float* act = reinterpret_cast<float*>(lds + L.act);
+    float* b1c = reinterpret_cast<float*>(lds + L.b1);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, g = lane >> 4;
+    const int n = 4 * d;
+
+    const int j = find_row_tile(unit_idx, P, M, ucache, count, rows, meta);
     if (j < 0) return;  // past the last tile (uniform)
 
     // ---- the tile's inputs, widened into LDS ----
@@ -354,13 +363,13 @@ __global__ __launch_bounds__(256) void mlp_fwd_tiles(const T* v, const int32_t* 
     // buffers (no copy, so no wait on loads in flight), and a tile's last block is followed by
     // its tail: the shares' sum, z1, the GELU and the second layer.
     float4 bufA[kTileBlock], bufB[kTileBlock];
-    load_block(bufA, 0, 0);
+    load_block(bufA, SPLIT ? int(blockIdx.y) : 0, 0);
     for (int c = tid; c < H; c += 256) b1c[c] = load_f32(b1, int64_t(j) * H + c);
     __syncthreads();  // the inputs and the bias are in LDS
 
     v4f acc[4];
     const float* arow = vs + lr * L.sv + k1;
-    const int total = tiles_h * blocks;
+    const int total = SPLIT ? blocks : tiles_h * blocks;
     auto load_w2 = [&](float (&w)[16], int h0, int t) {
         const int col = (wave + 4 * t) * 16 + lr;
 #pragma unroll
@@ -371,12 +380,13 @@ __global__ __launch_bounds__(256) void mlp_fwd_tiles(const T* v, const int32_t* 
         }
     };
     auto step = [&](int i, float4 (&cur)[kTileBlock], float4 (&nxt)[kTileBlock]) {
-        const int ht = i / blocks, bi = i % blocks;
+        const int ht = SPLIT ? int(blockIdx.y) : i / blocks, bi = i % blocks;
         if (bi == 0) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) acc[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        if (i + 1 < total) load_block(nxt, (i + 1) / blocks, (i + 1) % blocks);
+        if (i + 1 < total)
+            load_block(nxt, SPLIT ? int(blockIdx.y) : (i + 1) / blocks, (i + 1) % blocks);
         float av[kTileBlock];
 #pragma unroll
         for (int k = 0; k < kTileBlock; ++k) {
@@ -395,7 +405,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_tiles(const T* v, const int32_t* 
         // all of them) are in flight during the shares' sum
         const int h0 = ht * 64;
         float w2v[16];
-        load_w2(w2v, h0, 0);
+        if constexpr (!SPLIT) load_w2(w2v, h0, 0);
         // the wavefront's share: row 4 g + r, column 4 lr + t of the tile
 #pragma unroll
         for (int t = 0; t < 4; ++t)
@@ -413,6 +423,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_tiles(const T* v, const int32_t* 
             if (ok) store_f32(hidden, int64_t(q) * H + h0 + c, z);
             act[row * 65 + c] = ok ? gelu(z) : 0.0f;
         }
+        if constexpr (SPLIT) return;
         __syncthreads();
         // out += gelu(z1) W2[j][h0 .. h0 + 63]: output tile wave + 4 t, B[k][col] = W2[j][h0 + k][col]
         {
@@ -435,6 +446,7 @@ __global__ __launch_bounds__(256) void mlp_fwd_tiles(const T* v, const int32_t* 
         step(i, bufA, bufB);
         if (i + 1 < total) step(i + 1, bufB, bufA);
     }
+    if constexpr (SPLIT) return;
     int prow[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) prow[r] = rows[4 * g + r];
@@ -446,6 +458,106 @@ __global__ __launch_bounds__(256) void mlp_fwd_tiles(const T* v, const int32_t* 
 #pragma unroll
             for (int r = 0; r < 4; ++r)
                 if (prow[r] >= 0) store_f32(out, int64_t(prow[r]) * d + col, oacc[t][r] + bias);
+        }
+    }
+}
+
+// The second layer by (row tile, 16 output columns) workgroups, from the stored z1 (fp32
+// storage, so z1 is exact): out = gelu(z1) W2[j] + b2[j]. The tile's gelu(z1) for all H columns
+// goes into LDS; wavefront w takes hidden tiles w, w + 4, ... (their W2 columns loaded in one
+// batch while the activations are staged), and the four shares are summed in wavefront order.
+constexpr int kOutGroup = 4;  // hidden tiles a wavefront loads together
+struct OutLds {
+    int ucache, count, rows, meta, red, act, bytes;
+};
+__host__ __device__ inline OutLds out_lds(int P, int M, int H) {
+    OutLds L;
+    L.ucache = 0;                                   // uint16 [P]
+    L.count = (2 * P + 15) / 16 * 16;               // int [M]
+    L.rows = L.count + (4 * M + 15) / 16 * 16;      // int [16]
+    L.meta = L.rows + 64;                           // int [4]
+    L.red = L.meta + 16;                            // float [4][16][16]
+    L.act = L.red + 4 * 4 * 16 * 16;                // float [16][H + 1]
+    L.bytes = L.act + 4 * 16 * (H + 1);
+    return L;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void mlp_out_tiles(const int32_t* unit_idx, const T* W2,
+                                                     const T* b2, const T* hidden, T* out, int P,
+                                                     int M, int d, int H) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const OutLds L = out_lds(P, M, H);
+    uint16_t* ucache = reinterpret_cast<uint16_t*>(lds + L.ucache);
+    int* count = reinterpret_cast<int*>(lds + L.count);
+    int* rows = reinterpret_cast<int*>(lds + L.rows);
+    int* meta = reinterpret_cast<int*>(lds + L.meta);
+    float* red = reinterpret_cast<float*>(lds + L.red);
+    float* act = reinterpret_cast<float*>(lds + L.act);
+    const int j = find_row_tile(unit_idx, P, M, ucache, count, rows, meta);
+    if (j < 0) return;  // past the last tile (uniform)
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, g = lane >> 4;
+    const int sa = H + 1, tiles_h = (H + 63) / 64;
+    const int col = blockIdx.y * 16 + lr;
+    const T* W2j = W2 + int64_t(j) * H * d;
+    float wv[kOutGroup][16];
+    auto load_batch = [&](int base) {  // hidden tiles base + wave + 4 x (zeros past H)
+#pragma unroll
+        for (int x = 0; x < kOutGroup; ++x)
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const int h = (base + wave + 4 * x) * 64 + g * 16 + s;
+                wv[x][s] = col < d && h < H ? load_f32(W2j, int64_t(h) * d + col) : 0.0f;
+            }
+    };
+    load_batch(0);
+    {  // gelu(z1) of the tile's 16 pairs into LDS: 16 threads a row, each row's loads together
+        const int row = tid >> 4, c0 = tid & 15;
+        const int q = rows[row];
+        const T* hr = hidden + int64_t(q < 0 ? 0 : q) * H;
+        for (int cb = 0; cb < H; cb += 512) {
+            float z[32];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int c = cb + c0 + 16 * i;
+                z[i] = q >= 0 && c < H ? load_f32(hr, c) : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int c = cb + c0 + 16 * i;
+                if (c < H) act[row * sa + c] = q >= 0 ? gelu(z[i]) : 0.0f;
+            }
+        }
+    }
+    __syncthreads();  // act is in LDS
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int base = 0; base < tiles_h; base += 4 * kOutGroup) {
+        if (base > 0) load_batch(base);
+#pragma unroll
+        for (int x = 0; x < kOutGroup; ++x) {
+            const int h0 = (base + wave + 4 * x) * 64;
+            if (h0 < H) {  // uniform in the wavefront
+                const float* ar = act + lr * sa + h0 + g * 16;
+                float av[16];
+#pragma unroll
+                for (int s = 0; s < 16; ++s) av[s] = h0 + g * 16 + s < H ? ar[s] : 0.0f;
+#pragma unroll
+                for (int s = 0; s < 16; ++s) acc = mfma(av[s], wv[x][s], acc);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(wave * 16 + 4 * g + r) * 16 + lr] = acc[r];
+    __syncthreads();
+    if (wave == 0 && col < d) {
+        const float bias = load_f32(b2, int64_t(j) * d + col);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 4 * g + r, q = rows[row];
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) sum += red[(w * 16 + row) * 16 + lr];
+            if (q >= 0) store_f32(out, int64_t(q) * d + col, sum + bias);
         }
     }
 }
@@ -1386,6 +1498,29 @@ struct RunMlp {
                                    static_cast<const T*>(b2), static_cast<T*>(hidden),
                                    static_cast<T*>(out), P, M, d, H);
             };
+            const int olds = units::out_lds(P, M, H).bytes;
+            if (sizeof(T) == 4 && olds <= 160 * 1024) {
+                // fp32 storage: the hidden layer over (row tile, hidden tile) workgroups, then
+                // the second layer from the stored z1
+                auto kernel = H % 4 == 0 ? &units::mlp_fwd_tiles<T, true, true>
+                                         : &units::mlp_fwd_tiles<T, false, true>;
+                if (lds > 64 * 1024)
+                    HSN_HIP(allow_lds_raw(reinterpret_cast<const void*>(kernel), lds));
+                hipLaunchKernelGGL(kernel, dim3((P + 15) / 16 + M, (H + 63) / 64), dim3(256), lds,
+                                   st, static_cast<const T*>(v), idx, static_cast<const T*>(W1),
+                                   static_cast<const T*>(b1), static_cast<const T*>(W2),
+                                   static_cast<const T*>(b2), static_cast<T*>(hidden),
+                                   static_cast<T*>(out), P, M, d, H);
+                auto second = &units::mlp_out_tiles<T>;
+                if (olds > 64 * 1024)
+                    HSN_HIP(allow_lds_raw(reinterpret_cast<const void*>(second), olds));
+                hipLaunchKernelGGL(second, dim3((P + 15) / 16 + M, (d + 15) / 16), dim3(256), olds,
+                                   st, idx,
+                                   static_cast<const T*>(W2), static_cast<const T*>(b2),
+                                   static_cast<const T*>(hidden), static_cast<T*>(out), P, M, d,
+                                   H);
+                return;
+            }
             if (H % 4 == 0) launch(&units::mlp_fwd_tiles<T, true>);
             else launch(&units::mlp_fwd_tiles<T, false>);
             return;
