@@ -594,18 +594,63 @@ __global__ __launch_bounds__(256) void mlp_dw(const T* v, const int32_t* unit_id
     for (int t = 0; t < kMaxD16; ++t) gw2[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     float gb1 = 0.0f;  // thread tid < 64: column h0 + tid
     float gb2[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // first workgroup: columns tid + 256 u
+    // each pair's unit in LDS (P <= kDwCache), so a chunk's scan reads no global memory
+    constexpr int kDwCache = 16384;
+    __shared__ uint16_t ucache[kDwCache];
+    const bool cached = P <= kDwCache;
+    if (cached) {
+        for (int q0 = 0; q0 < P; q0 += 256 * 8) {
+            int uu[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int q = q0 + tid + 256 * i;
+                uu[i] = q < P ? unit_idx[q] : -1;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int q = q0 + tid + 256 * i;
+                if (q < P)
+                    ucache[q] = uu[i] >= 0 && uu[i] < 0xffff ? static_cast<uint16_t>(uu[i])
+                                                             : static_cast<uint16_t>(0xffff);
+            }
+        }
+    }
+    __syncthreads();
+    // the unit's next 16 pairs from `at` on, in pair order (next_pairs over the LDS copy)
+    auto next = [&](int& at) -> Chunk {
+        int n = 0, row = -1;
+        while (n < 16 && at < P) {
+            const int p = at + lane;
+            const bool hit = p < P && (cached ? int(ucache[p]) == j : unit_idx[p] == j);
+            uint64_t m = ballot(hit);
+            int last = -1;
+            while (m != 0ull && n < 16) {
+                const int bit = __builtin_ctzll(m);
+                m &= m - 1ull;
+                if (lane == n) row = at + bit;
+                ++n;
+                last = bit;
+            }
+            at = m != 0ull ? at + last + 1 : at + 64;  // stopped early: resume after the last taken
+        }
+        return Chunk{n, row};
+    };
     int cur = 0;
     const int hw = h0 + 16 * w + lr;  // the wavefront's hidden column for dz
     const bool hwin = hw < H;
     const T* w2h = W2j + int64_t(hwin ? hw : 0) * d;
     const int kr = tid >> 4, kc = tid & 15;  // the thread's row and column phase when staging
-    for (;;) {
-        const Chunk c = next_pairs(unit_idx, P, j, cur);
-        if (c.n == 0) break;
-        // every load of the chunk in one batch: the pairs' grad_out rows and v's 64 inputs (for
-        // LDS), W2's columns (dz's B operand) and z1 of the wavefront's rows
+    float b[16];  // dz's B operand W2[j][h][k] for k < 64: the same for every chunk
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int k = 4 * u + lq;
+        b[u] = hwin && k < d ? load_f32(w2h, k) : 0.0f;
+    }
+    // a chunk's loads in one batch: its pairs' grad_out rows and v's 64 inputs (for LDS), z1 of
+    // the wavefront's rows; the next chunk's batch is issued before this chunk's products
+    float gr[16], vr[4], z[4];
+    auto load_chunk = [&](const Chunk& c) {
         const int pr = pair_of(c, kr);
-        float gr[16], vr[4], b[16], z[4];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int o = kc + 16 * i;
@@ -617,15 +662,15 @@ __global__ __launch_bounds__(256) void mlp_dw(const T* v, const int32_t* unit_id
             vr[i] = pr >= 0 && x < in ? load_f32(v, int64_t(pr) * in + x) : 0.0f;
         }
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int k = 4 * u + lq;
-            b[u] = hwin && k < d ? load_f32(w2h, k) : 0.0f;
-        }
-#pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int p = pair_of(c, 4 * lq + r);
             z[r] = p >= 0 && hwin ? load_f32(hidden, int64_t(p) * H + hw) : 0.0f;
         }
+    };
+    Chunk c = next(cur);
+    if (c.n > 0) load_chunk(c);
+    while (c.n > 0) {  // uniform
+        const Chunk cn = next(cur);
         __syncthreads();  // the last chunk's reads of the tiles are done
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -634,6 +679,10 @@ __global__ __launch_bounds__(256) void mlp_dw(const T* v, const int32_t* unit_id
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) vs[kr][kc + 16 * i] = vr[i];
+        float zc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) zc[r] = z[r];
+        if (cn.n > 0) load_chunk(cn);  // uniform
         __syncthreads();
         // dz1 = (grad_out W2[j]^T) * gelu'(z1): A[pair][k] = grad_out rows (LDS), B[k][h] = W2
         v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -654,14 +703,14 @@ __global__ __launch_bounds__(256) void mlp_dw(const T* v, const int32_t* unit_id
         for (int r = 0; r < 4; ++r) {
             const int row = 4 * lq + r;
             const bool ok = pair_of(c, row) >= 0 && hwin;
-            dz[row][16 * w + lr] = ok ? acc[r] * gelu_grad(z[r]) : 0.0f;
-            if (first_in) act[row][16 * w + lr] = ok ? gelu(z[r]) : 0.0f;
+            dz[row][16 * w + lr] = ok ? acc[r] * gelu_grad(zc[r]) : 0.0f;
+            if (first_in) act[row][16 * w + lr] = ok ? gelu(zc[r]) : 0.0f;
         }
         __syncthreads();
         // grad_W1[i][h] += sum_k v[p_k][i] dz[k][h]: A = v^T (rows i, k = pairs), B = dz
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int k = 4 * s + lq;  // the pair
+        for (int s2 = 0; s2 < 4; ++s2) {
+            const int k = 4 * s2 + lq;  // the pair
             const float bv = dz[k][16 * w + lr];
 #pragma unroll
             for (int t = 0; t < 4; ++t) gw1[t] = mfma(vs[k][16 * t + lr], bv, gw1[t]);
@@ -669,8 +718,8 @@ __global__ __launch_bounds__(256) void mlp_dw(const T* v, const int32_t* unit_id
         if (first_in) {
             // grad_W2[h][o] += sum_k gelu(z1)[k][h] grad_out[p_k][o]: A = act^T, B = grad_out
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int k = 4 * s + lq;
+            for (int s2 = 0; s2 < 4; ++s2) {
+                const int k = 4 * s2 + lq;
                 const float av = act[k][16 * w + lr];
 #pragma unroll
                 for (int t = 0; t < kMaxD16; ++t) {
@@ -691,6 +740,7 @@ __global__ __launch_bounds__(256) void mlp_dw(const T* v, const int32_t* unit_id
                 }
             }
         }
+        c = cn;
     }
     const int h = h0 + 16 * w + lr;
 #pragma unroll
