@@ -562,6 +562,181 @@ __global__ __launch_bounds__(256) void mlp_out_tiles(const int32_t* unit_idx, co
     }
 }
 
+// The backward's grad_v in two launches when dz1 has fp32 room (the caller's grad_W2, written only
+// afterwards): mlp_dz_tiles stores dz1 = (grad_out W2[j]^T) * gelu'(z1) for (row tile, 64 hidden
+// columns) workgroups, then mlp_gv_tiles forms grad_v = dz1 W1[j]^T for (row tile, 16 inputs)
+// workgroups, the hidden tiles split over the wavefronts and summed in wavefront order.
+struct DzLds {
+    int ucache, count, rows, meta, go, bytes;
+};
+__host__ __device__ inline DzLds dz_lds(int P, int M, int d) {
+    DzLds L;
+    L.ucache = 0;                                   // uint16 [P]
+    L.count = (2 * P + 15) / 16 * 16;               // int [M]
+    L.rows = L.count + (4 * M + 15) / 16 * 16;      // int [16]
+    L.meta = L.rows + 64;                           // int [4]
+    L.go = L.meta + 16;                             // float [16][d]: the rows' grad_out
+    L.bytes = L.go + 4 * 16 * d;
+    return L;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void mlp_dz_tiles(const int32_t* unit_idx, const T* W2,
+                                                    const T* hidden, const T* grad_out, float* dz,
+                                                    int P, int M, int d, int H) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const DzLds L = dz_lds(P, M, d);
+    uint16_t* ucache = reinterpret_cast<uint16_t*>(lds + L.ucache);
+    int* count = reinterpret_cast<int*>(lds + L.count);
+    int* rows = reinterpret_cast<int*>(lds + L.rows);
+    int* meta = reinterpret_cast<int*>(lds + L.meta);
+    float* go = reinterpret_cast<float*>(lds + L.go);
+    const int j = find_row_tile(unit_idx, P, M, ucache, count, rows, meta);
+    if (j < 0) return;  // past the last tile (uniform)
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, g = lane >> 4;
+    const int h = blockIdx.y * 64 + 16 * wave + lr;
+    const bool hin = h < H;
+    const T* w2h = W2 + (int64_t(j) * H + (hin ? h : 0)) * d;  // B[k][h] = W2[j][h][k]
+    float b[16], z[4];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int k = 4 * u + g;
+        b[u] = hin && k < d ? load_f32(w2h, k) : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int q = rows[4 * g + r];
+        z[r] = q >= 0 && hin ? load_f32(hidden, int64_t(q) * H + h) : 0.0f;
+    }
+    {  // the rows' grad_out into LDS, 16 threads a row
+        const int row = tid >> 4, c0 = tid & 15, q = rows[row];
+        float gr[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int c = c0 + 16 * i;
+            gr[i] = q >= 0 && c < d ? load_f32(grad_out, int64_t(q) * d + c) : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (c0 + 16 * i < d) go[row * d + c0 + 16 * i] = gr[i];
+    }
+    __syncthreads();
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        const int k = 4 * u + g;
+        acc = mfma(k < d ? go[lr * d + k] : 0.0f, b[u], acc);
+    }
+    for (int k0 = 64; k0 < d; k0 += 64) {
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int k = k0 + 4 * u + g;
+            acc = mfma(k < d ? go[lr * d + k] : 0.0f, hin && k < d ? load_f32(w2h, k) : 0.0f, acc);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int q = rows[4 * g + r];
+        if (q >= 0 && hin) dz[int64_t(q) * H + h] = acc[r] * gelu_grad(z[r]);
+    }
+}
+
+struct GvLds {
+    int ucache, count, rows, meta, red, dz, bytes;
+};
+__host__ __device__ inline GvLds gv_lds(int P, int M, int H) {
+    GvLds L;
+    L.ucache = 0;                                   // uint16 [P]
+    L.count = (2 * P + 15) / 16 * 16;               // int [M]
+    L.rows = L.count + (4 * M + 15) / 16 * 16;      // int [16]
+    L.meta = L.rows + 64;                           // int [4]
+    L.red = L.meta + 16;                            // float [4][16][16]
+    L.dz = L.red + 4 * 4 * 16 * 16;                 // float [16][H + 1]
+    L.bytes = L.dz + 4 * 16 * (H + 1);
+    return L;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void mlp_gv_tiles(const int32_t* unit_idx, const T* W1,
+                                                    const float* dz, T* grad_v, int P, int M,
+                                                    int d, int H) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const GvLds L = gv_lds(P, M, H);
+    uint16_t* ucache = reinterpret_cast<uint16_t*>(lds + L.ucache);
+    int* count = reinterpret_cast<int*>(lds + L.count);
+    int* rows = reinterpret_cast<int*>(lds + L.rows);
+    int* meta = reinterpret_cast<int*>(lds + L.meta);
+    float* red = reinterpret_cast<float*>(lds + L.red);
+    float* dzs = reinterpret_cast<float*>(lds + L.dz);
+    const int j = find_row_tile(unit_idx, P, M, ucache, count, rows, meta);
+    if (j < 0) return;  // past the last tile (uniform)
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, g = lane >> 4;
+    const int n = 4 * d, sa = H + 1, tiles_h = (H + 63) / 64;
+    const int i = blockIdx.y * 16 + lr;  // the input column
+    const T* w1i = W1 + (int64_t(j) * n + (i < n ? i : 0)) * H;  // B[k][i] = W1[j][i][h]
+    const bool al = (H % 4) == 0 && (reinterpret_cast<uintptr_t>(W1) & (4 * sizeof(T) - 1)) == 0;
+    float wv[kOutGroup][16];
+    auto load_batch = [&](int base) {  // hidden tiles base + wave + 4 x (zeros past H)
+#pragma unroll
+        for (int x = 0; x < kOutGroup; ++x)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int h = (base + wave + 4 * x) * 64 + g * 16 + 4 * q4;
+                const float4 t = i < n ? row4w(w1i, h, H, al) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                wv[x][4 * q4] = t.x, wv[x][4 * q4 + 1] = t.y, wv[x][4 * q4 + 2] = t.z,
+                wv[x][4 * q4 + 3] = t.w;
+            }
+    };
+    load_batch(0);
+    {  // the rows' dz1 into LDS: 16 threads a row, each row's loads together
+        const int row = tid >> 4, c0 = tid & 15, q = rows[row];
+        const float* zr = dz + int64_t(q < 0 ? 0 : q) * H;
+        for (int cb = 0; cb < H; cb += 512) {
+            float zz[32];
+#pragma unroll
+            for (int x = 0; x < 32; ++x) {
+                const int c = cb + c0 + 16 * x;
+                zz[x] = q >= 0 && c < H ? zr[c] : 0.0f;
+            }
+#pragma unroll
+            for (int x = 0; x < 32; ++x) {
+                const int c = cb + c0 + 16 * x;
+                if (c < H) dzs[row * sa + c] = zz[x];
+            }
+        }
+    }
+    __syncthreads();
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int base = 0; base < tiles_h; base += 4 * kOutGroup) {
+        if (base > 0) load_batch(base);
+#pragma unroll
+        for (int x = 0; x < kOutGroup; ++x) {
+            const int h0 = (base + wave + 4 * x) * 64;
+            if (h0 < H) {  // uniform in the wavefront
+                const float* ar = dzs + lr * sa + h0 + g * 16;
+                float av[16];
+#pragma unroll
+                for (int s2 = 0; s2 < 16; ++s2) av[s2] = h0 + g * 16 + s2 < H ? ar[s2] : 0.0f;
+#pragma unroll
+                for (int s2 = 0; s2 < 16; ++s2) acc = mfma(av[s2], wv[x][s2], acc);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(wave * 16 + 4 * g + r) * 16 + lr] = acc[r];
+    __syncthreads();
+    if (wave == 0 && i < n) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 4 * g + r, q = rows[row];
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) sum += red[(w * 16 + row) * 16 + lr];
+            if (q >= 0) store_f32(grad_v, int64_t(q) * n + i, sum);
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------
 // grouped_unit_mlp backward
 // ------------------------------------------------------------------------------------------
@@ -1589,6 +1764,32 @@ struct RunMlpBwd {
     static void run(const void* v, const int32_t* idx, const void* W1, const void* W2,
                     const void* hidden, const void* dout, void* dv, void* dW1, void* db1,
                     void* dW2, void* db2, int P, int M, int d, int H, hipStream_t st) {
+        // grad_v through dz1 in fp32 in grad_W2's memory (4-byte aligned, P H floats of room),
+        // before the weight-gradient kernel writes grad_W2
+        const int dzl = units::dz_lds(P, M, d).bytes, gvl = units::gv_lds(P, M, H).bytes;
+        if (d % 4 == 0 && P <= units::kTileMaxSlots && M <= units::kTileMaxUnits &&
+            reinterpret_cast<uintptr_t>(dW2) % 4 == 0 &&
+            int64_t(M) * H * d * int64_t(sizeof(T)) >= int64_t(P) * H * 4 && dzl <= 160 * 1024 &&
+            gvl <= 160 * 1024) {
+            float* dz = static_cast<float*>(dW2);
+            auto k1 = &units::mlp_dz_tiles<T>;
+            if (dzl > 64 * 1024) HSN_HIP(allow_lds_raw(reinterpret_cast<const void*>(k1), dzl));
+            hipLaunchKernelGGL(k1, dim3((P + 15) / 16 + M, (H + 63) / 64), dim3(256), dzl, st, idx,
+                               static_cast<const T*>(W2), static_cast<const T*>(hidden),
+                               static_cast<const T*>(dout), dz, P, M, d, H);
+            auto k2 = &units::mlp_gv_tiles<T>;
+            if (gvl > 64 * 1024) HSN_HIP(allow_lds_raw(reinterpret_cast<const void*>(k2), gvl));
+            hipLaunchKernelGGL(k2, dim3((P + 15) / 16 + M, (4 * d + 15) / 16), dim3(256), gvl, st,
+                               idx, static_cast<const T*>(W1), static_cast<const float*>(dz),
+                               static_cast<T*>(dv), P, M, d, H);
+            hipLaunchKernelGGL((units::mlp_dw<T>), dim3((H + 63) / 64, M, (4 * d + 63) / 64),
+                               dim3(256), 0, st, static_cast<const T*>(v), idx,
+                               static_cast<const T*>(W2), static_cast<const T*>(hidden),
+                               static_cast<const T*>(dout), static_cast<T*>(dW1),
+                               static_cast<T*>(db1), static_cast<T*>(dW2), static_cast<T*>(db2),
+                               P, d, H);
+            return;
+        }
         hipLaunchKernelGGL((units::mlp_dw<T>), dim3((H + 63) / 64, M, (4 * d + 63) / 64),
                            dim3(256), 0, st, static_cast<const T*>(v), idx,
                            static_cast<const T*>(W2), static_cast<const T*>(hidden),

@@ -321,6 +321,7 @@ def test_unit_mlp_and_messages_are_reproducible(ops, cuda_device):
     (64, 4, 16, 77),     # H not a multiple of 4: the row-tile kernel's unaligned loads
     (20000, 2, 4, 8),    # more pairs than the row-tile kernel's slot table: the scanning kernel
     (300, 6, 64, 512),   # the reference model's widths, several tiles a unit
+    (2000, 2, 8, 64),    # grad_W2 too small to hold dz1: grad_v in one launch
 ])
 def test_unit_mlp_forward_paths_match_oracle(ops, cuda_device, P, M, d, H):
     """Both forward kernels and both grad_v kernels (by row tiles, and the pair-scanning ones for
