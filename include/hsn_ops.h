@@ -69,8 +69,10 @@ int hsn_grouped_unit_mlp_fwd(const void* v, const int32_t* unit_idx, const void*
  *   dz1 = (grad_out W2[j]^T) * gelu'(z1); grad_v = dz1 W1[j]^T;
  *   grad_W1[j] = sum_p v^T dz1, grad_b1[j] = sum_p dz1; grad_W2[j] = sum_p gelu(z1)^T grad_out,
  *   grad_b2[j] = sum_p grad_out; units without a pair get zeros.
- * dz1 is recomputed where it is consumed (the ABI has no workspace); every sum has a fixed
- * order, so `deterministic` holds either way.
+ * The ABI has no workspace: grad_v's dz1 is kept in fp32 in grad_W2's memory when it has room
+ * (P H floats), before grad_W2 is written, and is recomputed where it is consumed otherwise.
+ * So grad_W2 must not overlap any input. Every sum has a fixed order, so `deterministic` holds
+ * either way.
  */
 int hsn_grouped_unit_mlp_bwd(const void* v, const int32_t* unit_idx, const void* W1,
                              const void* W2, const void* hidden_saved, const void* grad_out,
