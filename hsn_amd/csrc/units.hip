@@ -1427,6 +1427,14 @@ __global__ __launch_bounds__(256) void csr_dh_rows(const Csr g, const T* a, cons
     float* gs = acc + 64 * 64;  // [K][64 rows o]
     const int r = blockIdx.x, c0 = blockIdx.y * 64, n0 = blockIdx.z * 128;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the first block of V's rows and of grad_m's values in flight during the slots' scan
+    float vpre[16], gpre[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int x = tid + 256 * i, oo = x >> 6, cc = x & 63;
+        vpre[i] = oo < d && c0 + cc < d ? load_f32(V, int64_t(oo) * d + c0 + cc) : 0.0f;
+        gpre[i] = x < K * 64 && cc < d ? load_f32(grad_m, (int64_t(r) * K + oo) * d + cc) : 0.0f;
+    }
     // the slots' edge ranges and their offsets in the list (an inclusive scan in wavefront 0)
     if (wave == 0) {
         int e0 = 0, e1 = 0;
@@ -1446,14 +1454,24 @@ __global__ __launch_bounds__(256) void csr_dh_rows(const Csr g, const T* a, cons
     for (int x = tid; x < K * 64; x += 256) u[x] = 0.0f;
     for (int o0 = 0; o0 < d; o0 += 64) {
         __syncthreads();
+        if (o0 == 0) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int x = tid + 256 * i, oo = x >> 6, cc = x & 63;
-            Vs[x] = o0 + oo < d && c0 + cc < d ? load_f32(V, int64_t(o0 + oo) * d + c0 + cc) : 0.0f;
-        }
-        for (int x = tid; x < K * 64; x += 256) {
-            const int k = x >> 6, oo = x & 63;
-            gs[x] = o0 + oo < d ? load_f32(grad_m, (int64_t(r) * K + k) * d + o0 + oo) : 0.0f;
+            for (int i = 0; i < 16; ++i) {
+                const int x = tid + 256 * i;
+                Vs[x] = vpre[i];
+                if (x < K * 64) gs[x] = gpre[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int x = tid + 256 * i, oo = x >> 6, cc = x & 63;
+                Vs[x] = o0 + oo < d && c0 + cc < d ? load_f32(V, int64_t(o0 + oo) * d + c0 + cc)
+                                                   : 0.0f;
+            }
+            for (int x = tid; x < K * 64; x += 256) {
+                const int k = x >> 6, oo = x & 63;
+                gs[x] = o0 + oo < d ? load_f32(grad_m, (int64_t(r) * K + k) * d + o0 + oo) : 0.0f;
+            }
         }
         __syncthreads();
         for (int x = tid; x < K * 64; x += 256) {  // the same thread owns u[x] every block
@@ -1486,9 +1504,19 @@ __global__ __launch_bounds__(256) void csr_dh_rows(const Csr g, const T* a, cons
             lslot[x] = klo;
         }
         __syncthreads();
-        for (int i = 0; i < cnt; ++i) {  // uniform test
-            const int src = lsrc[i];
-            if (src >= lo && src < hi) acc[(src - n0) * 64 + lane] += lw[i] * u[lslot[i] * 64 + lane];
+        for (int i0 = 0; i0 < cnt; i0 += 64) {  // 64 entries a lane, broadcast in order
+            const int m = min(64, cnt - i0);
+            const int my_src = lane < m ? lsrc[i0 + lane] : -1;
+            const int my_w = lane < m ? __float_as_int(lw[i0 + lane]) : 0;
+            const int my_slot = lane < m ? lslot[i0 + lane] : 0;
+            for (int t = 0; t < m; ++t) {
+                const int src = __builtin_amdgcn_readlane(my_src, t);
+                if (src >= lo && src < hi) {  // uniform
+                    const float wt = __int_as_float(__builtin_amdgcn_readlane(my_w, t));
+                    const int sl = __builtin_amdgcn_readlane(my_slot, t);
+                    acc[(src - n0) * 64 + lane] += wt * u[sl * 64 + lane];
+                }
+            }
         }
     }
     const int c = c0 + lane;
