@@ -150,14 +150,41 @@ __global__ __launch_bounds__(256) void gather_bwd(const F* grad_v, const int32_t
     const int r = static_cast<int>(e / d), x = static_cast<int>(e - int64_t(r) * d);
     const int64_t w = 4 * int64_t(d);
     float su = 0.0f, se = 0.0f;
-    for (int k = 0; k < K; ++k) {  // slot order: repeats of one cell add in that order
-        const int64_t s = int64_t(r) * K + k;
-        const F* gv = grad_v + s * w;
-        su += to_f32(gv[x]);
-        se += to_f32(gv[d + x]);
-        const int64_t hi = (int64_t(r) * N + cell_idx[s]) * d + x;
-        grad_h[hi] = from_f32<F>(to_f32(grad_h[hi]) + to_f32(gv[2 * d + x]));
-        grad_m[s * d + x] = gv[3 * d + x];
+    // slot order, 8 slots at a time: the batch's cells and grad_v values, then its reads of
+    // grad_h, are issued together; repeats of one cell add in slot order, a repeat inside the
+    // batch taking the earlier slot's stored sum
+    constexpr int G = 8;
+    for (int k0 = 0; k0 < K; k0 += G) {
+        int64_t hi[G];
+        float gu[G], ge[G], gh[G], old[G], stored[G];
+        F gm[G];
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const int64_t s = int64_t(r) * K + min(k0 + i, K - 1);
+            const F* gv = grad_v + s * w;
+            hi[i] = (int64_t(r) * N + cell_idx[s]) * d + x;
+            gu[i] = to_f32(gv[x]);
+            ge[i] = to_f32(gv[d + x]);
+            gh[i] = to_f32(gv[2 * d + x]);
+            gm[i] = gv[3 * d + x];
+        }
+#pragma unroll
+        for (int i = 0; i < G; ++i) old[i] = k0 + i < K ? to_f32(grad_h[hi[i]]) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            stored[i] = 0.0f;
+            if (k0 + i >= K) continue;
+            su += gu[i];
+            se += ge[i];
+            float prev = old[i];
+#pragma unroll
+            for (int t = 0; t < i; ++t)
+                if (hi[t] == hi[i]) prev = stored[t];  // the latest earlier slot of the batch
+            const F st = from_f32<F>(prev + gh[i]);
+            stored[i] = to_f32(st);
+            grad_h[hi[i]] = st;
+            grad_m[(int64_t(r) * K + k0 + i) * d + x] = gm[i];
+        }
     }
     grad_u[int64_t(r) * d + x] = from_f32<F>(su);
     grad_eps[int64_t(r) * d + x] = from_f32<F>(se);

@@ -88,6 +88,27 @@ def test_gather_concat_matches_golden(ops, cuda_device, size, dtype):
         _close(got, v[name], dtype, name)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gather_backward_slot_batches_match_oracle(ops, cuda_device, dtype):
+    """K = 19 slots, three of the kernel's batches of 8, with cells repeated inside a batch,
+    across batches and three times in a row: grad_h is the scatter-add of the slots' third
+    block, in slot order (the float64 oracle adds them in any order)."""
+    from oracle import hsn_oracle as O
+
+    g = torch.Generator().manual_seed(91)
+    B, N, K, d = 3, 30, 19, 36
+    grad_v = (torch.randn(B, K, 4 * d, generator=g) * 0.5).to(dtype)
+    cells = torch.randint(0, N, (B, K), generator=g, dtype=torch.int32)
+    cells[0, 5] = cells[0, 2]      # inside the first batch
+    cells[1, 17] = cells[1, 3]     # across batches
+    cells[2, [4, 9, 18]] = 7       # three batches
+    want = O.gather_concat_bwd(grad_v.double(), cells, N)
+    dev = cuda_device
+    got = ops.gather_concat_backward(grad_v.to(dev), cells.to(dev), N)
+    for name, g_, w_ in zip(("grad_u", "grad_eps", "grad_h", "grad_m"), got, want):
+        _close(g_, w_, dtype, name)
+
+
 def test_gather_autograd_matches_golden(ops, cuda_device):
     v = load_golden("odd_gather_concat.safetensors")
     D = _put(v, cuda_device, torch.float32)
