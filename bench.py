@@ -492,7 +492,9 @@ def _ops_main(args) -> int:
             for _ in range(max(1, args.warmup)):
                 fn()
             torch.cuda.synchronize()
-            for _ in range(args.steps // 8 + 8):
+            # one 256 MiB copy (about 100 us) a call queued ahead, so the host's dispatch of the
+            # calls (Python and the op wrappers, tens of us a call) ends before the device's work
+            for _ in range(args.steps + 8):
                 busy_dst.copy_(busy)
             ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             ev[0].record()
