@@ -41,7 +41,7 @@ def _args():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--config", default="ref")
     p.add_argument("--seed", type=int, default=1)
-    p.add_argument("--path", choices=["auto", "slice", "chain", "strip"], default="auto",
+    p.add_argument("--path", choices=["auto", "slice", "chain", "evmap"], default="auto",
                    help="the sweeps' design (auto: the library's choice by shape)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-h-max", action="store_true", help="do not produce the row maxima")

@@ -124,18 +124,20 @@ def unsupported(op: int, B: int, T: int, N: int, d: int, K: int) -> str | None:
     return lib.hsn_win_last_error().decode(errors="replace")
 
 
-PATHS = {"auto": 0, "slice": 1, "chain": 2, "strip": 3}
+PATHS = {"auto": 0, "slice": 1, "chain": 2, "evmap": 3}
 PATH_NAMES = {v: k for k, v in PATHS.items()}
 
 
 def set_path(path: str) -> None:
     """Fix the sweeps' design for later forward / backward calls of this process: ``"auto"``
-    (the default), ``"slice"`` (time-chunked slices in LDS) or ``"chain"`` (cell chains)."""
+    (the default), ``"slice"`` (time-chunked slices in LDS), ``"chain"`` (cell chains) or
+    ``"evmap"`` (time-chunked slices with event maps)."""
     call("hsn_win_set_path", PATHS[path])
 
 
 def path_for(op: int, B: int, T: int, N: int, d: int, K: int, io_code: int) -> str:
-    """The design a forward / backward call of this shape takes (``"slice"`` or ``"chain"``)."""
+    """The design a forward / backward call of this shape takes (``"slice"``, ``"chain"`` or
+    ``"evmap"``)."""
     out = ctypes.c_int(0)
     call("hsn_win_path", op, B, T, N, d, K, io_code, ctypes.byref(out))
     return PATH_NAMES[out.value]

@@ -5,6 +5,7 @@
 
 #include "abi_util.h"
 #include "chain.cuh"
+#include "evmap.cuh"
 #include "chain_host.h"
 
 namespace hsn {
@@ -65,19 +66,37 @@ bool chain_takes(int B, int T, int N, int d, int K, const char** why) {
     return r == nullptr;
 }
 
+bool evmap_takes(int op, int B, int T, int N, int d, int K, size_t elem, const char** why) {
+    (void)B;
+    const char* r = nullptr;
+    if (op != HSN_OP_FORWARD) r = "the event maps take the window forward only";
+    else if (elem != 4) r = "the event maps take fp32 rows only";
+    else if (d % evmap::kS != 0) r = "the event maps take d a multiple of 8";
+    else if (T > evmap::kChunks * evmap::kP) r = "the event maps take T <= 256";
+    else if (K > evmap::kK) r = "the event maps take K <= 8";
+    else if (evmap::fwd_layout(N).bytes > size_t(kLdsMax)) r = "the event maps' tables of N cells do not fit the LDS";
+    else if ((int64_t(T) + 32) * K * d * 4 >= (int64_t(1) << 31)) r = "the event maps take (T + 32) K d * 4 < 2^31 bytes a row";
+    if (r && why) *why = r;
+    return r == nullptr;
+}
+
 int choose_path(int op, int B, int T, int N, int d, int K, size_t elem) {
     const char* why_s = nullptr;
     const char* why_c = nullptr;
-    const char* why_p = nullptr;
+    const char* why_e = nullptr;
     const int setting = path_setting();
-    const bool any = setting == kPathAuto;
+    // the event maps have a forward only: a forced event-map setting leaves the backward to the
+    // automatic choice between the other two
+    const bool any = setting == kPathAuto || (setting == kPathEvmap && op != HSN_OP_FORWARD);
+    const bool e_ok = (setting == kPathAuto || setting == kPathEvmap) &&
+                      evmap_takes(op, B, T, N, d, K, elem, &why_e);
+    if (setting == kPathEvmap && op == HSN_OP_FORWARD && !e_ok)
+        throw AbiError{HSN_ERR_INVALID_ARGUMENT, std::string("(event-map path) ") + why_e};
+    // The event maps first where they take the shape: at B32 T256 N256 d64 K8 fp32 the forward
+    // moves its rows as two columns a lane with a chunk per half-wavefront (see evmap.cuh).
+    if (e_ok) return kPathEvmap;
     const bool s_ok = (any || setting == kPathSlice) && slice_takes(op, B, T, N, d, K, &why_s);
     const bool c_ok = (any || setting == kPathChain) && chain_takes(B, T, N, d, K, &why_c);
-    if (setting == kPathStrip) {  // the strips only where asked for (see below)
-        if (!strip_takes(op, B, T, N, d, K, &why_p))
-            throw AbiError{HSN_ERR_INVALID_ARGUMENT, std::string("(strip path) ") + why_p};
-        return kPathStrip;
-    }
     if (!s_ok && !c_ok) {
         std::string msg;
         if (setting == kPathSlice) msg = std::string("(slice path) ") + why_s;
@@ -87,18 +106,12 @@ int choose_path(int op, int B, int T, int N, int d, int K, size_t elem) {
     }
     if (!c_ok) return kPathSlice;
     if (!s_ok) return kPathChain;
-    // The strips are never the automatic choice: measured on MI355X at B32 T256 N256 d64 K8 fp32
-    // they take 30 + 35 us (forward + backward) against the slices' 30 + 29, and at B128 T128
-    // N512 d128 K8 fp32 0.44 ms against the chains' 0.31: their walk moves its bytes near the
-    // bandwidth the slices reach, but each of the 256 (one per CU) or more workgroups first builds
-    // the row's lists and afterwards sums and scans the row in LDS, phases that move no HBM bytes
-    // and run on every CU at once.
-    // Both slices and chains take it: the slices where a wavefront's piece of a slot row is a full 32-byte sector
-    // and the state slice (N * S words) leaves room for chunks of the row in LDS; the chains
-    // where the piece would be narrower (K large against d) or the slice large (N large). Measured
-    // on MI355X: slices at B32 T256 N256 d64 K8 fp32 (S 8, 68 against 95 us per step), chains at
-    // B64 T512 N1024 d64 K16 bf16 (S 4: 0.45 against 1.62 ms) and B128 T128 N512 d128 K8 fp32
-    // (S 8, N S 4096: 0.31 against 0.43 ms).
+    // Both slices and chains take it: the slices where a wavefront's piece of a slot row is a
+    // full 32-byte sector and the state slice (N * S words) leaves room for chunks of the row in
+    // LDS; the chains where the piece would be narrower (K large against d) or the slice large
+    // (N large). Measured on MI355X: slices at B32 T256 N256 d64 K8 fp32 (S 8, 68 against 95 us
+    // per step), chains at B64 T512 N1024 d64 K16 bf16 (S 4: 0.45 against 1.62 ms) and B128 T128
+    // N512 d128 K8 fp32 (S 8, N S 4096: 0.31 against 0.43 ms).
     Geometry g;
     const bool fwd = op == HSN_OP_FORWARD;
     if (fwd) choose_geometry(B, T, N, d, K, fwd_lds_bytes, g);
@@ -111,7 +124,7 @@ WorkspaceLayout workspace_layout(int op, int B, int T, int N, int d, int K, size
     WorkspaceLayout L;
     const int path = choose_path(op, B, T, N, d, K, elem);
     L.chain = path == kPathChain;
-    L.strip = path == kPathStrip;
+    L.evmap = path == kPathEvmap;
     const int64_t slots = int64_t(B) * T * K;
     size_t at = 0;
     if (L.chain) {
@@ -270,7 +283,7 @@ void chain_backward(const void* y, const void* gate_pre, const void* h_old, int 
 extern "C" int hsn_win_set_path(int path) {
     HSN_ABI_BEGIN
     HSN_REQUIRE(path == hsn::kPathAuto || path == hsn::kPathSlice || path == hsn::kPathChain ||
-                    path == hsn::kPathStrip,
+                    path == hsn::kPathEvmap,
                 HSN_ERR_INVALID_ARGUMENT, "hsn_win_set_path: path must be 0 (auto), 1, 2 or 3");
     hsn::set_path_setting(path);
     HSN_ABI_END

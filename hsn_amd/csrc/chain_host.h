@@ -1,6 +1,6 @@
 // The choice between the three sweep designs of the window (the time-chunked slices of
-// sweep.cuh, the cell chains of chain.cuh and the column strips of strip.cuh), the workspace each
-// entry point needs, and the chain and strip paths' launchers.
+// sweep.cuh, the cell chains of chain.cuh and the event-map slices of evmap.cuh), the workspace
+// each entry point needs, and the chain and event-map paths' launchers.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -9,14 +9,14 @@
 
 namespace hsn {
 
-enum PathCode : int { kPathAuto = 0, kPathSlice = 1, kPathChain = 2, kPathStrip = 3 };
+enum PathCode : int { kPathAuto = 0, kPathSlice = 1, kPathChain = 2, kPathEvmap = 3 };
 
 // The workspace of hsn_win_forward / hsn_win_backward, byte offsets into it (256-aligned):
 // the RMS candidate's normalised input (both paths), and on the chain path the row lists, the
 // per-position sums (the forward's D, the backward's share), the forward's fp32 per-slot deltas
 // (used with bf16 rows, or where the caller omits h_old or h_sel) and its per-group row maxima.
 struct WorkspaceLayout {
-    bool chain = false, strip = false;
+    bool chain = false, evmap = false;
     size_t ptr = 0, ev = 0, sum = 0, delta = 0, hmax = 0, rms = 0, bytes = 0;
 };
 
@@ -26,7 +26,7 @@ void set_path_setting(int path);
 // for the slices), with the reason when it does not.
 bool slice_takes(int op, int B, int T, int N, int d, int K, const char** why);
 bool chain_takes(int B, int T, int N, int d, int K, const char** why);
-bool strip_takes(int op, int B, int T, int N, int d, int K, const char** why);
+bool evmap_takes(int op, int B, int T, int N, int d, int K, size_t elem, const char** why);
 // The path hsn_win_forward / hsn_win_backward take (kPathSlice or kPathChain), or throws the
 // reason neither does.
 int choose_path(int op, int B, int T, int N, int d, int K, size_t elem);
@@ -47,16 +47,10 @@ void chain_backward(const void* y, const void* gate_pre, const void* h_old, int 
                     int T, int N, int d, int K, char* ws, const WorkspaceLayout& L,
                     hipStream_t st);
 
-void strip_forward(const void* y, const void* gate_pre, int io_dtype, const uint8_t* reset,
+void evmap_forward(const void* y, const void* gate_pre, const uint8_t* reset,
                    const int32_t* slots, const float* h0, const float* q0, const int64_t* age0,
                    const int64_t* pos0, void* q_pre, void* q_post, void* h_sel, void* h_old,
                    float* h_max, float* h_T, float* q_T, int64_t* age_T, int64_t* pos_T, int B,
                    int T, int N, int d, int K, hipStream_t st);
-
-void strip_backward(const void* y, const void* gate_pre, const void* h_old, int io_dtype,
-                    const int32_t* slots, const uint8_t* reset, const void* d_q_pre,
-                    const void* d_q_post, const void* d_h_sel, const float* d_h_T,
-                    const float* d_q_T, void* dy, void* dgate, float* d_h0, float* d_q0, int B,
-                    int T, int N, int d, int K, hipStream_t st);
 
 }  // namespace hsn

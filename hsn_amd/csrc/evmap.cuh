@@ -1,0 +1,625 @@
+// The window's forward sweep and backward recurrence as time-chunked slices with event maps.
+//
+// A workgroup owns (row b, a slice of 8 state columns) and the whole window. The window splits
+// into 16 chunks of P = ceil(T / 16) positions; each chunk belongs to a half-wavefront (32 lanes:
+// lane = 4 k + p, slot k of the position, column pair p of the slice, two fp32 columns a lane,
+// 8-byte loads and stores). The state recurrence is separable over columns and, for a fixed
+// chunk, affine in each cell's value at the chunk's start (h_end = alpha h_start + beta; a reset
+// zeroes both), so the kernel runs
+//   phase A  every half-wave loads its chunk, computes the activations and composes the maps of
+//            the cells its chunk touches,
+//   phase B  the workgroup walks every (cell, column pair) through the 16 chunks from h0: each
+//            touched chunk receives the cell's start value, the end state goes out, and the
+//            chunks' summary changes give every chunk its start q,
+//   phase C  every half-wave replays its chunk from those start values with the outputs.
+// Event maps. A chunk touches at most P K cells, so its maps live in a table of P K entries
+// instead of N: a cell's entry is the index i K + k of its first event in the chunk (position i,
+// slot k), found without a search: the chunk's half-wave writes every event's index into the
+// cell's byte of a [cell][chunk] table from the last position to the first, so the first
+// event's index is the one left (LDS executes one wave's accesses in order). The table's row of
+// a cell is its 16 chunks' entries, one 16-byte read in phase B.
+// The row maximum of |h| after each position is the larger of the chunk's untouched cells'
+// maximum at its start (fixed until a reset) and the current maxima of its touched cells, kept
+// per entry; the summary q needs no map: a chunk changes it by its cells' end - start over N
+// (after a reset: by their end), and the positions inside the chunk add their slots' deltas.
+#pragma once
+
+#include "sweep.cuh"
+
+namespace hsn {
+namespace evmap {
+
+constexpr int kS = 8;          // state columns per workgroup
+constexpr int kK = 8;          // slots per position, at most
+constexpr int kWaves = 8;      // wavefronts per workgroup
+constexpr int kChunks = 16;    // chunks per workgroup: two per wavefront
+constexpr int kP = 16;         // positions per chunk, at most (T <= 256)
+constexpr int kEv = kP * kK;   // event indices of a chunk
+constexpr int kConst = kEv;    // entry holding cell 0's value at the chunk's start
+constexpr int kDummy = kEv + 1;  // entry the padded and idle slots update, never read
+constexpr int kEnt = kEv + 2;  // entries of a chunk's table
+constexpr uint32_t kNone = 0xffu;
+constexpr uint32_t kEntBytes = kS * 4;                 // one entry's 8 columns
+constexpr uint32_t kMapBytes = 2u * kEnt * kEntBytes;  // a chunk's alpha and beta tables
+
+// LDS byte offsets: the chunks' maps [16][alpha, beta][kEnt][8] f32 (alpha becomes the entry's
+// value in phase C), the first-event table [N + 1][16] u8 (row N: where idle and padded slots
+// write), the entries' current maxima [16][kEnt] u32 (|h| bits), the ages' last selections
+// [N + 1] i32, per chunk its untouched cells' maximum and last reset, each chunk's summary map
+// q -> (reset ? 0 : q) + c ([16][8] c and [16] reset flags) and start q [16][8], and 8 bytes a
+// thread where a lane with nothing to store writes.
+struct Layout {
+    uint32_t maps, idx, cmx, last, umax, rlast, qmap, qreset, qstart, tdummy, bytes;
+};
+
+__host__ __device__ inline Layout fwd_layout(int N) {
+    Layout L{};
+    uint32_t at = 0;
+    L.maps = at;
+    at += kChunks * kMapBytes;
+    L.idx = at;
+    at += (uint32_t(N + 1) * kChunks + 15u) & ~15u;
+    L.cmx = at;
+    at += kChunks * kEnt * 4u;
+    L.last = at;
+    at += (uint32_t(N + 1) * 4u + 15u) & ~15u;
+    L.umax = at;
+    at += kChunks * 4u;
+    L.rlast = at;
+    at += kChunks * 4u;
+    L.qmap = at;
+    at += kChunks * kS * 4u;
+    L.qreset = at;
+    at += kChunks * 4u;
+    L.qstart = at;
+    at += kChunks * kS * 4u;
+    L.tdummy = at;
+    at += kWave * kWaves * 8u;
+    L.bytes = at;
+    return L;
+}
+
+__device__ __forceinline__ float2 ld2(rsrc_t r, uint32_t vo) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, vo, 0u, 0);
+    return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+}
+__device__ __forceinline__ void st2(float2 x, rsrc_t r, uint32_t vo) {
+    decltype(__builtin_amdgcn_raw_buffer_load_b64(r, 0u, 0u, 0)) v;
+    v[0] = __float_as_uint(x.x);
+    v[1] = __float_as_uint(x.y);
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, vo, 0u, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ T& lds_ref(unsigned char* lds, uint32_t byte) {
+    return *reinterpret_cast<T*>(lds + byte);
+}
+
+__device__ __forceinline__ uint32_t abs2_bits(float2 v) {
+    return umax(abs_bits(v.x), abs_bits(v.y));
+}
+
+// Sum with the lane m apart, the same column pair (m = 16, 8 or 4: a slot bit of the lane).
+template <int M>
+__device__ __forceinline__ float partner_f32(float v, int lane) {
+    if constexpr (M == 16) {
+        // the swap hands every lane {even row's value, odd row's value} of its row pair
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                       false, false);
+        return __uint_as_float((lane & 16) ? static_cast<uint32_t>(r[0]) : static_cast<uint32_t>(r[1]));
+    } else if constexpr (M == 8) {
+        return dpp_f32<dpp::kRor8>(v);
+    } else {
+        return __shfl_xor(v, M, kWave);
+    }
+}
+
+template <int M>
+__device__ __forceinline__ uint32_t partner_u32(uint32_t v, int lane) {
+    if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16) ? static_cast<uint32_t>(r[0]) : static_cast<uint32_t>(r[1]);
+    } else if constexpr (M == 8) {
+        return dpp_u32<dpp::kRor8>(v);
+    } else if constexpr (M == 4) {
+        // inside 8 lanes the half mirror pairs lane i with 7 - i: across bit 2, the same
+        // higher bits (what a maximum over the lanes needs; the columns do not matter here)
+        return dpp_u32<dpp::kHalfMirror>(v);
+    } else if constexpr (M == 2) {
+        return dpp_u32<dpp::kXor2>(v);
+    } else {
+        return dpp_u32<dpp::kXor1>(v);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Forward
+// ------------------------------------------------------------------------------------------
+
+// The forward's arguments: the window's tensors at their row starts (the kernel adds b times
+// the row size), 32-bit sizes, and the summary's 1/N (an exact product when N is a power of two).
+struct FwdEv {
+    const float* y;         // [B, T, K, d], also the gate's pre-activation g
+    const float* g;
+    const int32_t* slots;   // [B, T, K]: the cell, or -1 where padded
+    const uint8_t* reset;   // [B, T] or NULL
+    const float* h0;        // [B, N, d]
+    const float* q0;        // [B, d]
+    const int64_t* age0;    // [B, N]
+    const int64_t* pos0;    // [B]
+    float* q_pre;           // [B, T, d]
+    float* q_post;
+    float* h_sel;           // [B, T, K, d] (each may be NULL)
+    float* h_old;
+    float* h_max;           // [B, T], holding 0 on entry, or NULL
+    float* h_T;             // [B, N, d] or NULL
+    float* q_T;             // [B, d] or NULL
+    int64_t* age_T;         // [B, N] or NULL
+    int64_t* pos_T;         // [B] or NULL
+    int T, N, d, K, P;      // P: positions per chunk
+    DivN divn;
+};
+
+// A per-lane bit of a word as an all-ones or all-zero word: a mask for bitwise selects, so the
+// condition stays in a VGPR instead of a lane mask.
+__device__ __forceinline__ uint32_t bitmask_at(uint32_t word, int i) { return 0u - ((word >> i) & 1u); }
+__device__ __forceinline__ float and_f32(float v, uint32_t m) {
+    return __uint_as_float(__float_as_uint(v) & m);
+}
+__device__ __forceinline__ float sel_f32(uint32_t m, float x, float y) {  // m ? x : y, bitwise
+    return __uint_as_float((__float_as_uint(x) & m) | (__float_as_uint(y) & ~m));
+}
+// The maximum over lanes l, l ^ 16, l ^ 32, l ^ 48 (a cell's four column pairs in phase B).
+__device__ __forceinline__ uint32_t max_of_rows(uint32_t v) {
+    RowPair r = pair16(v);
+    v = umax(r.lo, r.hi);
+    r = pair32(v);
+    return umax(r.lo, r.hi);
+}
+
+template <typename IN>
+__global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
+    static_assert(sizeof(IN) == 4, "fp32 rows");
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int N = a.N, d = a.d, K = a.K, T = a.T;
+    const Layout Lo = fwd_layout(N);
+    const int lane = lane_id();
+    const int gl = threadIdx.x;
+    const int w = uniform(gl / kWave);
+    const int half = lane >> 5, hl = lane & 31;
+    const int ch = 2 * w + half;  // this half-wave's chunk
+    const int k = hl >> 2, cp = hl & 3;
+    int b, slice;
+    block_coords(b, slice);
+    const int P = a.P;
+    const int t0 = ch * P;
+    const int n = max(0, min(P, T - t0));  // positions of the chunk (uniform in the half)
+    const bool active = k < K;
+    const int col = slice * kS + 2 * cp;
+    const bool track_age = slice == 0 && a.age_T != nullptr;
+    const DivN divn = a.divn;
+
+    const uint32_t pos_bytes = uint32_t(K) * d * 4u;  // one position's slot rows
+    const size_t orow = size_t(b) * T * K * d;  // element offset of row b of [B, T, K, d]
+    const rsrc_t ry = make_rsrc(a.y + orow, uint32_t(T) * pos_bytes);
+    const rsrc_t rg = make_rsrc(a.g + orow, uint32_t(T) * pos_bytes);
+    const rsrc_t rc = make_rsrc(a.slots + size_t(b) * T * K, uint32_t(T) * K * 4u);
+    const rsrc_t rr = make_rsrc(a.reset ? a.reset + size_t(b) * T : nullptr, a.reset ? uint32_t(T) : 0u);
+    // a lane's piece of position i is vrow + i * pos_bytes: out of range (loads read zero, stores
+    // are dropped) for an idle lane (kOob) and for a position past the window (its offset is at
+    // least T * pos_bytes; the host keeps (T + 32) * pos_bytes < 2^31, so nothing wraps); a
+    // position past a short chunk (P < 16) reads the next chunk's data, which the chunk ignores,
+    // and its stores are sent out of range
+    const uint32_t vrow = (active ? uint32_t(k * d + col) * 4u : kOob) + uint32_t(t0) * pos_bytes;
+
+    // ---- phase B's first start values and the chunk's resets, loaded first --------------------
+    // phase B's threads: thread 2 c + q holds columns 4q .. 4q + 3 of cell c (+ 256 per pass)
+    const int bq = gl & 1;
+    const float* const h0_row = a.h0 + size_t(b) * N * d;
+    auto h0_at = [&](int cell) __attribute__((always_inline)) -> float4 {
+        return cell < N ? *reinterpret_cast<const float4*>(h0_row + int64_t(cell) * d + slice * kS + 4 * bq)
+                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    };
+    const float4 h0a = h0_at(gl >> 1);
+    const uint8_t rbyte = __builtin_amdgcn_raw_buffer_load_b8(rr, hl < n ? uint32_t(t0 + hl) : kOob, 0u, 0);
+
+    // ---- phase A: loads and activations, 8 positions ahead ------------------------------------
+    constexpr int kAhead = 8;
+    float2 yv[kP], gv[kP];
+    int32_t cv[kP];
+    auto fetch = [&](int i) __attribute__((always_inline)) {
+        const uint32_t vo = vrow + uint32_t(i) * pos_bytes;
+        yv[i] = ld2(ry, vo);
+        gv[i] = ld2(rg, vo);
+        cv[i] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+            rc, active ? uint32_t((t0 + i) * K + k) * 4u : kOob, 0u, 0));
+    };
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) fetch(i);
+
+    // the tables' initial values, while the loads are in flight
+    for (int e = gl; e < (N + 1) * kChunks / 4; e += kWave * kWaves)
+        lds_ref<uint32_t>(lds, Lo.idx + 4u * e) = e < N * kChunks / 4 ? 0xffffffffu : kDummy * 0x01010101u;
+    for (int e = gl; e < kChunks * kEnt; e += kWave * kWaves) lds_ref<uint32_t>(lds, Lo.cmx + 4u * e) = 0u;
+    if (gl < kChunks) lds_ref<uint32_t>(lds, Lo.umax + 4u * gl) = 0u;
+    if (gl < kChunks * kS) {  // the dummy entries hold the identity map (idle slots compose it)
+        const uint32_t at = Lo.maps + uint32_t(gl / kS) * kMapBytes + kDummy * kEntBytes + 4u * (gl % kS);
+        lds_ref<float>(lds, at) = 1.0f;
+        lds_ref<float>(lds, at + kEnt * kEntBytes) = 0.0f;
+    }
+    if (track_age)
+        for (int e = gl; e <= N; e += kWave * kWaves) lds_ref<int32_t>(lds, Lo.last + 4u * e) = -1;
+
+    float2 omb[kP], bcv[kP];
+    uint32_t vmask = 0u, pmask = 0u;  // valid and padded positions of this lane's slot
+#pragma unroll
+    for (int i = 0; i < kP; ++i) {
+        if (i + kAhead < kP) fetch(i + kAhead);
+        const int c = cv[i];
+        const bool inb = active && i < n;
+        const bool ok = inb && c >= 0;
+        const float b0 = fast_sigmoid(gv[i].x), b1 = fast_sigmoid(gv[i].y);
+        const float c0 = fast_tanh(yv[i].x), c1 = fast_tanh(yv[i].y);
+        omb[i] = ok ? make_float2(1.0f - b0, 1.0f - b1) : make_float2(1.0f, 1.0f);
+        bcv[i] = ok ? make_float2(b0 * c0, b1 * c1) : make_float2(0.0f, 0.0f);
+        vmask |= ok ? 1u << i : 0u;
+        pmask |= inb && c < 0 ? 1u << i : 0u;
+        cv[i] = ok ? c : N;  // the first-event table's row (N: the idle slots' row)
+    }
+    const uint32_t rmask = static_cast<uint32_t>(ballot(rbyte != 0) >> (32 * half));
+    __syncthreads();  // the tables are initialised
+
+    // first events: every event writes its index into its cell's byte of this chunk, latest
+    // position first, so each byte ends with the cell's first event; one lane a slot writes,
+    // the others into their own dummy byte; idle and padded slots read row N (kDummy)
+    unsigned char* const idx = lds + Lo.idx;
+    const uint32_t my_dummy = Lo.tdummy + 8u * uint32_t(gl);
+#pragma unroll
+    for (int i = kP - 1; i >= 0; --i)
+        lds[(vmask >> i) & 1u && cp == 0 ? Lo.idx + uint32_t(cv[i] * kChunks + ch) : my_dummy] =
+            static_cast<unsigned char>(i * kK + k);
+    uint32_t entw[kP / 4] = {};
+#pragma unroll
+    for (int i = 0; i < kP; ++i) entw[i / 4] |= uint32_t(idx[cv[i] * kChunks + ch]) << (8 * (i % 4));
+    auto ent = [&](int i) __attribute__((always_inline)) -> uint32_t {
+        return (entw[i / 4] >> (8 * (i % 4))) & 0xffu;
+    };
+    const uint32_t e0raw = idx[ch];  // cell 0's entry in this chunk
+    const uint32_t e0 = e0raw == kNone ? uint32_t(kConst) : e0raw;
+    // the entry a position's slot reads before its update: its own, or cell 0's if padded
+    uint32_t rentw[kP / 4] = {};
+#pragma unroll
+    for (int i = 0; i < kP; ++i) rentw[i / 4] |= ((pmask >> i) & 1u ? e0 : ent(i)) << (8 * (i % 4));
+    auto rent = [&](int i) __attribute__((always_inline)) -> uint32_t {
+        return (rentw[i / 4] >> (8 * (i % 4))) & 0xffu;
+    };
+    if (track_age && cp == 0)
+#pragma unroll
+        for (int i = 0; i < kP; ++i) atomicMax(&lds_ref<int32_t>(lds, Lo.last + 4u * cv[i]), t0 + i);
+    if (hl == 0) lds_ref<int32_t>(lds, Lo.rlast + 4u * ch) = rmask ? t0 + 31 - __builtin_clz(rmask) : -1;
+
+    const uint32_t cbase = Lo.maps + uint32_t(ch) * kMapBytes;
+    const uint32_t lofs = uint32_t(cp) * 8u;
+    auto al_at = [&](uint32_t e) __attribute__((always_inline)) -> float2& {
+        return lds_ref<float2>(lds, cbase + e * kEntBytes + lofs);
+    };
+    auto be_at = [&](uint32_t e) __attribute__((always_inline)) -> float2& {
+        return lds_ref<float2>(lds, cbase + kEnt * kEntBytes + e * kEntBytes + lofs);
+    };
+    // zero the maps (or values) of the entries below `e_end`, by the half-wave (a reset)
+    auto zero_entries = [&](int e_end, bool with_beta) __attribute__((always_inline)) {
+        for (int e = hl; e < e_end * 4; e += 32) {
+            const uint32_t at = cbase + uint32_t(e >> 2) * kEntBytes + uint32_t(e & 3) * 8u;
+            lds_ref<float2>(lds, at) = make_float2(0.0f, 0.0f);
+            if (with_beta) lds_ref<float2>(lds, at + kEnt * kEntBytes) = make_float2(0.0f, 0.0f);
+        }
+    };
+
+    // compose the chunk's maps: alpha' = (1 - b) alpha, beta' = (1 - b) beta + b c, an entry's
+    // first event starting from (1, 0), or (0, 0) after a reset in the chunk; a reset zeroes the
+    // entries created before it (idle and padded slots compose the identity on kDummy)
+    auto compose = [&](auto rs_c) __attribute__((always_inline)) {
+        constexpr bool kRs = decltype(rs_c)::value;
+        float ainit = 1.0f;
+#pragma unroll
+        for (int i = 0; i < kP; ++i) {
+            if (kRs && ((rmask >> i) & 1u)) {
+                zero_entries(i * kK, true);
+                ainit = 0.0f;
+            }
+            const uint32_t e = ent(i);
+            const bool first = e == uint32_t(i * kK + k);
+            const float2 al = al_at(e), be = be_at(e);
+            const float2 o = omb[i];
+            al_at(e) = make_float2(o.x * (first ? ainit : al.x), o.y * (first ? ainit : al.y));
+            be_at(e) = make_float2(o.x * (first ? 0.0f : be.x) + bcv[i].x,
+                                   o.y * (first ? 0.0f : be.y) + bcv[i].y);
+        }
+    };
+    const bool wave_rs = ballot(rmask != 0u) != 0u;
+    if (wave_rs) compose(std::true_type{});
+    else compose(std::false_type{});
+    __syncthreads();
+
+    // ---- phase B: every cell through the 16 chunks, two threads a cell -----------------------
+    {
+        uint32_t rflags = 0u;  // chunks with a reset
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j)
+            rflags |= lds_ref<int32_t>(lds, Lo.rlast + 4u * j) >= 0 ? 1u << j : 0u;
+        rflags = uniform(rflags);
+        uint32_t um[kChunks];  // the untouched cells' maxima over this thread's cells
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) um[j] = 0u;
+        float* const hT_row = a.h_T ? a.h_T + size_t(b) * N * d : nullptr;
+        const uint32_t qofs = uint32_t(bq) * 16u;  // the thread's half of an entry
+        for (int c0 = 0; c0 < N; c0 += kWave * kWaves / 2) {
+            const int cell = c0 + (gl >> 1);
+            const bool ok = cell < N;
+            float4 s = c0 == 0 ? h0a : h0_at(cell);
+            const uint4 iw = lds_ref<uint4>(lds, Lo.idx + uint32_t(ok ? cell : N) * kChunks);
+            const uint32_t words[4] = {ok ? iw.x : ~0u, ok ? iw.y : ~0u, ok ? iw.z : ~0u, ok ? iw.w : ~0u};
+#pragma unroll
+            for (int jh = 0; jh < kChunks; jh += kChunks / 4) {  // four chunks' reads at once
+                float4 al[kChunks / 4], be[kChunks / 4];
+#pragma unroll
+                for (int jj = 0; jj < kChunks / 4; ++jj) {
+                    const int j = jh + jj;
+                    const uint32_t ej = (words[j / 4] >> (8 * (j % 4))) & 0xffu;
+                    const uint32_t e = ej == kNone ? uint32_t(kDummy) : ej;  // the identity (1, 0)
+                    const uint32_t at = Lo.maps + uint32_t(j) * kMapBytes + e * kEntBytes + qofs;
+                    al[jj] = lds_ref<float4>(lds, at);
+                    be[jj] = lds_ref<float4>(lds, at + kEnt * kEntBytes);
+                }
+#pragma unroll
+                for (int jj = 0; jj < kChunks / 4; ++jj) {
+                    const int j = jh + jj;
+                    const uint32_t ej = (words[j / 4] >> (8 * (j % 4))) & 0xffu;
+                    const bool touched = ej != kNone;
+                    uint32_t m = umax(umax(abs_bits(s.x), abs_bits(s.y)), umax(abs_bits(s.z), abs_bits(s.w)));
+                    m = ok ? umax(m, dpp_u32<dpp::kXor1>(m)) : 0u;  // the cell's 8 columns
+                    const uint32_t jb = Lo.maps + uint32_t(j) * kMapBytes;
+                    // the entry's start value for the replay and its maximum; cell 0's start value
+                    // (padded slots read it where the chunk leaves cell 0 untouched)
+                    if (touched) {
+                        lds_ref<float4>(lds, jb + ej * kEntBytes + qofs) = s;
+                        if (bq == 0) lds_ref<uint32_t>(lds, Lo.cmx + 4u * (j * kEnt + ej)) = m;
+                    }
+                    if (cell == 0) lds_ref<float4>(lds, jb + kConst * kEntBytes + qofs) = s;
+                    um[j] = umax(um[j], touched ? 0u : m);
+                    // a chunk with a reset ends at beta whatever the start (not 0 * s: a NaN in
+                    // the start state must not cross the reset, as masked_fill); an untouched
+                    // cell's map is the dummy entry's identity (1, 0)
+                    if ((rflags >> j) & 1u) s = be[jj];
+                    else s = make_float4(al[jj].x * s.x + be[jj].x, al[jj].y * s.y + be[jj].y,
+                                         al[jj].z * s.z + be[jj].z, al[jj].w * s.w + be[jj].w);
+                }
+            }
+            if (ok && hT_row)
+                *reinterpret_cast<float4*>(hT_row + int64_t(cell) * d + slice * kS + 4 * bq) = s;
+        }
+        // the untouched cells' maxima: a max reduce-scatter over the wave (lane l ends with
+        // chunk l / 4), then one atomic a chunk and wave
+        const uint32_t mj = max_scatter<kChunks>(um, lane);
+        if ((lane & 3) == 0) atomicMax(&lds_ref<uint32_t>(lds, Lo.umax + 4u * uint32_t(lane >> 2)), mj);
+    }
+    if (track_age) {  // the ages and position at the window's end
+        int last_reset = -1;
+        for (int j = 0; j < kChunks; ++j) last_reset = max(last_reset, lds_ref<int32_t>(lds, Lo.rlast + 4u * j));
+        int64_t* const ageT_row = a.age_T + size_t(b) * N;
+        const int64_t* const age0_row = a.age0 + size_t(b) * N;
+        for (int c = gl; c < N; c += kWave * kWaves) {
+            const int ls = lds_ref<int32_t>(lds, Lo.last + 4u * c);
+            int64_t age;
+            if (ls >= 0 && ls >= last_reset) age = (T - 1) - ls;
+            else if (last_reset >= 0) age = T - last_reset;
+            else age = age0_row[c] + T;
+            ageT_row[c] = age;
+        }
+        if (a.pos_T && gl == 0) a.pos_T[b] = last_reset >= 0 ? int64_t(T - last_reset) : a.pos0[b] + T;
+    }
+    __syncthreads();
+
+    // ---- phase C: the replay -------------------------------------------------------------------
+    // b c moves to the chunk's beta table (free after phase B): 32 lanes x 16 positions x 8 bytes,
+    // the 4160 bytes of the table less 64, so the replay holds only 1 - b in registers
+    const uint32_t bc_base = cbase + kEnt * kEntBytes + uint32_t(hl) * 8u;
+#pragma unroll
+    for (int i = 0; i < kP; ++i) lds_ref<float2>(lds, bc_base + uint32_t(i) * 256u) = bcv[i];
+    const rsrc_t rho = make_rsrc(a.h_old ? a.h_old + orow : nullptr, a.h_old ? uint32_t(T) * pos_bytes : 0u);
+    const rsrc_t rhs = make_rsrc(a.h_sel ? a.h_sel + orow : nullptr, a.h_sel ? uint32_t(T) * pos_bytes : 0u);
+    const rsrc_t rqa = make_rsrc(a.q_pre ? a.q_pre + size_t(b) * T * d : nullptr, a.q_pre ? uint32_t(T) * d * 4u : 0u);
+    const rsrc_t rqb = make_rsrc(a.q_post ? a.q_post + size_t(b) * T * d : nullptr, a.q_post ? uint32_t(T) * d * 4u : 0u);
+    const uint32_t cmx_base = Lo.cmx + uint32_t(ch) * kEnt * 4u;
+    const bool wave_pad = ballot(pmask != 0u) != 0u;
+    uint32_t vrow_c = vrow;
+    asm volatile("" : "+v"(vrow_c));  // recomputed here, not held from phase A's loads
+    const uint32_t u = lds_ref<uint32_t>(lds, Lo.umax + 4u * ch);
+    const int first_reset = rmask ? __builtin_ctz(rmask) : 32;
+    const int g = hl >> 2;  // the lane group holding one position after the reductions
+    const uint32_t vq = uint32_t(col) * 4u;
+    // the summaries of the lane's positions g and 8 + g: D / N, the reset before it, the map of
+    // the half's earlier positions (rx ? 0 : q) + cx, and each half's whole map
+    float2 qc[2], qx[2], hc[2];
+    bool qr[2], qxr[2], hr[2];
+
+    // positions 8 H .. 8 H + 7: the steps, then each position's row maximum and summaries
+    auto eight = [&](auto rs_c, auto h_c) __attribute__((always_inline)) {
+        constexpr bool kRs = decltype(rs_c)::value;
+        constexpr int H = decltype(h_c)::value;
+        float2 dl[8];
+        uint32_t lmv[8];
+        // without a reset the next position's read goes out right after this position's write,
+        // ahead of the row-maximum bookkeeping (its entry may be the one just written: LDS keeps
+        // one wave's accesses in order)
+        float2 h = make_float2(0.0f, 0.0f), bc = h;
+        if (!kRs) {
+            h = al_at(rent(8 * H));
+            bc = lds_ref<float2>(lds, bc_base + uint32_t(8 * H) * 256u);
+        }
+#pragma unroll
+        for (int ii = 0; ii < 8; ++ii) {
+            const int i = 8 * H + ii;
+            if (kRs) {
+                if ((rmask >> i) & 1u) {  // every value of the chunk restarts at zero
+                    zero_entries(kEnt - 1, false);  // the entries and cell 0's start value
+                    for (int e = hl; e < kEnt; e += 32) lds_ref<uint32_t>(lds, cmx_base + 4u * e) = 0u;
+                }
+                h = al_at(rent(i));
+                bc = lds_ref<float2>(lds, bc_base + uint32_t(i) * 256u);
+            }
+            const uint32_t e = ent(i);
+            const float2 hn = make_float2(omb[i].x * h.x + bc.x, omb[i].y * h.y + bc.y);
+            al_at(e) = hn;
+            float2 hs = hn;
+            if (wave_pad) {  // a padded slot shows cell 0 after the position
+                const float2 c0 = al_at(e0);
+                const uint32_t pm = bitmask_at(pmask, i);
+                hs = make_float2(sel_f32(pm, c0.x, hn.x), sel_f32(pm, c0.y, hn.y));
+            }
+            const float2 hcur = h;
+            if (!kRs && ii + 1 < 8) {
+                h = al_at(rent(i + 1));
+                bc = lds_ref<float2>(lds, bc_base + uint32_t(i + 1) * 256u);
+            }
+            // past the chunk (P < 16): out of range, not the next chunk's rows
+            const uint32_t vo = i < n ? vrow_c + uint32_t(i) * pos_bytes : kOob;
+            st2(hcur, rho, vo);
+            st2(hs, rhs, vo);
+            const uint32_t vm = bitmask_at(vmask, i);
+            dl[ii] = make_float2(and_f32(hn.x - hcur.x, vm), and_f32(hn.y - hcur.y, vm));
+            const uint32_t mg = group_max<4>(abs2_bits(hn) & vm);
+            lds_ref<uint32_t>(lds, (vm & 1u) && cp == 0 ? cmx_base + 4u * e : my_dummy) = mg;
+            const uint32_t m0 = lds_ref<uint32_t>(lds, cmx_base + 4u * hl);
+            const uint32_t m1 = lds_ref<uint32_t>(lds, cmx_base + 4u * (hl + 32));
+            const uint32_t m2 = lds_ref<uint32_t>(lds, cmx_base + 4u * (hl + 64));
+            const uint32_t m3 = lds_ref<uint32_t>(lds, cmx_base + 4u * (hl + 96));
+            lmv[ii] = umax(umax(m0, m1), umax(m2, m3));
+        }
+        const int pos = 8 * H + g;
+        // the row maximum: a max reduce-scatter over the lane bits 4, 3, 2 (lane group g ends
+        // with position pos), then the group's four lanes, with the untouched cells' maximum
+        // until a reset
+        {
+            int cnt = 8;
+#pragma unroll
+            for (int m = 16; m >= 4; m >>= 1) {
+                const int h2 = cnt / 2;
+                const bool up = (hl & m) != 0;
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    if (ii < h2) {
+                        const uint32_t lo = lmv[ii], hi = lmv[h2 + ii];
+                        const uint32_t send = up ? lo : hi;
+                        uint32_t recv;
+                        if (m == 16) recv = partner_u32<16>(send, lane);
+                        else if (m == 8) recv = partner_u32<8>(send, lane);
+                        else recv = partner_u32<4>(send, lane);
+                        lmv[ii] = umax(up ? hi : lo, recv);
+                    }
+                }
+                cnt = h2;
+            }
+            uint32_t mx = lmv[0];
+            mx = umax(mx, partner_u32<2>(mx, lane));
+            mx = umax(mx, partner_u32<1>(mx, lane));
+            mx = umax(mx, pos < first_reset ? u : 0u);
+            if (a.h_max && (hl & 3) == 0 && pos < n)
+                atomicMax(reinterpret_cast<unsigned int*>(a.h_max + size_t(b) * T) + (t0 + pos), mx);
+        }
+        // the summaries: the slots' deltas summed by a reduce-scatter over the slot bits (lane
+        // group g ends with position pos, its column pair), then a scan of the positions' maps
+        // q -> (reset ? 0 : q) + D / N over the groups
+        {
+#pragma unroll
+            for (int m = 16; m >= 4; m >>= 1) {
+                const int h2 = m / 4;  // positions held before the step: 8, 4, 2
+                const bool up = (hl & m) != 0;
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    if (ii < h2) {
+                        const float2 lo = dl[ii], hi = dl[h2 + ii];
+                        const float2 send = up ? lo : hi;
+                        float rx, ry2;
+                        if (m == 16) rx = partner_f32<16>(send.x, lane), ry2 = partner_f32<16>(send.y, lane);
+                        else if (m == 8) rx = partner_f32<8>(send.x, lane), ry2 = partner_f32<8>(send.y, lane);
+                        else rx = partner_f32<4>(send.x, lane), ry2 = partner_f32<4>(send.y, lane);
+                        const float2 keep = up ? hi : lo;
+                        dl[ii] = make_float2(keep.x + rx, keep.y + ry2);
+                    }
+                }
+            }
+            const bool in = pos < n;
+            const float2 c = make_float2(divn(dl[0].x), divn(dl[0].y));
+            const bool r = in && ((rmask >> pos) & 1u);
+            bool rs = r;
+            float2 cg = in ? c : make_float2(0.0f, 0.0f);
+#pragma unroll
+            for (int sft = 1; sft < 8; sft <<= 1) {  // inclusive scan over the groups 0..g
+                const float px = __shfl_up(cg.x, 4 * sft, kWave), py = __shfl_up(cg.y, 4 * sft, kWave);
+                const int pr = __shfl_up(rs ? 1 : 0, 4 * sft, kWave);
+                if (g >= sft) {
+                    cg = rs ? cg : make_float2(px + cg.x, py + cg.y);
+                    rs = rs || pr != 0;
+                }
+            }
+            float cx = __shfl_up(cg.x, 4, kWave), cy = __shfl_up(cg.y, 4, kWave);
+            int rx = __shfl_up(rs ? 1 : 0, 4, kWave);
+            if (g == 0) cx = cy = 0.0f, rx = 0;
+            qc[H] = c, qr[H] = r, qx[H] = make_float2(cx, cy), qxr[H] = rx != 0;
+            const int src = (lane & 32) | (28 + cp);  // group 7: the half's whole map
+            hc[H] = make_float2(__shfl(cg.x, src, kWave), __shfl(cg.y, src, kWave));
+            hr[H] = __shfl(rs ? 1 : 0, src, kWave) != 0;
+        }
+    };
+    if (wave_rs) {
+        eight(std::true_type{}, std::integral_constant<int, 0>{});
+        eight(std::true_type{}, std::integral_constant<int, 1>{});
+    } else {
+        eight(std::false_type{}, std::integral_constant<int, 0>{});
+        eight(std::false_type{}, std::integral_constant<int, 1>{});
+    }
+
+    // the chunks' maps (half 0, then half 1), scanned across the chunks from q0, give each chunk
+    // its start q; then each lane's two positions
+    if (g == 0) {
+        const float2 c = hr[1] ? hc[1] : make_float2(hc[0].x + hc[1].x, hc[0].y + hc[1].y);
+        lds_ref<float2>(lds, Lo.qmap + 4u * (ch * kS + 2 * cp)) = c;
+        if (cp == 0) lds_ref<int32_t>(lds, Lo.qreset + 4u * ch) = hr[0] || hr[1] ? 1 : 0;
+    }
+    __syncthreads();
+    if (gl < kS) {  // one column a thread, the chunks in order
+        float cm[kChunks];
+        bool rm[kChunks];
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            cm[j] = lds_ref<float>(lds, Lo.qmap + 4u * (j * kS + gl));
+            rm[j] = lds_ref<int32_t>(lds, Lo.qreset + 4u * j) != 0;
+        }
+        float q = a.q0[size_t(b) * d + slice * kS + gl];
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            lds_ref<float>(lds, Lo.qstart + 4u * (j * kS + gl)) = q;
+            q = (rm[j] ? 0.0f : q) + cm[j];
+        }
+        if (a.q_T) a.q_T[size_t(b) * d + slice * kS + gl] = q;
+    }
+    __syncthreads();
+    {
+        const float2 qs = lds_ref<float2>(lds, Lo.qstart + 4u * (ch * kS + 2 * cp));
+        const float2 q1s = make_float2((hr[0] ? 0.0f : qs.x) + hc[0].x, (hr[0] ? 0.0f : qs.y) + hc[0].y);
+#pragma unroll
+        for (int H = 0; H < 2; ++H) {
+            const float2 qin = H == 0 ? qs : q1s;
+            float2 q = make_float2((qxr[H] ? 0.0f : qin.x) + qx[H].x, (qxr[H] ? 0.0f : qin.y) + qx[H].y);
+            if (qr[H]) q = make_float2(0.0f, 0.0f);
+            const int pos = 8 * H + g;
+            const uint32_t vqp = pos < n ? vq + uint32_t(t0 + pos) * d * 4u : kOob;
+            st2(q, rqa, vqp);
+            st2(make_float2(q.x + qc[H].x, q.y + qc[H].y), rqb, vqp);
+        }
+    }
+}
+
+}  // namespace evmap
+}  // namespace hsn

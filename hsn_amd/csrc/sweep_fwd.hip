@@ -65,9 +65,9 @@ void forward_launch(const void* y, const void* gate_pre, int io_dtype, const flo
         y = rms_normalise(y, io_dtype, cand_w, cand_eps, ws + L.rms, int64_t(B) * T * K, d, st);
         HSN_HIP(hipGetLastError());
     }
-    if (L.strip) {
-        strip_forward(y, gate_pre, io_dtype, reset, slots, h0, q0, age0, pos0, q_pre, q_post,
-                      h_sel, h_old, h_max, h_T, q_T, age_T, pos_T, B, T, N, d, K, st);
+    if (L.evmap) {
+        evmap_forward(y, gate_pre, reset, slots, h0, q0, age0, pos0, q_pre, q_post, h_sel,
+                      h_old, h_max, h_T, q_T, age_T, pos_T, B, T, N, d, K, st);
         return;
     }
     if (L.chain) {

@@ -262,7 +262,8 @@ def _align(n: int) -> int:
 @pytest.mark.parametrize("name", ["ref", "bf16", "tbptt", "skewed", "tiny"])
 def test_workspace_and_path_follow_the_shape(name):
     """The path a forward / backward call takes and the workspace it needs, host arithmetic
-    only: the slices where a wavefront's piece of a slot row is a full 32-byte sector and the
+    only: the event maps for an fp32 forward with d a multiple of 8, T <= 256, K <= 8 and the
+    tables of N cells in LDS (ref, tbptt, tiny), no workspace; otherwise the slices where a wavefront's piece of a slot row is a full 32-byte sector and the
     state slice N * S is at most 2048 words (ref: 8 fp32 columns of 256 cells), the cell chains
     where the piece would be narrower (bf16: 4 bf16 columns, skewed: 2) or the slice larger
     (tbptt: 8 columns of 512 cells); the chain workspace is the row lists (B(N+1) + BTK int32), the per-position
@@ -282,9 +283,11 @@ def test_workspace_and_path_follow_the_shape(name):
     B, T, N, d, K = c.B, c.T, c.N, c.d, c.K
     rms = _align(rms_scratch_bytes(B * T * K, d, elem))
     for op in (_lib.OP_FORWARD, _lib.OP_BACKWARD):
-        assert _lib.path_for(op, B, T, N, d, K, io) == want
+        evm = c.io == "f32" and d % 8 == 0 and T <= 256 and K <= 8 and N <= 512
+        auto = "evmap" if op == _lib.OP_FORWARD and evm else want
+        assert _lib.path_for(op, B, T, N, d, K, io) == auto
         chain, table = 0, (0, 0)
-        if want == "chain":
+        if auto == "chain":
             chain = _align(B * (N + 1) * 4) + _align(B * T * K * 4) + _align(B * T * d * 4)
             if op == _lib.OP_FORWARD:
                 chain += _align(B * T * K * d * 4)
@@ -299,18 +302,23 @@ def test_workspace_and_path_follow_the_shape(name):
         assert _lib.path_for(_lib.OP_FORWARD, B, T, N, d, K, io) == "slice"
     finally:
         _lib.set_path("auto")
-    # the strips, only when set: no workspace but the RMS input's; the forward holds a position's
-    # K * 8 deltas per row in LDS, so the bf16 and skewed rows (T K = 8192, 32768) do not fit
+    # the event maps, when set: the forward only (fp32, d a multiple of 8, T <= 256, K <= 8),
+    # no workspace but the RMS input's; the backward keeps the automatic choice
     try:
-        _lib.set_path("strip")
-        for op in (_lib.OP_FORWARD, _lib.OP_BACKWARD):
-            why = _lib.unsupported(op, B, T, N, d, K)
-            if name in ("ref", "tbptt", "tiny"):
-                assert why is None and _lib.path_for(op, B, T, N, d, K, io) == "strip"
-                assert _lib.workspace_bytes(op, B, T, N, d, K, io, False) == 0
-                assert _lib.workspace_bytes(op, B, T, N, d, K, io, True) == rms
-            elif op == _lib.OP_FORWARD:
-                assert "strip path" in why
+        _lib.set_path("evmap")
+        takes = c.io == "f32" and d % 8 == 0 and T <= 256 and K <= 8
+        why = None
+        try:
+            got_path = _lib.path_for(_lib.OP_FORWARD, B, T, N, d, K, io)
+        except RuntimeError as e:
+            got_path, why = None, str(e)
+        if takes:
+            assert got_path == "evmap"
+            assert _lib.workspace_bytes(_lib.OP_FORWARD, B, T, N, d, K, io, False) == 0
+            assert _lib.workspace_bytes(_lib.OP_FORWARD, B, T, N, d, K, io, True) == rms
+        else:
+            assert "event-map path" in why
+        assert _lib.path_for(_lib.OP_BACKWARD, B, T, N, d, K, io) == want
     finally:
         _lib.set_path("auto")
     lib = _lib.library()

@@ -29,7 +29,7 @@ def dev(cuda_device):
     return cuda_device
 
 
-@pytest.fixture(params=["slice", "chain", "strip"])
+@pytest.fixture(params=["evmap", "slice", "chain"])
 def path(request, dev):
     """Each forward / backward test runs on every sweep design (the library's path setting)."""
     from hsn_amd import _lib
@@ -40,13 +40,15 @@ def path(request, dev):
 
 
 def _skip_unless_taken(path, c):
-    """Skip where the forced sweep design does not take the case's shape (the strips' LDS holds
-    the row's per-slot deltas: T * K * 8 words)."""
+    """Skip where the forced sweep design does not take the case's shape (the event maps: fp32
+    rows, d a multiple of 8, T <= 256 and K <= 8)."""
     from hsn_amd import _lib
 
+    code = _lib.DTYPE_BF16 if c.get("io") == "bf16" else _lib.DTYPE_F32
     for op in (_lib.OP_FORWARD, _lib.OP_BACKWARD):
-        why = _lib.unsupported(op, c["B"], c["T"], c["N"], c["d"], c["K"])
-        if why is not None:
+        try:
+            _lib.path_for(op, c["B"], c["T"], c["N"], c["d"], c["K"], code)
+        except RuntimeError as why:
             pytest.skip(f"the {path} path does not take this shape: {why}")
 
 
@@ -362,6 +364,7 @@ def test_bf16_storage_rounds_like_torch(dev, path):
     from hsn_amd import window
 
     B, T, N, d, K = 2, 2, 16, 64, 16
+    _skip_unless_taken(path, dict(B=B, T=T, N=N, d=d, K=K, io="bf16"))
     g = torch.Generator().manual_seed(8)
     one = 1.0
     special = torch.tensor([one + 2.0 ** -8, one + 3 * 2.0 ** -8, -(one + 2.0 ** -8),

@@ -51,7 +51,7 @@ def _call(name, dev, w, slots, cand_w, out, dims, io, workspace=None):
     _lib.call(name, *head, *tail)
 
 
-@pytest.mark.parametrize("path", ["slice", "chain", "strip"])
+@pytest.mark.parametrize("path", ["slice", "chain", "evmap"])
 @pytest.mark.parametrize("io", ["f32", "bf16"])
 def test_noalloc_forward_equals_the_forward_with_a_workspace(cuda_device, io, path):
     from hsn_amd import _lib
@@ -60,7 +60,9 @@ def test_noalloc_forward_equals_the_forward_with_a_workspace(cuda_device, io, pa
     code = _lib.DTYPE_F32 if io == "f32" else _lib.DTYPE_BF16
     try:
         _lib.set_path(path)
-        odd_d = 8 if path == "strip" else 7  # (the strips take d a multiple of 4)
+        if path == "evmap" and io != "f32":
+            pytest.skip("the event maps take fp32 rows")
+        odd_d = 8 if path == "evmap" else 7  # (the event maps take d a multiple of 8)
         for dims, seed in (((6, 40, 64, 32, 8), 3), ((2, 9, 20, odd_d, 3), 4)):  # second smaller
             B, T, N, d, K = dims
             assert _lib.path_for(_lib.OP_FORWARD, B, T, N, d, K, code) == path
