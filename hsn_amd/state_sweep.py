@@ -90,23 +90,42 @@ class SweepShape(NamedTuple):
 
 
 def out_adjacency(pad_src: Tensor, pad_mask: Tensor) -> tuple[Tensor, Tensor]:
-    """The message graph by source (state_sweep.py:86-109): ``out_tgt [N, D_out]`` lists the
-    targets of cell ``n``'s out-edges ordered by target, then by the target's slot (-1 on
-    padding), ``out_edge [N, D_out]`` each edge's index ``target * D + slot`` in the padded view."""
+    """The message graph by source, for the reverse sweep's scatter to message sources
+    (interface and order of the reference's state_sweep.py:89-109): ``out_edge [N, D_out]``
+    holds each out-edge of cell ``n`` as its index ``target * D + slot`` into the padded
+    ``[N, D]`` view, ascending (by target, then slot), and ``out_tgt [N, D_out]`` its target;
+    rows are padded with -1 targets and edge 0, and ``D_out`` is the largest out-degree (1 at
+    least).
+
+    The real edges' flat indices come out of the mask already ascending, so one sort of the
+    composite key ``source * N * D + flat`` groups them by source in that order; an edge's
+    column is its distance from the first edge of its source in the sorted list."""
     N, D = (int(n) for n in pad_src.shape)
-    target, slot = pad_mask.nonzero(as_tuple=True)  # by target, then slot
-    source = pad_src[target, slot]
-    order = torch.argsort(source, stable=True)
-    source, target, flat = source[order], target[order], (target * D + slot)[order]
-    counts = torch.bincount(source, minlength=N)
-    d_out = max(int(counts.max()) if counts.numel() else 0, 1)
-    start = counts.cumsum(0) - counts
-    position = torch.arange(source.numel(), device=pad_src.device) - start[source]
-    out_tgt = torch.full((N, d_out), -1, dtype=torch.int64, device=pad_src.device)
-    out_edge = torch.zeros((N, d_out), dtype=torch.int64, device=pad_src.device)
-    out_tgt[source, position] = target
-    out_edge[source, position] = flat
+    dev = pad_src.device
+    flat = pad_mask.reshape(-1).nonzero().reshape(-1)  # real edges, ascending flat index
+    source = pad_src.reshape(-1)[flat].to(torch.int64)
+    if source.numel() and bool(((source < 0) | (source >= N)).any()):
+        raise ValueError("a message source lies outside [0, N)")
+    key, perm = torch.sort(source * (N * D) + flat)
+    source, flat = key // (N * D), flat[perm]
+    column = torch.arange(flat.numel(), device=dev) - torch.searchsorted(source, source)
+    d_out = int(column.max()) + 1 if column.numel() else 1
+    out_edge = torch.zeros((N, d_out), dtype=torch.int64, device=dev)
+    out_edge[source, column] = flat
+    out_tgt = torch.full((N, d_out), -1, dtype=torch.int64, device=dev)
+    out_tgt[source, column] = flat // D
     return out_tgt, out_edge
+
+
+def _graph_token(pad_src: Tensor, pad_mask: Tensor) -> tuple:
+    """What identifies a message graph between windows: both tensors and their version counters
+    (an in-place change of either bumps its counter, so a cached adjacency is rebuilt)."""
+    return (pad_src, pad_src._version, pad_mask, pad_mask._version)
+
+
+def _same_graph(token: Optional[tuple], pad_src: Tensor, pad_mask: Tensor) -> bool:
+    return (token is not None and token[0] is pad_src and token[1] == pad_src._version
+            and token[2] is pad_mask and token[3] == pad_mask._version)
 
 
 def sweep_shape(c: Tensor, record: dict[str, Tensor], consts: Any, n_cells: int, n_fast: int,
@@ -207,6 +226,9 @@ class ReverseSweep:
         rows = B * K
         self.A, self.R, self.sigma = torch.zeros(B, N, d, **f32), torch.zeros(B, d, **f32), \
             torch.zeros(B, K, **f32)
+        # the cotangents entering the window (after its last position), kept apart from the
+        # running A and R so that every pass, eager or replayed, starts from them
+        self.A_in, self.R_in = torch.zeros(B, N, d, **f32), torch.zeros(B, d, **f32)
         self.c, self.b, self.h_old = (torch.zeros(B, T, K, d, **f32) for _ in range(3))
         self.y, self.gate_pre, self.mv = (torch.zeros(B, T, K, d, **f32) for _ in range(3))
         self.alpha, self.rms = torch.ones(B, T, K, **f32), torch.ones(B, T, K, **f32)
@@ -223,7 +245,7 @@ class ReverseSweep:
         self.out_tgt = torch.full((N, d_out), -1, **i32)
         self.out_w = torch.zeros(N, d_out, **f32)
         self.in_src = torch.full((N, self.d_in), -1, **i32)
-        self._graph_of: Optional[Tensor] = None
+        self._graph_of: Optional[tuple] = None  # the message graph the adjacency was built from
         self.op1, self.op2 = torch.zeros(rows, M * d, **prod), torch.zeros(rows, M * H + d, **prod)
         self.act, self.dv = torch.zeros(rows, H, **prod), torch.zeros(rows, 2 * d, **prod)
         self.dc, self.db = torch.zeros(B, T, K, d, **f32), torch.zeros(B, T, K, d, **f32)
@@ -295,7 +317,7 @@ class ReverseSweep:
             self.cand_gain.copy_(consts.cand_gain)
         self.gate_bias.copy_(consts.gate_bias)
         self.b1.copy_(consts.b1)
-        if self._graph_of is not consts.pad_src:  # the topology: fixed between windows
+        if not _same_graph(self._graph_of, consts.pad_src, consts.pad_mask):
             pad_src = consts.pad_src.to(self.device)
             pad_mask = consts.pad_mask.to(self.device)
             if bool(((pad_src < 0) | (pad_src >= s.N))[pad_mask].any()):
@@ -307,7 +329,7 @@ class ReverseSweep:
             self.out_tgt.copy_(out_tgt)
             self._out_edge = out_edge
             self.in_src.copy_(torch.where(pad_mask, pad_src, torch.full_like(pad_src, -1)))
-            self._graph_of = consts.pad_src
+            self._graph_of = _graph_token(consts.pad_src, consts.pad_mask)
         weights = consts.edge_weights.to(self.device, torch.float32).reshape(-1)[self._out_edge]
         self.out_w.copy_(torch.where(self.out_tgt >= 0, weights, torch.zeros_like(weights)))
 
@@ -356,50 +378,45 @@ class ReverseSweep:
             torch.matmul(record["m"].to(self.device, torch.float32),
                          consts.v.to(self.device, torch.float32), out=self.mv)
         self.load_weights(consts)
-        if initial is None:
-            self.A.zero_()
-            self.R.zero_()
-        else:
-            self.A.copy_(initial[0])
-            self.R.copy_(initial[1])
-        self.op1.zero_()
-        self.op2.zero_()
+        for entry, value in zip((self.A_in, self.R_in), initial or (None, None)):
+            if value is None:
+                entry.zero_()
+            else:
+                entry.copy_(value)
 
     # -- the sweep -------------------------------------------------------------------------------
 
+    def _window(self) -> None:
+        """One whole pass over the loaded window: the running cotangents start from ``A_in`` /
+        ``R_in`` and the products' operand rows from zero (rows of padded slots are never
+        written), then the positions ``T - 1 .. 0``. The pass reads nothing a previous pass
+        left, so it may run any number of times, and a graph of it needs no restore."""
+        self.A.copy_(self.A_in)
+        self.R.copy_(self.R_in)
+        self.op1.zero_()  # fill kernels (no memset nodes in a captured graph)
+        self.op2.zero_()
+        for t in reversed(range(self.shape.T)):
+            self.step(t)
+
     def run(self) -> tuple[Tensor, Tensor]:
-        """The loaded window's sweep: ``(dc, db)``, the buffers; replays the captured graph when
-        there is one."""
-        if self._graph is not None:
-            self._graph.replay()
+        """The loaded window's sweep: ``(dc, db)``, the buffers (the graph when captured)."""
+        if self._graph is None:
+            self._window()
         else:
-            for t in range(self.shape.T - 1, -1, -1):
-                self.step(t)
+            self._graph.replay()
         return self.dc, self.db
 
     def capture(self, warm_up: int = 2) -> None:
-        """Capture the loop over the positions as a HIP graph (state_sweep.py:325-352): the
-        loaded window runs ``warm_up`` times eagerly, the loop is recorded, and the buffers are
-        put back as loaded; later ``run`` calls replay the graph."""
-        keep = (self.A.clone(), self.R.clone())
+        """Record one pass as a HIP graph for later ``run`` calls. ``warm_up`` eager passes go
+        first, so the products' library calls have chosen their kernels and workspaces before
+        the capture; since every pass restarts itself, nothing is saved or put back."""
         for _ in range(warm_up):
-            self._restart(keep)
-            for t in range(self.shape.T - 1, -1, -1):
-                self.step(t)
-        self._restart(keep)
+            self._window()
         torch.cuda.synchronize(self.device)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            for t in range(self.shape.T - 1, -1, -1):
-                self.step(t)
+            self._window()
         self._graph = graph
-        self._restart(keep)
-
-    def _restart(self, initial: tuple[Tensor, Tensor]) -> None:
-        self.A.copy_(initial[0])
-        self.R.copy_(initial[1])
-        self.op1.zero_()
-        self.op2.zero_()
 
     def step(self, t: int) -> None:
         """Position ``t``: the fused step and its tail, or the three glue steps and the two
@@ -429,7 +446,7 @@ class SweepRunner:
         self.sweeps: dict[tuple, ReverseSweep] = {}
         # the out-degree per message graph (its pad_src tensor, kept alive with it): the graph is
         # fixed between windows, and finding the degree takes host synchronisations
-        self._d_out: dict[int, tuple[Tensor, int]] = {}
+        self._d_out: dict[int, tuple[tuple, int]] = {}
         #: Windows swept, and how many of them captured a graph.
         self.calls = 0
         self.captures = 0
@@ -451,9 +468,9 @@ class SweepRunner:
         if product_dtype not in (torch.float32, torch.bfloat16):
             return None
         known = self._d_out.get(id(consts.pad_src))
-        if known is None or known[0] is not consts.pad_src:
+        if known is None or not _same_graph(known[0], consts.pad_src, consts.pad_mask):
             degree = int(out_adjacency(consts.pad_src, consts.pad_mask)[0].shape[1])
-            known = self._d_out[id(consts.pad_src)] = (consts.pad_src, degree)
+            known = self._d_out[id(consts.pad_src)] = (_graph_token(consts.pad_src, consts.pad_mask), degree)
         shape = sweep_shape(c, record, consts, n_cells, n_fast, n_read, d_out=known[1])
         cand_norm = consts.cand_gain is not None
         cell_norm = consts.norm_gain_state is not None

@@ -114,7 +114,7 @@ def adamw(
         1 - beta1,
         beta2,
         1 - beta2,
-        1.0 / bias_correction2_sqrt,  # torch divides a tensor list by a scalar this way
+        1.0 / bias_correction2_sqrt,  # multiplied by 1/s, matching torch's rounding of list / scalar
         eps,
         -step_size,
     )
@@ -161,7 +161,8 @@ def adamw_units(
 
 
 def lerp(selfs: Sequence[Tensor], ends: Sequence[Tensor], weight: float) -> bool:
-    """``torch._foreach_lerp_(selfs, ends, weight)`` as one pass."""
+    """Move every ``selfs[i]`` toward ``ends[i]`` by ``weight`` in place, one launch for the
+    whole list; the same result as ``torch._foreach_lerp_``."""
     if not _fits((selfs, ends)):
         return False
     _lib.call("hsn_tr_lerp", _pointers(selfs), _pointers(ends), _numels(selfs), len(selfs),
@@ -183,7 +184,8 @@ def scale64(grads: Sequence[Tensor], coefficient: Tensor) -> bool:
 
 
 def copy(dsts: Sequence[Tensor], srcs: Sequence[Tensor]) -> bool:
-    """``torch._foreach_copy_(dsts, srcs)`` for fp32 tensors as one pass."""
+    """Overwrite each fp32 ``dsts[i]`` with ``srcs[i]``, one launch for the whole list (what
+    ``torch._foreach_copy_`` does)."""
     if not _fits((dsts, srcs)):
         return False
     _lib.call("hsn_tr_copy", _pointers(dsts), _pointers(srcs), _numels(dsts), len(dsts),
@@ -197,8 +199,9 @@ def limit_squares(
     old_squares: Sequence[Tensor],
     delta_squares: Sequence[Tensor],
 ) -> bool:
-    """The squares ``UpdateLimiter.apply`` sums for its two norms: ``old ** 2`` and
-    ``(param - old) ** 2`` of every tensor, into the given buffers."""
+    """Element-wise squares for the limiter's two norms, written into the given buffers:
+    ``old_squares[i] = olds[i] ** 2`` (the norm of the previous weights) and
+    ``delta_squares[i] = (params[i] - olds[i]) ** 2`` (the norm of the proposed step)."""
     rows = (params, olds, old_squares, delta_squares)
     if not _fits(rows):
         return False
@@ -213,9 +216,10 @@ def limit_project(
     applied_squares: Sequence[Tensor],
     groups: Sequence[Tensor],
 ) -> bool:
-    """The projection of ``UpdateLimiter.apply``: ``param = old + (param - old) * scale`` on the
-    tensors of a clipped group (``groups[j]`` holds tensor ``j``'s group as two fp32 values on the
-    device, ``[scale, clipped]``), and the squares of the applied step ``(param - old) ** 2``."""
+    """Pull each tensor of a clipped group back toward its previous weights: for tensor ``j``,
+    ``groups[j]`` is a two-element fp32 device tensor ``[scale, clipped]``; where ``clipped`` is
+    set the step ``params[j] - olds[j]`` is multiplied by ``scale`` in place. Every tensor's
+    final step squared goes to ``applied_squares[j]``."""
     if len(groups) != len(params) or any(
             g.dtype != torch.float32 or g.numel() != 2 or not g.is_contiguous() for g in groups):
         return False
