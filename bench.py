@@ -467,20 +467,20 @@ def _ops_main(args) -> int:
     indices = torch.randint(0, N, (E,), generator=g).to(dev)
     a = torch.rand(E, generator=g).to(dev)
     V = rnd(d, d, scale=d ** -0.5)
-    out, hidden = ops.grouped_unit_mlp(v, unit, w1, b1, w2, b2)
+    out, hidden = ops.mlp_op(v, unit, w1, b1, w2, b2)
     calls = {
-        "gated_delta_update_functional": lambda: ops.gated_delta_update_functional(
+        "gated_delta_update_functional": lambda: ops.update_op(
             h, q, age.long(), idx, valid, c, b),
-        "gated_delta_update_backward": lambda: ops.gated_delta_update_backward(
+        "gated_delta_update_backward": lambda: ops.update_backward(
             idx, valid, c, b, c, h, q),
-        "gather_concat": lambda: ops.gather_concat(u, eps, h, m, idx),
-        "gather_concat_backward": lambda: ops.gather_concat_backward(
+        "gather_concat": lambda: ops.gather_op(u, eps, h, m, idx),
+        "gather_concat_backward": lambda: ops.gather_backward(
             rnd_dv, idx, N),
-        "grouped_unit_mlp": lambda: ops.grouped_unit_mlp(v, unit, w1, b1, w2, b2),
-        "grouped_unit_mlp_backward": lambda: ops.grouped_unit_mlp_backward(
+        "grouped_unit_mlp": lambda: ops.mlp_op(v, unit, w1, b1, w2, b2),
+        "grouped_unit_mlp_backward": lambda: ops.mlp_backward(
             v, unit, w1, w2, hidden, out),
-        "csr_messages": lambda: ops.csr_messages(h, indptr, indices, a, V, idx),
-        "csr_messages_backward": lambda: ops.csr_messages_backward(
+        "csr_messages": lambda: ops.messages_op(h, indptr, indices, a, V, idx),
+        "csr_messages_backward": lambda: ops.messages_backward(
             h, indptr, indices, a, V, idx, m),
     }
     rnd_dv = rnd(B, K, 4 * d)

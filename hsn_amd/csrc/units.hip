@@ -1216,6 +1216,9 @@ __device__ __forceinline__ void gather_sums(const T* h, const T* a, const int32_
 // (source, weight), then each (slot, column) sums its slot's entries in edge order with the loads
 // of h issued 8 at a time. A longer list takes gather_sums.
 constexpr int kListCap = 1024;
+// gather_sums_listed's static LDS (the 16 slots' edge list), which counts against the same
+// 64 KiB default limit as a caller's dynamic LDS
+constexpr size_t kListLds = (17 + 16 + 2 * size_t(kListCap)) * 4;
 template <typename T>
 __device__ __forceinline__ void gather_sums_listed(const T* h, const T* a,
                                                    const int32_t* cell_idx, const Csr& g, int s0,
@@ -1852,8 +1855,13 @@ struct RunCsr {
                     const void* V, const int32_t* idx, void* m, int B, int N, int d, int K, int E,
                     hipStream_t st) {
         const units::Csr g{indptr, indices, N, E};
+        // S [16][d] in dynamic LDS beside the static edge list: above the default 64 KiB from
+        // d = 894 on (d <= 1024: at most 72.3 KiB of the CU's 160)
+        const size_t lds = size_t(16) * d * 4;
+        if (lds + units::kListLds > 64 * 1024)
+            HSN_HIP(allow_lds_raw(reinterpret_cast<const void*>(units::csr_fwd<T>), lds));
         hipLaunchKernelGGL((units::csr_fwd<T>), dim3((B * K + 15) / 16, (d + 63) / 64),
-                           dim3(256), size_t(16) * d * 4, st, static_cast<const T*>(h), g,
+                           dim3(256), lds, st, static_cast<const T*>(h), g,
                            static_cast<const T*>(a), static_cast<const T*>(V), idx,
                            static_cast<T*>(m), B, K, d);
     }

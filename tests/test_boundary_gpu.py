@@ -76,28 +76,28 @@ def _cases(dev):
                                          dtype=torch.int32).to(dev),
            torch.rand(int(indptr[-1]), generator=g).to(dev))
     return {
-        "gather_concat": (ops.gather_concat, (f(B, d), f(B, d), f(B, N, d), f(B, K, d), idx),
+        "gather_concat": (ops.gather_op, (f(B, d), f(B, d), f(B, N, d), f(B, K, d), idx),
                           (0, 1, 2, 3)),
-        "gather_concat_backward": (ops.gather_concat_backward, (f(B, K, 4 * d), idx, N), ()),
-        "grouped_unit_mlp": (ops.grouped_unit_mlp,
+        "gather_concat_backward": (ops.gather_backward, (f(B, K, 4 * d), idx, N), ()),
+        "grouped_unit_mlp": (ops.mlp_op,
                              (f(5, 4 * d), torch.tensor([0, 1, 1, 0, 1], device=dev),
                               f(3, 4 * d, 6), f(3, 6), f(3, 6, d), f(3, d)), (0, 2, 3, 4, 5)),
-        "grouped_unit_mlp_backward": (ops.grouped_unit_mlp_backward,
+        "grouped_unit_mlp_backward": (ops.mlp_backward,
                                       (f(5, 4 * d), torch.tensor([0, 1, 1, 0, 1], device=dev),
                                        f(3, 4 * d, 6), f(3, 6, d), f(5, 6), f(5, d)), ()),
-        "csr_messages": (ops.csr_messages,
+        "csr_messages": (ops.messages_op,
                          (f(B, N, d), csr[0], csr[1], csr[2], f(d, d), idx), (0, 3, 4)),
-        "csr_messages_backward": (ops.csr_messages_backward,
+        "csr_messages_backward": (ops.messages_backward,
                                   (f(B, N, d), csr[0], csr[1], csr[2], f(d, d), idx, f(B, K, d)),
                                   ()),
-        "gated_delta_update": (ops.gated_delta_update,
+        "gated_delta_update": (ops.update_inplace,
                                (h.clone(), q.clone(), age.to(torch.int32), idx, valid, c, b), ()),
-        "gated_delta_update_functional": (ops.gated_delta_update_functional,
+        "gated_delta_update_functional": (ops.update_op,
                                           (h.clone(), q.clone(), age, idx, valid, c, b),
                                           (0, 1, 5, 6)),
-        "gated_delta_update_state": (ops.gated_delta_update_state,
+        "gated_delta_update_state": (ops.state_update_op,
                                      (h.clone(), q.clone(), age, idx, valid, c, b), (0, 1, 5, 6)),
-        "gated_delta_update_backward": (ops.gated_delta_update_backward,
+        "gated_delta_update_backward": (ops.update_backward,
                                         (idx, valid, c, b, h[:, :K].contiguous(), f(B, N, d),
                                          f(B, d)), ()),
         "window_select": (window.select_op, (logits, age, cost, K) + sel, ()),
