@@ -69,12 +69,13 @@ bool chain_takes(int B, int T, int N, int d, int K, const char** why) {
 bool evmap_takes(int op, int B, int T, int N, int d, int K, size_t elem, const char** why) {
     (void)B;
     const char* r = nullptr;
-    if (op != HSN_OP_FORWARD) r = "the event maps take the window forward only";
+    if (op != HSN_OP_FORWARD && op != HSN_OP_BACKWARD) r = "the event maps take the window forward and backward";
     else if (elem != 4) r = "the event maps take fp32 rows only";
     else if (d % evmap::kS != 0) r = "the event maps take d a multiple of 8";
     else if (T > evmap::kChunks * evmap::kP) r = "the event maps take T <= 256";
     else if (K > evmap::kK) r = "the event maps take K <= 8";
-    else if (evmap::fwd_layout(N).bytes > size_t(kLdsMax)) r = "the event maps' tables of N cells do not fit the LDS";
+    else if ((op == HSN_OP_FORWARD ? evmap::fwd_layout(N).bytes : evmap::bwd_layout(N).bytes) > size_t(kLdsMax))
+        r = "the event maps' tables of N cells do not fit the LDS";
     else if ((int64_t(T) + 32) * K * d * 4 >= (int64_t(1) << 31)) r = "the event maps take (T + 32) K d * 4 < 2^31 bytes a row";
     if (r && why) *why = r;
     return r == nullptr;
@@ -85,15 +86,12 @@ int choose_path(int op, int B, int T, int N, int d, int K, size_t elem) {
     const char* why_c = nullptr;
     const char* why_e = nullptr;
     const int setting = path_setting();
-    // the event maps have a forward only: a forced event-map setting leaves the backward to the
-    // automatic choice between the other two
-    const bool any = setting == kPathAuto || (setting == kPathEvmap && op != HSN_OP_FORWARD);
-    const bool e_ok = (setting == kPathAuto || setting == kPathEvmap) &&
-                      evmap_takes(op, B, T, N, d, K, elem, &why_e);
-    if (setting == kPathEvmap && op == HSN_OP_FORWARD && !e_ok)
+    const bool any = setting == kPathAuto;
+    const bool e_ok = (any || setting == kPathEvmap) && evmap_takes(op, B, T, N, d, K, elem, &why_e);
+    if (setting == kPathEvmap && !e_ok)
         throw AbiError{HSN_ERR_INVALID_ARGUMENT, std::string("(event-map path) ") + why_e};
-    // The event maps first where they take the shape: at B32 T256 N256 d64 K8 fp32 the forward
-    // moves its rows as two columns a lane with a chunk per half-wavefront (see evmap.cuh).
+    // The event maps first where they take the shape: at B32 T256 N256 d64 K8 fp32 both
+    // directions move their rows as two columns a lane with a chunk per half-wavefront.
     if (e_ok) return kPathEvmap;
     const bool s_ok = (any || setting == kPathSlice) && slice_takes(op, B, T, N, d, K, &why_s);
     const bool c_ok = (any || setting == kPathChain) && chain_takes(B, T, N, d, K, &why_c);

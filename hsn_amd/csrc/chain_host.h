@@ -52,5 +52,10 @@ void evmap_forward(const void* y, const void* gate_pre, const uint8_t* reset,
                    const int64_t* pos0, void* q_pre, void* q_post, void* h_sel, void* h_old,
                    float* h_max, float* h_T, float* q_T, int64_t* age_T, int64_t* pos_T, int B,
                    int T, int N, int d, int K, hipStream_t st);
+void evmap_backward(const void* y, const void* gate_pre, const void* h_old, const int32_t* slots,
+                    const uint8_t* reset, const void* d_q_pre, const void* d_q_post,
+                    const void* d_h_sel, const float* d_h_T, const float* d_q_T, void* dy,
+                    void* dgate, float* d_h0, float* d_q0, int B, int T, int N, int d, int K,
+                    hipStream_t st);
 
 }  // namespace hsn

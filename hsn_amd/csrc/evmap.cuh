@@ -621,5 +621,414 @@ __global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// Backward
+// ------------------------------------------------------------------------------------------
+//
+// The reverse recurrence of one cell and column is affine per event too: with A the cotangent
+// of the cell's value after the event, the value before it gets A' = (1 - b) (A + dsel) - b s,
+// where dsel is the slot's h_sel cotangent and s = R / N the position's share of the summary
+// cotangent R (the summary's cotangent enters every update once with + and once with -); a
+// reset at t zeroes every cell's A once position t is processed, and R as well. R depends on the
+// cotangents only, so the kernel first scans it (fp64, latest position first, one barrier across
+// the chunks) into every position's share; then, time reversed, the same three phases as the
+// forward: each chunk composes its cells' maps A_start = mu A_end + nu over its events latest
+// first (a cell's entry is its last event in the chunk), the cells are walked from d_h_T back
+// through the 16 chunks to d_h0, and each chunk replays its positions from the cells' end values
+// with the outputs d y = b (1 - c^2) G and d gate = (c - h_old) b (1 - b) G, G = A + dsel + s.
+// Padded and idle slots take part in nothing and write exact zeros.
+
+struct BwdEv {
+    const float* y;         // [B, T, K, d]: the candidate's pre-activation (tanh)
+    const float* g;         // the gate's pre-activation (sigmoid)
+    const float* h_old;     // the forward's gathered old values
+    const float* dsel;      // [B, T, K, d] cotangent of h_sel, or NULL (zero)
+    const int32_t* slots;   // [B, T, K]: the cell, or -1 where padded
+    const uint8_t* reset;   // [B, T] or NULL
+    const float* dq_pre;    // [B, T, d] or NULL
+    const float* dq_post;
+    const float* dh_T;      // [B, N, d] or NULL
+    const float* dq_T;      // [B, d] or NULL
+    float* dy;              // [B, T, K, d]
+    float* dg;
+    float* dh0;             // [B, N, d] or NULL
+    float* dq0;             // [B, d] or NULL
+    int T, N, d, K, P;
+    DivN divn;
+};
+
+// LDS byte offsets: the chunks' maps [16][mu, nu][kEnt][8] f32 (mu becomes the entry's cotangent
+// in phase C, nu the slots' h_sel cotangents), the last-event table [N + 1][16] u8 (row N:
+// kDummy), the positions' shares [16][16][8] f32, each chunk's summary-cotangent map
+// R -> (reset ? 0 : R) + c ([16][8] fp64 c, [16] reset flags), and 8 bytes a thread where a lane
+// with nothing to write does.
+struct BwdLayout {
+    uint32_t maps, idx, share, rsum, rflag, tdummy, bytes;
+};
+
+__host__ __device__ inline BwdLayout bwd_layout(int N) {
+    BwdLayout L{};
+    uint32_t at = 0;
+    L.maps = at;
+    at += kChunks * kMapBytes;
+    L.idx = at;
+    at += (uint32_t(N + 1) * kChunks + 15u) & ~15u;
+    L.share = at;
+    at += kChunks * kP * kS * 4u;
+    L.rsum = at;
+    at += kChunks * kS * 8u;
+    L.rflag = at;
+    at += kChunks * 4u;
+    L.tdummy = at;
+    at += kWave * kWaves * 8u;
+    L.bytes = at;
+    return L;
+}
+
+template <typename IN>
+__global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
+    static_assert(sizeof(IN) == 4, "fp32 rows");
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int N = a.N, d = a.d, K = a.K, T = a.T;
+    const BwdLayout Lo = bwd_layout(N);
+    const int lane = lane_id();
+    const int gl = threadIdx.x;
+    const int half = lane >> 5, hl = lane & 31;
+    const int ch = 2 * uniform(gl / kWave) + half;  // this half-wave's chunk
+    const int k = hl >> 2, cp = hl & 3;
+    int b, slice;
+    block_coords(b, slice);
+    const int P = a.P;
+    const int t0 = ch * P;
+    const int n = max(0, min(P, T - t0));  // positions of the chunk (uniform in the half)
+    const bool active = k < K;
+    const int col = slice * kS + 2 * cp;
+    const DivN divn = a.divn;
+
+    const uint32_t pos_bytes = uint32_t(K) * d * 4u;
+    const size_t orow = size_t(b) * T * K * d;
+    const uint32_t row_bytes = uint32_t(T) * pos_bytes;
+    const rsrc_t rg = make_rsrc(a.g + orow, row_bytes);
+    const rsrc_t rds = make_rsrc(a.dsel ? a.dsel + orow : nullptr, a.dsel ? row_bytes : 0u);
+    const rsrc_t rc = make_rsrc(a.slots + size_t(b) * T * K, uint32_t(T) * K * 4u);
+    const rsrc_t rr = make_rsrc(a.reset ? a.reset + size_t(b) * T : nullptr, a.reset ? uint32_t(T) : 0u);
+    const uint32_t qbytes = uint32_t(T) * d * 4u;
+    const rsrc_t rqa = make_rsrc(a.dq_pre ? a.dq_pre + size_t(b) * T * d : nullptr, a.dq_pre ? qbytes : 0u);
+    const rsrc_t rqb = make_rsrc(a.dq_post ? a.dq_post + size_t(b) * T * d : nullptr, a.dq_post ? qbytes : 0u);
+    // a lane's piece of position i is vrow + i * pos_bytes, out of range for an idle lane and
+    // past the window (as the forward's)
+    const uint32_t vrow = (active ? uint32_t(k * d + col) * 4u : kOob) + uint32_t(t0) * pos_bytes;
+
+    // ---- first loads: phase B's first end cotangents, the resets, the summary cotangents ----
+    const int bq = gl & 1;  // phase B: thread 2 c + q holds columns 4q .. 4q + 3 of cell c
+    const float* const dhT_row = a.dh_T ? a.dh_T + size_t(b) * N * d : nullptr;
+    auto dhT_at = [&](int cell) __attribute__((always_inline)) -> float4 {
+        return dhT_row && cell < N
+                   ? *reinterpret_cast<const float4*>(dhT_row + int64_t(cell) * d + slice * kS + 4 * bq)
+                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    };
+    const float4 dha = dhT_at(gl >> 1);
+    const uint8_t rbyte = __builtin_amdgcn_raw_buffer_load_b8(rr, hl < n ? uint32_t(t0 + hl) : kOob, 0u, 0);
+    // the summary cotangents of the lane's positions g and 8 + g, its column pair
+    const int g = hl >> 2;
+    const uint32_t vq = uint32_t(col) * 4u;
+    float2 qa[2], qb[2];
+#pragma unroll
+    for (int H = 0; H < 2; ++H) {
+        const int pos = 8 * H + g;
+        const uint32_t vqp = pos < n ? vq + uint32_t(t0 + pos) * d * 4u : kOob;
+        qa[H] = ld2(rqa, vqp);
+        qb[H] = ld2(rqb, vqp);
+    }
+
+    // ---- phase A: the gates, the selection cotangents and the decisions, 8 positions ahead ----
+    constexpr int kAhead = 8;
+    float2 gv[kP], dv[kP];
+    int32_t cv[kP];
+    auto fetch = [&](int i) __attribute__((always_inline)) {
+        const uint32_t vo = vrow + uint32_t(i) * pos_bytes;
+        gv[i] = ld2(rg, vo);
+        dv[i] = ld2(rds, vo);
+        cv[i] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+            rc, active ? uint32_t((t0 + i) * K + k) * 4u : kOob, 0u, 0));
+    };
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) fetch(i);
+
+    // this chunk's columns of the tables while the loads are in flight (no other half-wave reads
+    // them before phase B): no event (0xff; row N kDummy) and the dummy entry's identity (1, 0)
+    unsigned char* const idx = lds + Lo.idx;
+    for (int c = hl; c <= N; c += 32) idx[c * kChunks + ch] = c < N ? 0xffu : uint8_t(kDummy);
+    const uint32_t cbase = Lo.maps + uint32_t(ch) * kMapBytes;
+    if (hl < kS) {
+        lds_ref<float>(lds, cbase + kDummy * kEntBytes + 4u * hl) = 1.0f;
+        lds_ref<float>(lds, cbase + kEnt * kEntBytes + kDummy * kEntBytes + 4u * hl) = 0.0f;
+    }
+
+    // the summary cotangent's maps, latest position first: position p takes R to
+    // (reset ? 0 : R + dq_post + dq_pre); an inclusive scan over the lane groups g .. 7 of each
+    // half (later positions applied first), in fp64
+    const uint32_t rmask = static_cast<uint32_t>(ballot(rbyte != 0) >> (32 * half));
+    bool ir[2], er[2], wr[2];  // inclusive, exclusive (groups after g) and the whole half's
+    double icx[2], icy[2], ecx[2], ecy[2], wcx[2], wcy[2];
+#pragma unroll
+    for (int H = 0; H < 2; ++H) {
+        const int pos = 8 * H + g;
+        const bool in = pos < n;
+        bool r = in && ((rmask >> pos) & 1u);
+        double cx = in && !r ? double(qb[H].x) + double(qa[H].x) : 0.0;
+        double cy = in && !r ? double(qb[H].y) + double(qa[H].y) : 0.0;
+#pragma unroll
+        for (int sft = 1; sft < 8; sft <<= 1) {
+            const double nx = __shfl_down(cx, 4 * sft, kWave), ny = __shfl_down(cy, 4 * sft, kWave);
+            const int nr = __shfl_down(r ? 1 : 0, 4 * sft, kWave);
+            if (g + sft < 8) {
+                cx = r ? cx : cx + nx;
+                cy = r ? cy : cy + ny;
+                r = r || nr != 0;
+            }
+        }
+        ir[H] = r, icx[H] = cx, icy[H] = cy;
+        const double ex = __shfl_down(cx, 4, kWave), ey = __shfl_down(cy, 4, kWave);
+        const int ex_r = __shfl_down(r ? 1 : 0, 4, kWave);
+        er[H] = g < 7 && ex_r != 0;
+        ecx[H] = g < 7 ? ex : 0.0;
+        ecy[H] = g < 7 ? ey : 0.0;
+        const int src = (lane & 32) | cp;  // group 0 of this half: the half's whole map
+        wcx[H] = __shfl(cx, src, kWave);
+        wcy[H] = __shfl(cy, src, kWave);
+        wr[H] = __shfl(r ? 1 : 0, src, kWave) != 0;
+    }
+    if (g == 0) {  // the chunk's map: the later half first
+        const double cx = wr[0] ? wcx[0] : wcx[0] + wcx[1];
+        const double cy = wr[0] ? wcy[0] : wcy[0] + wcy[1];
+        lds_ref<double>(lds, Lo.rsum + 8u * (ch * kS + 2 * cp)) = cx;
+        lds_ref<double>(lds, Lo.rsum + 8u * (ch * kS + 2 * cp + 1)) = cy;
+        if (cp == 0) lds_ref<int32_t>(lds, Lo.rflag + 4u * ch) = wr[0] || wr[1] ? 1 : 0;
+    }
+
+    float2 omb[kP], dsv[kP];
+    uint32_t vmask = 0u;  // the lane's valid positions
+#pragma unroll
+    for (int i = 0; i < kP; ++i) {
+        if (i + kAhead < kP) fetch(i + kAhead);
+        const int c = cv[i];
+        const bool ok = active && i < n && c >= 0;
+        const float b0 = fast_sigmoid(gv[i].x), b1 = fast_sigmoid(gv[i].y);
+        omb[i] = ok ? make_float2(1.0f - b0, 1.0f - b1) : make_float2(1.0f, 1.0f);
+        dsv[i] = ok ? dv[i] : make_float2(0.0f, 0.0f);
+        vmask |= ok ? 1u << i : 0u;
+        cv[i] = ok ? c : N;  // the last-event table's row (N: the idle slots' row)
+    }
+
+    // last events: every event writes its index into its cell's byte of this chunk, earliest
+    // position first, so each byte ends with the cell's last event (one lane a slot writes)
+    const uint32_t my_dummy = Lo.tdummy + 8u * uint32_t(gl);
+#pragma unroll
+    for (int i = 0; i < kP; ++i)
+        lds[(vmask >> i) & 1u && cp == 0 ? Lo.idx + uint32_t(cv[i] * kChunks + ch) : my_dummy] =
+            static_cast<unsigned char>(i * kK + k);
+    uint32_t entw[kP / 4] = {};
+#pragma unroll
+    for (int i = 0; i < kP; ++i) entw[i / 4] |= uint32_t(idx[cv[i] * kChunks + ch]) << (8 * (i % 4));
+    auto ent = [&](int i) __attribute__((always_inline)) -> uint32_t {
+        return (entw[i / 4] >> (8 * (i % 4))) & 0xffu;
+    };
+    // the replay's inputs, latest position first, spread over the barrier and the composition
+    // (issued at once they stall the wave until the memory system drains them)
+    const rsrc_t ry = make_rsrc(a.y + orow, row_bytes);
+    const rsrc_t rho = make_rsrc(a.h_old + orow, row_bytes);
+    float2 yv[kP], hv[kP];
+    auto fetch_c = [&](int i) __attribute__((always_inline)) {
+        const uint32_t vo = vrow + uint32_t(i) * pos_bytes;
+        yv[i] = ld2(ry, vo);
+        hv[i] = ld2(rho, vo);
+    };
+    constexpr int kEarly = 4;  // positions issued before the barrier
+#pragma unroll
+    for (int i = kP - 1; i >= kP - kEarly; --i) fetch_c(i);
+    __syncthreads();  // every chunk's summary map
+
+    // R at the chunk's end: d q_T through the later chunks' maps; then each position's share
+    // (R after the later positions, plus the position's d q_post, over N), rounded once to fp32
+    {
+        double Rx = a.dq_T ? double(a.dq_T[size_t(b) * d + col]) : 0.0;
+        double Ry = a.dq_T ? double(a.dq_T[size_t(b) * d + col + 1]) : 0.0;
+#pragma unroll
+        for (int j = kChunks - 1; j > 0; --j) {
+            if (j > ch) {
+                const bool rj = lds_ref<int32_t>(lds, Lo.rflag + 4u * j) != 0;
+                const double cx = lds_ref<double>(lds, Lo.rsum + 8u * (j * kS + 2 * cp));
+                const double cy = lds_ref<double>(lds, Lo.rsum + 8u * (j * kS + 2 * cp + 1));
+                Rx = (rj ? 0.0 : Rx) + cx;
+                Ry = (rj ? 0.0 : Ry) + cy;
+            }
+        }
+        double Rhx[2], Rhy[2];  // R at each half's end
+        Rhx[1] = Rx, Rhy[1] = Ry;
+        Rhx[0] = (wr[1] ? 0.0 : Rx) + wcx[1];
+        Rhy[0] = (wr[1] ? 0.0 : Ry) + wcy[1];
+        const double inv = double(divn.inv), nf = double(divn.n);
+#pragma unroll
+        for (int H = 0; H < 2; ++H) {
+            const double bx = (er[H] ? 0.0 : Rhx[H]) + ecx[H] + double(qb[H].x);
+            const double by = (er[H] ? 0.0 : Rhy[H]) + ecy[H] + double(qb[H].y);
+            const float sx = static_cast<float>(divn.pow2 ? bx * inv : bx / nf);
+            const float sy = static_cast<float>(divn.pow2 ? by * inv : by / nf);
+            lds_ref<float2>(lds, Lo.share + 4u * uint32_t((ch * kP + 8 * H + g) * kS + 2 * cp)) =
+                make_float2(sx, sy);
+        }
+        if (a.dq0 && ch == 0 && g == 0) {  // R after position 0
+            const double sx = (wr[0] ? 0.0 : Rhx[0]) + wcx[0], sy = (wr[0] ? 0.0 : Rhy[0]) + wcy[0];
+            a.dq0[size_t(b) * d + col] = static_cast<float>(sx);
+            a.dq0[size_t(b) * d + col + 1] = static_cast<float>(sy);
+        }
+    }
+    const uint32_t sh_base = Lo.share + 4u * uint32_t(ch * kP * kS + 2 * cp);
+    auto share_at = [&](int i) __attribute__((always_inline)) -> float2 {
+        return lds_ref<float2>(lds, sh_base + uint32_t(i) * kS * 4u);
+    };
+    const uint32_t lofs = uint32_t(cp) * 8u;
+    auto mu_at = [&](uint32_t e) __attribute__((always_inline)) -> float2& {
+        return lds_ref<float2>(lds, cbase + e * kEntBytes + lofs);
+    };
+    auto nu_at = [&](uint32_t e) __attribute__((always_inline)) -> float2& {
+        return lds_ref<float2>(lds, cbase + kEnt * kEntBytes + e * kEntBytes + lofs);
+    };
+    // zero the maps of entries [e_begin, kEv) (a reset: the entries created so far)
+    auto zero_from = [&](int e_begin, bool with_nu) __attribute__((always_inline)) {
+        for (int e = e_begin * 4 + hl; e < kEv * 4; e += 32) {
+            const uint32_t at = cbase + uint32_t(e >> 2) * kEntBytes + uint32_t(e & 3) * 8u;
+            lds_ref<float2>(lds, at) = make_float2(0.0f, 0.0f);
+            if (with_nu) lds_ref<float2>(lds, at + kEnt * kEntBytes) = make_float2(0.0f, 0.0f);
+        }
+    };
+
+    // compose the chunk's maps latest position first: mu' = (1 - b) mu, nu' = (1 - b) (nu + dsel)
+    // - b s, an entry's first (latest) event from (1, 0), or (0, 0) once a reset has passed; a
+    // reset zeroes the entries created so far. Idle and padded slots compose the identity on
+    // kDummy (their b s term is an exact zero, whatever the share holds).
+    auto compose = [&](auto rs_c) __attribute__((always_inline)) {
+        constexpr bool kRs = decltype(rs_c)::value;
+        float ainit = 1.0f;
+#pragma unroll
+        for (int i = kP - 1; i >= 0; --i) {
+            if (i - kEarly >= 0) fetch_c(i - kEarly);
+            const uint32_t e = ent(i);
+            const bool first = e == uint32_t(i * kK + k);
+            const float2 sh = share_at(i);
+            const float2 mu = mu_at(e), nu = nu_at(e);
+            const float2 o = omb[i];
+            const uint32_t vm = bitmask_at(vmask, i);
+            const float bsx = and_f32((1.0f - o.x) * sh.x, vm), bsy = and_f32((1.0f - o.y) * sh.y, vm);
+            mu_at(e) = make_float2(o.x * (first ? ainit : mu.x), o.y * (first ? ainit : mu.y));
+            nu_at(e) = make_float2(o.x * ((first ? 0.0f : nu.x) + dsv[i].x) - bsx,
+                                   o.y * ((first ? 0.0f : nu.y) + dsv[i].y) - bsy);
+            if (kRs && ((rmask >> i) & 1u)) {
+                zero_from(i * kK, true);
+                ainit = 0.0f;
+            }
+        }
+    };
+    const bool wave_rs = ballot(rmask != 0u) != 0u;
+    if (wave_rs) compose(std::true_type{});
+    else compose(std::false_type{});
+
+    __syncthreads();
+
+    // ---- phase B: every cell from d_h_T back through the 16 chunks, two threads a cell -------
+    {
+        uint32_t rflags = 0u;  // chunks with a reset
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j)
+            rflags |= lds_ref<int32_t>(lds, Lo.rflag + 4u * j) != 0 ? 1u << j : 0u;
+        rflags = uniform(rflags);
+        float* const dh0_row = a.dh0 ? a.dh0 + size_t(b) * N * d : nullptr;
+        const uint32_t qofs = uint32_t(bq) * 16u;
+        auto walk = [&](int cell, float4 s) __attribute__((always_inline)) {
+            const bool ok = cell < N;
+            const uint4 iw = lds_ref<uint4>(lds, Lo.idx + uint32_t(ok ? cell : N) * kChunks);
+            const uint32_t words[4] = {ok ? iw.x : ~0u, ok ? iw.y : ~0u, ok ? iw.z : ~0u, ok ? iw.w : ~0u};
+#pragma unroll
+            for (int jh = kChunks - kChunks / 4; jh >= 0; jh -= kChunks / 4) {  // four chunks at once
+                float4 mu[kChunks / 4], nu[kChunks / 4];
+#pragma unroll
+                for (int jj = 0; jj < kChunks / 4; ++jj) {
+                    const int j = jh + jj;
+                    const uint32_t ej = (words[j / 4] >> (8 * (j % 4))) & 0xffu;
+                    const uint32_t e = ej == kNone ? uint32_t(kDummy) : ej;  // the identity (1, 0)
+                    const uint32_t at = Lo.maps + uint32_t(j) * kMapBytes + e * kEntBytes + qofs;
+                    mu[jj] = lds_ref<float4>(lds, at);
+                    nu[jj] = lds_ref<float4>(lds, at + kEnt * kEntBytes);
+                }
+#pragma unroll
+                for (int jj = kChunks / 4 - 1; jj >= 0; --jj) {
+                    const int j = jh + jj;
+                    const uint32_t ej = (words[j / 4] >> (8 * (j % 4))) & 0xffu;
+                    // the entry's cotangent at the chunk's end, for the replay
+                    if (ej != kNone)
+                        lds_ref<float4>(lds, Lo.maps + uint32_t(j) * kMapBytes + ej * kEntBytes + qofs) = s;
+                    // a chunk with a reset ends at nu whatever came after (a select, not 0 * A)
+                    if ((rflags >> j) & 1u) s = nu[jj];
+                    else s = make_float4(mu[jj].x * s.x + nu[jj].x, mu[jj].y * s.y + nu[jj].y,
+                                         mu[jj].z * s.z + nu[jj].z, mu[jj].w * s.w + nu[jj].w);
+                }
+            }
+            if (ok && dh0_row)
+                *reinterpret_cast<float4*>(dh0_row + int64_t(cell) * d + slice * kS + 4 * bq) = s;
+        };
+        // the first 256 cells from the values loaded at the start, in straight-line code: a
+        // load inside the loop would make its first use wait for every load in flight, the
+        // replay's inputs included
+        walk(gl >> 1, dha);
+        for (int c0 = kWave * kWaves / 2; c0 < N; c0 += kWave * kWaves / 2)
+            walk(c0 + (gl >> 1), dhT_at(c0 + (gl >> 1)));
+    }
+    __syncthreads();
+
+    // ---- phase C: the replay, latest position first ------------------------------------------
+    // the selection cotangents move to the chunk's nu table (free after phase B): 32 lanes x 16
+    // positions x 8 bytes
+    const uint32_t ds_base = cbase + kEnt * kEntBytes + uint32_t(hl) * 8u;
+#pragma unroll
+    for (int i = 0; i < kP; ++i) lds_ref<float2>(lds, ds_base + uint32_t(i) * 256u) = dsv[i];
+    const rsrc_t rdy = make_rsrc(a.dy + orow, row_bytes);
+    const rsrc_t rdg = make_rsrc(a.dg + orow, row_bytes);
+    uint32_t vrow_c = vrow;
+    asm volatile("" : "+v"(vrow_c));  // recomputed here, not held from phase A's loads
+    auto replay = [&](auto rs_c) __attribute__((always_inline)) {
+        constexpr bool kRs = decltype(rs_c)::value;
+        float2 A = make_float2(0.0f, 0.0f);
+        if (!kRs) A = mu_at(ent(kP - 1));
+#pragma unroll
+        for (int i = kP - 1; i >= 0; --i) {
+            const uint32_t e = ent(i);
+            if (kRs) A = mu_at(e);
+            const float2 ds = lds_ref<float2>(lds, ds_base + uint32_t(i) * 256u);
+            const float2 sh = share_at(i);
+            const float2 o = omb[i];
+            const float2 carried = make_float2(A.x + ds.x, A.y + ds.y);
+            const float2 G = make_float2(carried.x + sh.x, carried.y + sh.y);
+            const float bgx = 1.0f - o.x, bgy = 1.0f - o.y;
+            mu_at(e) = make_float2(o.x * carried.x - bgx * sh.x, o.y * carried.y - bgy * sh.y);
+            // without a reset the next position's read goes out right after this write (its
+            // entry may be the one just written: LDS keeps one wave's accesses in order)
+            if (!kRs && i > 0) A = mu_at(ent(i - 1));
+            const float cx = fast_tanh(yv[i].x), cy = fast_tanh(yv[i].y);
+            const uint32_t vm = bitmask_at(vmask, i);
+            const float dcx = and_f32(bgx * (1.0f - cx * cx) * G.x, vm);
+            const float dcy = and_f32(bgy * (1.0f - cy * cy) * G.y, vm);
+            const float dbx = and_f32((cx - hv[i].x) * (o.x * bgx) * G.x, vm);
+            const float dby = and_f32((cy - hv[i].y) * (o.y * bgy) * G.y, vm);
+            const uint32_t vo = i < n ? vrow_c + uint32_t(i) * pos_bytes : kOob;
+            st2(make_float2(dcx, dcy), rdy, vo);
+            st2(make_float2(dbx, dby), rdg, vo);
+            if (kRs && ((rmask >> i) & 1u)) zero_from(0, false);  // every cotangent restarts at 0
+        }
+    };
+    if (wave_rs) replay(std::true_type{});
+    else replay(std::false_type{});
+}
+
 }  // namespace evmap
 }  // namespace hsn

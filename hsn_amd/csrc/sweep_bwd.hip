@@ -104,7 +104,10 @@ extern "C" int hsn_win_backward(const void* y, const void* gate_pre, const void*
         HSN_HIP(hipGetLastError());
         pre = rms_scratch;
     }
-    if (L.chain) {
+    if (L.evmap) {
+        evmap_backward(pre, gate_pre, h_old, slots, reset, d_q_pre, d_q_post, d_h_sel, d_h_T,
+                       d_q_T, dy, dgate, d_h0, d_q0, B, T, N, d, K, st);
+    } else if (L.chain) {
         chain_backward(pre, gate_pre, h_old, io_dtype, slots, reset, d_q_pre, d_q_post, d_h_sel,
                        d_h_T, d_q_T, dy, dgate, d_h0, d_q0, B, T, N, d, K, ws, L, st);
     } else {

@@ -262,8 +262,8 @@ def _align(n: int) -> int:
 @pytest.mark.parametrize("name", ["ref", "bf16", "tbptt", "skewed", "tiny"])
 def test_workspace_and_path_follow_the_shape(name):
     """The path a forward / backward call takes and the workspace it needs, host arithmetic
-    only: the event maps for an fp32 forward with d a multiple of 8, T <= 256, K <= 8 and the
-    tables of N cells in LDS (ref, tbptt, tiny), no workspace; otherwise the slices where a wavefront's piece of a slot row is a full 32-byte sector and the
+    only: the event maps for an fp32 forward or backward with d a multiple of 8, T <= 256, K <= 8
+    and the tables of N cells in LDS (ref, tbptt, tiny), no workspace; otherwise the slices where a wavefront's piece of a slot row is a full 32-byte sector and the
     state slice N * S is at most 2048 words (ref: 8 fp32 columns of 256 cells), the cell chains
     where the piece would be narrower (bf16: 4 bf16 columns, skewed: 2) or the slice larger
     (tbptt: 8 columns of 512 cells); the chain workspace is the row lists (B(N+1) + BTK int32), the per-position
@@ -284,7 +284,7 @@ def test_workspace_and_path_follow_the_shape(name):
     rms = _align(rms_scratch_bytes(B * T * K, d, elem))
     for op in (_lib.OP_FORWARD, _lib.OP_BACKWARD):
         evm = c.io == "f32" and d % 8 == 0 and T <= 256 and K <= 8 and N <= 512
-        auto = "evmap" if op == _lib.OP_FORWARD and evm else want
+        auto = "evmap" if evm else want
         assert _lib.path_for(op, B, T, N, d, K, io) == auto
         chain, table = 0, (0, 0)
         if auto == "chain":
@@ -302,23 +302,23 @@ def test_workspace_and_path_follow_the_shape(name):
         assert _lib.path_for(_lib.OP_FORWARD, B, T, N, d, K, io) == "slice"
     finally:
         _lib.set_path("auto")
-    # the event maps, when set: the forward only (fp32, d a multiple of 8, T <= 256, K <= 8),
-    # no workspace but the RMS input's; the backward keeps the automatic choice
+    # the event maps, when set: both directions (fp32, d a multiple of 8, T <= 256, K <= 8), no
+    # workspace but the RMS input's; a shape they do not take is refused with the reason
     try:
         _lib.set_path("evmap")
         takes = c.io == "f32" and d % 8 == 0 and T <= 256 and K <= 8
-        why = None
-        try:
-            got_path = _lib.path_for(_lib.OP_FORWARD, B, T, N, d, K, io)
-        except RuntimeError as e:
-            got_path, why = None, str(e)
-        if takes:
-            assert got_path == "evmap"
-            assert _lib.workspace_bytes(_lib.OP_FORWARD, B, T, N, d, K, io, False) == 0
-            assert _lib.workspace_bytes(_lib.OP_FORWARD, B, T, N, d, K, io, True) == rms
-        else:
-            assert "event-map path" in why
-        assert _lib.path_for(_lib.OP_BACKWARD, B, T, N, d, K, io) == want
+        for op in (_lib.OP_FORWARD, _lib.OP_BACKWARD):
+            why = None
+            try:
+                got_path = _lib.path_for(op, B, T, N, d, K, io)
+            except RuntimeError as e:
+                got_path, why = None, str(e)
+            if takes:
+                assert got_path == "evmap"
+                assert _lib.workspace_bytes(op, B, T, N, d, K, io, False) == 0
+                assert _lib.workspace_bytes(op, B, T, N, d, K, io, True) == rms
+            else:
+                assert "event-map path" in why
     finally:
         _lib.set_path("auto")
     lib = _lib.library()
