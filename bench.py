@@ -102,6 +102,41 @@ def _traffic(workload: str):
         return None
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (``/proc/cpuinfo``), as ``lscpu`` reports it."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def _copy_gbs(dev, mib: int = 512, reps: int = 5) -> float:
+    """A plain device copy's bandwidth (bytes read plus written per second, in GB/s), of a
+    buffer larger than the 256 MB Infinity Cache so that it streams from HBM: the bandwidth a
+    kernel of perfect access pattern reaches on this card, beside the 8 TB/s peak."""
+    import torch
+
+    src = torch.ones(mib * (1 << 20) // 4, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    secs = t0.elapsed_time(t1) * 1e-3
+    del src, dst
+    return 2.0 * mib * (1 << 20) * reps / secs / 1e9
+
+
 def _cpu_baseline(cfg, seed, min_seconds):
     """The CPU oracle on one full window of the configuration (or a prefix of its positions for
     the large configurations), on all host cores, repeated until ``min_seconds`` have passed."""
@@ -140,6 +175,7 @@ def _cpu_baseline(cfg, seed, min_seconds):
         "value": positions / secs,
         "unit": "positions/s",
         "cores": torch.get_num_threads(),
+        "cpu": _cpu_model(),
         "kind": "port",
         "sample": f"{reps} x ({sample.B} rows x {sample.T} positions of the {cfg.name} window), "
                   f"fwd+bwd, the repository's PyTorch-CPU oracle ({secs:.1f} s)",
@@ -486,7 +522,7 @@ def _ops_main(args) -> int:
     rnd_dv = rnd(B, K, 4 * d)
     busy = torch.empty(64 << 20, device=dev)
     busy_dst = torch.empty_like(busy)
-    per_call = {}
+    per_call, end_to_end = {}, {}
     with torch.no_grad():
         for name, fn in calls.items():
             for _ in range(max(1, args.warmup)):
@@ -503,12 +539,18 @@ def _ops_main(args) -> int:
             ev[1].record()
             torch.cuda.synchronize()
             per_call[name] = ev[0].elapsed_time(ev[1]) / args.steps * 1e3  # us
+            # end to end: the same calls from an idle queue, host dispatch included
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                fn()
+            torch.cuda.synchronize()
+            end_to_end[name] = (time.perf_counter() - t0) / args.steps * 1e6
     del busy, busy_dst
     mlp_us = per_call["grouped_unit_mlp"]
     flops = 2.0 * P * (4 * d * H + H * d)
     achieved = flops / (mlp_us * 1e-6) / 1e12
     result = {
-        "metric": f"grouped unit MLP forward calls/sec ({args.ops} size, 1 GPU)",
+        "metric": f"grouped unit MLP forward calls/sec of device time ({args.ops} size, 1 GPU)",
         "value": 1e6 / mlp_us,
         "unit": "calls/s",
         "n_gpus": 1,
@@ -527,6 +569,8 @@ def _ops_main(args) -> int:
                      "achieved": achieved, "peak": 157.3, "unit": "TFLOP/s",
                      "frac": achieved / 157.3, "traffic": None, "flops_per_call": flops},
         "us_per_call": per_call,
+        # the rate a Python caller reaches: host dispatch (the op wrappers and ctypes) included
+        "us_per_call_end_to_end": end_to_end,
     }
     if not args.no_cpu:  # the oracle's unit MLP on the same size, one thread
         from oracle import hsn_oracle as O
@@ -834,6 +878,10 @@ def main() -> int:
         "window_gbs": window_gbs,
         "window_frac": window_gbs / HBM_PEAK_GBS,
     }
+    copy_gbs = _copy_gbs(dev)  # after the timed region
+    result["copy_gbs"] = copy_gbs
+    result["roofline"]["frac_of_copy"] = achieved / copy_gbs
+    result["window_frac_of_copy"] = window_gbs / copy_gbs
     if args.calibrate_copy > 0:  # outside the timed region: a plain copy of known size
         src = torch.ones(args.calibrate_copy * (1 << 20) // 4, device=dev)
         dst = torch.empty_like(src)

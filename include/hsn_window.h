@@ -73,18 +73,18 @@ int hsn_win_supports(int op, int B, int T, int N, int d, int K);
  *   HSN_PATH_CHAIN  cell chains (a wavefront per cell walks the cell's events in time; whole
  *                   slot rows per load and store; the summary by a scan over time): any N, K
  *                   up to 255, d up to 256;
- *   HSN_PATH_EVMAP  event maps, forward only (a workgroup per row and 8 columns; a chunk of 16
+ *   HSN_PATH_EVMAP  event maps (a workgroup per row and 8 columns; a chunk of up to 16
  *                   positions per half-wavefront composes each touched cell's affine map over
  *                   the chunk, every cell is walked through the 16 chunks' maps, then each chunk
- *                   replays its positions from the cells' start values): fp32 rows, d a
- *                   multiple of 8, T <= 256, K <= 8, the tables of N cells within the LDS
- *                   (N up to about 1000); no workspace.
+ *                   replays its positions from the cells' values at its edge; the backward
+ *                   runs the same steps in reverse time after an fp64 scan of the summary
+ *                   cotangent): fp32 rows, d a multiple of 8, T <= 256, K <= 8, the tables of
+ *                   N cells within the LDS (N up to about 1000); no workspace.
  * hsn_win_set_path fixes the path of every later hsn_win_forward / hsn_win_forward_noalloc /
- * hsn_win_backward call of the process. HSN_PATH_AUTO, the default: for the forward the event
- * maps where they take the shape; otherwise the slices where their piece is a full sector and
- * N * S <= 2048, else the chains. HSN_PATH_EVMAP forced leaves the backward to that automatic
- * choice. hsn_win_path reports the path a call of `op` (HSN_OP_FORWARD or HSN_OP_BACKWARD)
- * would take, or the reason none takes the shape.
+ * hsn_win_backward call of the process. HSN_PATH_AUTO, the default: the event maps where they
+ * take the shape; otherwise the slices where their piece is a full sector and N * S <= 2048,
+ * else the chains. hsn_win_path reports the path a call of `op` (HSN_OP_FORWARD or
+ * HSN_OP_BACKWARD) would take, or the reason none takes the shape.
  */
 #define HSN_PATH_AUTO 0
 #define HSN_PATH_SLICE 1

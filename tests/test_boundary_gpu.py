@@ -321,3 +321,119 @@ def test_update_fold_is_update_tape_and_the_next_row(mods, cuda_device, x_dtype,
             assert bool((x[others].float() == 7.0).all())
         else:
             assert bool((x.float() == 7.0).all())
+
+
+@pytest.mark.parametrize("x_dtype,cand_norm", [(torch.float32, True), (torch.bfloat16, False)])
+def test_folded_sweep_walks_a_block_like_the_oracle(mods, cuda_device, x_dtype, cand_norm):
+    """The folded sweep as the reference's model runs it over a block (``select_fold`` ->
+    ``update_fold`` position by position, the logits read in place from a wider scorer product,
+    a bf16 ``y``, the gate a strided view of a wider fp32 product), against the oracle's
+    per-position chain (``reset -> Router.select -> candidate / gate -> gated update -> tick``,
+    the state in float64): resets at the block's first, interior and last positions and two in
+    a row, two reserved cells with fixed units, probes on the ages, a row budget that pads
+    slots, and the fast read of the first three cells into each next row of ``x``. Decisions
+    and ages bit for bit; states, summaries, maxima and the folded rows within 1e-5 (fp32
+    ``x``) or one bf16 rounding."""
+    from oracle import hsn_oracle as O
+
+    from hsn_amd.window import BUDGET_SLACK
+
+    _, window = mods
+    dev = cuda_device
+    g = torch.Generator().manual_seed(71)
+    B, n, N, M, d, K, d_z, d_c, n_fast, pad = 4, 9, 30, 2, 16, 6, 5, 3, 3, 4
+    cost = torch.tensor([0.03125, 0.046875])
+    keys = dict(age_max=3, probes=True, lambda_cost=0.0, cell_overhead=0.0, shared_cost=0.0,
+                limit=0.12 * (1.0 + BUDGET_SLACK), reserved=2, reserved_units=True)
+    cand_w = torch.rand(d, generator=g) + 0.5
+    eps = 1e-6
+    reset = torch.zeros(B, n, dtype=torch.bool)
+    reset[0, 0] = True
+    reset[1, 4] = True
+    reset[2, n - 1] = True
+    reset[3, 2] = reset[3, 3] = True
+    h0 = torch.rand(B, N, d, generator=g) * 1.6 - 0.8
+    q0 = h0.mean(dim=1)
+    age0 = torch.randint(0, 6, (B, N), generator=g)
+    pos0 = torch.randint(0, 9, (B,), generator=g)
+    logits = torch.randn(B, n, N, M, generator=g)
+    ys = torch.randn(B, n, K, d, generator=g).to(torch.bfloat16)  # the product as the model has it
+    gates = torch.randn(n, B * K, d + pad, generator=g)  # the gate: columns pad.. of a wider product
+    z = torch.randn(B, n, d_z, generator=g).to(x_dtype)
+    ctx = torch.randn(B, n, d_c, generator=g)
+
+    # the oracle: float64 state, decisions from the fp32 logits and the integer ages
+    h, q, age, pos = h0.double(), q0.double(), age0.clone(), pos0.clone()
+    rec = {k: [] for k in ("h", "q", "age", "cells", "units", "valid", "theta", "refreshed",
+                           "q_post", "h_sel", "h_max")}
+    for t in range(n):
+        h, q, age, pos = O.reset_state(h, q, age, pos, reset[:, t])
+        rec["h"].append(h), rec["q"].append(q), rec["age"].append(age)
+        cells, units, valid, theta, refreshed = O.router_select(logits[:, t], age, cost, k=K, **keys)
+        gate_t = gates[t, :, pad:].reshape(B, K, d)
+        h, q, age, pos, h_sel, h_max, _ = O.cell_update(
+            ys[:, t].float(), gate_t, h, q, age, pos, cells, valid, cand_norm=cand_norm,
+            cand_w=cand_w.double() if cand_norm else None, cand_eps=eps)
+        for k_, v_ in (("cells", cells), ("units", units), ("valid", valid), ("theta", theta),
+                       ("refreshed", refreshed), ("q_post", q), ("h_sel", h_sel),
+                       ("h_max", h_max)):
+            rec[k_].append(v_)
+    rec["h"].append(h), rec["q"].append(q), rec["age"].append(age)  # the block's end
+    assert any(bool(v.all()) is False for v in rec["valid"])  # the budget padded some slots
+
+    # the GPU: the tapes, record 0 the start state after the first reset
+    first = O.reset_state(h0, q0, age0, pos0, reset[:, 0])
+    tape_h = torch.full((B, n + 1, N, d), 7.0, device=dev)
+    tape_q = torch.full((B, n + 1, d), 7.0, device=dev)
+    tape_age = torch.full((B, n + 1, N), 7, dtype=torch.int64, device=dev)
+    tape_h[:, 0], tape_q[:, 0], tape_age[:, 0] = first[0].to(dev), first[1].to(dev), first[2].to(dev)
+    cells = torch.zeros(B, n, K, dtype=torch.int64, device=dev)
+    units = torch.zeros(B, n, K, dtype=torch.int64, device=dev)
+    valid = torch.zeros(B, n, K, dtype=torch.bool, device=dev)
+    refreshed = torch.zeros(B, n, K, dtype=torch.bool, device=dev)
+    theta = torch.zeros(B, n, device=dev)
+    h_sel = torch.zeros(B, n, K, d, device=dev)
+    h_max = torch.zeros(B, n, device=dev)
+    qs = torch.zeros(B, n, d, device=dev)
+    x = torch.full((n, B, d_z + d + d_c + d), 7.0, device=dev).to(x_dtype)
+    zd, ctxd, cw, rd = z.to(dev), ctx.to(dev), cand_w.to(dev), reset.to(dev)
+    gd = gates.to(dev)
+    for t in range(n):
+        scored = torch.cat([logits[:, t].reshape(B * N, M), torch.randn(B * N, 3, generator=g)],
+                           dim=1).to(dev)  # the logits in the product's first M columns
+        window.select_fold_op(scored, tape_age, cost.to(dev), cells, units, valid, theta,
+                              refreshed, t, M, keys["age_max"], keys["probes"],
+                              keys["lambda_cost"], keys["cell_overhead"], keys["shared_cost"],
+                              keys["limit"], keys["reserved"], keys["reserved_units"])
+        window.update_fold_op(ys[:, t].to(dev), gd[t, :, pad:], tape_h, tape_q, tape_age, cells,
+                              valid, cw, rd, h_sel, h_max, qs, x, zd, ctxd, t, cand_norm, eps,
+                              n_fast)
+    torch.cuda.synchronize()
+
+    for name, got in (("cells", cells), ("units", units), ("valid", valid),
+                      ("refreshed", refreshed), ("theta", theta)):
+        want = torch.stack(rec[name], dim=1)
+        got = got.cpu()
+        if name in ("cells", "units"):  # padded slots: the router's placeholders
+            got, want = got.masked_fill(~valid.cpu(), 0), want.masked_fill(~valid.cpu(), 0)
+        assert torch.equal(got, want), name
+    assert torch.equal(tape_age.cpu(), torch.stack(rec["age"], dim=1))
+    tol = dict(atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(tape_h.cpu().double(), torch.stack(rec["h"], dim=1), **tol)
+    torch.testing.assert_close(tape_q.cpu().double(), torch.stack(rec["q"], dim=1), **tol)
+    torch.testing.assert_close(qs.cpu().double(), torch.stack(rec["q_post"], dim=1), **tol)
+    torch.testing.assert_close(h_max.cpu().double(), torch.stack(rec["h_max"], dim=1), **tol)
+    vm = valid.cpu()[..., None]
+    torch.testing.assert_close(torch.where(vm, h_sel.cpu().double(), 0.0),
+                               torch.where(vm, torch.stack(rec["h_sel"], dim=1), 0.0), **tol)
+    # the folded rows: record t + 1's [z; q; context; mean of cells 0 .. n_fast - 1]
+    for t in range(n - 1):
+        hr, qr = rec["h"][t + 1], rec["q"][t + 1]
+        fast = hr[:, :n_fast].sum(dim=1) / n_fast
+        want = torch.cat([z[:, t + 1].double(), qr, ctx[:, t + 1].double(), fast], dim=1)
+        xt = x[t + 1].cpu().double()
+        if x_dtype == torch.float32:
+            torch.testing.assert_close(xt, want, **tol)
+        else:  # one rounding to bf16 of values within fp32 error of the oracle's
+            torch.testing.assert_close(xt, want, atol=1e-2, rtol=8e-3)
+    assert bool((x[0].float() == 7.0).all())  # record 0 is the caller's

@@ -270,11 +270,14 @@ def test_window_forward_and_backward_match_oracle(dev, path, case):
     _close(got["h"], want["h"], tol, "h_T")
     _close(got["q"], want["q"], tol, "q_T")
 
-    # backward from the same tape (the oracle's h_old), cotangents masked by valid for h_sel
+    # backward from the same tape (the oracle's h_old), cotangents masked by valid for h_sel; the
+    # oracle in float64 for fp32 rows (its inputs are the fp32 values the GPU reads)
     d_h_sel = _valid_mask(cot["d_h_sel"], want["valid"])
-    wb = O.window_backward(w["y"], w["gate_pre"], want["h_old"], want["cells"], want["valid"],
-                           w["reset"], cfg_w.N, cot["d_q_pre"], cot["d_q_post"], d_h_sel,
-                           cot["d_h_T"], cot["d_q_T"], cand_norm=rms, cand_w=cand_w)
+    up = (lambda t: None if t is None else t.double()) if c["io"] == "f32" else (lambda t: t)  # noqa: E731
+    wb = O.window_backward(up(w["y"]), up(w["gate_pre"]), up(want["h_old"]), want["cells"],
+                           want["valid"], w["reset"], cfg_w.N, up(cot["d_q_pre"]),
+                           up(cot["d_q_post"]), up(d_h_sel), up(cot["d_h_T"]), up(cot["d_q_T"]),
+                           cand_norm=rms, cand_w=up(cand_w))
     gb = window.backward(D["y"], D["gate_pre"], want["h_old"].to(dev), got["slots"],
                          D["reset"], cfg_w.N, cot["d_q_pre"].to(dev),
                          cot["d_q_post"].to(dev), d_h_sel.to(dev), cot["d_h_T"].to(dev),
@@ -284,8 +287,8 @@ def test_window_forward_and_backward_match_oracle(dev, path, case):
         _close(g_, w_, tol, name)
     _close(gb[3], _d_q0_exact(w["reset"], cot["d_q_pre"], cot["d_q_post"], cot["d_q_T"], cfg_w.N),
            tol, "d_q0")
-    if rms:
-        _close(gb[4], wb[4], tol * 10, "d_cand_w")  # a sum over every slot of the window
+    if rms:  # a sum over every slot of the window: fp32 against float64 at the same bar
+        _close(gb[4], wb[4], tol if c["io"] == "f32" else tol * 10, "d_cand_w")
     zero_pad = ~want["valid"]
     assert bool((gb[0].cpu()[zero_pad] == 0).all()) and bool((gb[1].cpu()[zero_pad] == 0).all())
 
@@ -558,7 +561,7 @@ def test_window_recurrence_autograd_carries_across_windows(dev):
                                   wh.double())
     want = torch.autograd.grad(total, [y1c, g1c, h0c, q0c, y2c, g2c])
     for name, g_, w_ in zip(("dy1", "dg1", "dh0", "dq0", "dy2", "dg2"), got, want):
-        _close(g_, w_, 2e-5, name)
+        _close(g_, w_, 1e-5, name)
 
 
 def _two_window_objective(w1, w2, y1, g1, h0, q0, y2, g2, cost, wq, wh):
