@@ -81,6 +81,9 @@ bool evmap_takes(int op, int B, int T, int N, int d, int K, size_t elem, const c
     return r == nullptr;
 }
 
+// MI355X's compute units: the event maps' grid in one round
+constexpr int64_t kEvmapOneRound = 256;
+
 int choose_path(int op, int B, int T, int N, int d, int K, size_t elem) {
     const char* why_s = nullptr;
     const char* why_c = nullptr;
@@ -90,9 +93,14 @@ int choose_path(int op, int B, int T, int N, int d, int K, size_t elem) {
     const bool e_ok = (any || setting == kPathEvmap) && evmap_takes(op, B, T, N, d, K, elem, &why_e);
     if (setting == kPathEvmap && !e_ok)
         throw AbiError{HSN_ERR_INVALID_ARGUMENT, std::string("(event-map path) ") + why_e};
-    // The event maps first where they take the shape: at B32 T256 N256 d64 K8 fp32 both
-    // directions move their rows as two columns a lane with a chunk per half-wavefront.
-    if (e_ok) return kPathEvmap;
+    // The event maps first where they take the shape and their grid of B d / 8 workgroups (one
+    // a CU: the maps hold most of the LDS) runs in one round on MI355X's 256 CUs: every
+    // workgroup carries a fixed cost (the tables, the walk over all N cells), which a single
+    // round pays once. Measured: B32 T256 N256 d64 K8 fp32 (256 workgroups) 28.2 + 28.3 us
+    // against the slices' 30.2 + 29.0; B128 T128 N512 d128 K8 fp32 (2048, eight rounds) 213 +
+    // 240 us against the chains' 127 + 139.
+    if (e_ok && (setting == kPathEvmap || int64_t(B) * (d / evmap::kS) <= kEvmapOneRound))
+        return kPathEvmap;
     const bool s_ok = (any || setting == kPathSlice) && slice_takes(op, B, T, N, d, K, &why_s);
     const bool c_ok = (any || setting == kPathChain) && chain_takes(B, T, N, d, K, &why_c);
     if (!s_ok && !c_ok) {

@@ -43,13 +43,14 @@ constexpr uint32_t kEntBytes = kS * 4;                 // one entry's 8 columns
 constexpr uint32_t kMapBytes = 2u * kEnt * kEntBytes;  // a chunk's alpha and beta tables
 
 // LDS byte offsets: the chunks' maps [16][alpha, beta][kEnt][8] f32 (alpha becomes the entry's
-// value in phase C), the first-event table [N + 1][16] u8 (row N: where idle and padded slots
-// write), the entries' current maxima [16][kEnt] u32 (|h| bits), the ages' last selections
-// [N + 1] i32, per chunk its untouched cells' maximum and last reset, each chunk's summary map
+// value in phase C), the first-event table [N + 1][16] u8 (row N: kDummy, read by idle and
+// padded slots), the entries' current maxima [16][kEnt] u32 (|h| bits), the last-event table
+// [N + 1][16] u8 (the ages), per chunk its untouched cells' maximum and last reset, each chunk's
+// summary map
 // q -> (reset ? 0 : q) + c ([16][8] c and [16] reset flags) and start q [16][8], and 8 bytes a
 // thread where a lane with nothing to store writes.
 struct Layout {
-    uint32_t maps, idx, cmx, last, umax, rlast, qmap, qreset, qstart, tdummy, bytes;
+    uint32_t maps, idx, cmx, lastev, umax, rlast, qmap, qreset, qstart, tdummy, bytes;
 };
 
 __host__ __device__ inline Layout fwd_layout(int N) {
@@ -61,8 +62,8 @@ __host__ __device__ inline Layout fwd_layout(int N) {
     at += (uint32_t(N + 1) * kChunks + 15u) & ~15u;
     L.cmx = at;
     at += kChunks * kEnt * 4u;
-    L.last = at;
-    at += (uint32_t(N + 1) * 4u + 15u) & ~15u;
+    L.lastev = at;
+    at += (uint32_t(N + 1) * kChunks + 15u) & ~15u;
     L.umax = at;
     at += kChunks * 4u;
     L.rlast = at;
@@ -237,18 +238,22 @@ __global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
 #pragma unroll
     for (int i = 0; i < kAhead; ++i) fetch(i);
 
-    // the tables' initial values, while the loads are in flight
-    for (int e = gl; e < (N + 1) * kChunks / 4; e += kWave * kWaves)
-        lds_ref<uint32_t>(lds, Lo.idx + 4u * e) = e < N * kChunks / 4 ? 0xffffffffu : kDummy * 0x01010101u;
-    for (int e = gl; e < kChunks * kEnt; e += kWave * kWaves) lds_ref<uint32_t>(lds, Lo.cmx + 4u * e) = 0u;
-    if (gl < kChunks) lds_ref<uint32_t>(lds, Lo.umax + 4u * gl) = 0u;
-    if (gl < kChunks * kS) {  // the dummy entries hold the identity map (idle slots compose it)
-        const uint32_t at = Lo.maps + uint32_t(gl / kS) * kMapBytes + kDummy * kEntBytes + 4u * (gl % kS);
-        lds_ref<float>(lds, at) = 1.0f;
-        lds_ref<float>(lds, at + kEnt * kEntBytes) = 0.0f;
-    }
+    // this chunk's columns of the tables while the loads are in flight (no other half-wave
+    // reads them before phase B): no event (0xff; kDummy in row N) in the first-event table and
+    // in the last-event table, zero maxima, the dummy entry's identity map (1, 0) that idle slots
+    // compose, and the chunk's untouched maximum (phase B max-reduces into it)
+    unsigned char* const idx = lds + Lo.idx;
+    for (int c = hl; c <= N; c += 32) idx[c * kChunks + ch] = c < N ? 0xffu : uint8_t(kDummy);
     if (track_age)
-        for (int e = gl; e <= N; e += kWave * kWaves) lds_ref<int32_t>(lds, Lo.last + 4u * e) = -1;
+        for (int c = hl; c < N; c += 32) lds[Lo.lastev + uint32_t(c * kChunks + ch)] = 0xffu;
+    const uint32_t cmx_base = Lo.cmx + uint32_t(ch) * kEnt * 4u;
+    for (int e = hl; e < kEnt; e += 32) lds_ref<uint32_t>(lds, cmx_base + 4u * e) = 0u;
+    const uint32_t cbase = Lo.maps + uint32_t(ch) * kMapBytes;
+    if (hl < kS) {
+        lds_ref<float>(lds, cbase + kDummy * kEntBytes + 4u * hl) = 1.0f;
+        lds_ref<float>(lds, cbase + kEnt * kEntBytes + kDummy * kEntBytes + 4u * hl) = 0.0f;
+    }
+    if (hl == 0) lds_ref<uint32_t>(lds, Lo.umax + 4u * ch) = 0u;
 
     float2 omb[kP], bcv[kP];
     uint32_t vmask = 0u, pmask = 0u;  // valid and padded positions of this lane's slot
@@ -267,12 +272,10 @@ __global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
         cv[i] = ok ? c : N;  // the first-event table's row (N: the idle slots' row)
     }
     const uint32_t rmask = static_cast<uint32_t>(ballot(rbyte != 0) >> (32 * half));
-    __syncthreads();  // the tables are initialised
 
     // first events: every event writes its index into its cell's byte of this chunk, latest
     // position first, so each byte ends with the cell's first event; one lane a slot writes,
     // the others into their own dummy byte; idle and padded slots read row N (kDummy)
-    unsigned char* const idx = lds + Lo.idx;
     const uint32_t my_dummy = Lo.tdummy + 8u * uint32_t(gl);
 #pragma unroll
     for (int i = kP - 1; i >= 0; --i)
@@ -293,12 +296,13 @@ __global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
     auto rent = [&](int i) __attribute__((always_inline)) -> uint32_t {
         return (rentw[i / 4] >> (8 * (i % 4))) & 0xffu;
     };
-    if (track_age && cp == 0)
+    if (track_age)  // last events, earliest position first: each byte ends with the last one
 #pragma unroll
-        for (int i = 0; i < kP; ++i) atomicMax(&lds_ref<int32_t>(lds, Lo.last + 4u * cv[i]), t0 + i);
+        for (int i = 0; i < kP; ++i)
+            lds[(vmask >> i) & 1u && cp == 0 ? Lo.lastev + uint32_t(cv[i] * kChunks + ch) : my_dummy] =
+                static_cast<unsigned char>(i * kK + k);
     if (hl == 0) lds_ref<int32_t>(lds, Lo.rlast + 4u * ch) = rmask ? t0 + 31 - __builtin_clz(rmask) : -1;
 
-    const uint32_t cbase = Lo.maps + uint32_t(ch) * kMapBytes;
     const uint32_t lofs = uint32_t(cp) * 8u;
     auto al_at = [&](uint32_t e) __attribute__((always_inline)) -> float2& {
         return lds_ref<float2>(lds, cbase + e * kEntBytes + lofs);
@@ -409,7 +413,15 @@ __global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
         int64_t* const ageT_row = a.age_T + size_t(b) * N;
         const int64_t* const age0_row = a.age0 + size_t(b) * N;
         for (int c = gl; c < N; c += kWave * kWaves) {
-            const int ls = lds_ref<int32_t>(lds, Lo.last + 4u * c);
+            // the cell's last selection: the latest chunk with an event, at that event's position
+            const uint4 lw = lds_ref<uint4>(lds, Lo.lastev + uint32_t(c) * kChunks);
+            const uint32_t words[4] = {lw.x, lw.y, lw.z, lw.w};
+            int ls = -1;
+#pragma unroll
+            for (int j = 0; j < kChunks; ++j) {
+                const uint32_t e = (words[j / 4] >> (8 * (j % 4))) & 0xffu;
+                ls = e != kNone ? j * P + int(e / kK) : ls;
+            }
             int64_t age;
             if (ls >= 0 && ls >= last_reset) age = (T - 1) - ls;
             else if (last_reset >= 0) age = T - last_reset;
@@ -430,7 +442,6 @@ __global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
     const rsrc_t rhs = make_rsrc(a.h_sel ? a.h_sel + orow : nullptr, a.h_sel ? uint32_t(T) * pos_bytes : 0u);
     const rsrc_t rqa = make_rsrc(a.q_pre ? a.q_pre + size_t(b) * T * d : nullptr, a.q_pre ? uint32_t(T) * d * 4u : 0u);
     const rsrc_t rqb = make_rsrc(a.q_post ? a.q_post + size_t(b) * T * d : nullptr, a.q_post ? uint32_t(T) * d * 4u : 0u);
-    const uint32_t cmx_base = Lo.cmx + uint32_t(ch) * kEnt * 4u;
     const bool wave_pad = ballot(pmask != 0u) != 0u;
     uint32_t vrow_c = vrow;
     asm volatile("" : "+v"(vrow_c));  // recomputed here, not held from phase A's loads

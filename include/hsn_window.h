@@ -82,8 +82,8 @@ int hsn_win_supports(int op, int B, int T, int N, int d, int K);
  *                   N cells within the LDS (N up to about 1000); no workspace.
  * hsn_win_set_path fixes the path of every later hsn_win_forward / hsn_win_forward_noalloc /
  * hsn_win_backward call of the process. HSN_PATH_AUTO, the default: the event maps where they
- * take the shape; otherwise the slices where their piece is a full sector and N * S <= 2048,
- * else the chains. hsn_win_path reports the path a call of `op` (HSN_OP_FORWARD or
+ * take the shape and their B * d / 8 workgroups run in one round of the 256 CUs; otherwise the
+ * slices where their piece is a full sector and N * S <= 2048, else the chains. hsn_win_path reports the path a call of `op` (HSN_OP_FORWARD or
  * HSN_OP_BACKWARD) would take, or the reason none takes the shape.
  */
 #define HSN_PATH_AUTO 0

@@ -262,8 +262,9 @@ def _align(n: int) -> int:
 @pytest.mark.parametrize("name", ["ref", "bf16", "tbptt", "skewed", "tiny"])
 def test_workspace_and_path_follow_the_shape(name):
     """The path a forward / backward call takes and the workspace it needs, host arithmetic
-    only: the event maps for an fp32 forward or backward with d a multiple of 8, T <= 256, K <= 8
-    and the tables of N cells in LDS (ref, tbptt, tiny), no workspace; otherwise the slices where a wavefront's piece of a slot row is a full 32-byte sector and the
+    only: the event maps for an fp32 forward or backward with d a multiple of 8, T <= 256, K <= 8,
+    the tables of N cells in LDS and a grid of B d / 8 workgroups within one round of the 256
+    CUs (ref, tiny), no workspace; otherwise the slices where a wavefront's piece of a slot row is a full 32-byte sector and the
     state slice N * S is at most 2048 words (ref: 8 fp32 columns of 256 cells), the cell chains
     where the piece would be narrower (bf16: 4 bf16 columns, skewed: 2) or the slice larger
     (tbptt: 8 columns of 512 cells); the chain workspace is the row lists (B(N+1) + BTK int32), the per-position
@@ -283,7 +284,8 @@ def test_workspace_and_path_follow_the_shape(name):
     B, T, N, d, K = c.B, c.T, c.N, c.d, c.K
     rms = _align(rms_scratch_bytes(B * T * K, d, elem))
     for op in (_lib.OP_FORWARD, _lib.OP_BACKWARD):
-        evm = c.io == "f32" and d % 8 == 0 and T <= 256 and K <= 8 and N <= 512
+        evm = (c.io == "f32" and d % 8 == 0 and T <= 256 and K <= 8 and N <= 512
+               and B * (d // 8) <= 256)  # the grid in one round of the 256 CUs
         auto = "evmap" if evm else want
         assert _lib.path_for(op, B, T, N, d, K, io) == auto
         chain, table = 0, (0, 0)
