@@ -7,6 +7,8 @@
 // results are reproducible run to run whatever `deterministic` says.
 #include "common.cuh"
 
+#include <type_traits>
+
 namespace hsn {
 
 namespace {
@@ -190,6 +192,36 @@ __global__ __launch_bounds__(256) void gather_bwd(const F* grad_v, const int32_t
     grad_eps[int64_t(r) * d + x] = from_f32<F>(se);
 }
 
+// The 16-bit gather backward: a repeated cell's grad_h is the fp32 sum over its slots in slot
+// order, rounded once to F (the ABI's accumulation). A thread per (row, column) walks the slots;
+// each slot writes its cell's sum over the slots up to it (the same cells found by a scan of the
+// earlier slots), so the cell's last slot writes the whole sum.
+template <typename F>
+__global__ __launch_bounds__(256) void gather_bwd_narrow(const F* grad_v, const int32_t* cell_idx,
+                                                         F* grad_u, F* grad_eps, F* grad_h,
+                                                         F* grad_m, int B, int N, int d, int K) {
+    const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= int64_t(B) * d) return;
+    const int r = static_cast<int>(e / d), x = static_cast<int>(e - int64_t(r) * d);
+    const int64_t w = 4 * int64_t(d);
+    const int32_t* cells = cell_idx + int64_t(r) * K;
+    const F* gv = grad_v + int64_t(r) * K * w;
+    float su = 0.0f, se = 0.0f;
+    for (int i = 0; i < K; ++i) {
+        const F* g = gv + i * w;
+        su += to_f32(g[x]);
+        se += to_f32(g[d + x]);
+        grad_m[(int64_t(r) * K + i) * d + x] = g[3 * d + x];
+        const int c = cells[i];
+        float sum = 0.0f;
+        for (int j = 0; j <= i; ++j)
+            if (cells[j] == c) sum += to_f32(gv[j * w + 2 * d + x]);
+        grad_h[(int64_t(r) * N + c) * d + x] = from_f32<F>(sum);
+    }
+    grad_u[int64_t(r) * d + x] = from_f32<F>(su);
+    grad_eps[int64_t(r) * d + x] = from_f32<F>(se);
+}
+
 inline int grid_of(int64_t n) { return static_cast<int>((n + 255) / 256); }
 
 }  // namespace
@@ -268,7 +300,10 @@ struct RunGatherBwd {
         const int64_t n = int64_t(B) * N * d;
         hipLaunchKernelGGL((copy_or_zero<F>), dim3(grid_of(n)), dim3(256), 0, st,
                            static_cast<const F*>(nullptr), static_cast<F*>(grad_h), n);
-        hipLaunchKernelGGL((gather_bwd<F>), dim3(grid_of(int64_t(B) * d)), dim3(256), 0, st,
+        // fp32 rows: repeats forwarded in registers in slot order (exact); 16-bit rows: each
+        // cell's sum kept in fp32 and rounded once
+        auto kernel = std::is_same<F, float>::value ? gather_bwd<F> : gather_bwd_narrow<F>;
+        hipLaunchKernelGGL(kernel, dim3(grid_of(int64_t(B) * d)), dim3(256), 0, st,
                            static_cast<const F*>(grad_v), cell_idx, static_cast<F*>(grad_u),
                            static_cast<F*>(grad_eps), static_cast<F*>(grad_h),
                            static_cast<F*>(grad_m), B, N, d, K);

@@ -118,6 +118,34 @@ def test_gather_backward_slot_batches_match_oracle(ops, cuda_device, dtype):
         _close(g_, w_, dtype, name)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gather_backward_rounds_a_repeated_cell_once(ops, cuda_device, dtype):
+    """A cell taken by many slots of a row in 16-bit storage: its grad_h is the fp32 sum of the
+    slots' third blocks in slot order, rounded once to the storage dtype (the ABI's accumulation),
+    not a rounding after every repeat. 40 slots, 30 of them on cell 2 (five of the kernel's
+    batches of 8), with small values that a per-repeat rounding would lose."""
+    g = torch.Generator().manual_seed(93)
+    B, N, K, d = 2, 9, 40, 24
+    grad_v = torch.randn(B, K, 4 * d, generator=g)
+    grad_v[:, :, 2 * d:3 * d] = 1.0 + torch.rand(B, K, d, generator=g) * 2.0 ** -6
+    grad_v = grad_v.to(dtype)
+    cells = torch.randint(0, N, (B, K), generator=g, dtype=torch.int32)
+    cells[:, torch.randperm(K, generator=g)[:30]] = 2
+    # the expectation: slot-order fp32 sums per (row, cell), each rounded once
+    want = torch.zeros(B, N, d)
+    third = grad_v[:, :, 2 * d:3 * d].float()
+    for r in range(B):
+        acc = {}
+        for k in range(K):
+            c = int(cells[r, k])
+            acc[c] = acc.get(c, torch.zeros(d)) + third[r, k]
+        for c, v in acc.items():
+            want[r, c] = v
+    want = want.to(dtype)
+    got = ops.gather_backward(grad_v.to(cuda_device), cells.to(cuda_device), N)[2].cpu()
+    assert torch.equal(got, want)
+
+
 def test_gather_autograd_matches_golden(ops, cuda_device):
     v = load_golden("odd_gather_concat.safetensors")
     D = _put(v, cuda_device, torch.float32)
