@@ -647,3 +647,60 @@ def test_ref_shape_window_rows_match_oracle(dev, path):
     _close(g1[3][rows], _d_q0_exact(sub["reset"], csub["d_q_pre"], csub["d_q_post"],
                                     csub["d_q_T"], cfg_w.N), F32_TOL, "d_q0")
     assert math.isfinite(float(got["h_max"].max()))
+
+
+@pytest.mark.parametrize("path", ["evmap", "slice"])
+def test_backward_resets_at_chunk_edges_and_padded_nans(dev, path):
+    """The backward's chunked maps at their edges, on the ref shape's sizes (T = 256: sixteen
+    chunks of 16 positions on the event maps, eight of 32 on the slices) for two rows.
+    - Resets at position 0, at the last position of a chunk (15), at the first of the next (16)
+      and at the window's last position (255); two in a row (127, 128) on the other row.
+    - NaN and inf in the padded slots' y, gate and h_old (the slots write exact zeros and add
+      nothing).
+    - A NaN summary cotangent at a position the later reset cuts off from everything before it.
+    Against the float64 oracle, d_q0 against the exact sum."""
+    from hsn_amd import _lib, window
+
+    cfg_w, w, cot, cost, cfg, _ = _window_case(dict(B=2, T=256, N=256, d=64, K=8, io="f32",
+                                                    limit=0.02), 4242)  # 5 of 8 slots valid
+    reset = torch.zeros(2, 256, dtype=torch.bool)
+    reset[0, [0, 15, 16, 255]] = True
+    reset[1, [127, 128]] = True
+    fw = O.window_forward(w["logits"], w["y"], w["gate_pre"], reset, w["h0"], w["q0"], w["age0"],
+                          w["pos0"], cost, **_oracle_route_kwargs(cfg))
+    valid = fw["valid"]
+    assert bool((~valid).any())  # the budget pads slots
+    y, gp, h_old = w["y"].clone(), w["gate_pre"].clone(), fw["h_old"].clone()
+    pad = ~valid
+    y[pad] = float("nan")
+    gp[pad] = float("inf")
+    h_old[pad] = float("nan")
+    d_q_pre = cot["d_q_pre"].clone()
+    d_q_pre[1, 100, :] = float("nan")  # before the reset at 127: cut off from positions < 127
+    d_h_sel = _valid_mask(cot["d_h_sel"], valid)
+    wb = O.window_backward(w["y"].double(), w["gate_pre"].double(), fw["h_old"].double(),
+                           fw["cells"], valid, reset, 256, d_q_pre.double(),
+                           cot["d_q_post"].double(), d_h_sel.double(), cot["d_h_T"].double(),
+                           cot["d_q_T"].double())
+    _lib.set_path(path)
+    try:
+        if _lib.path_for(_lib.OP_BACKWARD, 2, 256, 256, 64, 8, _lib.DTYPE_F32) != path:
+            pytest.skip(f"the {path} path does not take this shape")
+        slots = torch.where(valid, fw["cells"], torch.full_like(fw["cells"], -1)).int()
+        gb = window.backward(y.to(dev), gp.to(dev), h_old.to(dev), slots.to(dev), reset.to(dev),
+                             256, d_q_pre.to(dev), cot["d_q_post"].to(dev), d_h_sel.to(dev),
+                             cot["d_h_T"].to(dev), cot["d_q_T"].to(dev))
+    finally:
+        _lib.set_path("auto")
+    dy, dg = gb[0].cpu(), gb[1].cpu()
+    assert bool((dy[pad] == 0).all()) and bool((dg[pad] == 0).all())  # exact zeros, no NaN
+    # row 1: the NaN at position 100 reaches the shares of positions <= 100 only up to the
+    # reset at 127 ... it lies before 127, so it spreads to every position up to 100 (its own
+    # q cotangent); positions from 127 on must be clean
+    d_h0 = gb[2].cpu()
+    for name, g_, w_ in (("dy", dy, wb[0]), ("dgate", dg, wb[1]), ("d_h0", d_h0, wb[2])):
+        nan = torch.isnan(w_)
+        assert torch.equal(torch.isnan(g_), nan), name  # NaN exactly where the oracle has it
+        assert not bool(torch.isnan(g_[0]).any()), name
+        _close(g_[~nan], w_[~nan], F32_TOL, name)
+    assert not bool(torch.isnan(dy[1, 127:]).any()) and not bool(torch.isnan(dg[1, 127:]).any())
