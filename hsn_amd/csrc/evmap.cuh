@@ -5,12 +5,12 @@
 // lane = 4 k + p, slot k of the position, column pair p of the slice, two fp32 columns a lane,
 // 8-byte loads and stores). The state recurrence is separable over columns and, for a fixed
 // chunk, affine in each cell's value at the chunk's start (h_end = alpha h_start + beta; a reset
-// zeroes both), so the kernel runs
+// zeroes both), so the forward runs
 //   phase A  every half-wave loads its chunk, computes the activations and composes the maps of
 //            the cells its chunk touches,
 //   phase B  the workgroup walks every (cell, column pair) through the 16 chunks from h0: each
-//            touched chunk receives the cell's start value, the end state goes out, and the
-//            chunks' summary changes give every chunk its start q,
+//            touched chunk receives the cell's start value (and its |h| maximum), the untouched
+//            cells' maximum per chunk is reduced, and the end state goes out,
 //   phase C  every half-wave replays its chunk from those start values with the outputs.
 // Event maps. A chunk touches at most P K cells, so its maps live in a table of P K entries
 // instead of N: a cell's entry is the index i K + k of its first event in the chunk (position i,
@@ -20,8 +20,12 @@
 // a cell is its 16 chunks' entries, one 16-byte read in phase B.
 // The row maximum of |h| after each position is the larger of the chunk's untouched cells'
 // maximum at its start (fixed until a reset) and the current maxima of its touched cells, kept
-// per entry; the summary q needs no map: a chunk changes it by its cells' end - start over N
-// (after a reset: by their end), and the positions inside the chunk add their slots' deltas.
+// per entry. The summary q: the replay sums each position's slot deltas across the 8 slots (a
+// reduce-scatter), each position maps q to (reset ? 0 : q) + D / N, and the maps are scanned
+// within the chunk and then across the chunks from q0.
+// The backward (below `bwd`) runs the same three phases in reverse time: a cell's entry is its
+// last event in the chunk, the maps carry the state's cotangent from the chunk's end to its
+// start, and the summary cotangent (which reads no state) is scanned first, in fp64.
 #pragma once
 
 #include "sweep.cuh"
