@@ -2,15 +2,16 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config ref] [--no-cpu]
 
-A step is one window of the configuration, inputs resident in HBM: the router
-(``hsn_win_route``), the forward sweep (``hsn_win_forward``) and the backward with the
-carried-state gradient (``hsn_win_backward``). ``value`` is positions/s over K timed steps
+A step is one window of the configuration, inputs resident in HBM: the router and the forward
+sweep (``hsn_win_route`` then ``hsn_win_forward``, the library's choice; ``--route-forward one``
+times ``hsn_win_route_forward`` as one launch, its forward's workgroups routing the window
+themselves) and the backward with the carried-state gradient (``hsn_win_backward``). ``value`` is positions/s over K timed steps
 launched eagerly as a PyTorch loop calls them (B*T positions per step, bracketed by
 synchronisations); ``--graph`` times K replays of the step captured as a HIP graph instead
 (``ms_per_step_graph`` is reported either way unless ``--no-graph``). Each kernel's average
 duration is measured with HIP events recorded on the stream the kernels run on (torch's current
 stream), over K eager steps queued behind device copies so that the kernels run back to back;
-``roofline`` reports the dominant kernel's algorithmic bytes per launch (the byte model of
+``roofline`` reports the dominant part's algorithmic bytes per launch (the byte model of
 ``hsn_amd.workload.byte_model``) over its average duration against the 8 TB/s HBM peak.
 ``cpu_baseline`` times the repository's CPU oracle (the reference's profile:cpu algorithm) on a
 bounded sample of the same workload on the host cores. One GPU only: ``--gpus`` above 1 exits.
@@ -45,6 +46,10 @@ def _args():
                    help="the sweeps' design (auto: the library's choice by shape)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-h-max", action="store_true", help="do not produce the row maxima")
+    p.add_argument("--route-forward", choices=["auto", "one", "two"], default="auto",
+                   help="route and forward sweep as the library chooses, as one launch "
+                        "(hsn_win_route_forward where the routed forward takes the shape) or as "
+                        "two (hsn_win_route, hsn_win_forward)")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="after the timed steps, copy a buffer of MIB MiB three times (outside "
                         "the timed region): the reference kernel for scaling rocprofv3's "
@@ -758,24 +763,37 @@ def main() -> int:
     cot = {k: (None if v is None else v.to(dev)) for k, v in cot.items()}
     rcfg = window.RouteConfig(k=cfg.K)
     B, T, N, d, K = cfg.B, cfg.T, cfg.N, cfg.d, cfg.K
+    # the parts of a step, each bracketed by HIP events: route and forward as one launch (the
+    # forward's workgroups route the window themselves) or as the two
+    _lib.set_route_forward(args.route_forward)
+    fuses, fuse_why = window.route_forward_fuses(B, T, N, d, K, M=cfg.M,
+                                                 logits_dtype=w["logits"].dtype,
+                                                 io=w["y"].dtype, device=dev)
+    parts = ["route_forward", "backward"] if fuses else ["route", "forward", "backward"]
 
     def step(ev=None):
-        h_max = None if args.no_h_max else torch.empty(B, T, device=dev)
         if ev:
             ev[0].record()
-        cells, units, valid, theta, refreshed, slots = window.route(
-            w["logits"], w["cost"], rcfg, h_max_zero=h_max, with_slots=True)
+        if not fuses:
+            h_max = None if args.no_h_max else torch.empty(B, T, device=dev)
+            cells, units, valid, theta, refreshed, slots = window.route(
+                w["logits"], w["cost"], rcfg, h_max_zero=h_max, with_slots=True)
+            if ev:
+                ev[1].record()
+            out = window.forward(w["y"], w["gate_pre"], w["reset"], slots, w["h0"], w["q0"],
+                                 w["age0"], w["pos0"], N, h_max=h_max, h_max_zeroed=True)
+        else:
+            out = window.route_forward(w["logits"], w["y"], w["gate_pre"], w["reset"], w["h0"],
+                                       w["q0"], w["age0"], w["pos0"], w["cost"], rcfg,
+                                       with_h_max=not args.no_h_max)
+            slots = out["slots"]
         if ev:
-            ev[1].record()
-        out = window.forward(w["y"], w["gate_pre"], w["reset"], slots, w["h0"], w["q0"],
-                             w["age0"], w["pos0"], N, h_max=h_max, h_max_zeroed=True)
-        if ev:
-            ev[2].record()
+            ev[len(parts) - 1].record()
         grads = window.backward(w["y"], w["gate_pre"], out["h_old"], slots, w["reset"], N,
                                 cot["d_q_pre"], cot["d_q_post"], cot["d_h_sel"], cot["d_h_T"],
                                 cot["d_q_T"])
         if ev:
-            ev[3].record()
+            ev[len(parts)].record()
         return out, grads
 
     for _ in range(args.warmup):
@@ -793,7 +811,8 @@ def main() -> int:
     # execution, not the host's launch latency)
     busy = torch.empty(64 << 20, device=dev)
     busy_dst = torch.empty_like(busy)
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(parts) + 1)]
+              for _ in range(args.steps)]
     torch.cuda.synchronize()
     for _ in range(2 * args.steps + 8):  # about 0.1 ms each, ahead of the host's issue rate
         busy_dst.copy_(busy)
@@ -826,18 +845,15 @@ def main() -> int:
     graphed = args.graph and graph_secs is not None
     if graphed:
         secs = graph_secs
-    per_kernel = {"route": 0.0, "forward": 0.0, "backward": 0.0}
-    for ev in events:
-        per_kernel["route"] += ev[0].elapsed_time(ev[1])
-        per_kernel["forward"] += ev[1].elapsed_time(ev[2])
-        per_kernel["backward"] += ev[2].elapsed_time(ev[3])
-    per_kernel = {k: v / args.steps for k, v in per_kernel.items()}  # ms per launch
+    per_kernel = {name: sum(ev[i].elapsed_time(ev[i + 1]) for ev in events) / args.steps
+                  for i, name in enumerate(parts)}  # ms per part
 
     bm = byte_model(cfg)
     positions = B * T
-    algo = {  # algorithmic bytes per launch
+    algo = {  # algorithmic bytes per part
         "route": bm["route"] * positions,
         "forward": bm["forward_update"] * positions,
+        "route_forward": bm["forward"] * positions,
         "backward": bm["backward"] * positions,
     }
     dominant = max(per_kernel, key=per_kernel.get)
@@ -860,7 +876,8 @@ def main() -> int:
         "data": "synthetic (seeded workload generator, hsn_amd/workload.py)",
         "config": {"workload": cfg.name, "shape": describe(cfg), "B": B, "T": T, "N": N, "d": d,
                    "K": K, "M": cfg.M, "storage": cfg.io, "h_max": not args.no_h_max,
-                   "sweep_path": paths, "parallelism": "single GPU"},
+                   "sweep_path": paths, "parallelism": "single GPU",
+                   "route_forward": "one launch" if fuses else f"two launches: {fuse_why}"},
         "roofline": {
             "bound": "hbm",
             "kernel": dominant,
@@ -875,6 +892,7 @@ def main() -> int:
         "ms_per_step_graph": None if graph_secs is None else graph_secs / args.steps * 1e3,
         "kernels_ms": per_kernel,
         "kernels_gbs": {k: algo[k] / (per_kernel[k] * 1e-3) / 1e9 for k in per_kernel},
+        "parts": parts,
         "window_gbs": window_gbs,
         "window_frac": window_gbs / HBM_PEAK_GBS,
     }

@@ -46,6 +46,12 @@ SIGNATURES: dict[str, list] = {
                         I, I, P],
     "hsn_win_forward_noalloc": [P, P, I, P, I, F, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I,
                                 I, I, I, I, P],
+    "hsn_win_route_forward": [P, I, L, P, P, P, I, P, P, P, P, I, F, F, F, F, I, I, P, P, I, P, I,
+                              F, P, L, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I,
+                              P],
+    "hsn_win_set_route_forward": [I],
+    "hsn_win_route_forward_fuses": [I, I, I, I, I, I, I, I, I, I, P, P],
+    "hsn_win_exchange_timeouts": [P, I],
     "hsn_win_backward": [P, P, P, I, P, I, F, P, L, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I,
                          I, P],
     "hsn_win_recurrence": [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P],
@@ -122,6 +128,16 @@ def unsupported(op: int, B: int, T: int, N: int, d: int, K: int) -> str | None:
     if lib.hsn_win_supports(op, B, T, N, d, K) == HSN_OK:
         return None
     return lib.hsn_win_last_error().decode(errors="replace")
+
+
+ROUTE_FORWARD = {"auto": 0, "one": 1, "two": 2}
+
+
+def set_route_forward(mode: str) -> None:
+    """How later route-and-forward calls of this process run: ``"auto"`` (the library's choice,
+    the default), ``"one"`` (one launch wherever the routed forward takes the call) or
+    ``"two"`` (the router, then the forward)."""
+    call("hsn_win_set_route_forward", ROUTE_FORWARD[mode])
 
 
 PATHS = {"auto": 0, "slice": 1, "chain": 2, "evmap": 3}

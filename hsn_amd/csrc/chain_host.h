@@ -52,6 +52,38 @@ void evmap_forward(const void* y, const void* gate_pre, const uint8_t* reset,
                    const int64_t* pos0, void* q_pre, void* q_post, void* h_sel, void* h_old,
                    float* h_max, float* h_T, float* q_T, int64_t* age_T, int64_t* pos_T, int B,
                    int T, int N, int d, int K, hipStream_t st);
+// The router's settings where the forward routes its own window (hsn_win_route_forward: one
+// unit, no probes, fp32 logits [B,T,N,width], int32 decisions).
+struct WindowRouteSpec {
+    const float* logits;
+    int64_t width;
+    const float* cost;
+    int32_t* cells;
+    int32_t* units;
+    uint8_t* valid;
+    float* theta;
+    uint8_t* refreshed;
+    int32_t* slots;
+    int reserved;
+    float lambda, overhead, shared, limit;
+};
+// Whether the routed forward takes the shape (the event maps' conditions, N <= 512, at most 256
+// workgroups, at most 32 positions to decide a workgroup), with the reason when it does not.
+bool evmap_routes(int B, int T, int N, int d, int K, const char** why);
+// Whether this call may use the routed forward's device buffers: the device's first stream that
+// takes them keeps them (`take`: this call takes them if free), a capturing stream never does,
+// and the grid must fit the device's compute units at once; the reason when not.
+bool evmap_route_claim(hipStream_t st, int B, int d, bool take, const char** why);
+void evmap_route_forward(const WindowRouteSpec& rs, const void* y, const void* gate_pre,
+                         const uint8_t* reset, const float* h0, const float* q0,
+                         const int64_t* age0, const int64_t* pos0, void* q_pre, void* q_post,
+                         void* h_sel, void* h_old, float* h_max, float* h_T, float* q_T,
+                         int64_t* age_T, int64_t* pos_T, int B, int T, int N, int d, int K,
+                         hipStream_t st);
+// The routed forward's exchange waits that hit their limit since the last clear (the device is
+// synchronised first).
+unsigned evmap_exchange_timeouts(bool clear);
+
 void evmap_backward(const void* y, const void* gate_pre, const void* h_old, const int32_t* slots,
                     const uint8_t* reset, const void* d_q_pre, const void* d_q_post,
                     const void* d_h_sel, const float* d_h_T, const float* d_q_T, void* dy,

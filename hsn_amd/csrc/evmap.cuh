@@ -182,8 +182,18 @@ __device__ __forceinline__ uint32_t max_of_rows(uint32_t v) {
     return umax(r.lo, r.hi);
 }
 
-template <typename IN>
-__global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
+// The decisions are the `slots` input.
+struct NoRoute {
+    static constexpr bool kOn = false;
+};
+
+// The forward of one (row, 8-column slice). With Route::kOn the row's workgroups route the
+// window themselves instead of reading `slots`; Route provides this launch's stamp,
+// the prefetch of the logits of the workgroup's share of positions, their decisions (each
+// handed to the row through a stamped word), the row's decisions gathered into LDS, and the
+// exchange of the row maxima's per-slice parts at the end.
+template <typename IN, typename Route>
+__device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     static_assert(sizeof(IN) == 4, "fp32 rows");
     extern __shared__ __align__(16) unsigned char lds[];
     const int N = a.N, d = a.d, K = a.K, T = a.T;
@@ -217,6 +227,14 @@ __global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
     // and its stores are sent out of range
     const uint32_t vrow = (active ? uint32_t(k * d + col) * 4u : kOob) + uint32_t(t0) * pos_bytes;
 
+    // the routing's loads (the logits of the workgroup's positions) go out first, so that the
+    // decisions wait for them and not for the slot rows
+    uint64_t stamp = 0;
+    if constexpr (Route::kOn) {
+        stamp = route.stamp(b);
+        route.prefetch(b, slice, w);
+    }
+
     // ---- phase B's first start values and the chunk's resets, loaded first --------------------
     // phase B's threads: thread 2 c + q holds columns 4q .. 4q + 3 of cell c (+ 256 per pass)
     const int bq = gl & 1;
@@ -228,16 +246,17 @@ __global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
     const float4 h0a = h0_at(gl >> 1);
     const uint8_t rbyte = __builtin_amdgcn_raw_buffer_load_b8(rr, hl < n ? uint32_t(t0 + hl) : kOob, 0u, 0);
 
-    // ---- phase A: loads and activations, 8 positions ahead ------------------------------------
-    constexpr int kAhead = 8;
+    // ---- phase A: loads and activations, 8 positions ahead (all 16 when routing) -------------
+    constexpr int kAhead = Route::kOn ? kP : 8;
     float2 yv[kP], gv[kP];
     int32_t cv[kP];
     auto fetch = [&](int i) __attribute__((always_inline)) {
         const uint32_t vo = vrow + uint32_t(i) * pos_bytes;
         yv[i] = ld2(ry, vo);
         gv[i] = ld2(rg, vo);
-        cv[i] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
-            rc, active ? uint32_t((t0 + i) * K + k) * 4u : kOob, 0u, 0));
+        if constexpr (!Route::kOn)
+            cv[i] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+                rc, active ? uint32_t((t0 + i) * K + k) * 4u : kOob, 0u, 0));
     };
 #pragma unroll
     for (int i = 0; i < kAhead; ++i) fetch(i);
@@ -259,18 +278,49 @@ __global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
     }
     if (hl == 0) lds_ref<uint32_t>(lds, Lo.umax + 4u * ch) = 0u;
 
+    // the wavefront's share of the decisions while the slot rows load (its LDS scratch in its
+    // first chunk's maps, below the dummy entry, before the chunk composes them)
+    if constexpr (Route::kOn) route.decide(b, slice, w, stamp, lds + Lo.maps + uint32_t(2 * w) * kMapBytes);
+
     float2 omb[kP], bcv[kP];
     uint32_t vmask = 0u, pmask = 0u;  // valid and padded positions of this lane's slot
+    if constexpr (Route::kOn) {
+        // the activations while the row's other workgroups decide, then the row's decisions
+#pragma unroll
+        for (int i = 0; i < kP; ++i) {
+            const float b0 = fast_sigmoid(gv[i].x), b1 = fast_sigmoid(gv[i].y);
+            const float c0 = fast_tanh(yv[i].x), c1 = fast_tanh(yv[i].y);
+            omb[i] = make_float2(1.0f - b0, 1.0f - b1);
+            bcv[i] = make_float2(b0 * c0, b1 * c1);
+        }
+        // the row's decisions as int16 in chunk 0's maps, below its dummy entry (T K <= 2048):
+        // the maps are free until the composition, and the gather's barrier orders its writes
+        // after every wavefront's decisions (whose scratch is there too)
+        route.gather(b, stamp, lds + Lo.maps);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kP; ++i)
+            cv[i] = active && i < n ? int32_t(lds_ref<int16_t>(lds, Lo.maps + 2u * uint32_t((t0 + i) * K + k)))
+                                    : -1;
+        __syncthreads();  // every read of the table before chunk 0 composes over it
+    }
 #pragma unroll
     for (int i = 0; i < kP; ++i) {
-        if (i + kAhead < kP) fetch(i + kAhead);
+        if constexpr (!Route::kOn) {
+            if (i + kAhead < kP) fetch(i + kAhead);
+        }
         const int c = cv[i];
         const bool inb = active && i < n;
         const bool ok = inb && c >= 0;
-        const float b0 = fast_sigmoid(gv[i].x), b1 = fast_sigmoid(gv[i].y);
-        const float c0 = fast_tanh(yv[i].x), c1 = fast_tanh(yv[i].y);
-        omb[i] = ok ? make_float2(1.0f - b0, 1.0f - b1) : make_float2(1.0f, 1.0f);
-        bcv[i] = ok ? make_float2(b0 * c0, b1 * c1) : make_float2(0.0f, 0.0f);
+        if constexpr (Route::kOn) {
+            omb[i] = ok ? omb[i] : make_float2(1.0f, 1.0f);
+            bcv[i] = ok ? bcv[i] : make_float2(0.0f, 0.0f);
+        } else {
+            const float b0 = fast_sigmoid(gv[i].x), b1 = fast_sigmoid(gv[i].y);
+            const float c0 = fast_tanh(yv[i].x), c1 = fast_tanh(yv[i].y);
+            omb[i] = ok ? make_float2(1.0f - b0, 1.0f - b1) : make_float2(1.0f, 1.0f);
+            bcv[i] = ok ? make_float2(b0 * c0, b1 * c1) : make_float2(0.0f, 0.0f);
+        }
         vmask |= ok ? 1u << i : 0u;
         pmask |= inb && c < 0 ? 1u << i : 0u;
         cv[i] = ok ? c : N;  // the first-event table's row (N: the idle slots' row)
@@ -539,8 +589,10 @@ __global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
             mx = umax(mx, partner_u32<2>(mx, lane));
             mx = umax(mx, partner_u32<1>(mx, lane));
             mx = umax(mx, pos < first_reset ? u : 0u);
-            if (a.h_max && (hl & 3) == 0 && pos < n)
-                atomicMax(reinterpret_cast<unsigned int*>(a.h_max + size_t(b) * T) + (t0 + pos), mx);
+            if (a.h_max && (hl & 3) == 0 && pos < n) {
+                if constexpr (Route::kOn) route.put_hmax(b, t0 + pos, slice, mx, stamp);
+                else atomicMax(reinterpret_cast<unsigned int*>(a.h_max + size_t(b) * T) + (t0 + pos), mx);
+            }
         }
         // the summaries: the slots' deltas summed by a reduce-scatter over the slot bits (lane
         // group g ends with position pos, its column pair), then a scan of the positions' maps
@@ -634,6 +686,14 @@ __global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
             st2(make_float2(q.x + qc[H].x, q.y + qc[H].y), rqb, vqp);
         }
     }
+    // the maps are free again: the row maxima's exchange accumulates in chunk 0's
+    if constexpr (Route::kOn) route.finish(b, slice, stamp, a.h_max, lds + Lo.maps);
+}
+
+template <typename IN>
+__global__ __launch_bounds__(kWave* kWaves) void fwd(FwdEv a) {
+    NoRoute route;
+    fwd_body<IN>(a, route);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -1,5 +1,6 @@
 // Entry points of the forward sweep: the whole window (hsn_win_forward) and the reference's
 // per-position end of round (hsn_win_cell_update), over the kernels of sweep.cuh.
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -176,6 +177,148 @@ extern "C" int hsn_win_forward_noalloc(const void* y, const void* gate_pre, int 
     forward_launch(y, gate_pre, io_dtype, cand_w, cand_norm, cand_eps, ws, L, reset, slots, h0,
                    q0, age0, pos0, q_pre, q_post, h_sel, h_old, h_max, h_T, q_T, age_T, pos_T, B,
                    T, N, d, K, stream);
+    HSN_ABI_END
+}
+
+namespace {
+
+// hsn_win_route_forward's choice (hsn_win_set_route_forward): HSN_ROUTE_FORWARD_AUTO takes the
+// two launches (the one launch measured slower at the ref shape: 42.8 against 9.3 + 30.3 us,
+// its wavefronts deciding four positions each at two wavefronts a SIMD), ONE the one launch
+// wherever it takes the call, TWO always the two.
+std::atomic<int> g_route_forward_mode{HSN_ROUTE_FORWARD_AUTO};
+
+// hsn_win_route's checks of the router's arguments (without probes).
+void route_checks(const char* fn, const void* logits, int logits_dtype, int64_t width,
+                  const float* cost, void* cells, void* units, int index_bits, uint8_t* valid,
+                  float* theta, uint8_t* refreshed, int M, int reserved, int reserved_units,
+                  int B, int T, int N, int K) {
+    const std::string f(fn);
+    HSN_REQUIRE(logits && cost && cells && units && valid && theta && refreshed,
+                HSN_ERR_INVALID_ARGUMENT, f + ": a required router pointer is NULL");
+    HSN_REQUIRE(M >= 1 && K <= kWave && N <= 64 * kWave, HSN_ERR_INVALID_ARGUMENT,
+                f + ": need M >= 1, K <= 64 and N <= 4096");
+    HSN_REQUIRE(width >= M, HSN_ERR_INVALID_ARGUMENT, f + ": width < M");
+    HSN_REQUIRE(reserved >= 0 && (reserved == 0 || reserved < K), HSN_ERR_INVALID_ARGUMENT,
+                f + ": reserved must be 0 or lie in [1, K)");
+    HSN_REQUIRE(!reserved_units || reserved > 0, HSN_ERR_INVALID_ARGUMENT,
+                f + ": reserved_units needs reserved > 0");
+    HSN_REQUIRE(index_bits == 32 || index_bits == 64, HSN_ERR_INVALID_ARGUMENT,
+                f + ": index_bits must be 32 or 64");
+    HSN_REQUIRE(logits_dtype == HSN_DTYPE_F32 || logits_dtype == HSN_DTYPE_BF16,
+                HSN_ERR_UNSUPPORTED_DTYPE, f + ": logits must be f32 or bf16");
+    HSN_REQUIRE(check_elems({int64_t(B) * T * N * width}), HSN_ERR_SIZE_OVERFLOW,
+                f + ": the logits are too large");
+}
+
+// Whether a call with these settings runs as one launch: the event maps' forward that routes
+// its own window takes the shape, the router has one unit and fp32 logits, the decisions are
+// int32, the rows fp32 (`claim`: and the call's stream may use the device's exchange buffers,
+// which it then keeps; otherwise only reported).
+bool route_forward_fuses(int M, int logits_dtype, int index_bits, int io_dtype, int cand_norm,
+                         int B, int T, int N, int d, int K, hipStream_t st, bool claim,
+                         const char** why) {
+    const char* r = nullptr;
+    const int mode = g_route_forward_mode.load(std::memory_order_relaxed);
+    if (mode != HSN_ROUTE_FORWARD_ONE)
+        r = mode == HSN_ROUTE_FORWARD_TWO ? "two launches are set (hsn_win_set_route_forward)"
+                                          : "two launches are the library's choice (measured faster)";
+    else if (M != 1) r = "the routed forward takes one unit";
+    else if (logits_dtype != HSN_DTYPE_F32) r = "the routed forward takes fp32 logits";
+    else if (index_bits != 32) r = "the routed forward writes int32 decisions";
+    else if (io_dtype != HSN_DTYPE_F32) r = "the routed forward takes fp32 rows";
+    else if (!workspace_layout(HSN_OP_FORWARD, B, T, N, d, K, 4, cand_norm).evmap)
+        r = "the forward of this shape is not on the event maps";
+    else if (!evmap_routes(B, T, N, d, K, &r)) {
+    } else if (!evmap_route_claim(st, B, d, claim, &r)) {
+    }
+    if (r && why) *why = r;
+    return r == nullptr;
+}
+
+}  // namespace
+
+extern "C" int hsn_win_route_forward(
+    const void* logits, int logits_dtype, int64_t width, const float* cost, void* cells,
+    void* units, int index_bits, uint8_t* valid, float* theta, uint8_t* refreshed,
+    int32_t* slots, int M, float lambda_cost, float cell_overhead, float shared_cost, float limit,
+    int reserved, int reserved_units, const void* y, const void* gate_pre, int io_dtype,
+    const float* cand_w, int cand_norm, float cand_eps, void* workspace, int64_t workspace_bytes,
+    const uint8_t* reset, const float* h0, const float* q0, const int64_t* age0,
+    const int64_t* pos0, void* q_pre, void* q_post, void* h_sel, void* h_old, float* h_max,
+    float* h_T, float* q_T, int64_t* age_T, int64_t* pos_T, int B, int T, int N, int d, int K,
+    void* stream) {
+    HSN_ABI_BEGIN
+    const char* fn = "hsn_win_route_forward";
+    HSN_REQUIRE(slots != nullptr, HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_route_forward: slots (the backward's decisions) is required");
+    route_checks(fn, logits, logits_dtype, width, cost, cells, units, index_bits, valid, theta,
+                 refreshed, M, reserved, reserved_units, B, T, N, K);
+    forward_checks(fn, y, gate_pre, io_dtype, cand_w, cand_norm, reset, slots, h0, q0, age0,
+                   pos0, age_T, pos_T, B, T, N, d, K);
+    const WorkspaceLayout L = workspace_layout(HSN_OP_FORWARD, B, T, N, d, K,
+                                               io_dtype == HSN_DTYPE_F32 ? 4 : 2, cand_norm);
+    HSN_REQUIRE(L.bytes == 0 || (workspace && workspace_bytes >= int64_t(L.bytes)),
+                HSN_ERR_INVALID_ARGUMENT,
+                "hsn_win_route_forward: the workspace must hold " + std::to_string(L.bytes) +
+                    " bytes (hsn_win_workspace_bytes)");
+    hipStream_t st = as_stream(stream);
+    if (route_forward_fuses(M, logits_dtype, index_bits, io_dtype, cand_norm, B, T, N, d, K, st,
+                            true, nullptr)) {
+        if (cand_norm) {
+            y = rms_normalise(y, io_dtype, cand_w, cand_eps, static_cast<char*>(workspace) + L.rms,
+                              int64_t(B) * T * K, d, st);
+            HSN_HIP(hipGetLastError());
+        }
+        WindowRouteSpec rs{};
+        rs.logits = static_cast<const float*>(logits), rs.width = width, rs.cost = cost;
+        rs.cells = static_cast<int32_t*>(cells), rs.units = static_cast<int32_t*>(units);
+        rs.valid = valid, rs.theta = theta, rs.refreshed = refreshed, rs.slots = slots;
+        rs.reserved = reserved;
+        rs.lambda = lambda_cost, rs.overhead = cell_overhead, rs.shared = shared_cost, rs.limit = limit;
+        evmap_route_forward(rs, y, gate_pre, reset, h0, q0, age0, pos0, q_pre, q_post, h_sel,
+                            h_old, h_max, h_T, q_T, age_T, pos_T, B, T, N, d, K, st);
+    } else {  // the two launches, the router zeroing h_max for the sweep's max-reduction
+        int rc = hsn_win_route(logits, logits_dtype, width, cost, nullptr, nullptr, cells, units,
+                               index_bits, valid, theta, refreshed, slots, h_max, B, T, N, M, K, 0,
+                               0, lambda_cost, cell_overhead, shared_cost, limit, reserved,
+                               reserved_units, stream);
+        if (rc != HSN_OK) throw AbiError{rc, hsn_win_last_error()};
+        rc = hsn_win_forward(y, gate_pre, io_dtype, cand_w, cand_norm, cand_eps, workspace,
+                             workspace_bytes, reset, slots, h0, q0, age0, pos0, q_pre, q_post,
+                             h_sel, h_old, h_max, h_T, q_T, age_T, pos_T, B, T, N, d, K, stream);
+        if (rc != HSN_OK) throw AbiError{rc, hsn_win_last_error()};
+    }
+    HSN_ABI_END
+}
+
+extern "C" int hsn_win_route_forward_fuses(int M, int logits_dtype, int index_bits, int io_dtype,
+                                           int cand_norm, int B, int T, int N, int d, int K,
+                                           void* stream, int* fuses) {
+    HSN_ABI_BEGIN
+    HSN_REQUIRE(fuses != nullptr, HSN_ERR_INVALID_ARGUMENT, "fuses is NULL");
+    HSN_REQUIRE(B >= 1 && T >= 1 && N >= 1 && d >= 1 && K >= 1 && K <= N, HSN_ERR_INVALID_ARGUMENT,
+                "bad dimensions");
+    const char* why = nullptr;
+    *fuses = route_forward_fuses(M, logits_dtype, index_bits, io_dtype, cand_norm, B, T, N, d, K,
+                                 as_stream(stream), false, &why) ? 1 : 0;
+    if (!*fuses && why) set_last_error(why);  // the reason, for hsn_win_last_error
+    HSN_ABI_END
+}
+
+extern "C" int hsn_win_set_route_forward(int mode) {
+    HSN_ABI_BEGIN
+    HSN_REQUIRE(mode == HSN_ROUTE_FORWARD_AUTO || mode == HSN_ROUTE_FORWARD_ONE ||
+                    mode == HSN_ROUTE_FORWARD_TWO,
+                HSN_ERR_INVALID_ARGUMENT, "hsn_win_set_route_forward: unknown mode");
+    g_route_forward_mode.store(mode, std::memory_order_relaxed);
+    HSN_ABI_END
+}
+
+extern "C" int hsn_win_exchange_timeouts(unsigned* count, int clear) {
+    HSN_ABI_BEGIN
+    HSN_REQUIRE(count != nullptr, HSN_ERR_INVALID_ARGUMENT, "count is NULL");
+    *count = evmap_exchange_timeouts(clear != 0);
     HSN_ABI_END
 }
 

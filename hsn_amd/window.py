@@ -3,9 +3,10 @@ carried-state gradient.
 
 This is the window-level counterpart of the reference's split/fused window
 (python/hsn/train/split.py:372-762, python/hsn/train/compile.py:892-1024): instead of one to
-five launches per position and a full-state tape ``[B, T+1, N, d]``, a window is three launches
-(``hsn_win_route``, ``hsn_win_forward``, ``hsn_win_backward``) and the tape is the slots'
-pre-round states ``h_old [B, T, K, d]``. Every function requires CUDA (ROCm) tensors and the
+five launches per position and a full-state tape ``[B, T+1, N, d]``, a window is the route and
+forward sweep (``hsn_win_route_forward``: one launch where the forward's workgroups decide the
+window themselves, else ``hsn_win_route`` then ``hsn_win_forward``) and the backward
+(``hsn_win_backward``), and the tape is the slots' pre-round states ``h_old [B, T, K, d]``. Every function requires CUDA (ROCm) tensors and the
 built HIP library; there is no CPU path here.
 
 Decisions (``cells``, ``units``) are int32 in the window form (the reference's per-position
@@ -33,6 +34,9 @@ __all__ = [
     "check_reserved",
     "route",
     "forward",
+    "route_forward",
+    "route_forward_fuses",
+    "exchange_timeouts",
     "backward",
     "window_forward",
     "window_backward",
@@ -249,12 +253,105 @@ def backward(y: Tensor, gate_pre: Tensor, h_old: Tensor, slots: Tensor,
     return dy, dgate, d_h0, d_q0, d_w
 
 
+def route_forward(logits: Tensor, y: Tensor, gate_pre: Tensor, reset: Tensor, h0: Tensor,
+                  q0: Tensor, age0: Tensor, pos0: Tensor, cost: Tensor, cfg: RouteConfig, *,
+                  cand_norm: bool = False, cand_w: Optional[Tensor] = None,
+                  cand_eps: float = 1e-6, with_h_max: bool = True) -> dict:
+    """:func:`route` (without probes) and :func:`forward` on its slots as one call
+    (``hsn_win_route_forward``): the decisions ``cells, units, valid, theta, refreshed, slots``,
+    the sweep's outputs and ``h_max [B,T]`` (when ``with_h_max``), bit for bit those of the two
+    calls. One launch where :func:`route_forward_fuses` says so, else the two."""
+    if cfg.probes:
+        raise ValueError("route_forward decides without probes (use route, then forward)")
+    B, T, N, M = (int(s) for s in logits.shape)
+    K, d = cfg.k, int(y.shape[3])
+    dev, io = y.device, y.dtype
+    _check(logits, "logits", (B, T, N, M), device=dev)
+    _check(cost, "cost", (M,), torch.float32, dev)
+    _check(y, "y", (B, T, K, d))
+    _check(gate_pre, "gate_pre", (B, T, K, d), io, dev)
+    _check(reset, "reset", (B, T), torch.bool, dev)
+    _check(h0, "h0", (B, N, d), torch.float32, dev)
+    _check(q0, "q0", (B, d), torch.float32, dev)
+    _check(age0, "age0", (B, N), torch.int64, dev)
+    _check(pos0, "pos0", (B,), torch.int64, dev)
+    if cand_norm:
+        if cand_w is None:
+            raise ValueError("cand_norm needs cand_w")
+        _check(cand_w, "cand_w", (d,), torch.float32, dev)
+    ws, ws_bytes = _workspace(_lib.OP_FORWARD, B, T, N, d, K, io, cand_norm, dev)
+    cells = torch.empty(B, T, K, dtype=torch.int32, device=dev)
+    out = {
+        "cells": cells,
+        "units": torch.empty_like(cells),
+        "valid": torch.empty(B, T, K, dtype=torch.bool, device=dev),
+        "refreshed": torch.empty(B, T, K, dtype=torch.bool, device=dev),
+        "theta": torch.empty(B, T, dtype=torch.float32, device=dev),
+        "slots": torch.empty_like(cells),
+        "q_pre": torch.empty(B, T, d, dtype=io, device=dev),
+        "q_post": torch.empty(B, T, d, dtype=io, device=dev),
+        "h_sel": torch.empty(B, T, K, d, dtype=io, device=dev),
+        "h_old": torch.empty(B, T, K, d, dtype=io, device=dev),
+        "h": torch.empty(B, N, d, dtype=torch.float32, device=dev),
+        "q": torch.empty(B, d, dtype=torch.float32, device=dev),
+        "age": torch.empty(B, N, dtype=torch.int64, device=dev),
+        "pos": torch.empty(B, dtype=torch.int64, device=dev),
+    }
+    h_max = torch.empty(B, T, dtype=torch.float32, device=dev) if with_h_max else None
+    if h_max is not None:
+        out["h_max"] = h_max
+    call("hsn_win_route_forward", ptr(logits), _io_code(logits.dtype), M, ptr(cost),
+         ptr(out["cells"]), ptr(out["units"]), 32, ptr(out["valid"]), ptr(out["theta"]),
+         ptr(out["refreshed"]), ptr(out["slots"]), M, float(cfg.lambda_cost),
+         float(cfg.cell_overhead), float(cfg.shared_cost), float(cfg.limit), int(cfg.reserved),
+         int(bool(cfg.reserved_units)), ptr(y), ptr(gate_pre), _io_code(io),
+         ptr(cand_w) if cand_norm else None, int(bool(cand_norm)), float(cand_eps), ptr(ws),
+         ws_bytes, ptr(reset), ptr(h0), ptr(q0), ptr(age0), ptr(pos0), ptr(out["q_pre"]),
+         ptr(out["q_post"]), ptr(out["h_sel"]), ptr(out["h_old"]), ptr(h_max), ptr(out["h"]),
+         ptr(out["q"]), ptr(out["age"]), ptr(out["pos"]), B, T, N, d, K, stream_of(dev))
+    return out
+
+
+def route_forward_fuses(B: int, T: int, N: int, d: int, K: int, *, M: int = 1,
+                        logits_dtype: torch.dtype = torch.float32,
+                        io: torch.dtype = torch.float32, cand_norm: bool = False,
+                        device=None) -> tuple[bool, Optional[str]]:
+    """Whether :func:`route_forward` of this shape on the current stream of ``device`` is one
+    launch, and the reason when it is two (host arithmetic; claims nothing)."""
+    import ctypes
+
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    out = ctypes.c_int(0)
+    call("hsn_win_route_forward_fuses", int(M), _io_code(logits_dtype), 32, _io_code(io),
+         int(bool(cand_norm)), B, T, N, d, K, stream_of(dev), ctypes.byref(out))
+    if out.value:
+        return True, None
+    return False, _lib.library().hsn_win_last_error().decode(errors="replace")
+
+
+def exchange_timeouts(clear: bool = True) -> int:
+    """The one-launch route and forward's exchange waits that hit their limit since the last
+    clear (0 unless a grid could not keep a row's workgroups resident; synchronises the
+    device)."""
+    import ctypes
+
+    out = ctypes.c_uint(0)
+    call("hsn_win_exchange_timeouts", ctypes.byref(out), int(bool(clear)))
+    return int(out.value)
+
+
 def window_forward(logits: Tensor, y: Tensor, gate_pre: Tensor, reset: Tensor, h0: Tensor,
                    q0: Tensor, age0: Tensor, pos0: Tensor, cost: Tensor, cfg: RouteConfig, *,
                    cand_norm: bool = False, cand_w: Optional[Tensor] = None,
                    cand_eps: float = 1e-6, with_h_max: bool = True) -> dict:
     """Route and forward sweep of one window: the decisions (``cells, units, valid, theta,
-    refreshed``), the sweep's outputs (:func:`forward`) and ``h_max [B,T]``."""
+    refreshed``), the sweep's outputs (:func:`forward`) and ``h_max [B,T]``; without probes
+    :func:`route_forward`, with them :func:`route` (whose ages evolve with the decisions) and
+    then :func:`forward`."""
+    if not cfg.probes:
+        return route_forward(logits, y, gate_pre, reset, h0, q0, age0, pos0, cost, cfg,
+                             cand_norm=cand_norm, cand_w=cand_w, cand_eps=cand_eps,
+                             with_h_max=with_h_max)
     B, T, N, M = (int(s) for s in logits.shape)
     h_max = torch.empty(B, T, dtype=torch.float32, device=y.device) if with_h_max else None
     cells, units, valid, theta, refreshed, slots = route(logits, cost, cfg, reset=reset,

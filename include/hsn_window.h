@@ -198,6 +198,52 @@ int hsn_win_forward_noalloc(const void* y, const void* gate_pre, int io_dtype,
                             int N, int d, int K, void* stream);
 
 /*
+ * Route and forward sweep of a window as one call: hsn_win_route (without probes) followed by
+ * hsn_win_forward on its slots, the two steps of every position of the reference's fused sweep
+ * (the per-position `hsn_win_select` and `hsn_win_cell_update` launches,
+ * kernels/cuda/hsn_window.cu:533-954; the position loop of python/hsn/train/compile.py:892-1024).
+ * Arguments are those two calls' (the router's first, then the forward's; `slots` is required,
+ * the backward's decisions; h_max needs no zeroing); outputs and results are bit for bit theirs.
+ * With hsn_win_set_route_forward(HSN_ROUTE_FORWARD_ONE), where the event maps take the forward
+ * (HSN_PATH_EVMAP), the router has one unit (M = 1), the logits and rows are f32, the decisions
+ * int32 (index_bits 32), N <= 512, B * d / 8 <= 256 and the device's compute units, and
+ * ceil(T / (d / 8)) <= 32, it is one launch: the forward's workgroups of a row each decide a
+ * share of the row's positions and hand the decisions to each other through device memory the
+ * library owns (one set a GPU). Those buffers serve one stream a GPU, the first that fuses;
+ * calls on other streams, or on a capturing stream, take the two launches. The default,
+ * HSN_ROUTE_FORWARD_AUTO, takes the two launches (faster at the ref shape on MI355X: the one
+ * launch's wavefronts decide four positions each with two wavefronts a SIMD to hide the
+ * decisions' latency); HSN_ROUTE_FORWARD_TWO always does. No counterpart in the reference for
+ * the setting. hsn_win_route_forward_fuses reports which a call takes (without claiming the
+ * buffers; the reason in hsn_win_last_error when it is two).
+ */
+#define HSN_ROUTE_FORWARD_AUTO 0
+#define HSN_ROUTE_FORWARD_ONE 1
+#define HSN_ROUTE_FORWARD_TWO 2
+int hsn_win_set_route_forward(int mode);
+int hsn_win_route_forward(const void* logits, int logits_dtype, int64_t width, const float* cost,
+                          void* cells, void* units, int index_bits, uint8_t* valid, float* theta,
+                          uint8_t* refreshed, int32_t* slots, int M, float lambda_cost,
+                          float cell_overhead, float shared_cost, float limit, int reserved,
+                          int reserved_units, const void* y, const void* gate_pre, int io_dtype,
+                          const float* cand_w, int cand_norm, float cand_eps, void* workspace,
+                          int64_t workspace_bytes, const uint8_t* reset, const float* h0,
+                          const float* q0, const int64_t* age0, const int64_t* pos0, void* q_pre,
+                          void* q_post, void* h_sel, void* h_old, float* h_max, float* h_T,
+                          float* q_T, int64_t* age_T, int64_t* pos_T, int B, int T, int N, int d,
+                          int K, void* stream);
+int hsn_win_route_forward_fuses(int M, int logits_dtype, int index_bits, int io_dtype,
+                                int cand_norm, int B, int T, int N, int d, int K, void* stream,
+                                int* fuses);
+/*
+ * The one-launch route and forward's waits for another workgroup's word that reached their
+ * limit (about a second each; only a grid whose workgroups cannot all be resident at once waits
+ * that long, and its results are then not to be used), counted since the last clear. Waits for
+ * the device's work to finish first. No counterpart in the reference.
+ */
+int hsn_win_exchange_timeouts(unsigned* count, int clear);
+
+/*
  * Backward of the window with the activations fused and the carried-state gradient: the
  * reverse recurrence of python/hsn/train/split.py:128-174 (A [N,d], R [d] resident on chip),
  * seeded with the end-state cotangent (python/hsn/train/state_gradient.py:402-416), the VJPs

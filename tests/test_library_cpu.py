@@ -357,3 +357,53 @@ def test_noalloc_forward_rejects_a_workspace_above_its_array_without_a_gpu():
                                          64, 16, None)
     assert status == 5
     assert b"scratch array" in lib.hsn_win_last_error()
+
+
+def test_route_forward_declines_follow_the_routed_kernels_limits():
+    """Where hsn_win_route_forward is two launches, and why (host arithmetic: every declined
+    shape is decided before the call touches a device)."""
+    import ctypes
+
+    from hsn_amd import _lib, build
+
+    if build.stale() is not None:
+        pytest.skip("library not built here")
+    lib = _lib.library()
+    F32, BF16 = _lib.DTYPE_F32, _lib.DTYPE_BF16
+    out = ctypes.c_int(1)
+
+    def reason(M, logits, bits, io, rms, B, T, N, d, K):
+        out.value = 1
+        assert lib.hsn_win_route_forward_fuses(M, logits, bits, io, rms, B, T, N, d, K, None,
+                                               ctypes.byref(out)) == _lib.HSN_OK
+        assert out.value == 0
+        return lib.hsn_win_last_error().decode()
+
+    assert "library's choice" in reason(1, F32, 32, F32, 0, 32, 256, 256, 64, 8)
+    _lib.set_route_forward("two")
+    assert "are set" in reason(1, F32, 32, F32, 0, 32, 256, 256, 64, 8)
+    _lib.set_route_forward("one")
+    try:
+        _route_forward_reasons(reason, F32, BF16)
+    finally:
+        _lib.set_route_forward("auto")
+    with pytest.raises(RuntimeError, match="unknown mode"):
+        _lib.call("hsn_win_set_route_forward", 7)
+
+
+def _route_forward_reasons(reason, F32, BF16):
+    from hsn_amd import _lib
+
+    assert "one unit" in reason(2, F32, 32, F32, 0, 2, 64, 64, 16, 4)
+    assert "fp32 logits" in reason(1, BF16, 32, F32, 0, 2, 64, 64, 16, 4)
+    assert "int32" in reason(1, F32, 64, F32, 0, 2, 64, 64, 16, 4)
+    assert "fp32 rows" in reason(1, F32, 32, BF16, 0, 2, 64, 64, 16, 4)
+    assert "event maps" in reason(1, F32, 32, F32, 0, 8, 300, 64, 64, 8)  # T > 256
+    assert "event maps" in reason(1, F32, 32, F32, 0, 64, 64, 64, 64, 8)  # 512 workgroups
+    assert "T <= 32 d / 8" in reason(1, F32, 32, F32, 0, 2, 100, 64, 16, 4)
+    assert "N <= 512" in reason(1, F32, 32, F32, 0, 2, 64, 513, 16, 4)
+    _lib.set_path("evmap")
+    try:
+        assert "256 workgroups" in reason(1, F32, 32, F32, 0, 64, 64, 64, 64, 8)
+    finally:
+        _lib.set_path("auto")
