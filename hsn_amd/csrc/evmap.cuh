@@ -246,8 +246,8 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     const float4 h0a = h0_at(gl >> 1);
     const uint8_t rbyte = __builtin_amdgcn_raw_buffer_load_b8(rr, hl < n ? uint32_t(t0 + hl) : kOob, 0u, 0);
 
-    // ---- phase A: loads and activations, 8 positions ahead (all 16 when routing) -------------
-    constexpr int kAhead = Route::kOn ? kP : 8;
+    // ---- phase A: loads and activations, 8 positions ahead ------------------------------------
+    constexpr int kAhead = 8;
     float2 yv[kP], gv[kP];
     int32_t cv[kP];
     auto fetch = [&](int i) __attribute__((always_inline)) {
@@ -278,16 +278,18 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     }
     if (hl == 0) lds_ref<uint32_t>(lds, Lo.umax + 4u * ch) = 0u;
 
-    // the wavefront's share of the decisions while the slot rows load (its LDS scratch in its
-    // first chunk's maps, below the dummy entry, before the chunk composes them)
+    // the wavefront's share of the decisions while the first slot rows load (its LDS scratch in
+    // its first chunk's maps, clear of the dummy entries, before the chunk composes them)
     if constexpr (Route::kOn) route.decide(b, slice, w, stamp, lds + Lo.maps + uint32_t(2 * w) * kMapBytes);
 
     float2 omb[kP], bcv[kP];
     uint32_t vmask = 0u, pmask = 0u;  // valid and padded positions of this lane's slot
     if constexpr (Route::kOn) {
-        // the activations while the row's other workgroups decide, then the row's decisions
+        // the loads and activations while the row's other workgroups decide, then the row's
+        // decisions
 #pragma unroll
         for (int i = 0; i < kP; ++i) {
+            if (i + kAhead < kP) fetch(i + kAhead);
             const float b0 = fast_sigmoid(gv[i].x), b1 = fast_sigmoid(gv[i].y);
             const float c0 = fast_tanh(yv[i].x), c1 = fast_tanh(yv[i].y);
             omb[i] = make_float2(1.0f - b0, 1.0f - b1);

@@ -82,48 +82,64 @@ __device__ unsigned int g_exchange_timeouts;
 constexpr int kSpinLimit = 1 << 20;
 
 constexpr int kRouteWaves = evmap::kWaves;
-constexpr int kRouteJ = 4;  // positions a wavefront decides, at most
+constexpr int kRouteJ = 4;  // consecutive positions a wavefront decides, at most
 constexpr int kRouteShare = kRouteWaves * kRouteJ;
-// the row's int16 decisions (T K <= 256 * 8), a workgroup's row-maximum accumulators and a
-// wavefront's selection scratch all fit in a chunk's maps below its dummy entry
+// the row's int16 decisions (T K <= 256 * 8) and a workgroup's row-maximum accumulators fit in a
+// chunk's maps below its dummy entry
 static_assert(kBoxPositions * evmap::kK * 2 <= evmap::kDummy * evmap::kEntBytes, "slot table");
 static_assert(kBoxPositions * 4 <= evmap::kDummy * evmap::kEntBytes, "row maxima");
-static_assert(2 * kWave * 16 + (kWave + 4) * 8 <= evmap::kDummy * evmap::kEntBytes, "scratch");
 
-template <int NPL>
+// The decisions of a wavefront's positions by decide_grouped (LP lanes a position, CPL cells a
+// lane; a position with more candidates than lanes by decide_select, NPLF cells a lane), its
+// scratch in its first chunk's maps: the scores, lists and order words below the alpha table's
+// dummy entry, the slot tables in the beta table.
+template <int LP, int CPL, int NPLF>
 struct WindowRoute {
     static constexpr bool kOn = true;
+    static constexpr int G = kWave / LP;
+    static constexpr int kCalls = kRouteJ / G;
+    static constexpr uint32_t kTabAt = evmap::kEnt * evmap::kEntBytes;
+    static_assert(CPL * kWave * 4 + kWave * 16 + G * (LP + 4) * 8 <= evmap::kDummy * evmap::kEntBytes,
+                  "scores, lists and order words below the dummy entry");
+    static_assert(kTabAt + kWave * 16 <= (evmap::kEnt + evmap::kDummy) * evmap::kEntBytes, "slot tables");
+    static_assert(G * (LP + 4) * 8 >= (kWave + 4) * 8, "decide_select's order words");
     const RouteArgs& ra;
     uint64_t launch;  // this launch's stamp
     int share;        // positions a workgroup decides
     int slices;       // workgroups a row
-    float raw[kRouteJ][NPL];
+    float raw[kCalls][CPL];
 
-    __device__ __forceinline__ int pos_of(int slice, int w, int j) const {
-        return slice * share + w + kRouteWaves * j;
+    __device__ __forceinline__ int q_first(int b, int slice, int w, int c) const {
+        return b * ra.P + slice * share + kRouteJ * w + G * c;
     }
-    __device__ __forceinline__ bool mine(int slice, int p) const {
-        return p < ra.P && p < (slice + 1) * share;
+    __device__ __forceinline__ int q_end(int b, int slice) const {
+        return b * ra.P + min(ra.P, (slice + 1) * share);
     }
     __device__ __forceinline__ uint64_t stamp(int) const { return launch; }
     __device__ __forceinline__ void prefetch(int b, int slice, int w) {
 #pragma unroll
-        for (int j = 0; j < kRouteJ; ++j) {
-            const int p = pos_of(slice, w, j);
-            if (mine(slice, p)) load_logits<NPL, float>(ra, b, p, raw[j]);
-        }
+        for (int c = 0; c < kCalls; ++c)
+            load_grouped<LP, CPL, float>(ra, q_first(b, slice, w, c), q_end(b, slice), raw[c]);
     }
-    // the wavefront's positions: decide_select's scratch (64 candidates, the slot table, the
-    // order words) at `scratch`, 2592 bytes
     __device__ __forceinline__ void decide(int b, int slice, int w, uint64_t st, unsigned char* scratch) {
-        uint4* cand = reinterpret_cast<uint4*>(scratch);
-        uint4* tab = cand + kWave;
-        uint64_t* ord = reinterpret_cast<uint64_t*>(tab + kWave);
+        GroupedScratch sm;
+        sm.sc = reinterpret_cast<float*>(scratch);
+        sm.cand = reinterpret_cast<uint4*>(scratch + CPL * kWave * 4);
+        sm.ord = reinterpret_cast<uint64_t*>(sm.cand + kWave);
+        sm.tab = reinterpret_cast<uint4*>(scratch + kTabAt);
+        const int qe = q_end(b, slice);
 #pragma unroll
-        for (int j = 0; j < kRouteJ; ++j) {
-            const int p = pos_of(slice, w, j);
-            if (mine(slice, p))
-                decide_select_from<NPL, true, float, int32_t>(ra, b, p, raw[j], cand, tab, ord, st);
+        for (int c = 0; c < kCalls; ++c) {
+            const int q0 = q_first(b, slice, w, c);
+            uint32_t need = decide_grouped_from<LP, CPL, float, int32_t>(ra, q0, qe, raw[c], sm, st);
+            while (need != 0u) {
+                __builtin_amdgcn_wave_barrier();
+                const int g = __builtin_ctz(need);
+                need &= need - 1u;
+                const int q = q0 + g;
+                decide_select<NPLF, true, float, int32_t>(ra, q / ra.P, q % ra.P, sm.cand, sm.tab, sm.ord, st);
+            }
+            __builtin_amdgcn_wave_barrier();
         }
     }
     // the row's T K decisions into LDS as int16 (the cell, -1 where padded): thread t polls
@@ -206,11 +222,11 @@ struct WindowRoute {
     }
 };
 
-template <int NPL>
+template <int LP, int CPL, int NPLF>
 __global__ __launch_bounds__(kWave* evmap::kWaves) void fwd_routed(evmap::FwdEv a, RouteArgs ra,
                                                                    uint64_t stamp, int share,
                                                                    int slices) {
-    WindowRoute<NPL> route{ra, stamp, share, slices, {}};
+    WindowRoute<LP, CPL, NPLF> route{ra, stamp, share, slices, {}};
     evmap::fwd_body<float>(a, route);
 }
 
@@ -322,22 +338,20 @@ void evmap_route_forward(const WindowRouteSpec& rs, const void* y, const void* g
     const int slices = d / evmap::kS;
     const int share = (T + slices - 1) / slices;
     const size_t lds = evmap::fwd_layout(N).bytes;
-    const int npl = (N + kWave - 1) / kWave;
     const dim3 grid = sweep_grid(B, slices), block(kWave * evmap::kWaves);
-#define HSN_ROUTED_CASE(V)                                                  \
-    if (npl <= V) {                                                         \
-        auto k = fwd_routed<V>;                                             \
-        HSN_HIP(allow_lds(k, lds));                                         \
-        hipLaunchKernelGGL(k, grid, block, lds, st, a, ra, stamp, share, slices); \
-        HSN_HIP(hipGetLastError());                                         \
-        return;                                                             \
-    }
-    HSN_ROUTED_CASE(1)
-    HSN_ROUTED_CASE(2)
-    HSN_ROUTED_CASE(4)
-    HSN_ROUTED_CASE(8)
-#undef HSN_ROUTED_CASE
-    HSN_REQUIRE(false, HSN_ERR_INVALID_ARGUMENT, "the routed forward takes N <= 512");
+    auto launch = [&](auto k) {
+        HSN_HIP(allow_lds(k, lds));
+        hipLaunchKernelGGL(k, grid, block, lds, st, a, ra, stamp, share, slices);
+        HSN_HIP(hipGetLastError());
+    };
+    // the router's layouts (route.hip): two positions of 32 lanes a wavefront up to N = 256, one
+    // of 64 lanes up to 512
+    if (N <= 32) launch(fwd_routed<32, 1, 1>);
+    else if (N <= 64) launch(fwd_routed<32, 2, 1>);
+    else if (N <= 128) launch(fwd_routed<32, 4, 2>);
+    else if (N <= 256) launch(fwd_routed<32, 8, 4>);
+    else if (N <= 512) launch(fwd_routed<64, 8, 8>);
+    else HSN_REQUIRE(false, HSN_ERR_INVALID_ARGUMENT, "the routed forward takes N <= 512");
 }
 
 unsigned evmap_exchange_timeouts(bool clear) {

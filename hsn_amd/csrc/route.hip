@@ -643,6 +643,33 @@ __device__ __forceinline__ void decide_lean(const RouteArgs& a, int b, int p, ui
         decide_lean_body<NPL, false, IO, IDX>(a, b, p, cand, tab, ord);
 }
 
+// Whole window without probes, one unit, N <= 1024 and K < LP: G = 64 / LP positions a
+// wavefront (decide_grouped), four wavefronts a workgroup; a group with more candidates than
+// lanes is decided afterwards by the wavefront's one-position selection (NPLF cells a lane).
+template <int LP, int CPL, int NPLF, typename IO, typename IDX>
+__global__ __launch_bounds__(256) void route_grouped(RouteArgs a) {
+    constexpr int G = kWave / LP;
+    constexpr int kBytes = grouped_scratch_bytes<LP, CPL>();
+    __shared__ __align__(16) unsigned char smem[4][kBytes];
+    const int wv = uniform(threadIdx.x / kWave);
+    const int q0 = (blockIdx.x * 4 + wv) * G;
+    if (q0 >= a.B * a.P) return;
+    unsigned char* const sw = smem[wv];
+    uint32_t need = decide_grouped<LP, CPL, IO, IDX>(a, q0, sw);
+    if (need != 0u) {  // its scratch is the groups' lists, order words and slot tables
+        __builtin_amdgcn_wave_barrier();
+        const GroupedScratch sm = grouped_scratch<LP, CPL>(sw);
+        while (need != 0u) {
+            const int g = __builtin_ctz(need);
+            need &= need - 1u;
+            const int q = q0 + g;
+            if constexpr (NPLF >= 16) decide_lean<NPLF, IO, IDX>(a, q / a.P, q % a.P, sm.cand, sm.tab, sm.ord);
+            else decide_select<NPLF, true, IO, IDX>(a, q / a.P, q % a.P, sm.cand, sm.tab, sm.ord);
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+}
+
 // Whole window without probes: a wavefront per (row, position), four per workgroup; kOne
 // (one unit) is a kernel of its own, so its register budget is not the multi-unit one.
 template <int NPL, bool kOne, typename IO, typename IDX>
@@ -892,9 +919,34 @@ __global__ __launch_bounds__(64) void route_sequential(RouteArgs a) {
     }
 }
 
+template <int LP, int CPL, int NPLF, typename IO, typename IDX>
+hipError_t launch_grouped(const RouteArgs& a, hipStream_t stream) {
+    constexpr int G = kWave / LP;
+    const int64_t groups = (int64_t(a.B) * a.P + G - 1) / G;
+    hipLaunchKernelGGL((route_grouped<LP, CPL, NPLF, IO, IDX>), dim3(unsigned((groups + 3) / 4)),
+                       dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
 template <typename IO, typename IDX>
 hipError_t launch_route(const RouteArgs& a, bool sequential, hipStream_t stream) {
     const int npl = (a.N + kWave - 1) / kWave;
+    // one unit, N <= 1024: two positions a wavefront of 32 lanes each up to N = 256, else one of
+    // 64 lanes, at most 8 cells a lane up to N = 512, while a position's slots fit its lanes with
+    // one to spare (K < LP). Sixteen lanes of sixteen cells measured slower: at N = 256 about one
+    // position in twenty has more candidates than lanes and falls back to the one-position
+    // selection, and a quarter of the wavefronts (two a SIMD at the ref shape) wait for one.
+    if (!sequential && a.M == 1 && a.N <= 1024) {
+        const int N = a.N, K = a.K;
+        if (N <= 256 && K < 32) {
+            if (N <= 32) return launch_grouped<32, 1, 1, IO, IDX>(a, stream);
+            if (N <= 64) return launch_grouped<32, 2, 1, IO, IDX>(a, stream);
+            if (N <= 128) return launch_grouped<32, 4, 2, IO, IDX>(a, stream);
+            return launch_grouped<32, 8, 4, IO, IDX>(a, stream);
+        }
+        if (N > 256 && N <= 512 && K < 64) return launch_grouped<64, 8, 8, IO, IDX>(a, stream);
+        if (N > 512 && K < 64) return launch_grouped<64, 16, 16, IO, IDX>(a, stream);
+    }
     if (!sequential && a.M == 1 && a.N > 1024) {  // a workgroup per position (N <= 4096)
         hipLaunchKernelGGL((route_block<16, IO, IDX>), dim3(a.P, a.B), dim3(256), 0, stream, a);
         return hipGetLastError();
