@@ -931,21 +931,18 @@ hipError_t launch_grouped(const RouteArgs& a, hipStream_t stream) {
 template <typename IO, typename IDX>
 hipError_t launch_route(const RouteArgs& a, bool sequential, hipStream_t stream) {
     const int npl = (a.N + kWave - 1) / kWave;
-    // one unit, N <= 1024: two positions a wavefront of 32 lanes each up to N = 256, else one of
-    // 64 lanes, at most 8 cells a lane up to N = 512, while a position's slots fit its lanes with
-    // one to spare (K < LP). Sixteen lanes of sixteen cells measured slower: at N = 256 about one
-    // position in twenty has more candidates than lanes and falls back to the one-position
-    // selection, and a quarter of the wavefronts (two a SIMD at the ref shape) wait for one.
-    if (!sequential && a.M == 1 && a.N <= 1024) {
-        const int N = a.N, K = a.K;
-        if (N <= 256 && K < 32) {
-            if (N <= 32) return launch_grouped<32, 1, 1, IO, IDX>(a, stream);
-            if (N <= 64) return launch_grouped<32, 2, 1, IO, IDX>(a, stream);
-            if (N <= 128) return launch_grouped<32, 4, 2, IO, IDX>(a, stream);
-            return launch_grouped<32, 8, 4, IO, IDX>(a, stream);
-        }
-        if (N > 256 && N <= 512 && K < 64) return launch_grouped<64, 8, 8, IO, IDX>(a, stream);
-        if (N > 512 && K < 64) return launch_grouped<64, 16, 16, IO, IDX>(a, stream);
+    // one unit, N <= 256, K < 32: two positions a wavefront of 32 lanes each. Sixteen lanes of
+    // sixteen cells measured slower (about one position in twenty has more candidates than lanes
+    // and falls back to the one-position selection, and a quarter of the wavefronts wait for
+    // one), and so did one position of 64 lanes above N = 256 (no second position to share the
+    // instructions, and the 64-lane sort costs more than the one-position bisection: tbptt's
+    // router 20.4 against 17.2 us, bf16's 45.0 against 42.0)
+    if (!sequential && a.M == 1 && a.N <= 256 && a.K < 32) {
+        const int N = a.N;
+        if (N <= 32) return launch_grouped<32, 1, 1, IO, IDX>(a, stream);
+        if (N <= 64) return launch_grouped<32, 2, 1, IO, IDX>(a, stream);
+        if (N <= 128) return launch_grouped<32, 4, 2, IO, IDX>(a, stream);
+        return launch_grouped<32, 8, 4, IO, IDX>(a, stream);
     }
     if (!sequential && a.M == 1 && a.N > 1024) {  // a workgroup per position (N <= 4096)
         hipLaunchKernelGGL((route_block<16, IO, IDX>), dim3(a.P, a.B), dim3(256), 0, stream, a);

@@ -115,6 +115,15 @@ ROUTE_CASES = [
     (2, 4, 130, 1, 8, dict(lambda_cost=0.05), torch.float32, "ties"),
     (2, 4, 100, 1, 6, dict(reserved=2), torch.bfloat16, "nan"),
     (2, 3, 200, 1, 8, dict(), torch.bfloat16, "plain"),
+    # one unit, two positions a wavefront of 32 lanes (N <= 256, K < 32): every score +-0 (more
+    # candidates than the group's lanes: the one-position fallback), the uniform rows (N = 256)
+    # with ties and with a cost term, an odd number of positions (a wavefront's second group
+    # past the window), reserved cells with NaN / inf, 31 slots
+    (2, 3, 200, 1, 8, dict(), torch.float32, "zeros"),
+    (3, 3, 256, 1, 8, dict(), torch.float32, "ties"),
+    (1, 5, 256, 1, 8, dict(lambda_cost=0.05, limit=0.02), torch.float32, "plain"),
+    (2, 4, 48, 1, 5, dict(reserved=2), torch.float32, "nan"),
+    (2, 3, 256, 1, 31, dict(), torch.bfloat16, "ties"),
     # one unit, sixteen or more cells a lane (keys recomputed from the logits in each pass): a row
     # not a multiple of the lane block (scalar loads) with half-integer ties; reserved cells with
     # a cost term and NaN / inf; every logit +-0 (more than 64 candidates: the argmax rounds);
