@@ -246,17 +246,24 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     const float4 h0a = h0_at(gl >> 1);
     const uint8_t rbyte = __builtin_amdgcn_raw_buffer_load_b8(rr, hl < n ? uint32_t(t0 + hl) : kOob, 0u, 0);
 
-    // ---- phase A: loads and activations, 8 positions ahead ------------------------------------
+    // ---- phase A: the chunk's decisions first (its tables need them all), then the slot rows 8
+    // positions ahead, each position's activations and composition as its row arrives ---------
     constexpr int kAhead = 8;
     float2 yv[kP], gv[kP];
     int32_t cv[kP];
+    if constexpr (!Route::kOn) {
+#pragma unroll
+        for (int i = 0; i < kP; ++i)
+            cv[i] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+                rc, active ? uint32_t((t0 + i) * K + k) * 4u : kOob, 0u, 0));
+    }
+    // (issued in position order, the scheduler held at each: position i's wait is then for its
+    // own row and the older ones only)
     auto fetch = [&](int i) __attribute__((always_inline)) {
         const uint32_t vo = vrow + uint32_t(i) * pos_bytes;
         yv[i] = ld2(ry, vo);
         gv[i] = ld2(rg, vo);
-        if constexpr (!Route::kOn)
-            cv[i] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
-                rc, active ? uint32_t((t0 + i) * K + k) * 4u : kOob, 0u, 0));
+        __builtin_amdgcn_sched_barrier(0);
     };
 #pragma unroll
     for (int i = 0; i < kAhead; ++i) fetch(i);
@@ -282,19 +289,7 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     // its first chunk's maps, clear of the dummy entries, before the chunk composes them)
     if constexpr (Route::kOn) route.decide(b, slice, w, stamp, lds + Lo.maps + uint32_t(2 * w) * kMapBytes);
 
-    float2 omb[kP], bcv[kP];
-    uint32_t vmask = 0u, pmask = 0u;  // valid and padded positions of this lane's slot
     if constexpr (Route::kOn) {
-        // the loads and activations while the row's other workgroups decide, then the row's
-        // decisions
-#pragma unroll
-        for (int i = 0; i < kP; ++i) {
-            if (i + kAhead < kP) fetch(i + kAhead);
-            const float b0 = fast_sigmoid(gv[i].x), b1 = fast_sigmoid(gv[i].y);
-            const float c0 = fast_tanh(yv[i].x), c1 = fast_tanh(yv[i].y);
-            omb[i] = make_float2(1.0f - b0, 1.0f - b1);
-            bcv[i] = make_float2(b0 * c0, b1 * c1);
-        }
         // the row's decisions as int16 in chunk 0's maps, below its dummy entry (T K <= 2048):
         // the maps are free until the composition, and the gather's barrier orders its writes
         // after every wavefront's decisions (whose scratch is there too)
@@ -306,23 +301,12 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
                                     : -1;
         __syncthreads();  // every read of the table before chunk 0 composes over it
     }
+    uint32_t vmask = 0u, pmask = 0u;  // valid and padded positions of this lane's slot
 #pragma unroll
     for (int i = 0; i < kP; ++i) {
-        if constexpr (!Route::kOn) {
-            if (i + kAhead < kP) fetch(i + kAhead);
-        }
         const int c = cv[i];
         const bool inb = active && i < n;
         const bool ok = inb && c >= 0;
-        if constexpr (Route::kOn) {
-            omb[i] = ok ? omb[i] : make_float2(1.0f, 1.0f);
-            bcv[i] = ok ? bcv[i] : make_float2(0.0f, 0.0f);
-        } else {
-            const float b0 = fast_sigmoid(gv[i].x), b1 = fast_sigmoid(gv[i].y);
-            const float c0 = fast_tanh(yv[i].x), c1 = fast_tanh(yv[i].y);
-            omb[i] = ok ? make_float2(1.0f - b0, 1.0f - b1) : make_float2(1.0f, 1.0f);
-            bcv[i] = ok ? make_float2(b0 * c0, b1 * c1) : make_float2(0.0f, 0.0f);
-        }
         vmask |= ok ? 1u << i : 0u;
         pmask |= inb && c < 0 ? 1u << i : 0u;
         cv[i] = ok ? c : N;  // the first-event table's row (N: the idle slots' row)
@@ -377,12 +361,23 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
 
     // compose the chunk's maps: alpha' = (1 - b) alpha, beta' = (1 - b) beta + b c, an entry's
     // first event starting from (1, 0), or (0, 0) after a reset in the chunk; a reset zeroes the
-    // entries created before it (idle and padded slots compose the identity on kDummy)
+    // entries created before it (idle and padded slots compose the identity on kDummy). Position
+    // i's activations come first: its row is the oldest load in flight, and the loads 8 positions
+    // ahead go out as each position is taken, so the composition runs while the rows arrive.
+    float2 omb[kP], bcv[kP];
     auto compose = [&](auto rs_c) __attribute__((always_inline)) {
         constexpr bool kRs = decltype(rs_c)::value;
         float ainit = 1.0f;
 #pragma unroll
         for (int i = 0; i < kP; ++i) {
+            if (i + kAhead < kP) fetch(i + kAhead);
+            {
+                const bool ok = (vmask >> i) & 1u;
+                const float b0 = fast_sigmoid(gv[i].x), b1 = fast_sigmoid(gv[i].y);
+                const float c0 = fast_tanh(yv[i].x), c1 = fast_tanh(yv[i].y);
+                omb[i] = ok ? make_float2(1.0f - b0, 1.0f - b1) : make_float2(1.0f, 1.0f);
+                bcv[i] = ok ? make_float2(b0 * c0, b1 * c1) : make_float2(0.0f, 0.0f);
+            }
             if (kRs && ((rmask >> i) & 1u)) {
                 zero_entries(i * kK, true);
                 ainit = 0.0f;
