@@ -812,20 +812,30 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
         qa[H] = ld2(rqa, vqp);
         qb[H] = ld2(rqb, vqp);
     }
+    // the window-end summary cotangent of the column pair (the chunks' R starts there): loaded
+    // here, before the gates, so that the wait for it after the barrier holds none of them
+    const rsrc_t rqT = make_rsrc(a.dq_T ? a.dq_T + size_t(b) * d : nullptr, a.dq_T ? uint32_t(d) * 4u : 0u);
+    const float2 dqT = ld2(rqT, vq);
 
-    // ---- phase A: the gates, the selection cotangents and the decisions, 8 positions ahead ----
+    // ---- phase A: the chunk's decisions first (its tables need them all), then the gates and
+    // the selection cotangents latest position first, 8 positions ahead of the composition ----
     constexpr int kAhead = 8;
     float2 gv[kP], dv[kP];
     int32_t cv[kP];
+#pragma unroll
+    for (int i = 0; i < kP; ++i)
+        cv[i] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+            rc, active ? uint32_t((t0 + i) * K + k) * 4u : kOob, 0u, 0));
+    // (issued in the composition's order, the scheduler held at each: a position's wait is then
+    // for its own rows and the ones issued before)
     auto fetch = [&](int i) __attribute__((always_inline)) {
         const uint32_t vo = vrow + uint32_t(i) * pos_bytes;
         gv[i] = ld2(rg, vo);
         dv[i] = ld2(rds, vo);
-        cv[i] = static_cast<int32_t>(__builtin_amdgcn_raw_buffer_load_b32(
-            rc, active ? uint32_t((t0 + i) * K + k) * 4u : kOob, 0u, 0));
+        __builtin_amdgcn_sched_barrier(0);
     };
 #pragma unroll
-    for (int i = 0; i < kAhead; ++i) fetch(i);
+    for (int i = kP - 1; i >= kP - kAhead; --i) fetch(i);
 
     // this chunk's columns of the tables while the loads are in flight (no other half-wave reads
     // them before phase B): no event (0xff; row N kDummy) and the dummy entry's identity (1, 0)
@@ -879,16 +889,11 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
         if (cp == 0) lds_ref<int32_t>(lds, Lo.rflag + 4u * ch) = wr[0] || wr[1] ? 1 : 0;
     }
 
-    float2 omb[kP], dsv[kP];
     uint32_t vmask = 0u;  // the lane's valid positions
 #pragma unroll
     for (int i = 0; i < kP; ++i) {
-        if (i + kAhead < kP) fetch(i + kAhead);
         const int c = cv[i];
         const bool ok = active && i < n && c >= 0;
-        const float b0 = fast_sigmoid(gv[i].x), b1 = fast_sigmoid(gv[i].y);
-        omb[i] = ok ? make_float2(1.0f - b0, 1.0f - b1) : make_float2(1.0f, 1.0f);
-        dsv[i] = ok ? dv[i] : make_float2(0.0f, 0.0f);
         vmask |= ok ? 1u << i : 0u;
         cv[i] = ok ? c : N;  // the last-event table's row (N: the idle slots' row)
     }
@@ -918,14 +923,16 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
     };
     constexpr int kEarly = 4;  // positions issued before the barrier
 #pragma unroll
-    for (int i = kP - 1; i >= kP - kEarly; --i) fetch_c(i);
+    for (int i = kP - 1; i >= kP - kEarly; --i) {
+        fetch_c(i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     __syncthreads();  // every chunk's summary map
 
     // R at the chunk's end: d q_T through the later chunks' maps; then each position's share
     // (R after the later positions, plus the position's d q_post, over N), rounded once to fp32
     {
-        double Rx = a.dq_T ? double(a.dq_T[size_t(b) * d + col]) : 0.0;
-        double Ry = a.dq_T ? double(a.dq_T[size_t(b) * d + col + 1]) : 0.0;
+        double Rx = double(dqT.x), Ry = double(dqT.y);
 #pragma unroll
         for (int j = kChunks - 1; j > 0; --j) {
             if (j > ch) {
@@ -979,13 +986,26 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
     // compose the chunk's maps latest position first: mu' = (1 - b) mu, nu' = (1 - b) (nu + dsel)
     // - b s, an entry's first (latest) event from (1, 0), or (0, 0) once a reset has passed; a
     // reset zeroes the entries created so far. Idle and padded slots compose the identity on
-    // kDummy (their b s term is an exact zero, whatever the share holds).
+    // kDummy (their b s term is an exact zero, whatever the share holds). Each position's gate
+    // comes first (its rows are the oldest of the gates in flight); the gates 8 positions on and
+    // the replay's rows 4 on go out as each position is taken.
+    float2 omb[kP], dsv[kP];
     auto compose = [&](auto rs_c) __attribute__((always_inline)) {
         constexpr bool kRs = decltype(rs_c)::value;
         float ainit = 1.0f;
 #pragma unroll
         for (int i = kP - 1; i >= 0; --i) {
-            if (i - kEarly >= 0) fetch_c(i - kEarly);
+            if (i - kAhead >= 0) fetch(i - kAhead);
+            if (i - kEarly >= 0) {
+                fetch_c(i - kEarly);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            {
+                const bool ok = (vmask >> i) & 1u;
+                const float b0 = fast_sigmoid(gv[i].x), b1 = fast_sigmoid(gv[i].y);
+                omb[i] = ok ? make_float2(1.0f - b0, 1.0f - b1) : make_float2(1.0f, 1.0f);
+                dsv[i] = ok ? dv[i] : make_float2(0.0f, 0.0f);
+            }
             const uint32_t e = ent(i);
             const bool first = e == uint32_t(i * kK + k);
             const float2 sh = share_at(i);
