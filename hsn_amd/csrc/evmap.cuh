@@ -989,9 +989,12 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
     // kDummy (their b s term is an exact zero, whatever the share holds). Each position's gate
     // comes first (its rows are the oldest of the gates in flight); the gates 8 positions on and
     // the replay's rows 4 on go out as each position is taken.
+    // One code path for chunks with and without resets: the replay's loads issued here stay in
+    // flight through the barrier below, where two paths would join with different loads pending
+    // and the join would wait for all of them.
+    const bool wave_rs = ballot(rmask != 0u) != 0u;  // a reset in the wave's chunks (the replay)
     float2 omb[kP], dsv[kP];
-    auto compose = [&](auto rs_c) __attribute__((always_inline)) {
-        constexpr bool kRs = decltype(rs_c)::value;
+    {
         float ainit = 1.0f;
 #pragma unroll
         for (int i = kP - 1; i >= 0; --i) {
@@ -1016,15 +1019,14 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
             mu_at(e) = make_float2(o.x * (first ? ainit : mu.x), o.y * (first ? ainit : mu.y));
             nu_at(e) = make_float2(o.x * ((first ? 0.0f : nu.x) + dsv[i].x) - bsx,
                                    o.y * ((first ? 0.0f : nu.y) + dsv[i].y) - bsy);
-            if (kRs && ((rmask >> i) & 1u)) {
+            if ((rmask >> i) & 1u) {
                 zero_from(i * kK, true);
                 ainit = 0.0f;
             }
+            // the replay reads the slot's validity from the sign: 1 - b is +0 or more when valid
+            omb[i] = (vmask >> i) & 1u ? o : make_float2(-1.0f, -1.0f);
         }
-    };
-    const bool wave_rs = ballot(rmask != 0u) != 0u;
-    if (wave_rs) compose(std::true_type{});
-    else compose(std::false_type{});
+    }
 
     __syncthreads();
 
@@ -1107,7 +1109,7 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
             // entry may be the one just written: LDS keeps one wave's accesses in order)
             if (!kRs && i > 0) A = mu_at(ent(i - 1));
             const float cx = fast_tanh(yv[i].x), cy = fast_tanh(yv[i].y);
-            const uint32_t vm = bitmask_at(vmask, i);
+            const uint32_t vm = ~uint32_t(__float_as_int(o.x) >> 31);  // -1 marks an idle slot
             const float dcx = and_f32(bgx * (1.0f - cx * cx) * G.x, vm);
             const float dcy = and_f32(bgy * (1.0f - cy * cy) * G.y, vm);
             const float dbx = and_f32((cx - hv[i].x) * (o.x * bgx) * G.x, vm);
