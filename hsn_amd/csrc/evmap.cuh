@@ -1023,7 +1023,8 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
                 zero_from(i * kK, true);
                 ainit = 0.0f;
             }
-            // the replay reads the slot's validity from the sign: 1 - b is +0 or more when valid
+            // the replay reads the slot's validity from here: 1 - b is never -1 (it is in [0, 1],
+            // or NaN from a NaN gate, which the replay propagates as before)
             omb[i] = (vmask >> i) & 1u ? o : make_float2(-1.0f, -1.0f);
         }
     }
@@ -1109,7 +1110,7 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
             // entry may be the one just written: LDS keeps one wave's accesses in order)
             if (!kRs && i > 0) A = mu_at(ent(i - 1));
             const float cx = fast_tanh(yv[i].x), cy = fast_tanh(yv[i].y);
-            const uint32_t vm = ~uint32_t(__float_as_int(o.x) >> 31);  // -1 marks an idle slot
+            const uint32_t vm = o.x == -1.0f ? 0u : ~0u;  // -1 marks an idle or padded slot
             const float dcx = and_f32(bgx * (1.0f - cx * cx) * G.x, vm);
             const float dcy = and_f32(bgy * (1.0f - cy * cy) * G.y, vm);
             const float dbx = and_f32((cx - hv[i].x) * (o.x * bgx) * G.x, vm);

@@ -59,7 +59,7 @@ def _close(got, want, tol, what=""):
     both_nan = torch.isnan(got) & torch.isnan(want)
     err = (got - want).abs().masked_fill(both_nan, 0)
     bound = tol * want.abs().clamp(min=1.0)
-    bad = ~(err <= bound)
+    bad = ~((err <= bound) | both_nan)  # (a NaN in want makes its bound NaN)
     if bool(bad.any()):
         i = int(bad.flatten().nonzero()[0])
         raise AssertionError(f"{what}: {int(bad.sum())} elements out of tolerance {tol}; first at "
@@ -366,6 +366,39 @@ def test_backward_without_optional_cotangents(dev, path):
                    f"d_q0 {present}")
         else:
             assert bool((gb[3] == 0).all())
+
+
+def test_backward_propagates_a_nan_gate(dev, path):
+    """A NaN gate input on a selected slot: the backward's NaNs fall where the oracle's do (that
+    slot's column, the cell's earlier positions through its cotangent, its later ones through
+    h_old) and the rest stays within tolerance; padded slots still write exact zeros."""
+    from hsn_amd import window
+
+    c = dict(B=2, T=40, N=24, d=16, K=4, io="f32", limit=0.15)
+    _skip_unless_taken(path, c)
+    cfg_w, w, cot, cost, cfg, _ = _window_case(c, 91)
+    plain = O.window_forward(w["logits"], w["y"], w["gate_pre"], w["reset"], w["h0"], w["q0"],
+                             w["age0"], w["pos0"], cost, **_oracle_route_kwargs(cfg))
+    t, k = 21, 1
+    assert bool(plain["valid"][0, t, k]) and bool((~plain["valid"]).any())
+    w["gate_pre"][0, t, k, 3] = float("nan")
+    fw = O.window_forward(w["logits"], w["y"], w["gate_pre"], w["reset"], w["h0"], w["q0"],
+                          w["age0"], w["pos0"], cost, **_oracle_route_kwargs(cfg))
+    sel = _valid_mask(cot["d_h_sel"], fw["valid"])
+    wb = O.window_backward(w["y"], w["gate_pre"], fw["h_old"], fw["cells"], fw["valid"],
+                           w["reset"], cfg_w.N, cot["d_q_pre"], cot["d_q_post"], sel,
+                           cot["d_h_T"], cot["d_q_T"])
+    gb = window.window_backward(w["y"].to(dev), w["gate_pre"].to(dev), fw["h_old"].to(dev),
+                                fw["cells"].int().to(dev), fw["valid"].to(dev),
+                                w["reset"].to(dev), cfg_w.N, cot["d_q_pre"].to(dev),
+                                cot["d_q_post"].to(dev), sel.to(dev), cot["d_h_T"].to(dev),
+                                cot["d_q_T"].to(dev))
+    assert bool(torch.isnan(wb[0][0, t, k, 3])) and bool(torch.isnan(wb[1][0, t, k, 3]))
+    for name, g_, w_ in zip(("dy", "dgate", "d_h0"), gb[:3], wb[:3]):
+        assert torch.equal(torch.isnan(g_.cpu()), torch.isnan(w_)), name
+        _close(g_, w_, F32_TOL, name)
+    pad = ~fw["valid"]
+    assert bool((gb[0].cpu()[pad] == 0).all()) and bool((gb[1].cpu()[pad] == 0).all())
 
 
 def test_bf16_storage_rounds_like_torch(dev, path):
