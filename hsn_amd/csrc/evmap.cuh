@@ -30,6 +30,15 @@
 
 #include "sweep.cuh"
 
+// Phase stamps: a measurement build (hsn_amd/probes/evmap_phases.hip) defines HSN_EVMAP_STAMPS
+// and these hooks, which record the real-time counter at the kernels' phase edges; in the
+// library they compile to nothing.
+#ifndef HSN_EVMAP_STAMPS
+#define HSN_EVMAP_STAMPS_BEGIN()
+#define HSN_EVMAP_STAMP(i)
+#define HSN_EVMAP_STAMPS_END(which)
+#endif
+
 namespace hsn {
 namespace evmap {
 
@@ -196,6 +205,7 @@ template <typename IN, typename Route>
 __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     static_assert(sizeof(IN) == 4, "fp32 rows");
     extern __shared__ __align__(16) unsigned char lds[];
+    HSN_EVMAP_STAMPS_BEGIN();
     const int N = a.N, d = a.d, K = a.K, T = a.T;
     const Layout Lo = fwd_layout(N);
     const int lane = lane_id();
@@ -246,6 +256,7 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     const float4 h0a = h0_at(gl >> 1);
     const uint8_t rbyte = __builtin_amdgcn_raw_buffer_load_b8(rr, hl < n ? uint32_t(t0 + hl) : kOob, 0u, 0);
 
+    HSN_EVMAP_STAMP(1);
     // ---- phase A: the chunk's decisions first (its tables need them all), then the slot rows 8
     // positions ahead, each position's activations and composition as its row arrives ---------
     constexpr int kAhead = 8;
@@ -364,6 +375,7 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     // entries created before it (idle and padded slots compose the identity on kDummy). Position
     // i's activations come first: its row is the oldest load in flight, and the loads 8 positions
     // ahead go out as each position is taken, so the composition runs while the rows arrive.
+    HSN_EVMAP_STAMP(2);
     float2 omb[kP], bcv[kP];
     auto compose = [&](auto rs_c) __attribute__((always_inline)) {
         constexpr bool kRs = decltype(rs_c)::value;
@@ -396,6 +408,7 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     else compose(std::false_type{});
     __syncthreads();
 
+    HSN_EVMAP_STAMP(3);
     // ---- phase B: every cell through the 16 chunks, two threads a cell -----------------------
     {
         uint32_t rflags = 0u;  // chunks with a reset
@@ -483,6 +496,7 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     }
     __syncthreads();
 
+    HSN_EVMAP_STAMP(4);
     // ---- phase C: the replay -------------------------------------------------------------------
     // b c moves to the chunk's beta table (free after phase B): 32 lanes x 16 positions x 8 bytes,
     // the 4160 bytes of the table less 64, so the replay holds only 1 - b in registers
@@ -644,6 +658,7 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
         eight(std::false_type{}, std::integral_constant<int, 1>{});
     }
 
+    HSN_EVMAP_STAMP(5);
     // the chunks' maps (half 0, then half 1), scanned across the chunks from q0, give each chunk
     // its start q; then each lane's two positions
     if (g == 0) {
@@ -683,6 +698,8 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
             st2(make_float2(q.x + qc[H].x, q.y + qc[H].y), rqb, vqp);
         }
     }
+    HSN_EVMAP_STAMP(6);
+    HSN_EVMAP_STAMPS_END(0);
     // the maps are free again: the row maxima's exchange accumulates in chunk 0's
     if constexpr (Route::kOn) route.finish(b, slice, stamp, a.h_max, lds + Lo.maps);
 }
@@ -761,6 +778,7 @@ template <typename IN>
 __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
     static_assert(sizeof(IN) == 4, "fp32 rows");
     extern __shared__ __align__(16) unsigned char lds[];
+    HSN_EVMAP_STAMPS_BEGIN();
     const int N = a.N, d = a.d, K = a.K, T = a.T;
     const BwdLayout Lo = bwd_layout(N);
     const int lane = lane_id();
@@ -817,6 +835,7 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
     const rsrc_t rqT = make_rsrc(a.dq_T ? a.dq_T + size_t(b) * d : nullptr, a.dq_T ? uint32_t(d) * 4u : 0u);
     const float2 dqT = ld2(rqT, vq);
 
+    HSN_EVMAP_STAMP(1);
     // ---- phase A: the chunk's decisions first (its tables need them all), then the gates and
     // the selection cotangents latest position first, 8 positions ahead of the composition ----
     constexpr int kAhead = 8;
@@ -927,6 +946,7 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
         fetch_c(i);
         __builtin_amdgcn_sched_barrier(0);
     }
+    HSN_EVMAP_STAMP(2);
     __syncthreads();  // every chunk's summary map
 
     // R at the chunk's end: d q_T through the later chunks' maps; then each position's share
@@ -963,6 +983,7 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
             a.dq0[size_t(b) * d + col + 1] = static_cast<float>(sy);
         }
     }
+    HSN_EVMAP_STAMP(3);
     const uint32_t sh_base = Lo.share + 4u * uint32_t(ch * kP * kS + 2 * cp);
     auto share_at = [&](int i) __attribute__((always_inline)) -> float2 {
         return lds_ref<float2>(lds, sh_base + uint32_t(i) * kS * 4u);
@@ -1031,6 +1052,7 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
 
     __syncthreads();
 
+    HSN_EVMAP_STAMP(4);
     // ---- phase B: every cell from d_h_T back through the 16 chunks, two threads a cell -------
     {
         uint32_t rflags = 0u;  // chunks with a reset
@@ -1081,6 +1103,7 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
     }
     __syncthreads();
 
+    HSN_EVMAP_STAMP(5);
     // ---- phase C: the replay, latest position first ------------------------------------------
     // the selection cotangents move to the chunk's nu table (free after phase B): 32 lanes x 16
     // positions x 8 bytes
@@ -1123,6 +1146,8 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
     };
     if (wave_rs) replay(std::true_type{});
     else replay(std::false_type{});
+    HSN_EVMAP_STAMP(6);
+    HSN_EVMAP_STAMPS_END(1);
 }
 
 }  // namespace evmap
