@@ -298,7 +298,10 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
 
     // the wavefront's share of the decisions while the first slot rows load (its LDS scratch in
     // its first chunk's maps, clear of the dummy entries, before the chunk composes them)
-    if constexpr (Route::kOn) route.decide(b, slice, w, stamp, lds + Lo.maps + uint32_t(2 * w) * kMapBytes);
+    if constexpr (Route::kOn) {
+        route.decide(b, slice, w, stamp, lds + Lo.maps + uint32_t(2 * w) * kMapBytes);
+        HSN_EVMAP_STAMP(9);
+    }
 
     if constexpr (Route::kOn) {
         // the row's decisions as int16 in chunk 0's maps, below its dummy entry (T K <= 2048):

@@ -51,8 +51,11 @@ void hsn::clear_last_error() {}
 
 namespace {
 
-void report(const char* what, const std::vector<unsigned long long>& h, const char* const* names) {
-    constexpr int kEdges = 9;  // stamps 0..6, the last store issued (7), every store done (8)
+// `edges`: the stamps in the order the kernel reaches them (0..6 at the phase edges, 7 the last
+// store issued, 8 every store done, 9 the routed forward's decisions made)
+void report(const char* what, const std::vector<unsigned long long>& h, const char* const* names,
+            const std::vector<int>& edges) {
+    const int kEdges = int(edges.size());
     unsigned long long t0 = ~0ull;
     for (size_t i = 0; i < h.size(); i += 10) t0 = std::min(t0, h[i]);
     const auto us = [&](unsigned long long t) { return double(t - t0) * 0.01; };
@@ -61,15 +64,16 @@ void report(const char* what, const std::vector<unsigned long long>& h, const ch
         double sum = 0, mx = 0;
         size_t n = 0;
         for (size_t i = 0; i < h.size(); i += 10, ++n) {
-            sum += us(h[i + p]);
-            mx = std::max(mx, us(h[i + p]));
+            sum += us(h[i + edges[p]]);
+            mx = std::max(mx, us(h[i + edges[p]]));
         }
         std::printf("  %-28s mean %6.2f  max %6.2f\n", names[p], sum / n, mx);
     }
     std::printf("  span of each phase over the wavefronts (us):\n");
     for (int p = 1; p < kEdges; ++p) {
         std::vector<double> d;
-        for (size_t i = 0; i < h.size(); i += 10) d.push_back(double(h[i + p] - h[i + p - 1]) * 0.01);
+        for (size_t i = 0; i < h.size(); i += 10)
+            d.push_back(double(h[i + edges[p]] - h[i + edges[p - 1]]) * 0.01);
         std::sort(d.begin(), d.end());
         std::printf("    %-26s p10 %5.2f  p50 %5.2f  p90 %5.2f  max %5.2f\n", names[p], d[d.size() / 10],
                     d[d.size() / 2], d[d.size() * 9 / 10], d.back());
@@ -77,7 +81,7 @@ void report(const char* what, const std::vector<unsigned long long>& h, const ch
     const size_t nwg = h.size() / 80;
     std::vector<double> end(nwg, 0.0);
     for (size_t w = 0; w < nwg; ++w)
-        for (int v = 0; v < 8; ++v) end[w] = std::max(end[w], us(h[(w * 8 + v) * 10 + kEdges - 1]));
+        for (int v = 0; v < 8; ++v) end[w] = std::max(end[w], us(h[(w * 8 + v) * 10 + 8]));
     std::sort(end.begin(), end.end());
     std::printf("  workgroups' last store done (us): p10 %.2f  p50 %.2f  p90 %.2f  max %.2f\n",
                 end[nwg / 10], end[nwg / 2], end[nwg * 9 / 10], end.back());
@@ -187,12 +191,71 @@ int main() {
                                 "phase A barrier passed", "phase B (walk) barrier passed",
                                 "replay done", "summary scanned and stored",
                                 "last store issued", "every store done"};
-    report("forward", h, fwd_names);
+    const std::vector<int> in_order = {0, 1, 2, 3, 4, 5, 6, 7, 8};
+    report("forward", h, fwd_names, in_order);
     CK(hipMemcpy(h.data(), st_b, words * 8, hipMemcpyDeviceToHost));
     const char* bwd_names[9] = {"start", "first loads issued", "summary maps, tables built",
                                 "shares written, compose starts", "phase A barrier passed",
                                 "phase B (walk) barrier passed", "replay done",
                                 "last store issued", "every store done"};
-    report("backward", h, bwd_names);
+    report("backward", h, bwd_names, in_order);
+
+    // the forward that routes its own window (hsn_win_route_forward's one launch): logits N(0, 1)
+    std::vector<float> logits(size_t(B) * T * N);
+    for (auto& v : logits) v = nd(rng);
+    float *lg_, *cost_, *th_;
+    int32_t *cells_, *units_, *rslots_;
+    uint8_t *valid_, *refr_;
+    CK(hipMalloc(&lg_, logits.size() * 4));
+    CK(hipMalloc(&cost_, 4));
+    CK(hipMalloc(&th_, size_t(B) * T * 4));
+    for (int32_t** p : {&cells_, &units_, &rslots_}) CK(hipMalloc(p, size_t(B) * T * K * 4));
+    for (uint8_t** p : {&valid_, &refr_}) CK(hipMalloc(p, size_t(B) * T * K));
+    CK(hipMemcpy(lg_, logits.data(), logits.size() * 4, hipMemcpyHostToDevice));
+    const float c0 = 1.0f / N;
+    CK(hipMemcpy(cost_, &c0, 4, hipMemcpyHostToDevice));
+    WindowRouteSpec r{};
+    r.logits = lg_, r.width = 1, r.cost = cost_, r.cells = cells_, r.units = units_;
+    r.valid = valid_, r.theta = th_, r.refreshed = refr_, r.slots = rslots_, r.reserved = 0;
+    r.lambda = 0.0f, r.overhead = 0.0f, r.shared = 0.0f, r.limit = 1.00001f;
+    const char* why = nullptr;
+    if (!evmap_route_claim(nullptr, B, d, true, &why)) {
+        std::printf("routed forward not taken: %s\n", why);
+        return 0;
+    }
+    const auto routed = [&] {
+        evmap_route_forward(r, y_, g_, rs_, h0_, q0_, a0_, p0_, qa_, qb_, hs_, ho_, hm_, hT_, qT_,
+                            aT_, pT_, B, T, N, d, K, nullptr);
+    };
+    try {
+        CK(hipMemcpyToSymbol(HIP_SYMBOL(g_evmap_stamps), none, sizeof(none)));
+        for (int i = 0; i < 3; ++i) routed();
+        CK(hipDeviceSynchronize());
+        float tr = 0;
+        CK(hipEventRecord(e0));
+        for (int i = 0; i < 20; ++i) routed();
+        CK(hipEventRecord(e1));
+        CK(hipEventSynchronize(e1));
+        CK(hipEventElapsedTime(&tr, e0, e1));
+        std::printf("back-to-back launches (instrumented build): routed forward %.2f us\n", tr * 1e3f / 20);
+        unsigned long long* on[2] = {st_f, st_b};
+        CK(hipMemcpyToSymbol(HIP_SYMBOL(g_evmap_stamps), on, sizeof(on)));
+        routed();
+        CK(hipDeviceSynchronize());
+    } catch (const AbiError& e) {
+        std::printf("library error: %s\n", e.message.c_str());
+        return 1;
+    }
+    CK(hipMemcpy(h.data(), st_f, words * 8, hipMemcpyDeviceToHost));
+    const char* routed_names[10] = {"start", "first loads issued (logits first)",
+                                    "the wavefront's decisions made",
+                                    "row's decisions gathered, tables built",
+                                    "phase A barrier passed", "phase B (walk) barrier passed",
+                                    "replay done", "summary scanned and stored",
+                                    "last store issued", "every store done"};
+    report("routed forward", h, routed_names, {0, 1, 9, 2, 3, 4, 5, 6, 7, 8});
+    unsigned timeouts = 0;
+    CK(hipMemcpyFromSymbol(&timeouts, HIP_SYMBOL(g_exchange_timeouts), sizeof(timeouts)));
+    std::printf("exchange waits that reached their limit: %u\n", timeouts);
     return 0;
 }
