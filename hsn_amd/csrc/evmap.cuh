@@ -528,14 +528,12 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
         constexpr int H = decltype(h_c)::value;
         float2 dl[8];
         uint32_t lmv[8];
-        // without a reset the next position's read goes out right after this position's write,
-        // ahead of the row-maximum bookkeeping (its entry may be the one just written: LDS keeps
-        // one wave's accesses in order)
-        float2 h = make_float2(0.0f, 0.0f), bc = h;
-        if (!kRs) {
-            h = al_at(rent(8 * H));
-            bc = lds_ref<float2>(lds, bc_base + uint32_t(8 * H) * 256u);
-        }
+        // the next position's read goes out right after this position's write, ahead of the
+        // row-maximum bookkeeping (its entry may be the one just written: LDS keeps one wave's
+        // accesses in order); at a reset the entries are zeroed after that read, so the value is
+        // taken as zero
+        float2 h = al_at(rent(8 * H));
+        float2 bc = lds_ref<float2>(lds, bc_base + uint32_t(8 * H) * 256u);
 #pragma unroll
         for (int ii = 0; ii < 8; ++ii) {
             const int i = 8 * H + ii;
@@ -543,9 +541,8 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
                 if ((rmask >> i) & 1u) {  // every value of the chunk restarts at zero
                     zero_entries(kEnt - 1, false);  // the entries and cell 0's start value
                     for (int e = hl; e < kEnt; e += 32) lds_ref<uint32_t>(lds, cmx_base + 4u * e) = 0u;
+                    h = make_float2(0.0f, 0.0f);
                 }
-                h = al_at(rent(i));
-                bc = lds_ref<float2>(lds, bc_base + uint32_t(i) * 256u);
             }
             const uint32_t e = ent(i);
             const float2 hn = make_float2(omb[i].x * h.x + bc.x, omb[i].y * h.y + bc.y);
@@ -557,7 +554,7 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
                 hs = make_float2(sel_f32(pm, c0.x, hn.x), sel_f32(pm, c0.y, hn.y));
             }
             const float2 hcur = h;
-            if (!kRs && ii + 1 < 8) {
+            if (ii + 1 < 8) {
                 h = al_at(rent(i + 1));
                 bc = lds_ref<float2>(lds, bc_base + uint32_t(i + 1) * 256u);
             }
@@ -1119,12 +1116,13 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
     asm volatile("" : "+v"(vrow_c));  // recomputed here, not held from phase A's loads
     auto replay = [&](auto rs_c) __attribute__((always_inline)) {
         constexpr bool kRs = decltype(rs_c)::value;
-        float2 A = make_float2(0.0f, 0.0f);
-        if (!kRs) A = mu_at(ent(kP - 1));
+        // the next position's read goes out right after this position's write (its entry may be
+        // the one just written: LDS keeps one wave's accesses in order); a reset zeroes the
+        // entries after that read, so the value is taken as zero
+        float2 A = mu_at(ent(kP - 1));
 #pragma unroll
         for (int i = kP - 1; i >= 0; --i) {
             const uint32_t e = ent(i);
-            if (kRs) A = mu_at(e);
             const float2 ds = lds_ref<float2>(lds, ds_base + uint32_t(i) * 256u);
             const float2 sh = share_at(i);
             const float2 o = omb[i];
@@ -1132,9 +1130,7 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
             const float2 G = make_float2(carried.x + sh.x, carried.y + sh.y);
             const float bgx = 1.0f - o.x, bgy = 1.0f - o.y;
             mu_at(e) = make_float2(o.x * carried.x - bgx * sh.x, o.y * carried.y - bgy * sh.y);
-            // without a reset the next position's read goes out right after this write (its
-            // entry may be the one just written: LDS keeps one wave's accesses in order)
-            if (!kRs && i > 0) A = mu_at(ent(i - 1));
+            if (i > 0) A = mu_at(ent(i - 1));
             const float cx = fast_tanh(yv[i].x), cy = fast_tanh(yv[i].y);
             const uint32_t vm = o.x == -1.0f ? 0u : ~0u;  // -1 marks an idle or padded slot
             const float dcx = and_f32(bgx * (1.0f - cx * cx) * G.x, vm);
@@ -1144,7 +1140,10 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
             const uint32_t vo = i < n ? vrow_c + uint32_t(i) * pos_bytes : kOob;
             st2(make_float2(dcx, dcy), rdy, vo);
             st2(make_float2(dbx, dby), rdg, vo);
-            if (kRs && ((rmask >> i) & 1u)) zero_from(0, false);  // every cotangent restarts at 0
+            if (kRs && ((rmask >> i) & 1u)) {  // every cotangent restarts at 0
+                zero_from(0, false);
+                A = make_float2(0.0f, 0.0f);
+            }
         }
     };
     if (wave_rs) replay(std::true_type{});

@@ -6,6 +6,7 @@
 // uninstrumented launch sequence for comparison (the stamps cost a few instructions a phase).
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <random>
 #include <vector>
 
@@ -89,8 +90,10 @@ void report(const char* what, const std::vector<unsigned long long>& h, const ch
 
 }  // namespace
 
-int main() {
+int main(int argc, char** argv) {
     using namespace hsn;
+    // argv[1]: one reset in this many positions (default 256; 0 for none)
+    const int reset_every = argc > 1 ? std::atoi(argv[1]) : 256;
     const int B = 32, T = 256, N = 256, d = 64, K = 8;
     const size_t ne = size_t(B) * T * K * d, nq = size_t(B) * T * d, nh = size_t(B) * N * d;
     // the ref workload's distributions: rows N(0, 1), gates N(2, 0.5), start state N(0, 0.1),
@@ -112,7 +115,9 @@ int main() {
         for (int k = 0; k < K; ++k) slots[bt * K + k] = perm[k];
     }
     std::vector<uint8_t> reset(size_t(B) * T);
-    for (auto& r : reset) r = ud(rng) < 1.0f / 256 ? 1 : 0;
+    for (auto& r : reset) r = reset_every > 0 && ud(rng) < 1.0f / float(reset_every) ? 1 : 0;
+    std::printf("resets: Bernoulli(1/%d), %d in the window's %d rows\n", reset_every,
+                int(std::count(reset.begin(), reset.end(), uint8_t(1))), B);
 
     float *dy_, *dg_, *y_, *g_, *ho_, *hs_, *qa_, *qb_, *hm_, *h0_, *q0_, *hT_, *qT_, *ds_, *dqa_,
         *dqb_, *dhT_, *dqT_, *dh0_, *dq0_;

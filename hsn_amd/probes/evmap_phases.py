@@ -1,6 +1,7 @@
 """Build and run the event-map phase timeline (``evmap_phases.hip``) on the current GPU.
 
-``python -m hsn_amd.probes.evmap_phases`` compiles the probe with the library's hipcc flags into
+``python -m hsn_amd.probes.evmap_phases [N]`` (one reset in N positions, default 256, 0 for
+none) compiles the probe with the library's hipcc flags into
 ``_build/evmap_phases`` (the event-map kernels with their phase-stamp hooks on) and prints its
 report: for the forward and the backward at the ref shape, when each phase edge is reached
 (mean and largest over the wavefronts), the spread of each phase's span and of the workgroups'
@@ -30,7 +31,7 @@ def compile_probe() -> Path:
 def main() -> int:
     exe = compile_probe()
     print(f"built {exe}", flush=True)
-    return subprocess.run([str(exe)]).returncode
+    return subprocess.run([str(exe), *sys.argv[1:]]).returncode
 
 
 if __name__ == "__main__":
