@@ -31,11 +31,12 @@
 #include "sweep.cuh"
 
 // Phase stamps: a measurement build (hsn_amd/probes/evmap_phases.hip) defines HSN_EVMAP_STAMPS
-// and these hooks, which record the real-time counter at the kernels' phase edges; in the
-// library they compile to nothing.
+// and these hooks, which record the real-time counter at the kernels' phase edges (and a value
+// that tells the wavefronts apart, HSN_EVMAP_NOTE); in the library they compile to nothing.
 #ifndef HSN_EVMAP_STAMPS
 #define HSN_EVMAP_STAMPS_BEGIN()
 #define HSN_EVMAP_STAMP(i)
+#define HSN_EVMAP_NOTE(i, v)
 #define HSN_EVMAP_STAMPS_END(which)
 #endif
 
@@ -407,6 +408,7 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
         }
     };
     const bool wave_rs = ballot(rmask != 0u) != 0u;
+    if constexpr (!Route::kOn) HSN_EVMAP_NOTE(9, wave_rs ? 1u : 0u);
     if (wave_rs) compose(std::true_type{});
     else compose(std::false_type{});
     __syncthreads();
@@ -523,26 +525,22 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     bool qr[2], qxr[2], hr[2];
 
     // positions 8 H .. 8 H + 7: the steps, then each position's row maximum and summaries
-    auto eight = [&](auto rs_c, auto h_c) __attribute__((always_inline)) {
-        constexpr bool kRs = decltype(rs_c)::value;
+    auto eight = [&](auto h_c) __attribute__((always_inline)) {
         constexpr int H = decltype(h_c)::value;
         float2 dl[8];
         uint32_t lmv[8];
-        // the next position's read goes out right after this position's write, ahead of the
-        // row-maximum bookkeeping (its entry may be the one just written: LDS keeps one wave's
-        // accesses in order); at a reset the entries are zeroed after that read, so the value is
-        // taken as zero
+        // the next position's read goes out after this position's write and its row-maximum
+        // reads (its entry may be the one just written: LDS keeps one wave's accesses in order);
+        // at a reset the entries are zeroed after that read, so the value is taken as zero
         float2 h = al_at(rent(8 * H));
         float2 bc = lds_ref<float2>(lds, bc_base + uint32_t(8 * H) * 256u);
 #pragma unroll
         for (int ii = 0; ii < 8; ++ii) {
             const int i = 8 * H + ii;
-            if (kRs) {
-                if ((rmask >> i) & 1u) {  // every value of the chunk restarts at zero
-                    zero_entries(kEnt - 1, false);  // the entries and cell 0's start value
-                    for (int e = hl; e < kEnt; e += 32) lds_ref<uint32_t>(lds, cmx_base + 4u * e) = 0u;
-                    h = make_float2(0.0f, 0.0f);
-                }
+            if ((rmask >> i) & 1u) {  // every value of the chunk restarts at zero
+                zero_entries(kEnt - 1, false);  // the entries and cell 0's start value
+                for (int e = hl; e < kEnt; e += 32) lds_ref<uint32_t>(lds, cmx_base + 4u * e) = 0u;
+                h = make_float2(0.0f, 0.0f);
             }
             const uint32_t e = ent(i);
             const float2 hn = make_float2(omb[i].x * h.x + bc.x, omb[i].y * h.y + bc.y);
@@ -554,10 +552,12 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
                 hs = make_float2(sel_f32(pm, c0.x, hn.x), sel_f32(pm, c0.y, hn.y));
             }
             const float2 hcur = h;
-            if (ii + 1 < 8) {
-                h = al_at(rent(i + 1));
-                bc = lds_ref<float2>(lds, bc_base + uint32_t(i + 1) * 256u);
-            }
+            auto read_ahead = [&]() __attribute__((always_inline)) {
+                if (ii + 1 < 8) {
+                    h = al_at(rent(i + 1));
+                    bc = lds_ref<float2>(lds, bc_base + uint32_t(i + 1) * 256u);
+                }
+            };
             // past the chunk (P < 16): out of range, not the next chunk's rows
             const uint32_t vo = i < n ? vrow_c + uint32_t(i) * pos_bytes : kOob;
             st2(hcur, rho, vo);
@@ -570,6 +570,10 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
             const uint32_t m1 = lds_ref<uint32_t>(lds, cmx_base + 4u * (hl + 32));
             const uint32_t m2 = lds_ref<uint32_t>(lds, cmx_base + 4u * (hl + 64));
             const uint32_t m3 = lds_ref<uint32_t>(lds, cmx_base + 4u * (hl + 96));
+            // each position starts with the reset's branch, past which the compiler cannot move
+            // this position's reductions: the read-ahead goes out after the maxima's reads, so
+            // that taking them waits for these reads only
+            read_ahead();
             lmv[ii] = umax(umax(m0, m1), umax(m2, m3));
         }
         const int pos = 8 * H + g;
@@ -650,13 +654,11 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
             hr[H] = __shfl(rs ? 1 : 0, src, kWave) != 0;
         }
     };
-    if (wave_rs) {
-        eight(std::true_type{}, std::integral_constant<int, 0>{});
-        eight(std::true_type{}, std::integral_constant<int, 1>{});
-    } else {
-        eight(std::false_type{}, std::integral_constant<int, 0>{});
-        eight(std::false_type{}, std::integral_constant<int, 1>{});
-    }
+    // one code path for every wavefront, with or without a reset in its chunks: a separate path
+    // for the few wavefronts with resets ran from a cold instruction cache and ended their
+    // workgroups about 1.5 us after the others
+    eight(std::integral_constant<int, 0>{});
+    eight(std::integral_constant<int, 1>{});
 
     HSN_EVMAP_STAMP(5);
     // the chunks' maps (half 0, then half 1), scanned across the chunks from q0, give each chunk
@@ -1013,7 +1015,8 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
     // One code path for chunks with and without resets: the replay's loads issued here stay in
     // flight through the barrier below, where two paths would join with different loads pending
     // and the join would wait for all of them.
-    const bool wave_rs = ballot(rmask != 0u) != 0u;  // a reset in the wave's chunks (the replay)
+    [[maybe_unused]] const bool wave_rs = ballot(rmask != 0u) != 0u;  // a reset in the wave's chunks
+    HSN_EVMAP_NOTE(9, wave_rs ? 1u : 0u);
     float2 omb[kP], dsv[kP];
     {
         float ainit = 1.0f;
@@ -1114,23 +1117,27 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
     const rsrc_t rdg = make_rsrc(a.dg + orow, row_bytes);
     uint32_t vrow_c = vrow;
     asm volatile("" : "+v"(vrow_c));  // recomputed here, not held from phase A's loads
-    auto replay = [&](auto rs_c) __attribute__((always_inline)) {
-        constexpr bool kRs = decltype(rs_c)::value;
-        // the next position's read goes out right after this position's write (its entry may be
-        // the one just written: LDS keeps one wave's accesses in order); a reset zeroes the
-        // entries after that read, so the value is taken as zero
+    // One code path for every wavefront, as in the forward's replay. The next position's entry,
+    // selection cotangent and share are read right after this position's write (its entry may
+    // be the one just written: LDS keeps one wave's accesses in order); a reset zeroes the entries
+    // after that read, so the value is taken as zero.
+    {
         float2 A = mu_at(ent(kP - 1));
+        float2 ds = lds_ref<float2>(lds, ds_base + uint32_t(kP - 1) * 256u);
+        float2 sh = share_at(kP - 1);
 #pragma unroll
         for (int i = kP - 1; i >= 0; --i) {
             const uint32_t e = ent(i);
-            const float2 ds = lds_ref<float2>(lds, ds_base + uint32_t(i) * 256u);
-            const float2 sh = share_at(i);
             const float2 o = omb[i];
             const float2 carried = make_float2(A.x + ds.x, A.y + ds.y);
             const float2 G = make_float2(carried.x + sh.x, carried.y + sh.y);
             const float bgx = 1.0f - o.x, bgy = 1.0f - o.y;
             mu_at(e) = make_float2(o.x * carried.x - bgx * sh.x, o.y * carried.y - bgy * sh.y);
-            if (i > 0) A = mu_at(ent(i - 1));
+            if (i > 0) {
+                A = mu_at(ent(i - 1));
+                ds = lds_ref<float2>(lds, ds_base + uint32_t(i - 1) * 256u);
+                sh = share_at(i - 1);
+            }
             const float cx = fast_tanh(yv[i].x), cy = fast_tanh(yv[i].y);
             const uint32_t vm = o.x == -1.0f ? 0u : ~0u;  // -1 marks an idle or padded slot
             const float dcx = and_f32(bgx * (1.0f - cx * cx) * G.x, vm);
@@ -1140,14 +1147,12 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
             const uint32_t vo = i < n ? vrow_c + uint32_t(i) * pos_bytes : kOob;
             st2(make_float2(dcx, dcy), rdy, vo);
             st2(make_float2(dbx, dby), rdg, vo);
-            if (kRs && ((rmask >> i) & 1u)) {  // every cotangent restarts at 0
+            if ((rmask >> i) & 1u) {  // every cotangent restarts at 0
                 zero_from(0, false);
                 A = make_float2(0.0f, 0.0f);
             }
         }
-    };
-    if (wave_rs) replay(std::true_type{});
-    else replay(std::false_type{});
+    }
     HSN_EVMAP_STAMP(6);
     HSN_EVMAP_STAMPS_END(1);
 }
