@@ -538,8 +538,18 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
         for (int ii = 0; ii < 8; ++ii) {
             const int i = 8 * H + ii;
             if ((rmask >> i) & 1u) {  // every value of the chunk restarts at zero
-                zero_entries(kEnt - 1, false);  // the entries and cell 0's start value
-                for (int e = hl; e < kEnt; e += 32) lds_ref<uint32_t>(lds, cmx_base + 4u * e) = 0u;
+                // the entries, cell 0's start value and their maxima, in straight-line writes
+                // (as a loop, the writes measured 0.4 us more on the wavefronts with a reset)
+#pragma unroll
+                for (int q = 0; q < ((kEnt - 1) * 4 + 31) / 32; ++q) {
+                    const int ee = hl + 32 * q;
+                    if (ee < (kEnt - 1) * 4)
+                        lds_ref<float2>(lds, cbase + uint32_t(ee >> 2) * kEntBytes + uint32_t(ee & 3) * 8u) =
+                            make_float2(0.0f, 0.0f);
+                }
+#pragma unroll
+                for (int q = 0; q < (kEnt + 31) / 32; ++q)
+                    if (hl + 32 * q < kEnt) lds_ref<uint32_t>(lds, cmx_base + 4u * uint32_t(hl + 32 * q)) = 0u;
                 h = make_float2(0.0f, 0.0f);
             }
             const uint32_t e = ent(i);
@@ -1147,8 +1157,13 @@ __global__ __launch_bounds__(kWave* kWaves) void bwd(BwdEv a) {
             const uint32_t vo = i < n ? vrow_c + uint32_t(i) * pos_bytes : kOob;
             st2(make_float2(dcx, dcy), rdy, vo);
             st2(make_float2(dbx, dby), rdg, vo);
-            if ((rmask >> i) & 1u) {  // every cotangent restarts at 0
-                zero_from(0, false);
+            if ((rmask >> i) & 1u) {  // every cotangent restarts at 0 (straight-line writes)
+#pragma unroll
+                for (int q = 0; q < kEv * 4 / 32; ++q) {
+                    const int ee = hl + 32 * q;
+                    lds_ref<float2>(lds, cbase + uint32_t(ee >> 2) * kEntBytes + uint32_t(ee & 3) * 8u) =
+                        make_float2(0.0f, 0.0f);
+                }
                 A = make_float2(0.0f, 0.0f);
             }
         }
