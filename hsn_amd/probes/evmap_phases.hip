@@ -18,6 +18,7 @@ __device__ unsigned long long* g_evmap_stamps[2];  // [workgroup][wavefront][10]
     unsigned long long stamp_[10] = {}; \
     stamp_[0] = __builtin_amdgcn_s_memrealtime()
 #define HSN_EVMAP_STAMP(i) stamp_[i] = __builtin_amdgcn_s_memrealtime()
+#define HSN_EVMAP_NOTE(i, v) stamp_[i] = (v)
 #define HSN_EVMAP_STAMPS_END(which)                                                               \
     do {                                                                                          \
         stamp_[7] = __builtin_amdgcn_s_memrealtime();                                             \
@@ -53,9 +54,10 @@ void hsn::clear_last_error() {}
 namespace {
 
 // `edges`: the stamps in the order the kernel reaches them (0..6 at the phase edges, 7 the last
-// store issued, 8 every store done, 9 the routed forward's decisions made)
+// store issued, 8 every store done, 9 the routed forward's decisions made); in the forward and
+// the backward word 9 notes whether the wavefront's chunks hold a reset (`split_by_note`)
 void report(const char* what, const std::vector<unsigned long long>& h, const char* const* names,
-            const std::vector<int>& edges) {
+            const std::vector<int>& edges, bool split_by_note = false) {
     const int kEdges = int(edges.size());
     unsigned long long t0 = ~0ull;
     for (size_t i = 0; i < h.size(); i += 10) t0 = std::min(t0, h[i]);
@@ -78,6 +80,18 @@ void report(const char* what, const std::vector<unsigned long long>& h, const ch
         std::sort(d.begin(), d.end());
         std::printf("    %-26s p10 %5.2f  p50 %5.2f  p90 %5.2f  max %5.2f\n", names[p], d[d.size() / 10],
                     d[d.size() / 2], d[d.size() * 9 / 10], d.back());
+    }
+    if (split_by_note) {  // the wavefronts whose chunks hold a reset against the others
+        std::printf("  span of each phase, wavefronts with a reset in their chunks | without (p50 / max us):\n");
+        for (int p = 1; p < kEdges; ++p) {
+            std::vector<double> d[2];
+            for (size_t i = 0; i < h.size(); i += 10)
+                d[h[i + 9] != 0 ? 0 : 1].push_back(double(h[i + edges[p]] - h[i + edges[p - 1]]) * 0.01);
+            for (auto& v : d) std::sort(v.begin(), v.end());
+            if (d[0].empty() || d[1].empty()) break;
+            std::printf("    %-26s %5.2f / %5.2f | %5.2f / %5.2f   (%zu | %zu)\n", names[p], d[0][d[0].size() / 2],
+                        d[0].back(), d[1][d[1].size() / 2], d[1].back(), d[0].size(), d[1].size());
+        }
     }
     const size_t nwg = h.size() / 80;
     std::vector<double> end(nwg, 0.0);
@@ -197,13 +211,13 @@ int main(int argc, char** argv) {
                                 "replay done", "summary scanned and stored",
                                 "last store issued", "every store done"};
     const std::vector<int> in_order = {0, 1, 2, 3, 4, 5, 6, 7, 8};
-    report("forward", h, fwd_names, in_order);
+    report("forward", h, fwd_names, in_order, true);
     CK(hipMemcpy(h.data(), st_b, words * 8, hipMemcpyDeviceToHost));
     const char* bwd_names[9] = {"start", "first loads issued", "summary maps, tables built",
                                 "shares written, compose starts", "phase A barrier passed",
                                 "phase B (walk) barrier passed", "replay done",
                                 "last store issued", "every store done"};
-    report("backward", h, bwd_names, in_order);
+    report("backward", h, bwd_names, in_order, true);
 
     // the forward that routes its own window (hsn_win_route_forward's one launch): logits N(0, 1)
     std::vector<float> logits(size_t(B) * T * N);
