@@ -283,11 +283,15 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     for (int i = 0; i < kAhead; ++i) fetch(i);
 
     // this chunk's columns of the tables while the loads are in flight (no other half-wave
-    // reads them before phase B): no event (0xff; kDummy in row N) in the first-event table and
-    // in the last-event table, zero maxima, the dummy entry's identity map (1, 0) that idle slots
-    // compose, and the chunk's untouched maximum (phase B max-reduces into it)
+    // reads them before phase B): no event (0xff; kDummy in row N; cell 0 kConst, below) in the
+    // first-event table and in the last-event table, zero maxima, the dummy entry's identity map
+    // (1, 0) that idle slots compose, and the chunk's untouched maximum (phase B max-reduces
+    // into it). Cell 0 without an event in the chunk keeps kConst, an entry with the identity map:
+    // phase B then stores cell 0's start value there as for any touched cell (padded slots read
+    // it), with no write of its own (that one branch a chunk measured 0.7 us of the walk).
     unsigned char* const idx = lds + Lo.idx;
-    for (int c = hl; c <= N; c += 32) idx[c * kChunks + ch] = c < N ? 0xffu : uint8_t(kDummy);
+    for (int c = hl; c <= N; c += 32)
+        idx[c * kChunks + ch] = c == 0 ? uint8_t(kConst) : c < N ? 0xffu : uint8_t(kDummy);
     if (track_age)
         for (int c = hl; c < N; c += 32) lds[Lo.lastev + uint32_t(c * kChunks + ch)] = 0xffu;
     const uint32_t cmx_base = Lo.cmx + uint32_t(ch) * kEnt * 4u;
@@ -296,6 +300,9 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
     if (hl < kS) {
         lds_ref<float>(lds, cbase + kDummy * kEntBytes + 4u * hl) = 1.0f;
         lds_ref<float>(lds, cbase + kEnt * kEntBytes + kDummy * kEntBytes + 4u * hl) = 0.0f;
+    } else if (hl < 2 * kS) {
+        lds_ref<float>(lds, cbase + kConst * kEntBytes + 4u * (hl - kS)) = 1.0f;
+        lds_ref<float>(lds, cbase + kEnt * kEntBytes + kConst * kEntBytes + 4u * (hl - kS)) = 0.0f;
     }
     if (hl == 0) lds_ref<uint32_t>(lds, Lo.umax + 4u * ch) = 0u;
 
@@ -455,14 +462,13 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
                     uint32_t m = umax(umax(abs_bits(s.x), abs_bits(s.y)), umax(abs_bits(s.z), abs_bits(s.w)));
                     m = ok ? umax(m, dpp_u32<dpp::kXor1>(m)) : 0u;  // the cell's 8 columns
                     const uint32_t jb = Lo.maps + uint32_t(j) * kMapBytes;
-                    // the entry's start value for the replay and its maximum; cell 0's start value
-                    // (padded slots read it where the chunk leaves cell 0 untouched)
+                    // the entry's start value for the replay and its maximum (kConst: cell 0 where
+                    // the chunk leaves it untouched, which still counts among the untouched)
                     if (touched) {
                         lds_ref<float4>(lds, jb + ej * kEntBytes + qofs) = s;
                         if (bq == 0) lds_ref<uint32_t>(lds, Lo.cmx + 4u * (j * kEnt + ej)) = m;
                     }
-                    if (cell == 0) lds_ref<float4>(lds, jb + kConst * kEntBytes + qofs) = s;
-                    um[j] = umax(um[j], touched ? 0u : m);
+                    um[j] = umax(um[j], touched && ej != uint32_t(kConst) ? 0u : m);
                     // a chunk with a reset ends at beta whatever the start (not 0 * s: a NaN in
                     // the start state must not cross the reset, as masked_fill); an untouched
                     // cell's map is the dummy entry's identity (1, 0)

@@ -85,22 +85,22 @@ constexpr int kRouteWaves = evmap::kWaves;
 constexpr int kRouteJ = 4;  // consecutive positions a wavefront decides, at most
 constexpr int kRouteShare = kRouteWaves * kRouteJ;
 // the row's int16 decisions (T K <= 256 * 8) and a workgroup's row-maximum accumulators fit in a
-// chunk's maps below its dummy entry
-static_assert(kBoxPositions * evmap::kK * 2 <= evmap::kDummy * evmap::kEntBytes, "slot table");
-static_assert(kBoxPositions * 4 <= evmap::kDummy * evmap::kEntBytes, "row maxima");
+// chunk's maps below cell 0's entry (kConst) and the dummy entry, which hold identity maps
+static_assert(kBoxPositions * evmap::kK * 2 <= evmap::kConst * evmap::kEntBytes, "slot table");
+static_assert(kBoxPositions * 4 <= evmap::kConst * evmap::kEntBytes, "row maxima");
 
 // The decisions of a wavefront's positions by decide_grouped (LP lanes a position, CPL cells a
 // lane; a position with more candidates than lanes by decide_select, NPLF cells a lane), its
 // scratch in its first chunk's maps: the scores, lists and order words below the alpha table's
-// dummy entry, the slot tables in the beta table.
+// cell-0 and dummy entries, the slot tables in the beta table.
 template <int LP, int CPL, int NPLF>
 struct WindowRoute {
     static constexpr bool kOn = true;
     static constexpr int G = kWave / LP;
     static constexpr int kCalls = kRouteJ / G;
     static constexpr uint32_t kTabAt = evmap::kEnt * evmap::kEntBytes;
-    static_assert(CPL * kWave * 4 + kWave * 16 + G * (LP + 4) * 8 <= evmap::kDummy * evmap::kEntBytes,
-                  "scores, lists and order words below the dummy entry");
+    static_assert(CPL * kWave * 4 + kWave * 16 + G * (LP + 4) * 8 <= evmap::kConst * evmap::kEntBytes,
+                  "scores, lists and order words below cell 0's and the dummy entries");
     static_assert(kTabAt + kWave * 16 <= (evmap::kEnt + evmap::kDummy) * evmap::kEntBytes, "slot tables");
     static_assert(G * (LP + 4) * 8 >= (kWave + 4) * 8, "decide_select's order words");
     const RouteArgs& ra;
