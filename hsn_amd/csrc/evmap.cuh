@@ -459,14 +459,16 @@ __device__ __forceinline__ void fwd_body(const FwdEv& a, Route& route) {
                     const int j = jh + jj;
                     const uint32_t ej = (words[j / 4] >> (8 * (j % 4))) & 0xffu;
                     const bool touched = ej != kNone;
+                    // the thread's 4 columns (the cell's other half comes in through the atomic
+                    // maximum below, and through the reduction of the untouched maxima)
                     uint32_t m = umax(umax(abs_bits(s.x), abs_bits(s.y)), umax(abs_bits(s.z), abs_bits(s.w)));
-                    m = ok ? umax(m, dpp_u32<dpp::kXor1>(m)) : 0u;  // the cell's 8 columns
+                    m = ok ? m : 0u;
                     const uint32_t jb = Lo.maps + uint32_t(j) * kMapBytes;
                     // the entry's start value for the replay and its maximum (kConst: cell 0 where
                     // the chunk leaves it untouched, which still counts among the untouched)
                     if (touched) {
                         lds_ref<float4>(lds, jb + ej * kEntBytes + qofs) = s;
-                        if (bq == 0) lds_ref<uint32_t>(lds, Lo.cmx + 4u * (j * kEnt + ej)) = m;
+                        atomicMax(&lds_ref<uint32_t>(lds, Lo.cmx + 4u * (j * kEnt + ej)), m);
                     }
                     um[j] = umax(um[j], touched && ej != uint32_t(kConst) ? 0u : m);
                     // a chunk with a reset ends at beta whatever the start (not 0 * s: a NaN in
