@@ -110,6 +110,52 @@ def build(verbose: bool = False, incremental: bool = False) -> Path:
     return LIBRARY
 
 
+#: The host helper module (``hsn_amd/host/tables.cpp``): the trainer's pointer tables, built with
+#: the host compiler against the installed PyTorch's headers and libraries.
+HOST_SOURCE = PKG / "host" / "tables.cpp"
+HOST_MODULE = PKG / "_tables.so"
+HOST_MANIFEST = PKG / "_tables.json"
+
+
+def build_host(verbose: bool = False) -> Path:
+    """Compile ``hsn_amd/_tables.so`` (CPython extension, host code only); returns its path."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_lib = str(Path(torch.__file__).resolve().parent / "lib")
+    tmp = HOST_MODULE.with_suffix(".so.tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           *[f"-isystem{p}" for p in cpp_extension.include_paths()],
+           f"-isystem{sysconfig.get_paths()['include']}",
+           str(HOST_SOURCE), "-o", str(tmp),
+           f"-L{torch_lib}", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+           f"-Wl,-rpath,{torch_lib}"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"host helper build failed:\n{proc.stderr[-6000:]}")
+    os.replace(tmp, HOST_MODULE)
+    HOST_MANIFEST.write_text(json.dumps({"source_sha256": _sha(HOST_SOURCE),
+                                         "module_sha256": _sha(HOST_MODULE)}, indent=1) + "\n")
+    if verbose:
+        print(f"built {HOST_MODULE} ({HOST_MODULE.stat().st_size} bytes)")
+    return HOST_MODULE
+
+
+def host_stale() -> str | None:
+    """Why ``hsn_amd/_tables.so`` is not the build of the current source, or None."""
+    if not HOST_MODULE.is_file() or not HOST_MANIFEST.is_file():
+        return "hsn_amd/_tables.so is not built"
+    manifest = json.loads(HOST_MANIFEST.read_text())
+    if manifest.get("module_sha256") != _sha(HOST_MODULE):
+        return "hsn_amd/_tables.so differs from its build manifest"
+    if manifest.get("source_sha256") != _sha(HOST_SOURCE):
+        return "hsn_amd/host/tables.cpp changed since hsn_amd/_tables.so was built"
+    return None
+
+
 def stale() -> str | None:
     """Why the built library does not match the sources (None: it matches)."""
     if not LIBRARY.is_file() or not MANIFEST.is_file():
@@ -129,4 +175,5 @@ def stale() -> str | None:
 
 if __name__ == "__main__":
     build(verbose=True, incremental="--incremental" in sys.argv[1:])
+    build_host(verbose=True)
     sys.exit(0)

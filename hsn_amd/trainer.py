@@ -21,6 +21,13 @@ import torch
 from torch import Tensor
 
 from . import _lib
+from . import build as _build
+
+# The pointer tables in one native call (hsn_amd/host/tables.cpp) when that module is built from
+# the current source; otherwise the same checks and tables are made here, tensor by tensor.
+_native = None
+if _build.host_stale() is None:
+    from . import _tables as _native
 
 __all__ = [
     "MAX_UNITS",
@@ -64,6 +71,7 @@ def ready(device: torch.device) -> bool:
 
 
 def _fits(rows: Sequence[Sequence[Tensor]]) -> bool:
+    """Whether the rows fit a pass, checked tensor by tensor (the native tables' checks)."""
     first = rows[0]
     if not first or any(len(row) != len(first) for row in rows):
         return False
@@ -86,6 +94,25 @@ def _numels(row: Sequence[Tensor]):
     return (ctypes.c_int64 * len(row))(*[t.numel() for t in row])
 
 
+def _tables(rows: Sequence[Sequence[Tensor]]):
+    """``(pointer arrays, element counts)`` of R lists of n tensors as the C entry points take
+    them (one ``void*[n]`` a list, the first list's ``int64[n]``), or ``None`` when the lists do
+    not fit a pass: an empty list, lists of different lengths, a tensor that is not a contiguous
+    fp32 tensor on the first one's device, different counts at one index, or passes that do not
+    run on that device (:func:`ready`)."""
+    if _native is None:
+        if not _fits(rows):
+            return None
+        return [_pointers(r) for r in rows], _numels(rows[0])
+    buf = _native.list_table(rows)
+    if buf is None or not ready(rows[0][0].device):
+        return None
+    n, R = len(rows[0]), len(rows)
+    pointers = ctypes.c_void_p * n
+    return ([pointers.from_buffer(buf, 8 * n * r) for r in range(R)],
+            (ctypes.c_int64 * n).from_buffer(buf, 8 * n * R))
+
+
 def adamw(
     params: Sequence[Tensor],
     grads: Sequence[Tensor],
@@ -102,8 +129,8 @@ def adamw(
     """``LazyAdamW._dense_steps`` as one pass: the AdamW step of ordinary tensors at the step
     count ``step`` (already advanced); the coefficients from the same host arithmetic (reference
     ``python/hsn/kernels/trainer.py:111-144``)."""
-    rows = (params, grads, exp_avgs, exp_avg_sqs)
-    if not _fits(rows):
+    tables = _tables((params, grads, exp_avgs, exp_avg_sqs))
+    if tables is None:
         return False
     bias_correction1 = 1 - beta1**step
     bias_correction2 = 1 - beta2**step
@@ -119,8 +146,8 @@ def adamw(
         -step_size,
     )
     device = params[0].device
-    _lib.call("hsn_tr_adamw", *[_pointers(r) for r in rows], _numels(params), len(params),
-              int(weight_decay != 0), coefs, _lib.stream_of(device))
+    _lib.call("hsn_tr_adamw", *tables[0], tables[1], len(params), int(weight_decay != 0), coefs,
+              _lib.stream_of(device))
     return True
 
 
@@ -144,10 +171,10 @@ def adamw_units(
     """``LazyAdamW._unit_step`` as one pass for stacked unit tensors ``[n_units, ...]`` that
     share their per-unit coefficients (each a sequence of ``n_units`` values: the coefficient
     tensors of ``_unit_step``; reference ``trainer.py:147-191``)."""
-    rows = (params, grads, exp_avgs, exp_avg_sqs)
     if n_units > MAX_UNITS or n_units < 1 or any(p.dim() == 0 or p.shape[0] != n_units for p in params):
         return False
-    if not _fits(rows):
+    tables = _tables((params, grads, exp_avgs, exp_avg_sqs))
+    if tables is None:
         return False
     table = [[1.0 if flag else 0.0 for flag in active], decay, lerp_weight, beta2_factor,
              bias_correction2_sqrt, step_size]
@@ -155,41 +182,42 @@ def adamw_units(
         return False
     coefs = (ctypes.c_float * (6 * n_units))(*[float(v) for row in table for v in row])
     device = params[0].device
-    _lib.call("hsn_tr_adamw_units", *[_pointers(r) for r in rows], _numels(params), len(params),
-              n_units, int(weight_decay != 0), coefs, 1 - beta2, eps, _lib.stream_of(device))
+    _lib.call("hsn_tr_adamw_units", *tables[0], tables[1], len(params), n_units, int(weight_decay != 0), coefs, 1 - beta2, eps, _lib.stream_of(device))
     return True
 
 
 def lerp(selfs: Sequence[Tensor], ends: Sequence[Tensor], weight: float) -> bool:
     """Move every ``selfs[i]`` toward ``ends[i]`` by ``weight`` in place, one launch for the
     whole list; the same result as ``torch._foreach_lerp_``."""
-    if not _fits((selfs, ends)):
+    tables = _tables((selfs, ends))
+    if tables is None:
         return False
-    _lib.call("hsn_tr_lerp", _pointers(selfs), _pointers(ends), _numels(selfs), len(selfs),
-              float(weight), _lib.stream_of(selfs[0].device))
+    _lib.call("hsn_tr_lerp", *tables[0], tables[1], len(selfs), float(weight),
+              _lib.stream_of(selfs[0].device))
     return True
 
 
 def scale64(grads: Sequence[Tensor], coefficient: Tensor) -> bool:
     """``grad.copy_((grad.double() * coefficient).float())`` for every gradient as one pass;
     ``coefficient`` is a one-element float64 tensor on the gradients' device."""
-    if not _fits((grads,)):
+    tables = _tables((grads,))
+    if tables is None:
         return False
     if (coefficient.dtype != torch.float64 or coefficient.numel() != 1
             or coefficient.device != grads[0].device):
         return False
-    _lib.call("hsn_tr_scale64", _pointers(grads), _numels(grads), len(grads),
-              coefficient.data_ptr(), _lib.stream_of(grads[0].device))
+    _lib.call("hsn_tr_scale64", *tables[0], tables[1], len(grads), coefficient.data_ptr(),
+              _lib.stream_of(grads[0].device))
     return True
 
 
 def copy(dsts: Sequence[Tensor], srcs: Sequence[Tensor]) -> bool:
     """Overwrite each fp32 ``dsts[i]`` with ``srcs[i]``, one launch for the whole list (what
     ``torch._foreach_copy_`` does)."""
-    if not _fits((dsts, srcs)):
+    tables = _tables((dsts, srcs))
+    if tables is None:
         return False
-    _lib.call("hsn_tr_copy", _pointers(dsts), _pointers(srcs), _numels(dsts), len(dsts),
-              _lib.stream_of(dsts[0].device))
+    _lib.call("hsn_tr_copy", *tables[0], tables[1], len(dsts), _lib.stream_of(dsts[0].device))
     return True
 
 
@@ -202,11 +230,11 @@ def limit_squares(
     """Element-wise squares for the limiter's two norms, written into the given buffers:
     ``old_squares[i] = olds[i] ** 2`` (the norm of the previous weights) and
     ``delta_squares[i] = (params[i] - olds[i]) ** 2`` (the norm of the proposed step)."""
-    rows = (params, olds, old_squares, delta_squares)
-    if not _fits(rows):
+    tables = _tables((params, olds, old_squares, delta_squares))
+    if tables is None:
         return False
-    _lib.call("hsn_tr_limit_squares", *[_pointers(r) for r in rows], _numels(params),
-              len(params), _lib.stream_of(params[0].device))
+    _lib.call("hsn_tr_limit_squares", *tables[0], tables[1], len(params),
+              _lib.stream_of(params[0].device))
     return True
 
 
@@ -220,14 +248,15 @@ def limit_project(
     ``groups[j]`` is a two-element fp32 device tensor ``[scale, clipped]``; where ``clipped`` is
     set the step ``params[j] - olds[j]`` is multiplied by ``scale`` in place. Every tensor's
     final step squared goes to ``applied_squares[j]``."""
-    if len(groups) != len(params) or any(
-            g.dtype != torch.float32 or g.numel() != 2 or not g.is_contiguous() for g in groups):
+    if len(groups) != len(params):
         return False
-    if not _fits((params, olds, applied_squares)):
+    tables = _tables((params, olds, applied_squares))
+    if tables is None:
         return False
-    if any(g.device != params[0].device for g in groups):
+    # the groups: contiguous fp32 pairs on the same device
+    pairs = _tables((groups,))
+    if pairs is None or any(c != 2 for c in pairs[1]) or groups[0].device != params[0].device:
         return False
-    _lib.call("hsn_tr_limit_project", _pointers(params), _pointers(olds),
-              _pointers(applied_squares), _pointers(groups), _numels(params), len(params),
+    _lib.call("hsn_tr_limit_project", *tables[0], pairs[0][0], tables[1], len(params),
               _lib.stream_of(params[0].device))
     return True
