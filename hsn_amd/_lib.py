@@ -89,6 +89,18 @@ SIGNATURES: dict[str, list] = {
 _lock = threading.Lock()
 
 
+
+@lru_cache(maxsize=None)
+def host_tables():
+    """The host helper module ``hsn_amd._tables`` (the Python mirror's checks and pointer tables
+    in one native call) when it is built from the current source, else ``None``: the callers then
+    make the same checks and tables in Python."""
+    if _build.host_stale() is not None:
+        return None
+    from . import _tables
+
+    return _tables
+
 @lru_cache(maxsize=1)
 def library() -> ctypes.CDLL:
     """The loaded library (built in-tree and matching its sources), else ``RuntimeError``."""

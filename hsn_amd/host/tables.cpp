@@ -1,4 +1,5 @@
-// Pointer tables for the trainer's list passes (hsn_amd/trainer.py), built in one call.
+// Pointer tables for the library's Python mirror, built in one call: the trainer's list passes
+// (hsn_amd/trainer.py) and the fused cell round's operands (hsn_amd/kernels/window.py).
 //
 // Each pass takes R lists of n tensors and hands the C entry points of include/hsn_trainer.h one
 // array of n device pointers a list and the n element counts. Before that, every tensor must be a
@@ -14,8 +15,15 @@
 // device or a column's element counts differ; otherwise R * n pointers (list after list), then
 // the first list's n element counts, as 8-byte native integers. Anything that is not a sequence
 // of sequences of tensors raises TypeError.
+//   tensor_table(tensors, dtypes, shapes, device) -> bytearray | int
+// tensors: a sequence of n tensors; dtypes and shapes: sequences of n torch dtypes and n tuples
+// of ints; device: the device index every tensor must be on (-1: the CPU). Returns the index of
+// the first tensor that is not contiguous, or whose dtype, shape or device differ from the given
+// ones (the caller then names the mismatch), else the n data pointers as 8-byte integers. The
+// cell round makes these checks of its twenty operands at every call.
 #include <Python.h>
 
+#include <torch/csrc/Dtype.h>
 #include <torch/csrc/autograd/python_variable.h>
 
 #include <cstdint>
@@ -79,15 +87,72 @@ PyObject* list_table(PyObject*, PyObject* rows) {
     }
 }
 
+PyObject* tensor_table(PyObject*, PyObject* args) {
+    PyObject *tensors, *dtypes, *shapes;
+    long long device;
+    if (!PyArg_ParseTuple(args, "OOOL", &tensors, &dtypes, &shapes, &device)) return nullptr;
+    try {
+        Fast ts, ds, ss;
+        ts.seq = PySequence_Fast(tensors, "tensor_table: tensors must be a sequence");
+        if (!ts.seq) return nullptr;
+        ds.seq = PySequence_Fast(dtypes, "tensor_table: dtypes must be a sequence");
+        if (!ds.seq) return nullptr;
+        ss.seq = PySequence_Fast(shapes, "tensor_table: shapes must be a sequence");
+        if (!ss.seq) return nullptr;
+        const Py_ssize_t n = PySequence_Fast_GET_SIZE(ts.seq);
+        if (PySequence_Fast_GET_SIZE(ds.seq) != n || PySequence_Fast_GET_SIZE(ss.seq) != n) {
+            PyErr_SetString(PyExc_ValueError, "tensor_table: as many dtypes and shapes as tensors");
+            return nullptr;
+        }
+        std::vector<int64_t> table(static_cast<size_t>(n));
+        for (Py_ssize_t i = 0; i < n; ++i) {
+            PyObject* item = PySequence_Fast_GET_ITEM(ts.seq, i);
+            PyObject* dt = PySequence_Fast_GET_ITEM(ds.seq, i);
+            if (!THPVariable_Check(item) || !THPDtype_Check(dt)) {
+                PyErr_SetString(PyExc_TypeError, "tensor_table: tensors and torch dtypes expected");
+                return nullptr;
+            }
+            const at::Tensor& t = THPVariable_Unpack(item);
+            bool ok = t.scalar_type() == reinterpret_cast<THPDtype*>(dt)->scalar_type &&
+                      t.has_storage() && t.is_contiguous() &&
+                      (t.is_cuda() ? static_cast<long long>(t.get_device()) : -1LL) == device;
+            if (ok) {
+                Fast shape;
+                shape.seq = PySequence_Fast(PySequence_Fast_GET_ITEM(ss.seq, i),
+                                            "tensor_table: every shape must be a sequence of ints");
+                if (!shape.seq) return nullptr;
+                const Py_ssize_t dims = PySequence_Fast_GET_SIZE(shape.seq);
+                ok = dims == t.dim();
+                for (Py_ssize_t k = 0; ok && k < dims; ++k) {
+                    const long long v = PyLong_AsLongLong(PySequence_Fast_GET_ITEM(shape.seq, k));
+                    if (v == -1 && PyErr_Occurred()) return nullptr;
+                    ok = v == t.size(k);
+                }
+            }
+            if (!ok) return PyLong_FromSsize_t(i);
+            table[i] = static_cast<int64_t>(reinterpret_cast<uintptr_t>(t.data_ptr()));
+        }
+        return PyByteArray_FromStringAndSize(reinterpret_cast<const char*>(table.data()),
+                                             static_cast<Py_ssize_t>(table.size() * sizeof(int64_t)));
+    } catch (const std::exception& e) {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        return nullptr;
+    }
+}
+
 PyMethodDef kMethods[] = {
     {"list_table", list_table, METH_O,
      "list_table(rows) -> bytearray | None: the pointer tables and element counts of R lists of n "
      "contiguous fp32 tensors on one device (R * n pointers, then n counts, 8-byte integers)"},
+    {"tensor_table", tensor_table, METH_VARARGS,
+     "tensor_table(tensors, dtypes, shapes, device) -> bytearray | int: the data pointers of "
+     "contiguous tensors of the given dtypes and shapes on one device, or the first mismatch's "
+     "index"},
     {nullptr, nullptr, 0, nullptr},
 };
 
 PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_tables",
-                       "Pointer tables for the trainer's list passes (host code only).", -1,
+                       "Pointer tables for the library's Python mirror (host code only).", -1,
                        kMethods};
 
 }  // namespace

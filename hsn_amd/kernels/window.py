@@ -430,6 +430,11 @@ def _round_struct(B, N, d, K, M, H, D, cand_norm, norm_eps, cand_eps, **pointers
 
 
 _round_work: dict[tuple, int] = {}  # scratch bytes by (B, K, d, H): host arithmetic only
+#: The operands' dtypes and shapes by (B, N, d, K, M, H, D), in the struct's pointer order.
+_round_specs: dict[tuple, tuple] = {}
+#: Byte offset of the struct's first pointer field; the operands' pointers are the next twenty.
+_ROUND_FIRST = _Round.u.offset
+_ROUND_OPERANDS = _ROUND_POINTERS[:20]
 
 
 def _round_unsupported(B, N, d, K, M, H, D, cand_norm) -> Optional[str]:
@@ -494,16 +499,25 @@ def cell_round_op(u: Tensor, eps: Tensor, h: Tensor, q: Tensor, age: Tensor, cel
     dev = h.device
     index = h.get_device()
     f32, i64 = torch.float32, torch.int64
-    for name, t, dtype, shape in (
-            ("u", u, f32, (B, d)), ("eps", eps, f32, (B, d)), ("h", h, f32, (B, N, d)),
-            ("q", q, f32, (B, d)), ("age", age, i64, (B, N)), ("cells", cells, i64, (B, K)),
-            ("units", units, i64, (B, K)), ("valid", valid, torch.bool, (B, K)),
-            ("alpha", alpha, f32, (B, K)), ("V", V, f32, (d, d)), ("edge_w", edge_w, f32, (N, D)),
-            ("pad_src", pad_src, i64, (N, D)), ("norm_w", norm_w, f32, (4 * d,)),
-            ("gate_w", gate_w, f32, (d, 4 * d)), ("gate_b", gate_b, f32, (d,)),
-            ("W1", W1, f32, (M, 4 * d, H)), ("b1", b1, f32, (M, H)), ("W2", W2, f32, (M, H, d)),
-            ("b2", b2, f32, (M, d)), ("W_out", W_out, f32, (d, d))):
-        _need(name, t, dtype, shape, index)
+    operands = (u, eps, h, q, age, cells, units, valid, alpha, V, edge_w, pad_src, norm_w, gate_w,
+                gate_b, W1, b1, W2, b2, W_out)
+    skey = (B, N, d, K, M, H, D)
+    specs = _round_specs.get(skey)
+    if specs is None:
+        shapes = ((B, d), (B, d), (B, N, d), (B, d), (B, N), (B, K), (B, K), (B, K), (B, K), (d, d),
+                  (N, D), (N, D), (4 * d,), (d, 4 * d), (d,), (M, 4 * d, H), (M, H), (M, H, d),
+                  (M, d), (d, d))
+        dtypes = (f32, f32, f32, f32, i64, i64, i64, torch.bool, f32, f32, f32, i64, f32, f32, f32,
+                  f32, f32, f32, f32, f32)
+        specs = _round_specs[skey] = (dtypes, shapes)
+    # the checks and the pointers in one native call where the host helper is built; a mismatch
+    # (or no helper) takes the checks one by one, which name it
+    native = _lib.host_tables()
+    table = native.tensor_table(operands, specs[0], specs[1], index) if native is not None else None
+    if not isinstance(table, bytearray):
+        for name, t, dtype, shape in zip(_ROUND_OPERANDS, operands, *specs):
+            _need(name, t, dtype, shape, index)
+        table = bytearray((ctypes.c_int64 * 20)(*[t.data_ptr() for t in operands]))
     if cand_norm:  # otherwise unused (the reference passes the cell norm's gain in its place)
         _need("cand_w", cand_w, f32, (d,), index)
     h_new = torch.empty_like(h)
@@ -518,14 +532,17 @@ def cell_round_op(u: Tensor, eps: Tensor, h: Tensor, q: Tensor, age: Tensor, cel
         call("hsn_win_cell_round_workspace", ctypes.byref(probe), ctypes.byref(out))
         nbytes = _round_work[key] = int(out.value)
     work = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    s = _Round(B, N, d, K, M, H, D, int(bool(cand_norm)), float(norm_eps), float(cand_eps),
-               u.data_ptr(), eps.data_ptr(), h.data_ptr(), q.data_ptr(), age.data_ptr(),
-               cells.data_ptr(), units.data_ptr(), valid.data_ptr(), alpha.data_ptr(),
-               V.data_ptr(), edge_w.data_ptr() if D else None, pad_src.data_ptr() if D else None,
-               norm_w.data_ptr(), gate_w.data_ptr(), gate_b.data_ptr(), W1.data_ptr(),
-               b1.data_ptr(), W2.data_ptr(), b2.data_ptr(), W_out.data_ptr(),
-               cand_w.data_ptr() if cand_norm else None, work.data_ptr(), h_new.data_ptr(),
-               q_new.data_ptr(), age_new.data_ptr(), h_sel.data_ptr())
+    s = _Round(B, N, d, K, M, H, D, int(bool(cand_norm)), float(norm_eps), float(cand_eps))
+    ctypes.memmove(ctypes.addressof(s) + _ROUND_FIRST, bytes(table), 8 * 20)  # u .. W_out
+    if not D:  # no edges: no edge weights or sources
+        s.edge_w = None
+        s.pad_src = None
+    s.cand_w = cand_w.data_ptr() if cand_norm else None
+    s.work = work.data_ptr()
+    s.h_new = h_new.data_ptr()
+    s.q_new = q_new.data_ptr()
+    s.age_new = age_new.data_ptr()
+    s.h_sel = h_sel.data_ptr()
     call("hsn_win_cell_round", ctypes.byref(s), stream_of(dev))
     return h_new, q_new, age_new, h_sel
 

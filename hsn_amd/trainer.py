@@ -21,13 +21,10 @@ import torch
 from torch import Tensor
 
 from . import _lib
-from . import build as _build
 
 # The pointer tables in one native call (hsn_amd/host/tables.cpp) when that module is built from
 # the current source; otherwise the same checks and tables are made here, tensor by tensor.
-_native = None
-if _build.host_stale() is None:
-    from . import _tables as _native
+_native = _lib.host_tables()
 
 __all__ = [
     "MAX_UNITS",

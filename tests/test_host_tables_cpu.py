@@ -1,6 +1,8 @@
-"""The trainer's pointer tables on the CPU: the native module (``hsn_amd/_tables.so``, built from
-``hsn_amd/host/tables.cpp``) takes and declines exactly the lists the per-tensor checks do, and
-its tables hold each tensor's data pointer and element count. Host code only: no kernel runs."""
+"""The host helper's pointer tables on the CPU (``hsn_amd/_tables.so``, built from
+``hsn_amd/host/tables.cpp``): for the trainer's lists it takes and declines exactly the lists the
+per-tensor checks do, and its tables hold each tensor's data pointer and element count; for the
+cell round's operands it checks dtype, shape, layout and device and names the first mismatch.
+Host code only: no kernel runs."""
 
 from __future__ import annotations
 
@@ -104,3 +106,31 @@ def test_pass_tables_match_the_per_tensor_path(native, monkeypatch):
     assert [list(t) for t in with_native[0]] == [list(t) for t in without[0]]
     assert list(with_native[1]) == list(without[1])
     assert trainer._tables(([], [])) is None
+
+
+def test_operand_table_checks_dtype_shape_device_and_layout(native):
+    """``tensor_table`` (the cell round's twenty operands): the data pointers when every tensor
+    has its dtype and shape, is contiguous and on the device (-1: the CPU); else the index of the
+    first that does not."""
+    f32, i64 = torch.float32, torch.int64
+    ts = [torch.zeros(4, 3), torch.zeros(5, dtype=i64), torch.zeros(2, 0), torch.zeros((), dtype=f32),
+          torch.zeros(6, dtype=torch.bool)]
+    dtypes = [f32, i64, f32, f32, torch.bool]
+    shapes = [(4, 3), (5,), (2, 0), (), (6,)]
+    buf = native.tensor_table(ts, dtypes, shapes, -1)
+    assert isinstance(buf, bytearray)
+    got = list((ctypes.c_int64 * len(ts)).from_buffer(buf))
+    assert [v & 0xFFFFFFFFFFFFFFFF for v in got] == [t.data_ptr() & 0xFFFFFFFFFFFFFFFF for t in ts]
+    assert native.tensor_table(ts, dtypes, shapes, 0) == 0  # not on device 0
+    for i, (t, dt, sh) in enumerate([
+            (torch.zeros(5, dtype=torch.int32), i64, (5,)),  # dtype
+            (torch.zeros(3, 4), f32, (4, 3)),  # shape
+            (torch.zeros(4, 3)[:, :2].contiguous().t(), f32, (2, 4)),  # layout
+            (torch.zeros(4, 3), f32, (4, 3, 1))]):  # rank
+        bad_ts, bad_dt, bad_sh = list(ts), list(dtypes), list(shapes)
+        bad_ts[1], bad_dt[1], bad_sh[1] = t, dt, sh
+        assert native.tensor_table(bad_ts, bad_dt, bad_sh, -1) == 1, i
+    with pytest.raises(ValueError):
+        native.tensor_table(ts, dtypes[:2], shapes, -1)
+    with pytest.raises(TypeError):
+        native.tensor_table(ts, ["float32"] * 5, shapes, -1)
