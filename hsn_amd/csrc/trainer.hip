@@ -20,6 +20,7 @@
 // coalesced run. The passes are HBM-bound: AdamW moves 28 bytes an element (four rows read, three
 // written).
 #include <string>
+#include <type_traits>
 
 #include "../../include/hsn_trainer.h"
 #include "abi_util.h"
@@ -31,7 +32,6 @@ namespace hsn {
 namespace {
 
 constexpr int kTrRows = 4;      // operands per tensor
-constexpr int kTrTensors = 48;  // tensors per launch (a longer list takes several)
 constexpr int kTrUnits = 64;    // units of a stacked unit tensor (the reference's HSN_TR_UNITS)
 constexpr int kTrThreads = 256;
 constexpr int kTrPer = 4;       // elements per thread
@@ -39,19 +39,29 @@ constexpr int kTrChunk = kTrThreads * kTrPer;
 
 enum TrOp : int { kAdamW, kAdamWUnits, kLerp, kScale64, kCopy, kLimitSquares, kLimitProject };
 
-// The by-value launch descriptor (under the 4 KiB of kernel arguments).
-struct TrArgs {
-    float* p[kTrRows][kTrTensors];  // operand r of tensor j
-    int64_t numel[kTrTensors];
-    int32_t chunk0[kTrTensors + 1];  // the first chunk of tensor j; chunk0[n] = all chunks
-    int32_t n;                       // tensors
-    int32_t flag;                    // AdamW: weight decay on
-    int32_t units;                   // AdamW units: M
+// The by-value launch descriptor (under the 4 KiB of kernel arguments): T tensors a launch (a
+// longer list takes several), and with U the unit coefficients of the stacked-unit AdamW, whose
+// 1.5 KiB leave room for 48 tensors; the other passes take 88 (the model's 198 tensors in three
+// launches, not five).
+template <int T, bool U>
+struct TrArgsT {
+    static constexpr int kTensors = T;
+    float* p[kTrRows][T];  // operand r of tensor j
+    int64_t numel[T];
+    int32_t chunk0[T + 1];  // the first chunk of tensor j; chunk0[n] = all chunks
+    int32_t n;              // tensors
+    int32_t flag;           // AdamW: weight decay on
+    int32_t units;          // AdamW units: M
     float f[8];
-    float u[6][kTrUnits];
+    float u[U ? 6 : 1][U ? kTrUnits : 1];
     const double* coef;  // scale64: the coefficient, one f64 on the device
 };
-static_assert(sizeof(TrArgs) <= 4096, "kernel arguments take at most 4 KiB");
+using TrArgsUnits = TrArgsT<48, true>;
+using TrArgs = TrArgsT<88, false>;
+static_assert(sizeof(TrArgsUnits) <= 4096 && sizeof(TrArgs) <= 4096,
+              "kernel arguments take at most 4 KiB");
+template <int OP>
+using TrArgsOf = std::conditional_t<OP == kAdamWUnits, TrArgsUnits, TrArgs>;
 
 // at::native::lerp (ATen/native/Lerp.h) as the device compiles it: the small-weight form
 // self + w (end - self) and the large one end - (end - self)(1 - w), each with its product
@@ -99,9 +109,8 @@ struct TrUniform {
 
 // One element: x[r] holds row r's value on entry (the rows the pass reads) and on exit (the
 // rows it writes); o is the element's index in its tensor.
-template <int OP>
-__device__ __forceinline__ void tr_op(const TrArgs& a, const TrUniform& q, int64_t o,
-                                      float (&x)[4]) {
+template <int OP, typename A>
+__device__ __forceinline__ void tr_op(const A& a, const TrUniform& q, int64_t o, float (&x)[4]) {
     if constexpr (OP == kAdamW) {
         // lazy_adam._dense_steps: p *= 1 - lr wd; m = lerp(m, g, 1 - beta1); v *= beta2;
         // v = addcmul(v, g, g, 1 - beta2); den = sqrt(v) * (1 / sqrt(1 - beta2^t)) + eps;
@@ -158,7 +167,7 @@ __device__ __forceinline__ void tr_op(const TrArgs& a, const TrUniform& q, int64
 // accesses (runs of four elements a thread, loads issued together or per run) and sixteen elements
 // a thread measured 5.3-5.4 TB/s, a grid-stride loop 4.5 TB/s.
 template <int OP>
-__global__ __launch_bounds__(kTrThreads) void tr_pass(TrArgs a) {
+__global__ __launch_bounds__(kTrThreads) void tr_pass(TrArgsOf<OP> a) {
     constexpr int kRd = TrRows<OP>::rd;
     const int c = blockIdx.x;
     int lo = 0, hi = a.n - 1;  // the tensor holding chunk c: the last j with chunk0[j] <= c
@@ -205,14 +214,14 @@ __global__ __launch_bounds__(kTrThreads) void tr_pass(TrArgs a) {
     }
 }
 
-// The list, in launches of at most kTrTensors tensors (empty tensors skipped).
+// The list, in launches of at most TrArgsOf<OP>::kTensors tensors (empty tensors skipped).
 template <int OP>
-void tr_launch(TrArgs& a, float* const* const rows[kTrRows], const int64_t* numels, int n,
+void tr_launch(TrArgsOf<OP>& a, float* const* const rows[kTrRows], const int64_t* numels, int n,
                hipStream_t st) {
     int j = 0;
     while (j < n) {
         int m = 0, chunks = 0;
-        for (; j < n && m < kTrTensors; ++j) {
+        for (; j < n && m < TrArgsOf<OP>::kTensors; ++j) {
             if (numels[j] == 0) continue;
             for (int r = 0; r < kTrRows; ++r) a.p[r][m] = rows[r] ? rows[r][j] : nullptr;
             a.numel[m] = numels[j];
@@ -291,7 +300,7 @@ extern "C" int hsn_tr_adamw_units(float* const* params, float* const* grads,
     for (int j = 0; j < n; ++j)
         HSN_REQUIRE(numels[j] % n_units == 0, HSN_ERR_INVALID_ARGUMENT,
                     "hsn_tr_adamw_units: a tensor's elements are not a whole number per unit");
-    TrArgs a{};
+    TrArgsUnits a{};
     a.flag = weight_decay_on ? 1 : 0;
     a.units = n_units;
     a.f[3] = one_minus_beta2;
