@@ -608,7 +608,7 @@ def _round_main(args) -> int:
     replay stream around the timed replays (the two kernels' rocprofv3 averages add up to it)."""
     import torch
 
-    from hsn_amd.kernels.window import cell_round_op
+    from hsn_amd.kernels.window import _cell_round_run, cell_round_op
     from hsn_amd.workload import (ROUND_CONFIGS, make_round_cell, make_round_positions,
                                   round_bytes)
 
@@ -629,15 +629,14 @@ def _round_main(args) -> int:
     alpha = pos["valid"].float()
     start = pos["state"]
 
-    def one(t, h, q, age):
-        return cell_round_op(pos["u"][t], pos["eps"][t], h, q, age, pos["cells"][t],
-                             pos["units"][t], pos["valid"][t], alpha[t], *weights, True, 1e-6,
-                             1e-6)[:3]
+    def one(t, h, q, age, fn=cell_round_op):
+        return fn(pos["u"][t], pos["eps"][t], h, q, age, pos["cells"][t], pos["units"][t],
+                  pos["valid"][t], alpha[t], *weights, True, 1e-6, 1e-6)[:3]
 
-    def step():
+    def step(fn=cell_round_op):
         h, q, age = start.h, start.q, start.age
         for t in range(T):
-            h, q, age = one(t, h, q, age)
+            h, q, age = one(t, h, q, age, fn)
         return h
 
     with torch.no_grad():
@@ -649,6 +648,15 @@ def _round_main(args) -> int:
             step()
         torch.cuda.synchronize()
         eager_secs = (time.perf_counter() - t0) / args.steps
+        # the same rounds as hsn_amd.kernels.window.cell_round runs them eagerly: the op's body
+        # without the custom op's dispatch
+        step(_cell_round_run)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step(_cell_round_run)
+        torch.cuda.synchronize()
+        call_secs = (time.perf_counter() - t0) / args.steps
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             step()
@@ -691,6 +699,7 @@ def _round_main(args) -> int:
         "position_us_device": device_us,
         "position_us_wall": step_secs / T * 1e6,
         "position_us_eager": eager_secs / T * 1e6,
+        "position_us_eager_call": call_secs / T * 1e6,
     }
     if not args.no_cpu:  # the oracle on a bounded sample: 2 rows x 4 positions, one thread
         from oracle import hsn_oracle as O

@@ -482,16 +482,15 @@ def _need(name: str, t: Tensor, dtype: torch.dtype, shape: tuple, index: int) ->
         raise ValueError(f"cell round: {name} must be contiguous")
 
 
-@torch.library.custom_op("hsn::window_cell_round", mutates_args=(), device_types="cuda")
-def cell_round_op(u: Tensor, eps: Tensor, h: Tensor, q: Tensor, age: Tensor, cells: Tensor,
-                  units: Tensor, valid: Tensor, alpha: Tensor, V: Tensor, edge_w: Tensor,
-                  pad_src: Tensor, norm_w: Tensor, gate_w: Tensor, gate_b: Tensor, W1: Tensor,
-                  b1: Tensor, W2: Tensor, b2: Tensor, W_out: Tensor, cand_w: Tensor,
-                  cand_norm: bool, norm_eps: float, cand_eps: float
-                  ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """The sparse round and the tick, forward only: ``(h_new, q_new, age_new, h_sel)``
-    (reference window.py:233-330; ``hsn_win_cell_round``). Contiguous fp32 / int64 / bool
-    tensors on one device, as the reference's op takes them; not differentiable."""
+def _cell_round_run(u: Tensor, eps: Tensor, h: Tensor, q: Tensor, age: Tensor, cells: Tensor,
+                    units: Tensor, valid: Tensor, alpha: Tensor, V: Tensor, edge_w: Tensor,
+                    pad_src: Tensor, norm_w: Tensor, gate_w: Tensor, gate_b: Tensor, W1: Tensor,
+                    b1: Tensor, W2: Tensor, b2: Tensor, W_out: Tensor, cand_w: Tensor,
+                    cand_norm: bool, norm_eps: float, cand_eps: float
+                    ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """The op's body: the checks, the outputs and the call of ``hsn_win_cell_round``. Eager
+    callers outside a compiled region call it directly (:func:`cell_round`): the custom op's
+    dispatch adds its Python autograd and aliasing layers to every position."""
     B, N, d = (int(n) for n in h.shape)
     K = int(cells.shape[1])
     M, n_in, H = (int(n) for n in W1.shape)
@@ -547,6 +546,21 @@ def cell_round_op(u: Tensor, eps: Tensor, h: Tensor, q: Tensor, age: Tensor, cel
     return h_new, q_new, age_new, h_sel
 
 
+@torch.library.custom_op("hsn::window_cell_round", mutates_args=(), device_types="cuda")
+def cell_round_op(u: Tensor, eps: Tensor, h: Tensor, q: Tensor, age: Tensor, cells: Tensor,
+                  units: Tensor, valid: Tensor, alpha: Tensor, V: Tensor, edge_w: Tensor,
+                  pad_src: Tensor, norm_w: Tensor, gate_w: Tensor, gate_b: Tensor, W1: Tensor,
+                  b1: Tensor, W2: Tensor, b2: Tensor, W_out: Tensor, cand_w: Tensor,
+                  cand_norm: bool, norm_eps: float, cand_eps: float
+                  ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """The sparse round and the tick, forward only: ``(h_new, q_new, age_new, h_sel)``
+    (reference window.py:233-330; ``hsn_win_cell_round``). Contiguous fp32 / int64 / bool
+    tensors on one device, as the reference's op takes them; not differentiable."""
+    return _cell_round_run(u, eps, h, q, age, cells, units, valid, alpha, V, edge_w, pad_src,
+                           norm_w, gate_w, gate_b, W1, b1, W2, b2, W_out, cand_w, cand_norm,
+                           norm_eps, cand_eps)
+
+
 @cell_round_op.register_fake
 def _cell_round_fake(u, eps, h, q, age, cells, units, valid, alpha, V, edge_w, pad_src, norm_w,
                      gate_w, gate_b, W1, b1, W2, b2, W_out, cand_w, cand_norm, norm_eps, cand_eps):
@@ -563,8 +577,10 @@ def cell_round(cell, u: Tensor, eps: Tensor, state: CellGraphState, cells: Tenso
     window.py:1007-1048)."""
     cand_norm = getattr(cell, "cand_norm_kind", "none") != "none"
     norm_w = cell.norm.weight
+    # eagerly the op's body itself; inside a compiled region the registered op
+    run = cell_round_op if torch.compiler.is_compiling() else _cell_round_run
     with torch.no_grad():
-        h_new, q_new, age_new, h_sel = cell_round_op(
+        h_new, q_new, age_new, h_sel = run(
             u.contiguous(), eps.contiguous(), state.h.contiguous(), state.q.contiguous(),
             state.age.contiguous(), cells.contiguous(), units.contiguous(), valid.contiguous(),
             valid.to(torch.float32).contiguous(), cell.V.weight.detach(),

@@ -187,6 +187,19 @@ def test_cell_round_wrapper_and_its_declines(dev):
     _close(st.q, want[1], "wrapper q")
     assert torch.equal(st.age.cpu(), want[2]) and torch.equal(st.pos.cpu(), want[3])
     _close(h_sel, want[4], "wrapper h_sel")
+    # the eager wrapper runs the op's body without the custom op's dispatch: the registered op
+    # gives the same bits
+    with torch.no_grad():
+        op = W.cell_round_op(
+            pos["u"][0], pos["eps"][0], pos["state"].h, pos["state"].q, pos["state"].age,
+            pos["cells"][0], pos["units"][0], pos["valid"][0], pos["valid"][0].float(),
+            cell.V.weight, edge_w.float(), cell.graph._pad_src, cell.norm.weight,
+            cell.gate.weight, cell.gate.bias, cell.units.W1, cell.units.b1, cell.units.W2,
+            cell.units.b2, cell.W_out.weight, cell.cand_norm.weight, True,
+            float(getattr(cell.norm, "eps", None) or 0.0),
+            float(getattr(cell.cand_norm, "eps", None) or 0.0))
+    for got, ref, what in zip((st.h, st.q, st.age, h_sel), op, ("h", "q", "age", "h_sel")):
+        assert torch.equal(got, ref), f"wrapper against the registered op: {what}"
 
     def variant(**kw):
         v = SimpleNamespace(**vars(cell))
