@@ -524,10 +524,25 @@ def _ops_main(args) -> int:
         "csr_messages_backward": lambda: ops.messages_backward(
             h, indptr, indices, a, V, idx, m),
     }
+    # the same calls as the adapters make them outside grad mode: the ops' bodies without the
+    # custom op's dispatch
+    direct = {
+        "gated_delta_update_functional": lambda: ops._functional(
+            h, q, age.long(), idx, valid, c, b),
+        "gated_delta_update_backward": lambda: ops._update_bwd_body(
+            idx, valid, c, b, c, h, q),
+        "gather_concat": lambda: ops._gather_body(u, eps, h, m, idx),
+        "gather_concat_backward": lambda: ops._gather_bwd_body(rnd_dv, idx, N),
+        "grouped_unit_mlp": lambda: ops._mlp_body(v, unit, w1, b1, w2, b2),
+        "grouped_unit_mlp_backward": lambda: ops._mlp_bwd_body(v, unit, w1, w2, hidden, out),
+        "csr_messages": lambda: ops._messages_body(h, indptr, indices, a, V, idx),
+        "csr_messages_backward": lambda: ops._messages_bwd_body(
+            h, indptr, indices, a, V, idx, m),
+    }
     rnd_dv = rnd(B, K, 4 * d)
     busy = torch.empty(64 << 20, device=dev)
     busy_dst = torch.empty_like(busy)
-    per_call, end_to_end = {}, {}
+    per_call, end_to_end, end_to_end_direct = {}, {}, {}
     with torch.no_grad():
         for name, fn in calls.items():
             for _ in range(max(1, args.warmup)):
@@ -550,6 +565,11 @@ def _ops_main(args) -> int:
                 fn()
             torch.cuda.synchronize()
             end_to_end[name] = (time.perf_counter() - t0) / args.steps * 1e6
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                direct[name]()
+            torch.cuda.synchronize()
+            end_to_end_direct[name] = (time.perf_counter() - t0) / args.steps * 1e6
     del busy, busy_dst
     mlp_us = per_call["grouped_unit_mlp"]
     flops = 2.0 * P * (4 * d * H + H * d)
@@ -576,6 +596,7 @@ def _ops_main(args) -> int:
         "us_per_call": per_call,
         # the rate a Python caller reaches: host dispatch (the op wrappers and ctypes) included
         "us_per_call_end_to_end": end_to_end,
+        "us_per_call_end_to_end_direct": end_to_end_direct,
     }
     if not args.no_cpu:  # the oracle's unit MLP on the same size, one thread
         from oracle import hsn_oracle as O

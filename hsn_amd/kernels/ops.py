@@ -27,6 +27,7 @@ from __future__ import annotations
 from typing import Any, Optional
 
 import torch
+from torch.utils._python_dispatch import _get_current_dispatch_mode
 from torch import Tensor
 
 from .._lib import call, ptr, stream_of
@@ -88,6 +89,20 @@ def prepare_cuda(device: int = 0) -> None:
         torch.cuda.synchronize(dev)
 
 
+def _eager(op: Any, body: Any, *args: Any) -> Any:
+    """``op(*args)`` where a gradient can flow or anything traces (a compiled region, a dispatch
+    mode such as AOT autograd's, fake or functional tensors); elsewhere (plain tensors, no grad
+    mode or no input that requires grad, as in the backward formulas) the op's body itself, with
+    the same results: the custom op's dispatch adds its Python autograd and aliasing layers,
+    about 10 us, to every call."""
+    tensors = [a for a in args if isinstance(a, Tensor)]
+    if (torch.compiler.is_compiling() or _get_current_dispatch_mode() is not None
+            or any(type(t) not in (Tensor, torch.nn.Parameter) for t in tensors)
+            or (torch.is_grad_enabled() and any(t.requires_grad for t in tensors))):
+        return op(*args)
+    return body(*args)
+
+
 def _code(t: Tensor) -> int:
     try:
         return _DTYPE[t.dtype]
@@ -111,9 +126,7 @@ def _flags(t: Tensor) -> Tensor:
     return t.to(torch.int32).contiguous()
 
 
-@torch.library.custom_op("hsn::gather_concat", mutates_args=(), device_types="cuda")
-def gather_op(u: Tensor, eps: Tensor, h: Tensor, m: Tensor, idx: Tensor) -> Tensor:
-    """``v[r,k] = [u[r]; eps[r]; h[r, idx[r,k]]; m[r,k]]`` (reference hsn_ops.h:79-87)."""
+def _gather_body(u: Tensor, eps: Tensor, h: Tensor, m: Tensor, idx: Tensor) -> Tensor:
     B, N, d = h.shape
     K = idx.shape[1]
     u, eps, h, m, idx = u.contiguous(), eps.contiguous(), h.contiguous(), m.contiguous(), _i32(idx)
@@ -123,14 +136,18 @@ def gather_op(u: Tensor, eps: Tensor, h: Tensor, m: Tensor, idx: Tensor) -> Tens
     return v
 
 
+@torch.library.custom_op("hsn::gather_concat", mutates_args=(), device_types="cuda")
+def gather_op(u: Tensor, eps: Tensor, h: Tensor, m: Tensor, idx: Tensor) -> Tensor:
+    """``v[r,k] = [u[r]; eps[r]; h[r, idx[r,k]]; m[r,k]]`` (reference hsn_ops.h:79-87)."""
+    return _gather_body(u, eps, h, m, idx)
+
+
 @gather_op.register_fake
 def _gather_fake(u, eps, h, m, idx):
     return h.new_empty((*idx.shape, 4 * h.shape[2]))
 
 
-@torch.library.custom_op("hsn::gather_concat_backward", mutates_args=(), device_types="cuda")
-def gather_backward(dv: Tensor, idx: Tensor, n: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """``(grad_u, grad_eps, grad_h, grad_m)`` of the gather (reference hsn_ops.h:88-99)."""
+def _gather_bwd_body(dv: Tensor, idx: Tensor, n: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     B, K, width = dv.shape
     d = width // 4
     dv, idx = dv.contiguous(), _i32(idx)
@@ -139,6 +156,12 @@ def gather_backward(dv: Tensor, idx: Tensor, n: int) -> tuple[Tensor, Tensor, Te
     call("hsn_gather_concat_bwd", ptr(dv), ptr(idx), ptr(du), ptr(de), ptr(dh), ptr(dm), B, n, d,
          K, _code(dv), 1, stream_of(dv.device))
     return du, de, dh, dm
+
+
+@torch.library.custom_op("hsn::gather_concat_backward", mutates_args=(), device_types="cuda")
+def gather_backward(dv: Tensor, idx: Tensor, n: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """``(grad_u, grad_eps, grad_h, grad_m)`` of the gather (reference hsn_ops.h:88-99)."""
+    return _gather_bwd_body(dv, idx, n)
 
 
 @gather_backward.register_fake
@@ -154,7 +177,8 @@ def _gather_setup(ctx: Any, inputs: tuple[Any, ...], output: Tensor) -> None:
 
 
 def _gather_grad(ctx: Any, dv: Tensor) -> tuple[Any, ...]:
-    return (*gather_backward(dv.contiguous(), ctx.saved_tensors[0], ctx.n), None)
+    return (*_eager(gather_backward, _gather_bwd_body, dv.contiguous(), ctx.saved_tensors[0],
+                    ctx.n), None)
 
 
 gather_op.register_autograd(_gather_grad, setup_context=_gather_setup)
@@ -236,11 +260,8 @@ def _state_update_fake(h, q, age, idx, valid, c, b):
     return torch.empty_like(h), torch.empty_like(q), torch.empty_like(age), torch.empty_like(c)
 
 
-@torch.library.custom_op("hsn::gated_delta_update_backward", mutates_args=(), device_types="cuda")
-def update_backward(idx: Tensor, valid: Tensor, c: Tensor, b: Tensor, old: Tensor, G: Tensor,
-                    g: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """``(grad_h, grad_q, grad_c, grad_b)`` from ``grad_h_out = G``, ``grad_q_out = g``
-    (reference hsn_ops.h:173-187)."""
+def _update_bwd_body(idx: Tensor, valid: Tensor, c: Tensor, b: Tensor, old: Tensor, G: Tensor,
+                     g: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     B, N, d = G.shape
     K = idx.shape[1]
     c, b, old, G, g = c.contiguous(), b.contiguous(), old.contiguous(), G.contiguous(), g.contiguous()
@@ -250,6 +271,14 @@ def update_backward(idx: Tensor, valid: Tensor, c: Tensor, b: Tensor, old: Tenso
          ptr(G), ptr(g), ptr(dh), ptr(dq), ptr(dc), ptr(db), B, N, d, K, _code(G),
          stream_of(G.device))
     return dh, dq, dc, db
+
+
+@torch.library.custom_op("hsn::gated_delta_update_backward", mutates_args=(), device_types="cuda")
+def update_backward(idx: Tensor, valid: Tensor, c: Tensor, b: Tensor, old: Tensor, G: Tensor,
+                    g: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """``(grad_h, grad_q, grad_c, grad_b)`` from ``grad_h_out = G``, ``grad_q_out = g``
+    (reference hsn_ops.h:173-187)."""
+    return _update_bwd_body(idx, valid, c, b, old, G, g)
 
 
 @update_backward.register_fake
@@ -264,7 +293,8 @@ def _update_setup(ctx: Any, inputs: tuple[Any, ...], output: tuple[Tensor, ...])
 
 
 def _update_grad(ctx: Any, G: Tensor, g: Tensor, dage: Tensor, dold: Tensor) -> tuple[Any, ...]:
-    dh, dq, dc, db = update_backward(*ctx.saved_tensors, G.contiguous(), g.contiguous())
+    dh, dq, dc, db = _eager(update_backward, _update_bwd_body, *ctx.saved_tensors,
+                            G.contiguous(), g.contiguous())
     return dh, dq, None, None, None, dc, db
 
 
@@ -277,11 +307,8 @@ state_update_op.register_autograd(_update_grad, setup_context=_update_setup)
 # --------------------------------------------------------------------------------------------
 
 
-@torch.library.custom_op("hsn::grouped_unit_mlp", mutates_args=(), device_types="cuda")
-def mlp_op(v: Tensor, idx: Tensor, w1: Tensor, b1: Tensor, w2: Tensor,
-           b2: Tensor) -> tuple[Tensor, Tensor]:
-    """``(out [P,d], hidden [P,H])``: unit ``idx[p]`` on pair ``p``, ``hidden`` the saved
-    pre-GELU ``z1`` (reference hsn_ops.h:101-112)."""
+def _mlp_body(v: Tensor, idx: Tensor, w1: Tensor, b1: Tensor, w2: Tensor,
+              b2: Tensor) -> tuple[Tensor, Tensor]:
     P, M, d, H = v.shape[0], w1.shape[0], w2.shape[2], w1.shape[2]
     v, idx, w1, b1, w2, b2 = (v.contiguous(), _i32(idx), w1.contiguous(), b1.contiguous(),
                               w2.contiguous(), b2.contiguous())
@@ -291,15 +318,21 @@ def mlp_op(v: Tensor, idx: Tensor, w1: Tensor, b1: Tensor, w2: Tensor,
     return out, hidden
 
 
+@torch.library.custom_op("hsn::grouped_unit_mlp", mutates_args=(), device_types="cuda")
+def mlp_op(v: Tensor, idx: Tensor, w1: Tensor, b1: Tensor, w2: Tensor,
+           b2: Tensor) -> tuple[Tensor, Tensor]:
+    """``(out [P,d], hidden [P,H])``: unit ``idx[p]`` on pair ``p``, ``hidden`` the saved
+    pre-GELU ``z1`` (reference hsn_ops.h:101-112)."""
+    return _mlp_body(v, idx, w1, b1, w2, b2)
+
+
 @mlp_op.register_fake
 def _mlp_fake(v, idx, w1, b1, w2, b2):
     return v.new_empty((v.shape[0], w2.shape[2])), v.new_empty((v.shape[0], w1.shape[2]))
 
 
-@torch.library.custom_op("hsn::grouped_unit_mlp_backward", mutates_args=(), device_types="cuda")
-def mlp_backward(v: Tensor, idx: Tensor, w1: Tensor, w2: Tensor, hidden: Tensor,
-                 dout: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """``(dv, dw1, db1, dw2, db2)`` from the saved ``z1`` (reference hsn_ops.h:114-130)."""
+def _mlp_bwd_body(v: Tensor, idx: Tensor, w1: Tensor, w2: Tensor, hidden: Tensor,
+                  dout: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     P, M, d, H = v.shape[0], w1.shape[0], w2.shape[2], w1.shape[2]
     v, idx, w1, w2, hidden, dout = (v.contiguous(), _i32(idx), w1.contiguous(), w2.contiguous(),
                                     hidden.contiguous(), dout.contiguous())
@@ -309,6 +342,13 @@ def mlp_backward(v: Tensor, idx: Tensor, w1: Tensor, w2: Tensor, hidden: Tensor,
          ptr(dv), ptr(dw1), ptr(db1), ptr(dw2), ptr(db2), P, M, d, H, _code(v), 1,
          stream_of(v.device))
     return dv, dw1, db1, dw2, db2
+
+
+@torch.library.custom_op("hsn::grouped_unit_mlp_backward", mutates_args=(), device_types="cuda")
+def mlp_backward(v: Tensor, idx: Tensor, w1: Tensor, w2: Tensor, hidden: Tensor,
+                 dout: Tensor) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """``(dv, dw1, db1, dw2, db2)`` from the saved ``z1`` (reference hsn_ops.h:114-130)."""
+    return _mlp_bwd_body(v, idx, w1, w2, hidden, dout)
 
 
 @mlp_backward.register_fake
@@ -324,7 +364,8 @@ def _mlp_setup(ctx: Any, inputs: tuple[Any, ...], output: tuple[Tensor, Tensor])
 
 
 def _mlp_grad(ctx: Any, dout: Tensor, dhidden: Tensor) -> tuple[Any, ...]:
-    dv, dw1, db1, dw2, db2 = mlp_backward(*ctx.saved_tensors, dout.contiguous())
+    dv, dw1, db1, dw2, db2 = _eager(mlp_backward, _mlp_bwd_body, *ctx.saved_tensors,
+                                    dout.contiguous())
     return dv, None, dw1, db1, dw2, db2
 
 
@@ -336,11 +377,8 @@ mlp_op.register_autograd(_mlp_grad, setup_context=_mlp_setup)
 # --------------------------------------------------------------------------------------------
 
 
-@torch.library.custom_op("hsn::csr_messages", mutates_args=(), device_types="cuda")
-def messages_op(h: Tensor, indptr: Tensor, indices: Tensor, a: Tensor, V: Tensor,
-                idx: Tensor) -> Tensor:
-    """``m [B,K,d]``: ``m[r,k] = sum_e a[e] (V h[r, indices[e]])`` over the edges of row
-    ``idx[r,k]`` (reference hsn_ops.h:132-143)."""
+def _messages_body(h: Tensor, indptr: Tensor, indices: Tensor, a: Tensor, V: Tensor,
+                   idx: Tensor) -> Tensor:
     B, N, d = h.shape
     K, E = idx.shape[1], a.numel()
     h, indptr, indices, a, V, idx = (h.contiguous(), _i32(indptr), _i32(indices), a.contiguous(),
@@ -351,15 +389,21 @@ def messages_op(h: Tensor, indptr: Tensor, indices: Tensor, a: Tensor, V: Tensor
     return m
 
 
+@torch.library.custom_op("hsn::csr_messages", mutates_args=(), device_types="cuda")
+def messages_op(h: Tensor, indptr: Tensor, indices: Tensor, a: Tensor, V: Tensor,
+                idx: Tensor) -> Tensor:
+    """``m [B,K,d]``: ``m[r,k] = sum_e a[e] (V h[r, indices[e]])`` over the edges of row
+    ``idx[r,k]`` (reference hsn_ops.h:132-143)."""
+    return _messages_body(h, indptr, indices, a, V, idx)
+
+
 @messages_op.register_fake
 def _messages_fake(h, indptr, indices, a, V, idx):
     return h.new_empty((*idx.shape, h.shape[2]))
 
 
-@torch.library.custom_op("hsn::csr_messages_backward", mutates_args=(), device_types="cuda")
-def messages_backward(h: Tensor, indptr: Tensor, indices: Tensor, a: Tensor, V: Tensor,
-                      idx: Tensor, dm: Tensor) -> tuple[Tensor, Tensor, Tensor]:
-    """``(dh, da, dV)`` of the messages (reference hsn_ops.h:145-153)."""
+def _messages_bwd_body(h: Tensor, indptr: Tensor, indices: Tensor, a: Tensor, V: Tensor,
+                       idx: Tensor, dm: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     B, N, d = h.shape
     K, E = idx.shape[1], a.numel()
     h, indptr, indices, a, V, idx, dm = (h.contiguous(), _i32(indptr), _i32(indices),
@@ -369,6 +413,13 @@ def messages_backward(h: Tensor, indptr: Tensor, indices: Tensor, a: Tensor, V: 
     call("hsn_csr_messages_bwd", ptr(h), ptr(indptr), ptr(indices), ptr(a), ptr(V), ptr(idx),
          ptr(dm), ptr(dh), ptr(da), ptr(dV), B, N, d, K, E, _code(h), 1, stream_of(h.device))
     return dh, da, dV
+
+
+@torch.library.custom_op("hsn::csr_messages_backward", mutates_args=(), device_types="cuda")
+def messages_backward(h: Tensor, indptr: Tensor, indices: Tensor, a: Tensor, V: Tensor,
+                      idx: Tensor, dm: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """``(dh, da, dV)`` of the messages (reference hsn_ops.h:145-153)."""
+    return _messages_bwd_body(h, indptr, indices, a, V, idx, dm)
 
 
 @messages_backward.register_fake
@@ -381,7 +432,8 @@ def _messages_setup(ctx: Any, inputs: tuple[Any, ...], output: Tensor) -> None:
 
 
 def _messages_grad(ctx: Any, dm: Tensor) -> tuple[Any, ...]:
-    dh, da, dV = messages_backward(*ctx.saved_tensors, dm.contiguous())
+    dh, da, dV = _eager(messages_backward, _messages_bwd_body, *ctx.saved_tensors,
+                        dm.contiguous())
     return dh, None, None, da, dV, None
 
 
@@ -443,8 +495,8 @@ def gather_concat(u: Optional[Tensor], eps: Tensor, h: Tensor, m: Tensor, cell_i
         return _declined("gather_concat", why)(u, eps, h, m, cell_idx)
     if u.dtype != h.dtype or eps.dtype != h.dtype:
         raise ValueError("u, eps and h must have the same state dtype")
-    return gather_op(u.contiguous(), eps.contiguous(), h.contiguous(), m.to(h.dtype).contiguous(),
-                     _i32(cell_idx))
+    return _eager(gather_op, _gather_body, u.contiguous(), eps.contiguous(), h.contiguous(),
+                  m.to(h.dtype).contiguous(), _i32(cell_idx))
 
 
 def grouped_unit_mlp(v: Tensor, unit_idx: Tensor, bank: Any, *, static: bool = False,
@@ -478,9 +530,9 @@ def grouped_unit_mlp(v: Tensor, unit_idx: Tensor, bank: Any, *, static: bool = F
     # reach the masters through the cast
     w1 = bank.W1 if w1_flat is None else \
         w1_flat.reshape(bank.in_dim, bank.n_units, bank.hidden).permute(1, 0, 2)
-    out, _ = mlp_op(v.to(dtype).contiguous(), _i32(unit_idx), w1.to(dtype).contiguous(),
-                    bank.b1.to(dtype).contiguous(), bank.W2.to(dtype).contiguous(),
-                    bank.b2.to(dtype).contiguous())
+    out, _ = _eager(mlp_op, _mlp_body, v.to(dtype).contiguous(), _i32(unit_idx),
+                    w1.to(dtype).contiguous(), bank.b1.to(dtype).contiguous(),
+                    bank.W2.to(dtype).contiguous(), bank.b2.to(dtype).contiguous())
     return out
 
 
@@ -502,8 +554,9 @@ def csr_messages(h: Tensor, graph: Any, V: Any, cell_idx: Tensor, *,
         raise ValueError("CSR messages need a projection without bias")
     a = graph.edge_weights() if weights is None else weights.reshape(-1)[graph._edge_pos]
     dtype = _dtype_for(h)
-    return messages_op(h.to(dtype).contiguous(), _i32(graph.indptr), _i32(graph.indices),
-                       a.to(dtype).contiguous(), V.weight.to(dtype).contiguous(), _i32(cell_idx))
+    return _eager(messages_op, _messages_body, h.to(dtype).contiguous(), _i32(graph.indptr),
+                  _i32(graph.indices), a.to(dtype).contiguous(), V.weight.to(dtype).contiguous(),
+                  _i32(cell_idx))
 
 
 def _check_valid(valid: Any, shape: tuple, device: torch.device) -> None:
@@ -562,6 +615,7 @@ def gated_delta_update(state: Any, cell_idx: Tensor, c: Tensor, b: Tensor, valid
     _check_valid(valid, tuple(cell_idx.shape), h.device)
     if validate:
         _check_selection(cell_idx, valid, int(h.shape[1]))
-    hn, qn, age, _ = state_update_op(h.contiguous(), state.q.contiguous(), state.age.contiguous(),
-                                     _i32(cell_idx), _flags(valid), c.contiguous(), b.contiguous())
+    hn, qn, age, _ = _eager(state_update_op, _functional, h.contiguous(), state.q.contiguous(),
+                            state.age.contiguous(), _i32(cell_idx), _flags(valid), c.contiguous(),
+                            b.contiguous())
     return _with_state(state, hn, qn, age, state.pos)

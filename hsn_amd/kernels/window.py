@@ -16,6 +16,7 @@ from typing import Optional
 
 import torch
 from torch import Tensor
+from torch.utils._python_dispatch import _get_current_dispatch_mode
 
 from .. import _lib
 from .._lib import DTYPE_BF16, DTYPE_F32, call, ptr, stream_of
@@ -577,8 +578,11 @@ def cell_round(cell, u: Tensor, eps: Tensor, state: CellGraphState, cells: Tenso
     window.py:1007-1048)."""
     cand_norm = getattr(cell, "cand_norm_kind", "none") != "none"
     norm_w = cell.norm.weight
-    # eagerly the op's body itself; inside a compiled region the registered op
-    run = cell_round_op if torch.compiler.is_compiling() else _cell_round_run
+    # eagerly the op's body itself; the registered op where anything traces (a compiled region,
+    # a dispatch mode, fake or functional tensors)
+    traced = (torch.compiler.is_compiling() or _get_current_dispatch_mode() is not None
+              or type(state.h) is not Tensor)
+    run = cell_round_op if traced else _cell_round_run
     with torch.no_grad():
         h_new, q_new, age_new, h_sel = run(
             u.contiguous(), eps.contiguous(), state.h.contiguous(), state.q.contiguous(),

@@ -263,3 +263,54 @@ def test_graph_replay_follows_changed_routing(ops, cuda_device, op):
             torch.testing.assert_close(out[k], eager[k], msg=k)
         for k in want:
             torch.testing.assert_close(grads[k], want[k], msg=k)
+
+
+def test_eager_bodies_equal_the_registered_ops(ops):
+    """Outside grad mode (and in the backward formulas) the adapters call each op's body without
+    the custom op's dispatch: every forward and backward body gives the registered op's bits."""
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(12)
+    B, K, N, d, E, P, M, H = 4, 4, 32, 64, 128, 16, 8, 512
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(dev)
+
+    idx = torch.stack([torch.randperm(N, generator=g)[:K] for _ in range(B)]).to(dev)
+    valid = torch.ones(B, K, dtype=torch.int32, device=dev)
+    valid[1, 2] = 0
+    h, q = rnd(B, N, d, scale=0.5), rnd(B, d)
+    age = torch.randint(0, 9, (B, N), generator=g).to(dev)
+    c, b = rnd(B, K, d).tanh(), torch.sigmoid(rnd(B, K, d))
+    u, eps, m = rnd(B, d), rnd(B, d), rnd(B, K, d)
+    unit = torch.randint(0, M, (P,), generator=g).to(dev)
+    v = rnd(P, 4 * d)
+    w1, b1 = rnd(M, 4 * d, H, scale=(4 * d) ** -0.5), rnd(M, H, scale=0.1)
+    w2, b2 = rnd(M, H, d, scale=H ** -0.5), rnd(M, d, scale=0.1)
+    indptr = torch.arange(0, E + 1, E // N, dtype=torch.int64).to(dev)
+    indices = torch.randint(0, N, (E,), generator=g).to(dev)
+    a = torch.rand(E, generator=g).to(dev)
+    V = rnd(d, d, scale=d ** -0.5)
+    with torch.no_grad():
+        out, hidden = ops.mlp_op(v, unit, w1, b1, w2, b2)
+        cases = {
+            "gather": (ops.gather_op, ops._gather_body, (u, eps, h, m, idx)),
+            "gather backward": (ops.gather_backward, ops._gather_bwd_body,
+                                (rnd(B, K, 4 * d), idx, N)),
+            "mlp": (ops.mlp_op, ops._mlp_body, (v, unit, w1, b1, w2, b2)),
+            "mlp backward": (ops.mlp_backward, ops._mlp_bwd_body, (v, unit, w1, w2, hidden, out)),
+            "messages": (ops.messages_op, ops._messages_body, (h, indptr, indices, a, V, idx)),
+            "messages backward": (ops.messages_backward, ops._messages_bwd_body,
+                                  (h, indptr, indices, a, V, idx, m)),
+            "update": (ops.state_update_op, ops._functional, (h, q, age, idx, valid, c, b)),
+            "update backward": (ops.update_backward, ops._update_bwd_body,
+                                (idx, valid, c, b, c, h, q)),
+        }
+        for name, (op, body, args) in cases.items():
+            want, got = op(*args), body(*args)
+            want = want if isinstance(want, tuple) else (want,)
+            got = got if isinstance(got, tuple) else (got,)
+            assert len(want) == len(got), name
+            for i, (x, y) in enumerate(zip(got, want)):
+                assert x.dtype == y.dtype and x.shape == y.shape, (name, i)
+                assert torch.equal(x, y) or bool(((x == y) | (x.isnan() & y.isnan())).all()), \
+                    f"{name}: output {i} differs from the registered op's"
