@@ -89,7 +89,6 @@ SIGNATURES: dict[str, list] = {
 _lock = threading.Lock()
 
 
-
 @lru_cache(maxsize=None)
 def host_tables():
     """The host helper module ``hsn_amd._tables`` (the Python mirror's checks and pointer tables
@@ -100,6 +99,7 @@ def host_tables():
     from . import _tables
 
     return _tables
+
 
 @lru_cache(maxsize=1)
 def library() -> ctypes.CDLL:
@@ -181,8 +181,14 @@ def workspace_bytes(op: int, B: int, T: int, N: int, d: int, K: int, io_code: in
 
 
 def ptr(t) -> int | None:
-    """Device address of a tensor (``None`` for an absent optional tensor)."""
-    return None if t is None else t.data_ptr()
+    """Device address of a tensor (``None`` for an absent optional tensor); a tensor in host
+    memory raises ``ValueError`` (the kernels would read its address as device memory)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError(f"a {tuple(t.shape)} tensor on {t.device}: the kernels take ROCm device "
+                         "tensors")
+    return t.data_ptr()
 
 
 def stream_of(device) -> int:

@@ -497,6 +497,8 @@ def _cell_round_run(u: Tensor, eps: Tensor, h: Tensor, q: Tensor, age: Tensor, c
     M, n_in, H = (int(n) for n in W1.shape)
     D = int(edge_w.shape[1])
     dev = h.device
+    if not h.is_cuda:
+        raise ValueError(f"cell round: h on {dev}; the round takes tensors on one ROCm device")
     index = h.get_device()
     f32, i64 = torch.float32, torch.int64
     operands = (u, eps, h, q, age, cells, units, valid, alpha, V, edge_w, pad_src, norm_w, gate_w,

@@ -407,3 +407,13 @@ def _route_forward_reasons(reason, F32, BF16):
         assert "256 workgroups" in reason(1, F32, 32, F32, 0, 64, 64, 64, 64, 8)
     finally:
         _lib.set_path("auto")
+
+
+def test_device_pointers_refuse_host_tensors():
+    """A host tensor never reaches a kernel as an address (the eager paths that skip the custom
+    ops' device dispatch rely on it): ``ptr`` raises for it and passes ``None`` through."""
+    from hsn_amd import _lib
+
+    assert _lib.ptr(None) is None
+    with pytest.raises(ValueError, match="ROCm device"):
+        _lib.ptr(torch.zeros(3))
